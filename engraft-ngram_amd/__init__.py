@@ -1,0 +1,20 @@
+"""MI355X-native Engram/PLE n-gram table path (import name ``engraft_ngram_amd``).
+
+Drop-in for the table path of fulvian/engraft-ngram: the n-gram row hash, the
+gather + dequantisation of block-quantised table rows, their add into the
+residual stream, and the descent backward (deterministic sparse gradient
+scatter + Adam + requantisation on the touched overlay rows).  Host code is
+Python on PyTorch-ROCm; every stage runs in hand-written gfx950 HIP kernels
+behind the C ABI of ``include/engraft_ngram.h`` (``libengraft_ngram.so``).
+
+Modules mirror the reference's:
+  table    -- ``engraft.table``       (DeviceTable = PleTable duck type)
+  lens     -- ``engraft.lens``        (.pleo, local_to_global, RowSet)
+  overlay  -- ``engraft.replica.seq`` OverlayEmb / ``model.ple_true_emb``
+  descent  -- ``engraft.replica.distill`` row vars + the optimizer step
+  pack     -- ``engraft.replica.pack`` segments
+  damage   -- ``engraft.damage``      vectorized ngram_rows / scan_hits
+"""
+from . import _lib  # noqa: F401
+
+__all__ = ["_lib"]

@@ -1,0 +1,130 @@
+"""ctypes binding of the C ABI declared in ``include/engraft_ngram.h``.
+
+The library is loaded on first use and never replaced by anything else: if
+``libengraft_ngram.so`` is missing or does not load, every product entry point
+raises ``RuntimeError`` (there is no CPU fallback).
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_int32, c_int64, c_uint64, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libengraft_ngram.so"
+
+EG_MAX_NGRAM = 4
+EG_MAX_HEADS = 32
+EG_MAX_LAYERS = 2
+
+EG_OK = 0
+EG_ERR_ARG = -1
+EG_ERR_HIP = -2
+EG_ERR_UNSUPPORTED = -3
+EG_ERR_WORKSPACE = -4
+
+FMT_BF16 = 1
+FMT_Q8_0 = 2
+FMT_MXFP8 = 3
+FMT_IQ4_NL = 4
+FMT_F32 = 5
+
+FMT_CODES = {"bf16": FMT_BF16, "q8_0": FMT_Q8_0, "mxfp8": FMT_MXFP8, "iq4_nl": FMT_IQ4_NL, "f32": FMT_F32}
+
+
+class EgHashSpec(ctypes.Structure):
+    _fields_ = [
+        ("eos_token_id", c_uint64),
+        ("ngram_size", c_int32),
+        ("heads_per_ngram", c_int32),
+        ("layer_multipliers", c_uint64 * EG_MAX_NGRAM),
+        ("head_multipliers", c_void_p),
+        ("head_vocab_sizes", c_uint64 * EG_MAX_HEADS),
+        ("head_offsets", c_int64 * EG_MAX_HEADS),
+    ]
+
+
+class EgTable(ctypes.Structure):
+    _fields_ = [
+        ("fmt", c_int32),
+        ("dim", c_int32),
+        ("n_rows", c_int64),
+        ("payload", c_void_p),
+        ("scales", c_void_p),
+    ]
+
+
+class EgOverlay(ctypes.Structure):
+    _fields_ = [
+        ("n", c_int64),
+        ("ids", c_void_p),
+        ("index", c_void_p),
+        ("rows", EgTable),
+    ]
+
+
+# name -> (restype, argtypes); every symbol the header declares.
+SIGNATURES = {
+    "eg_last_error": (c_char_p, []),
+    "eg_abi_version": (c_int32, []),
+    "eg_hash_rows": (c_int32, [POINTER(EgHashSpec), c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p,
+                               c_void_p]),
+    "eg_forward": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,
+                             c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "eg_gather": (c_int32, [POINTER(EgTable), POINTER(EgOverlay), c_void_p, c_int64, c_int32, c_void_p,
+                            c_void_p]),
+    "eg_synth_table": (c_int32, [POINTER(EgTable), c_uint64, c_void_p, c_int64, c_int64, c_void_p]),
+}
+
+_LIB = None
+
+
+def load(path: Path | None = None) -> ctypes.CDLL:
+    """Loads (once) and returns the library; raises RuntimeError if absent."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(
+            f"HIP library {p} not found: build it with `python engraft-ngram_amd/build.py` "
+            "(or __graft_entry__.build()); there is no CPU fallback")
+    lib = ctypes.CDLL(str(p))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+class EgError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"engraft_ngram error {code}: {message}")
+        self.code = code
+
+
+def check(code: int) -> None:
+    if code != EG_OK:
+        msg = load().eg_last_error()
+        msg = msg.decode() if msg else ""
+        if code == EG_ERR_ARG:
+            raise ValueError(msg)
+        raise EgError(code, msg)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))
+
+
+def stream_ptr(device=None) -> int:
+    import torch
+
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None for None)."""
+    if t is None:
+        return None
+    return int(t.data_ptr())

@@ -1,0 +1,250 @@
+// Device-side building blocks shared by the gfx950 kernels of the n-gram table
+// path: the row hash, the unsigned 64-by-32-bit modulus, row-format decoders
+// and rounding helpers.  Everything here is integer or exact fp32 arithmetic, so
+// the kernels reproduce the CPU definitions bit for bit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "engraft_ngram.h"
+
+namespace eg {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Hash parameters as a kernel argument.
+// ---------------------------------------------------------------------------
+struct LayerHash {
+  uint64_t eos;
+  int32_t ngram_size;
+  int32_t heads_per_ngram;
+  int32_t n_heads;
+  int32_t pad_;
+  uint64_t mult[EG_MAX_NGRAM];       // shared multipliers (reference mode)
+  const uint64_t* head_mult;         // device [n_heads][ngram_size] or nullptr
+  uint64_t magic[EG_MAX_HEADS];      // floor((2^64 - 1) / vocab[h])
+  uint32_t vocab[EG_MAX_HEADS];
+  int32_t offset[EG_MAX_HEADS];
+};
+
+// x mod p for p in [1, 2^32).  magic = floor((2^64-1)/p) gives
+// q = floor(x*magic / 2^64) in [floor(x/p) - 2, floor(x/p)], so the remainder
+// x - q*p lies in [0, 3p): at most two corrections.
+__host__ __device__ inline uint32_t fastmod_u64(uint64_t x, uint32_t p, uint64_t magic) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  uint64_t q = __umul64hi(x, magic);
+#else
+  uint64_t q = (uint64_t)(((unsigned __int128)x * magic) >> 64);
+#endif
+  uint64_t r = x - q * (uint64_t)p;
+  if (r >= p) r -= p;
+  if (r >= p) r -= p;
+  return (uint32_t)r;
+}
+
+// ctx = [x_t, x_{t-1}, ...]: a predecessor before the segment start, or an EOS
+// met while walking back, sets its slot and every older slot to the EOS id; the
+// current token's own EOS does not cut (engraft/table.py:121-131).
+__device__ inline void build_ctx(const LayerHash& L, const int64_t* __restrict__ tokens,
+                                 int64_t p, int64_t seg0, uint64_t ctx[EG_MAX_NGRAM]) {
+  ctx[0] = (uint64_t)tokens[p];
+  bool cut = false;
+#pragma unroll
+  for (int s = 1; s < EG_MAX_NGRAM; ++s) {
+    uint64_t tok = L.eos;
+    if (s < L.ngram_size) {
+      const int64_t pos = p - s;
+      if (!cut && pos >= seg0) tok = (uint64_t)tokens[pos];
+      if (cut || pos < seg0 || tok == L.eos) {
+        cut = true;
+        tok = L.eos;
+      }
+    }
+    ctx[s] = tok;
+  }
+}
+
+// Global row of head h: offset + (XOR_{j<order} ctx[j]*m[j]) mod vocab.
+__device__ inline int32_t head_row(const LayerHash& L, int h, const uint64_t ctx[EG_MAX_NGRAM],
+                                   bool global_ids) {
+  const int order = 2 + h / L.heads_per_ngram;
+  uint64_t mixed = 0;
+  if (L.head_mult) {
+    const uint64_t* m = L.head_mult + (int64_t)h * L.ngram_size;
+#pragma unroll
+    for (int j = 0; j < EG_MAX_NGRAM; ++j)
+      if (j < order) mixed ^= ctx[j] * m[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < EG_MAX_NGRAM; ++j)
+      if (j < order) mixed ^= ctx[j] * L.mult[j];
+  }
+  const uint32_t local = fastmod_u64(mixed, L.vocab[h], L.magic[h]);
+  return global_ids ? L.offset[h] + (int32_t)local : (int32_t)local;
+}
+
+// Segment start of flat position p.
+// (A caller-supplied start below 0 is read as 0: the hash never reads before
+// the token array.)
+__device__ inline int64_t seg_start_of(int64_t p, int64_t seq_len, const int32_t* seg_start) {
+  if (seg_start) return seg_start[p] < 0 ? 0 : seg_start[p];
+  if (seq_len > 0) return (p / seq_len) * seq_len;
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Number formats
+// ---------------------------------------------------------------------------
+__device__ inline float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// Round to nearest even; NaN stays a quiet NaN.
+__host__ __device__ inline uint32_t f32_to_bf16(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  uint32_t u = __float_as_uint(f);
+#else
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+#endif
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ inline float f16_to_f32(uint16_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, h);
+  return (float)v;
+}
+
+__device__ inline uint16_t f32_to_f16(float f) {
+  _Float16 v = (_Float16)f;  // round to nearest even
+  return __builtin_bit_cast(uint16_t, v);
+}
+
+// OCP e4m3 (float8_e4m3fn): bias 7, subnormals m*2^-9, 0x7f/0xff NaN.
+__device__ inline float e4m3_to_f32(uint32_t b) {
+  const uint32_t e = (b >> 3) & 0xfu, m = b & 7u;
+  float v;
+  if ((b & 0x7fu) == 0x7fu) {
+    v = __uint_as_float(0x7fc00000u);
+  } else if (e == 0) {
+    v = (float)m * 0.001953125f;  // 2^-9
+  } else {
+    v = __uint_as_float(((e + 120u) << 23) | (m << 20));  // (1+m/8)*2^(e-7)
+  }
+  return (b & 0x80u) ? -v : v;
+}
+
+// e8m0 scale 2^(e-127); 0xff is NaN.
+__device__ inline float e8m0_to_f32(uint32_t e) {
+  if (e == 0xffu) return __uint_as_float(0x7fc00000u);
+  if (e == 0) return __uint_as_float(0x00400000u);  // 2^-127 (subnormal)
+  return __uint_as_float(e << 23);
+}
+
+// RNE fp32 -> e4m3 for |x| <= 448 (callers clamp); the sign bit is kept.
+__device__ inline uint32_t f32_to_e4m3(float x) {
+  const uint32_t sign = (__float_as_uint(x) >> 24) & 0x80u;
+  const float a = fabsf(x);
+  uint32_t code;
+  if (a < 0.015625f) {                      // below 2^-6: subnormal grid m*2^-9
+    code = (uint32_t)rintf(a * 512.0f);     // 0..8; 8 is the smallest normal
+  } else {
+    int e = (int)((__float_as_uint(a) >> 23) & 0xffu) - 127;  // floor(log2 a), -6..8
+    const float mant = __uint_as_float((__float_as_uint(a) & 0x807fffffu) | 0x3f800000u);
+    uint32_t m = (uint32_t)rintf((mant - 1.0f) * 8.0f);
+    if (m == 8u) { m = 0u; ++e; }
+    code = ((uint32_t)(e + 7) << 3) | m;
+  }
+  return code | sign;
+}
+
+// IQ4_NL codebook (GGML kvalues_iq4nl; engraft/table.py:26-29).
+__device__ inline float iq4nl_value(uint32_t nib) {
+  constexpr int8_t kv[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                             1,    13,   25,  38,  53,  69,  89,  113};
+  return (float)kv[nib & 15u];
+}
+
+// ---------------------------------------------------------------------------
+// Row chunk loads: 8 consecutive values [off, off+8) of a row, dequantised to
+// fp32.  off is a multiple of 8, so a chunk never straddles a 32-value block.
+// ---------------------------------------------------------------------------
+struct TableDev {
+  const uint8_t* payload;
+  const uint8_t* scales;
+  int64_t n_rows;
+  int32_t fmt;
+  int32_t dim;
+};
+
+template <int FMT>
+__device__ inline void load_chunk(const TableDev& t, int dim, int64_t row, int off, float v[8]) {
+  if constexpr (FMT == EG_FMT_Q8_0) {
+    const u32x2 q = *(const u32x2*)(t.payload + row * dim + off);
+    const float d = f16_to_f32(*(const uint16_t*)(t.scales + (row * (dim >> 5) + (off >> 5)) * 2));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w = q[i >> 2];
+      v[i] = (float)(int8_t)(w >> ((i & 3) * 8)) * d;
+    }
+  } else if constexpr (FMT == EG_FMT_BF16) {
+    const u32x4 q = *(const u32x4*)(t.payload + (row * dim + off) * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(q[i] << 16);
+      v[2 * i + 1] = __uint_as_float(q[i] & 0xffff0000u);
+    }
+  } else if constexpr (FMT == EG_FMT_MXFP8) {
+    const u32x2 q = *(const u32x2*)(t.payload + row * dim + off);
+    const float s = e8m0_to_f32(t.scales[row * (dim >> 5) + (off >> 5)]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = e4m3_to_f32((q[i >> 2] >> ((i & 3) * 8)) & 0xffu) * s;
+  } else if constexpr (FMT == EG_FMT_IQ4_NL) {
+    // 18-byte blocks: fp16 d, then 16 bytes of nibbles; value j < 16 is the low
+    // nibble of byte j, value j >= 16 the high nibble of byte j-16.
+    const uint8_t* blk = t.payload + row * (int64_t)((dim >> 5) * 18) + (off >> 5) * 18;
+    const float d = f16_to_f32(*(const uint16_t*)blk);
+    const int j = off & 31;
+    const uint16_t* qs = (const uint16_t*)(blk + 2 + (j & 15));
+    const int sh = (j >= 16) ? 4 : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t w = qs[i];
+      v[2 * i] = iq4nl_value((w >> sh) & 15u) * d;
+      v[2 * i + 1] = iq4nl_value((w >> (8 + sh)) & 15u) * d;
+    }
+  } else {  // EG_FMT_F32
+    const u32x4* src = (const u32x4*)(t.payload + (row * dim + off) * 4);
+    const u32x4 a = src[0], b = src[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = __uint_as_float(a[i]);
+      v[4 + i] = __uint_as_float(b[i]);
+    }
+  }
+}
+
+// Runtime-format variant (overlay rows).
+__device__ inline void load_chunk_rt(const TableDev& t, int64_t row, int off, float v[8]) {
+  switch (t.fmt) {
+    case EG_FMT_Q8_0: load_chunk<EG_FMT_Q8_0>(t, t.dim, row, off, v); break;
+    case EG_FMT_BF16: load_chunk<EG_FMT_BF16>(t, t.dim, row, off, v); break;
+    case EG_FMT_MXFP8: load_chunk<EG_FMT_MXFP8>(t, t.dim, row, off, v); break;
+    case EG_FMT_IQ4_NL: load_chunk<EG_FMT_IQ4_NL>(t, t.dim, row, off, v); break;
+    default: load_chunk<EG_FMT_F32>(t, t.dim, row, off, v); break;
+  }
+}
+
+// Index of `key` in the sorted array ids[0..n), or -1.
+__device__ inline int64_t sorted_find(const int32_t* __restrict__ ids, int64_t n, int32_t key) {
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (ids[mid] < key) lo = mid + 1; else hi = mid;
+  }
+  return (lo < n && ids[lo] == key) ? lo : -1;
+}
+
+}  // namespace eg

@@ -1,0 +1,373 @@
+// Forward half of the n-gram table path on gfx950: the row hash, the fused
+// hash -> gather -> dequant -> (overlay) -> residual-add kernel, and the gather
+// by explicit row ids.  All of it is HBM-bound integer/byte work: one
+// wavefront per position, 8 values per lane per 16-byte chunk, coalesced
+// row-segment reads, streaming (non-temporal) residual traffic so the L2 and
+// the Infinity Cache keep the Zipf-hot table rows.
+#include <string.h>
+
+#include "eg_common.h"
+
+namespace eg {
+
+// ---------------------------------------------------------------------------
+// Error reporting and argument translation
+// ---------------------------------------------------------------------------
+static thread_local char g_err[512];
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int make_layer_hash(const eg_hash_spec* s, LayerHash* L) {
+  EG_CHECK_ARG(s != nullptr, "hash spec is NULL");
+  EG_CHECK_ARG(s->ngram_size >= 2 && s->ngram_size <= EG_MAX_NGRAM,
+               "ngram_size=%d outside [2, %d]", s->ngram_size, EG_MAX_NGRAM);
+  EG_CHECK_ARG(s->heads_per_ngram >= 1, "heads_per_ngram=%d < 1", s->heads_per_ngram);
+  const int n_heads = (s->ngram_size - 1) * s->heads_per_ngram;
+  EG_CHECK_ARG(n_heads <= EG_MAX_HEADS, "n_heads=%d > %d", n_heads, EG_MAX_HEADS);
+  memset(L, 0, sizeof(*L));
+  L->eos = s->eos_token_id;
+  L->ngram_size = s->ngram_size;
+  L->heads_per_ngram = s->heads_per_ngram;
+  L->n_heads = n_heads;
+  for (int j = 0; j < EG_MAX_NGRAM; ++j) L->mult[j] = s->layer_multipliers[j];
+  L->head_mult = s->head_multipliers;
+  for (int h = 0; h < n_heads; ++h) {
+    const uint64_t p = s->head_vocab_sizes[h];
+    EG_CHECK_ARG(p >= 1 && p < (1ull << 32), "head_vocab_sizes[%d]=%llu outside [1, 2^32)", h,
+                 (unsigned long long)p);
+    const int64_t off = s->head_offsets[h];
+    EG_CHECK_ARG(off >= 0 && off + (int64_t)p <= 2147483647LL,
+                 "head %d: offset %lld + vocab %llu exceeds int32 global ids", h, (long long)off,
+                 (unsigned long long)p);
+    L->vocab[h] = (uint32_t)p;
+    L->magic[h] = UINT64_MAX / p;
+    L->offset[h] = (int32_t)off;
+  }
+  return EG_OK;
+}
+
+int make_table(const eg_table* t, TableDev* out, const char* what) {
+  EG_CHECK_ARG(t != nullptr, "%s: table is NULL", what);
+  EG_CHECK_ARG(t->dim > 0 && t->dim % 32 == 0 && t->dim <= 512, "%s: dim=%d must be a multiple of 32 in [32, 512]",
+               what, t->dim);
+  EG_CHECK_ARG(t->fmt >= EG_FMT_BF16 && t->fmt <= EG_FMT_F32, "%s: unknown row format %d", what, t->fmt);
+  EG_CHECK_ARG(t->payload != nullptr || t->n_rows == 0, "%s: payload is NULL", what);
+  const bool scaled = t->fmt == EG_FMT_Q8_0 || t->fmt == EG_FMT_MXFP8;
+  EG_CHECK_ARG(!scaled || t->scales != nullptr || t->n_rows == 0, "%s: format %d needs scales", what, t->fmt);
+  EG_CHECK_ARG(t->n_rows >= 0, "%s: n_rows < 0", what);
+  out->payload = (const uint8_t*)t->payload;
+  out->scales = (const uint8_t*)t->scales;
+  out->n_rows = t->n_rows;
+  out->fmt = t->fmt;
+  out->dim = t->dim;
+  return EG_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Hash: one thread per (position, head)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void hash_kernel(const LayerHash L, const int64_t* __restrict__ tokens,
+                                                   int64_t n_pos, int64_t seq_len,
+                                                   const int32_t* __restrict__ seg_start, int32_t global_ids,
+                                                   int32_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n_pos * L.n_heads) return;
+  const int64_t p = i / L.n_heads;
+  const int h = (int)(i - p * L.n_heads);
+  uint64_t ctx[EG_MAX_NGRAM];
+  build_ctx(L, tokens, p, seg_start_of(p, seq_len, seg_start), ctx);
+  out[i] = head_row(L, h, ctx, global_ids != 0);
+}
+
+// ---------------------------------------------------------------------------
+// Fused forward: one wavefront per position
+// ---------------------------------------------------------------------------
+struct OverlayDev {
+  const int32_t* ids;
+  const int32_t* index;
+  int64_t n;
+  TableDev rows;
+};
+
+struct FwdArgs {
+  LayerHash hash[EG_MAX_LAYERS];
+  TableDev table[EG_MAX_LAYERS];
+  OverlayDev ov[EG_MAX_LAYERS];
+  const int64_t* tokens;    // hash mode
+  const int32_t* rows_in;   // gather mode: [n_pos, heads] global ids
+  const int32_t* seg_start;
+  const uint16_t* residual; // bf16 [n_pos, W] or nullptr
+  void* out;
+  int32_t* rows_out;
+  int64_t seq_len;
+  int64_t n_pos;
+  int32_t n_layers;
+  int32_t heads;
+  int32_t dim;
+  int32_t nch;              // 8-value chunks per lane: ceil(W / 512)
+};
+
+constexpr int kMaxChunks = 8;  // W <= 4096
+constexpr int kWavesPerBlock = 4;
+
+// NCH: 8-value chunks per lane (exact for the specialised shapes, an upper
+// bound for the generic kernel); OVL: overlay lookups compiled in.
+template <int FMT, int DIM, int NCH, bool F32OUT, bool OVL>
+__global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t p = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (p >= a.n_pos) return;  // uniform per wavefront
+  const int dim = DIM ? DIM : a.dim;
+  const int H = a.heads;
+  const int W = H * dim;
+
+  // The residual stream is read once: issue its loads first (they do not
+  // depend on the hash) and keep them out of the caches.
+  float acc[NCH][8];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e0 = (lane + 64 * c) * 8;
+    if (a.residual != nullptr && e0 < W) {
+      const u32x4 r = __builtin_nontemporal_load((const u32x4*)(a.residual + p * W + e0));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[c][2 * i] = __uint_as_float(r[i] << 16);
+        acc[c][2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[c][i] = -0.0f;  // -0 + x == x for every x
+    }
+  }
+
+  for (int l = 0; l < a.n_layers; ++l) {
+    const LayerHash& L = a.hash[l];
+    int32_t rid = 0;
+    if (lane < H) {
+      if (a.rows_in != nullptr) {
+        rid = a.rows_in[p * H + lane];
+      } else {
+        uint64_t ctx[EG_MAX_NGRAM];
+        build_ctx(L, a.tokens, p, seg_start_of(p, a.seq_len, a.seg_start), ctx);
+        rid = head_row(L, lane, ctx, true);
+      }
+      if (a.rows_out != nullptr) a.rows_out[((int64_t)l * a.n_pos + p) * H + lane] = rid;
+    }
+    int32_t ovk = -1;
+    const OverlayDev& ov = a.ov[l];
+    if constexpr (OVL) {
+      if (ov.n > 0 && lane < H) {
+        const int64_t k = sorted_find(ov.ids, ov.n, rid);
+        if (k >= 0) ovk = ov.index ? ov.index[k] : (int32_t)k;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int e0 = (lane + 64 * c) * 8;
+      const int h = min(e0, W - 8) / dim;
+      const int32_t row = __shfl(rid, h);
+      int32_t k = -1;
+      if constexpr (OVL) k = __shfl(ovk, h);
+      if (e0 < W) {
+        const int off = e0 - h * dim;
+        float v[8];
+        // Row ids handed in by the caller (gather mode) and overlay indices
+        // are checked here: an id outside the table reads NaN, never memory.
+        if (OVL && k >= 0) {
+          if (k < ov.rows.n_rows) {
+            load_chunk_rt(ov.rows, k, off, v);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(0x7fc00000u);
+          }
+        } else if ((uint32_t)row < (uint64_t)a.table[l].n_rows) {
+          load_chunk<FMT>(a.table[l], dim, row, off, v);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(0x7fc00000u);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[c][i] += v[i];
+      }
+    }
+  }
+
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e0 = (lane + 64 * c) * 8;
+    if (e0 < W) {
+      if constexpr (F32OUT) {
+        u32x4* dst = (u32x4*)((float*)a.out + p * W + e0);
+        u32x4 lo, hi;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lo[i] = __float_as_uint(acc[c][i]);
+          hi[i] = __float_as_uint(acc[c][4 + i]);
+        }
+        dst[0] = lo;
+        dst[1] = hi;
+      } else {
+        u32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = f32_to_bf16(acc[c][2 * i]) | (f32_to_bf16(acc[c][2 * i + 1]) << 16);
+        __builtin_nontemporal_store(o, (u32x4*)((uint16_t*)a.out + p * W + e0));
+      }
+    }
+  }
+}
+
+#define EG_LAUNCH(...) hipLaunchKernelGGL((forward_kernel<__VA_ARGS__>), grid, dim3(256), 0, st, a)
+
+// Specialised residual-add shapes: dim 128 with 16 (W = 2048) or 24 (W = 3072)
+// heads; everything else goes through the generic kernel.
+template <int FMT>
+static bool launch_special(const FwdArgs& a, bool ovl, dim3 grid, hipStream_t st) {
+  if (a.dim != 128) return false;
+  if (a.nch == 4) {
+    if (ovl) EG_LAUNCH(FMT, 128, 4, false, true); else EG_LAUNCH(FMT, 128, 4, false, false);
+    return true;
+  }
+  if (a.nch == 6) {
+    if (ovl) EG_LAUNCH(FMT, 128, 6, false, true); else EG_LAUNCH(FMT, 128, 6, false, false);
+    return true;
+  }
+  return false;
+}
+
+template <bool F32OUT>
+static int launch_forward(const FwdArgs& a, hipStream_t st) {
+  if (a.n_pos == 0) return EG_OK;
+  const dim3 grid((unsigned)((a.n_pos + kWavesPerBlock - 1) / kWavesPerBlock));
+  bool ovl = false;
+  for (int l = 0; l < a.n_layers; ++l) ovl = ovl || a.ov[l].n > 0;
+  const int fmt = a.table[0].fmt;
+  if (!F32OUT) {
+    bool done = false;
+    if (fmt == EG_FMT_Q8_0) done = launch_special<EG_FMT_Q8_0>(a, ovl, grid, st);
+    else if (fmt == EG_FMT_BF16) done = launch_special<EG_FMT_BF16>(a, ovl, grid, st);
+    else if (fmt == EG_FMT_MXFP8) done = launch_special<EG_FMT_MXFP8>(a, ovl, grid, st);
+    if (done) return launch_status("forward_kernel");
+  }
+  switch (fmt) {
+    case EG_FMT_Q8_0: EG_LAUNCH(EG_FMT_Q8_0, 0, kMaxChunks, F32OUT, true); break;
+    case EG_FMT_BF16: EG_LAUNCH(EG_FMT_BF16, 0, kMaxChunks, F32OUT, true); break;
+    case EG_FMT_MXFP8: EG_LAUNCH(EG_FMT_MXFP8, 0, kMaxChunks, F32OUT, true); break;
+    case EG_FMT_IQ4_NL: EG_LAUNCH(EG_FMT_IQ4_NL, 0, kMaxChunks, F32OUT, true); break;
+    case EG_FMT_F32: EG_LAUNCH(EG_FMT_F32, 0, kMaxChunks, F32OUT, true); break;
+    default: return set_error(EG_ERR_UNSUPPORTED, "row format %d", fmt);
+  }
+  return launch_status("forward_kernel");
+}
+
+#undef EG_LAUNCH
+
+static int fill_overlay(const eg_overlay* o, const TableDev& base, OverlayDev* out) {
+  memset(out, 0, sizeof(*out));
+  if (o == nullptr || o->n == 0) return EG_OK;
+  EG_CHECK_ARG(o->n > 0 && o->ids != nullptr, "overlay: n=%lld with NULL ids", (long long)o->n);
+  int rc = make_table(&o->rows, &out->rows, "overlay rows");
+  if (rc != EG_OK) return rc;
+  EG_CHECK_ARG(o->rows.dim == base.dim, "overlay dim %d != table dim %d", o->rows.dim, base.dim);
+  EG_CHECK_ARG(o->index != nullptr || o->rows.n_rows >= o->n, "overlay: %lld ids but %lld rows",
+               (long long)o->n, (long long)o->rows.n_rows);
+  out->ids = o->ids;
+  out->index = o->index;
+  out->n = o->n;
+  return EG_OK;
+}
+
+}  // namespace eg
+
+using namespace eg;
+
+extern "C" {
+
+const char* eg_last_error(void) { return g_err; }
+
+int eg_abi_version(void) { return EG_ABI_VERSION; }
+
+int eg_hash_rows(const eg_hash_spec* spec, const int64_t* tokens, int64_t n_pos, int64_t seq_len,
+                 const int32_t* seg_start, int32_t global_ids, int32_t* rows_out, void* stream) {
+  LayerHash L;
+  int rc = make_layer_hash(spec, &L);
+  if (rc != EG_OK) return rc;
+  EG_CHECK_ARG(n_pos >= 0, "n_pos < 0");
+  if (n_pos == 0) return EG_OK;
+  EG_CHECK_ARG(tokens != nullptr && rows_out != nullptr, "tokens/rows_out is NULL");
+  const int64_t n = n_pos * L.n_heads;
+  hipLaunchKernelGGL(hash_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, L,
+                     tokens, n_pos, seq_len, seg_start, global_ids, rows_out);
+  return launch_status("hash_kernel");
+}
+
+int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables, const eg_overlay* overlays,
+               const int64_t* tokens, int64_t n_pos, int64_t seq_len, const int32_t* seg_start,
+               const uint16_t* residual, void* out, int32_t* rows_out, void* stream) {
+  EG_CHECK_ARG(n_layers >= 1 && n_layers <= EG_MAX_LAYERS, "n_layers=%d outside [1, %d]", n_layers,
+               EG_MAX_LAYERS);
+  EG_CHECK_ARG(specs != nullptr && tables != nullptr, "specs/tables is NULL");
+  EG_CHECK_ARG(n_pos >= 0, "n_pos < 0");
+  EG_CHECK_ARG(n_pos == 0 || (tokens != nullptr && out != nullptr), "tokens/out is NULL");
+  FwdArgs a;
+  memset(&a, 0, sizeof(a));
+  for (int l = 0; l < n_layers; ++l) {
+    int rc = make_layer_hash(&specs[l], &a.hash[l]);
+    if (rc != EG_OK) return rc;
+    rc = make_table(&tables[l], &a.table[l], "table");
+    if (rc != EG_OK) return rc;
+    EG_CHECK_ARG(tables[l].fmt == tables[0].fmt && tables[l].dim == tables[0].dim,
+                 "layer %d: format/dim differ from layer 0", l);
+    EG_CHECK_ARG(a.hash[l].n_heads == a.hash[0].n_heads, "layer %d: n_heads differ from layer 0", l);
+    for (int h = 0; h < a.hash[l].n_heads; ++h)
+      EG_CHECK_ARG((int64_t)a.hash[l].offset[h] + a.hash[l].vocab[h] <= tables[l].n_rows,
+                   "layer %d head %d: rows [%d, %lld) exceed the table's %lld rows", l, h, a.hash[l].offset[h],
+                   (long long)a.hash[l].offset[h] + a.hash[l].vocab[h], (long long)tables[l].n_rows);
+    rc = fill_overlay(overlays ? &overlays[l] : nullptr, a.table[l], &a.ov[l]);
+    if (rc != EG_OK) return rc;
+  }
+  a.tokens = tokens;
+  a.seg_start = seg_start;
+  a.residual = residual;
+  a.out = out;
+  a.rows_out = rows_out;
+  a.seq_len = seq_len;
+  a.n_pos = n_pos;
+  a.n_layers = n_layers;
+  a.heads = a.hash[0].n_heads;
+  a.dim = tables[0].dim;
+  const int W = a.heads * a.dim;
+  EG_CHECK_ARG(W <= 512 * kMaxChunks, "row width %d > %d", W, 512 * kMaxChunks);
+  a.nch = (W + 511) / 512;
+  return residual ? launch_forward<false>(a, (hipStream_t)stream) : launch_forward<true>(a, (hipStream_t)stream);
+}
+
+int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* rows, int64_t n_pos, int32_t heads,
+              float* out, void* stream) {
+  EG_CHECK_ARG(heads >= 1 && heads <= EG_MAX_HEADS, "heads=%d outside [1, %d]", heads, EG_MAX_HEADS);
+  EG_CHECK_ARG(n_pos >= 0, "n_pos < 0");
+  EG_CHECK_ARG(n_pos == 0 || (rows != nullptr && out != nullptr), "rows/out is NULL");
+  FwdArgs a;
+  memset(&a, 0, sizeof(a));
+  int rc = make_table(table, &a.table[0], "table");
+  if (rc != EG_OK) return rc;
+  rc = fill_overlay(overlay, a.table[0], &a.ov[0]);
+  if (rc != EG_OK) return rc;
+  a.rows_in = rows;
+  a.out = out;
+  a.n_pos = n_pos;
+  a.n_layers = 1;
+  a.heads = heads;
+  a.dim = table->dim;
+  const int W = heads * a.dim;
+  EG_CHECK_ARG(W <= 512 * kMaxChunks, "row width %d > %d", W, 512 * kMaxChunks);
+  a.nch = (W + 511) / 512;
+  return launch_forward<true>(a, (hipStream_t)stream);
+}
+
+}  // extern "C"

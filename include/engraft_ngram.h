@@ -1,0 +1,134 @@
+/*
+ * engraft_ngram.h -- C ABI of the MI355X (gfx950) Engram/PLE n-gram table path.
+ *
+ * Plain C: device pointers and sizes, an explicit hipStream_t passed as void*,
+ * an int status (EG_OK == 0, negative on error; eg_last_error() gives the
+ * message of the calling thread's last failure).  No entry point allocates
+ * device memory except where stated; every buffer is caller-owned.  Calls are
+ * asynchronous on `stream` and never synchronise unless stated.
+ *
+ * Reference interfaces replaced (fulvian/engraft-ngram, Python):
+ *   eg_hash_rows     PleTable.ngram_addresses        engraft/table.py:111-144
+ *                    (+ local_to_global              engraft/lens.py:108-110,
+ *                     vectorized ngram_rows          engraft/damage.py:68-104)
+ *   eg_gather        PleTable.read_rows(_raw) + dequant_iq4nl
+ *                                                    engraft/table.py:90-109,147-169
+ *                    _read_true_rows                 engraft/replica/distill.py:378-395
+ *   eg_forward       RowSet.from_position per position + overlay substitution
+ *                    + the residual consumer         engraft/lens.py:126-136,
+ *                                                    engraft/replica/model.py:473-495,845-853,
+ *                                                    engraft/replica/seq.py:372-444
+ *   eg_scatter_grad  autograd of rows_var[idx_r] + index_put (accumulate)
+ *                                                    engraft/replica/seq.py:433-441
+ *   eg_descent_step  scatter + torch.optim.Adam step on the overlay rows
+ *                                                    engraft/descend_corpus.py:785-790,921-947
+ */
+#ifndef ENGRAFT_NGRAM_H
+#define ENGRAFT_NGRAM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EG_ABI_VERSION 1
+
+#define EG_MAX_NGRAM 4   /* context slots per hash (2-, 3- and 4-grams) */
+#define EG_MAX_HEADS 32  /* row slots per position and table layer */
+#define EG_MAX_LAYERS 2  /* table layers summed by one eg_forward */
+
+enum eg_status {
+  EG_OK = 0,
+  EG_ERR_ARG = -1,         /* invalid argument (shape, pointer, range) */
+  EG_ERR_HIP = -2,         /* a HIP runtime call failed */
+  EG_ERR_UNSUPPORTED = -3, /* valid but not built (format/dim combination) */
+  EG_ERR_WORKSPACE = -4    /* workspace too small */
+};
+
+enum eg_row_format {
+  EG_FMT_BF16 = 1,   /* payload bf16 [rows, dim]                                  */
+  EG_FMT_Q8_0 = 2,   /* payload int8 [rows, dim] + scales fp16 [rows, dim/32]     */
+  EG_FMT_MXFP8 = 3,  /* payload e4m3 [rows, dim] + scales e8m0 u8 [rows, dim/32]  */
+  EG_FMT_IQ4_NL = 4, /* payload u8 [rows, dim/32*18], GGML IQ4_NL blocks          */
+  EG_FMT_F32 = 5     /* payload f32 [rows, dim]                                   */
+};
+
+/* Hash parameters of one table layer (engraft/table.py:60-67).  Head h belongs
+ * to order n = 2 + h / heads_per_ngram and reads
+ *   global = head_offsets[h] + (XOR_{j<n} ctx[j]*mult_h[j] mod 2^64) % head_vocab_sizes[h]
+ * where ctx = [x_t, x_{t-1}, ...] with the reference's EOS rule.  mult_h is
+ * layer_multipliers (the reference's mode) unless head_multipliers is given. */
+typedef struct eg_hash_spec {
+  uint64_t eos_token_id;
+  int32_t ngram_size;                    /* 2..EG_MAX_NGRAM                       */
+  int32_t heads_per_ngram;               /* n_heads = (ngram_size-1)*heads_per_ngram */
+  uint64_t layer_multipliers[EG_MAX_NGRAM];
+  const uint64_t* head_multipliers;      /* DEVICE pointer [n_heads][ngram_size] or NULL */
+  uint64_t head_vocab_sizes[EG_MAX_HEADS]; /* each in [1, 2^32)                   */
+  int64_t head_offsets[EG_MAX_HEADS];    /* offset + vocab <= 2^31 - 1            */
+} eg_hash_spec;
+
+/* A table (or an overlay's row store) resident in device memory; rows are
+ * indexed by global row id. */
+typedef struct eg_table {
+  int32_t fmt;          /* eg_row_format */
+  int32_t dim;          /* values per row, a multiple of 32, <= 512 */
+  int64_t n_rows;
+  const void* payload;  /* device */
+  const void* scales;   /* device; Q8_0 and MXFP8 only, NULL otherwise */
+} eg_table;
+
+/* Replacement rows resolved per id (engraft/replica/model.py:473-495):
+ * a slot whose global row equals ids[k] reads row index[k] (or k when index is
+ * NULL) of `rows` instead of the base table. */
+typedef struct eg_overlay {
+  int64_t n;            /* 0: no overlay */
+  const int32_t* ids;   /* device, sorted ascending, unique */
+  const int32_t* index; /* device or NULL */
+  eg_table rows;        /* rows.dim must equal the base table's dim */
+} eg_overlay;
+
+const char* eg_last_error(void);
+int eg_abi_version(void);
+
+/* Row ids of every position of a flat token stream.
+ * tokens int64 [n_pos]; the hash context of position p never reaches before
+ * its segment start: seg_start[p] when seg_start != NULL, otherwise
+ * (p / seq_len) * seq_len (seq_len <= 0: one sequence).
+ * rows_out int32 [n_pos, n_heads]; global_ids = 0 gives local rows. */
+int eg_hash_rows(const eg_hash_spec* spec, const int64_t* tokens, int64_t n_pos,
+                 int64_t seq_len, const int32_t* seg_start, int32_t global_ids,
+                 int32_t* rows_out, void* stream);
+
+/* Fused forward over n_layers (1..EG_MAX_LAYERS) table layers with the same
+ * n_heads and dim (W = n_heads*dim):
+ *   residual != NULL: out bf16 [n_pos, W] = bf16_rne(f32(residual) + emb_0 + ...)
+ *   residual == NULL: out f32  [n_pos, W] = emb_0 + ... (the OverlayEmb base)
+ * overlays: NULL or n_layers entries.  rows_out: NULL or int32
+ * [n_layers, n_pos, n_heads] global ids (for the backward).  out may alias
+ * residual (in-place residual update). */
+int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,
+               const eg_overlay* overlays, const int64_t* tokens, int64_t n_pos,
+               int64_t seq_len, const int32_t* seg_start, const uint16_t* residual,
+               void* out, int32_t* rows_out, void* stream);
+
+/* Gather by explicit global row ids: rows int32 [n_pos, heads] ->
+ * out f32 [n_pos, heads*dim] (dequantised, overlay resolved; NULL overlay = base). */
+int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* rows,
+              int64_t n_pos, int32_t heads, float* out, void* stream);
+
+/* Seeded synthetic table rows [row0, row0+n_rows) (benchmark/test inputs):
+ * value j of row r = qtable[mix64(seed*0xD1B54A32D192ED03 + r*dim + j) >> 50]
+ * (qtable f32 [16384], device), quantised with the format's rule
+ * (BF16: RNE; Q8_0: d = fp16(amax/127), q = rint(x/d); MXFP8: e4m3 with the
+ * smallest shared exponent e that keeps amax*2^-e <= 448). */
+int eg_synth_table(const eg_table* table, uint64_t seed, const float* qtable,
+                   int64_t row0, int64_t n_rows, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ENGRAFT_NGRAM_H */
