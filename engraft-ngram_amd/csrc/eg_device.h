@@ -45,20 +45,37 @@ __host__ __device__ inline uint32_t fastmod_u64(uint64_t x, uint32_t p, uint64_t
   return (uint32_t)r;
 }
 
+// Raw tokens x_t, x_{t-1}, ... of position p (indices clamped at 0; slots
+// before the segment start are discarded by ctx_from).  Loading them apart from
+// their use lets a kernel issue them before its bulk loads: vmcnt retires
+// vector memory operations in order, so a wait for the tokens then does not
+// wait for the bulk data.
+__device__ inline void load_ctx_tokens(const int64_t* __restrict__ tokens, int64_t p, int ngram_size,
+                                       uint64_t raw[EG_MAX_NGRAM]) {
+#pragma unroll
+  for (int s = 0; s < EG_MAX_NGRAM; ++s) {
+    raw[s] = 0;
+    if (s < ngram_size) {
+      const int64_t pos = p - s;
+      raw[s] = (uint64_t)tokens[pos < 0 ? 0 : pos];
+    }
+  }
+}
+
 // ctx = [x_t, x_{t-1}, ...]: a predecessor before the segment start, or an EOS
 // met while walking back, sets its slot and every older slot to the EOS id; the
 // current token's own EOS does not cut (engraft/table.py:121-131).
-__device__ inline void build_ctx(const LayerHash& L, const int64_t* __restrict__ tokens,
-                                 int64_t p, int64_t seg0, uint64_t ctx[EG_MAX_NGRAM]) {
-  ctx[0] = (uint64_t)tokens[p];
+__device__ inline void ctx_from(const LayerHash& L, const uint64_t raw[EG_MAX_NGRAM], int64_t p, int64_t seg0,
+                                uint64_t ctx[EG_MAX_NGRAM]) {
+  ctx[0] = raw[0];
   bool cut = false;
 #pragma unroll
   for (int s = 1; s < EG_MAX_NGRAM; ++s) {
     uint64_t tok = L.eos;
     if (s < L.ngram_size) {
-      const int64_t pos = p - s;
-      if (!cut && pos >= seg0) tok = (uint64_t)tokens[pos];
-      if (cut || pos < seg0 || tok == L.eos) {
+      const bool valid = !cut && p - s >= seg0;
+      if (valid) tok = raw[s];
+      if (!valid || tok == L.eos) {
         cut = true;
         tok = L.eos;
       }
@@ -67,23 +84,40 @@ __device__ inline void build_ctx(const LayerHash& L, const int64_t* __restrict__
   }
 }
 
+__device__ inline void build_ctx(const LayerHash& L, const int64_t* __restrict__ tokens, int64_t p, int64_t seg0,
+                                 uint64_t ctx[EG_MAX_NGRAM]) {
+  uint64_t raw[EG_MAX_NGRAM];
+  load_ctx_tokens(tokens, p, L.ngram_size, raw);
+  ctx_from(L, raw, p, seg0, ctx);
+}
+
+// Multipliers of head h (loaded ahead of use like the tokens).
+__device__ inline void load_head_mult(const LayerHash& L, int h, uint64_t m[EG_MAX_NGRAM]) {
+#pragma unroll
+  for (int j = 0; j < EG_MAX_NGRAM; ++j) {
+    m[j] = L.mult[j];
+    if (L.head_mult && j < L.ngram_size) m[j] = L.head_mult[(int64_t)h * L.ngram_size + j];
+  }
+}
+
+// Global (or local) row of head h from its context and multipliers.
+__device__ inline int32_t row_of(const LayerHash& L, int h, const uint64_t ctx[EG_MAX_NGRAM],
+                                 const uint64_t m[EG_MAX_NGRAM], bool global_ids) {
+  const int order = 2 + h / L.heads_per_ngram;
+  uint64_t mixed = 0;
+#pragma unroll
+  for (int j = 0; j < EG_MAX_NGRAM; ++j)
+    if (j < order) mixed ^= ctx[j] * m[j];
+  const uint32_t local = fastmod_u64(mixed, L.vocab[h], L.magic[h]);
+  return global_ids ? L.offset[h] + (int32_t)local : (int32_t)local;
+}
+
 // Global row of head h: offset + (XOR_{j<order} ctx[j]*m[j]) mod vocab.
 __device__ inline int32_t head_row(const LayerHash& L, int h, const uint64_t ctx[EG_MAX_NGRAM],
                                    bool global_ids) {
-  const int order = 2 + h / L.heads_per_ngram;
-  uint64_t mixed = 0;
-  if (L.head_mult) {
-    const uint64_t* m = L.head_mult + (int64_t)h * L.ngram_size;
-#pragma unroll
-    for (int j = 0; j < EG_MAX_NGRAM; ++j)
-      if (j < order) mixed ^= ctx[j] * m[j];
-  } else {
-#pragma unroll
-    for (int j = 0; j < EG_MAX_NGRAM; ++j)
-      if (j < order) mixed ^= ctx[j] * L.mult[j];
-  }
-  const uint32_t local = fastmod_u64(mixed, L.vocab[h], L.magic[h]);
-  return global_ids ? L.offset[h] + (int32_t)local : (int32_t)local;
+  uint64_t m[EG_MAX_NGRAM];
+  load_head_mult(L, h, m);
+  return row_of(L, h, ctx, m, global_ids);
 }
 
 // Segment start of flat position p.
@@ -179,62 +213,102 @@ struct TableDev {
   int32_t dim;
 };
 
+// Raw bytes of one chunk, loaded apart from their decoding so that a kernel can
+// issue every load before it waits for any.
+struct RawChunk {
+  u32x4 w0;     // payload words (BF16: 8 values; Q8_0/MXFP8: .xy; IQ4_NL: 4 nibble halfwords)
+  u32x4 w1;     // F32 only: values 4..7
+  uint32_t s;   // scale bits (Q8_0/IQ4_NL: fp16; MXFP8: e8m0)
+};
+
 template <int FMT>
-__device__ inline void load_chunk(const TableDev& t, int dim, int64_t row, int off, float v[8]) {
-  if constexpr (FMT == EG_FMT_Q8_0) {
+__device__ inline RawChunk load_raw(const TableDev& t, int dim, int64_t row, int off) {
+  RawChunk r;
+  if constexpr (FMT == EG_FMT_Q8_0 || FMT == EG_FMT_MXFP8) {
     const u32x2 q = *(const u32x2*)(t.payload + row * dim + off);
-    const float d = f16_to_f32(*(const uint16_t*)(t.scales + (row * (dim >> 5) + (off >> 5)) * 2));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t w = q[i >> 2];
-      v[i] = (float)(int8_t)(w >> ((i & 3) * 8)) * d;
-    }
+    r.w0 = u32x4{q.x, q.y, 0u, 0u};
+    if constexpr (FMT == EG_FMT_Q8_0)
+      r.s = *(const uint16_t*)(t.scales + (row * (dim >> 5) + (off >> 5)) * 2);
+    else
+      r.s = t.scales[row * (dim >> 5) + (off >> 5)];
   } else if constexpr (FMT == EG_FMT_BF16) {
-    const u32x4 q = *(const u32x4*)(t.payload + (row * dim + off) * 2);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = __uint_as_float(q[i] << 16);
-      v[2 * i + 1] = __uint_as_float(q[i] & 0xffff0000u);
-    }
-  } else if constexpr (FMT == EG_FMT_MXFP8) {
-    const u32x2 q = *(const u32x2*)(t.payload + row * dim + off);
-    const float s = e8m0_to_f32(t.scales[row * (dim >> 5) + (off >> 5)]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = e4m3_to_f32((q[i >> 2] >> ((i & 3) * 8)) & 0xffu) * s;
+    r.w0 = *(const u32x4*)(t.payload + (row * dim + off) * 2);
   } else if constexpr (FMT == EG_FMT_IQ4_NL) {
     // 18-byte blocks: fp16 d, then 16 bytes of nibbles; value j < 16 is the low
     // nibble of byte j, value j >= 16 the high nibble of byte j-16.
     const uint8_t* blk = t.payload + row * (int64_t)((dim >> 5) * 18) + (off >> 5) * 18;
-    const float d = f16_to_f32(*(const uint16_t*)blk);
-    const int j = off & 31;
-    const uint16_t* qs = (const uint16_t*)(blk + 2 + (j & 15));
-    const int sh = (j >= 16) ? 4 : 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t w = qs[i];
-      v[2 * i] = iq4nl_value((w >> sh) & 15u) * d;
-      v[2 * i + 1] = iq4nl_value((w >> (8 + sh)) & 15u) * d;
-    }
+    r.s = *(const uint16_t*)blk;
+    const uint16_t* qs = (const uint16_t*)(blk + 2 + (off & 15));
+    r.w0 = u32x4{qs[0], qs[1], qs[2], qs[3]};
   } else {  // EG_FMT_F32
     const u32x4* src = (const u32x4*)(t.payload + (row * dim + off) * 4);
-    const u32x4 a = src[0], b = src[1];
+    r.w0 = src[0];
+    r.w1 = src[1];
+  }
+  return r;
+}
+
+template <int FMT>
+__device__ inline void decode(const RawChunk& r, int off, float v[8]) {
+  if constexpr (FMT == EG_FMT_Q8_0) {
+    const float d = f16_to_f32((uint16_t)r.s);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)(r.w0[i >> 2] >> ((i & 3) * 8)) * d;
+  } else if constexpr (FMT == EG_FMT_BF16) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      v[i] = __uint_as_float(a[i]);
-      v[4 + i] = __uint_as_float(b[i]);
+      v[2 * i] = __uint_as_float(r.w0[i] << 16);
+      v[2 * i + 1] = __uint_as_float(r.w0[i] & 0xffff0000u);
+    }
+  } else if constexpr (FMT == EG_FMT_MXFP8) {
+    const float sc = e8m0_to_f32(r.s);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = e4m3_to_f32((r.w0[i >> 2] >> ((i & 3) * 8)) & 0xffu) * sc;
+  } else if constexpr (FMT == EG_FMT_IQ4_NL) {
+    const float d = f16_to_f32((uint16_t)r.s);
+    const int sh = ((off & 31) >= 16) ? 4 : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = iq4nl_value((r.w0[i] >> sh) & 15u) * d;
+      v[2 * i + 1] = iq4nl_value((r.w0[i] >> (8 + sh)) & 15u) * d;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = __uint_as_float(r.w0[i]);
+      v[4 + i] = __uint_as_float(r.w1[i]);
     }
   }
 }
 
-// Runtime-format variant (overlay rows).
-__device__ inline void load_chunk_rt(const TableDev& t, int64_t row, int off, float v[8]) {
+template <int FMT>
+__device__ inline void load_chunk(const TableDev& t, int dim, int64_t row, int off, float v[8]) {
+  decode<FMT>(load_raw<FMT>(t, dim, row, off), off, v);
+}
+
+// Runtime-format variants (overlay rows).
+__device__ inline RawChunk load_raw_rt(const TableDev& t, int64_t row, int off) {
   switch (t.fmt) {
-    case EG_FMT_Q8_0: load_chunk<EG_FMT_Q8_0>(t, t.dim, row, off, v); break;
-    case EG_FMT_BF16: load_chunk<EG_FMT_BF16>(t, t.dim, row, off, v); break;
-    case EG_FMT_MXFP8: load_chunk<EG_FMT_MXFP8>(t, t.dim, row, off, v); break;
-    case EG_FMT_IQ4_NL: load_chunk<EG_FMT_IQ4_NL>(t, t.dim, row, off, v); break;
-    default: load_chunk<EG_FMT_F32>(t, t.dim, row, off, v); break;
+    case EG_FMT_Q8_0: return load_raw<EG_FMT_Q8_0>(t, t.dim, row, off);
+    case EG_FMT_BF16: return load_raw<EG_FMT_BF16>(t, t.dim, row, off);
+    case EG_FMT_MXFP8: return load_raw<EG_FMT_MXFP8>(t, t.dim, row, off);
+    case EG_FMT_IQ4_NL: return load_raw<EG_FMT_IQ4_NL>(t, t.dim, row, off);
+    default: return load_raw<EG_FMT_F32>(t, t.dim, row, off);
   }
+}
+
+__device__ inline void decode_rt(int fmt, const RawChunk& r, int off, float v[8]) {
+  switch (fmt) {
+    case EG_FMT_Q8_0: decode<EG_FMT_Q8_0>(r, off, v); break;
+    case EG_FMT_BF16: decode<EG_FMT_BF16>(r, off, v); break;
+    case EG_FMT_MXFP8: decode<EG_FMT_MXFP8>(r, off, v); break;
+    case EG_FMT_IQ4_NL: decode<EG_FMT_IQ4_NL>(r, off, v); break;
+    default: decode<EG_FMT_F32>(r, off, v); break;
+  }
+}
+
+__device__ inline void load_chunk_rt(const TableDev& t, int64_t row, int off, float v[8]) {
+  decode_rt(t.fmt, load_raw_rt(t, row, off), off, v);
 }
 
 // Index of `key` in the sorted array ids[0..n), or -1.

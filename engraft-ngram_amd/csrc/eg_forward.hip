@@ -118,7 +118,7 @@ constexpr int kWavesPerBlock = 4;
 
 // NCH: 8-value chunks per lane (exact for the specialised shapes, an upper
 // bound for the generic kernel); OVL: overlay lookups compiled in.
-template <int FMT, int DIM, int NCH, bool F32OUT, bool OVL>
+template <int FMT, int DIM, int NCH, int MAXL, bool F32OUT, bool OVL>
 __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t p = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
@@ -127,43 +127,66 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   const int H = a.heads;
   const int W = H * dim;
 
-  // The residual stream is read once: issue its loads first (they do not
-  // depend on the hash) and keep them out of the caches.
-  float acc[NCH][8];
+  // 1. Everything the row ids depend on (tokens, segment start, multipliers,
+  //    or the caller's row ids) is loaded first: vmcnt retires loads in issue
+  //    order, so the hash below then waits for these and not for the residual.
+  const int nl = a.n_layers;
+  uint64_t raw[EG_MAX_NGRAM];
+  uint64_t mult[EG_MAX_LAYERS][EG_MAX_NGRAM];
+  int64_t seg0 = 0;
+  int32_t rid[EG_MAX_LAYERS] = {0, 0};
+  static_assert(MAXL >= 1 && MAXL <= EG_MAX_LAYERS, "layer count");
+  const bool hashing = a.rows_in == nullptr;
+  if (lane < H) {
+    if (hashing) {
+      seg0 = seg_start_of(p, a.seq_len, a.seg_start);
+      int ng = a.hash[0].ngram_size;
+      if (MAXL > 1 && nl > 1 && a.hash[1].ngram_size > ng) ng = a.hash[1].ngram_size;
+      load_ctx_tokens(a.tokens, p, ng, raw);
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int e0 = (lane + 64 * c) * 8;
-    if (a.residual != nullptr && e0 < W) {
-      const u32x4 r = __builtin_nontemporal_load((const u32x4*)(a.residual + p * W + e0));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[c][2 * i] = __uint_as_float(r[i] << 16);
-        acc[c][2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
-      }
+      for (int l = 0; l < MAXL; ++l)
+        if (l < nl) load_head_mult(a.hash[l], lane, mult[l]);
     } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[c][i] = -0.0f;  // -0 + x == x for every x
+      rid[0] = a.rows_in[p * H + lane];
     }
   }
 
-  for (int l = 0; l < a.n_layers; ++l) {
-    const LayerHash& L = a.hash[l];
-    int32_t rid = 0;
-    if (lane < H) {
-      if (a.rows_in != nullptr) {
-        rid = a.rows_in[p * H + lane];
-      } else {
+  // 2. The residual stream is read once: streaming (non-temporal) loads.
+  u32x4 res[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e0 = (lane + 64 * c) * 8;
+    if (a.residual != nullptr && e0 < W)
+      res[c] = __builtin_nontemporal_load((const u32x4*)(a.residual + p * W + e0));
+    else
+      res[c] = u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};  // -0 + x == x for every x
+  }
+
+  // 3. Row ids of head `lane`, one per layer.
+  if (lane < H && hashing) {
+#pragma unroll
+    for (int l = 0; l < MAXL; ++l) {
+      if (l < nl) {
         uint64_t ctx[EG_MAX_NGRAM];
-        build_ctx(L, a.tokens, p, seg_start_of(p, a.seq_len, a.seg_start), ctx);
-        rid = head_row(L, lane, ctx, true);
+        ctx_from(a.hash[l], raw, p, seg0, ctx);
+        rid[l] = row_of(a.hash[l], lane, ctx, mult[l], true);
       }
-      if (a.rows_out != nullptr) a.rows_out[((int64_t)l * a.n_pos + p) * H + lane] = rid;
     }
+  }
+  // 4. Issue the table (or overlay) row loads of every layer and chunk.  Row
+  //    ids handed in by the caller (gather mode) and overlay indices are
+  //    checked: an id outside its table reads NaN, never memory.
+  RawChunk tr[MAXL][NCH];
+  uint32_t src[MAXL][NCH];  // 0: base table, 1: overlay, 2: invalid id
+#pragma unroll
+  for (int l = 0; l < MAXL; ++l) {
+    if (l >= nl) break;
+    if (lane < H && a.rows_out != nullptr) a.rows_out[((int64_t)l * a.n_pos + p) * H + lane] = rid[l];
     int32_t ovk = -1;
     const OverlayDev& ov = a.ov[l];
     if constexpr (OVL) {
       if (ov.n > 0 && lane < H) {
-        const int64_t k = sorted_find(ov.ids, ov.n, rid);
+        const int64_t k = sorted_find(ov.ids, ov.n, rid[l]);
         if (k >= 0) ovk = ov.index ? ov.index[k] : (int32_t)k;
       }
     }
@@ -171,30 +194,52 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
     for (int c = 0; c < NCH; ++c) {
       const int e0 = (lane + 64 * c) * 8;
       const int h = min(e0, W - 8) / dim;
-      const int32_t row = __shfl(rid, h);
+      const int32_t row = __shfl(rid[l], h);
       int32_t k = -1;
       if constexpr (OVL) k = __shfl(ovk, h);
+      const int off = e0 - h * dim;
+      src[l][c] = 2;
       if (e0 < W) {
-        const int off = e0 - h * dim;
-        float v[8];
-        // Row ids handed in by the caller (gather mode) and overlay indices
-        // are checked here: an id outside the table reads NaN, never memory.
         if (OVL && k >= 0) {
           if (k < ov.rows.n_rows) {
-            load_chunk_rt(ov.rows, k, off, v);
-          } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(0x7fc00000u);
+            tr[l][c] = load_raw_rt(ov.rows, k, off);
+            src[l][c] = 1;
           }
         } else if ((uint32_t)row < (uint64_t)a.table[l].n_rows) {
-          load_chunk<FMT>(a.table[l], dim, row, off, v);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(0x7fc00000u);
+          tr[l][c] = load_raw<FMT>(a.table[l], dim, row, off);
+          src[l][c] = 0;
         }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[c][i] += v[i];
       }
+    }
+  }
+
+  // 5. Residual + every layer, fp32, in layer order.
+  float acc[NCH][8];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[c][2 * i] = __uint_as_float(res[c][i] << 16);
+      acc[c][2 * i + 1] = __uint_as_float(res[c][i] & 0xffff0000u);
+    }
+#pragma unroll
+  for (int l = 0; l < MAXL; ++l) {
+    if (l >= nl) break;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int e0 = (lane + 64 * c) * 8;
+      const int off = e0 - (min(e0, W - 8) / dim) * dim;
+      float v[8];
+      if (src[l][c] == 0) {
+        decode<FMT>(tr[l][c], off, v);
+      } else if (OVL && src[l][c] == 1) {
+        decode_rt(a.ov[l].rows.fmt, tr[l][c], off, v);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(0x7fc00000u);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[c][i] += v[i];
     }
   }
 
@@ -225,19 +270,35 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
 #define EG_LAUNCH(...) hipLaunchKernelGGL((forward_kernel<__VA_ARGS__>), grid, dim3(256), 0, st, a)
 
 // Specialised residual-add shapes: dim 128 with 16 (W = 2048) or 24 (W = 3072)
-// heads; everything else goes through the generic kernel.
+// heads, one or two layers; everything else goes through the generic kernel.
+template <int FMT, int NCH>
+static void launch_special_nch(const FwdArgs& a, bool ovl, dim3 grid, hipStream_t st) {
+  if (a.n_layers == 1) {
+    if (ovl) EG_LAUNCH(FMT, 128, NCH, 1, false, true); else EG_LAUNCH(FMT, 128, NCH, 1, false, false);
+  } else {
+    if (ovl) EG_LAUNCH(FMT, 128, NCH, 2, false, true); else EG_LAUNCH(FMT, 128, NCH, 2, false, false);
+  }
+}
+
 template <int FMT>
 static bool launch_special(const FwdArgs& a, bool ovl, dim3 grid, hipStream_t st) {
   if (a.dim != 128) return false;
   if (a.nch == 4) {
-    if (ovl) EG_LAUNCH(FMT, 128, 4, false, true); else EG_LAUNCH(FMT, 128, 4, false, false);
+    launch_special_nch<FMT, 4>(a, ovl, grid, st);
     return true;
   }
   if (a.nch == 6) {
-    if (ovl) EG_LAUNCH(FMT, 128, 6, false, true); else EG_LAUNCH(FMT, 128, 6, false, false);
+    launch_special_nch<FMT, 6>(a, ovl, grid, st);
     return true;
   }
   return false;
+}
+
+// Any shape: runtime dim, up to kMaxChunks chunks, overlays compiled in.
+template <int FMT, bool F32OUT>
+static void launch_generic(const FwdArgs& a, dim3 grid, hipStream_t st) {
+  if (a.n_layers == 1) EG_LAUNCH(FMT, 0, kMaxChunks, 1, F32OUT, true);
+  else EG_LAUNCH(FMT, 0, kMaxChunks, 2, F32OUT, true);
 }
 
 template <bool F32OUT>
@@ -255,11 +316,11 @@ static int launch_forward(const FwdArgs& a, hipStream_t st) {
     if (done) return launch_status("forward_kernel");
   }
   switch (fmt) {
-    case EG_FMT_Q8_0: EG_LAUNCH(EG_FMT_Q8_0, 0, kMaxChunks, F32OUT, true); break;
-    case EG_FMT_BF16: EG_LAUNCH(EG_FMT_BF16, 0, kMaxChunks, F32OUT, true); break;
-    case EG_FMT_MXFP8: EG_LAUNCH(EG_FMT_MXFP8, 0, kMaxChunks, F32OUT, true); break;
-    case EG_FMT_IQ4_NL: EG_LAUNCH(EG_FMT_IQ4_NL, 0, kMaxChunks, F32OUT, true); break;
-    case EG_FMT_F32: EG_LAUNCH(EG_FMT_F32, 0, kMaxChunks, F32OUT, true); break;
+    case EG_FMT_Q8_0: launch_generic<EG_FMT_Q8_0, F32OUT>(a, grid, st); break;
+    case EG_FMT_BF16: launch_generic<EG_FMT_BF16, F32OUT>(a, grid, st); break;
+    case EG_FMT_MXFP8: launch_generic<EG_FMT_MXFP8, F32OUT>(a, grid, st); break;
+    case EG_FMT_IQ4_NL: launch_generic<EG_FMT_IQ4_NL, F32OUT>(a, grid, st); break;
+    case EG_FMT_F32: launch_generic<EG_FMT_F32, F32OUT>(a, grid, st); break;
     default: return set_error(EG_ERR_UNSUPPORTED, "row format %d", fmt);
   }
   return launch_status("forward_kernel");
