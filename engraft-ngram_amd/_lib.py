@@ -62,6 +62,31 @@ class EgOverlay(ctypes.Structure):
     ]
 
 
+class EgAdam(ctypes.Structure):
+    _fields_ = [
+        ("lr", ctypes.c_float),
+        ("beta1", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("eps", ctypes.c_float),
+        ("step", c_int64),
+        ("dense", c_int32),
+        ("l2_coef", ctypes.c_float),
+    ]
+
+
+class EgDescentState(ctypes.Structure):
+    _fields_ = [
+        ("n", c_int64),
+        ("dim", c_int32),
+        ("ids", c_void_p),
+        ("master", c_void_p),
+        ("m", c_void_p),
+        ("v", c_void_p),
+        ("stamp", c_void_p),
+        ("quant", EgTable),
+    ]
+
+
 # name -> (restype, argtypes); every symbol the header declares.
 SIGNATURES = {
     "eg_last_error": (c_char_p, []),
@@ -73,6 +98,11 @@ SIGNATURES = {
     "eg_gather": (c_int32, [POINTER(EgTable), POINTER(EgOverlay), c_void_p, c_int64, c_int32, c_void_p,
                             c_void_p]),
     "eg_synth_table": (c_int32, [POINTER(EgTable), c_uint64, c_void_p, c_int64, c_int64, c_void_p]),
+    "eg_backward_workspace_size": (ctypes.c_size_t, [c_int64]),
+    "eg_scatter_grad": (c_int32, [c_void_p, c_int32, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64,
+                                  c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
+    "eg_descent_step": (c_int32, [c_void_p, c_int32, c_void_p, c_int64, c_int32, POINTER(EgDescentState),
+                                  POINTER(EgAdam), POINTER(EgTable), c_void_p, ctypes.c_size_t, c_void_p]),
 }
 
 _LIB = None

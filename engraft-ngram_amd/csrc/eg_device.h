@@ -311,6 +311,28 @@ __device__ inline void load_chunk_rt(const TableDev& t, int64_t row, int off, fl
   decode_rt(t.fmt, load_raw_rt(t, row, off), off, v);
 }
 
+// One dequantised value: column `col` of row `row` (any format).
+__device__ inline float load_value_rt(const TableDev& t, int64_t row, int col) {
+  const int nb = t.dim >> 5;
+  switch (t.fmt) {
+    case EG_FMT_Q8_0:
+      return (float)(int8_t)t.payload[row * t.dim + col] *
+             f16_to_f32(((const uint16_t*)t.scales)[row * nb + (col >> 5)]);
+    case EG_FMT_BF16:
+      return __uint_as_float((uint32_t)((const uint16_t*)t.payload)[row * t.dim + col] << 16);
+    case EG_FMT_MXFP8:
+      return e4m3_to_f32(t.payload[row * t.dim + col]) * e8m0_to_f32(t.scales[row * nb + (col >> 5)]);
+    case EG_FMT_IQ4_NL: {
+      const uint8_t* blk = t.payload + row * (int64_t)(nb * 18) + (col >> 5) * 18;
+      const int j = col & 31;
+      const uint32_t byte = blk[2 + (j & 15)];
+      return iq4nl_value(j < 16 ? (byte & 15u) : (byte >> 4)) * f16_to_f32(*(const uint16_t*)blk);
+    }
+    default:
+      return ((const float*)t.payload)[row * t.dim + col];
+  }
+}
+
 // Index of `key` in the sorted array ids[0..n), or -1.
 __device__ inline int64_t sorted_find(const int32_t* __restrict__ ids, int64_t n, int32_t key) {
   int64_t lo = 0, hi = n;

@@ -1,0 +1,239 @@
+"""Descent on the overlay rows: the drop-in for the optimizer core of the
+reference (``engraft/replica/distill.py:378-453`` row variables,
+``engraft/descend_corpus.py:776-790, 921-947`` the step).
+
+* ``_read_true_rows`` / ``build_rows_var`` -- the variable rows and their start
+  values, read from the device table (same names, arguments and errors).
+* ``scatter_grad`` -- the gradient of the variables from ``d_out`` and the slot
+  row ids: the autograd of ``rows_var[idx_r]`` + ``index_put``
+  (``engraft/replica/seq.py:433-441``), computed by a stable radix sort of
+  (variable, slot) and a segmented reduction in ascending slot order on the
+  device -- bitwise repeatable.
+* ``DescentState`` -- ``rows_var`` (fp32 master rows), Adam moments and a
+  requantised copy in HBM; ``step`` runs scatter + Adam (torch's single-tensor
+  order, fp32) + requantisation in one call (``eg_descent_step``), in the
+  reference's dense mode (every variable steps, ``torch.optim.Adam([rows_var])``)
+  or the sparse mode of BASELINE config 2 (only the rows this batch hit).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import torch
+
+from . import _lib
+from .overlay import DeviceOverlay
+from .table import DeviceTable, RowStore
+
+_POLICIES = ("all-read", "private", "entity", "t8-answer")
+
+
+class _Workspace:
+    """Grow-only device workspace for the backward kernels (per device)."""
+
+    def __init__(self):
+        self._buf: dict[torch.device, torch.Tensor] = {}
+
+    def get(self, n_slots: int, device) -> torch.Tensor:
+        need = int(_lib.load().eg_backward_workspace_size(int(n_slots)))
+        dev = torch.device(device)
+        buf = self._buf.get(dev)
+        if buf is None or buf.numel() < need:
+            buf = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+            self._buf[dev] = buf
+        return buf
+
+
+_WS = _Workspace()
+
+
+def _dout_args(d_out: torch.Tensor):
+    if d_out.dtype == torch.bfloat16:
+        return 0
+    if d_out.dtype == torch.float32:
+        return 1
+    raise ValueError(f"d_out must be bf16 or f32, got {d_out.dtype}")
+
+
+def scatter_grad(d_out: torch.Tensor, rows: torch.Tensor, ids: torch.Tensor, dim: int,
+                 grad: torch.Tensor | None = None) -> torch.Tensor:
+    """Gradient of the variables ``ids`` (sorted unique int32 global rows):
+    ``grad[k] = sum over slots (p, h) with rows[p, h] == ids[k] of
+    d_out[p, h*dim:(h+1)*dim]`` (f32 ``[len(ids), dim]``; accumulated into
+    ``grad`` when given)."""
+    dev = d_out.device
+    rows = rows.to(device=dev, dtype=torch.int32).contiguous()
+    n_pos, heads = rows.shape
+    if d_out.numel() != n_pos * heads * dim or not d_out.is_contiguous():
+        raise ValueError(f"d_out must be contiguous with {n_pos}x{heads * dim} elements")
+    ids = ids.to(device=dev, dtype=torch.int32).contiguous()
+    if grad is None:
+        grad = torch.zeros((ids.numel(), dim), dtype=torch.float32, device=dev)
+    elif grad.shape != (ids.numel(), dim) or grad.dtype != torch.float32 or not grad.is_contiguous():
+        raise ValueError("grad must be a contiguous f32 [len(ids), dim] tensor")
+    ws = _WS.get(n_pos * heads, dev)
+    _lib.call("eg_scatter_grad", _lib.ptr(d_out), _dout_args(d_out), _lib.ptr(rows), n_pos, heads, dim,
+              _lib.ptr(ids), ids.numel(), _lib.ptr(grad), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
+    return grad
+
+
+class DescentState:
+    """Overlay variables and their Adam state, resident in HBM.
+
+    ``ids`` int32 ``[R]`` sorted unique global rows (``row_map`` keys, whose
+    values are ``0..R-1`` in ascending id order as ``build_rows_var`` makes
+    them); ``master`` f32 ``[R, D]`` (``rows_var``); ``m``/``v`` the moments;
+    ``quant`` the requantised copy the forward reads (``None``: keep fp32 only)."""
+
+    def __init__(self, ids: torch.Tensor, master: torch.Tensor, quant_fmt: str | None = "q8_0",
+                 base: DeviceTable | None = None):
+        if ids.dtype != torch.int32 or ids.dim() != 1:
+            raise ValueError("ids must be a 1-D int32 tensor")
+        if master.dtype != torch.float32 or master.dim() != 2 or master.shape[0] != ids.numel():
+            raise ValueError("master must be f32 [len(ids), D]")
+        if ids.numel() > 1 and not bool((ids[1:] > ids[:-1]).all()):
+            raise ValueError("ids must be sorted ascending and unique")
+        self.ids = ids.contiguous()
+        self.master = master.contiguous()
+        self.dim = int(master.shape[1])
+        dev = master.device
+        self.m = torch.zeros_like(self.master)
+        self.v = torch.zeros_like(self.master)
+        self.stamp = torch.zeros(ids.numel(), dtype=torch.int32, device=dev)
+        self.step_count = 0
+        self.base = base
+        self.quant = RowStore.empty(quant_fmt, ids.numel(), self.dim, dev) if quant_fmt else None
+        # ||rows0||^2 of the start rows (engraft/descend_corpus.py:936), for the pull term
+        self.rows0_sq = float(self.master.pow(2).sum().clamp_min(1e-12).item()) if ids.numel() else 0.0
+
+    @property
+    def n(self) -> int:
+        return int(self.ids.numel())
+
+    @property
+    def device(self) -> torch.device:
+        return self.master.device
+
+    @classmethod
+    def from_rows(cls, table: DeviceTable, rows, quant_fmt: str | None = "q8_0") -> "DescentState":
+        """Variables = every distinct row in ``rows`` (e.g. the forward's slot ids),
+        started from their true (dequantised) table values."""
+        r = rows if isinstance(rows, torch.Tensor) else torch.as_tensor(np.asarray(rows))
+        ids = torch.unique(r.to(device=table.device, dtype=torch.int64).reshape(-1)).to(torch.int32)
+        master = table.gather(ids.reshape(-1, 1)) if ids.numel() else torch.zeros(
+            (0, table.row_len), dtype=torch.float32, device=table.device)
+        return cls(ids, master, quant_fmt=quant_fmt, base=table)
+
+    def c_state(self) -> _lib.EgDescentState:
+        s = _lib.EgDescentState()
+        s.n = self.n
+        s.dim = self.dim
+        s.ids = _lib.ptr(self.ids)
+        s.master = _lib.ptr(self.master)
+        s.m = _lib.ptr(self.m)
+        s.v = _lib.ptr(self.v)
+        s.stamp = _lib.ptr(self.stamp)
+        if self.quant is not None:
+            s.quant = self.quant.c_table()
+        return s
+
+    def step(self, d_out: torch.Tensor, rows: torch.Tensor, *, lr: float, betas=(0.9, 0.999), eps: float = 1e-8,
+             dense: bool = False, mu: float = 0.0) -> None:
+        """One optimizer step from ``d_out`` (bf16/f32 ``[n_pos, heads*D]``) and the
+        slots' row ids ``rows`` (int32 ``[n_pos, heads]``).  ``mu``: the pull
+        term ``mu*||rows_var - rows0||^2/||rows0||^2`` (rows0 = the base table)."""
+        dev = self.device
+        rows = rows.to(device=dev, dtype=torch.int32).contiguous()
+        n_pos, heads = rows.shape
+        if d_out.numel() != n_pos * heads * self.dim or not d_out.is_contiguous() or d_out.device != dev:
+            raise ValueError(f"d_out must be contiguous on {dev} with {n_pos}x{heads * self.dim} elements")
+        self.step_count += 1
+        opt = _lib.EgAdam()
+        opt.lr, opt.beta1, opt.beta2, opt.eps = float(lr), float(betas[0]), float(betas[1]), float(eps)
+        opt.step = self.step_count
+        opt.dense = 1 if dense else 0
+        base = None
+        if mu != 0.0:
+            if self.base is None:
+                raise ValueError("the pull term needs the base table (DescentState(base=...))")
+            opt.l2_coef = float(np.float32(mu) / np.float32(self.rows0_sq))
+            base = self.base.c_table
+        ws = _WS.get(n_pos * heads, dev)
+        st = self.c_state()
+        _lib.call("eg_descent_step", _lib.ptr(d_out), _dout_args(d_out), _lib.ptr(rows), n_pos, heads,
+                  ctypes.byref(st), ctypes.byref(opt), ctypes.byref(base) if base is not None else None,
+                  _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
+
+    def overlay(self, quantized: bool = True) -> DeviceOverlay:
+        """The variables as a forward overlay: the requantised rows, or the fp32
+        master rows (the reference's ``.pleo`` semantics)."""
+        if quantized and self.quant is not None:
+            return DeviceOverlay(self.ids, self.quant)
+        return DeviceOverlay(self.ids, RowStore("f32", self.dim, self.master))
+
+
+# ---------------------------------------------------------------------------------------------
+# Row variables (engraft/replica/distill.py:378-453)
+# ---------------------------------------------------------------------------------------------
+
+def _read_true_rows(table: DeviceTable, rows_global) -> np.ndarray:
+    """TRUE (dequantised) rows for global row ids in any order, f32 ``[n, row_len]``
+    (``engraft/replica/distill.py:378-395``); ``ValueError`` for an id outside
+    every head."""
+    g = np.asarray(list(rows_global), dtype=np.int64).reshape(-1)
+    offsets = np.asarray(table.head_offsets, dtype=np.int64)
+    ends = offsets + np.asarray(table.head_vocab_sizes, dtype=np.int64)
+    for x in g.tolist():
+        h = int(np.searchsorted(offsets, x, side="right") - 1)
+        h = max(0, min(h, len(offsets) - 1))
+        if not (offsets[h] <= x < ends[h]):
+            raise ValueError(f"_read_true_rows: global row {x} outside all heads")
+    if g.size == 0:
+        return np.zeros((0, table.row_len), dtype=np.float32)
+    ids = torch.as_tensor(g.astype(np.int32), device=table.device).reshape(-1, 1)
+    return table.gather(ids).cpu().numpy()
+
+
+def build_rows_var(table: DeviceTable, sequences: list[list[int]], policy: str, row_sets: dict,
+                   exclude_positions: dict | None = None) -> tuple[dict, torch.Tensor]:
+    """``(row_map, rows_var)`` for a locality policy (``engraft/replica/distill.py:
+    401-453``): variable rows by policy minus every row read at an excluded
+    position; ``row_map`` = ``{global_row: index}`` in ascending row order;
+    ``rows_var`` f32 ``[R, row_len]`` (CPU, like the reference) holding the TRUE
+    values."""
+    if policy not in _POLICIES:
+        raise ValueError(f"build_rows_var: unknown policy {policy!r} (expected: {_POLICIES})")
+
+    def rows_of(key: str) -> set[int]:
+        return {int(r) for r in row_sets[key]}
+
+    if policy == "all-read":
+        candidate = rows_of("all_read")
+    elif policy == "private":
+        candidate = rows_of("all_read") - rows_of("neutral_read")
+    elif policy == "entity":
+        candidate = rows_of("entity") | rows_of("terme")
+    else:
+        candidate = rows_of("t8_answer")
+    excluded: set[int] = set()
+    for seq_idx, positions in (exclude_positions or {}).items():
+        if not positions:
+            continue
+        ids = table.rows(sequences[seq_idx]).cpu().numpy()
+        for p in positions:
+            excluded.update(int(g) for g in ids[p])
+    selected = sorted(candidate - excluded)
+    row_map = {g: i for i, g in enumerate(selected)}
+    if not selected:
+        return row_map, torch.zeros(0, table.row_len, dtype=torch.float32)
+    return row_map, torch.from_numpy(_read_true_rows(table, selected).copy())
+
+
+def descent_lr(rows0: torch.Tensor, lr_scale: float = 1.0) -> float:
+    """``engraft/descend_corpus.py:785-789``: ``lr_scale * 0.01 * mean_row_norm / sqrt(row_len)``."""
+    if rows0.shape[0] == 0:
+        return 0.0
+    mean_row_norm = float(rows0.norm(dim=1).mean().item())
+    return lr_scale * 0.01 * mean_row_norm / math.sqrt(rows0.shape[1])

@@ -119,6 +119,55 @@ int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tabl
 int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* rows,
               int64_t n_pos, int32_t heads, float* out, void* stream);
 
+/* ---- descent backward ----------------------------------------------------
+ * The overlay variables are R rows with sorted unique global ids
+ * (engraft/replica/distill.py:401-453 row_map, ascending).  Every slot (p, h)
+ * whose row id is one of them contributes d_out[p, h*dim:(h+1)*dim] to that
+ * variable's gradient (the autograd of rows_var[idx_r] + index_put,
+ * engraft/replica/seq.py:433-441).  Contributions are merged by a stable radix
+ * sort of (variable, slot) and a segmented reduction in ascending slot order:
+ * the result is bitwise repeatable and independent of scheduling. */
+
+/* Adam hyper-parameters of one step (torch.optim.Adam, engraft/descend_corpus.py:785-790). */
+typedef struct eg_adam {
+  float lr, beta1, beta2, eps;
+  int64_t step;     /* the step being taken: 1 on the first */
+  int32_t dense;    /* 1: every variable row steps, as torch.optim.Adam([rows_var]) does;
+                       0: only the rows hit by this batch (sparse / lazy Adam) */
+  float l2_coef;    /* mu / ||rows0||^2 of engraft/descend_corpus.py:935-939 (0: no pull
+                       term); rows0 = the base table rows of the variables */
+} eg_adam;
+
+/* Optimizer state of the R overlay variables, all device memory. */
+typedef struct eg_descent_state {
+  int64_t n;          /* R */
+  int32_t dim;
+  const int32_t* ids; /* [R] sorted unique global rows */
+  float* master;      /* [R, dim] fp32 rows (rows_var) */
+  float* m;           /* [R, dim] Adam first moment */
+  float* v;           /* [R, dim] Adam second moment */
+  int32_t* stamp;     /* [R] last step that hit the row (0 before the first) */
+  eg_table quant;     /* requantised copy [R] written after the update (Q8_0 or MXFP8;
+                         payload NULL: none) -- the rows a forward overlay reads */
+} eg_descent_state;
+
+/* Workspace bytes eg_scatter_grad / eg_descent_step need for n_slots = n_pos*heads. */
+size_t eg_backward_workspace_size(int64_t n_slots);
+
+/* grad_out f32 [n_var, dim] += sum over slots hitting each variable (rows not
+ * hit are left untouched: pass a zeroed buffer for the plain gradient).
+ * d_out: bf16 (d_out_f32 = 0) or f32 [n_pos, heads*dim]; rows int32 [n_pos, heads]. */
+int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos,
+                    int32_t heads, int32_t dim, const int32_t* ids, int64_t n_var,
+                    float* grad_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* One descent step: gradient as eg_scatter_grad, then Adam on state->master/m/v
+ * (torch's single-tensor op order, fp32), then requantisation into state->quant.
+ * base: the table the variables were read from (needed when opt->l2_coef != 0). */
+int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos,
+                    int32_t heads, const eg_descent_state* state, const eg_adam* opt,
+                    const eg_table* base, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Seeded synthetic table rows [row0, row0+n_rows) (benchmark/test inputs):
  * value j of row r = qtable[mix64(seed*0xD1B54A32D192ED03 + r*dim + j) >> 50]
  * (qtable f32 [16384], device), quantised with the format's rule

@@ -68,14 +68,18 @@ def scatter_grad_exact(d_emb, rows, ids_sorted) -> np.ndarray:
 
 
 def adam_step(param, grad, m, v, step: int, lr: float, beta1: float = 0.9, beta2: float = 0.999,
-              eps: float = 1e-8, touched=None):
+              eps: float = 1e-8, touched=None, rows0=None, l2_coef: float = 0.0):
     """One Adam step (``step`` = the new step count, 1 on the first step).
 
     fp32, torch single-tensor order: ``m.lerp_(g, 1-b1)``;
     ``v.mul_(b2).addcmul_(g, g, 1-b2)``; ``denom = sqrt(v)/sqrt(1-b2**t) + eps``;
     ``p.addcdiv_(m, denom, -lr/(1-b1**t))``.  ``touched`` (bool ``[R]``) restricts
     the update to those rows (sparse mode); ``None`` updates all rows (dense,
-    the reference's ``torch.optim.Adam([rows_var])``).  Returns new arrays."""
+    the reference's ``torch.optim.Adam([rows_var])``).  ``l2_coef`` (fp32
+    ``mu / ||rows0||^2``) adds the pull term's gradient
+    ``l2_coef * (2 * (p - rows0))`` of ``engraft/descend_corpus.py:935-939`` to
+    ``grad`` first (autograd's order: the pow backward ``2 * diff``, then the
+    scalar).  Returns new arrays."""
     param = np.array(param, dtype=np.float32, copy=True)
     m = np.array(m, dtype=np.float32, copy=True)
     v = np.array(v, dtype=np.float32, copy=True)
@@ -83,6 +87,9 @@ def adam_step(param, grad, m, v, step: int, lr: float, beta1: float = 0.9, beta2
     sel = slice(None) if touched is None else np.asarray(touched, dtype=bool)
     w1 = np.float32(1.0 - beta1)
     gs, ms, vs, ps = g[sel], m[sel], v[sel], param[sel]
+    if l2_coef != 0.0:
+        r0 = np.asarray(rows0, dtype=np.float32)[sel]
+        gs = (gs + np.float32(l2_coef) * (np.float32(2.0) * (ps - r0))).astype(np.float32)
     ms = (ms + w1 * (gs - ms)).astype(np.float32)
     vs = (vs * np.float32(beta2) + np.float32(1.0 - beta2) * gs * gs).astype(np.float32)
     bc1 = 1.0 - beta1 ** step

@@ -1,0 +1,193 @@
+"""GPU parity of the descent backward: the deterministic scatter (sort +
+segmented reduce) and the optimizer step + requantisation.
+
+Bar: gradients bit-exact against the oracle's sequential ascending-slot fp32
+sum; overlay rows after a step within 1e-5 relative of the oracle (asserted
+bit-exact too: the step is IEEE fp32 in the same order); requantised rows
+bit-exact against the oracle's rule applied to the device's fp32 rows; two runs
+from the same state bitwise identical."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import backward as B
+from oracle import formats as F
+from oracle import forward as FW
+from oracle import hash as H
+from oracle import synth
+from tests import gpu_util as G
+from tests.params import CFG1, synthetic_spec
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg: str) -> None:
+    print(f"[gpu-test] {msg}", file=sys.stderr, flush=True)
+
+
+def _rel_ok(got: np.ndarray, exp: np.ndarray, tol: float = 1e-5) -> float:
+    """max |got - exp| / max |exp| per row (the 1e-5 relative bar)."""
+    scale = np.maximum(np.abs(exp).max(axis=1, keepdims=True), 1e-30)
+    rel = float((np.abs(got - exp) / scale).max()) if got.size else 0.0
+    assert rel <= tol, f"relative error {rel}"
+    return rel
+
+
+@pytest.mark.parametrize("f32_grad", [False, True])
+def test_scatter_grad_bit_exact(cuda, f32_grad):
+    from engraft_ngram_amd import descent as D
+    spec = synthetic_spec(n_rows=16 * 3000, seed=61)
+    tokens = synth.zipf_tokens(62, 3000, 2000)  # many repeated bigrams -> long segments
+    rows = H.ngram_rows_np(spec, tokens)
+    uniq = np.unique(rows)
+    ids = uniq[::2].astype(np.int32)  # half of the rows are variables, the rest frozen
+    g = torch.Generator(device=cuda).manual_seed(63)
+    d = torch.randn((3000, 2048), generator=g, device=cuda) * 1e-3
+    d = d if f32_grad else d.to(torch.bfloat16)
+    grad = D.scatter_grad(d, torch.from_numpy(rows.astype(np.int32)), torch.from_numpy(ids), 128).cpu().numpy()
+    d_np = d.float().cpu().numpy()
+    exp, hits = B.scatter_grad(d_np, rows, ids)
+    assert hits.max() > 50  # a long segment was exercised
+    assert np.array_equal(grad, exp)
+    # repeatable, and accumulates into a given buffer
+    again = D.scatter_grad(d, torch.from_numpy(rows.astype(np.int32)), torch.from_numpy(ids), 128,
+                           grad=torch.from_numpy(grad).to(cuda)).cpu().numpy()
+    assert np.array_equal(again, (grad + exp).astype(np.float32))
+
+
+def test_scatter_grad_edge_cases(cuda):
+    """Empty batch, no variable hit, a single variable hit by every position."""
+    from engraft_ngram_amd import descent as D
+    ids = torch.tensor([5, 9], dtype=torch.int32)
+    d = torch.ones((0, 128), device=cuda)
+    assert D.scatter_grad(d, torch.zeros((0, 1), dtype=torch.int32), ids, 128).abs().sum().item() == 0
+    rows = torch.full((70, 1), 7, dtype=torch.int32)
+    d = torch.randn((70, 128), device=cuda)
+    assert D.scatter_grad(d, rows, ids, 128).abs().sum().item() == 0
+    rows = torch.full((5000, 1), 9, dtype=torch.int32)
+    d = torch.randn((5000, 128), device=cuda)
+    got = D.scatter_grad(d, rows, ids, 128).cpu().numpy()
+    exp, _ = B.scatter_grad(d.cpu().numpy(), rows.numpy(), ids.numpy())
+    assert np.array_equal(got, exp)
+
+
+def test_descent_step_config2_full_size(cuda):
+    """BASELINE config 2 at its own size: the config-1 table and batch, d_residual
+    [16384, 2048] bf16 ~ N(0, 1e-3), duplicates merged deterministically, Adam
+    (lr 1e-3, betas 0.9/0.999, eps 1e-8) on the touched rows, requantised to Q8_0."""
+    from engraft_ngram_amd import descent as D
+    _say("descent cfg2 (43.5 GB table)")
+    c = CFG1
+    spec = synthetic_spec(n_rows=c["n_rows"], seed=300)
+    tab = G.device_table(spec, "q8_0", c["n_rows"], 128, seed=301)
+    n = c["batch"] * c["seq"]
+    tokens = synth.zipf_tokens(302, n, c["vocab"])
+    _, rows = tab.forward(torch.from_numpy(tokens), None, seq_len=c["seq"], return_rows=True)
+    rows = rows[0]
+    g = torch.Generator(device=cuda).manual_seed(303)
+    d_res = (torch.randn((n, 2048), generator=g, device=cuda) * 1e-3).to(torch.bfloat16)
+    st = D.DescentState.from_rows(tab, rows)
+    st2 = D.DescentState.from_rows(tab, rows)
+    st.step(d_res, rows, lr=1e-3)
+    st2.step(d_res, rows, lr=1e-3)
+    torch.cuda.synchronize()
+    ids = st.ids.cpu().numpy()
+    rows_np = rows.cpu().numpy()
+    assert np.array_equal(ids, np.unique(rows_np))
+    master0 = G.synth_fetch("q8_0", 301, 128)(ids)
+    grad, hits = B.scatter_grad(d_res.float().cpu().numpy(), rows_np, ids)
+    _say(f"cfg2: {ids.size} unique rows, longest segment {hits.max()}")
+    p1, m1, v1 = B.adam_step(master0, grad, np.zeros_like(master0), np.zeros_like(master0), 1, 1e-3)
+    got = st.master.cpu().numpy()
+    _rel_ok(got, p1)
+    assert np.array_equal(got, p1)
+    assert np.array_equal(st.m.cpu().numpy(), m1) and np.array_equal(st.v.cpu().numpy(), v1)
+    q, dq = F.quant_q8_0(got)
+    assert np.array_equal(st.quant.payload.cpu().numpy().view(np.int8), q)
+    assert np.array_equal(st.quant.scales.cpu().numpy(), dq)
+    # bitwise repeatable
+    assert torch.equal(st.master, st2.master) and torch.equal(st.quant.payload, st2.quant.payload)
+    del tab, st, st2
+    torch.cuda.empty_cache()
+
+
+def test_sparse_multistep_against_oracle(cuda):
+    """Three steps on different batches: only the rows a batch hits step
+    (their moments lazily), with the global step count in the bias corrections."""
+    from engraft_ngram_amd import descent as D
+    spec = synthetic_spec(n_rows=16 * 4000, seed=71)
+    tab = G.device_table(spec, "q8_0", 16 * 4000, 128, seed=72)
+    batches = [synth.zipf_tokens(73 + k, 1024, 5000) for k in range(3)]
+    all_rows = [H.ngram_rows_np(spec, b) for b in batches]
+    st = D.DescentState.from_rows(tab, torch.from_numpy(np.concatenate(all_rows).astype(np.int32)))
+    ids = st.ids.cpu().numpy()
+    p = G.synth_fetch("q8_0", 72, 128)(ids)
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    for k, r in enumerate(all_rows, start=1):
+        d = (torch.randn((1024, 2048), device=cuda) * 1e-3).to(torch.bfloat16)
+        st.step(d, torch.from_numpy(r.astype(np.int32)), lr=2e-3)
+        grad, hits = B.scatter_grad(d.float().cpu().numpy(), r, ids)
+        p, m, v = B.adam_step(p, grad, m, v, k, 2e-3, touched=hits > 0)
+    got = st.master.cpu().numpy()
+    _rel_ok(got, p)
+    assert np.array_equal(got, p)
+    assert np.array_equal(st.v.cpu().numpy(), v)
+
+
+def test_dense_with_pull_term_against_torch_adam(cuda):
+    """The reference's own step (engraft/descend_corpus.py:921-947): dense
+    torch.optim.Adam over rows_var with the pull term mu*||rows_var-rows0||^2/
+    ||rows0||^2, three steps, against torch on the CPU (1e-5 relative)."""
+    from engraft_ngram_amd import descent as D
+    spec = synthetic_spec(n_rows=16 * 2000, seed=81)
+    tab = G.device_table(spec, "q8_0", 16 * 2000, 128, seed=82)
+    tokens = synth.zipf_tokens(83, 2048, 3000)
+    rows = H.ngram_rows_np(spec, tokens)
+    st = D.DescentState.from_rows(tab, torch.from_numpy(rows.astype(np.int32)))
+    ids = st.ids.cpu().numpy()
+    rows0 = G.synth_fetch("q8_0", 82, 128)(ids)
+    rv = torch.from_numpy(rows0.copy()).requires_grad_(True)
+    r0 = torch.from_numpy(rows0.copy())
+    opt = torch.optim.Adam([rv], lr=1e-3)
+    mu = 0.1
+    for k in range(3):
+        # a batch that hits only part of the variables: the dense step moves the rest too
+        sub = rows[k * 600:(k + 1) * 600]
+        d = (torch.randn((600, 2048), device=cuda) * 1e-3).to(torch.bfloat16)
+        st.step(d, torch.from_numpy(sub.astype(np.int32)), lr=1e-3, dense=True, mu=mu)
+        grad, _ = B.scatter_grad(d.float().cpu().numpy(), sub, ids)
+        opt.zero_grad()
+        rv.grad = torch.from_numpy(grad)
+        reg = mu * ((rv - r0).pow(2).sum() / r0.pow(2).sum().clamp_min(1e-12))
+        reg.backward()
+        opt.step()
+    _rel_ok(st.master.cpu().numpy(), rv.detach().numpy())
+
+
+def test_updated_rows_read_back_through_forward_overlay(cuda):
+    """The requantised rows of a step are what the next forward reads
+    (overlay-vs-base resolved per id on the device)."""
+    from engraft_ngram_amd import descent as D
+    spec = synthetic_spec(n_rows=16 * 3000, seed=91)
+    tab = G.device_table(spec, "q8_0", 16 * 3000, 128, seed=92)
+    tokens = synth.zipf_tokens(93, 1024, 4000)
+    rows = H.ngram_rows_np(spec, tokens)
+    st = D.DescentState.from_rows(tab, torch.from_numpy(rows[:500].astype(np.int32)))
+    d = (torch.randn((500, 2048), device=cuda) * 1e-2).to(torch.bfloat16)
+    st.step(d, torch.from_numpy(rows[:500].astype(np.int32)), lr=1e-2)
+    res = G.residual(1024, 2048, seed=94)
+    for quantized in (True, False):
+        out = tab.forward(torch.from_numpy(tokens), res, overlay=st.overlay(quantized=quantized))
+        ids = st.ids.cpu().numpy()
+        if quantized:
+            vals = F.dequant_q8_0(st.quant.payload.cpu().numpy().view(np.int8), st.quant.scales.cpu().numpy())
+        else:
+            vals = st.master.cpu().numpy()
+        _, _, exp = FW.forward(spec, tokens, G.synth_fetch("q8_0", 92, 128), G.bf16_bits(res),
+                               overlay=(ids, vals))
+        G.assert_out_matches(G.bf16_bits(out), exp)

@@ -172,3 +172,27 @@ def test_product_synthetic_params_equal_oracle_params():
         assert tuple(tuple(r) for r in hp["head_multipliers"]) == spec.head_multipliers
         assert hp["eos_token_id"] == spec.eos_token_id
     assert np.array_equal(S.zipf_tokens(5, 1000, 151_936), synth.zipf_tokens(5, 1000, 151_936))
+
+
+def test_adam_pull_term_matches_torch_autograd():
+    """The pull term of engraft/descend_corpus.py:935-939 through torch autograd
+    + torch.optim.Adam on CPU, three dense steps."""
+    rng = np.random.default_rng(5)
+    rows0 = (rng.standard_normal((30, 128)) * 0.02).astype(np.float32)
+    mu = 0.1
+    t = torch.from_numpy(rows0.copy()).requires_grad_(True)
+    r0t = torch.from_numpy(rows0.copy())
+    opt = torch.optim.Adam([t], lr=1e-3)
+    p, m, v = rows0.copy(), np.zeros_like(rows0), np.zeros_like(rows0)
+    s = np.float32((rows0.astype(np.float32) ** 2).sum(dtype=np.float32))
+    coef = float(np.float32(mu) / s)
+    for k in range(1, 4):
+        g = (rng.standard_normal((30, 128)) * 1e-3).astype(np.float32)
+        opt.zero_grad()
+        t.grad = torch.from_numpy(g.copy())
+        reg = mu * ((t - r0t).pow(2).sum() / r0t.pow(2).sum().clamp_min(1e-12))
+        reg.backward()
+        opt.step()
+        p, m, v = B.adam_step(p, g, m, v, k, 1e-3, rows0=rows0, l2_coef=coef)
+        ref = t.detach().numpy()
+        assert np.max(np.abs(p - ref)) <= 1e-6 * np.max(np.abs(ref))
