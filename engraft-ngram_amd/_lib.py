@@ -64,10 +64,10 @@ class EgOverlay(ctypes.Structure):
 
 class EgAdam(ctypes.Structure):
     _fields_ = [
-        ("lr", ctypes.c_float),
-        ("beta1", ctypes.c_float),
-        ("beta2", ctypes.c_float),
-        ("eps", ctypes.c_float),
+        ("lr", ctypes.c_double),
+        ("beta1", ctypes.c_double),
+        ("beta2", ctypes.c_double),
+        ("eps", ctypes.c_double),
         ("step", c_int64),
         ("dense", c_int32),
         ("l2_coef", ctypes.c_float),

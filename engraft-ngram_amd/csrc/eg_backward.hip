@@ -422,8 +422,8 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   EG_CHECK_ARG(state->n == 0 || (state->master && state->m && state->v && state->stamp),
                "state master/m/v/stamp is NULL");
   EG_CHECK_ARG(opt->step >= 1 && opt->step < (1LL << 31), "step=%lld", (long long)opt->step);
-  EG_CHECK_ARG(opt->lr >= 0.0f && opt->beta1 >= 0.0f && opt->beta1 < 1.0f && opt->beta2 >= 0.0f &&
-                   opt->beta2 < 1.0f && opt->eps >= 0.0f,
+  EG_CHECK_ARG(opt->lr >= 0.0 && opt->beta1 >= 0.0 && opt->beta1 < 1.0 && opt->beta2 >= 0.0 &&
+                   opt->beta2 < 1.0 && opt->eps >= 0.0,
                "invalid Adam hyper-parameters");
   SegArgs a;
   memset(&a, 0, sizeof(a));
@@ -470,8 +470,8 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   a.b2 = (float)b2;
   a.w2 = (float)(1.0 - b2);
   a.bc2s = (float)sqrt(bc2);
-  a.eps = opt->eps;
-  a.neg_step_size = -(float)((double)opt->lr / bc1);
+  a.eps = (float)opt->eps;
+  a.neg_step_size = -(float)(opt->lr / bc1);
   a.l2c = opt->l2_coef;
   if (n > 0) {
     launch_segments<true>(a, st);

@@ -130,7 +130,8 @@ int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* r
 
 /* Adam hyper-parameters of one step (torch.optim.Adam, engraft/descend_corpus.py:785-790). */
 typedef struct eg_adam {
-  float lr, beta1, beta2, eps;
+  double lr, beta1, beta2, eps; /* doubles, like torch's Python scalars: lr/(1-beta1^t) and
+                                   1-beta1 are formed in double and rounded to fp32 once */
   int64_t step;     /* the step being taken: 1 on the first */
   int32_t dense;    /* 1: every variable row steps, as torch.optim.Adam([rows_var]) does;
                        0: only the rows hit by this batch (sparse / lazy Adam) */
