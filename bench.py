@@ -79,6 +79,49 @@ def cpu_baseline(hp: dict, tokens_np, residual_cpu, budget_s: float) -> dict:
             "gb_per_s": n * forward_bytes(tokens_np.size) / el / 1e9, "steps": n, "seconds": el}
 
 
+def backward_bytes(positions: int, n_unique: int) -> int:
+    """Algorithmic HBM bytes of one descent step (fp32 master
+    kept): d_residual read (2 B x W per position), the slots' int32 row ids, and
+    per touched row the Q8_0 row read + write (2 x 136 B), the fp32 moments read +
+    write (4 x 512 B) and the fp32 master read + write (2 x 512 B)."""
+    return positions * 2 * WIDTH + positions * SLOTS * 4 + n_unique * (2 * Q8_ROW_BYTES + 4 * 512 + 2 * 512)
+
+
+def bench_backward(tab, tokens, steps: int, warmup: int) -> dict:
+    """d_residual [16384, 2048] bf16 ~ N(0, 1e-3); scatter of
+    the per-slot row gradients into the fp32 overlay of the touched rows (stable
+    radix sort + segmented reduce), Adam (lr 1e-3, betas 0.9/0.999, eps 1e-8) on
+    the touched rows and requantisation to Q8_0 blocks.  One step = one
+    eg_descent_step call (a handful of launches)."""
+    import torch
+
+    from engraft_ngram_amd import descent as D
+    from engraft_ngram_amd import synthetic as S
+
+    _, rows = tab.forward(tokens, None, seq_len=SEQ, return_rows=True)
+    rows = rows[0].contiguous()
+    d_res = S.residual(rows.shape[0], WIDTH, seed=RES_SEED + 100, device=tab.device, std=1e-3)
+    state = D.DescentState.from_rows(tab, rows)
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        state.step(d_res, rows, lr=1e-3)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        state.step(d_res, rows, lr=1e-3)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    nb = backward_bytes(rows.shape[0], state.n)
+    gbs = nb / (ms * 1e-3) / 1e9
+    return {"us_per_step": ms * 1e3, "touched_rows": state.n, "slot_gradients": rows.numel(),
+            "algorithmic_bytes_per_step": nb, "gb_per_s": gbs, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
+            "rows_per_s": rows.numel() / (ms * 1e-3),
+            "workload": "BASELINE config 2: scatter (sort + segmented reduce) + sparse Adam + Q8_0 requant, "
+                        "fp32 master/m/v kept"}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -86,6 +129,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-backward", action="store_true", help="skip the config-2 descent step leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures the table path on one "
@@ -184,6 +228,12 @@ def main() -> None:
             "us_per_step_wall": ms_per_step * 1e3,
         },
     }
+
+    if not args.no_backward:
+        bw = bench_backward(tab, tokens, max(1, args.steps // 4), max(1, args.warmup // 4))
+        result["backward"] = bw
+        log(f"backward: {bw['us_per_step']:.1f} us/step, {bw['touched_rows']} touched rows, "
+            f"{bw['gb_per_s']:.0f} GB/s algorithmic ({100 * bw['frac_of_hbm_peak']:.1f}% of peak)")
 
     if not args.no_cpu:
         cb = cpu_baseline(hp, tokens_np, res[0].cpu(), args.cpu_seconds)
