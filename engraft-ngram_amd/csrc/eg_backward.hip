@@ -1,106 +1,183 @@
 // Backward half of the n-gram table path on gfx950: the deterministic sparse
 // gradient scatter and the optimizer step on the touched overlay rows.
 //
-//   keys     slot s = p*heads + h  ->  (variable index of rows[s], s)
-//   sort     stable LSD radix sort of the pairs by variable index (per-tile
-//            digit histograms, one scan, a ballot-ranked stable scatter per
-//            digit pass): equal variables keep ascending slot order
-//   segment  one 32-lane group per sorted segment sums the slots' d_out
-//            slices in that order (fp32), then runs Adam on the variable's
-//            master row and requantises it
-//   dense    rows no slot hit take their zero-gradient Adam step (dense mode)
+//   keys     slot s = p*heads + h -> (variable index of rows[s], s); the
+//            variable is found through an LDS splitter table of the sorted
+//            ids; the first digit's per-tile histogram is built on the way
+//   sort     stable LSD radix sort of the pairs by variable index, digits of
+//            up to 9 bits: one scan and one ballot-ranked stable scatter per
+//            pass (the scatter also counts the next pass's digits), so equal
+//            variables keep ascending slot order
+//   segment  one 32-lane group per segment of at most 32 slots sums the
+//            slots' d_out slices in slot order (fp32) and runs Adam +
+//            requantisation on the variable; longer segments are listed and
+//   long     reduced by a whole workgroup: pieces of 32 slots summed in order,
+//            piece sums accumulated per group (pieces j = g mod 8), the eight
+//            group sums added in group order
+//   dense    variables no slot hit take their zero-gradient step (dense mode)
 //
-// No floating-point atomics anywhere: the result is bitwise repeatable and is
-// the sequential ascending-slot sum the CPU oracle computes.
+// No floating-point atomics: the association of every sum is fixed by the
+// sorted order alone, so results are bitwise repeatable, and the CPU oracle
+// reproduces them exactly.
 #include <string.h>
 
 #include "eg_common.h"
 
 namespace eg {
 
-constexpr int kSortThreads = 256;
-constexpr int kSortIPT = 16;
-constexpr int kSortTile = kSortThreads * kSortIPT;  // 4096 keys per tile
+constexpr int kTileThreads = 256;
+constexpr int kTileIPT = 4;
+constexpr int kTile = kTileThreads * kTileIPT;  // 1024 keys per tile
+constexpr int kMaxDigitBits = 9;
+constexpr int kMaxBuckets = 1 << kMaxDigitBits;
 constexpr int kScanThreads = 1024;
+constexpr int kSplitMax = 8192;  // splitters staged in LDS (32 KB)
+constexpr int kPiece = 32;       // slots per piece of a long segment
+constexpr int kLongGroups = 8;   // 32-lane groups per long-segment workgroup
 
-__global__ __launch_bounds__(256) void keys_kernel(const int32_t* __restrict__ rows, int64_t n,
-                                                   const int32_t* __restrict__ ids, int64_t n_var,
-                                                   uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const int64_t k = sorted_find(ids, n_var, rows[i]);
-  keys[i] = k >= 0 ? (uint32_t)k : (uint32_t)n_var;  // frozen rows sort after every variable
-  vals[i] = (uint32_t)i;
-}
-
-// Per-tile digit counts, digit-major: hist[d * n_tiles + tile].
-__global__ __launch_bounds__(kSortThreads) void sort_hist(const uint32_t* __restrict__ keys, int64_t n, int shift,
-                                                          int n_buckets, int n_tiles, uint32_t* __restrict__ hist) {
-  __shared__ uint32_t h[256];
-  for (int i = threadIdx.x; i < 256; i += kSortThreads) h[i] = 0;
-  __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kSortTile;
-  const uint32_t mask = (uint32_t)n_buckets - 1u;
-#pragma unroll 4
-  for (int r = 0; r < kSortIPT; ++r) {
-    const int64_t idx = base + r * kSortThreads + threadIdx.x;
-    if (idx < n) atomicAdd(&h[(keys[idx] >> shift) & mask], 1u);
-  }
-  __syncthreads();
-  for (int d = threadIdx.x; d < n_buckets; d += kSortThreads) hist[(int64_t)d * n_tiles + blockIdx.x] = h[d];
-}
-
-// In-place exclusive scan of a[0..len) by one workgroup.
-__global__ __launch_bounds__(kScanThreads) void sort_scan(uint32_t* __restrict__ a, int64_t len) {
-  __shared__ uint32_t tot[kScanThreads];
+// ---------------------------------------------------------------------------
+// Keys + first histogram
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kTileThreads) void keys_hist_kernel(
+    const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ ids, int64_t n_var, int split_shift,
+    uint32_t* __restrict__ keys, uint32_t* __restrict__ vals, int dbits, int n_tiles, uint32_t* __restrict__ hist,
+    uint32_t* __restrict__ long_count) {
+  __shared__ int32_t spl[kSplitMax];
+  __shared__ uint32_t h[kMaxBuckets];
   const int tid = threadIdx.x;
-  const int64_t per = (len + kScanThreads - 1) / kScanThreads;
-  const int64_t lo = tid * per, hi = min(lo + per, len);
-  uint32_t s = 0;
-  for (int64_t i = lo; i < hi; ++i) s += a[i];
-  tot[tid] = s;
+  const int ns = (int)((n_var + (1LL << split_shift) - 1) >> split_shift);
+  for (int i = tid; i < ns; i += kTileThreads) spl[i] = ids[(int64_t)i << split_shift];
+  for (int i = tid; i < kMaxBuckets; i += kTileThreads) h[i] = 0;
+  if (blockIdx.x == 0 && tid == 0) *long_count = 0;
   __syncthreads();
-  for (int off = 1; off < kScanThreads; off <<= 1) {  // Hillis-Steele inclusive scan
-    const uint32_t add = tid >= off ? tot[tid - off] : 0u;
-    __syncthreads();
-    tot[tid] += add;
-    __syncthreads();
+  const uint32_t mask = (1u << dbits) - 1u;
+#pragma unroll
+  for (int r = 0; r < kTileIPT; ++r) {
+    const int64_t idx = (int64_t)blockIdx.x * kTile + r * kTileThreads + tid;
+    if (idx >= n) break;
+    const int32_t row = rows[idx];
+    int lo = 0, hi = ns;  // first splitter > row
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (spl[mid] <= row) lo = mid + 1; else hi = mid;
+    }
+    uint32_t key = (uint32_t)n_var;
+    if (lo > 0) {
+      const int64_t w0 = (int64_t)(lo - 1) << split_shift;
+      const int64_t w1 = min(w0 + (1LL << split_shift), n_var);
+      const int64_t k = sorted_find(ids + w0, w1 - w0, row);
+      if (k >= 0) key = (uint32_t)(w0 + k);
+    }
+    keys[idx] = key;
+    vals[idx] = (uint32_t)idx;
+    atomicAdd(&h[key & mask], 1u);
   }
-  uint32_t run = tot[tid] - s;
-  for (int64_t i = lo; i < hi; ++i) {
-    const uint32_t v = a[i];
-    a[i] = run;
-    run += v;
+  __syncthreads();
+  for (int d = tid; d < (1 << dbits); d += kTileThreads) hist[(int64_t)d * n_tiles + blockIdx.x] = h[d];
+}
+
+// ---------------------------------------------------------------------------
+// Exclusive scan (one workgroup, coalesced strips) + clearing of the next
+// pass's histogram
+// ---------------------------------------------------------------------------
+__device__ inline uint32_t wave_inclusive_scan(uint32_t x, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Block-wide exclusive scan of one value per thread (1024 threads).
+__device__ inline uint32_t block_exclusive_scan(uint32_t t, uint32_t* wsum, uint32_t* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t incl = wave_inclusive_scan(t, lane);
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kScanThreads / 64; ++w) {
+    const uint32_t x = wsum[w];
+    if (w < wave) before += x;
+    all += x;
+  }
+  *total = all;
+  return before + incl - t;
+}
+
+constexpr int kScanChunk = 4 * kScanThreads;  // entries per scan workgroup
+
+// Pass 1 of the exclusive scan: the total of every chunk; also clears the next
+// pass's histogram.
+__global__ __launch_bounds__(kScanThreads) void scan_partials(const uint32_t* __restrict__ a, int64_t len,
+                                                              uint32_t* __restrict__ partial,
+                                                              uint32_t* __restrict__ clear, int64_t clear_len) {
+  __shared__ uint32_t wsum[kScanThreads / 64];
+  const int tid = threadIdx.x;
+  for (int64_t i = (int64_t)blockIdx.x * kScanThreads + tid; i < clear_len; i += (int64_t)gridDim.x * kScanThreads)
+    clear[i] = 0;
+  const int64_t i0 = (int64_t)blockIdx.x * kScanChunk + 4 * tid;
+  uint32_t t = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) t += (i0 + u < len) ? a[i0 + u] : 0u;
+  uint32_t total;
+  block_exclusive_scan(t, wsum, &total);
+  if (tid == 0) partial[blockIdx.x] = total;
+}
+
+// Pass 2: exclusive scan of every chunk, offset by the totals of the chunks
+// before it.
+__global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict__ a, int64_t len,
+                                                           const uint32_t* __restrict__ partial) {
+  __shared__ uint32_t wsum[kScanThreads / 64];
+  __shared__ uint32_t wsum2[kScanThreads / 64];
+  const int tid = threadIdx.x;
+  uint32_t pre = 0;
+  for (int g = tid; g < (int)blockIdx.x; g += kScanThreads) pre += partial[g];
+  const int64_t i0 = (int64_t)blockIdx.x * kScanChunk + 4 * tid;
+  uint32_t v[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) v[u] = (i0 + u < len) ? a[i0 + u] : 0u;
+  uint32_t base;
+  block_exclusive_scan(pre, wsum2, &base);  // base = sum of every thread's share of the earlier chunks
+  __syncthreads();
+  uint32_t total;
+  uint32_t run = base + block_exclusive_scan(v[0] + v[1] + v[2] + v[3], wsum, &total);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    if (i0 + u < len) a[i0 + u] = run;
+    run += v[u];
   }
 }
 
-// Stable scatter of one digit pass.  Items are taken in index order (round r,
-// then wave, then lane); within a wave the lanes holding the same digit are
-// found with one ballot per digit bit, their rank is the popcount of the lower
-// lanes, and per-digit LDS counters carry the running offset across waves and
-// rounds.
-__global__ __launch_bounds__(kSortThreads) void sort_scatter(const uint32_t* __restrict__ keys_in,
-                                                             const uint32_t* __restrict__ vals_in,
-                                                             uint32_t* __restrict__ keys_out,
-                                                             uint32_t* __restrict__ vals_out, int64_t n, int shift,
-                                                             int dbits, int n_tiles,
-                                                             const uint32_t* __restrict__ offs) {
-  constexpr int kWaves = kSortThreads / 64;
-  __shared__ uint32_t run[256];
-  __shared__ uint32_t wcnt[kWaves][256];
+// ---------------------------------------------------------------------------
+// Stable scatter of one digit pass.  Items are taken in index order (round,
+// then wave, then lane); lanes holding the same digit are found with one
+// ballot per digit bit, their rank is the popcount of the lower lanes, and
+// per-digit LDS counters carry the running offset across waves and rounds.
+// The next pass's per-tile histogram is counted at the destination.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kTileThreads) void scatter_kernel(
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint32_t* __restrict__ keys_out,
+    uint32_t* __restrict__ vals_out, int64_t n, int shift, int dbits, int n_tiles, const uint32_t* __restrict__ offs,
+    uint32_t* __restrict__ hist_next, int next_shift, int next_dbits) {
+  constexpr int kWaves = kTileThreads / 64;
+  __shared__ uint32_t run[kMaxBuckets];
+  __shared__ uint32_t wcnt[kWaves][kMaxBuckets];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n_buckets = 1 << dbits;
-  for (int d = tid; d < 256; d += kSortThreads) {
-    run[d] = d < n_buckets ? offs[(int64_t)d * n_tiles + blockIdx.x] : 0u;
+  for (int d = tid; d < n_buckets; d += kTileThreads) {
+    run[d] = offs[(int64_t)d * n_tiles + blockIdx.x];
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) wcnt[w][d] = 0;
   }
   __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kSortTile;
   const uint32_t mask = (uint32_t)n_buckets - 1u;
+  const uint32_t next_mask = (1u << next_dbits) - 1u;
   const uint64_t lt = (1ull << lane) - 1ull;
-  for (int r = 0; r < kSortIPT; ++r) {
-    const int64_t idx = base + r * kSortThreads + tid;
+  for (int r = 0; r < kTileIPT; ++r) {
+    const int64_t idx = (int64_t)blockIdx.x * kTile + r * kTileThreads + tid;
     const bool valid = idx < n;
     uint32_t key = 0, val = 0, d = 0;
     if (valid) {
@@ -122,9 +199,11 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter(const uint32_t* __r
       for (int w = 0; w < wave; ++w) pos += wcnt[w][d];
       keys_out[pos] = key;
       vals_out[pos] = val;
+      if (hist_next != nullptr)
+        atomicAdd(&hist_next[(int64_t)((key >> next_shift) & next_mask) * n_tiles + pos / kTile], 1u);
     }
     __syncthreads();
-    for (int dd = tid; dd < n_buckets; dd += kSortThreads) {
+    for (int dd = tid; dd < n_buckets; dd += kTileThreads) {
       uint32_t t = 0;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
@@ -145,6 +224,8 @@ struct SegArgs {
   const uint32_t* svals;  // slot ids in the same order
   int64_t n;
   int64_t n_var;
+  uint32_t* long_list;    // first sorted position of every segment longer than kPiece
+  uint32_t* long_count;
   const void* d_out;
   int32_t d_out_f32;
   int32_t heads;
@@ -158,213 +239,410 @@ struct SegArgs {
   float* v;
   int32_t* stamp;
   TableDev quant;         // fmt 0: no requantised copy
-  TableDev base;          // for the L2 pull term
+  TableDev base;          // for the pull term
   int64_t step;
   float w1, b2, w2, bc2s, eps, neg_step_size, l2c;
 };
 
-__device__ inline float grad_value(const SegArgs& a, int64_t idx) {
-  if (a.d_out_f32) return ((const float*)a.d_out)[idx];
-  return __uint_as_float((uint32_t)((const uint16_t*)a.d_out)[idx] << 16);
+// A lane owns VPL columns of a row: consecutive (sub*VPL + t) when VPL divides
+// 32 (vector loads, a 32-value block spans 32/VPL lanes), else strided
+// (sub + 32 t: block t spans the 32 lanes).
+template <int VPL, bool CONSEC>
+__device__ inline int col_of(int sub, int t) {
+  return CONSEC ? sub * VPL + t : sub + 32 * t;
 }
 
-// Adam on variable k (lane `sub` owns columns sub + 32 t), torch's
-// single-tensor order without contractions: m.lerp_(g, 1-b1);
-// v.mul_(b2).addcmul_(g, g, 1-b2); p.addcdiv_(m, sqrt(v)/sqrt(bc2) + eps, -lr/bc1);
-// then the requantised copy (block t is spread over the 32 lanes).
-template <int NT>
-__device__ void adam_row(const SegArgs& a, int64_t k, int sub, int nt, float g[NT]) {
-#pragma clang fp contract(off)
-  float pv[NT];
+template <int VPL, bool CONSEC>
+__device__ inline void load_f32(const float* __restrict__ row, int sub, float x[VPL]) {
+  if constexpr (CONSEC && VPL == 4) {
+    const u32x4 q = *(const u32x4*)(row + sub * 4);
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    if (t >= nt) break;
-    const int col = sub + 32 * t;
-    const int64_t idx = k * a.dim + col;
-    float p = a.master[idx], m = a.m[idx], v = a.v[idx];
+    for (int t = 0; t < 4; ++t) x[t] = __uint_as_float(q[t]);
+  } else {
+#pragma unroll
+    for (int t = 0; t < VPL; ++t) x[t] = row[col_of<VPL, CONSEC>(sub, t)];
+  }
+}
+
+template <int VPL, bool CONSEC>
+__device__ inline void store_f32(float* __restrict__ row, int sub, const float x[VPL]) {
+  if constexpr (CONSEC && VPL == 4) {
+    *(u32x4*)(row + sub * 4) = u32x4{__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
+                                     __float_as_uint(x[3])};
+  } else {
+#pragma unroll
+    for (int t = 0; t < VPL; ++t) row[col_of<VPL, CONSEC>(sub, t)] = x[t];
+  }
+}
+
+// d_out slice of one slot (bf16 or f32), VPL values of this lane.
+template <int VPL, bool CONSEC>
+__device__ inline void load_grad(const SegArgs& a, uint32_t slot, int sub, float x[VPL]) {
+  const int64_t p = slot / (uint32_t)a.heads;
+  const int h = (int)(slot - p * a.heads);
+  const int64_t base = p * a.width + (int64_t)h * a.dim;
+  if (a.d_out_f32) {
+    load_f32<VPL, CONSEC>((const float*)a.d_out + base, sub, x);
+  } else {
+    const uint16_t* src = (const uint16_t*)a.d_out + base;
+    if constexpr (CONSEC && VPL == 4) {
+      const u32x2 q = *(const u32x2*)(src + sub * 4);
+      x[0] = __uint_as_float(q.x << 16);
+      x[1] = __uint_as_float(q.x & 0xffff0000u);
+      x[2] = __uint_as_float(q.y << 16);
+      x[3] = __uint_as_float(q.y & 0xffff0000u);
+    } else {
+#pragma unroll
+      for (int t = 0; t < VPL; ++t) x[t] = __uint_as_float((uint32_t)src[col_of<VPL, CONSEC>(sub, t)] << 16);
+    }
+  }
+}
+
+// Sums the d_out slices of `cnt` (<= 32) consecutive sorted slots whose slot
+// ids sit in lane (gbase + e) of `vl`, in order, onto g.  Loads go out eight
+// slots at a time; the additions stay in slot order.
+template <int VPL, bool CONSEC>
+__device__ inline void sum_piece(const SegArgs& a, uint32_t vl, int gbase, int cnt, int sub, float g[VPL]) {
+  for (int e0 = 0; e0 < cnt; e0 += 8) {
+    float x[8][VPL];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const uint32_t s = (uint32_t)__shfl((int)vl, gbase + ((e0 + u) & 31));
+      if (e0 + u < cnt) load_grad<VPL, CONSEC>(a, s, sub, x[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (e0 + u < cnt) {
+#pragma unroll
+        for (int t = 0; t < VPL; ++t) g[t] = g[t] + x[u][t];
+      }
+  }
+}
+
+// Adam on variable k (torch's single-tensor order, no contractions):
+// m.lerp_(g, 1-b1); v.mul_(b2).addcmul_(g, g, 1-b2);
+// p.addcdiv_(m, sqrt(v)/sqrt(bc2) + eps, -lr/bc1); then the requantised copy.
+template <int VPL, bool CONSEC>
+__device__ void adam_apply(const SegArgs& a, int64_t k, int sub, const float g[VPL], float p[VPL], float m[VPL],
+                           float v[VPL]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int t = 0; t < VPL; ++t) {
     float gt = g[t];
     if (a.l2c != 0.0f) {
       const int32_t row0 = a.ids[k];
-      const float p0 = ((uint32_t)row0 < (uint64_t)a.base.n_rows) ? load_value_rt(a.base, row0, col)
-                                                                  : __uint_as_float(0x7fc00000u);
-      gt = gt + a.l2c * (2.0f * (p - p0));
+      const float p0 = ((uint32_t)row0 < (uint64_t)a.base.n_rows)
+                           ? load_value_rt(a.base, row0, col_of<VPL, CONSEC>(sub, t))
+                           : __uint_as_float(0x7fc00000u);
+      gt = gt + a.l2c * (2.0f * (p[t] - p0));
     }
-    m = m + a.w1 * (gt - m);
-    v = v * a.b2 + (a.w2 * gt) * gt;
-    const float denom = sqrtf(v) / a.bc2s + a.eps;
-    p = p + a.neg_step_size * (m / denom);
-    a.master[idx] = p;
-    a.m[idx] = m;
-    a.v[idx] = v;
-    pv[t] = p;
+    m[t] = m[t] + a.w1 * (gt - m[t]);
+    v[t] = v[t] * a.b2 + (a.w2 * gt) * gt;
+    const float denom = sqrtf(v[t]) / a.bc2s + a.eps;
+    p[t] = p[t] + a.neg_step_size * (m[t] / denom);
   }
+  const int64_t off = k * a.dim;
+  store_f32<VPL, CONSEC>(a.master + off, sub, p);
+  store_f32<VPL, CONSEC>(a.m + off, sub, m);
+  store_f32<VPL, CONSEC>(a.v + off, sub, v);
   if (a.quant.fmt == 0) return;
   const int nb = a.dim >> 5;
+  uint8_t* payload = (uint8_t*)a.quant.payload;
+  if constexpr (CONSEC) {
+    // this lane's values all lie in block sub / (32 / VPL)
+    constexpr int kLanesPerBlock = 32 / VPL;
+    float amax = 0.0f;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    if (t >= nt) break;
-    float amax = fabsf(pv[t]);
+    for (int t = 0; t < VPL; ++t) amax = fmaxf(amax, fabsf(p[t]));
 #pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
-    const int64_t qi = k * a.dim + sub + 32 * t;
-    uint8_t* payload = (uint8_t*)a.quant.payload;
+    for (int o = kLanesPerBlock / 2; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+    const int blk = sub / kLanesPerBlock;
+    uint32_t packed = 0;
     if (a.quant.fmt == EG_FMT_Q8_0) {
       const uint16_t dh = f32_to_f16(amax / 127.0f);
       const float d = f16_to_f32(dh);
-      float r = (d == 0.0f) ? 0.0f : rintf(pv[t] / d);
-      r = fminf(fmaxf(r, -127.0f), 127.0f);
-      payload[qi] = (uint8_t)(int32_t)r;
-      if (sub == 0) ((uint16_t*)a.quant.scales)[k * nb + t] = dh;
+#pragma unroll
+      for (int t = 0; t < VPL; ++t) {
+        float r = (d == 0.0f) ? 0.0f : rintf(p[t] / d);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        const uint32_t b = (uint32_t)(int32_t)r & 0xffu;
+        if constexpr (VPL == 4) packed |= b << (8 * t);
+        else payload[off + col_of<VPL, CONSEC>(sub, t)] = (uint8_t)b;
+      }
+      if (sub % kLanesPerBlock == 0) ((uint16_t*)a.quant.scales)[k * nb + blk] = dh;
     } else {  // EG_FMT_MXFP8
       const int ebits = (int)((__float_as_uint(amax) >> 23) & 0xffu);
       int e = (amax > 0.0f ? ebits - 127 : -127) - 8;
       e = min(max(e, -127), 127);
       if (amax * ldexpf(1.0f, -e) > 448.0f) e = min(e + 1, 127);
-      const float s = fminf(fmaxf(pv[t] * ldexpf(1.0f, -e), -448.0f), 448.0f);
-      payload[qi] = (uint8_t)f32_to_e4m3(s);
-      if (sub == 0) ((uint8_t*)a.quant.scales)[k * nb + t] = (uint8_t)(e + 127);
+      const float inv = ldexpf(1.0f, -e);
+#pragma unroll
+      for (int t = 0; t < VPL; ++t) {
+        const uint32_t b = f32_to_e4m3(fminf(fmaxf(p[t] * inv, -448.0f), 448.0f));
+        if constexpr (VPL == 4) packed |= b << (8 * t);
+        else payload[off + col_of<VPL, CONSEC>(sub, t)] = (uint8_t)b;
+      }
+      if (sub % kLanesPerBlock == 0) ((uint8_t*)a.quant.scales)[k * nb + blk] = (uint8_t)(e + 127);
+    }
+    if constexpr (VPL == 4) *(uint32_t*)(payload + off + sub * 4) = packed;
+  } else {
+#pragma unroll
+    for (int t = 0; t < VPL; ++t) {
+      float amax = fabsf(p[t]);
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+      const int64_t qi = off + sub + 32 * t;
+      if (a.quant.fmt == EG_FMT_Q8_0) {
+        const uint16_t dh = f32_to_f16(amax / 127.0f);
+        const float d = f16_to_f32(dh);
+        float r = (d == 0.0f) ? 0.0f : rintf(p[t] / d);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        payload[qi] = (uint8_t)(int32_t)r;
+        if (sub == 0) ((uint16_t*)a.quant.scales)[k * nb + t] = dh;
+      } else {
+        const int ebits = (int)((__float_as_uint(amax) >> 23) & 0xffu);
+        int e = (amax > 0.0f ? ebits - 127 : -127) - 8;
+        e = min(max(e, -127), 127);
+        if (amax * ldexpf(1.0f, -e) > 448.0f) e = min(e + 1, 127);
+        payload[qi] = (uint8_t)f32_to_e4m3(fminf(fmaxf(p[t] * ldexpf(1.0f, -e), -448.0f), 448.0f));
+        if (sub == 0) ((uint8_t*)a.quant.scales)[k * nb + t] = (uint8_t)(e + 127);
+      }
     }
   }
 }
 
-// One 32-lane group per sorted position; the group at a segment's first
-// position reduces the whole segment in slot order.
-template <int NT, bool ADAM>
+// The sum g of variable k is final: optimizer step, or accumulation into grad_out.
+template <int VPL, bool CONSEC, bool ADAM>
+__device__ inline void finish(const SegArgs& a, int64_t k, int sub, const float g[VPL], float p[VPL], float m[VPL],
+                              float v[VPL]) {
+  if constexpr (ADAM) {
+    adam_apply<VPL, CONSEC>(a, k, sub, g, p, m, v);
+    if (sub == 0) a.stamp[k] = (int32_t)a.step;
+  } else {
+    float* dst = a.grad_out + k * a.dim;
+    float cur[VPL];
+    load_f32<VPL, CONSEC>(dst, sub, cur);
+#pragma unroll
+    for (int t = 0; t < VPL; ++t) cur[t] = cur[t] + g[t];
+    store_f32<VPL, CONSEC>(dst, sub, cur);
+  }
+}
+
+// One 32-lane group per sorted position; the group at the first slot of a
+// segment of at most kPiece slots reduces it; longer segments are listed.
+template <int VPL, bool CONSEC, bool ADAM>
 __global__ __launch_bounds__(256) void segment_kernel(const SegArgs a) {
-  const int sub = threadIdx.x & 31;
+  const int lane = threadIdx.x & 63, sub = lane & 31, gbase = lane & 32;
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 5;
   if (i >= a.n) return;  // uniform per group
   const uint32_t key = a.skeys[i];
-  if ((int64_t)key >= a.n_var) return;                 // frozen rows: no variable
-  if (i > 0 && a.skeys[i - 1] == key) return;          // not the segment's first slot
-  const int nt = a.dim >> 5;
-  float g[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) g[t] = 0.0f;
-  // Walk the segment four slots at a time: the loads of four slots are issued
-  // together, the additions stay in slot order.
-  for (int64_t j = i;; j += 4) {
-    uint32_t kk[4], vv[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      kk[u] = (j + u < a.n) ? a.skeys[j + u] : 0xffffffffu;
-      vv[u] = (j + u < a.n) ? a.svals[j + u] : 0u;
-    }
-    float x[4][NT];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (kk[u] == key) {
-        const int64_t p = vv[u] / (uint32_t)a.heads;
-        const int h = (int)(vv[u] - p * a.heads);
-        const int64_t base = p * a.width + (int64_t)h * a.dim + sub;
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-          if (t < nt) x[u][t] = grad_value(a, base + 32 * t);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (kk[u] == key) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-          if (t < nt) g[t] = g[t] + x[u][t];
-      }
-    if (kk[3] != key) break;
+  if ((int64_t)key >= a.n_var) return;         // frozen rows: no variable
+  if (i > 0 && a.skeys[i - 1] == key) return;  // not the segment's first slot
+  const uint32_t kl = (i + sub < a.n) ? a.skeys[i + sub] : 0xffffffffu;
+  const uint32_t vl = (i + sub < a.n) ? a.svals[i + sub] : 0u;
+  const bool longer = (i + kPiece < a.n) && a.skeys[i + kPiece] == key;
+  if (longer) {
+    if (sub == 0) a.long_list[atomicAdd(a.long_count, 1u)] = (uint32_t)i;
+    return;
   }
-  if constexpr (ADAM) {
-    adam_row<NT>(a, key, sub, nt, g);
-    if (sub == 0) a.stamp[key] = (int32_t)a.step;
-  } else {
+  float p[VPL], m[VPL], v[VPL];
+  if constexpr (ADAM) {  // the state rows do not depend on the gradient: fetch them first
+    const int64_t off = (int64_t)key * a.dim;
+    load_f32<VPL, CONSEC>(a.master + off, sub, p);
+    load_f32<VPL, CONSEC>(a.m + off, sub, m);
+    load_f32<VPL, CONSEC>(a.v + off, sub, v);
+  }
+  const int cnt = __popc((uint32_t)(__ballot(kl == key) >> gbase));
+  float g[VPL];
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-      if (t < nt) {
-        float* dst = a.grad_out + (int64_t)key * a.dim + sub + 32 * t;
-        *dst = *dst + g[t];
+  for (int t = 0; t < VPL; ++t) g[t] = 0.0f;
+  sum_piece<VPL, CONSEC>(a, vl, gbase, cnt, sub, g);
+  finish<VPL, CONSEC, ADAM>(a, key, sub, g, p, m, v);
+}
+
+// One workgroup per listed long segment (grid-stride over the list).
+template <int VPL, bool CONSEC, bool ADAM>
+__global__ __launch_bounds__(256) void long_kernel(const SegArgs a) {
+  __shared__ float part[kLongGroups][512];
+  const int grp = threadIdx.x >> 5, sub = threadIdx.x & 31, gbase = threadIdx.x & 32;
+  const uint32_t count = *a.long_count;
+  for (uint32_t li = blockIdx.x; li < count; li += gridDim.x) {
+    const int64_t i0 = a.long_list[li];
+    const uint32_t key = a.skeys[i0];
+    float G[VPL];
+#pragma unroll
+    for (int t = 0; t < VPL; ++t) G[t] = 0.0f;
+    for (int64_t j = grp;; j += kLongGroups) {
+      const int64_t start = i0 + j * kPiece;
+      if (start >= a.n) break;
+      const uint32_t kl = (start + sub < a.n) ? a.skeys[start + sub] : 0xffffffffu;
+      const uint32_t vl = (start + sub < a.n) ? a.svals[start + sub] : 0u;
+      const int cnt = __popc((uint32_t)(__ballot(kl == key) >> gbase));
+      if (cnt == 0) break;
+      float P[VPL];
+#pragma unroll
+      for (int t = 0; t < VPL; ++t) P[t] = 0.0f;
+      sum_piece<VPL, CONSEC>(a, vl, gbase, cnt, sub, P);
+#pragma unroll
+      for (int t = 0; t < VPL; ++t) G[t] = G[t] + P[t];
+      if (cnt < kPiece) break;
+    }
+#pragma unroll
+    for (int t = 0; t < VPL; ++t) part[grp][col_of<VPL, CONSEC>(sub, t)] = G[t];
+    __syncthreads();
+    if (grp == 0) {
+      float g[VPL], p[VPL], m[VPL], v[VPL];
+#pragma unroll
+      for (int t = 0; t < VPL; ++t) {
+        const int c = col_of<VPL, CONSEC>(sub, t);
+        g[t] = part[0][c];
+        for (int q = 1; q < kLongGroups; ++q) g[t] = g[t] + part[q][c];
       }
+      if constexpr (ADAM) {
+        const int64_t off = (int64_t)key * a.dim;
+        load_f32<VPL, CONSEC>(a.master + off, sub, p);
+        load_f32<VPL, CONSEC>(a.m + off, sub, m);
+        load_f32<VPL, CONSEC>(a.v + off, sub, v);
+      }
+      finish<VPL, CONSEC, ADAM>(a, key, sub, g, p, m, v);
+    }
+    __syncthreads();
   }
 }
 
 // Dense mode: the variables no slot hit this step take a zero-gradient step.
-template <int NT>
+template <int VPL, bool CONSEC>
 __global__ __launch_bounds__(256) void dense_kernel(const SegArgs a) {
   const int sub = threadIdx.x & 31;
   const int64_t k = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 5;
   if (k >= a.n_var) return;
   if (a.stamp[k] == (int32_t)a.step) return;
-  float g[NT];
+  float g[VPL], p[VPL], m[VPL], v[VPL];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) g[t] = 0.0f;
-  adam_row<NT>(a, k, sub, a.dim >> 5, g);
+  for (int t = 0; t < VPL; ++t) g[t] = 0.0f;
+  const int64_t off = k * a.dim;
+  load_f32<VPL, CONSEC>(a.master + off, sub, p);
+  load_f32<VPL, CONSEC>(a.m + off, sub, m);
+  load_f32<VPL, CONSEC>(a.v + off, sub, v);
+  adam_apply<VPL, CONSEC>(a, k, sub, g, p, m, v);
 }
 
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
 struct Workspace {
   uint32_t* keys[2];
   uint32_t* vals[2];
-  uint32_t* hist;
+  uint32_t* hist[2];
+  uint32_t* partial;  // per scan chunk
+  uint32_t* long_count;
+  uint32_t* long_list;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+static int64_t n_tiles_of(int64_t n) { return (n + kTile - 1) / kTile; }
+
+static size_t partial_bytes(int64_t n) {
+  return align256((size_t)((n_tiles_of(n) * kMaxBuckets + kScanChunk - 1) / kScanChunk + 1) * 4);
+}
+
 static size_t workspace_bytes(int64_t n) {
-  const int64_t tiles = (n + kSortTile - 1) / kSortTile;
-  return 4 * align256((size_t)n * 4) + align256((size_t)tiles * 256 * 4);
+  const size_t kb = align256((size_t)n * 4);
+  const size_t hb = align256((size_t)n_tiles_of(n) * kMaxBuckets * 4);
+  return 4 * kb + 2 * hb + partial_bytes(n) + 256 + align256((size_t)(n / (kPiece + 1) + 1) * 4);
 }
 
 static Workspace carve(void* ws, int64_t n) {
   Workspace w;
   char* p = (char*)ws;
   const size_t kb = align256((size_t)n * 4);
+  const size_t hb = align256((size_t)n_tiles_of(n) * kMaxBuckets * 4);
   w.keys[0] = (uint32_t*)p;
   w.vals[0] = (uint32_t*)(p + kb);
   w.keys[1] = (uint32_t*)(p + 2 * kb);
   w.vals[1] = (uint32_t*)(p + 3 * kb);
-  w.hist = (uint32_t*)(p + 4 * kb);
+  w.hist[0] = (uint32_t*)(p + 4 * kb);
+  w.hist[1] = (uint32_t*)(p + 4 * kb + hb);
+  w.partial = (uint32_t*)(p + 4 * kb + 2 * hb);
+  w.long_count = (uint32_t*)(p + 4 * kb + 2 * hb + partial_bytes(n));
+  w.long_list = (uint32_t*)(p + 4 * kb + 2 * hb + partial_bytes(n) + 256);
   return w;
 }
 
-// keys + stable radix sort; returns the index (0/1) of the sorted buffers.
+// keys + stable radix sort; *sorted = index (0/1) of the sorted buffers.
 static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_t n_var, const Workspace& w,
                       hipStream_t st, int* sorted) {
-  hipLaunchKernelGGL(keys_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, rows, n, ids, n_var,
-                     w.keys[0], w.vals[0]);
-  int rc = launch_status("keys_kernel");
-  if (rc != EG_OK) return rc;
   int bits = 0;
   while (bits < 32 && ((uint64_t)n_var >> bits) != 0) ++bits;  // keys lie in [0, n_var]
+  const int passes = bits == 0 ? 0 : (bits + kMaxDigitBits - 1) / kMaxDigitBits;
+  const int dbits = passes == 0 ? 1 : (bits + passes - 1) / passes;
+  int split_shift = 0;
+  while (((n_var + (1LL << split_shift) - 1) >> split_shift) > kSplitMax) ++split_shift;
+  const int n_tiles = (int)n_tiles_of(n);
+  hipLaunchKernelGGL(keys_hist_kernel, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var, split_shift,
+                     w.keys[0], w.vals[0], dbits, n_tiles, w.hist[0], w.long_count);
+  int rc = launch_status("keys_hist_kernel");
+  if (rc != EG_OK) return rc;
   int cur = 0;
-  if (bits > 0) {
-    const int passes = (bits + 7) / 8;
-    const int dbits = (bits + passes - 1) / passes;
-    const int n_tiles = (int)((n + kSortTile - 1) / kSortTile);
-    for (int pass = 0; pass < passes; ++pass) {
-      const int shift = pass * dbits;
-      hipLaunchKernelGGL(sort_hist, dim3(n_tiles), dim3(kSortThreads), 0, st, w.keys[cur], n, shift, 1 << dbits,
-                         n_tiles, w.hist);
-      hipLaunchKernelGGL(sort_scan, dim3(1), dim3(kScanThreads), 0, st, w.hist, (int64_t)n_tiles << dbits);
-      hipLaunchKernelGGL(sort_scatter, dim3(n_tiles), dim3(kSortThreads), 0, st, w.keys[cur], w.vals[cur],
-                         w.keys[cur ^ 1], w.vals[cur ^ 1], n, shift, dbits, n_tiles, w.hist);
-      rc = launch_status("radix sort pass");
-      if (rc != EG_OK) return rc;
-      cur ^= 1;
-    }
+  for (int pass = 0; pass < passes; ++pass) {
+    const bool last = pass + 1 == passes;
+    uint32_t* h = w.hist[pass & 1];
+    uint32_t* h_next = last ? nullptr : w.hist[(pass + 1) & 1];
+    const int64_t len = (int64_t)n_tiles << dbits;
+    const unsigned chunks = (unsigned)((len + kScanChunk - 1) / kScanChunk);
+    hipLaunchKernelGGL(scan_partials, dim3(chunks), dim3(kScanThreads), 0, st, h, len, w.partial, h_next,
+                       last ? (int64_t)0 : len);
+    hipLaunchKernelGGL(scan_apply, dim3(chunks), dim3(kScanThreads), 0, st, h, len, w.partial);
+    hipLaunchKernelGGL(scatter_kernel, dim3(n_tiles), dim3(kTileThreads), 0, st, w.keys[cur], w.vals[cur],
+                       w.keys[cur ^ 1], w.vals[cur ^ 1], n, pass * dbits, dbits, n_tiles, h, h_next,
+                       (pass + 1) * dbits, dbits);
+    rc = launch_status("radix sort pass");
+    if (rc != EG_OK) return rc;
+    cur ^= 1;
   }
   *sorted = cur;
   return EG_OK;
 }
 
-template <bool ADAM>
-static void launch_segments(const SegArgs& a, hipStream_t st) {
+template <bool ADAM, int VPL, bool CONSEC>
+static void launch_reduce_t(const SegArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)((a.n * 32 + 255) / 256));
-  const int nt = a.dim >> 5;
-  if (nt == 4) hipLaunchKernelGGL((segment_kernel<4, ADAM>), grid, dim3(256), 0, st, a);
-  else if (nt == 5) hipLaunchKernelGGL((segment_kernel<5, ADAM>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((segment_kernel<16, ADAM>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((segment_kernel<VPL, CONSEC, ADAM>), grid, dim3(256), 0, st, a);
+  const int64_t max_long = a.n / (kPiece + 1) + 1;
+  const unsigned long_grid = (unsigned)(max_long < 1024 ? max_long : 1024);
+  hipLaunchKernelGGL((long_kernel<VPL, CONSEC, ADAM>), dim3(long_grid), dim3(256), 0, st, a);
+}
+
+template <bool ADAM>
+static int launch_reduce(const SegArgs& a, hipStream_t st) {
+  switch (a.dim) {
+    case 128: launch_reduce_t<ADAM, 4, true>(a, st); break;
+    case 64: launch_reduce_t<ADAM, 2, true>(a, st); break;
+    case 256: launch_reduce_t<ADAM, 8, true>(a, st); break;
+    case 160: launch_reduce_t<ADAM, 5, false>(a, st); break;
+    default: return set_error(EG_ERR_UNSUPPORTED, "backward for dim %d (built: 64, 128, 160, 256)", a.dim);
+  }
+  return launch_status("segment/long kernels");
+}
+
+static int launch_dense(const SegArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)((a.n_var * 32 + 255) / 256));
+  switch (a.dim) {
+    case 128: hipLaunchKernelGGL((dense_kernel<4, true>), grid, dim3(256), 0, st, a); break;
+    case 64: hipLaunchKernelGGL((dense_kernel<2, true>), grid, dim3(256), 0, st, a); break;
+    case 256: hipLaunchKernelGGL((dense_kernel<8, true>), grid, dim3(256), 0, st, a); break;
+    case 160: hipLaunchKernelGGL((dense_kernel<5, false>), grid, dim3(256), 0, st, a); break;
+    default: return set_error(EG_ERR_UNSUPPORTED, "backward for dim %d", a.dim);
+  }
+  return launch_status("dense_kernel");
 }
 
 static int check_common(const void* d_out, const int32_t* rows, int64_t n_pos, int32_t heads, int32_t dim,
                         const int32_t* ids, int64_t n_var, void* ws, size_t ws_bytes) {
   EG_CHECK_ARG(n_pos >= 0 && heads >= 1 && heads <= EG_MAX_HEADS, "n_pos=%lld heads=%d", (long long)n_pos, heads);
-  EG_CHECK_ARG(dim > 0 && dim % 32 == 0 && dim <= 512, "dim=%d must be a multiple of 32 in [32, 512]", dim);
+  EG_CHECK_ARG(dim == 64 || dim == 128 || dim == 160 || dim == 256, "backward dim=%d (built: 64, 128, 160, 256)",
+               dim);
   EG_CHECK_ARG(n_var >= 0 && n_var < (1LL << 31), "n_var=%lld", (long long)n_var);
   const int64_t n = n_pos * heads;
   EG_CHECK_ARG(n < (1LL << 31), "n_pos*heads=%lld slots exceed 2^31", (long long)n);
@@ -403,14 +681,15 @@ int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   a.svals = w.vals[cur];
   a.n = n;
   a.n_var = n_var;
+  a.long_list = w.long_list;
+  a.long_count = w.long_count;
   a.d_out = d_out;
   a.d_out_f32 = d_out_f32;
   a.heads = heads;
   a.dim = dim;
   a.width = (int64_t)heads * dim;
   a.grad_out = grad_out;
-  launch_segments<false>(a, st);
-  return launch_status("segment_kernel");
+  return launch_reduce<false>(a, st);
 }
 
 int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos, int32_t heads,
@@ -422,8 +701,8 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   EG_CHECK_ARG(state->n == 0 || (state->master && state->m && state->v && state->stamp),
                "state master/m/v/stamp is NULL");
   EG_CHECK_ARG(opt->step >= 1 && opt->step < (1LL << 31), "step=%lld", (long long)opt->step);
-  EG_CHECK_ARG(opt->lr >= 0.0 && opt->beta1 >= 0.0 && opt->beta1 < 1.0 && opt->beta2 >= 0.0 &&
-                   opt->beta2 < 1.0 && opt->eps >= 0.0,
+  EG_CHECK_ARG(opt->lr >= 0.0 && opt->beta1 >= 0.0 && opt->beta1 < 1.0 && opt->beta2 >= 0.0 && opt->beta2 < 1.0 &&
+                   opt->eps >= 0.0,
                "invalid Adam hyper-parameters");
   SegArgs a;
   memset(&a, 0, sizeof(a));
@@ -452,6 +731,8 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   a.svals = w.vals[cur];
   a.n = n;
   a.n_var = state->n;
+  a.long_list = w.long_list;
+  a.long_count = w.long_count;
   a.d_out = d_out;
   a.d_out_f32 = d_out_f32;
   a.heads = heads;
@@ -474,18 +755,10 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   a.neg_step_size = -(float)(opt->lr / bc1);
   a.l2c = opt->l2_coef;
   if (n > 0) {
-    launch_segments<true>(a, st);
-    rc = launch_status("segment_kernel");
+    rc = launch_reduce<true>(a, st);
     if (rc != EG_OK) return rc;
   }
-  if (opt->dense) {
-    const dim3 grid((unsigned)((state->n * 32 + 255) / 256));
-    const int nt = state->dim >> 5;
-    if (nt == 4) hipLaunchKernelGGL(dense_kernel<4>, grid, dim3(256), 0, st, a);
-    else if (nt == 5) hipLaunchKernelGGL(dense_kernel<5>, grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(dense_kernel<16>, grid, dim3(256), 0, st, a);
-    rc = launch_status("dense_kernel");
-  }
+  if (opt->dense) rc = launch_dense(a, st);
   return rc;
 }
 

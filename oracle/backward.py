@@ -4,17 +4,20 @@
 * ``scatter_grad``  -- the gradient of the overlay variables: autograd of
   ``rows_var[idx_r]`` + ``index_put`` (``engraft/replica/seq.py:433-441``)
   gives ``grad[r] = sum over (t, h) with row_map[rows[t, h]] == r of
-  d_emb[t, h, :]``.  The sum is taken in ascending slot order
-  (``slot = t*n_heads + h``) in fp32, one addition at a time (``np.add.at`` is
-  sequential in index order), which is the order the device's sort +
-  segmented reduce fixes; ``scatter_grad_exact`` gives the fp64 sum.
+  d_emb[t, h, :]``.  The slots of a variable are taken in ascending slot order
+  (``slot = t*n_heads + h``) and summed in fp32 with the association the
+  device's sort + segmented reduce fixes (``segment_sum``: sequential up to 32
+  slots, pieces of 32 grouped mod 8 beyond); ``scatter_grad_exact`` gives the
+  fp64 sum.
 * ``adam_step``     -- ``torch.optim.Adam`` (``engraft/descend_corpus.py:
   785-790, 947``) restated in fp32 with torch's single-tensor op order; the
   dense mode updates every variable row like the reference, the sparse mode
   only the rows hit in this step (their moments, lazily).
 
-Pinning (tests/test_oracle_backward.py): ``scatter_grad`` against the fp64
-exact sum (error bound) and its permutation invariance as a set; ``adam_step``
+Pinning (tests/test_oracle_forward_backward.py): ``scatter_grad`` against the
+fp64 exact sum (error bound), against a plain per-slot loop for segments of at
+most 32 slots, and ``segment_sum`` against an independent reshape formulation
+for long segments; ``adam_step``
 dense against ``torch.optim.Adam`` itself on CPU (the library routine the
 reference calls), multi-step, and the first-step closed form
 ``p - lr*g/(|g| + eps)`` (m_hat = g, v_hat = g**2).
@@ -37,8 +40,45 @@ def slot_keys(rows, ids_sorted) -> np.ndarray:
     return np.where(ids[posc] == flat, posc, -1)
 
 
+PIECE = 32        # slots per piece of a long segment
+LONG_GROUPS = 8   # piece sums are accumulated per group j mod 8
+
+
+def _seq_sum(x: np.ndarray) -> np.ndarray:
+    """((0 + x[0]) + x[1]) + ... in fp32, one addition at a time."""
+    acc = np.zeros(x.shape[1:], dtype=np.float32)
+    for row in x:
+        acc = (acc + row).astype(np.float32)
+    return acc
+
+
+def segment_sum(vals: np.ndarray) -> np.ndarray:
+    """Sum of one variable's slot gradients ``vals [L, D]`` (ascending slot order)
+    with the association the device uses: a segment of at most 32 slots is summed
+    in order; a longer one is cut into pieces of 32 slots (each summed in order),
+    piece j is added (in order of j) to group ``j mod 8``'s sum, and the eight
+    group sums are added in group order."""
+    vals = np.asarray(vals, dtype=np.float32)
+    n = vals.shape[0]
+    if n <= PIECE:
+        return _seq_sum(vals)
+    pieces = [_seq_sum(vals[j:j + PIECE]) for j in range(0, n, PIECE)]
+    groups = []
+    for g in range(LONG_GROUPS):
+        acc = np.zeros(vals.shape[1:], dtype=np.float32)
+        for j in range(g, len(pieces), LONG_GROUPS):
+            acc = (acc + pieces[j]).astype(np.float32)
+        groups.append(acc)
+    tot = groups[0]
+    for g in range(1, LONG_GROUPS):
+        tot = (tot + groups[g]).astype(np.float32)
+    return tot
+
+
 def scatter_grad(d_emb, rows, ids_sorted) -> tuple[np.ndarray, np.ndarray]:
-    """``(grad f32 [R, D], hits int64 [R])`` -- sequential fp32 in slot order."""
+    """``(grad f32 [R, D], hits int64 [R])``: each variable's slots in ascending
+    slot order, summed with ``segment_sum``'s association (sequential for the
+    segments of at most 32 slots, which ``np.add.at`` does in index order)."""
     d_emb = np.asarray(d_emb, dtype=np.float32)
     rows = np.asarray(rows, dtype=np.int64)
     p, hh = rows.shape
@@ -47,11 +87,18 @@ def scatter_grad(d_emb, rows, ids_sorted) -> tuple[np.ndarray, np.ndarray]:
     r = int(np.asarray(ids_sorted).size)
     grad = np.zeros((r, d), dtype=np.float32)
     hits = np.zeros(r, dtype=np.int64)
-    sel = keys >= 0
-    if sel.any():
-        vals = d_emb.reshape(p * hh, d)[sel]
-        np.add.at(grad, keys[sel], vals)
-        np.add.at(hits, keys[sel], 1)
+    sel = np.flatnonzero(keys >= 0)
+    if sel.size == 0:
+        return grad, hits
+    order = np.argsort(keys[sel], kind="stable")
+    slots = sel[order]
+    ks = keys[slots]
+    np.add.at(hits, ks, 1)
+    flat = d_emb.reshape(p * hh, d)
+    short = hits[ks] <= PIECE
+    np.add.at(grad, ks[short], flat[slots[short]])  # sequential in index (= slot) order
+    for k in np.unique(ks[~short]):
+        grad[k] = segment_sum(flat[slots[ks == k]])
     return grad, hits
 
 

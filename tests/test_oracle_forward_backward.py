@@ -75,7 +75,10 @@ def test_residual_add_is_fp32_add_then_bf16_rne():
 def test_scatter_grad_against_exact_sum_and_order():
     rng = np.random.default_rng(1)
     p, hh, d = 300, 16, 32
-    rows = rng.integers(0, 40, size=(p, hh)) + np.arange(hh)[None, :] * 40  # many duplicates
+    # many duplicates; heads 8..15 draw from 4 rows only: segments of ~75 slots
+    rows = rng.integers(0, 40, size=(p, hh))
+    rows[:, 8:] %= 4
+    rows = rows + np.arange(hh)[None, :] * 40
     ids = np.unique(rows)[::2]  # half of the rows are variables
     d_emb = (rng.standard_normal((p, hh * d)) * 1e-3).astype(np.float32)
     grad, hits = B.scatter_grad(d_emb, rows, ids)
@@ -85,13 +88,40 @@ def test_scatter_grad_against_exact_sum_and_order():
     absum = B.scatter_grad_exact(np.abs(d_emb), rows, ids)
     bound = hits[:, None] * np.finfo(np.float32).eps * absum + 1e-30
     assert np.all(np.abs(grad - exact) <= bound)
-    # the order is ascending slot order: a manual loop reproduces it bit for bit
+    # segments of at most 32 slots: ascending slot order, one addition at a
+    # time -- a manual loop reproduces them bit for bit
     keys = B.slot_keys(rows, ids)
     manual = np.zeros_like(grad)
     for s in range(p * hh):
         if keys[s] >= 0:
             manual[keys[s]] += d_emb.reshape(p * hh, d)[s]
-    assert np.array_equal(manual, grad)
+    short = hits <= B.PIECE
+    assert short.any() and (~short).any()
+    assert np.array_equal(manual[short], grad[short])
+
+
+def test_segment_sum_long_association():
+    """Long segments: pieces of 32 summed in order, piece j added to group j % 8,
+    groups added in order -- restated here with reshapes and cumsum."""
+    rng = np.random.default_rng(6)
+    for n in (33, 64, 255, 256, 257, 1000, 5000):
+        x = (rng.standard_normal((n, 16)) * 1e-3).astype(np.float32)
+        pad = (-n) % 32
+        xp = np.concatenate([x, np.zeros((pad, 16), np.float32)])
+        pieces = []
+        for blk in xp.reshape(-1, 32, 16):
+            acc = np.zeros(16, np.float32)
+            for r in blk:  # trailing zero rows do not change an fp32 sum
+                acc = np.float32(acc + r)
+            pieces.append(acc)
+        groups = [np.zeros(16, np.float32) for _ in range(8)]
+        for j, pc in enumerate(pieces):
+            groups[j % 8] = np.float32(groups[j % 8] + pc)
+        tot = groups[0]
+        for g in groups[1:]:
+            tot = np.float32(tot + g)
+        assert np.array_equal(B.segment_sum(x), tot)
+        assert np.allclose(B.segment_sum(x), x.astype(np.float64).sum(0), rtol=0, atol=1e-6)
 
 
 def test_adam_dense_matches_torch_adam_multistep():
