@@ -31,7 +31,7 @@ constexpr int kTile = kTileThreads * kTileIPT;  // 1024 keys per tile
 constexpr int kMaxDigitBits = 9;
 constexpr int kMaxBuckets = 1 << kMaxDigitBits;
 constexpr int kScanThreads = 1024;
-constexpr int kSplitMax = 8192;  // splitters staged in LDS (32 KB)
+constexpr int kSplitMax = 2048;  // splitters staged in LDS (8 KB)
 constexpr int kPiece = 32;       // slots per piece of a long segment
 constexpr int kLongGroups = 8;   // 32-lane groups per long-segment workgroup
 
@@ -241,6 +241,7 @@ struct SegArgs {
   TableDev quant;         // fmt 0: no requantised copy
   TableDev base;          // for the pull term
   int64_t step;
+  int32_t dense;          // stamp the rows hit (the dense pass skips them)
   float w1, b2, w2, bc2s, eps, neg_step_size, l2c;
 };
 
@@ -417,7 +418,7 @@ __device__ inline void finish(const SegArgs& a, int64_t k, int sub, const float 
                               float v[VPL]) {
   if constexpr (ADAM) {
     adam_apply<VPL, CONSEC>(a, k, sub, g, p, m, v);
-    if (sub == 0) a.stamp[k] = (int32_t)a.step;
+    if (a.dense && sub == 0) a.stamp[k] = (int32_t)a.step;
   } else {
     float* dst = a.grad_out + k * a.dim;
     float cur[VPL];
@@ -435,13 +436,15 @@ __global__ __launch_bounds__(256) void segment_kernel(const SegArgs a) {
   const int lane = threadIdx.x & 63, sub = lane & 31, gbase = lane & 32;
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 5;
   if (i >= a.n) return;  // uniform per group
-  const uint32_t key = a.skeys[i];
-  if ((int64_t)key >= a.n_var) return;         // frozen rows: no variable
-  if (i > 0 && a.skeys[i - 1] == key) return;  // not the segment's first slot
+  // The window [i, i+32), its neighbours i-1 and i+32: one round of loads.
   const uint32_t kl = (i + sub < a.n) ? a.skeys[i + sub] : 0xffffffffu;
   const uint32_t vl = (i + sub < a.n) ? a.svals[i + sub] : 0u;
-  const bool longer = (i + kPiece < a.n) && a.skeys[i + kPiece] == key;
-  if (longer) {
+  const uint32_t prev = (i > 0) ? a.skeys[i - 1] : 0xffffffffu;
+  const uint32_t next = (i + kPiece < a.n) ? a.skeys[i + kPiece] : 0xffffffffu;
+  const uint32_t key = (uint32_t)__shfl((int)kl, gbase);
+  if ((int64_t)key >= a.n_var) return;  // frozen rows: no variable
+  if (prev == key) return;              // not the segment's first slot
+  if (next == key) {
     if (sub == 0) a.long_list[atomicAdd(a.long_count, 1u)] = (uint32_t)i;
     return;
   }
@@ -744,6 +747,7 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   a.v = state->v;
   a.stamp = state->stamp;
   a.step = opt->step;
+  a.dense = opt->dense != 0;
   const double b1 = opt->beta1, b2 = opt->beta2;
   const double bc1 = 1.0 - pow(b1, (double)opt->step);
   const double bc2 = 1.0 - pow(b2, (double)opt->step);

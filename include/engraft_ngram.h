@@ -147,7 +147,7 @@ typedef struct eg_descent_state {
   float* master;      /* [R, dim] fp32 rows (rows_var) */
   float* m;           /* [R, dim] Adam first moment */
   float* v;           /* [R, dim] Adam second moment */
-  int32_t* stamp;     /* [R] last step that hit the row (0 before the first) */
+  int32_t* stamp;     /* [R] last dense step that hit the row (0 before the first) */
   eg_table quant;     /* requantised copy [R] written after the update (Q8_0 or MXFP8;
                          payload NULL: none) -- the rows a forward overlay reads */
 } eg_descent_state;
