@@ -51,23 +51,43 @@ __global__ __launch_bounds__(kTileThreads) void keys_hist_kernel(
   if (blockIdx.x == 0 && tid == 0) *long_count = 0;
   __syncthreads();
   const uint32_t mask = (1u << dbits) - 1u;
+  // The kTileIPT lookups of a thread run in lockstep (fixed-length branchless
+  // searches), so their memory latencies overlap.
+  int32_t row[kTileIPT];
+  bool ok[kTileIPT];
 #pragma unroll
   for (int r = 0; r < kTileIPT; ++r) {
     const int64_t idx = (int64_t)blockIdx.x * kTile + r * kTileThreads + tid;
-    if (idx >= n) break;
-    const int32_t row = rows[idx];
-    int lo = 0, hi = ns;  // first splitter > row
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (spl[mid] <= row) lo = mid + 1; else hi = mid;
-    }
-    uint32_t key = (uint32_t)n_var;
-    if (lo > 0) {
-      const int64_t w0 = (int64_t)(lo - 1) << split_shift;
-      const int64_t w1 = min(w0 + (1LL << split_shift), n_var);
-      const int64_t k = sorted_find(ids + w0, w1 - w0, row);
-      if (k >= 0) key = (uint32_t)(w0 + k);
-    }
+    ok[r] = idx < n;
+    row[r] = ok[r] ? rows[idx] : 0;
+  }
+  // level 1 (LDS): lo = number of splitters <= row
+  int lo[kTileIPT];
+#pragma unroll
+  for (int r = 0; r < kTileIPT; ++r) lo[r] = 0;
+  for (int step = kSplitMax; step >= 1; step >>= 1) {
+#pragma unroll
+    for (int r = 0; r < kTileIPT; ++r)
+      if (lo[r] + step <= ns && spl[lo[r] + step - 1] <= row[r]) lo[r] += step;
+  }
+  // level 2 (global): the last id <= row inside that splitter's window
+  const int64_t win = 1LL << split_shift;
+  int64_t pos[kTileIPT], end[kTileIPT];
+#pragma unroll
+  for (int r = 0; r < kTileIPT; ++r) {
+    pos[r] = lo[r] > 0 ? ((int64_t)(lo[r] - 1) << split_shift) : 0;
+    end[r] = lo[r] > 0 ? min(pos[r] + win, n_var) : 0;
+  }
+  for (int64_t step = win >> 1; step >= 1; step >>= 1) {
+#pragma unroll
+    for (int r = 0; r < kTileIPT; ++r)
+      if (pos[r] + step < end[r] && ids[pos[r] + step] <= row[r]) pos[r] += step;
+  }
+#pragma unroll
+  for (int r = 0; r < kTileIPT; ++r) {
+    if (!ok[r]) continue;
+    const int64_t idx = (int64_t)blockIdx.x * kTile + r * kTileThreads + tid;
+    const uint32_t key = (lo[r] > 0 && ids[pos[r]] == row[r]) ? (uint32_t)pos[r] : (uint32_t)n_var;
     keys[idx] = key;
     vals[idx] = (uint32_t)idx;
     atomicAdd(&h[key & mask], 1u);
@@ -253,10 +273,12 @@ __device__ inline int col_of(int sub, int t) {
   return CONSEC ? sub * VPL + t : sub + 32 * t;
 }
 
+// (The state rows and d_out slices are touched once per step: streaming,
+// non-temporal accesses keep them from evicting the sorted keys from L2.)
 template <int VPL, bool CONSEC>
 __device__ inline void load_f32(const float* __restrict__ row, int sub, float x[VPL]) {
   if constexpr (CONSEC && VPL == 4) {
-    const u32x4 q = *(const u32x4*)(row + sub * 4);
+    const u32x4 q = __builtin_nontemporal_load((const u32x4*)(row + sub * 4));
 #pragma unroll
     for (int t = 0; t < 4; ++t) x[t] = __uint_as_float(q[t]);
   } else {
@@ -268,8 +290,9 @@ __device__ inline void load_f32(const float* __restrict__ row, int sub, float x[
 template <int VPL, bool CONSEC>
 __device__ inline void store_f32(float* __restrict__ row, int sub, const float x[VPL]) {
   if constexpr (CONSEC && VPL == 4) {
-    *(u32x4*)(row + sub * 4) = u32x4{__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
-                                     __float_as_uint(x[3])};
+    __builtin_nontemporal_store(u32x4{__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
+                                      __float_as_uint(x[3])},
+                                (u32x4*)(row + sub * 4));
   } else {
 #pragma unroll
     for (int t = 0; t < VPL; ++t) row[col_of<VPL, CONSEC>(sub, t)] = x[t];
@@ -287,7 +310,7 @@ __device__ inline void load_grad(const SegArgs& a, uint32_t slot, int sub, float
   } else {
     const uint16_t* src = (const uint16_t*)a.d_out + base;
     if constexpr (CONSEC && VPL == 4) {
-      const u32x2 q = *(const u32x2*)(src + sub * 4);
+      const u32x2 q = __builtin_nontemporal_load((const u32x2*)(src + sub * 4));
       x[0] = __uint_as_float(q.x << 16);
       x[1] = __uint_as_float(q.x & 0xffff0000u);
       x[2] = __uint_as_float(q.y << 16);
@@ -300,19 +323,19 @@ __device__ inline void load_grad(const SegArgs& a, uint32_t slot, int sub, float
 }
 
 // Sums the d_out slices of `cnt` (<= 32) consecutive sorted slots whose slot
-// ids sit in lane (gbase + e) of `vl`, in order, onto g.  Loads go out eight
+// ids sit in lane (gbase + e) of `vl`, in order, onto g.  Loads go out kBatch
 // slots at a time; the additions stay in slot order.
-template <int VPL, bool CONSEC>
+template <int VPL, bool CONSEC, int kBatch>
 __device__ inline void sum_piece(const SegArgs& a, uint32_t vl, int gbase, int cnt, int sub, float g[VPL]) {
-  for (int e0 = 0; e0 < cnt; e0 += 8) {
-    float x[8][VPL];
+  for (int e0 = 0; e0 < cnt; e0 += kBatch) {
+    float x[kBatch][VPL];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kBatch; ++u) {
       const uint32_t s = (uint32_t)__shfl((int)vl, gbase + ((e0 + u) & 31));
       if (e0 + u < cnt) load_grad<VPL, CONSEC>(a, s, sub, x[u]);
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kBatch; ++u)
       if (e0 + u < cnt) {
 #pragma unroll
         for (int t = 0; t < VPL; ++t) g[t] = g[t] + x[u][t];
@@ -459,7 +482,7 @@ __global__ __launch_bounds__(256) void segment_kernel(const SegArgs a) {
   float g[VPL];
 #pragma unroll
   for (int t = 0; t < VPL; ++t) g[t] = 0.0f;
-  sum_piece<VPL, CONSEC>(a, vl, gbase, cnt, sub, g);
+  sum_piece<VPL, CONSEC, 4>(a, vl, gbase, cnt, sub, g);
   finish<VPL, CONSEC, ADAM>(a, key, sub, g, p, m, v);
 }
 
@@ -472,6 +495,13 @@ __global__ __launch_bounds__(256) void long_kernel(const SegArgs a) {
   for (uint32_t li = blockIdx.x; li < count; li += gridDim.x) {
     const int64_t i0 = a.long_list[li];
     const uint32_t key = a.skeys[i0];
+    float p[VPL], m[VPL], v[VPL];
+    if (ADAM && grp == 0) {  // independent of the gradient: fetched first
+      const int64_t off = (int64_t)key * a.dim;
+      load_f32<VPL, CONSEC>(a.master + off, sub, p);
+      load_f32<VPL, CONSEC>(a.m + off, sub, m);
+      load_f32<VPL, CONSEC>(a.v + off, sub, v);
+    }
     float G[VPL];
 #pragma unroll
     for (int t = 0; t < VPL; ++t) G[t] = 0.0f;
@@ -485,7 +515,7 @@ __global__ __launch_bounds__(256) void long_kernel(const SegArgs a) {
       float P[VPL];
 #pragma unroll
       for (int t = 0; t < VPL; ++t) P[t] = 0.0f;
-      sum_piece<VPL, CONSEC>(a, vl, gbase, cnt, sub, P);
+      sum_piece<VPL, CONSEC, 16>(a, vl, gbase, cnt, sub, P);
 #pragma unroll
       for (int t = 0; t < VPL; ++t) G[t] = G[t] + P[t];
       if (cnt < kPiece) break;
@@ -494,18 +524,12 @@ __global__ __launch_bounds__(256) void long_kernel(const SegArgs a) {
     for (int t = 0; t < VPL; ++t) part[grp][col_of<VPL, CONSEC>(sub, t)] = G[t];
     __syncthreads();
     if (grp == 0) {
-      float g[VPL], p[VPL], m[VPL], v[VPL];
+      float g[VPL];
 #pragma unroll
       for (int t = 0; t < VPL; ++t) {
         const int c = col_of<VPL, CONSEC>(sub, t);
         g[t] = part[0][c];
         for (int q = 1; q < kLongGroups; ++q) g[t] = g[t] + part[q][c];
-      }
-      if constexpr (ADAM) {
-        const int64_t off = (int64_t)key * a.dim;
-        load_f32<VPL, CONSEC>(a.master + off, sub, p);
-        load_f32<VPL, CONSEC>(a.m + off, sub, m);
-        load_f32<VPL, CONSEC>(a.v + off, sub, v);
       }
       finish<VPL, CONSEC, ADAM>(a, key, sub, g, p, m, v);
     }
