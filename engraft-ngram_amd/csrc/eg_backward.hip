@@ -452,47 +452,32 @@ __device__ inline void finish(const SegArgs& a, int64_t k, int sub, const float 
   }
 }
 
-// One 32-lane group per sorted position; the group at the first slot of a
-// segment of at most kPiece slots reduces it; longer segments are listed.
-template <int VPL, bool CONSEC, bool ADAM>
-__global__ __launch_bounds__(256) void segment_kernel(const SegArgs a) {
-  const int lane = threadIdx.x & 63, sub = lane & 31, gbase = lane & 32;
-  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 5;
-  if (i >= a.n) return;  // uniform per group
-  // The window [i, i+32), its neighbours i-1 and i+32: one round of loads.
-  const uint32_t kl = (i + sub < a.n) ? a.skeys[i + sub] : 0xffffffffu;
-  const uint32_t vl = (i + sub < a.n) ? a.svals[i + sub] : 0u;
-  const uint32_t prev = (i > 0) ? a.skeys[i - 1] : 0xffffffffu;
-  const uint32_t next = (i + kPiece < a.n) ? a.skeys[i + kPiece] : 0xffffffffu;
-  const uint32_t key = (uint32_t)__shfl((int)kl, gbase);
-  if ((int64_t)key >= a.n_var) return;  // frozen rows: no variable
-  if (prev == key) return;              // not the segment's first slot
-  if (next == key) {
-    if (sub == 0) a.long_list[atomicAdd(a.long_count, 1u)] = (uint32_t)i;
-    return;
-  }
-  float p[VPL], m[VPL], v[VPL];
-  if constexpr (ADAM) {  // the state rows do not depend on the gradient: fetch them first
-    const int64_t off = (int64_t)key * a.dim;
-    load_f32<VPL, CONSEC>(a.master + off, sub, p);
-    load_f32<VPL, CONSEC>(a.m + off, sub, m);
-    load_f32<VPL, CONSEC>(a.v + off, sub, v);
-  }
-  const int cnt = __popc((uint32_t)(__ballot(kl == key) >> gbase));
-  float g[VPL];
-#pragma unroll
-  for (int t = 0; t < VPL; ++t) g[t] = 0.0f;
-  sum_piece<VPL, CONSEC, 4>(a, vl, gbase, cnt, sub, g);
-  finish<VPL, CONSEC, ADAM>(a, key, sub, g, p, m, v);
+// Lists the first sorted position of every segment longer than kPiece slots.
+__global__ __launch_bounds__(256) void long_detect_kernel(const uint32_t* __restrict__ skeys, int64_t n,
+                                                          int64_t n_var, uint32_t* __restrict__ long_list,
+                                                          uint32_t* __restrict__ long_count) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i + kPiece >= n) return;
+  const uint32_t key = skeys[i];
+  if ((int64_t)key >= n_var || skeys[i + kPiece] != key) return;
+  if (i > 0 && skeys[i - 1] == key) return;
+  long_list[atomicAdd(long_count, 1u)] = (uint32_t)i;
 }
 
-// One workgroup per listed long segment (grid-stride over the list).
+// One launch for every segment.  The first n_long_blocks workgroups take the
+// listed long segments (one each: pieces of kPiece slots summed in order,
+// piece j added to group j mod kLongGroups, the group sums added in group
+// order); they are dispatched first, so their longer chains overlap the rest.
+// Every other workgroup holds eight 32-lane groups, one per sorted position:
+// the group at the first slot of a segment of at most kPiece slots reduces it.
 template <int VPL, bool CONSEC, bool ADAM>
-__global__ __launch_bounds__(256) void long_kernel(const SegArgs a) {
+__global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_long_blocks) {
   __shared__ float part[kLongGroups][512];
-  const int grp = threadIdx.x >> 5, sub = threadIdx.x & 31, gbase = threadIdx.x & 32;
-  const uint32_t count = *a.long_count;
-  for (uint32_t li = blockIdx.x; li < count; li += gridDim.x) {
+  const int lane = threadIdx.x & 63, sub = lane & 31, gbase = lane & 32;
+  if ((int64_t)blockIdx.x < n_long_blocks) {
+    const uint32_t li = blockIdx.x;
+    if (li >= *a.long_count) return;  // uniform per workgroup
+    const int grp = threadIdx.x >> 5;
     const int64_t i0 = a.long_list[li];
     const uint32_t key = a.skeys[i0];
     float p[VPL], m[VPL], v[VPL];
@@ -515,7 +500,7 @@ __global__ __launch_bounds__(256) void long_kernel(const SegArgs a) {
       float P[VPL];
 #pragma unroll
       for (int t = 0; t < VPL; ++t) P[t] = 0.0f;
-      sum_piece<VPL, CONSEC, 16>(a, vl, gbase, cnt, sub, P);
+      sum_piece<VPL, CONSEC, 4>(a, vl, gbase, cnt, sub, P);
 #pragma unroll
       for (int t = 0; t < VPL; ++t) G[t] = G[t] + P[t];
       if (cnt < kPiece) break;
@@ -533,8 +518,32 @@ __global__ __launch_bounds__(256) void long_kernel(const SegArgs a) {
       }
       finish<VPL, CONSEC, ADAM>(a, key, sub, g, p, m, v);
     }
-    __syncthreads();
+    return;
   }
+  const int64_t i = (((int64_t)blockIdx.x - n_long_blocks) * 256 + threadIdx.x) >> 5;
+  if (i >= a.n) return;  // uniform per group
+  // The window [i, i+32), its neighbours i-1 and i+32: one round of loads.
+  const uint32_t kl = (i + sub < a.n) ? a.skeys[i + sub] : 0xffffffffu;
+  const uint32_t vl = (i + sub < a.n) ? a.svals[i + sub] : 0u;
+  const uint32_t prev = (i > 0) ? a.skeys[i - 1] : 0xffffffffu;
+  const uint32_t next = (i + kPiece < a.n) ? a.skeys[i + kPiece] : 0xffffffffu;
+  const uint32_t key = (uint32_t)__shfl((int)kl, gbase);
+  if ((int64_t)key >= a.n_var) return;  // frozen rows: no variable
+  if (prev == key) return;              // not the segment's first slot
+  if (next == key) return;              // a long segment: its own workgroup takes it
+  float p[VPL], m[VPL], v[VPL];
+  if constexpr (ADAM) {  // the state rows do not depend on the gradient: fetch them first
+    const int64_t off = (int64_t)key * a.dim;
+    load_f32<VPL, CONSEC>(a.master + off, sub, p);
+    load_f32<VPL, CONSEC>(a.m + off, sub, m);
+    load_f32<VPL, CONSEC>(a.v + off, sub, v);
+  }
+  const int cnt = __popc((uint32_t)(__ballot(kl == key) >> gbase));
+  float g[VPL];
+#pragma unroll
+  for (int t = 0; t < VPL; ++t) g[t] = 0.0f;
+  sum_piece<VPL, CONSEC, 4>(a, vl, gbase, cnt, sub, g);
+  finish<VPL, CONSEC, ADAM>(a, key, sub, g, p, m, v);
 }
 
 // Dense mode: the variables no slot hit this step take a zero-gradient step.
@@ -634,11 +643,11 @@ static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_
 
 template <bool ADAM, int VPL, bool CONSEC>
 static void launch_reduce_t(const SegArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)((a.n * 32 + 255) / 256));
-  hipLaunchKernelGGL((segment_kernel<VPL, CONSEC, ADAM>), grid, dim3(256), 0, st, a);
-  const int64_t max_long = a.n / (kPiece + 1) + 1;
-  const unsigned long_grid = (unsigned)(max_long < 1024 ? max_long : 1024);
-  hipLaunchKernelGGL((long_kernel<VPL, CONSEC, ADAM>), dim3(long_grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(long_detect_kernel, dim3((unsigned)((a.n + 255) / 256)), dim3(256), 0, st, a.skeys, a.n,
+                     a.n_var, a.long_list, a.long_count);
+  const int64_t n_long_blocks = a.n / (kPiece + 1) + 1;  // more long segments cannot fit in n slots
+  const dim3 grid((unsigned)(n_long_blocks + (a.n * 32 + 255) / 256));
+  hipLaunchKernelGGL((reduce_kernel<VPL, CONSEC, ADAM>), grid, dim3(256), 0, st, a, n_long_blocks);
 }
 
 template <bool ADAM>
@@ -650,7 +659,7 @@ static int launch_reduce(const SegArgs& a, hipStream_t st) {
     case 160: launch_reduce_t<ADAM, 5, false>(a, st); break;
     default: return set_error(EG_ERR_UNSUPPORTED, "backward for dim %d (built: 64, 128, 160, 256)", a.dim);
   }
-  return launch_status("segment/long kernels");
+  return launch_status("long_detect/reduce kernels");
 }
 
 static int launch_dense(const SegArgs& a, hipStream_t st) {
