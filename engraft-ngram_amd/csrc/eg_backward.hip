@@ -10,10 +10,10 @@
 //            variables keep ascending slot order
 //   segment  one 32-lane group per segment of at most 32 slots sums the
 //            slots' d_out slices in slot order (fp32) and runs Adam +
-//            requantisation on the variable; longer segments are listed and
-//   long     reduced by a whole workgroup: pieces of 32 slots summed in order,
-//            piece sums accumulated per group (pieces j = g mod 8), the eight
-//            group sums added in group order
+//            requantisation on the variable; a longer segment is reduced by
+//            a whole workgroup of the same launch: pieces of 32 slots summed
+//            in order, piece sums accumulated per group (pieces j = g mod 8),
+//            the eight group sums added in group order
 //   dense    variables no slot hit take their zero-gradient step (dense mode)
 //
 // No floating-point atomics: the association of every sum is fixed by the
@@ -40,15 +40,13 @@ constexpr int kLongGroups = 8;   // 32-lane groups per long-segment workgroup
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kTileThreads) void keys_hist_kernel(
     const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ ids, int64_t n_var, int split_shift,
-    uint32_t* __restrict__ keys, uint32_t* __restrict__ vals, int dbits, int n_tiles, uint32_t* __restrict__ hist,
-    uint32_t* __restrict__ long_count) {
+    uint32_t* __restrict__ keys, uint32_t* __restrict__ vals, int dbits, int n_tiles, uint32_t* __restrict__ hist) {
   __shared__ int32_t spl[kSplitMax];
   __shared__ uint32_t h[kMaxBuckets];
   const int tid = threadIdx.x;
   const int ns = (int)((n_var + (1LL << split_shift) - 1) >> split_shift);
   for (int i = tid; i < ns; i += kTileThreads) spl[i] = ids[(int64_t)i << split_shift];
   for (int i = tid; i < kMaxBuckets; i += kTileThreads) h[i] = 0;
-  if (blockIdx.x == 0 && tid == 0) *long_count = 0;
   __syncthreads();
   const uint32_t mask = (1u << dbits) - 1u;
   // The kTileIPT lookups of a thread run in lockstep (fixed-length branchless
@@ -93,7 +91,7 @@ __global__ __launch_bounds__(kTileThreads) void keys_hist_kernel(
     atomicAdd(&h[key & mask], 1u);
   }
   __syncthreads();
-  for (int d = tid; d < (1 << dbits); d += kTileThreads) hist[(int64_t)d * n_tiles + blockIdx.x] = h[d];
+  for (int d = tid; d < (1 << dbits); d += kTileThreads) hist[(int64_t)blockIdx.x * (1 << dbits) + d] = h[d];
 }
 
 // ---------------------------------------------------------------------------
@@ -130,7 +128,16 @@ constexpr int kScanChunk = 4 * kScanThreads;  // entries per scan workgroup
 
 // Pass 1 of the exclusive scan: the total of every chunk; also clears the next
 // pass's histogram.
+// The histograms are tile-major (tile t's digit d at t * n_buckets + d, so every
+// tile writes its counts contiguously); the scans run over them in digit-major
+// order L = d * n_tiles + t.
+__device__ inline int64_t hist_phys(int64_t L, int n_tiles, int dbits) {
+  const int64_t d = L / n_tiles;
+  return (L - d * n_tiles) * (1LL << dbits) + d;
+}
+
 __global__ __launch_bounds__(kScanThreads) void scan_partials(const uint32_t* __restrict__ a, int64_t len,
+                                                              int n_tiles, int dbits,
                                                               uint32_t* __restrict__ partial,
                                                               uint32_t* __restrict__ clear, int64_t clear_len) {
   __shared__ uint32_t wsum[kScanThreads / 64];
@@ -140,7 +147,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_partials(const uint32_t* __
   const int64_t i0 = (int64_t)blockIdx.x * kScanChunk + 4 * tid;
   uint32_t t = 0;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) t += (i0 + u < len) ? a[i0 + u] : 0u;
+  for (int u = 0; u < 4; ++u) t += (i0 + u < len) ? a[hist_phys(i0 + u, n_tiles, dbits)] : 0u;
   uint32_t total;
   block_exclusive_scan(t, wsum, &total);
   if (tid == 0) partial[blockIdx.x] = total;
@@ -148,8 +155,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_partials(const uint32_t* __
 
 // Pass 2: exclusive scan of every chunk, offset by the totals of the chunks
 // before it.
-__global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict__ a, int64_t len,
-                                                           const uint32_t* __restrict__ partial) {
+__global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict__ a, int64_t len, int n_tiles,
+                                                           int dbits, const uint32_t* __restrict__ partial) {
   __shared__ uint32_t wsum[kScanThreads / 64];
   __shared__ uint32_t wsum2[kScanThreads / 64];
   const int tid = threadIdx.x;
@@ -158,7 +165,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict_
   const int64_t i0 = (int64_t)blockIdx.x * kScanChunk + 4 * tid;
   uint32_t v[4];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) v[u] = (i0 + u < len) ? a[i0 + u] : 0u;
+  for (int u = 0; u < 4; ++u) v[u] = (i0 + u < len) ? a[hist_phys(i0 + u, n_tiles, dbits)] : 0u;
   uint32_t base;
   block_exclusive_scan(pre, wsum2, &base);  // base = sum of every thread's share of the earlier chunks
   __syncthreads();
@@ -166,7 +173,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict_
   uint32_t run = base + block_exclusive_scan(v[0] + v[1] + v[2] + v[3], wsum, &total);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    if (i0 + u < len) a[i0 + u] = run;
+    if (i0 + u < len) a[hist_phys(i0 + u, n_tiles, dbits)] = run;
     run += v[u];
   }
 }
@@ -188,7 +195,7 @@ __global__ __launch_bounds__(kTileThreads) void scatter_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n_buckets = 1 << dbits;
   for (int d = tid; d < n_buckets; d += kTileThreads) {
-    run[d] = offs[(int64_t)d * n_tiles + blockIdx.x];
+    run[d] = offs[(int64_t)blockIdx.x * n_buckets + d];
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) wcnt[w][d] = 0;
   }
@@ -220,7 +227,7 @@ __global__ __launch_bounds__(kTileThreads) void scatter_kernel(
       keys_out[pos] = key;
       vals_out[pos] = val;
       if (hist_next != nullptr)
-        atomicAdd(&hist_next[(int64_t)((key >> next_shift) & next_mask) * n_tiles + pos / kTile], 1u);
+        atomicAdd(&hist_next[(int64_t)(pos / kTile) * (1 << next_dbits) + ((key >> next_shift) & next_mask)], 1u);
     }
     __syncthreads();
     for (int dd = tid; dd < n_buckets; dd += kTileThreads) {
@@ -244,8 +251,6 @@ struct SegArgs {
   const uint32_t* svals;  // slot ids in the same order
   int64_t n;
   int64_t n_var;
-  uint32_t* long_list;    // first sorted position of every segment longer than kPiece
-  uint32_t* long_count;
   const void* d_out;
   int32_t d_out_f32;
   int32_t heads;
@@ -452,22 +457,13 @@ __device__ inline void finish(const SegArgs& a, int64_t k, int sub, const float 
   }
 }
 
-// Lists the first sorted position of every segment longer than kPiece slots.
-__global__ __launch_bounds__(256) void long_detect_kernel(const uint32_t* __restrict__ skeys, int64_t n,
-                                                          int64_t n_var, uint32_t* __restrict__ long_list,
-                                                          uint32_t* __restrict__ long_count) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i + kPiece >= n) return;
-  const uint32_t key = skeys[i];
-  if ((int64_t)key >= n_var || skeys[i + kPiece] != key) return;
-  if (i > 0 && skeys[i - 1] == key) return;
-  long_list[atomicAdd(long_count, 1u)] = (uint32_t)i;
-}
-
-// One launch for every segment.  The first n_long_blocks workgroups take the
-// listed long segments (one each: pieces of kPiece slots summed in order,
-// piece j added to group j mod kLongGroups, the group sums added in group
-// order); they are dispatched first, so their longer chains overlap the rest.
+// One launch for every segment.  A segment longer than kPiece slots is taken
+// by one of the first n_long_blocks workgroups: block b owns the sorted
+// positions [(kPiece+1) b, (kPiece+1)(b+1)), which hold at most one long
+// segment's first slot (two such firsts are more than kPiece apart).  It sums
+// pieces of kPiece slots in order, adds piece j to group j mod kLongGroups and
+// the group sums in group order.  These blocks are dispatched first, so their
+// longer chains overlap the rest.
 // Every other workgroup holds eight 32-lane groups, one per sorted position:
 // the group at the first slot of a segment of at most kPiece slots reduces it.
 template <int VPL, bool CONSEC, bool ADAM>
@@ -475,10 +471,20 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
   __shared__ float part[kLongGroups][512];
   const int lane = threadIdx.x & 63, sub = lane & 31, gbase = lane & 32;
   if ((int64_t)blockIdx.x < n_long_blocks) {
-    const uint32_t li = blockIdx.x;
-    if (li >= *a.long_count) return;  // uniform per workgroup
+    __shared__ int64_t found;
+    if (threadIdx.x == 0) found = -1;
+    __syncthreads();
+    if (threadIdx.x <= kPiece) {
+      const int64_t c = (int64_t)blockIdx.x * (kPiece + 1) + threadIdx.x;
+      if (c + kPiece < a.n) {
+        const uint32_t kc = a.skeys[c];
+        if ((int64_t)kc < a.n_var && a.skeys[c + kPiece] == kc && (c == 0 || a.skeys[c - 1] != kc)) found = c;
+      }
+    }
+    __syncthreads();
+    if (found < 0) return;  // uniform per workgroup
     const int grp = threadIdx.x >> 5;
-    const int64_t i0 = a.long_list[li];
+    const int64_t i0 = found;
     const uint32_t key = a.skeys[i0];
     float p[VPL], m[VPL], v[VPL];
     if (ADAM && grp == 0) {  // independent of the gradient: fetched first
@@ -571,8 +577,6 @@ struct Workspace {
   uint32_t* vals[2];
   uint32_t* hist[2];
   uint32_t* partial;  // per scan chunk
-  uint32_t* long_count;
-  uint32_t* long_list;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -586,7 +590,7 @@ static size_t partial_bytes(int64_t n) {
 static size_t workspace_bytes(int64_t n) {
   const size_t kb = align256((size_t)n * 4);
   const size_t hb = align256((size_t)n_tiles_of(n) * kMaxBuckets * 4);
-  return 4 * kb + 2 * hb + partial_bytes(n) + 256 + align256((size_t)(n / (kPiece + 1) + 1) * 4);
+  return 4 * kb + 2 * hb + partial_bytes(n);
 }
 
 static Workspace carve(void* ws, int64_t n) {
@@ -601,8 +605,6 @@ static Workspace carve(void* ws, int64_t n) {
   w.hist[0] = (uint32_t*)(p + 4 * kb);
   w.hist[1] = (uint32_t*)(p + 4 * kb + hb);
   w.partial = (uint32_t*)(p + 4 * kb + 2 * hb);
-  w.long_count = (uint32_t*)(p + 4 * kb + 2 * hb + partial_bytes(n));
-  w.long_list = (uint32_t*)(p + 4 * kb + 2 * hb + partial_bytes(n) + 256);
   return w;
 }
 
@@ -617,7 +619,7 @@ static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_
   while (((n_var + (1LL << split_shift) - 1) >> split_shift) > kSplitMax) ++split_shift;
   const int n_tiles = (int)n_tiles_of(n);
   hipLaunchKernelGGL(keys_hist_kernel, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var, split_shift,
-                     w.keys[0], w.vals[0], dbits, n_tiles, w.hist[0], w.long_count);
+                     w.keys[0], w.vals[0], dbits, n_tiles, w.hist[0]);
   int rc = launch_status("keys_hist_kernel");
   if (rc != EG_OK) return rc;
   int cur = 0;
@@ -627,9 +629,9 @@ static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_
     uint32_t* h_next = last ? nullptr : w.hist[(pass + 1) & 1];
     const int64_t len = (int64_t)n_tiles << dbits;
     const unsigned chunks = (unsigned)((len + kScanChunk - 1) / kScanChunk);
-    hipLaunchKernelGGL(scan_partials, dim3(chunks), dim3(kScanThreads), 0, st, h, len, w.partial, h_next,
-                       last ? (int64_t)0 : len);
-    hipLaunchKernelGGL(scan_apply, dim3(chunks), dim3(kScanThreads), 0, st, h, len, w.partial);
+    hipLaunchKernelGGL(scan_partials, dim3(chunks), dim3(kScanThreads), 0, st, h, len, n_tiles, dbits, w.partial,
+                       h_next, last ? (int64_t)0 : len);
+    hipLaunchKernelGGL(scan_apply, dim3(chunks), dim3(kScanThreads), 0, st, h, len, n_tiles, dbits, w.partial);
     hipLaunchKernelGGL(scatter_kernel, dim3(n_tiles), dim3(kTileThreads), 0, st, w.keys[cur], w.vals[cur],
                        w.keys[cur ^ 1], w.vals[cur ^ 1], n, pass * dbits, dbits, n_tiles, h, h_next,
                        (pass + 1) * dbits, dbits);
@@ -643,9 +645,7 @@ static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_
 
 template <bool ADAM, int VPL, bool CONSEC>
 static void launch_reduce_t(const SegArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(long_detect_kernel, dim3((unsigned)((a.n + 255) / 256)), dim3(256), 0, st, a.skeys, a.n,
-                     a.n_var, a.long_list, a.long_count);
-  const int64_t n_long_blocks = a.n / (kPiece + 1) + 1;  // more long segments cannot fit in n slots
+  const int64_t n_long_blocks = (a.n + kPiece) / (kPiece + 1);
   const dim3 grid((unsigned)(n_long_blocks + (a.n * 32 + 255) / 256));
   hipLaunchKernelGGL((reduce_kernel<VPL, CONSEC, ADAM>), grid, dim3(256), 0, st, a, n_long_blocks);
 }
@@ -659,7 +659,7 @@ static int launch_reduce(const SegArgs& a, hipStream_t st) {
     case 160: launch_reduce_t<ADAM, 5, false>(a, st); break;
     default: return set_error(EG_ERR_UNSUPPORTED, "backward for dim %d (built: 64, 128, 160, 256)", a.dim);
   }
-  return launch_status("long_detect/reduce kernels");
+  return launch_status("reduce_kernel");
 }
 
 static int launch_dense(const SegArgs& a, hipStream_t st) {
@@ -717,8 +717,6 @@ int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   a.svals = w.vals[cur];
   a.n = n;
   a.n_var = n_var;
-  a.long_list = w.long_list;
-  a.long_count = w.long_count;
   a.d_out = d_out;
   a.d_out_f32 = d_out_f32;
   a.heads = heads;
@@ -767,8 +765,6 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   a.svals = w.vals[cur];
   a.n = n;
   a.n_var = state->n;
-  a.long_list = w.long_list;
-  a.long_count = w.long_count;
   a.d_out = d_out;
   a.d_out_f32 = d_out_f32;
   a.heads = heads;
