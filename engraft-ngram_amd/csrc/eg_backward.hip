@@ -36,15 +36,47 @@ constexpr int kPiece = 32;       // slots per piece of a long segment
 constexpr int kLongGroups = 8;   // 32-lane groups per long-segment workgroup
 
 // ---------------------------------------------------------------------------
+// Row index: open addressing over a power-of-two table of (row << 32 | k)
+// entries, Fibonacci hashing, linear probing.  Lookups are deterministic
+// whatever order the entries were inserted in.
+// ---------------------------------------------------------------------------
+constexpr unsigned long long kIndexEmpty = ~0ull;
+
+__device__ inline uint64_t index_slot(int32_t row, int bits) {
+  return (uint64_t)(((uint32_t)row * 0x9E3779B1u) >> (32 - bits));
+}
+
+__global__ __launch_bounds__(256) void index_fill_kernel(unsigned long long* __restrict__ tab, int64_t cap) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < cap; i += (int64_t)gridDim.x * 256)
+    tab[i] = kIndexEmpty;
+}
+
+__global__ __launch_bounds__(256) void index_build_kernel(const int32_t* __restrict__ ids, int64_t n,
+                                                          unsigned long long* __restrict__ tab, int bits) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= n) return;
+  const int32_t row = ids[k];
+  const uint64_t mask = (1ull << bits) - 1ull;
+  const unsigned long long packed = ((unsigned long long)(uint32_t)row << 32) | (uint32_t)k;
+  uint64_t h = index_slot(row, bits);
+  for (uint64_t probe = 0; probe <= mask; ++probe) {  // the table is at most half full
+    if (atomicCAS(&tab[h], kIndexEmpty, packed) == kIndexEmpty) return;
+    h = (h + 1) & mask;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Keys + first histogram
 // ---------------------------------------------------------------------------
+template <bool INDEX>
 __global__ __launch_bounds__(kTileThreads) void keys_hist_kernel(
     const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ ids, int64_t n_var, int split_shift,
-    uint32_t* __restrict__ keys, uint32_t* __restrict__ vals, int dbits, int n_tiles, uint32_t* __restrict__ hist) {
+    const unsigned long long* __restrict__ index, int index_bits, uint32_t* __restrict__ keys,
+    uint32_t* __restrict__ vals, int dbits, int n_tiles, uint32_t* __restrict__ hist) {
   __shared__ int32_t spl[kSplitMax];
   __shared__ uint32_t h[kMaxBuckets];
   const int tid = threadIdx.x;
-  const int ns = (int)((n_var + (1LL << split_shift) - 1) >> split_shift);
+  const int ns = INDEX ? 0 : (int)((n_var + (1LL << split_shift) - 1) >> split_shift);
   for (int i = tid; i < ns; i += kTileThreads) spl[i] = ids[(int64_t)i << split_shift];
   for (int i = tid; i < kMaxBuckets; i += kTileThreads) h[i] = 0;
   __syncthreads();
@@ -59,39 +91,74 @@ __global__ __launch_bounds__(kTileThreads) void keys_hist_kernel(
     ok[r] = idx < n;
     row[r] = ok[r] ? rows[idx] : 0;
   }
-  // level 1 (LDS): lo = number of splitters <= row
-  int lo[kTileIPT];
+  uint32_t key[kTileIPT];
+  if constexpr (INDEX) {
+    // probe the row index; the items' probes advance in lockstep
+    const uint64_t imask = (1ull << index_bits) - 1ull;
+    uint64_t hslot[kTileIPT];
+    bool done[kTileIPT];
 #pragma unroll
-  for (int r = 0; r < kTileIPT; ++r) lo[r] = 0;
-  for (int step = kSplitMax; step >= 1; step >>= 1) {
+    for (int r = 0; r < kTileIPT; ++r) {
+      hslot[r] = index_slot(row[r], index_bits);
+      done[r] = !ok[r];
+      key[r] = (uint32_t)n_var;
+    }
+    for (uint64_t probe = 0; probe <= imask; ++probe) {
+      bool any = false;
 #pragma unroll
-    for (int r = 0; r < kTileIPT; ++r)
-      if (lo[r] + step <= ns && spl[lo[r] + step - 1] <= row[r]) lo[r] += step;
-  }
-  // level 2 (global): the last id <= row inside that splitter's window
-  const int64_t win = 1LL << split_shift;
-  int64_t pos[kTileIPT], end[kTileIPT];
+      for (int r = 0; r < kTileIPT; ++r) {
+        if (done[r]) continue;
+        const unsigned long long e = index[hslot[r]];
+        if (e == kIndexEmpty) {
+          done[r] = true;
+        } else if ((uint32_t)(e >> 32) == (uint32_t)row[r]) {
+          key[r] = (uint32_t)e;
+          done[r] = true;
+        } else {
+          hslot[r] = (hslot[r] + 1) & imask;
+          any = true;
+        }
+      }
+      if (!any) break;
+    }
+  } else {
+    // level 1 (LDS): lo = number of splitters <= row
+    int lo[kTileIPT];
 #pragma unroll
-  for (int r = 0; r < kTileIPT; ++r) {
-    pos[r] = lo[r] > 0 ? ((int64_t)(lo[r] - 1) << split_shift) : 0;
-    end[r] = lo[r] > 0 ? min(pos[r] + win, n_var) : 0;
-  }
-  for (int64_t step = win >> 1; step >= 1; step >>= 1) {
+    for (int r = 0; r < kTileIPT; ++r) lo[r] = 0;
+    for (int step = kSplitMax; step >= 1; step >>= 1) {
 #pragma unroll
-    for (int r = 0; r < kTileIPT; ++r)
-      if (pos[r] + step < end[r] && ids[pos[r] + step] <= row[r]) pos[r] += step;
+      for (int r = 0; r < kTileIPT; ++r)
+        if (lo[r] + step <= ns && spl[lo[r] + step - 1] <= row[r]) lo[r] += step;
+    }
+    // level 2 (global): the last id <= row inside that splitter's window
+    const int64_t win = 1LL << split_shift;
+    int64_t pos[kTileIPT], end[kTileIPT];
+#pragma unroll
+    for (int r = 0; r < kTileIPT; ++r) {
+      pos[r] = lo[r] > 0 ? ((int64_t)(lo[r] - 1) << split_shift) : 0;
+      end[r] = lo[r] > 0 ? min(pos[r] + win, n_var) : 0;
+    }
+    for (int64_t step = win >> 1; step >= 1; step >>= 1) {
+#pragma unroll
+      for (int r = 0; r < kTileIPT; ++r)
+        if (pos[r] + step < end[r] && ids[pos[r] + step] <= row[r]) pos[r] += step;
+    }
+#pragma unroll
+    for (int r = 0; r < kTileIPT; ++r) {
+      key[r] = (ok[r] && lo[r] > 0 && ids[pos[r]] == row[r]) ? (uint32_t)pos[r] : (uint32_t)n_var;
+    }
   }
 #pragma unroll
   for (int r = 0; r < kTileIPT; ++r) {
     if (!ok[r]) continue;
     const int64_t idx = (int64_t)blockIdx.x * kTile + r * kTileThreads + tid;
-    const uint32_t key = (lo[r] > 0 && ids[pos[r]] == row[r]) ? (uint32_t)pos[r] : (uint32_t)n_var;
-    keys[idx] = key;
+    keys[idx] = key[r];
     vals[idx] = (uint32_t)idx;
-    atomicAdd(&h[key & mask], 1u);
+    atomicAdd(&h[key[r] & mask], 1u);
   }
   __syncthreads();
-  for (int d = tid; d < (1 << dbits); d += kTileThreads) hist[(int64_t)blockIdx.x * (1 << dbits) + d] = h[d];
+  for (int d = tid; d < (1 << dbits); d += kTileThreads) hist[(int64_t)d * n_tiles + blockIdx.x] = h[d];
 }
 
 // ---------------------------------------------------------------------------
@@ -128,16 +195,7 @@ constexpr int kScanChunk = 4 * kScanThreads;  // entries per scan workgroup
 
 // Pass 1 of the exclusive scan: the total of every chunk; also clears the next
 // pass's histogram.
-// The histograms are tile-major (tile t's digit d at t * n_buckets + d, so every
-// tile writes its counts contiguously); the scans run over them in digit-major
-// order L = d * n_tiles + t.
-__device__ inline int64_t hist_phys(int64_t L, int n_tiles, int dbits) {
-  const int64_t d = L / n_tiles;
-  return (L - d * n_tiles) * (1LL << dbits) + d;
-}
-
 __global__ __launch_bounds__(kScanThreads) void scan_partials(const uint32_t* __restrict__ a, int64_t len,
-                                                              int n_tiles, int dbits,
                                                               uint32_t* __restrict__ partial,
                                                               uint32_t* __restrict__ clear, int64_t clear_len) {
   __shared__ uint32_t wsum[kScanThreads / 64];
@@ -147,7 +205,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_partials(const uint32_t* __
   const int64_t i0 = (int64_t)blockIdx.x * kScanChunk + 4 * tid;
   uint32_t t = 0;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) t += (i0 + u < len) ? a[hist_phys(i0 + u, n_tiles, dbits)] : 0u;
+  for (int u = 0; u < 4; ++u) t += (i0 + u < len) ? a[i0 + u] : 0u;
   uint32_t total;
   block_exclusive_scan(t, wsum, &total);
   if (tid == 0) partial[blockIdx.x] = total;
@@ -155,8 +213,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_partials(const uint32_t* __
 
 // Pass 2: exclusive scan of every chunk, offset by the totals of the chunks
 // before it.
-__global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict__ a, int64_t len, int n_tiles,
-                                                           int dbits, const uint32_t* __restrict__ partial) {
+__global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict__ a, int64_t len,
+                                                           const uint32_t* __restrict__ partial) {
   __shared__ uint32_t wsum[kScanThreads / 64];
   __shared__ uint32_t wsum2[kScanThreads / 64];
   const int tid = threadIdx.x;
@@ -165,7 +223,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict_
   const int64_t i0 = (int64_t)blockIdx.x * kScanChunk + 4 * tid;
   uint32_t v[4];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) v[u] = (i0 + u < len) ? a[hist_phys(i0 + u, n_tiles, dbits)] : 0u;
+  for (int u = 0; u < 4; ++u) v[u] = (i0 + u < len) ? a[i0 + u] : 0u;
   uint32_t base;
   block_exclusive_scan(pre, wsum2, &base);  // base = sum of every thread's share of the earlier chunks
   __syncthreads();
@@ -173,7 +231,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict_
   uint32_t run = base + block_exclusive_scan(v[0] + v[1] + v[2] + v[3], wsum, &total);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    if (i0 + u < len) a[hist_phys(i0 + u, n_tiles, dbits)] = run;
+    if (i0 + u < len) a[i0 + u] = run;
     run += v[u];
   }
 }
@@ -195,7 +253,7 @@ __global__ __launch_bounds__(kTileThreads) void scatter_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n_buckets = 1 << dbits;
   for (int d = tid; d < n_buckets; d += kTileThreads) {
-    run[d] = offs[(int64_t)blockIdx.x * n_buckets + d];
+    run[d] = offs[(int64_t)d * n_tiles + blockIdx.x];
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) wcnt[w][d] = 0;
   }
@@ -227,7 +285,7 @@ __global__ __launch_bounds__(kTileThreads) void scatter_kernel(
       keys_out[pos] = key;
       vals_out[pos] = val;
       if (hist_next != nullptr)
-        atomicAdd(&hist_next[(int64_t)(pos / kTile) * (1 << next_dbits) + ((key >> next_shift) & next_mask)], 1u);
+        atomicAdd(&hist_next[(int64_t)((key >> next_shift) & next_mask) * n_tiles + pos / kTile], 1u);
     }
     __syncthreads();
     for (int dd = tid; dd < n_buckets; dd += kTileThreads) {
@@ -609,8 +667,8 @@ static Workspace carve(void* ws, int64_t n) {
 }
 
 // keys + stable radix sort; *sorted = index (0/1) of the sorted buffers.
-static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_t n_var, const Workspace& w,
-                      hipStream_t st, int* sorted) {
+static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_t n_var, const int64_t* index,
+                      int64_t index_capacity, const Workspace& w, hipStream_t st, int* sorted) {
   int bits = 0;
   while (bits < 32 && ((uint64_t)n_var >> bits) != 0) ++bits;  // keys lie in [0, n_var]
   const int passes = bits == 0 ? 0 : (bits + kMaxDigitBits - 1) / kMaxDigitBits;
@@ -618,8 +676,16 @@ static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_
   int split_shift = 0;
   while (((n_var + (1LL << split_shift) - 1) >> split_shift) > kSplitMax) ++split_shift;
   const int n_tiles = (int)n_tiles_of(n);
-  hipLaunchKernelGGL(keys_hist_kernel, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var, split_shift,
-                     w.keys[0], w.vals[0], dbits, n_tiles, w.hist[0]);
+  if (index != nullptr) {
+    int ib = 0;
+    while ((1LL << ib) < index_capacity) ++ib;
+    hipLaunchKernelGGL(keys_hist_kernel<true>, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
+                       (const unsigned long long*)index, ib, w.keys[0], w.vals[0], dbits, n_tiles, w.hist[0]);
+  } else {
+    hipLaunchKernelGGL(keys_hist_kernel<false>, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var,
+                       split_shift, (const unsigned long long*)nullptr, 0, w.keys[0], w.vals[0], dbits, n_tiles,
+                       w.hist[0]);
+  }
   int rc = launch_status("keys_hist_kernel");
   if (rc != EG_OK) return rc;
   int cur = 0;
@@ -629,9 +695,9 @@ static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_
     uint32_t* h_next = last ? nullptr : w.hist[(pass + 1) & 1];
     const int64_t len = (int64_t)n_tiles << dbits;
     const unsigned chunks = (unsigned)((len + kScanChunk - 1) / kScanChunk);
-    hipLaunchKernelGGL(scan_partials, dim3(chunks), dim3(kScanThreads), 0, st, h, len, n_tiles, dbits, w.partial,
-                       h_next, last ? (int64_t)0 : len);
-    hipLaunchKernelGGL(scan_apply, dim3(chunks), dim3(kScanThreads), 0, st, h, len, n_tiles, dbits, w.partial);
+    hipLaunchKernelGGL(scan_partials, dim3(chunks), dim3(kScanThreads), 0, st, h, len, w.partial, h_next,
+                       last ? (int64_t)0 : len);
+    hipLaunchKernelGGL(scan_apply, dim3(chunks), dim3(kScanThreads), 0, st, h, len, w.partial);
     hipLaunchKernelGGL(scatter_kernel, dim3(n_tiles), dim3(kTileThreads), 0, st, w.keys[cur], w.vals[cur],
                        w.keys[cur ^ 1], w.vals[cur ^ 1], n, pass * dbits, dbits, n_tiles, h, h_next,
                        (pass + 1) * dbits, dbits);
@@ -698,6 +764,23 @@ extern "C" {
 
 size_t eg_backward_workspace_size(int64_t n_slots) { return workspace_bytes(n_slots < 0 ? 0 : n_slots); }
 
+int eg_build_row_index(const int32_t* ids, int64_t n, int64_t* table, int64_t capacity, void* stream) {
+  EG_CHECK_ARG(n >= 0 && n < (1LL << 31), "n=%lld", (long long)n);
+  EG_CHECK_ARG(capacity >= 2 && capacity >= 2 * n && (capacity & (capacity - 1)) == 0 && capacity <= (1LL << 32),
+               "capacity=%lld must be a power of two >= 2*n", (long long)capacity);
+  EG_CHECK_ARG(table != nullptr && (n == 0 || ids != nullptr), "ids/table is NULL");
+  int bits = 0;
+  while ((1LL << bits) < capacity) ++bits;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t fill_blocks = (capacity + 255) / 256;
+  hipLaunchKernelGGL(index_fill_kernel, dim3((unsigned)(fill_blocks < 4096 ? fill_blocks : 4096)), dim3(256), 0, st,
+                     (unsigned long long*)table, capacity);
+  if (n > 0)
+    hipLaunchKernelGGL(index_build_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, ids, n,
+                       (unsigned long long*)table, bits);
+  return launch_status("row index kernels");
+}
+
 int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos, int32_t heads,
                     int32_t dim, const int32_t* ids, int64_t n_var, float* grad_out, void* workspace,
                     size_t workspace_bytes_, void* stream) {
@@ -709,7 +792,7 @@ int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   hipStream_t st = (hipStream_t)stream;
   const Workspace w = carve(workspace, n);
   int cur = 0;
-  rc = sort_slots(rows, n, ids, n_var, w, st, &cur);
+  rc = sort_slots(rows, n, ids, n_var, nullptr, 0, w, st, &cur);
   if (rc != EG_OK) return rc;
   SegArgs a;
   memset(&a, 0, sizeof(a));
@@ -738,6 +821,10 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   EG_CHECK_ARG(opt->lr >= 0.0 && opt->beta1 >= 0.0 && opt->beta1 < 1.0 && opt->beta2 >= 0.0 && opt->beta2 < 1.0 &&
                    opt->eps >= 0.0,
                "invalid Adam hyper-parameters");
+  if (state->index != nullptr)
+    EG_CHECK_ARG(state->index_capacity >= 2 * state->n && state->index_capacity >= 2 &&
+                     (state->index_capacity & (state->index_capacity - 1)) == 0 && state->index_capacity <= (1LL << 32),
+                 "index_capacity=%lld must be a power of two >= 2*n", (long long)state->index_capacity);
   SegArgs a;
   memset(&a, 0, sizeof(a));
   if (state->quant.payload != nullptr) {
@@ -758,7 +845,7 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   const Workspace w = carve(workspace, n);
   int cur = 0;
   if (n > 0) {
-    rc = sort_slots(rows, n, state->ids, state->n, w, st, &cur);
+    rc = sort_slots(rows, n, state->ids, state->n, state->index, state->index_capacity, w, st, &cur);
     if (rc != EG_OK) return rc;
   }
   a.skeys = w.keys[cur];

@@ -105,6 +105,13 @@ class DescentState:
         self.step_count = 0
         self.base = base
         self.quant = RowStore.empty(quant_fmt, ids.numel(), self.dim, dev) if quant_fmt else None
+        # open-addressing index of the ids for the backward's lookups (built once)
+        cap = 64
+        while cap < 2 * ids.numel():
+            cap *= 2
+        self.index = torch.empty(cap, dtype=torch.int64, device=dev)
+        _lib.call("eg_build_row_index", _lib.ptr(self.ids), ids.numel(), _lib.ptr(self.index), cap,
+                  _lib.stream_ptr(dev))
         # ||rows0||^2 of the start rows (engraft/descend_corpus.py:936), for the pull term
         self.rows0_sq = float(self.master.pow(2).sum().clamp_min(1e-12).item()) if ids.numel() else 0.0
 
@@ -137,6 +144,8 @@ class DescentState:
         s.stamp = _lib.ptr(self.stamp)
         if self.quant is not None:
             s.quant = self.quant.c_table()
+        s.index = _lib.ptr(self.index)
+        s.index_capacity = self.index.numel()
         return s
 
     def step(self, d_out: torch.Tensor, rows: torch.Tensor, *, lr: float, betas=(0.9, 0.999), eps: float = 1e-8,

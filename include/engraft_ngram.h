@@ -150,7 +150,15 @@ typedef struct eg_descent_state {
   int32_t* stamp;     /* [R] last dense step that hit the row (0 before the first) */
   eg_table quant;     /* requantised copy [R] written after the update (Q8_0 or MXFP8;
                          payload NULL: none) -- the rows a forward overlay reads */
+  const int64_t* index;   /* optional eg_build_row_index table of ids (NULL: the ids are
+                             searched directly) */
+  int64_t index_capacity;
 } eg_descent_state;
+
+/* Builds an open-addressing index of sorted unique ids for the backward's
+ * lookups: table int64 [capacity] (capacity a power of two >= 2*n), entries
+ * (row << 32 | position in ids), -1 when empty.  Built once per state. */
+int eg_build_row_index(const int32_t* ids, int64_t n, int64_t* table, int64_t capacity, void* stream);
 
 /* Workspace bytes eg_scatter_grad / eg_descent_step need for n_slots = n_pos*heads. */
 size_t eg_backward_workspace_size(int64_t n_slots);
