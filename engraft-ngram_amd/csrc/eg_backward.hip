@@ -192,6 +192,7 @@ __device__ inline uint32_t block_exclusive_scan(uint32_t t, uint32_t* wsum, uint
 }
 
 constexpr int kScanChunk = 4 * kScanThreads;  // entries per scan workgroup
+constexpr int kMaxChunksLds = 2048;            // scan chunks a scatter can count in LDS
 
 // Pass 1 of the exclusive scan: the total of every chunk; also clears the next
 // pass's histogram.
@@ -214,10 +215,13 @@ __global__ __launch_bounds__(kScanThreads) void scan_partials(const uint32_t* __
 // Pass 2: exclusive scan of every chunk, offset by the totals of the chunks
 // before it.
 __global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict__ a, int64_t len,
-                                                           const uint32_t* __restrict__ partial) {
+                                                           const uint32_t* __restrict__ partial,
+                                                           uint32_t* __restrict__ clear, int64_t clear_len) {
   __shared__ uint32_t wsum[kScanThreads / 64];
   __shared__ uint32_t wsum2[kScanThreads / 64];
   const int tid = threadIdx.x;
+  for (int64_t i = (int64_t)blockIdx.x * kScanThreads + tid; i < clear_len; i += (int64_t)gridDim.x * kScanThreads)
+    clear[i] = 0;
   uint32_t pre = 0;
   for (int g = tid; g < (int)blockIdx.x; g += kScanThreads) pre += partial[g];
   const int64_t i0 = (int64_t)blockIdx.x * kScanChunk + 4 * tid;
@@ -246,10 +250,11 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict_
 __global__ __launch_bounds__(kTileThreads) void scatter_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, int64_t n, int shift, int dbits, int n_tiles, const uint32_t* __restrict__ offs,
-    uint32_t* __restrict__ hist_next, int next_shift, int next_dbits) {
+    uint32_t* __restrict__ hist_next, uint32_t* __restrict__ partial_next, int next_shift, int next_dbits) {
   constexpr int kWaves = kTileThreads / 64;
   __shared__ uint32_t run[kMaxBuckets];
   __shared__ uint32_t wcnt[kWaves][kMaxBuckets];
+  __shared__ uint32_t chunk_cnt[kMaxChunksLds];  // the next scan's chunk totals, this tile's share
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n_buckets = 1 << dbits;
   for (int d = tid; d < n_buckets; d += kTileThreads) {
@@ -257,6 +262,10 @@ __global__ __launch_bounds__(kTileThreads) void scatter_kernel(
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) wcnt[w][d] = 0;
   }
+  __syncthreads();
+  const int64_t next_chunks =
+      partial_next ? (((int64_t)n_tiles << next_dbits) + kScanChunk - 1) / kScanChunk : 0;  // <= kMaxChunksLds
+  for (int c = tid; c < next_chunks; c += kTileThreads) chunk_cnt[c] = 0;
   __syncthreads();
   const uint32_t mask = (uint32_t)n_buckets - 1u;
   const uint32_t next_mask = (1u << next_dbits) - 1u;
@@ -284,8 +293,11 @@ __global__ __launch_bounds__(kTileThreads) void scatter_kernel(
       for (int w = 0; w < wave; ++w) pos += wcnt[w][d];
       keys_out[pos] = key;
       vals_out[pos] = val;
-      if (hist_next != nullptr)
-        atomicAdd(&hist_next[(int64_t)((key >> next_shift) & next_mask) * n_tiles + pos / kTile], 1u);
+      if (hist_next != nullptr) {
+        const int64_t hi = (int64_t)((key >> next_shift) & next_mask) * n_tiles + pos / kTile;
+        atomicAdd(&hist_next[hi], 1u);
+        if (partial_next != nullptr) atomicAdd(&chunk_cnt[hi / kScanChunk], 1u);
+      }
     }
     __syncthreads();
     for (int dd = tid; dd < n_buckets; dd += kTileThreads) {
@@ -299,6 +311,8 @@ __global__ __launch_bounds__(kTileThreads) void scatter_kernel(
     }
     __syncthreads();
   }
+  for (int c = tid; c < next_chunks; c += kTileThreads)
+    if (chunk_cnt[c] != 0) atomicAdd(&partial_next[c], chunk_cnt[c]);
 }
 
 // ---------------------------------------------------------------------------
@@ -634,7 +648,7 @@ struct Workspace {
   uint32_t* keys[2];
   uint32_t* vals[2];
   uint32_t* hist[2];
-  uint32_t* partial;  // per scan chunk
+  uint32_t* partial[2];  // per scan chunk, one buffer per pass parity
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -648,7 +662,7 @@ static size_t partial_bytes(int64_t n) {
 static size_t workspace_bytes(int64_t n) {
   const size_t kb = align256((size_t)n * 4);
   const size_t hb = align256((size_t)n_tiles_of(n) * kMaxBuckets * 4);
-  return 4 * kb + 2 * hb + partial_bytes(n);
+  return 4 * kb + 2 * hb + 2 * partial_bytes(n);
 }
 
 static Workspace carve(void* ws, int64_t n) {
@@ -662,7 +676,8 @@ static Workspace carve(void* ws, int64_t n) {
   w.vals[1] = (uint32_t*)(p + 3 * kb);
   w.hist[0] = (uint32_t*)(p + 4 * kb);
   w.hist[1] = (uint32_t*)(p + 4 * kb + hb);
-  w.partial = (uint32_t*)(p + 4 * kb + 2 * hb);
+  w.partial[0] = (uint32_t*)(p + 4 * kb + 2 * hb);
+  w.partial[1] = (uint32_t*)(p + 4 * kb + 2 * hb + partial_bytes(n));
   return w;
 }
 
@@ -695,11 +710,21 @@ static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_
     uint32_t* h_next = last ? nullptr : w.hist[(pass + 1) & 1];
     const int64_t len = (int64_t)n_tiles << dbits;
     const unsigned chunks = (unsigned)((len + kScanChunk - 1) / kScanChunk);
-    hipLaunchKernelGGL(scan_partials, dim3(chunks), dim3(kScanThreads), 0, st, h, len, w.partial, h_next,
-                       last ? (int64_t)0 : len);
-    hipLaunchKernelGGL(scan_apply, dim3(chunks), dim3(kScanThreads), 0, st, h, len, w.partial);
+    // Pass 0 sums its scan chunks here; a later pass's chunk totals are counted
+    // by the scatter before it when they fit its LDS (fused), else summed here.
+    // What the next scatter accumulates into is cleared before it runs.
+    const bool fused = chunks <= (unsigned)kMaxChunksLds;
+    uint32_t* part = w.partial[pass & 1];
+    uint32_t* part_next = (last || !fused) ? nullptr : w.partial[(pass + 1) & 1];
+    if (pass == 0 || !fused)
+      hipLaunchKernelGGL(scan_partials, dim3(chunks), dim3(kScanThreads), 0, st, h, len, part, h_next,
+                         last ? (int64_t)0 : len);
+    else if (!last)
+      hipLaunchKernelGGL(scan_partials, dim3(1), dim3(kScanThreads), 0, st, h, (int64_t)0, part_next, h_next, len);
+    hipLaunchKernelGGL(scan_apply, dim3(chunks), dim3(kScanThreads), 0, st, h, len, part, part_next,
+                       part_next ? (int64_t)chunks + 1 : (int64_t)0);
     hipLaunchKernelGGL(scatter_kernel, dim3(n_tiles), dim3(kTileThreads), 0, st, w.keys[cur], w.vals[cur],
-                       w.keys[cur ^ 1], w.vals[cur ^ 1], n, pass * dbits, dbits, n_tiles, h, h_next,
+                       w.keys[cur ^ 1], w.vals[cur ^ 1], n, pass * dbits, dbits, n_tiles, h, h_next, part_next,
                        (pass + 1) * dbits, dbits);
     rc = launch_status("radix sort pass");
     if (rc != EG_OK) return rc;
