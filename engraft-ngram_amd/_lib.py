@@ -102,6 +102,11 @@ SIGNATURES = {
     "eg_synth_table": (c_int32, [POINTER(EgTable), c_uint64, c_void_p, c_int64, c_int64, c_void_p]),
     "eg_backward_workspace_size": (ctypes.c_size_t, [c_int64]),
     "eg_build_row_index": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
+    "eg_lookup_rows": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
+    "eg_gather_slots": (c_int32, [POINTER(EgTable), c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_int64,
+                                  c_void_p, c_void_p]),
+    "eg_scatter_grad_slots": (c_int32, [c_void_p, c_int32, c_void_p, c_int64, c_int32, c_int32, c_int64, c_void_p,
+                                        c_void_p, ctypes.c_size_t, c_void_p]),
     "eg_scatter_grad": (c_int32, [c_void_p, c_int32, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64,
                                   c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     "eg_descent_step": (c_int32, [c_void_p, c_int32, c_void_p, c_int64, c_int32, POINTER(EgDescentState),

@@ -68,7 +68,9 @@ __global__ __launch_bounds__(256) void index_build_kernel(const int32_t* __restr
 // ---------------------------------------------------------------------------
 // Keys + first histogram
 // ---------------------------------------------------------------------------
-template <bool INDEX>
+// MODE 0: search the sorted ids; 1: probe the row index; 2: rows already hold
+// variable indices (< 0 or >= n_var: no variable).
+template <int MODE>
 __global__ __launch_bounds__(kTileThreads) void keys_hist_kernel(
     const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ ids, int64_t n_var, int split_shift,
     const unsigned long long* __restrict__ index, int index_bits, uint32_t* __restrict__ keys,
@@ -76,7 +78,7 @@ __global__ __launch_bounds__(kTileThreads) void keys_hist_kernel(
   __shared__ int32_t spl[kSplitMax];
   __shared__ uint32_t h[kMaxBuckets];
   const int tid = threadIdx.x;
-  const int ns = INDEX ? 0 : (int)((n_var + (1LL << split_shift) - 1) >> split_shift);
+  const int ns = MODE == 0 ? (int)((n_var + (1LL << split_shift) - 1) >> split_shift) : 0;
   for (int i = tid; i < ns; i += kTileThreads) spl[i] = ids[(int64_t)i << split_shift];
   for (int i = tid; i < kMaxBuckets; i += kTileThreads) h[i] = 0;
   __syncthreads();
@@ -92,7 +94,11 @@ __global__ __launch_bounds__(kTileThreads) void keys_hist_kernel(
     row[r] = ok[r] ? rows[idx] : 0;
   }
   uint32_t key[kTileIPT];
-  if constexpr (INDEX) {
+  if constexpr (MODE == 2) {
+#pragma unroll
+    for (int r = 0; r < kTileIPT; ++r)
+      key[r] = (row[r] >= 0 && (int64_t)row[r] < n_var) ? (uint32_t)row[r] : (uint32_t)n_var;
+  } else if constexpr (MODE == 1) {
     // probe the row index; the items' probes advance in lockstep
     const uint64_t imask = (1ull << index_bits) - 1ull;
     uint64_t hslot[kTileIPT];
@@ -683,7 +689,7 @@ static Workspace carve(void* ws, int64_t n) {
 
 // keys + stable radix sort; *sorted = index (0/1) of the sorted buffers.
 static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_t n_var, const int64_t* index,
-                      int64_t index_capacity, const Workspace& w, hipStream_t st, int* sorted) {
+                      int64_t index_capacity, bool direct, const Workspace& w, hipStream_t st, int* sorted) {
   int bits = 0;
   while (bits < 32 && ((uint64_t)n_var >> bits) != 0) ++bits;  // keys lie in [0, n_var]
   const int passes = bits == 0 ? 0 : (bits + kMaxDigitBits - 1) / kMaxDigitBits;
@@ -691,13 +697,16 @@ static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_
   int split_shift = 0;
   while (((n_var + (1LL << split_shift) - 1) >> split_shift) > kSplitMax) ++split_shift;
   const int n_tiles = (int)n_tiles_of(n);
-  if (index != nullptr) {
+  if (direct) {
+    hipLaunchKernelGGL(keys_hist_kernel<2>, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
+                       (const unsigned long long*)nullptr, 0, w.keys[0], w.vals[0], dbits, n_tiles, w.hist[0]);
+  } else if (index != nullptr) {
     int ib = 0;
     while ((1LL << ib) < index_capacity) ++ib;
-    hipLaunchKernelGGL(keys_hist_kernel<true>, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
+    hipLaunchKernelGGL(keys_hist_kernel<1>, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
                        (const unsigned long long*)index, ib, w.keys[0], w.vals[0], dbits, n_tiles, w.hist[0]);
   } else {
-    hipLaunchKernelGGL(keys_hist_kernel<false>, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var,
+    hipLaunchKernelGGL(keys_hist_kernel<0>, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var,
                        split_shift, (const unsigned long long*)nullptr, 0, w.keys[0], w.vals[0], dbits, n_tiles,
                        w.hist[0]);
   }
@@ -806,10 +815,11 @@ int eg_build_row_index(const int32_t* ids, int64_t n, int64_t* table, int64_t ca
   return launch_status("row index kernels");
 }
 
-int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos, int32_t heads,
-                    int32_t dim, const int32_t* ids, int64_t n_var, float* grad_out, void* workspace,
-                    size_t workspace_bytes_, void* stream) {
-  int rc = check_common(d_out, rows, n_pos, heads, dim, ids, n_var, workspace, workspace_bytes_);
+static int scatter_grad_impl(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos,
+                             int32_t heads, int32_t dim, const int32_t* ids, int64_t n_var, bool direct,
+                             float* grad_out, void* workspace, size_t workspace_bytes_, void* stream) {
+  int rc = check_common(d_out, rows, n_pos, heads, dim, direct ? (const int32_t*)rows : ids, n_var, workspace,
+                        workspace_bytes_);
   if (rc != EG_OK) return rc;
   EG_CHECK_ARG(n_var == 0 || grad_out != nullptr, "grad_out is NULL");
   const int64_t n = n_pos * heads;
@@ -817,7 +827,7 @@ int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   hipStream_t st = (hipStream_t)stream;
   const Workspace w = carve(workspace, n);
   int cur = 0;
-  rc = sort_slots(rows, n, ids, n_var, nullptr, 0, w, st, &cur);
+  rc = sort_slots(rows, n, ids, n_var, nullptr, 0, direct, w, st, &cur);
   if (rc != EG_OK) return rc;
   SegArgs a;
   memset(&a, 0, sizeof(a));
@@ -832,6 +842,20 @@ int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   a.width = (int64_t)heads * dim;
   a.grad_out = grad_out;
   return launch_reduce<false>(a, st);
+}
+
+int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos, int32_t heads,
+                    int32_t dim, const int32_t* ids, int64_t n_var, float* grad_out, void* workspace,
+                    size_t workspace_bytes_, void* stream) {
+  return scatter_grad_impl(d_out, d_out_f32, rows, n_pos, heads, dim, ids, n_var, false, grad_out, workspace,
+                           workspace_bytes_, stream);
+}
+
+int eg_scatter_grad_slots(const void* d_out, int32_t d_out_f32, const int32_t* slot_var, int64_t n_pos,
+                          int32_t heads, int32_t dim, int64_t n_var, float* grad_out, void* workspace,
+                          size_t workspace_bytes_, void* stream) {
+  return scatter_grad_impl(d_out, d_out_f32, slot_var, n_pos, heads, dim, nullptr, n_var, true, grad_out, workspace,
+                           workspace_bytes_, stream);
 }
 
 int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos, int32_t heads,
@@ -870,7 +894,7 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   const Workspace w = carve(workspace, n);
   int cur = 0;
   if (n > 0) {
-    rc = sort_slots(rows, n, state->ids, state->n, state->index, state->index_capacity, w, st, &cur);
+    rc = sort_slots(rows, n, state->ids, state->n, state->index, state->index_capacity, false, w, st, &cur);
     if (rc != EG_OK) return rc;
   }
   a.skeys = w.keys[cur];

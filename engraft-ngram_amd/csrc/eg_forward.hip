@@ -101,6 +101,7 @@ struct FwdArgs {
   OverlayDev ov[EG_MAX_LAYERS];
   const int64_t* tokens;    // hash mode
   const int32_t* rows_in;   // gather mode: [n_pos, heads] global ids
+  const int32_t* slot_var;  // gather mode: [n_pos, heads] overlay row per slot (-1: table)
   const int32_t* seg_start;
   const uint16_t* residual; // bf16 [n_pos, W] or nullptr
   void* out;
@@ -185,9 +186,13 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
     int32_t ovk = -1;
     const OverlayDev& ov = a.ov[l];
     if constexpr (OVL) {
-      if (ov.n > 0 && lane < H) {
-        const int64_t k = sorted_find(ov.ids, ov.n, rid[l]);
-        if (k >= 0) ovk = ov.index ? ov.index[k] : (int32_t)k;
+      if (lane < H) {
+        if (a.slot_var != nullptr) {
+          ovk = a.slot_var[p * H + lane];
+        } else if (ov.n > 0) {
+          const int64_t k = sorted_find(ov.ids, ov.n, rid[l]);
+          if (k >= 0) ovk = ov.index ? ov.index[k] : (int32_t)k;
+        }
       }
     }
 #pragma unroll
@@ -305,7 +310,7 @@ template <bool F32OUT>
 static int launch_forward(const FwdArgs& a, hipStream_t st) {
   if (a.n_pos == 0) return EG_OK;
   const dim3 grid((unsigned)((a.n_pos + kWavesPerBlock - 1) / kWavesPerBlock));
-  bool ovl = false;
+  bool ovl = a.slot_var != nullptr;
   for (int l = 0; l < a.n_layers; ++l) ovl = ovl || a.ov[l].n > 0;
   const int fmt = a.table[0].fmt;
   if (!F32OUT) {
@@ -327,6 +332,19 @@ static int launch_forward(const FwdArgs& a, hipStream_t st) {
 }
 
 #undef EG_LAUNCH
+
+// Variable index of each row id (-1 if absent) + per-id read counts.
+__global__ __launch_bounds__(256) void lookup_kernel(const int32_t* __restrict__ rows, int64_t n,
+                                                     const int32_t* __restrict__ ids,
+                                                     const int32_t* __restrict__ index, int64_t n_ids,
+                                                     int32_t* __restrict__ out,
+                                                     unsigned long long* __restrict__ counts) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t k = n_ids > 0 ? sorted_find(ids, n_ids, rows[i]) : -1;
+  if (out != nullptr) out[i] = k < 0 ? -1 : (index ? index[k] : (int32_t)k);
+  if (counts != nullptr && k >= 0) atomicAdd(&counts[k], 1ull);
+}
 
 static int fill_overlay(const eg_overlay* o, const TableDev& base, OverlayDev* out) {
   memset(out, 0, sizeof(*out));
@@ -406,6 +424,45 @@ int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tabl
   EG_CHECK_ARG(W <= 512 * kMaxChunks, "row width %d > %d", W, 512 * kMaxChunks);
   a.nch = (W + 511) / 512;
   return residual ? launch_forward<false>(a, (hipStream_t)stream) : launch_forward<true>(a, (hipStream_t)stream);
+}
+
+int eg_lookup_rows(const int32_t* rows, int64_t n, const int32_t* ids, const int32_t* index, int64_t n_ids,
+                   int32_t* out, int64_t* counts, void* stream) {
+  EG_CHECK_ARG(n >= 0 && n_ids >= 0, "n=%lld n_ids=%lld", (long long)n, (long long)n_ids);
+  EG_CHECK_ARG(n == 0 || rows != nullptr, "rows is NULL");
+  EG_CHECK_ARG(n_ids == 0 || ids != nullptr, "ids is NULL");
+  if (n == 0) return EG_OK;
+  hipLaunchKernelGGL(lookup_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, rows, n,
+                     ids, index, n_ids, out, (unsigned long long*)counts);
+  return launch_status("lookup_kernel");
+}
+
+int eg_gather_slots(const eg_table* table, const int32_t* rows, const int32_t* slot_var, int64_t n_pos,
+                    int32_t heads, const float* vars, int64_t n_vars, float* out, void* stream) {
+  EG_CHECK_ARG(heads >= 1 && heads <= EG_MAX_HEADS, "heads=%d outside [1, %d]", heads, EG_MAX_HEADS);
+  EG_CHECK_ARG(n_pos >= 0 && n_vars >= 0, "n_pos=%lld n_vars=%lld", (long long)n_pos, (long long)n_vars);
+  EG_CHECK_ARG(n_pos == 0 || (rows != nullptr && slot_var != nullptr && out != nullptr),
+               "rows/slot_var/out is NULL");
+  EG_CHECK_ARG(n_vars == 0 || vars != nullptr, "vars is NULL");
+  FwdArgs a;
+  memset(&a, 0, sizeof(a));
+  int rc = make_table(table, &a.table[0], "table");
+  if (rc != EG_OK) return rc;
+  a.ov[0].rows.payload = (const uint8_t*)vars;
+  a.ov[0].rows.n_rows = n_vars;
+  a.ov[0].rows.fmt = EG_FMT_F32;
+  a.ov[0].rows.dim = table->dim;
+  a.rows_in = rows;
+  a.slot_var = slot_var;
+  a.out = out;
+  a.n_pos = n_pos;
+  a.n_layers = 1;
+  a.heads = heads;
+  a.dim = table->dim;
+  const int W = heads * a.dim;
+  EG_CHECK_ARG(W <= 512 * kMaxChunks, "row width %d > %d", W, 512 * kMaxChunks);
+  a.nch = (W + 511) / 512;
+  return launch_forward<true>(a, (hipStream_t)stream);
 }
 
 int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* rows, int64_t n_pos, int32_t heads,

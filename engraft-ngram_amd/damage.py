@@ -1,0 +1,126 @@
+"""The damage plan's table half on the device: the drop-in for
+``ngram_rows`` / ``iter_blocks`` / ``scan_hits`` / ``compute_rows_delta``
+(``engraft/damage.py:68-224``).
+
+``scan_hits`` hashes a corpus block (``eg_hash_rows``, the whole block as one
+sequence, so every position sees its real predecessors), resolves each of the
+``n_heads`` rows of every position against the sorted overlay ids with
+``eg_lookup_rows`` (which also counts the reads of every overlay row), and
+reduces per position the number of overlay rows read and the max / sum of
+their ``dnorm``.  Blocks overlap by ``ngram_size - 1`` tokens, whose positions
+are dropped, so the result equals a scan of the whole corpus as one sequence.
+"""
+from __future__ import annotations
+
+import time
+from typing import Iterator
+
+import numpy as np
+import torch
+
+from . import _lib
+from .descent import _read_true_rows
+
+BLOCK_TOKENS = 8_000_000  # engraft/damage.py:60
+
+
+def ngram_rows(tokens: np.ndarray, table) -> tuple[np.ndarray, ...]:
+    """Global rows of every position of ``tokens``, one int64 ``[n,
+    heads_per_ngram]`` array per n-gram order (bigram, trigram, ...;
+    ``engraft/damage.py:68-104`` returns the bigram and trigram arrays of an
+    ``ngram_size = 3`` table)."""
+    tok = np.asarray(tokens).reshape(-1)
+    if tok.size == 0:
+        return tuple(np.zeros((0, table.heads_per_ngram), dtype=np.int64) for _ in range(table.ngram_size - 1))
+    rows = table.rows(torch.as_tensor(tok.astype(np.int64))).cpu().numpy().astype(np.int64)
+    k = table.heads_per_ngram
+    return tuple(rows[:, o * k:(o + 1) * k] for o in range(table.ngram_size - 1))
+
+
+def iter_blocks(tokens: np.ndarray, block: int = BLOCK_TOKENS, overlap: int = 2) -> Iterator[tuple[int, np.ndarray]]:
+    """``(offset, tokens[offset-overlap : offset+block])`` -- ``overlap``
+    tokens of history (none on the first block; ``engraft/damage.py:107-118``
+    uses 2, the context of a trigram table)."""
+    n = len(tokens)
+    offset = 0
+    first = True
+    while offset < n:
+        this_block = min(block, n - offset)
+        start = offset if first else offset - overlap
+        yield offset, tokens[start:offset + this_block]
+        offset += this_block
+        first = False
+
+
+def compute_rows_delta(table, rows_global: np.ndarray, data: np.ndarray) -> dict:
+    """``(dnorm, ratio, cos)`` of every overlay row against its true row
+    (``engraft/damage.py:126-151``); the true rows come from the device
+    gather."""
+    true = _read_true_rows(table, np.asarray(rows_global).tolist())
+    data = np.asarray(data, dtype=np.float32)
+    diff = data.astype(np.float64) - true.astype(np.float64)
+    dnorm = np.linalg.norm(diff, axis=1).astype(np.float32)
+    norm_true = np.linalg.norm(true, axis=1).astype(np.float64)
+    norm_ov = np.linalg.norm(data, axis=1).astype(np.float64)
+    ratio = np.where(norm_true > 0, norm_ov / np.maximum(norm_true, 1e-30), np.nan).astype(np.float32)
+    denom = norm_ov * norm_true
+    dot = np.sum(data.astype(np.float64) * true.astype(np.float64), axis=1)
+    cos = np.where(denom > 0, dot / np.maximum(denom, 1e-30), np.nan).astype(np.float32)
+    return {"rows_global": np.asarray(rows_global, dtype=np.int32), "dnorm": dnorm, "ratio": ratio, "cos": cos,
+            "true": true}
+
+
+def scan_hits(tokens: np.ndarray, table, overlay_sorted: np.ndarray, dnorm_sorted: np.ndarray,
+              block: int = BLOCK_TOKENS) -> dict:
+    """Positions of ``tokens`` that read at least one row of the sorted overlay
+    ids (``engraft/damage.py:159-224``): ``pos`` / ``n_hit_rows`` /
+    ``dnorm_max`` / ``dnorm_sum`` per hit position (the corpus's last
+    position excluded), and ``read_count`` per overlay row."""
+    tokens = np.asarray(tokens).reshape(-1)
+    n = int(tokens.shape[0])
+    dev = table.device
+    ov = np.asarray(overlay_sorted, dtype=np.int64).reshape(-1)
+    n_ov = int(ov.shape[0])
+    if n_ov > 1 and np.any(ov[1:] <= ov[:-1]):
+        raise ValueError("scan_hits: overlay_sorted must be strictly ascending")
+    if n_ov and (ov[0] < 0 or ov[-1] > np.iinfo(np.int32).max):
+        raise ValueError("scan_hits: overlay ids must be global rows in [0, 2^31)")
+    ids = torch.as_tensor(ov.astype(np.int32), device=dev)
+    dn = torch.as_tensor(np.asarray(dnorm_sorted, dtype=np.float32).reshape(-1), device=dev)
+    if dn.numel() != n_ov:
+        raise ValueError("scan_hits: dnorm_sorted must match overlay_sorted")
+    counts = torch.zeros(max(n_ov, 1), dtype=torch.int64, device=dev)
+    hist = table.ngram_size - 1
+    pos_parts, nh_parts, dmax_parts, dsum_parts = [], [], [], []
+    t0 = time.time()
+    for offset, blk in iter_blocks(tokens, block=block, overlap=hist):
+        start_local = 0 if offset == 0 else hist
+        rows = table.rows(torch.as_tensor(np.asarray(blk, dtype=np.int64)))[start_local:].contiguous()
+        m = rows.shape[0]
+        if m == 0 or n_ov == 0:
+            continue
+        k = torch.empty_like(rows)
+        _lib.call("eg_lookup_rows", _lib.ptr(rows), rows.numel(), _lib.ptr(ids), None, n_ov, _lib.ptr(k),
+                  _lib.ptr(counts), _lib.stream_ptr(dev))
+        matched = k >= 0
+        n_hit = matched.sum(dim=1)
+        hit_local = torch.nonzero(n_hit > 0).reshape(-1)
+        pos_here = hit_local + offset
+        keep = pos_here < (n - 1)
+        hit_local = hit_local[keep]
+        if hit_local.numel() == 0:
+            continue
+        md = torch.where(matched[hit_local], dn[k[hit_local].clamp_min(0).long()], torch.zeros((), device=dev))
+        pos_parts.append(pos_here[keep].cpu().numpy().astype(np.int64))
+        nh_parts.append(n_hit[hit_local].cpu().numpy().astype(np.int32))
+        dmax_parts.append(md.max(dim=1).values.cpu().numpy().astype(np.float32))
+        dsum_parts.append(md.sum(dim=1).cpu().numpy().astype(np.float32))
+    read_count = counts[:n_ov].cpu().numpy().astype(np.int64)
+    dt = time.time() - t0
+
+    def _cat(parts, dtype):
+        return np.concatenate(parts) if parts else np.zeros(0, dtype=dtype)
+
+    return {"pos": _cat(pos_parts, np.int64), "n_hit_rows": _cat(nh_parts, np.int32),
+            "dnorm_max": _cat(dmax_parts, np.float32), "dnorm_sum": _cat(dsum_parts, np.float32),
+            "read_count": read_count, "scan_time_s": dt, "n_tokens": n}

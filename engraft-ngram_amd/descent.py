@@ -194,11 +194,10 @@ def _read_true_rows(table: DeviceTable, rows_global) -> np.ndarray:
     g = np.asarray(list(rows_global), dtype=np.int64).reshape(-1)
     offsets = np.asarray(table.head_offsets, dtype=np.int64)
     ends = offsets + np.asarray(table.head_vocab_sizes, dtype=np.int64)
-    for x in g.tolist():
-        h = int(np.searchsorted(offsets, x, side="right") - 1)
-        h = max(0, min(h, len(offsets) - 1))
-        if not (offsets[h] <= x < ends[h]):
-            raise ValueError(f"_read_true_rows: global row {x} outside all heads")
+    h = np.clip(np.searchsorted(offsets, g, side="right") - 1, 0, len(offsets) - 1)
+    bad = ~((offsets[h] <= g) & (g < ends[h]))
+    if bad.any():
+        raise ValueError(f"_read_true_rows: global row {int(g[bad][0])} outside all heads")
     if g.size == 0:
         return np.zeros((0, table.row_len), dtype=np.float32)
     ids = torch.as_tensor(g.astype(np.int32), device=table.device).reshape(-1, 1)

@@ -1,0 +1,287 @@
+"""The differentiable sequence overlay and the per-position true embedding, on
+the device: the drop-ins for ``OverlayEmb`` / ``overlay_key_len``
+(``engraft/replica/seq.py:222-444``) and ``Replica.ple_true_emb``
+(``engraft/replica/model.py:473-495``).
+
+``OverlayEmb.build`` does in a few launches what the reference does with a
+per-position Python loop:
+
+1. hash every position (``eg_hash_rows``; with ``segment_ids`` each position
+   looks back only to its segment's first token, which is what hashing the
+   isolated ``tokens[s(t):]`` gives);
+2. resolve every slot's variable (``eg_lookup_rows`` over the sorted int keys
+   of ``row_map``), then overwrite the slots of the long ``(window, head)``
+   keys, which win over the global row -- host dict lookups, one per
+   position, only when ``row_map`` has tuple keys;
+3. gather: every slot reads ``rows_var[slot_var]`` or, without a variable, its
+   dequantised table row (``eg_gather_slots``).
+
+The slot plan (rows + slot variables, the part that does not depend on
+``rows_var``) is cached per ``(tokens, start, n_positions, segment starts)``
+on the instance, and per fragment in the caller's ``overlay_cache`` (FIFO,
+4096 entries), like the reference's base cache.  The backward of the gather
+is ``eg_scatter_grad_slots``: every variable's slot gradients summed in
+ascending slot order, deterministically (the same association as the descent
+step's scatter).
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+
+import numpy as np
+import torch
+
+from . import _lib
+from .descent import _WS, _dout_args
+from .overlay import DeviceOverlay
+from .pack import seg_starts_from_segment_ids
+
+OVERLAY_CACHE_MAX_ENTRIES = 4096  # engraft/replica/seq.py:182
+
+
+def overlay_key_len(row_map: dict) -> int | None:
+    """Length ``K`` of the long-key windows of ``row_map`` (``None`` without
+    tuple keys); all windows must share one length
+    (``engraft/replica/seq.py:222-234``, same ``AssertionError``)."""
+    lengths = {len(key[0]) for key in row_map if isinstance(key, tuple)}
+    if not lengths:
+        return None
+    assert len(lengths) == 1, f"overlay_key_len: long keys of different lengths in row_map: {lengths}"
+    return next(iter(lengths))
+
+
+class _GatherSlots(torch.autograd.Function):
+    """out f32 ``[n, H*D]`` = per slot ``vars[slot_var]`` or the table row;
+    backward: ``eg_scatter_grad_slots``."""
+
+    @staticmethod
+    def forward(ctx, rows_var, table, rows, slot_var):
+        n, heads = rows.shape
+        dim = table.row_len
+        dev = table.device
+        vars32 = rows_var.detach().to(device=dev, dtype=torch.float32).contiguous()
+        out = torch.empty((n, heads * dim), dtype=torch.float32, device=dev)
+        _lib.call("eg_gather_slots", ctypes.byref(table.c_table), _lib.ptr(rows), _lib.ptr(slot_var), n, heads,
+                  _lib.ptr(vars32), vars32.shape[0], _lib.ptr(out), _lib.stream_ptr(dev))
+        ctx.save_for_backward(slot_var)
+        ctx.meta = (heads, dim, vars32.shape[0], rows_var.dtype, rows_var.device)
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        (slot_var,) = ctx.saved_tensors
+        heads, dim, n_var, dtype, device = ctx.meta
+        dev = slot_var.device
+        d = d_out.to(device=dev)
+        if d.dtype not in (torch.float32, torch.bfloat16):
+            d = d.float()
+        d = d.contiguous()
+        n = slot_var.shape[0]
+        grad = torch.zeros((n_var, dim), dtype=torch.float32, device=dev)
+        if n > 0 and n_var > 0:
+            ws = _WS.get(n * heads, dev)
+            _lib.call("eg_scatter_grad_slots", _lib.ptr(d), _dout_args(d), _lib.ptr(slot_var), n, heads, dim,
+                      n_var, _lib.ptr(grad), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
+        return grad.to(device=device, dtype=dtype), None, None, None
+
+
+@dataclasses.dataclass
+class OverlayEmb:
+    """For positions ``start..n_positions-1`` of ``tokens``, the PLE embedding
+    ``[n_positions-start, n_heads*row_len]`` with ``row_map``'s rows replaced
+    by ``rows_var`` -- differentiable in ``rows_var``, the plain gather
+    everywhere else (``engraft/replica/seq.py:237-444``).
+
+    ``row_map`` keys: ``int`` = global row, or ``((K tokens), head)`` = a long
+    key that wins over the global row at a position whose last ``K`` tokens
+    (all inside its segment) are the window.  Values: rows of ``rows_var``.
+    ``n_key_hits`` / ``n_id_hits`` count the slots each kind replaced in the
+    last ``build``."""
+
+    table: object
+    tokens: list[int]
+    rows_var: torch.Tensor
+    row_map: dict
+    segment_ids: torch.Tensor | None = None
+    overlay_cache: dict | None = None
+
+    def __post_init__(self) -> None:
+        if isinstance(self.tokens, torch.Tensor):
+            self._tok = [int(x) for x in self.tokens.reshape(-1).tolist()]
+        else:
+            self._tok = [int(x) for x in self.tokens]
+        self._plans: dict[tuple, dict] = {}
+        self._seg_starts: np.ndarray | None = None
+        self._seg_ranges: list[tuple[int, int]] | None = None
+        if self.segment_ids is not None:
+            starts = seg_starts_from_segment_ids(self.segment_ids)
+            self._seg_starts = starts
+            bounds = np.flatnonzero(np.diff(starts) != 0) + 1
+            edges = [0] + bounds.tolist() + [len(starts)]
+            self._seg_ranges = [(edges[i], edges[i + 1]) for i in range(len(edges) - 1) if edges[i + 1] > edges[i]]
+        dev = self.table.device
+        int_keys = [k for k in self.row_map if not isinstance(k, tuple)]
+        ids = np.array(int_keys, dtype=np.int64)
+        var = np.array([self.row_map[k] for k in int_keys], dtype=np.int64)
+        order = np.argsort(ids, kind="stable")
+        ids, var = ids[order], var[order]
+        if ids.size and (ids[0] < 0 or ids[-1] > np.iinfo(np.int32).max):
+            raise ValueError("row_map int keys must be global rows in [0, 2^31)")
+        self._ids = torch.from_numpy(ids.astype(np.int32)).to(dev)
+        self._ids_var = torch.from_numpy(var.astype(np.int32)).to(dev)
+        self._key_len = overlay_key_len(self.row_map)
+        self._windows: dict[tuple, list[tuple[int, int]]] = {}
+        for k, r in self.row_map.items():
+            if isinstance(k, tuple):
+                self._windows.setdefault(tuple(int(x) for x in k[0]), []).append((int(k[1]), int(r)))
+        vals = [int(r) for r in self.row_map.values()]
+        self._max_var = max(vals) if vals else -1
+        if vals and min(vals) < 0:
+            raise IndexError("row_map values must be rows of rows_var (>= 0)")
+        self.n_key_hits = 0
+        self.n_id_hits = 0
+
+    # ---- the slot plan -----------------------------------------------------------------------
+    def _plan_tokens(self, tokens: list[int], seg_start: np.ndarray | None, start: int, end: int) -> dict:
+        """Rows and slot variables of positions ``start..end-1`` of ``tokens``
+        (``seg_start``: per-position segment start, or ``None`` = one sequence)."""
+        table = self.table
+        dev = table.device
+        heads = table.n_heads
+        n = end - start
+        if n <= 0:
+            z = torch.zeros((0, heads), dtype=torch.int32, device=dev)
+            return {"rows": z, "slot_var": z.clone(), "n_key_hits": 0, "n_id_hits": 0}
+        rows = table.rows(tokens[:end], seg_start=None if seg_start is None else seg_start[:end])[start:].contiguous()
+        slot_var = torch.empty_like(rows)
+        _lib.call("eg_lookup_rows", _lib.ptr(rows), rows.numel(), _lib.ptr(self._ids), _lib.ptr(self._ids_var),
+                  self._ids.numel(), _lib.ptr(slot_var), None, _lib.stream_ptr(dev))
+        n_key = 0
+        n_overridden_id = 0
+        if self._key_len is not None:
+            K = self._key_len
+            kt: list[int] = []
+            kh: list[int] = []
+            kr: list[int] = []
+            for t in range(max(start, K - 1), end):
+                t_local = t - (int(seg_start[t]) if seg_start is not None else 0)
+                if t_local < K - 1:
+                    continue
+                hits = self._windows.get(tuple(tokens[t - K + 1:t + 1]))
+                if hits is None:
+                    continue
+                for h, r in hits:
+                    if 0 <= h < heads:
+                        kt.append(t - start)
+                        kh.append(h)
+                        kr.append(r)
+            if kt:
+                ti = torch.tensor(kt, dtype=torch.int64, device=dev)
+                hi = torch.tensor(kh, dtype=torch.int64, device=dev)
+                n_overridden_id = int((slot_var[ti, hi] >= 0).sum().item())
+                slot_var.index_put_((ti, hi), torch.tensor(kr, dtype=torch.int32, device=dev))
+                n_key = len(kt)
+        n_id_total = int((slot_var >= 0).sum().item()) if self._ids.numel() or n_key else 0
+        return {"rows": rows, "slot_var": slot_var, "n_key_hits": n_key, "n_id_hits": n_id_total - n_key}
+
+    def _plan_fragments(self, n_positions: int) -> dict:
+        """The plan assembled fragment by fragment through ``overlay_cache``
+        (``engraft/replica/seq.py:324-370``): a fragment's plan depends only on
+        its own tokens (its hash never looks before its first token)."""
+        rows_parts: list[torch.Tensor] = []
+        slot_parts: list[torch.Tensor] = []
+        n_key = n_id = 0
+        for s_i, e_i in self._seg_ranges or []:
+            if s_i >= n_positions:
+                break
+            frag = tuple(self._tok[s_i:e_i])
+            entry = self.overlay_cache.get(frag)
+            if entry is None:
+                entry = self._plan_tokens(list(frag), None, 0, len(frag))
+                sv = entry["slot_var"]
+                entry["key_per_pos"] = None
+                entry["id_per_pos"] = (sv >= 0).sum(dim=1).cpu().numpy()
+                if self._key_len is not None:
+                    entry["key_per_pos"] = self._key_hits_per_pos(list(frag))
+                if len(self.overlay_cache) >= OVERLAY_CACHE_MAX_ENTRIES:
+                    self.overlay_cache.pop(next(iter(self.overlay_cache)))  # FIFO: oldest first
+                self.overlay_cache[frag] = entry
+            m = min(e_i, n_positions) - s_i
+            rows_parts.append(entry["rows"][:m])
+            slot_parts.append(entry["slot_var"][:m])
+            kpp = entry["key_per_pos"]
+            k = int(kpp[:m].sum()) if kpp is not None else 0
+            n_key += k
+            n_id += int(entry["id_per_pos"][:m].sum()) - k
+        heads = self.table.n_heads
+        dev = self.table.device
+        if rows_parts:
+            rows = torch.cat(rows_parts).contiguous()
+            slot_var = torch.cat(slot_parts).contiguous()
+        else:
+            rows = torch.zeros((0, heads), dtype=torch.int32, device=dev)
+            slot_var = rows.clone()
+        return {"rows": rows, "slot_var": slot_var, "n_key_hits": n_key, "n_id_hits": n_id}
+
+    def _key_hits_per_pos(self, frag: list[int]) -> np.ndarray:
+        K = self._key_len
+        out = np.zeros(len(frag), dtype=np.int64)
+        for t in range(K - 1, len(frag)):
+            hits = self._windows.get(tuple(frag[t - K + 1:t + 1]))
+            if hits:
+                out[t] = sum(1 for h, _ in hits if 0 <= h < self.table.n_heads)
+        return out
+
+    # ---- the reference's method ----------------------------------------------------------------
+    def build(self, n_positions: int, start: int = 0) -> torch.Tensor:
+        if not 0 <= start <= n_positions <= len(self._tok):
+            raise IndexError(f"positions [{start}, {n_positions}) outside the {len(self._tok)} tokens")
+        if self.rows_var.dim() != 2 or self.rows_var.shape[1] != self.table.row_len:
+            raise ValueError(f"rows_var must be [R, {self.table.row_len}], got {tuple(self.rows_var.shape)}")
+        if self._max_var >= self.rows_var.shape[0]:
+            raise IndexError(f"row_map names row {self._max_var} of a {self.rows_var.shape[0]}-row rows_var")
+        if self.overlay_cache is not None and self._seg_ranges is not None and start == 0:
+            plan = self._plan_fragments(n_positions)
+        else:
+            seg_key = None if self._seg_starts is None else self._seg_starts[:n_positions].tobytes()
+            key = (tuple(self._tok[:n_positions]), start, n_positions, seg_key)
+            plan = self._plans.get(key)
+            if plan is None:
+                plan = self._plan_tokens(self._tok, self._seg_starts, start, n_positions)
+                self._plans[key] = plan
+        self.n_key_hits = plan["n_key_hits"]
+        self.n_id_hits = plan["n_id_hits"]
+        out = _GatherSlots.apply(self.rows_var, self.table, plan["rows"], plan["slot_var"])
+        out = out.to(device=self.rows_var.device, dtype=self.rows_var.dtype)
+        return out.reshape(n_positions - start, self.table.n_heads * self.table.row_len)
+
+
+def _as_overlay(table, overlay) -> DeviceOverlay | None:
+    if overlay is None:
+        return None
+    if isinstance(overlay, DeviceOverlay):
+        return overlay
+    if not overlay:
+        return None
+    return DeviceOverlay.from_dict(overlay, table.row_len, device=table.device)
+
+
+def ple_true_emb(table, tokens: list[int], t: int, overlay=None) -> torch.Tensor:
+    """``emb [1, n_heads*row_len]`` f32 of position ``t`` of ``tokens``, the
+    rows whose global id is in ``overlay`` (``{global_row: vector}`` or a
+    ``DeviceOverlay``) replaced (``engraft/replica/model.py:473-495``).  On
+    the table's device."""
+    if not 0 <= t < len(tokens):
+        raise IndexError(f"position {t} outside [0, {len(tokens)})")
+    lo = max(0, t - table.ngram_size + 1)
+    return ple_true_emb_range(table, list(tokens[lo:t + 1]), t - lo, t - lo + 1, overlay)
+
+
+def ple_true_emb_range(table, tokens, start: int, end: int, overlay=None, seg_start=None) -> torch.Tensor:
+    """``ple_true_emb`` of positions ``start..end-1`` in one launch: the
+    ``torch.cat`` of the per-position loop at ``engraft/replica/model.py:
+    845-853``; f32 ``[end-start, n_heads*row_len]``."""
+    tok = tokens if isinstance(tokens, torch.Tensor) else torch.as_tensor(np.asarray(tokens, dtype=np.int64))
+    rows = table.rows(tok[:end], seg_start=None if seg_start is None else np.asarray(seg_start)[:end])
+    return table.gather(rows[start:end].contiguous(), overlay=_as_overlay(table, overlay))

@@ -19,7 +19,12 @@
  *                                                    engraft/replica/model.py:473-495,845-853,
  *                                                    engraft/replica/seq.py:372-444
  *   eg_scatter_grad  autograd of rows_var[idx_r] + index_put (accumulate)
- *                                                    engraft/replica/seq.py:433-441
+ *   (+ _slots)                                       engraft/replica/seq.py:433-441
+ *   eg_lookup_rows   row_map / sorted-overlay membership + read counts
+ *                                                    engraft/replica/seq.py:412-417,
+ *                                                    engraft/damage.py:192-197
+ *   eg_gather_slots  OverlayEmb.build's base gather + index_put
+ *                                                    engraft/replica/seq.py:372-444
  *   eg_descent_step  scatter + torch.optim.Adam step on the overlay rows
  *                                                    engraft/descend_corpus.py:785-790,921-947
  */
@@ -176,6 +181,27 @@ int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
 int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos,
                     int32_t heads, const eg_descent_state* state, const eg_adam* opt,
                     const eg_table* base, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- per-slot variables (OverlayEmb) ---------------------------------------
+ * Variable index of each row id: out[i] = index[k] (k when index is NULL) for
+ * rows[i] == ids[k], else -1; counts (optional, int64 [n_ids], accumulated)
+ * += the number of reads of each id (engraft/damage.py:192-197 read_count). */
+int eg_lookup_rows(const int32_t* rows, int64_t n, const int32_t* ids, const int32_t* index,
+                   int64_t n_ids, int32_t* out, int64_t* counts, void* stream);
+
+/* Gather with per-slot replacement rows (engraft/replica/seq.py:433-441):
+ * out f32 [n_pos, heads*dim]; slot (p, h) reads vars[slot_var[p, h]] (f32
+ * [n_vars, dim]) when slot_var[p, h] >= 0, else the table row rows[p, h]. */
+int eg_gather_slots(const eg_table* table, const int32_t* rows, const int32_t* slot_var,
+                    int64_t n_pos, int32_t heads, const float* vars, int64_t n_vars, float* out,
+                    void* stream);
+
+/* eg_scatter_grad keyed by per-slot variables: grad_out f32 [n_var, dim] +=
+ * the d_out slices of the slots with slot_var == k (slot_var < 0: none),
+ * merged deterministically as in eg_scatter_grad. */
+int eg_scatter_grad_slots(const void* d_out, int32_t d_out_f32, const int32_t* slot_var,
+                          int64_t n_pos, int32_t heads, int32_t dim, int64_t n_var,
+                          float* grad_out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Seeded synthetic table rows [row0, row0+n_rows) (benchmark/test inputs):
  * value j of row r = qtable[mix64(seed*0xD1B54A32D192ED03 + r*dim + j) >> 50]

@@ -79,22 +79,30 @@ def scatter_grad(d_emb, rows, ids_sorted) -> tuple[np.ndarray, np.ndarray]:
     """``(grad f32 [R, D], hits int64 [R])``: each variable's slots in ascending
     slot order, summed with ``segment_sum``'s association (sequential for the
     segments of at most 32 slots, which ``np.add.at`` does in index order)."""
-    d_emb = np.asarray(d_emb, dtype=np.float32)
     rows = np.asarray(rows, dtype=np.int64)
-    p, hh = rows.shape
-    d = d_emb.shape[1] // hh
-    keys = slot_keys(rows, ids_sorted)
-    r = int(np.asarray(ids_sorted).size)
-    grad = np.zeros((r, d), dtype=np.float32)
-    hits = np.zeros(r, dtype=np.int64)
-    sel = np.flatnonzero(keys >= 0)
+    return scatter_grad_keys(d_emb, slot_keys(rows, ids_sorted), rows.shape[1],
+                             int(np.asarray(ids_sorted).size))
+
+
+def scatter_grad_keys(d_emb, keys, heads: int, n_var: int) -> tuple[np.ndarray, np.ndarray]:
+    """``scatter_grad`` with the variable of every slot given directly
+    (``keys [P*heads]``, ``-1`` or ``>= n_var`` = no variable): the gradient of
+    ``rows_var`` through ``base.index_put((idx_t, idx_h), rows_var[idx_r])``
+    (``engraft/replica/seq.py:433-441``) with ``keys[t*heads + h] = idx_r``."""
+    d_emb = np.asarray(d_emb, dtype=np.float32)
+    keys = np.asarray(keys, dtype=np.int64).reshape(-1)
+    p = keys.size // heads
+    d = d_emb.shape[1] // heads if d_emb.size else 0
+    grad = np.zeros((n_var, d), dtype=np.float32)
+    hits = np.zeros(n_var, dtype=np.int64)
+    sel = np.flatnonzero((keys >= 0) & (keys < n_var))
     if sel.size == 0:
         return grad, hits
     order = np.argsort(keys[sel], kind="stable")
     slots = sel[order]
     ks = keys[slots]
     np.add.at(hits, ks, 1)
-    flat = d_emb.reshape(p * hh, d)
+    flat = d_emb.reshape(p * heads, d)
     short = hits[ks] <= PIECE
     np.add.at(grad, ks[short], flat[slots[short]])  # sequential in index (= slot) order
     for k in np.unique(ks[~short]):

@@ -67,3 +67,10 @@ def assert_out_matches(out_bits: np.ndarray, exp_bits: np.ndarray) -> None:
 
 __all__ = ["device_table", "table_from_arrays", "synth_fetch", "bf16_bits", "residual", "assert_out_matches",
            "FW", "F", "synth"]
+
+
+def f32_table(spec: HashSpec, dim: int, seed: int, device="cuda:0"):
+    """A small F32 device table of normal rows (x0.05) and its oracle fetch."""
+    n = int(sum(spec.head_vocab_sizes))
+    data = (np.random.default_rng(seed).standard_normal((n, dim)) * 0.05).astype(np.float32)
+    return table_from_arrays(spec, "f32", dim, data, device=device), (lambda ids: data[np.asarray(ids, np.int64)])

@@ -1,0 +1,110 @@
+"""Host-side logic of the drop-in (no GPU): packing, ``.pleo`` IO,
+``build_overlay``, ``overlay_key_len``, block iteration -- against the
+reference's own tests and fixtures."""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import hash as H
+
+GOLDEN = Path(__file__).parent / "golden"
+
+
+def _pkg():
+    from engraft_ngram_amd import damage, lens, pack, seq  # noqa: F401
+    return lens, pack, seq, damage
+
+
+def test_pack_segment_ids_reference_case():
+    """tests/test_seq.py:54-57: frags [3,5,7,2], [9,4,6] -> one bin, segment
+    ids [0,0,0,0,0,1,1,1]."""
+    _, pack, _, _ = _pkg()
+    p = pack.pack_fragments([[3, 5, 7, 2], [9, 4, 6]], 99, max_len=64)
+    assert len(p) == 1
+    p = p[0]
+    assert p.tokens == [99, 3, 5, 7, 2, 99, 9, 4, 6]
+    assert p.segment_ids.tolist() == [0, 0, 0, 0, 0, 1, 1, 1]
+    assert p.positions.tolist() == [0, 1, 2, 3, 4, 0, 1, 2]
+    assert p.frag_slices == [(0, 4), (5, 8)]
+    assert p.seg_start().tolist() == [0, 0, 0, 0, 0, 5, 5, 5]
+    assert p.seg_start().tolist() == H.seg_starts_from_segment_ids(p.segment_ids.numpy()).tolist()
+
+
+def test_pack_greedy_bins_and_oversize():
+    _, pack, _, _ = _pkg()
+    frags = [[1] * 5, [2] * 5, [3] * 3, [4] * 9]
+    bins = pack.pack_fragments(frags, 0, max_len=10)
+    # canonical lengths 6, 6, 4, 10 -> [6], [6, 4], [10]
+    assert [len(b.tokens) for b in bins] == [6, 10, 10]
+    assert bins[1].segment_ids.tolist() == [0] * 6 + [1] * 3
+    with pytest.raises(ValueError):
+        pack.pack_fragments([[1] * 10], 0, max_len=10)
+    assert pack.pack_fragments([], 0, max_len=10) == []
+
+
+def test_pleo_roundtrip_and_bad_magic(tmp_path):
+    """tests/test_lens.py:57-72."""
+    lens, _, _, _ = _pkg()
+    rows = np.array([5, 100000, 3, 999999999], dtype=np.int32)
+    data = np.random.default_rng(0).standard_normal((4, 160)).astype(np.float32)
+    path = tmp_path / "x.pleo"
+    lens.write_pleo(path, rows, data)
+    r, d = lens.read_pleo(path)
+    np.testing.assert_array_equal(r, rows)
+    np.testing.assert_array_equal(d, data)
+    bad = tmp_path / "bad.pleo"
+    bad.write_bytes(b"NOPE" + b"\x00" * 20)
+    with pytest.raises(ValueError):
+        lens.read_pleo(bad)
+    with pytest.raises(ValueError):
+        lens.write_pleo(path, rows, data[:3])
+
+
+@pytest.mark.parametrize("name,n_rows", [("real_en_dog.pleo", 16), ("real_it_gatto.pleo", 48)])
+def test_pleo_real_fixtures_byte_exact(tmp_path, name, n_rows):
+    """Real overlays written by the reference (results/2026-09-05/facts/*):
+    read, then written back byte for byte."""
+    lens, _, _, _ = _pkg()
+    src = GOLDEN / name
+    rows, data = lens.read_pleo(src)
+    assert rows.shape == (n_rows,) and data.shape == (n_rows, 160)
+    assert np.all(np.isfinite(data))
+    assert 0 < float(np.abs(data).max()) < 1.0
+    out = tmp_path / name
+    lens.write_pleo(out, rows, data)
+    assert out.read_bytes() == src.read_bytes()
+
+
+def test_build_overlay_dedup_and_conflict():
+    """tests/test_lens.py:184-208."""
+    lens, _, _, _ = _pkg()
+    rows1 = np.array([5, 10], dtype=np.int32)
+    data1 = np.ones((2, 160), dtype=np.float32)
+    rows2 = np.array([10, 20], dtype=np.int32)
+    data2 = np.stack([np.ones(160, np.float32), np.full(160, 2.0, np.float32)])
+    rows, data = lens.RowSet.build_overlay([(rows1, data1), (rows2, data2)])
+    assert rows.tolist() == [5, 10, 20]
+    np.testing.assert_array_equal(data[2], np.full(160, 2.0))
+    with pytest.raises(ValueError):
+        lens.RowSet.build_overlay([(np.array([5]), np.ones((1, 160), np.float32)),
+                                   (np.array([5]), np.full((1, 160), 2.0, np.float32))])
+
+
+def test_overlay_key_len():
+    _, _, seq, _ = _pkg()
+    assert seq.overlay_key_len({1: 0, 7: 1}) is None
+    assert seq.overlay_key_len({1: 0, ((3, 4, 5), 2): 1}) == 3
+    with pytest.raises(AssertionError):
+        seq.overlay_key_len({((3, 4), 2): 0, ((3, 4, 5), 2): 1})
+
+
+def test_iter_blocks_overlap():
+    """engraft/damage.py:107-118: 2 tokens of history except on the first block."""
+    _, _, _, damage = _pkg()
+    toks = np.arange(10)
+    blocks = list(damage.iter_blocks(toks, block=4))
+    assert [o for o, _ in blocks] == [0, 4, 8]
+    assert [b.tolist() for _, b in blocks] == [[0, 1, 2, 3], [2, 3, 4, 5, 6, 7], [6, 7, 8, 9]]
