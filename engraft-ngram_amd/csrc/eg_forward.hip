@@ -6,6 +6,8 @@
 // the Infinity Cache keep the Zipf-hot table rows.
 #include <string.h>
 
+#include <hip/hip_ext.h>
+
 #include "eg_common.h"
 
 namespace eg {
@@ -272,7 +274,19 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   }
 }
 
-#define EG_LAUNCH(...) hipLaunchKernelGGL((forward_kernel<__VA_ARGS__>), grid, dim3(256), 0, st, a)
+// Events of eg_forward_timed: when set, the forward kernel is launched with
+// hipExtLaunchKernelGGL so the events carry the dispatch's own start and end.
+static thread_local hipEvent_t g_ev_start = nullptr;
+static thread_local hipEvent_t g_ev_stop = nullptr;
+
+#define EG_LAUNCH(...)                                                                                  \
+  do {                                                                                                  \
+    if (g_ev_start != nullptr)                                                                          \
+      hipExtLaunchKernelGGL((forward_kernel<__VA_ARGS__>), grid, dim3(256), 0, st, g_ev_start, g_ev_stop, \
+                            0u, a);                                                                     \
+    else                                                                                                \
+      hipLaunchKernelGGL((forward_kernel<__VA_ARGS__>), grid, dim3(256), 0, st, a);                     \
+  } while (0)
 
 // Specialised residual-add shapes: dim 128 with 16 (W = 2048) or 24 (W = 3072)
 // heads, one or two layers; everything else goes through the generic kernel.
@@ -424,6 +438,20 @@ int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tabl
   EG_CHECK_ARG(W <= 512 * kMaxChunks, "row width %d > %d", W, 512 * kMaxChunks);
   a.nch = (W + 511) / 512;
   return residual ? launch_forward<false>(a, (hipStream_t)stream) : launch_forward<true>(a, (hipStream_t)stream);
+}
+
+int eg_forward_timed(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,
+                     const eg_overlay* overlays, const int64_t* tokens, int64_t n_pos, int64_t seq_len,
+                     const int32_t* seg_start, const uint16_t* residual, void* out, int32_t* rows_out,
+                     void* start_event, void* stop_event, void* stream) {
+  EG_CHECK_ARG(start_event != nullptr && stop_event != nullptr, "start_event/stop_event is NULL");
+  g_ev_start = (hipEvent_t)start_event;
+  g_ev_stop = (hipEvent_t)stop_event;
+  const int rc = eg_forward(n_layers, specs, tables, overlays, tokens, n_pos, seq_len, seg_start, residual, out,
+                            rows_out, stream);
+  g_ev_start = nullptr;
+  g_ev_stop = nullptr;
+  return rc;
 }
 
 int eg_lookup_rows(const int32_t* rows, int64_t n, const int32_t* ids, const int32_t* index, int64_t n_ids,

@@ -391,6 +391,14 @@ class PreparedForward:
         if rc != _lib.EG_OK:
             _lib.check(rc)
 
+    def timed(self, start_event: int, stop_event: int, stream: int | None = None) -> None:
+        """The same launch through ``eg_forward_timed``: the two hipEvent_t
+        handles receive the kernel dispatch's own start / end timestamps."""
+        st = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
+        rc = _lib.load().eg_forward_timed(*self._args, start_event, stop_event, st)
+        if rc != _lib.EG_OK:
+            _lib.check(rc)
+
 
 def forward(tables: list[DeviceTable], tokens, residual: torch.Tensor | None = None, *,
             out: torch.Tensor | None = None, overlays=None, seq_len: int | None = None, seg_start=None,

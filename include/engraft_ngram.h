@@ -119,6 +119,17 @@ int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tabl
                int64_t seq_len, const int32_t* seg_start, const uint16_t* residual,
                void* out, int32_t* rows_out, void* stream);
 
+/* eg_forward with the kernel launched through hipExtLaunchKernelGGL, so that
+ * start_event / stop_event (hipEvent_t, created by the caller) hold the
+ * dispatch's own start and end timestamps.  No counterpart in the reference:
+ * a measurement hook for benchmarks (kernel time without the gaps of event
+ * packets around the launch). */
+int eg_forward_timed(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,
+                     const eg_overlay* overlays, const int64_t* tokens, int64_t n_pos,
+                     int64_t seq_len, const int32_t* seg_start, const uint16_t* residual,
+                     void* out, int32_t* rows_out, void* start_event, void* stop_event,
+                     void* stream);
+
 /* Gather by explicit global row ids: rows int32 [n_pos, heads] ->
  * out f32 [n_pos, heads*dim] (dequantised, overlay resolved; NULL overlay = base). */
 int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* rows,
