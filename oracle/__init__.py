@@ -22,6 +22,13 @@ Modules (each function cites the reference ``file:line`` it restates):
 * ``oracle.backward`` -- the sparse gradient scatter and the optimizer step
   (``engraft/replica/seq.py:433-441`` autograd, ``engraft/descend_corpus.py:
   785-790, 921-947``).
+* ``oracle.overlay_emb`` -- ``OverlayEmb.build`` / ``ple_true_emb`` per
+  position (``engraft/replica/seq.py:185-234, 372-444``,
+  ``engraft/replica/model.py:473-495``).
+* ``oracle.damage``   -- the damage plan's corpus scan (``engraft/damage.py:
+  107-224``).
+* ``oracle.cpu_baseline`` -- the vectorized CPU forward timed beside the GPU
+  by ``bench.py`` (numpy hash, torch gather / dequant / add).
 
 Pinning status of every function is listed in the header of its module.
 """

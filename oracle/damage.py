@@ -6,7 +6,7 @@ blocks with 2 tokens of history (``iter_blocks``, ``:107-118``), with the
 vectorized hash of ``oracle.hash.ngram_rows_np`` in place of
 ``ngram_rows`` (``:68-104``).
 
-Pinning (tests/test_oracle_damage.py): the reference's own known-answer test
+Pinning (tests/test_oracle_overlay_emb.py): the reference's own known-answer test
 ``tests/test_damage.py:38-61`` (seed-7 FakeTable parameters, 20,000 tokens
 with an EOS every 200, block 4,000: the hit positions equal those of the
 scalar ``ngram_addresses`` loop, the last position never a hit), block-size

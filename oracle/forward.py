@@ -12,7 +12,7 @@
 * ``residual_add``  -- BASELINE's consumer: ``bf16_rne(f32(residual) + emb_0
   [+ emb_1 ...])``, the layers added in order, fp32 accumulate.
 
-Pinning (tests/test_oracle_forward.py): the substitution invariants of
+Pinning (tests/test_oracle_forward_backward.py): the substitution invariants of
 ``tests/test_replica_graft.py:43-70`` (present rows replaced, absent rows
 bit-identical, empty overlay == plain gather), the fp32-add-then-RNE rule
 against torch's ``.to(torch.bfloat16)`` (library routine), and the gather
