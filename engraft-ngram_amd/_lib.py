@@ -103,7 +103,7 @@ SIGNATURES = {
     "eg_gather": (c_int32, [POINTER(EgTable), POINTER(EgOverlay), c_void_p, c_int64, c_int32, c_void_p,
                             c_void_p]),
     "eg_synth_table": (c_int32, [POINTER(EgTable), c_uint64, c_void_p, c_int64, c_int64, c_void_p]),
-    "eg_backward_workspace_size": (ctypes.c_size_t, [c_int64]),
+    "eg_backward_workspace_size": (ctypes.c_size_t, [c_int64, c_int64]),
     "eg_build_row_index": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "eg_lookup_rows": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
     "eg_gather_slots": (c_int32, [POINTER(EgTable), c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_int64,

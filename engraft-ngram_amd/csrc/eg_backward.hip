@@ -1,24 +1,27 @@
 // Backward half of the n-gram table path on gfx950: the deterministic sparse
 // gradient scatter and the optimizer step on the touched overlay rows.
 //
-//   keys     slot s = p*heads + h -> (variable index of rows[s], s); the
-//            variable is found through an LDS splitter table of the sorted
-//            ids; the first digit's per-tile histogram is built on the way
-//   sort     stable LSD radix sort of the pairs by variable index, digits of
-//            up to 9 bits: one scan and one ballot-ranked stable scatter per
-//            pass (the scatter also counts the next pass's digits), so equal
-//            variables keep ascending slot order
-//   segment  one 32-lane group per segment of at most 32 slots sums the
-//            slots' d_out slices in slot order (fp32) and runs Adam +
-//            requantisation on the variable; a longer segment is reduced by
-//            a whole workgroup of the same launch: pieces of 32 slots summed
-//            in order, piece sums accumulated per group (pieces j = g mod 8),
-//            the eight group sums added in group order
+//   keys     slot s = p*heads + h -> variable index k of rows[s] (an LDS
+//            splitter search of the sorted ids, a probe of the row index, or
+//            given directly); every variable's slot count is accumulated
+//   offsets  exclusive scan of the counts; variables hit by more than 32
+//            slots are listed
+//   fill     every slot id is placed in its variable's range (CSR); the order
+//            inside a range is whatever the atomics gave
+//   order    each range is put in ascending slot order inside the reduction:
+//            ranges of at most 32 slots by a 32-lane bitonic network on
+//            registers, longer ones by their workgroup (LDS bitonic network,
+//            or the same network on global memory beyond the LDS capacity)
+//   segment  one 32-lane group per variable hit by at most 32 slots sums the
+//            slots' d_out slices in ascending slot order (fp32) and runs
+//            Adam + requantisation; a longer range is reduced by a whole
+//            workgroup: pieces of 32 slots summed in order, piece j added to
+//            group j mod 8's sum, the eight group sums added in group order
 //   dense    variables no slot hit take their zero-gradient step (dense mode)
 //
 // No floating-point atomics: the association of every sum is fixed by the
-// sorted order alone, so results are bitwise repeatable, and the CPU oracle
-// reproduces them exactly.
+// ascending slot order alone, so results are bitwise repeatable, and the CPU
+// oracle reproduces them exactly.
 #include <string.h>
 
 #include "eg_common.h"
@@ -26,10 +29,8 @@
 namespace eg {
 
 constexpr int kTileThreads = 256;
-constexpr int kTileIPT = 4;
-constexpr int kTile = kTileThreads * kTileIPT;  // 1024 keys per tile
-constexpr int kMaxDigitBits = 9;
-constexpr int kMaxBuckets = 1 << kMaxDigitBits;
+constexpr int kTileIPT = 2;                       // lockstep lookups per thread in the keys kernel
+constexpr int kTile = kTileThreads * kTileIPT;    // slots per keys workgroup
 constexpr int kScanThreads = 1024;
 constexpr int kSplitMax = 2048;  // splitters staged in LDS (8 KB)
 constexpr int kPiece = 32;       // slots per piece of a long segment
@@ -66,23 +67,22 @@ __global__ __launch_bounds__(256) void index_build_kernel(const int32_t* __restr
 }
 
 // ---------------------------------------------------------------------------
-// Keys + first histogram
+// Keys + per-variable counts
 // ---------------------------------------------------------------------------
 // MODE 0: search the sorted ids; 1: probe the row index; 2: rows already hold
-// variable indices (< 0 or >= n_var: no variable).
+// variable indices (< 0 or >= n_var: no variable).  cnt[k] += the slots of k.
 template <int MODE>
-__global__ __launch_bounds__(kTileThreads) void keys_hist_kernel(
+__global__ __launch_bounds__(kTileThreads) void keys_count_kernel(
     const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ ids, int64_t n_var, int split_shift,
     const unsigned long long* __restrict__ index, int index_bits, uint32_t* __restrict__ keys,
-    uint32_t* __restrict__ vals, int dbits, int n_tiles, uint32_t* __restrict__ hist) {
+    uint32_t* __restrict__ cnt) {
   __shared__ int32_t spl[kSplitMax];
-  __shared__ uint32_t h[kMaxBuckets];
   const int tid = threadIdx.x;
   const int ns = MODE == 0 ? (int)((n_var + (1LL << split_shift) - 1) >> split_shift) : 0;
-  for (int i = tid; i < ns; i += kTileThreads) spl[i] = ids[(int64_t)i << split_shift];
-  for (int i = tid; i < kMaxBuckets; i += kTileThreads) h[i] = 0;
-  __syncthreads();
-  const uint32_t mask = (1u << dbits) - 1u;
+  if constexpr (MODE == 0) {
+    for (int i = tid; i < ns; i += kTileThreads) spl[i] = ids[(int64_t)i << split_shift];
+    __syncthreads();
+  }
   // The kTileIPT lookups of a thread run in lockstep (fixed-length branchless
   // searches), so their memory latencies overlap.
   int32_t row[kTileIPT];
@@ -160,16 +160,16 @@ __global__ __launch_bounds__(kTileThreads) void keys_hist_kernel(
     if (!ok[r]) continue;
     const int64_t idx = (int64_t)blockIdx.x * kTile + r * kTileThreads + tid;
     keys[idx] = key[r];
-    vals[idx] = (uint32_t)idx;
-    atomicAdd(&h[key[r] & mask], 1u);
+    if ((int64_t)key[r] < n_var) atomicAdd(&cnt[key[r]], 1u);
   }
-  __syncthreads();
-  for (int d = tid; d < (1 << dbits); d += kTileThreads) hist[(int64_t)d * n_tiles + blockIdx.x] = h[d];
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(uint32_t* __restrict__ a, int64_t len) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < len; i += (int64_t)gridDim.x * 256) a[i] = 0;
 }
 
 // ---------------------------------------------------------------------------
-// Exclusive scan (one workgroup, coalesced strips) + clearing of the next
-// pass's histogram
+// Exclusive scan (two kernels over 4096-entry chunks), in place
 // ---------------------------------------------------------------------------
 __device__ inline uint32_t wave_inclusive_scan(uint32_t x, int lane) {
 #pragma unroll
@@ -198,17 +198,12 @@ __device__ inline uint32_t block_exclusive_scan(uint32_t t, uint32_t* wsum, uint
 }
 
 constexpr int kScanChunk = 4 * kScanThreads;  // entries per scan workgroup
-constexpr int kMaxChunksLds = 2048;            // scan chunks a scatter can count in LDS
 
-// Pass 1 of the exclusive scan: the total of every chunk; also clears the next
-// pass's histogram.
+// Pass 1: the total of every chunk.
 __global__ __launch_bounds__(kScanThreads) void scan_partials(const uint32_t* __restrict__ a, int64_t len,
-                                                              uint32_t* __restrict__ partial,
-                                                              uint32_t* __restrict__ clear, int64_t clear_len) {
+                                                              uint32_t* __restrict__ partial) {
   __shared__ uint32_t wsum[kScanThreads / 64];
   const int tid = threadIdx.x;
-  for (int64_t i = (int64_t)blockIdx.x * kScanThreads + tid; i < clear_len; i += (int64_t)gridDim.x * kScanThreads)
-    clear[i] = 0;
   const int64_t i0 = (int64_t)blockIdx.x * kScanChunk + 4 * tid;
   uint32_t t = 0;
 #pragma unroll
@@ -219,15 +214,14 @@ __global__ __launch_bounds__(kScanThreads) void scan_partials(const uint32_t* __
 }
 
 // Pass 2: exclusive scan of every chunk, offset by the totals of the chunks
-// before it.
+// before it.  Entries whose count exceeds kPiece are appended to long_list.
 __global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict__ a, int64_t len,
                                                            const uint32_t* __restrict__ partial,
-                                                           uint32_t* __restrict__ clear, int64_t clear_len) {
+                                                           uint32_t* __restrict__ long_list,
+                                                           uint32_t* __restrict__ n_long) {
   __shared__ uint32_t wsum[kScanThreads / 64];
   __shared__ uint32_t wsum2[kScanThreads / 64];
   const int tid = threadIdx.x;
-  for (int64_t i = (int64_t)blockIdx.x * kScanThreads + tid; i < clear_len; i += (int64_t)gridDim.x * kScanThreads)
-    clear[i] = 0;
   uint32_t pre = 0;
   for (int g = tid; g < (int)blockIdx.x; g += kScanThreads) pre += partial[g];
   const int64_t i0 = (int64_t)blockIdx.x * kScanChunk + 4 * tid;
@@ -241,92 +235,60 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict_
   uint32_t run = base + block_exclusive_scan(v[0] + v[1] + v[2] + v[3], wsum, &total);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    if (i0 + u < len) a[i0 + u] = run;
+    if (i0 + u < len) {
+      a[i0 + u] = run;
+      if (v[u] > (uint32_t)kPiece) long_list[atomicAdd(n_long, 1u)] = (uint32_t)(i0 + u);
+    }
     run += v[u];
   }
 }
 
 // ---------------------------------------------------------------------------
-// Stable scatter of one digit pass.  Items are taken in index order (round,
-// then wave, then lane); lanes holding the same digit are found with one
-// ballot per digit bit, their rank is the popcount of the lower lanes, and
-// per-digit LDS counters carry the running offset across waves and rounds.
-// The next pass's per-tile histogram is counted at the destination.
+// CSR fill and the ordering of long ranges
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kTileThreads) void scatter_kernel(
-    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint32_t* __restrict__ keys_out,
-    uint32_t* __restrict__ vals_out, int64_t n, int shift, int dbits, int n_tiles, const uint32_t* __restrict__ offs,
-    uint32_t* __restrict__ hist_next, uint32_t* __restrict__ partial_next, int next_shift, int next_dbits) {
-  constexpr int kWaves = kTileThreads / 64;
-  __shared__ uint32_t run[kMaxBuckets];
-  __shared__ uint32_t wcnt[kWaves][kMaxBuckets];
-  __shared__ uint32_t chunk_cnt[kMaxChunksLds];  // the next scan's chunk totals, this tile's share
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n_buckets = 1 << dbits;
-  for (int d = tid; d < n_buckets; d += kTileThreads) {
-    run[d] = offs[(int64_t)d * n_tiles + blockIdx.x];
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) wcnt[w][d] = 0;
-  }
-  __syncthreads();
-  const int64_t next_chunks =
-      partial_next ? (((int64_t)n_tiles << next_dbits) + kScanChunk - 1) / kScanChunk : 0;  // <= kMaxChunksLds
-  for (int c = tid; c < next_chunks; c += kTileThreads) chunk_cnt[c] = 0;
-  __syncthreads();
-  const uint32_t mask = (uint32_t)n_buckets - 1u;
-  const uint32_t next_mask = (1u << next_dbits) - 1u;
-  const uint64_t lt = (1ull << lane) - 1ull;
-  for (int r = 0; r < kTileIPT; ++r) {
-    const int64_t idx = (int64_t)blockIdx.x * kTile + r * kTileThreads + tid;
-    const bool valid = idx < n;
-    uint32_t key = 0, val = 0, d = 0;
-    if (valid) {
-      key = keys_in[idx];
-      val = vals_in[idx];
-      d = (key >> shift) & mask;
-    }
-    uint64_t peers = __ballot(valid);
-    for (int b = 0; b < dbits; ++b) {
-      const bool bit = (d >> b) & 1u;
-      const uint64_t bal = __ballot(bit);
-      peers &= bit ? bal : ~bal;
-    }
-    const uint32_t rank = (uint32_t)__popcll(peers & lt);
-    if (valid && rank == 0) wcnt[wave][d] = (uint32_t)__popcll(peers);
-    __syncthreads();
-    if (valid) {
-      uint32_t pos = run[d] + rank;
-      for (int w = 0; w < wave; ++w) pos += wcnt[w][d];
-      keys_out[pos] = key;
-      vals_out[pos] = val;
-      if (hist_next != nullptr) {
-        const int64_t hi = (int64_t)((key >> next_shift) & next_mask) * n_tiles + pos / kTile;
-        atomicAdd(&hist_next[hi], 1u);
-        if (partial_next != nullptr) atomicAdd(&chunk_cnt[hi / kScanChunk], 1u);
+// off[k] enters as variable k's first position and leaves as its end.
+__global__ __launch_bounds__(256) void fill_kernel(const uint32_t* __restrict__ keys, int64_t n, int64_t n_var,
+                                                   uint32_t* __restrict__ off, uint32_t* __restrict__ slots) {
+  const int64_t s = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (s >= n) return;
+  const uint32_t k = keys[s];
+  if ((int64_t)k < n_var) slots[atomicAdd(&off[k], 1u)] = (uint32_t)s;
+}
+
+// Ascending order of x[0, len) with the bitonic network in its one-direction
+// form: for each block size k, compare i with i ^ (k-1), then i with i ^ j for
+// j = k/4 .. 1, the smaller value to the lower index.  Entries at len and
+// beyond count as +infinity, so comparisons that reach them are skipped.
+template <typename Ptr>
+__device__ void bitonic_sort(Ptr x, int64_t len) {
+  int64_t P = 1;
+  while (P < len) P <<= 1;
+  for (int64_t k = 2; k <= P; k <<= 1) {
+    for (int64_t j = k >> 1; j > 0; j >>= 1) {
+      for (int64_t i = threadIdx.x; i < (P >> 1); i += blockDim.x) {
+        const int64_t lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));  // i with a zero bit inserted at j
+        const int64_t hi = (j == (k >> 1)) ? (lo ^ (k - 1)) : (lo + j);
+        if (hi < len) {
+          const uint32_t u = x[lo], w = x[hi];
+          if (w < u) {
+            x[lo] = w;
+            x[hi] = u;
+          }
+        }
       }
+      __syncthreads();
     }
-    __syncthreads();
-    for (int dd = tid; dd < n_buckets; dd += kTileThreads) {
-      uint32_t t = 0;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        t += wcnt[w][dd];
-        wcnt[w][dd] = 0;
-      }
-      run[dd] += t;
-    }
-    __syncthreads();
   }
-  for (int c = tid; c < next_chunks; c += kTileThreads)
-    if (chunk_cnt[c] != 0) atomicAdd(&partial_next[c], chunk_cnt[c]);
 }
 
 // ---------------------------------------------------------------------------
 // Segmented reduction + optimizer
 // ---------------------------------------------------------------------------
 struct SegArgs {
-  const uint32_t* skeys;  // sorted variable index per slot (n_var = frozen)
-  const uint32_t* svals;  // slot ids in the same order
+  const uint32_t* ends;       // [n_var] end of each variable's range in slots
+  const uint32_t* slots;      // slot ids grouped by variable (CSR)
+  const uint32_t* long_list;  // variables with more than kPiece slots
+  const uint32_t* n_long;     // their number
   int64_t n;
   int64_t n_var;
   const void* d_out;
@@ -535,35 +497,46 @@ __device__ inline void finish(const SegArgs& a, int64_t k, int sub, const float 
   }
 }
 
-// One launch for every segment.  A segment longer than kPiece slots is taken
-// by one of the first n_long_blocks workgroups: block b owns the sorted
-// positions [(kPiece+1) b, (kPiece+1)(b+1)), which hold at most one long
-// segment's first slot (two such firsts are more than kPiece apart).  It sums
-// pieces of kPiece slots in order, adds piece j to group j mod kLongGroups and
-// the group sums in group order.  These blocks are dispatched first, so their
-// longer chains overlap the rest.
-// Every other workgroup holds eight 32-lane groups, one per sorted position:
-// the group at the first slot of a segment of at most kPiece slots reduces it.
+// 32-lane ascending sort of one value per lane (bitonic, one-direction form).
+__device__ inline uint32_t sort32(uint32_t v, int sub) {
+#pragma unroll
+  for (int k = 2; k <= 32; k <<= 1) {
+    {
+      const uint32_t o = (uint32_t)__shfl_xor((int)v, k - 1, 32);
+      v = (sub < (sub ^ (k - 1))) ? min(v, o) : max(v, o);
+    }
+#pragma unroll
+    for (int j = k >> 2; j > 0; j >>= 1) {
+      const uint32_t o = (uint32_t)__shfl_xor((int)v, j, 32);
+      v = ((sub & j) == 0) ? min(v, o) : max(v, o);
+    }
+  }
+  return v;
+}
+
+// One launch for every variable hit.  The first n_long_blocks workgroups take
+// the listed variables of more than kPiece slots: the workgroup puts the
+// variable's slot ids in ascending order (in LDS up to kLongLds ids, else in
+// place on global memory), sums pieces of kPiece slots in order, adds piece j
+// to group j mod kLongGroups and the group sums in group order.  They are
+// dispatched first, so their longer chains overlap the rest.  Every other
+// workgroup holds eight 32-lane groups, one per variable: a variable of
+// 1..kPiece slots loads its slot ids, sorts them on the lanes and reduces them
+// in order.
+constexpr int kLongLds = kLongGroups * 512;  // slot ids a long range orders in LDS (the partial-sum buffer)
+
 template <int VPL, bool CONSEC, bool ADAM>
 __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_long_blocks) {
-  __shared__ float part[kLongGroups][512];
+  __shared__ uint32_t lds[kLongLds];
+  float* part = (float*)lds;  // [kLongGroups][512] once the slot ids are no longer needed
   const int lane = threadIdx.x & 63, sub = lane & 31, gbase = lane & 32;
   if ((int64_t)blockIdx.x < n_long_blocks) {
-    __shared__ int64_t found;
-    if (threadIdx.x == 0) found = -1;
-    __syncthreads();
-    if (threadIdx.x <= kPiece) {
-      const int64_t c = (int64_t)blockIdx.x * (kPiece + 1) + threadIdx.x;
-      if (c + kPiece < a.n) {
-        const uint32_t kc = a.skeys[c];
-        if ((int64_t)kc < a.n_var && a.skeys[c + kPiece] == kc && (c == 0 || a.skeys[c - 1] != kc)) found = c;
-      }
-    }
-    __syncthreads();
-    if (found < 0) return;  // uniform per workgroup
+    if (blockIdx.x >= *a.n_long) return;  // uniform per workgroup
     const int grp = threadIdx.x >> 5;
-    const int64_t i0 = found;
-    const uint32_t key = a.skeys[i0];
+    const uint32_t key = a.long_list[blockIdx.x];
+    const int64_t lo = key == 0 ? 0 : a.ends[key - 1];
+    const int64_t hi = a.ends[key];
+    const int64_t len = hi - lo;
     float p[VPL], m[VPL], v[VPL];
     if (ADAM && grp == 0) {  // independent of the gradient: fetched first
       const int64_t off = (int64_t)key * a.dim;
@@ -571,63 +544,63 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
       load_f32<VPL, CONSEC>(a.m + off, sub, m);
       load_f32<VPL, CONSEC>(a.v + off, sub, v);
     }
+    const bool in_lds = len <= kLongLds;
+    uint32_t* gseg = (uint32_t*)a.slots + lo;
+    if (in_lds) {
+      for (int64_t i = threadIdx.x; i < len; i += 256) lds[i] = gseg[i];
+      __syncthreads();
+      bitonic_sort(lds, len);
+    } else {
+      bitonic_sort(gseg, len);  // global memory; the workgroup barrier orders its accesses
+    }
     float G[VPL];
 #pragma unroll
     for (int t = 0; t < VPL; ++t) G[t] = 0.0f;
-    for (int64_t j = grp;; j += kLongGroups) {
-      const int64_t start = i0 + j * kPiece;
-      if (start >= a.n) break;
-      const uint32_t kl = (start + sub < a.n) ? a.skeys[start + sub] : 0xffffffffu;
-      const uint32_t vl = (start + sub < a.n) ? a.svals[start + sub] : 0u;
-      const int cnt = __popc((uint32_t)(__ballot(kl == key) >> gbase));
-      if (cnt == 0) break;
+    for (int64_t start = (int64_t)grp * kPiece; start < len; start += (int64_t)kLongGroups * kPiece) {
+      const int cnt = (int)min((int64_t)kPiece, len - start);
+      const uint32_t vl = (sub < cnt) ? (in_lds ? lds[start + sub] : gseg[start + sub]) : 0u;
       float P[VPL];
 #pragma unroll
       for (int t = 0; t < VPL; ++t) P[t] = 0.0f;
       sum_piece<VPL, CONSEC, 4>(a, vl, gbase, cnt, sub, P);
 #pragma unroll
       for (int t = 0; t < VPL; ++t) G[t] = G[t] + P[t];
-      if (cnt < kPiece) break;
     }
+    __syncthreads();  // every slot id has been read: the buffer takes the group sums
 #pragma unroll
-    for (int t = 0; t < VPL; ++t) part[grp][col_of<VPL, CONSEC>(sub, t)] = G[t];
+    for (int t = 0; t < VPL; ++t) part[grp * 512 + col_of<VPL, CONSEC>(sub, t)] = G[t];
     __syncthreads();
     if (grp == 0) {
       float g[VPL];
 #pragma unroll
       for (int t = 0; t < VPL; ++t) {
         const int c = col_of<VPL, CONSEC>(sub, t);
-        g[t] = part[0][c];
-        for (int q = 1; q < kLongGroups; ++q) g[t] = g[t] + part[q][c];
+        g[t] = part[c];
+        for (int q = 1; q < kLongGroups; ++q) g[t] = g[t] + part[q * 512 + c];
       }
       finish<VPL, CONSEC, ADAM>(a, key, sub, g, p, m, v);
     }
     return;
   }
-  const int64_t i = (((int64_t)blockIdx.x - n_long_blocks) * 256 + threadIdx.x) >> 5;
-  if (i >= a.n) return;  // uniform per group
-  // The window [i, i+32), its neighbours i-1 and i+32: one round of loads.
-  const uint32_t kl = (i + sub < a.n) ? a.skeys[i + sub] : 0xffffffffu;
-  const uint32_t vl = (i + sub < a.n) ? a.svals[i + sub] : 0u;
-  const uint32_t prev = (i > 0) ? a.skeys[i - 1] : 0xffffffffu;
-  const uint32_t next = (i + kPiece < a.n) ? a.skeys[i + kPiece] : 0xffffffffu;
-  const uint32_t key = (uint32_t)__shfl((int)kl, gbase);
-  if ((int64_t)key >= a.n_var) return;  // frozen rows: no variable
-  if (prev == key) return;              // not the segment's first slot
-  if (next == key) return;              // a long segment: its own workgroup takes it
+  const int64_t k = (((int64_t)blockIdx.x - n_long_blocks) * 256 + threadIdx.x) >> 5;
+  if (k >= a.n_var) return;  // uniform per group
+  const int64_t lo = k == 0 ? 0 : a.ends[k - 1];
+  const int64_t len = (int64_t)a.ends[k] - lo;
+  if (len == 0 || len > kPiece) return;  // not hit, or a long range (its own workgroup)
   float p[VPL], m[VPL], v[VPL];
   if constexpr (ADAM) {  // the state rows do not depend on the gradient: fetch them first
-    const int64_t off = (int64_t)key * a.dim;
+    const int64_t off = k * a.dim;
     load_f32<VPL, CONSEC>(a.master + off, sub, p);
     load_f32<VPL, CONSEC>(a.m + off, sub, m);
     load_f32<VPL, CONSEC>(a.v + off, sub, v);
   }
-  const int cnt = __popc((uint32_t)(__ballot(kl == key) >> gbase));
+  const int cnt = (int)len;
+  const uint32_t vl = sort32((sub < cnt) ? a.slots[lo + sub] : 0xffffffffu, sub);
   float g[VPL];
 #pragma unroll
   for (int t = 0; t < VPL; ++t) g[t] = 0.0f;
   sum_piece<VPL, CONSEC, 4>(a, vl, gbase, cnt, sub, g);
-  finish<VPL, CONSEC, ADAM>(a, key, sub, g, p, m, v);
+  finish<VPL, CONSEC, ADAM>(a, k, sub, g, p, m, v);
 }
 
 // Dense mode: the variables no slot hit this step take a zero-gradient step.
@@ -651,102 +624,85 @@ __global__ __launch_bounds__(256) void dense_kernel(const SegArgs a) {
 // Host side
 // ---------------------------------------------------------------------------
 struct Workspace {
-  uint32_t* keys[2];
-  uint32_t* vals[2];
-  uint32_t* hist[2];
-  uint32_t* partial[2];  // per scan chunk, one buffer per pass parity
+  uint32_t* keys;       // [n] variable of every slot (n_var: none)
+  uint32_t* slots;      // [n] slot ids grouped by variable
+  uint32_t* off;        // [n_var + 1] counts -> offsets -> ends; [n_var]: long-list length
+  uint32_t* partial;    // scan chunk totals
+  uint32_t* long_list;  // variables of more than kPiece slots
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-static int64_t n_tiles_of(int64_t n) { return (n + kTile - 1) / kTile; }
+static int64_t n_long_max(int64_t n) { return n / (kPiece + 1) + 1; }
 
-static size_t partial_bytes(int64_t n) {
-  return align256((size_t)((n_tiles_of(n) * kMaxBuckets + kScanChunk - 1) / kScanChunk + 1) * 4);
+static int64_t scan_chunks(int64_t n_var) { return (n_var + kScanChunk - 1) / kScanChunk; }
+
+static size_t workspace_bytes(int64_t n, int64_t n_var) {
+  return 2 * align256((size_t)n * 4) + align256((size_t)(n_var + 1) * 4) +
+         align256((size_t)(scan_chunks(n_var) + 1) * 4) + align256((size_t)n_long_max(n) * 4);
 }
 
-static size_t workspace_bytes(int64_t n) {
-  const size_t kb = align256((size_t)n * 4);
-  const size_t hb = align256((size_t)n_tiles_of(n) * kMaxBuckets * 4);
-  return 4 * kb + 2 * hb + 2 * partial_bytes(n);
-}
-
-static Workspace carve(void* ws, int64_t n) {
+static Workspace carve(void* ws, int64_t n, int64_t n_var) {
   Workspace w;
   char* p = (char*)ws;
-  const size_t kb = align256((size_t)n * 4);
-  const size_t hb = align256((size_t)n_tiles_of(n) * kMaxBuckets * 4);
-  w.keys[0] = (uint32_t*)p;
-  w.vals[0] = (uint32_t*)(p + kb);
-  w.keys[1] = (uint32_t*)(p + 2 * kb);
-  w.vals[1] = (uint32_t*)(p + 3 * kb);
-  w.hist[0] = (uint32_t*)(p + 4 * kb);
-  w.hist[1] = (uint32_t*)(p + 4 * kb + hb);
-  w.partial[0] = (uint32_t*)(p + 4 * kb + 2 * hb);
-  w.partial[1] = (uint32_t*)(p + 4 * kb + 2 * hb + partial_bytes(n));
+  w.keys = (uint32_t*)p;
+  p += align256((size_t)n * 4);
+  w.slots = (uint32_t*)p;
+  p += align256((size_t)n * 4);
+  w.off = (uint32_t*)p;
+  p += align256((size_t)(n_var + 1) * 4);
+  w.partial = (uint32_t*)p;
+  p += align256((size_t)(scan_chunks(n_var) + 1) * 4);
+  w.long_list = (uint32_t*)p;
   return w;
 }
 
-// keys + stable radix sort; *sorted = index (0/1) of the sorted buffers.
-static int sort_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_t n_var, const int64_t* index,
-                      int64_t index_capacity, bool direct, const Workspace& w, hipStream_t st, int* sorted) {
-  int bits = 0;
-  while (bits < 32 && ((uint64_t)n_var >> bits) != 0) ++bits;  // keys lie in [0, n_var]
-  const int passes = bits == 0 ? 0 : (bits + kMaxDigitBits - 1) / kMaxDigitBits;
-  const int dbits = passes == 0 ? 1 : (bits + passes - 1) / passes;
+static unsigned grid_for(int64_t items, int64_t per_block, int64_t cap) {
+  const int64_t b = (items + per_block - 1) / per_block;
+  return (unsigned)(b < 1 ? 1 : (b > cap ? cap : b));
+}
+
+// Keys, counts, offsets and the CSR fill.
+static int group_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_t n_var, const int64_t* index,
+                       int64_t index_capacity, bool direct, const Workspace& w, hipStream_t st) {
   int split_shift = 0;
   while (((n_var + (1LL << split_shift) - 1) >> split_shift) > kSplitMax) ++split_shift;
-  const int n_tiles = (int)n_tiles_of(n);
+  hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n_var + 1, 256, 1024)), dim3(256), 0, st, w.off, n_var + 1);
+  const dim3 kgrid((unsigned)((n + kTile - 1) / kTile));
   if (direct) {
-    hipLaunchKernelGGL(keys_hist_kernel<2>, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
-                       (const unsigned long long*)nullptr, 0, w.keys[0], w.vals[0], dbits, n_tiles, w.hist[0]);
+    hipLaunchKernelGGL(keys_count_kernel<2>, kgrid, dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
+                       (const unsigned long long*)nullptr, 0, w.keys, w.off);
   } else if (index != nullptr) {
     int ib = 0;
     while ((1LL << ib) < index_capacity) ++ib;
-    hipLaunchKernelGGL(keys_hist_kernel<1>, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
-                       (const unsigned long long*)index, ib, w.keys[0], w.vals[0], dbits, n_tiles, w.hist[0]);
+    hipLaunchKernelGGL(keys_count_kernel<1>, kgrid, dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
+                       (const unsigned long long*)index, ib, w.keys, w.off);
   } else {
-    hipLaunchKernelGGL(keys_hist_kernel<0>, dim3(n_tiles), dim3(kTileThreads), 0, st, rows, n, ids, n_var,
-                       split_shift, (const unsigned long long*)nullptr, 0, w.keys[0], w.vals[0], dbits, n_tiles,
-                       w.hist[0]);
+    hipLaunchKernelGGL(keys_count_kernel<0>, kgrid, dim3(kTileThreads), 0, st, rows, n, ids, n_var, split_shift,
+                       (const unsigned long long*)nullptr, 0, w.keys, w.off);
   }
-  int rc = launch_status("keys_hist_kernel");
-  if (rc != EG_OK) return rc;
-  int cur = 0;
-  for (int pass = 0; pass < passes; ++pass) {
-    const bool last = pass + 1 == passes;
-    uint32_t* h = w.hist[pass & 1];
-    uint32_t* h_next = last ? nullptr : w.hist[(pass + 1) & 1];
-    const int64_t len = (int64_t)n_tiles << dbits;
-    const unsigned chunks = (unsigned)((len + kScanChunk - 1) / kScanChunk);
-    // Pass 0 sums its scan chunks here; a later pass's chunk totals are counted
-    // by the scatter before it when they fit its LDS (fused), else summed here.
-    // What the next scatter accumulates into is cleared before it runs.
-    const bool fused = chunks <= (unsigned)kMaxChunksLds;
-    uint32_t* part = w.partial[pass & 1];
-    uint32_t* part_next = (last || !fused) ? nullptr : w.partial[(pass + 1) & 1];
-    if (pass == 0 || !fused)
-      hipLaunchKernelGGL(scan_partials, dim3(chunks), dim3(kScanThreads), 0, st, h, len, part, h_next,
-                         last ? (int64_t)0 : len);
-    else if (!last)
-      hipLaunchKernelGGL(scan_partials, dim3(1), dim3(kScanThreads), 0, st, h, (int64_t)0, part_next, h_next, len);
-    hipLaunchKernelGGL(scan_apply, dim3(chunks), dim3(kScanThreads), 0, st, h, len, part, part_next,
-                       part_next ? (int64_t)chunks + 1 : (int64_t)0);
-    hipLaunchKernelGGL(scatter_kernel, dim3(n_tiles), dim3(kTileThreads), 0, st, w.keys[cur], w.vals[cur],
-                       w.keys[cur ^ 1], w.vals[cur ^ 1], n, pass * dbits, dbits, n_tiles, h, h_next, part_next,
-                       (pass + 1) * dbits, dbits);
-    rc = launch_status("radix sort pass");
-    if (rc != EG_OK) return rc;
-    cur ^= 1;
-  }
-  *sorted = cur;
-  return EG_OK;
+  const unsigned chunks = (unsigned)scan_chunks(n_var);
+  hipLaunchKernelGGL(scan_partials, dim3(chunks), dim3(kScanThreads), 0, st, w.off, n_var, w.partial);
+  hipLaunchKernelGGL(scan_apply, dim3(chunks), dim3(kScanThreads), 0, st, w.off, n_var, w.partial, w.long_list,
+                     w.off + n_var);
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w.keys, n, n_var, w.off,
+                     w.slots);
+  return launch_status("slot grouping kernels");
+}
+
+static void fill_seg(SegArgs* a, const Workspace& w, int64_t n, int64_t n_var) {
+  a->ends = w.off;
+  a->slots = w.slots;
+  a->long_list = w.long_list;
+  a->n_long = w.off + n_var;
+  a->n = n;
+  a->n_var = n_var;
 }
 
 template <bool ADAM, int VPL, bool CONSEC>
 static void launch_reduce_t(const SegArgs& a, hipStream_t st) {
-  const int64_t n_long_blocks = (a.n + kPiece) / (kPiece + 1);
-  const dim3 grid((unsigned)(n_long_blocks + (a.n * 32 + 255) / 256));
+  const int64_t n_long_blocks = n_long_max(a.n);
+  const dim3 grid((unsigned)(n_long_blocks + (a.n_var * 32 + 255) / 256));
   hipLaunchKernelGGL((reduce_kernel<VPL, CONSEC, ADAM>), grid, dim3(256), 0, st, a, n_long_blocks);
 }
 
@@ -784,8 +740,8 @@ static int check_common(const void* d_out, const int32_t* rows, int64_t n_pos, i
   EG_CHECK_ARG(n < (1LL << 31), "n_pos*heads=%lld slots exceed 2^31", (long long)n);
   EG_CHECK_ARG(n == 0 || (d_out != nullptr && rows != nullptr), "d_out/rows is NULL");
   EG_CHECK_ARG(n_var == 0 || ids != nullptr, "ids is NULL");
-  if (ws_bytes < workspace_bytes(n))
-    return set_error(EG_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", ws_bytes, workspace_bytes(n));
+  if (ws_bytes < workspace_bytes(n, n_var))
+    return set_error(EG_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", ws_bytes, workspace_bytes(n, n_var));
   EG_CHECK_ARG(n == 0 || ws != nullptr, "workspace is NULL");
   return EG_OK;
 }
@@ -796,7 +752,9 @@ using namespace eg;
 
 extern "C" {
 
-size_t eg_backward_workspace_size(int64_t n_slots) { return workspace_bytes(n_slots < 0 ? 0 : n_slots); }
+size_t eg_backward_workspace_size(int64_t n_slots, int64_t n_var) {
+  return workspace_bytes(n_slots < 0 ? 0 : n_slots, n_var < 0 ? 0 : n_var);
+}
 
 int eg_build_row_index(const int32_t* ids, int64_t n, int64_t* table, int64_t capacity, void* stream) {
   EG_CHECK_ARG(n >= 0 && n < (1LL << 31), "n=%lld", (long long)n);
@@ -825,16 +783,12 @@ static int scatter_grad_impl(const void* d_out, int32_t d_out_f32, const int32_t
   const int64_t n = n_pos * heads;
   if (n == 0 || n_var == 0) return EG_OK;
   hipStream_t st = (hipStream_t)stream;
-  const Workspace w = carve(workspace, n);
-  int cur = 0;
-  rc = sort_slots(rows, n, ids, n_var, nullptr, 0, direct, w, st, &cur);
+  const Workspace w = carve(workspace, n, n_var);
+  rc = group_slots(rows, n, ids, n_var, nullptr, 0, direct, w, st);
   if (rc != EG_OK) return rc;
   SegArgs a;
   memset(&a, 0, sizeof(a));
-  a.skeys = w.keys[cur];
-  a.svals = w.vals[cur];
-  a.n = n;
-  a.n_var = n_var;
+  fill_seg(&a, w, n, n_var);
   a.d_out = d_out;
   a.d_out_f32 = d_out_f32;
   a.heads = heads;
@@ -891,16 +845,12 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   const int64_t n = n_pos * heads;
   if (state->n == 0) return EG_OK;
   hipStream_t st = (hipStream_t)stream;
-  const Workspace w = carve(workspace, n);
-  int cur = 0;
+  const Workspace w = carve(workspace, n, state->n);
   if (n > 0) {
-    rc = sort_slots(rows, n, state->ids, state->n, state->index, state->index_capacity, false, w, st, &cur);
+    rc = group_slots(rows, n, state->ids, state->n, state->index, state->index_capacity, false, w, st);
     if (rc != EG_OK) return rc;
   }
-  a.skeys = w.keys[cur];
-  a.svals = w.vals[cur];
-  a.n = n;
-  a.n_var = state->n;
+  fill_seg(&a, w, n, state->n);
   a.d_out = d_out;
   a.d_out_f32 = d_out_f32;
   a.heads = heads;

@@ -36,8 +36,8 @@ class _Workspace:
     def __init__(self):
         self._buf: dict[torch.device, torch.Tensor] = {}
 
-    def get(self, n_slots: int, device) -> torch.Tensor:
-        need = int(_lib.load().eg_backward_workspace_size(int(n_slots)))
+    def get(self, n_slots: int, n_var: int, device) -> torch.Tensor:
+        need = int(_lib.load().eg_backward_workspace_size(int(n_slots), int(n_var)))
         dev = torch.device(device)
         buf = self._buf.get(dev)
         if buf is None or buf.numel() < need:
@@ -73,7 +73,7 @@ def scatter_grad(d_out: torch.Tensor, rows: torch.Tensor, ids: torch.Tensor, dim
         grad = torch.zeros((ids.numel(), dim), dtype=torch.float32, device=dev)
     elif grad.shape != (ids.numel(), dim) or grad.dtype != torch.float32 or not grad.is_contiguous():
         raise ValueError("grad must be a contiguous f32 [len(ids), dim] tensor")
-    ws = _WS.get(n_pos * heads, dev)
+    ws = _WS.get(n_pos * heads, ids.numel(), dev)
     _lib.call("eg_scatter_grad", _lib.ptr(d_out), _dout_args(d_out), _lib.ptr(rows), n_pos, heads, dim,
               _lib.ptr(ids), ids.numel(), _lib.ptr(grad), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
     return grad
@@ -169,7 +169,7 @@ class DescentState:
                 raise ValueError("the pull term needs the base table (DescentState(base=...))")
             opt.l2_coef = float(np.float32(mu) / np.float32(self.rows0_sq))
             base = self.base.c_table
-        ws = _WS.get(n_pos * heads, dev)
+        ws = _WS.get(n_pos * heads, self.n, dev)
         st = self.c_state()
         _lib.call("eg_descent_step", _lib.ptr(d_out), _dout_args(d_out), _lib.ptr(rows), n_pos, heads,
                   ctypes.byref(st), ctypes.byref(opt), ctypes.byref(base) if base is not None else None,

@@ -80,7 +80,7 @@ class _GatherSlots(torch.autograd.Function):
         n = slot_var.shape[0]
         grad = torch.zeros((n_var, dim), dtype=torch.float32, device=dev)
         if n > 0 and n_var > 0:
-            ws = _WS.get(n * heads, dev)
+            ws = _WS.get(n * heads, n_var, dev)
             _lib.call("eg_scatter_grad_slots", _lib.ptr(d), _dout_args(d), _lib.ptr(slot_var), n, heads, dim,
                       n_var, _lib.ptr(grad), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
         return grad.to(device=device, dtype=dtype), None, None, None

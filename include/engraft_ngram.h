@@ -176,8 +176,9 @@ typedef struct eg_descent_state {
  * (row << 32 | position in ids), -1 when empty.  Built once per state. */
 int eg_build_row_index(const int32_t* ids, int64_t n, int64_t* table, int64_t capacity, void* stream);
 
-/* Workspace bytes eg_scatter_grad / eg_descent_step need for n_slots = n_pos*heads. */
-size_t eg_backward_workspace_size(int64_t n_slots);
+/* Workspace bytes eg_scatter_grad(_slots) / eg_descent_step need for
+ * n_slots = n_pos*heads slots and n_var variables (no initial contents needed). */
+size_t eg_backward_workspace_size(int64_t n_slots, int64_t n_var);
 
 /* grad_out f32 [n_var, dim] += sum over slots hitting each variable (rows not
  * hit are left untouched: pass a zeroed buffer for the plain gradient).

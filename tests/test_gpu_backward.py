@@ -68,11 +68,14 @@ def test_scatter_grad_edge_cases(cuda):
     rows = torch.full((70, 1), 7, dtype=torch.int32)
     d = torch.randn((70, 128), device=cuda)
     assert D.scatter_grad(d, rows, ids, 128).abs().sum().item() == 0
-    rows = torch.full((5000, 1), 9, dtype=torch.int32)
-    d = torch.randn((5000, 128), device=cuda)
-    got = D.scatter_grad(d, rows, ids, 128).cpu().numpy()
-    exp, _ = B.scatter_grad(d.cpu().numpy(), rows.numpy(), ids.numpy())
-    assert np.array_equal(got, exp)
+    # one variable hit by every slot: ordered in LDS (5,000 slots) and, past the
+    # LDS capacity of 8,192 slot ids, on global memory (20,000 slots)
+    for n in (5000, 20000):
+        rows = torch.full((n, 1), 9, dtype=torch.int32)
+        d = torch.randn((n, 128), device=cuda)
+        got = D.scatter_grad(d, rows, ids, 128).cpu().numpy()
+        exp, _ = B.scatter_grad(d.cpu().numpy(), rows.numpy(), ids.numpy())
+        assert np.array_equal(got, exp)
 
 
 def test_descent_step_config2_full_size(cuda):
