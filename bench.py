@@ -31,6 +31,7 @@ HBM_PEAK_GBS = 8000.0
 
 N_ROWS, DIM, BATCH, SEQ, VOCAB, WIDTH, SLOTS = 320_000_000, 128, 8, 2048, 151_936, 2048, 16
 TABLE_SEED, HASH_SEED, TOKEN_SEED, RES_SEED = 201, 200, 202, 203
+DECODE_SEED, C4_SEED = 300, 400
 Q8_ROW_BYTES = DIM + 2 * DIM // 32  # 128 B int8 + 4 fp16 scales = 136 B
 
 
@@ -172,6 +173,89 @@ def bench_backward(tab, tokens, steps: int, warmup: int) -> dict:
                         "fp32 master/m/v kept"}
 
 
+def bench_decode(tab, steps: int) -> dict:
+    """the config-1 table plus a 500,000-row Q8_0 overlay
+    (sorted ids, seeded rows), 256 sequences x (2 context tokens + 1 new); one
+    eg_forward_decode per step, latency per call from HIP events around it."""
+    import numpy as np
+    import torch
+
+    from engraft_ngram_amd import synthetic as S
+    from engraft_ngram_amd import table as T
+    from engraft_ngram_amd.overlay import DeviceOverlay
+
+    dev = tab.device
+    n_seq, ctx, n_ov = 256, 3, 500_000
+    ids = np.unique(np.random.default_rng(DECODE_SEED).integers(0, N_ROWS, size=n_ov + 4096))[:n_ov]
+    store = T.RowStore.empty("q8_0", ids.size, DIM, dev)
+    T.fill_synthetic(store, seed=DECODE_SEED + 1, sigma=0.02)
+    ov = DeviceOverlay(torch.from_numpy(ids.astype(np.int32)).to(dev), store)
+    tok = torch.from_numpy(S.zipf_tokens(DECODE_SEED + 2, n_seq * ctx, VOCAB).reshape(n_seq, ctx)).to(dev)
+    res = S.residual(n_seq, WIDTH, seed=DECODE_SEED + 3, device=dev)
+    out = torch.empty_like(res)
+    call = T.PreparedForward([tab], tok, res, out=out, overlays=[ov], decode_ctx=ctx)
+    for _ in range(20):
+        call()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        call()
+        b.record()
+    torch.cuda.synchronize()
+    lat = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+    nbytes = n_seq * (SLOTS * Q8_ROW_BYTES + 2 * 2 * WIDTH + ctx * 8)
+    return {"workload": "BASELINE config 3: 256 sequences x (2 context + 1 new token), config-1 table + "
+                        "500,000-row Q8_0 overlay resolved per id (binary search over sorted int32 ids)",
+            "calls": steps, "us_p50": lat[len(lat) // 2], "us_p99": lat[min(len(lat) - 1, int(len(lat) * 0.99))],
+            "us_min": lat[0], "lookups_per_call": n_seq * SLOTS, "algorithmic_bytes_per_call": nbytes}
+
+
+def bench_config4(steps: int, warmup: int) -> dict:
+    """2 table layers x 160,000,000 MXFP8 rows, 2-/3-/4-gram
+    hashes (24 slots per layer), 32,768 Zipf tokens over 129,280, residual width
+    3,072; one fused launch per step (both layers summed in fp32)."""
+    import torch
+
+    from engraft_ngram_amd import synthetic as S
+    from engraft_ngram_amd import table as T
+
+    dev = torch.device("cuda", 0)
+    rows4, seq4, vocab4, width4, slots4 = 160_000_000, 32_768, 129_280, 3072, 24
+    tabs = []
+    for l in range(2):
+        hp = S.hash_params(rows4, C4_SEED + l, ngram_size=4)
+        tabs.append(T.DeviceTable.synthetic("mxfp8", rows4, DIM, seed=C4_SEED + 10 + l, sigma=0.02, device=dev,
+                                            **hp))
+    tok = torch.from_numpy(S.zipf_tokens(C4_SEED + 20, seq4, vocab4)).to(dev)
+    res = [S.residual(seq4, width4, seed=C4_SEED + 30 + i, device=dev) for i in range(2)]
+    outs = [torch.empty_like(r) for r in res]
+    calls = [T.PreparedForward(tabs, tok, res[i], out=outs[i]) for i in range(2)]
+    for i in range(warmup):
+        calls[i % 2]()
+    ev = _Events(4)
+    torch.cuda.synchronize()
+    for i in range(steps):
+        c = calls[i % 2]
+        if i == 0:
+            c.timed(ev[0], ev[1] if steps > 1 else ev[3])
+        elif i == steps - 1:
+            c.timed(ev[2], ev[3])
+        else:
+            c()
+    torch.cuda.synchronize()
+    us = ev.elapsed_ms(0, 3) / steps * 1e3
+    ev.destroy()
+    row_bytes = DIM + DIM // 32  # e4m3 values + e8m0 scales
+    nbytes = seq4 * (2 * slots4 * row_bytes + 2 * 2 * width4 + 8)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del tabs
+    torch.cuda.empty_cache()
+    return {"workload": "BASELINE config 4: 2 layers x 160M MXFP8 rows, 24 slots/layer, seq 32768, width 3072",
+            "us_per_launch": us, "rows_per_s": seq4 * 2 * slots4 / (us * 1e-6), "gb_per_s": gbs,
+            "frac_of_hbm_peak": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": nbytes}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -180,6 +264,7 @@ def main() -> None:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-backward", action="store_true", help="skip the config-2 descent step leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config-3 decode and config-4 legs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (torch copy_) 10 times: the known-size kernel the "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by")
@@ -298,6 +383,15 @@ def main() -> None:
         result["backward"] = bw
         log(f"backward: {bw['us_per_step']:.1f} us/step, {bw['touched_rows']} touched rows, "
             f"{bw['gb_per_s']:.0f} GB/s algorithmic ({100 * bw['frac_of_hbm_peak']:.1f}% of peak)")
+
+    if not args.no_extra:
+        dc = bench_decode(tab, 200)
+        result["decode_config3"] = dc
+        log(f"decode (config 3): p50 {dc['us_p50']:.1f} us, p99 {dc['us_p99']:.1f} us per call")
+        c4 = bench_config4(max(1, args.steps // 4), max(1, args.warmup // 4))
+        result["forward_config4"] = c4
+        log(f"forward (config 4): {c4['us_per_launch']:.1f} us/launch, {c4['gb_per_s']:.0f} GB/s algorithmic "
+            f"({100 * c4['frac_of_hbm_peak']:.1f}% of peak)")
 
     if not args.no_cpu:
         cb = cpu_baseline(hp, tokens_np, res[0].cpu(), args.cpu_seconds)

@@ -113,22 +113,32 @@ struct FwdArgs {
   int32_t n_layers;
   int32_t heads;
   int32_t dim;
-  int32_t nch;              // 8-value chunks per lane: ceil(W / 512)
+  int32_t decode_ctx;       // > 0: position p is the last token of sequence p, tokens [n_pos, decode_ctx]
+  int32_t parts;            // wavefronts per position: ceil(W / (NCH * 512))
 };
 
-constexpr int kMaxChunks = 8;  // W <= 4096
+constexpr int kMaxWidth = 4096;  // W = heads * dim
 constexpr int kWavesPerBlock = 4;
 
-// NCH: 8-value chunks per lane (exact for the specialised shapes, an upper
-// bound for the generic kernel); OVL: overlay lookups compiled in.
-template <int FMT, int DIM, int NCH, int MAXL, bool F32OUT, bool OVL>
+// One wavefront per (position, column part): part q of position p covers the
+// columns [q*NCH*512, (q+1)*NCH*512) of the position's W, NCH 8-value chunks
+// per lane, and hashes the heads those columns touch (a head whose row spans
+// two parts is hashed by both).  OVL: overlay lookups compiled in.
+template <int FMT, int DIM, int NCH, int MAXL, bool F32OUT, bool OVL, int PARTS>
 __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t p = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const uint32_t wid = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);  // n_pos * parts < 2^32
+  const uint32_t parts = PARTS ? (uint32_t)PARTS : (uint32_t)a.parts;     // PARTS: known at compile time
+  const uint32_t pu = parts == 1 ? wid : wid / parts;
+  const int64_t p = pu;
   if (p >= a.n_pos) return;  // uniform per wavefront
   const int dim = DIM ? DIM : a.dim;
   const int H = a.heads;
   const int W = H * dim;
+  const int cb = (int)(wid - pu * parts) * (NCH * 512);  // first column of this wavefront
+  const int h_lo = cb / dim;                                // first head it touches
+  const int nh = min(H, (cb + NCH * 512 + dim - 1) / dim) - h_lo;  // heads it touches
+  const int hh = h_lo + lane;                               // the head lane < nh hashes
 
   // 1. Everything the row ids depend on (tokens, segment start, multipliers,
   //    or the caller's row ids) is loaded first: vmcnt retires loads in issue
@@ -137,20 +147,22 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   uint64_t raw[EG_MAX_NGRAM];
   uint64_t mult[EG_MAX_LAYERS][EG_MAX_NGRAM];
   int64_t seg0 = 0;
+  int64_t tp = p;  // index of position p's own token
   int32_t rid[EG_MAX_LAYERS] = {0, 0};
   static_assert(MAXL >= 1 && MAXL <= EG_MAX_LAYERS, "layer count");
   const bool hashing = a.rows_in == nullptr;
-  if (lane < H) {
+  if (lane < nh) {
     if (hashing) {
-      seg0 = seg_start_of(p, a.seq_len, a.seg_start);
+      tp = a.decode_ctx > 0 ? p * a.decode_ctx + (a.decode_ctx - 1) : p;
+      seg0 = a.decode_ctx > 0 ? p * a.decode_ctx : seg_start_of(p, a.seq_len, a.seg_start);
       int ng = a.hash[0].ngram_size;
       if (MAXL > 1 && nl > 1 && a.hash[1].ngram_size > ng) ng = a.hash[1].ngram_size;
-      load_ctx_tokens(a.tokens, p, ng, raw);
+      load_ctx_tokens(a.tokens, tp, ng, raw);
 #pragma unroll
       for (int l = 0; l < MAXL; ++l)
-        if (l < nl) load_head_mult(a.hash[l], lane, mult[l]);
+        if (l < nl) load_head_mult(a.hash[l], hh, mult[l]);
     } else {
-      rid[0] = a.rows_in[p * H + lane];
+      rid[0] = a.rows_in[p * H + hh];
     }
   }
 
@@ -158,21 +170,21 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   u32x4 res[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int e0 = (lane + 64 * c) * 8;
+    const int e0 = cb + (lane + 64 * c) * 8;
     if (a.residual != nullptr && e0 < W)
       res[c] = __builtin_nontemporal_load((const u32x4*)(a.residual + p * W + e0));
     else
       res[c] = u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};  // -0 + x == x for every x
   }
 
-  // 3. Row ids of head `lane`, one per layer.
-  if (lane < H && hashing) {
+  // 3. Row ids of head hh, one per layer.
+  if (lane < nh && hashing) {
 #pragma unroll
     for (int l = 0; l < MAXL; ++l) {
       if (l < nl) {
         uint64_t ctx[EG_MAX_NGRAM];
-        ctx_from(a.hash[l], raw, p, seg0, ctx);
-        rid[l] = row_of(a.hash[l], lane, ctx, mult[l], true);
+        ctx_from(a.hash[l], raw, tp, seg0, ctx);
+        rid[l] = row_of(a.hash[l], hh, ctx, mult[l], true);
       }
     }
   }
@@ -184,13 +196,14 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
 #pragma unroll
   for (int l = 0; l < MAXL; ++l) {
     if (l >= nl) break;
-    if (lane < H && a.rows_out != nullptr) a.rows_out[((int64_t)l * a.n_pos + p) * H + lane] = rid[l];
+    if (lane < nh && hh * dim >= cb && a.rows_out != nullptr)  // the part holding the head's first column
+      a.rows_out[((int64_t)l * a.n_pos + p) * H + hh] = rid[l];
     int32_t ovk = -1;
     const OverlayDev& ov = a.ov[l];
     if constexpr (OVL) {
-      if (lane < H) {
+      if (lane < nh) {
         if (a.slot_var != nullptr) {
-          ovk = a.slot_var[p * H + lane];
+          ovk = a.slot_var[p * H + hh];
         } else if (ov.n > 0) {
           const int64_t k = sorted_find(ov.ids, ov.n, rid[l]);
           if (k >= 0) ovk = ov.index ? ov.index[k] : (int32_t)k;
@@ -199,11 +212,11 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
     }
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const int e0 = (lane + 64 * c) * 8;
+      const int e0 = cb + (lane + 64 * c) * 8;
       const int h = min(e0, W - 8) / dim;
-      const int32_t row = __shfl(rid[l], h);
+      const int32_t row = __shfl(rid[l], h - h_lo);
       int32_t k = -1;
-      if constexpr (OVL) k = __shfl(ovk, h);
+      if constexpr (OVL) k = __shfl(ovk, h - h_lo);
       const int off = e0 - h * dim;
       src[l][c] = 2;
       if (e0 < W) {
@@ -234,7 +247,7 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
     if (l >= nl) break;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const int e0 = (lane + 64 * c) * 8;
+      const int e0 = cb + (lane + 64 * c) * 8;
       const int off = e0 - (min(e0, W - 8) / dim) * dim;
       float v[8];
       if (src[l][c] == 0) {
@@ -252,7 +265,7 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
 
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int e0 = (lane + 64 * c) * 8;
+    const int e0 = cb + (lane + 64 * c) * 8;
     if (e0 < W) {
       if constexpr (F32OUT) {
         u32x4* dst = (u32x4*)((float*)a.out + p * W + e0);
@@ -288,58 +301,65 @@ static thread_local hipEvent_t g_ev_stop = nullptr;
       hipLaunchKernelGGL((forward_kernel<__VA_ARGS__>), grid, dim3(256), 0, st, a);                     \
   } while (0)
 
-// Specialised residual-add shapes: dim 128 with 16 (W = 2048) or 24 (W = 3072)
-// heads, one or two layers; everything else goes through the generic kernel.
-template <int FMT, int NCH>
-static void launch_special_nch(const FwdArgs& a, bool ovl, dim3 grid, hipStream_t st) {
-  if (a.n_layers == 1) {
-    if (ovl) EG_LAUNCH(FMT, 128, NCH, 1, false, true); else EG_LAUNCH(FMT, 128, NCH, 1, false, false);
-  } else {
-    if (ovl) EG_LAUNCH(FMT, 128, NCH, 2, false, true); else EG_LAUNCH(FMT, 128, NCH, 2, false, false);
-  }
+// One launch: parts = ceil(W / (NCH * 512)) wavefronts per position (PARTS:
+// the same number when the caller's shape fixes it, 0 otherwise).
+template <int FMT, int DIM, int NCH, int MAXL, bool F32OUT, bool OVL, int PARTS = 0>
+static void launch_nch(FwdArgs a, hipStream_t st) {
+  a.parts = (a.heads * a.dim + NCH * 512 - 1) / (NCH * 512);
+  const int64_t waves = a.n_pos * a.parts;
+  const dim3 grid((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock));
+  EG_LAUNCH(FMT, DIM, NCH, MAXL, F32OUT, OVL, PARTS);
 }
 
+// Specialised residual-add shapes (dim 128): a whole W = 2048 row per
+// wavefront for one layer without overlay (the config-1 shape), W = 3072 in
+// two halves; two layers and overlay lookups take 1024-column parts, which
+// keeps their registers (and so their occupancy) close to the one-layer
+// kernel's.  Everything else goes through the generic kernel.
 template <int FMT>
-static bool launch_special(const FwdArgs& a, bool ovl, dim3 grid, hipStream_t st) {
+static bool launch_special(const FwdArgs& a, bool ovl, hipStream_t st) {
   if (a.dim != 128) return false;
-  if (a.nch == 4) {
-    launch_special_nch<FMT, 4>(a, ovl, grid, st);
-    return true;
+  const int W = a.heads * a.dim;
+  if (W != 2048 && W != 3072) return false;
+  if (a.n_layers == 1 && !ovl) {
+    if (W == 2048) launch_nch<FMT, 128, 4, 1, false, false, 1>(a, st);
+    else launch_nch<FMT, 128, 3, 1, false, false, 2>(a, st);
+  } else if (a.n_layers == 1) {
+    launch_nch<FMT, 128, 2, 1, false, true>(a, st);
+  } else if (!ovl) {
+    launch_nch<FMT, 128, 2, 2, false, false>(a, st);
+  } else {
+    launch_nch<FMT, 128, 2, 2, false, true>(a, st);
   }
-  if (a.nch == 6) {
-    launch_special_nch<FMT, 6>(a, ovl, grid, st);
-    return true;
-  }
-  return false;
+  return true;
 }
 
-// Any shape: runtime dim, up to kMaxChunks chunks, overlays compiled in.
+// Any shape: runtime dim, 1024-column parts, overlays compiled in.
 template <int FMT, bool F32OUT>
-static void launch_generic(const FwdArgs& a, dim3 grid, hipStream_t st) {
-  if (a.n_layers == 1) EG_LAUNCH(FMT, 0, kMaxChunks, 1, F32OUT, true);
-  else EG_LAUNCH(FMT, 0, kMaxChunks, 2, F32OUT, true);
+static void launch_generic(const FwdArgs& a, hipStream_t st) {
+  if (a.n_layers == 1) launch_nch<FMT, 0, 2, 1, F32OUT, true>(a, st);
+  else launch_nch<FMT, 0, 2, 2, F32OUT, true>(a, st);
 }
 
 template <bool F32OUT>
 static int launch_forward(const FwdArgs& a, hipStream_t st) {
   if (a.n_pos == 0) return EG_OK;
-  const dim3 grid((unsigned)((a.n_pos + kWavesPerBlock - 1) / kWavesPerBlock));
   bool ovl = a.slot_var != nullptr;
   for (int l = 0; l < a.n_layers; ++l) ovl = ovl || a.ov[l].n > 0;
   const int fmt = a.table[0].fmt;
   if (!F32OUT) {
     bool done = false;
-    if (fmt == EG_FMT_Q8_0) done = launch_special<EG_FMT_Q8_0>(a, ovl, grid, st);
-    else if (fmt == EG_FMT_BF16) done = launch_special<EG_FMT_BF16>(a, ovl, grid, st);
-    else if (fmt == EG_FMT_MXFP8) done = launch_special<EG_FMT_MXFP8>(a, ovl, grid, st);
+    if (fmt == EG_FMT_Q8_0) done = launch_special<EG_FMT_Q8_0>(a, ovl, st);
+    else if (fmt == EG_FMT_BF16) done = launch_special<EG_FMT_BF16>(a, ovl, st);
+    else if (fmt == EG_FMT_MXFP8) done = launch_special<EG_FMT_MXFP8>(a, ovl, st);
     if (done) return launch_status("forward_kernel");
   }
   switch (fmt) {
-    case EG_FMT_Q8_0: launch_generic<EG_FMT_Q8_0, F32OUT>(a, grid, st); break;
-    case EG_FMT_BF16: launch_generic<EG_FMT_BF16, F32OUT>(a, grid, st); break;
-    case EG_FMT_MXFP8: launch_generic<EG_FMT_MXFP8, F32OUT>(a, grid, st); break;
-    case EG_FMT_IQ4_NL: launch_generic<EG_FMT_IQ4_NL, F32OUT>(a, grid, st); break;
-    case EG_FMT_F32: launch_generic<EG_FMT_F32, F32OUT>(a, grid, st); break;
+    case EG_FMT_Q8_0: launch_generic<EG_FMT_Q8_0, F32OUT>(a, st); break;
+    case EG_FMT_BF16: launch_generic<EG_FMT_BF16, F32OUT>(a, st); break;
+    case EG_FMT_MXFP8: launch_generic<EG_FMT_MXFP8, F32OUT>(a, st); break;
+    case EG_FMT_IQ4_NL: launch_generic<EG_FMT_IQ4_NL, F32OUT>(a, st); break;
+    case EG_FMT_F32: launch_generic<EG_FMT_F32, F32OUT>(a, st); break;
     default: return set_error(EG_ERR_UNSUPPORTED, "row format %d", fmt);
   }
   return launch_status("forward_kernel");
@@ -399,13 +419,15 @@ int eg_hash_rows(const eg_hash_spec* spec, const int64_t* tokens, int64_t n_pos,
   return launch_status("hash_kernel");
 }
 
-int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables, const eg_overlay* overlays,
-               const int64_t* tokens, int64_t n_pos, int64_t seq_len, const int32_t* seg_start,
-               const uint16_t* residual, void* out, int32_t* rows_out, void* stream) {
+static int forward_entry(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,
+                         const eg_overlay* overlays, const int64_t* tokens, int64_t n_pos, int64_t seq_len,
+                         const int32_t* seg_start, int32_t decode_ctx, const uint16_t* residual, void* out,
+                         int32_t* rows_out, void* stream) {
   EG_CHECK_ARG(n_layers >= 1 && n_layers <= EG_MAX_LAYERS, "n_layers=%d outside [1, %d]", n_layers,
                EG_MAX_LAYERS);
+  EG_CHECK_ARG(decode_ctx >= 0, "decode_ctx < 0");
   EG_CHECK_ARG(specs != nullptr && tables != nullptr, "specs/tables is NULL");
-  EG_CHECK_ARG(n_pos >= 0, "n_pos < 0");
+  EG_CHECK_ARG(n_pos >= 0 && n_pos < (1LL << 30), "n_pos=%lld outside [0, 2^30)", (long long)n_pos);
   EG_CHECK_ARG(n_pos == 0 || (tokens != nullptr && out != nullptr), "tokens/out is NULL");
   FwdArgs a;
   memset(&a, 0, sizeof(a));
@@ -435,9 +457,24 @@ int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tabl
   a.heads = a.hash[0].n_heads;
   a.dim = tables[0].dim;
   const int W = a.heads * a.dim;
-  EG_CHECK_ARG(W <= 512 * kMaxChunks, "row width %d > %d", W, 512 * kMaxChunks);
-  a.nch = (W + 511) / 512;
+  EG_CHECK_ARG(W <= kMaxWidth, "row width %d > %d", W, kMaxWidth);
+  a.decode_ctx = decode_ctx;
   return residual ? launch_forward<false>(a, (hipStream_t)stream) : launch_forward<true>(a, (hipStream_t)stream);
+}
+
+int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables, const eg_overlay* overlays,
+               const int64_t* tokens, int64_t n_pos, int64_t seq_len, const int32_t* seg_start,
+               const uint16_t* residual, void* out, int32_t* rows_out, void* stream) {
+  return forward_entry(n_layers, specs, tables, overlays, tokens, n_pos, seq_len, seg_start, 0, residual, out,
+                       rows_out, stream);
+}
+
+int eg_forward_decode(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,
+                      const eg_overlay* overlays, const int64_t* tokens, int64_t n_seq, int32_t ctx_len,
+                      const uint16_t* residual, void* out, int32_t* rows_out, void* stream) {
+  EG_CHECK_ARG(ctx_len >= 1, "ctx_len=%d < 1", ctx_len);
+  return forward_entry(n_layers, specs, tables, overlays, tokens, n_seq, 0, nullptr, ctx_len, residual, out,
+                       rows_out, stream);
 }
 
 int eg_forward_timed(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,
@@ -468,7 +505,8 @@ int eg_lookup_rows(const int32_t* rows, int64_t n, const int32_t* ids, const int
 int eg_gather_slots(const eg_table* table, const int32_t* rows, const int32_t* slot_var, int64_t n_pos,
                     int32_t heads, const float* vars, int64_t n_vars, float* out, void* stream) {
   EG_CHECK_ARG(heads >= 1 && heads <= EG_MAX_HEADS, "heads=%d outside [1, %d]", heads, EG_MAX_HEADS);
-  EG_CHECK_ARG(n_pos >= 0 && n_vars >= 0, "n_pos=%lld n_vars=%lld", (long long)n_pos, (long long)n_vars);
+  EG_CHECK_ARG(n_pos >= 0 && n_pos < (1LL << 30) && n_vars >= 0, "n_pos=%lld n_vars=%lld", (long long)n_pos,
+               (long long)n_vars);
   EG_CHECK_ARG(n_pos == 0 || (rows != nullptr && slot_var != nullptr && out != nullptr),
                "rows/slot_var/out is NULL");
   EG_CHECK_ARG(n_vars == 0 || vars != nullptr, "vars is NULL");
@@ -488,15 +526,14 @@ int eg_gather_slots(const eg_table* table, const int32_t* rows, const int32_t* s
   a.heads = heads;
   a.dim = table->dim;
   const int W = heads * a.dim;
-  EG_CHECK_ARG(W <= 512 * kMaxChunks, "row width %d > %d", W, 512 * kMaxChunks);
-  a.nch = (W + 511) / 512;
+  EG_CHECK_ARG(W <= kMaxWidth, "row width %d > %d", W, kMaxWidth);
   return launch_forward<true>(a, (hipStream_t)stream);
 }
 
 int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* rows, int64_t n_pos, int32_t heads,
               float* out, void* stream) {
   EG_CHECK_ARG(heads >= 1 && heads <= EG_MAX_HEADS, "heads=%d outside [1, %d]", heads, EG_MAX_HEADS);
-  EG_CHECK_ARG(n_pos >= 0, "n_pos < 0");
+  EG_CHECK_ARG(n_pos >= 0 && n_pos < (1LL << 30), "n_pos=%lld outside [0, 2^30)", (long long)n_pos);
   EG_CHECK_ARG(n_pos == 0 || (rows != nullptr && out != nullptr), "rows/out is NULL");
   FwdArgs a;
   memset(&a, 0, sizeof(a));
@@ -511,8 +548,7 @@ int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* r
   a.heads = heads;
   a.dim = table->dim;
   const int W = heads * a.dim;
-  EG_CHECK_ARG(W <= 512 * kMaxChunks, "row width %d > %d", W, 512 * kMaxChunks);
-  a.nch = (W + 511) / 512;
+  EG_CHECK_ARG(W <= kMaxWidth, "row width %d > %d", W, kMaxWidth);
   return launch_forward<true>(a, (hipStream_t)stream);
 }
 

@@ -347,13 +347,19 @@ class PreparedForward:
 
     def __init__(self, tables: list[DeviceTable], tokens, residual: torch.Tensor | None = None, *,
                  out: torch.Tensor | None = None, overlays=None, seq_len: int | None = None, seg_start=None,
-                 return_rows: bool = False):
+                 return_rows: bool = False, decode_ctx: int | None = None):
         if not 1 <= len(tables) <= _lib.EG_MAX_LAYERS:
             raise ValueError(f"{len(tables)} table layers (1..{_lib.EG_MAX_LAYERS} supported)")
         t0 = tables[0]
         dev = t0.device
         tok = _tokens_tensor(tokens, dev)
         n = tok.numel()
+        if decode_ctx is not None:
+            if decode_ctx < 1 or n % decode_ctx != 0:
+                raise ValueError(f"{n} tokens are not [n_seq, {decode_ctx}]")
+            if seq_len is not None or seg_start is not None:
+                raise ValueError("decode: every sequence is its own segment (no seq_len / seg_start)")
+            n //= decode_ctx
         w = t0.n_heads * t0.row_len
         if residual is not None:
             if residual.dtype != torch.bfloat16 or residual.device != dev:
@@ -379,9 +385,15 @@ class PreparedForward:
         self.rows = torch.empty((nl, n, t0.n_heads), dtype=torch.int32, device=dev) if return_rows else None
         self.out = out
         self._keep = (tables, tok, residual, seg)
-        self._fn = _lib.load().eg_forward
-        self._args = (nl, self._specs, self._ctabs, self._ovs, _lib.ptr(tok), n, int(seq_len or 0), _lib.ptr(seg),
-                      _lib.ptr(residual), _lib.ptr(out), _lib.ptr(self.rows))
+        if decode_ctx is None:
+            self._fn = _lib.load().eg_forward
+            self._args = (nl, self._specs, self._ctabs, self._ovs, _lib.ptr(tok), n, int(seq_len or 0),
+                          _lib.ptr(seg), _lib.ptr(residual), _lib.ptr(out), _lib.ptr(self.rows))
+        else:
+            self._fn = _lib.load().eg_forward_decode
+            self._args = (nl, self._specs, self._ctabs, self._ovs, _lib.ptr(tok), n, int(decode_ctx),
+                          _lib.ptr(residual), _lib.ptr(out), _lib.ptr(self.rows))
+        self._decode = decode_ctx is not None
         self.device = dev
         self.n_positions = n
 
@@ -394,6 +406,8 @@ class PreparedForward:
     def timed(self, start_event: int, stop_event: int, stream: int | None = None) -> None:
         """The same launch through ``eg_forward_timed``: the two hipEvent_t
         handles receive the kernel dispatch's own start / end timestamps."""
+        if self._decode:
+            raise ValueError("timed launches are for eg_forward")
         st = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
         rc = _lib.load().eg_forward_timed(*self._args, start_event, stop_event, st)
         if rc != _lib.EG_OK:
@@ -409,6 +423,21 @@ def forward(tables: list[DeviceTable], tokens, residual: torch.Tensor | None = N
     ``[n_layers, n, n_heads]`` with ``return_rows``)."""
     call = PreparedForward(tables, tokens, residual, out=out, overlays=overlays, seq_len=seq_len,
                            seg_start=seg_start, return_rows=return_rows)
+    call()
+    return (call.out, call.rows) if return_rows else call.out
+
+
+def forward_decode(tables: list[DeviceTable], tokens, residual: torch.Tensor | None = None, *,
+                   out: torch.Tensor | None = None, overlays=None, return_rows: bool = False):
+    """One decode step: ``tokens`` int ``[n_seq, ctx]`` (each sequence's last
+    ``ctx`` tokens, the new one last), ``residual`` bf16 ``[n_seq, W]``: the
+    embedding of every sequence's new position added into its residual
+    (overlays resolved per id).  Returns ``out`` (and the row ids)."""
+    tok = tokens if isinstance(tokens, torch.Tensor) else torch.as_tensor(np.asarray(tokens, dtype=np.int64))
+    if tok.dim() != 2:
+        raise ValueError("decode tokens must be [n_seq, ctx]")
+    call = PreparedForward(tables, tok, residual, out=out, overlays=overlays, return_rows=return_rows,
+                           decode_ctx=int(tok.shape[1]))
     call()
     return (call.out, call.rows) if return_rows else call.out
 

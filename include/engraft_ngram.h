@@ -119,6 +119,17 @@ int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tabl
                int64_t seq_len, const int32_t* seg_start, const uint16_t* residual,
                void* out, int32_t* rows_out, void* stream);
 
+/* Decode step: one new position per sequence.  tokens int64 [n_seq, ctx_len]
+ * holds each sequence's last ctx_len tokens (the new one last; the hash never
+ * looks before the first); residual / out / rows_out as eg_forward with
+ * n_pos = n_seq: the embedding of every sequence's last position
+ * (engraft/replica/model.py:473-495 at t = the new token; the engine's
+ * per-token gather with the overlay resolved per id). */
+int eg_forward_decode(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,
+                      const eg_overlay* overlays, const int64_t* tokens, int64_t n_seq,
+                      int32_t ctx_len, const uint16_t* residual, void* out, int32_t* rows_out,
+                      void* stream);
+
 /* eg_forward with the kernel launched through hipExtLaunchKernelGGL, so that
  * start_event / stop_event (hipEvent_t, created by the caller) hold the
  * dispatch's own start and end timestamps.  No counterpart in the reference:

@@ -59,3 +59,5 @@ CFG0 = dict(n_rows=4_194_304, dim=128, fmt="bf16", batch=1, seq=2048, vocab=151_
 CFG1 = dict(n_rows=320_000_000, dim=128, fmt="q8_0", batch=8, seq=2048, vocab=151_936, width=2048, sigma=0.02)
 CFG4 = dict(n_rows=160_000_000, dim=128, fmt="mxfp8", batch=1, seq=32_768, vocab=129_280, width=3072, sigma=0.02,
             layers=2, ngram_size=4)
+CFG3 = dict(n_rows=320_000_000, dim=128, fmt="q8_0", n_seq=256, ctx=3, overlay_rows=500_000, vocab=151_936,
+            width=2048, sigma=0.02)

@@ -16,7 +16,7 @@ from oracle import forward as FW
 from oracle import hash as H
 from oracle import synth
 from tests import gpu_util as G
-from tests.params import CFG0, CFG1, fake_table_spec, reference_corpus, synthetic_spec, tiny_hparams_spec
+from tests.params import CFG0, CFG1, CFG3, CFG4, fake_table_spec, reference_corpus, synthetic_spec, tiny_hparams_spec
 
 pytestmark = pytest.mark.gpu
 
@@ -225,4 +225,102 @@ def test_forward_config1_full_size(cuda):
     got_hi = tab.store.payload[hi].cpu().numpy()
     assert np.array_equal(got_hi, synth.synth_rows("q8_0", 201, hi, 128, 0.02)[0].view(np.uint8))
     del tab, out, rows, res
+    torch.cuda.empty_cache()
+
+
+def _q8_overlay(ids: np.ndarray, seed: int, dim: int = 128):
+    """A seeded Q8_0 overlay store for sorted ``ids`` (row k = synthetic row k of
+    ``seed``) and its oracle rows."""
+    from engraft_ngram_amd import table as T
+    from engraft_ngram_amd.overlay import DeviceOverlay
+    store = T.RowStore.empty("q8_0", ids.size, dim, "cuda:0")
+    T.fill_synthetic(store, seed=seed, sigma=0.02)
+    ov = DeviceOverlay(torch.from_numpy(ids.astype(np.int32)).cuda(), store)
+    return ov, (lambda k: synth.synth_dequant("q8_0", seed, np.asarray(k), dim, 0.02))
+
+
+def _decode_expect(spec, tok2d, fetch, ov_ids, ov_fetch, res_bits):
+    """Oracle of one decode step: each sequence hashed alone, its last position."""
+    n_seq, ctx = tok2d.shape
+    rows, emb, _ = FW.forward(spec, tok2d.reshape(-1), fetch, seq_len=ctx)
+    rows, emb = rows[ctx - 1::ctx], emb[ctx - 1::ctx]
+    hit = np.isin(ov_ids, rows)
+    emb, _ = FW.substitute(emb, rows, ov_ids[hit], ov_fetch(np.flatnonzero(hit)))
+    return rows, FW.residual_add(res_bits, [emb])
+
+
+def test_decode_with_overlay_config3_shape(cuda):
+    """BASELINE config 3's shape on a 1.6M-row table: 256 sequences x (2 context
+    tokens + 1 new), a 500,000-row Q8_0 overlay resolved per id; the decode step
+    equals the oracle and the full forward's last positions."""
+    from engraft_ngram_amd import table as T
+    c = CFG3
+    spec = synthetic_spec(n_rows=16 * 100_000, seed=61)
+    tab = G.device_table(spec, "q8_0", 16 * 100_000, 128, seed=62)
+    rng = np.random.default_rng(63)
+    ov_ids = np.sort(rng.choice(16 * 100_000, size=c["overlay_rows"], replace=False))
+    ov, ov_fetch = _q8_overlay(ov_ids, seed=64)
+    tok = synth.zipf_tokens(65, c["n_seq"] * c["ctx"], c["vocab"]).reshape(c["n_seq"], c["ctx"])
+    tok[::7, 0] = 151_643  # some sequences open with EOS in their context
+    res = G.residual(c["n_seq"], c["width"], seed=66)
+    out, rows = T.forward_decode([tab], torch.from_numpy(tok), res, overlays=[ov], return_rows=True)
+    exp_rows, exp_out = _decode_expect(spec, tok, G.synth_fetch("q8_0", 62, 128), ov_ids, ov_fetch,
+                                       G.bf16_bits(res))
+    assert np.array_equal(rows[0].cpu().numpy(), exp_rows)
+    assert np.isin(exp_rows, ov_ids).any()  # the overlay was exercised
+    G.assert_out_matches(G.bf16_bits(out), exp_out)
+    # the same as the full forward over the flattened sequences, last positions
+    res_full = torch.zeros((tok.size, c["width"]), dtype=torch.bfloat16, device=cuda)
+    res_full[c["ctx"] - 1::c["ctx"]] = res
+    full = tab.forward(torch.from_numpy(tok.reshape(-1)), res_full, overlay=ov, seq_len=c["ctx"])
+    assert torch.equal(full[c["ctx"] - 1::c["ctx"]], out)
+
+
+def test_decode_config3_full_size(cuda):
+    """BASELINE config 3 at its own size: the 320M-row config-1 table plus a
+    500,000-row overlay, 256 sequences x 3 tokens."""
+    from engraft_ngram_amd import table as T
+    _say("decode cfg3 (43.5 GB table + 500k overlay)")
+    c = CFG3
+    spec = synthetic_spec(n_rows=c["n_rows"], seed=200)
+    tab = G.device_table(spec, "q8_0", c["n_rows"], 128, seed=201)
+    ov_ids = np.unique(np.random.default_rng(300).integers(0, c["n_rows"], size=c["overlay_rows"] + 2000))
+    ov_ids = ov_ids[:c["overlay_rows"]]
+    tok = synth.zipf_tokens(302, c["n_seq"] * c["ctx"], c["vocab"]).reshape(c["n_seq"], c["ctx"])
+    rows_all = H.ngram_rows_np(spec, tok.reshape(-1), seq_len=c["ctx"])[c["ctx"] - 1::c["ctx"]]
+    ov_ids = np.unique(np.concatenate([ov_ids[:-200], rows_all.reshape(-1)[:200]]))  # some ids are read
+    ov, ov_fetch = _q8_overlay(ov_ids, seed=301)
+    res = G.residual(c["n_seq"], c["width"], seed=303)
+    out, rows = T.forward_decode([tab], torch.from_numpy(tok), res, overlays=[ov], return_rows=True)
+    exp_rows, exp_out = _decode_expect(spec, tok, G.synth_fetch("q8_0", 201, 128), ov_ids, ov_fetch,
+                                       G.bf16_bits(res))
+    assert np.array_equal(rows[0].cpu().numpy(), exp_rows)
+    G.assert_out_matches(G.bf16_bits(out), exp_out)
+    del tab, ov
+    torch.cuda.empty_cache()
+
+
+def test_forward_config4_full_size(cuda):
+    """BASELINE config 4 at its own size: 2 layers x 160,000,000 MXFP8 rows
+    (42.2 GB), 2-/3-/4-gram hashes (24 slots per layer), 32,768 Zipf tokens over
+    129,280, residual width 3,072.  Every row id is compared; the output on 4,096
+    sampled positions (the oracle regenerates those rows)."""
+    from engraft_ngram_amd import table as T
+    _say("forward cfg4 (2 x 21 GB MXFP8 tables)")
+    c = CFG4
+    specs = [synthetic_spec(n_rows=c["n_rows"], seed=400 + l, ngram_size=4) for l in range(2)]
+    tabs = [G.device_table(specs[l], "mxfp8", c["n_rows"], 128, seed=410 + l) for l in range(2)]
+    tokens = synth.zipf_tokens(420, c["seq"], c["vocab"])
+    res = G.residual(c["seq"], c["width"], seed=421)
+    out, rows = T.forward(tabs, torch.from_numpy(tokens), res, return_rows=True)
+    sample = np.sort(np.random.default_rng(422).choice(c["seq"], size=4096, replace=False))
+    sample[:2] = [0, 1]  # the EOS-padded first positions
+    embs = []
+    for l in range(2):
+        r = H.ngram_rows_np(specs[l], tokens)
+        assert np.array_equal(rows[l].cpu().numpy(), r)
+        embs.append(FW.gather(r[sample], G.synth_fetch("mxfp8", 410 + l, 128)))
+    got = G.bf16_bits(out)[sample]
+    G.assert_out_matches(got, FW.residual_add(G.bf16_bits(res)[sample], embs))
+    del tabs, out, rows, res
     torch.cuda.empty_cache()
