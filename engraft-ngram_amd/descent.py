@@ -187,11 +187,12 @@ class DescentState:
 # Row variables (engraft/replica/distill.py:378-453)
 # ---------------------------------------------------------------------------------------------
 
-def _read_true_rows(table: DeviceTable, rows_global) -> np.ndarray:
-    """TRUE (dequantised) rows for global row ids in any order, f32 ``[n, row_len]``
-    (``engraft/replica/distill.py:378-395``); ``ValueError`` for an id outside
-    every head."""
-    g = np.asarray(list(rows_global), dtype=np.int64).reshape(-1)
+def true_rows_device(table: DeviceTable, rows_global) -> torch.Tensor:
+    """TRUE (dequantised) rows for global ids in any order, as a device f32
+    tensor ``[n, row_len]``; ``ValueError`` for an id outside every head
+    (``engraft/replica/distill.py:378-395``)."""
+    g = np.asarray(list(rows_global) if not isinstance(rows_global, np.ndarray) else rows_global,
+                   dtype=np.int64).reshape(-1)
     offsets = np.asarray(table.head_offsets, dtype=np.int64)
     ends = offsets + np.asarray(table.head_vocab_sizes, dtype=np.int64)
     h = np.clip(np.searchsorted(offsets, g, side="right") - 1, 0, len(offsets) - 1)
@@ -199,9 +200,13 @@ def _read_true_rows(table: DeviceTable, rows_global) -> np.ndarray:
     if bad.any():
         raise ValueError(f"_read_true_rows: global row {int(g[bad][0])} outside all heads")
     if g.size == 0:
-        return np.zeros((0, table.row_len), dtype=np.float32)
-    ids = torch.as_tensor(g.astype(np.int32), device=table.device).reshape(-1, 1)
-    return table.gather(ids).cpu().numpy()
+        return torch.zeros((0, table.row_len), dtype=torch.float32, device=table.device)
+    return table.gather(torch.as_tensor(g.astype(np.int32), device=table.device).reshape(-1, 1))
+
+
+def _read_true_rows(table: DeviceTable, rows_global) -> np.ndarray:
+    """``engraft/replica/distill.py:378-395``: the true rows as host f32 ``[n, row_len]``."""
+    return true_rows_device(table, rows_global).cpu().numpy()
 
 
 def build_rows_var(table: DeviceTable, sequences: list[list[int]], policy: str, row_sets: dict,

@@ -168,3 +168,45 @@ def test_scan_hits_against_oracle(cuda):
         for k in ("pos", "n_hit_rows", "dnorm_max", "read_count"):
             assert np.array_equal(got[k], exp[k]), k
         np.testing.assert_allclose(got["dnorm_sum"], exp["dnorm_sum"], rtol=1e-6)
+
+
+@pytest.mark.parametrize("n_files", [4, 40])
+def test_sum_overlays_against_oracle(cuda, tmp_path, n_files):
+    """engraft/replica/overlay_sum.py:38-112 on the device: the union, the
+    merged rows (bit-exact; 40 files put 40 deltas on one row, past the
+    32-slot sequential range) and the manifest; write_merged_pleo's order."""
+    from engraft_ngram_amd import lens, overlay_sum
+    from oracle import overlay_sum as OS
+    spec = synthetic_spec(n_rows=16 * 2000, seed=71)
+    tab = G.device_table(spec, "q8_0", 16 * 2000, 128, seed=72)
+    fetch = G.synth_fetch("q8_0", 72, 128)
+    rng = np.random.default_rng(73)
+    always = np.array([5, 7000, 31999])  # in every file
+    paths, files = [], []
+    for i in range(n_files):
+        rows = np.unique(np.concatenate([rng.choice(16 * 2000, size=int(rng.integers(20, 60)), replace=False),
+                                         always])).astype(np.int32)
+        data = (fetch(rows) + rng.standard_normal((rows.size, 128)) * 1e-2).astype(np.float32)
+        data[::4] = fetch(rows[::4])
+        path = tmp_path / f"f{i}.pleo"
+        lens.write_pleo(path, rows, data)
+        paths.append(path)
+        files.append((rows, data))
+    rows_u, merged, man = overlay_sum.sum_overlays(tab, paths)
+    e_rows, e_merged, e_man = OS.sum_overlays(files, fetch)
+    assert np.array_equal(rows_u, e_rows)
+    assert np.array_equal(merged, e_merged)
+    for k in ("n_files", "n_rows_union", "n_rows_moved_any", "n_rows_shared", "facts_per_row_histogram"):
+        assert man[k] == e_man[k], k
+    for k in ("shared_rows_sum_abs_norm_max", "shared_rows_abs_sum_norm_max", "max_row_delta_norm"):
+        assert man[k] == pytest.approx(e_man[k], rel=1e-9), k
+    r, d = overlay_sum.delta_for_pleo(tab, paths[0])
+    assert np.array_equal(d, (files[0][1] - fetch(files[0][0])).astype(np.float32))
+    # merged.pleo: variables in row_map order, then frozen rows ascending at true values
+    row_map = {int(e_rows[3]): 0, int(e_rows[1]): 1}
+    rv = torch.full((2, 128), 0.25)
+    info = overlay_sum.write_merged_pleo(tab, row_map, rv, e_rows[:10].tolist(), tmp_path / "merged.pleo")
+    got_rows, got_data = lens.read_pleo(tmp_path / "merged.pleo")
+    exp_rows, exp_data = OS.write_merged_rows(row_map, rv.numpy(), e_rows[:10].tolist(), fetch)
+    assert np.array_equal(got_rows, exp_rows) and np.array_equal(got_data, exp_data)
+    assert info["n_rows_frozen"] == 8

@@ -146,3 +146,55 @@ def test_scan_hits_reference_known_answer():
         assert np.array_equal(hits[k], one[k])
     rows = H.ngram_rows_np(spec, tokens)
     assert hits["read_count"].tolist() == [int((rows == g).sum()) for g in ov]
+
+
+def _files(rng, fetch, n_files, pool, dim=32, unchanged_every=3):
+    files = []
+    for i in range(n_files):
+        rows = np.sort(rng.choice(pool, size=int(rng.integers(5, 12)), replace=False)).astype(np.int32)
+        data = fetch(rows) + rng.standard_normal((rows.size, dim)).astype(np.float32) * 1e-2
+        data[::unchanged_every] = fetch(rows[::unchanged_every])  # rows the fact left untouched
+        files.append((rows, data.astype(np.float32)))
+    return files
+
+
+def test_overlay_sum_against_dict_loop():
+    """engraft/replica/overlay_sum.py:38-112 by a per-row dictionary loop:
+    union ascending, deltas added in file order, merged = true + sum; an
+    untouched row's delta is exactly zero and is not counted as moved."""
+    from oracle import overlay_sum as OS
+    data = np.random.default_rng(8).standard_normal((500, 32)).astype(np.float32) * 0.05
+    fetch = lambda ids: data[np.asarray(ids, np.int64)]
+    rng = np.random.default_rng(9)
+    files = _files(rng, fetch, 5, 40)
+    rows_u, merged, man = OS.sum_overlays(files, fetch)
+    acc: dict[int, np.ndarray] = {}
+    moved: dict[int, int] = {}
+    for rows, d in files:
+        for r, v in zip(rows.tolist(), d):
+            delta = (v - data[r]).astype(np.float32)
+            acc[r] = (acc.get(r, np.zeros(32, np.float32)) + delta).astype(np.float32)
+            if np.linalg.norm(delta.astype(np.float64)) > 0:
+                moved[r] = moved.get(r, 0) + 1
+    assert rows_u.tolist() == sorted(acc)
+    for i, r in enumerate(rows_u.tolist()):
+        assert np.array_equal(merged[i], (data[r] + acc[r]).astype(np.float32))
+    assert man["n_rows_moved_any"] == len(moved)
+    assert man["n_rows_shared"] == sum(1 for c in moved.values() if c >= 2)
+    assert sum(man["facts_per_row_histogram"].values()) == len(moved)
+    # one file alone: merged == true + (data - true), untouched rows bit-identical
+    r1, m1, man1 = OS.sum_overlays(files[:1], fetch)
+    assert np.array_equal(m1[::3], files[0][1][::3]) and man1["n_rows_shared"] == 0
+
+
+def test_write_merged_rows_order():
+    """engraft/descend_corpus.py:627-647: variables in row_map order, then the
+    frozen rows ascending at their true values (not globally sorted)."""
+    from oracle import overlay_sum as OS
+    data = np.arange(50 * 4, dtype=np.float32).reshape(50, 4)
+    fetch = lambda ids: data[np.asarray(ids, np.int64)]
+    row_map = {30: 0, 7: 1}
+    rv = np.full((2, 4), -1.0, np.float32)
+    rows, d = OS.write_merged_rows(row_map, rv, [3, 30, 12, 7, 3], fetch)
+    assert rows.tolist() == [30, 7, 3, 12]
+    assert np.array_equal(d[:2], rv) and np.array_equal(d[2:], data[[3, 12]])
