@@ -1,0 +1,105 @@
+"""A minimal GGUF reader for the PLE table file (host side).
+
+The reference opens its table with the ``gguf`` package's ``GGUFReader``
+(``engraft/table.py:50-88``), which is not available here; this module reads
+the same file layout from the published GGUF format (v2/v3, little endian):
+
+    magic b"GGUF", u32 version, u64 n_tensors, u64 n_kv
+    n_kv x (string key, u32 value type, value)
+    n_tensors x (string name, u32 n_dims, u64 dims[n_dims], u32 ggml type, u64 offset)
+    padding to general.alignment (default 32), then the tensor data
+
+with ``string = u64 length + UTF-8 bytes`` and array values ``u32 item type +
+u64 count + items``.  Only the metadata is parsed; tensor data stays in the
+file and is read by offset.
+"""
+from __future__ import annotations
+
+import dataclasses
+import struct
+from pathlib import Path
+
+GGUF_MAGIC = b"GGUF"
+GGML_TYPE_IQ4_NL = 20
+
+# value types: (struct code, size)
+_SCALARS = {0: ("<B", 1), 1: ("<b", 1), 2: ("<H", 2), 3: ("<h", 2), 4: ("<I", 4), 5: ("<i", 4), 6: ("<f", 4),
+            7: ("<?", 1), 10: ("<Q", 8), 11: ("<q", 8), 12: ("<d", 8)}
+_STRING, _ARRAY = 8, 9
+
+
+@dataclasses.dataclass(frozen=True)
+class TensorInfo:
+    name: str
+    shape: tuple[int, ...]  # ne0 first (ne0 = values per row)
+    ggml_type: int
+    data_offset: int        # absolute offset in the file
+
+
+class _Cursor:
+    def __init__(self, f):
+        self.f = f
+
+    def read(self, n: int) -> bytes:
+        b = self.f.read(n)
+        if len(b) != n:
+            raise ValueError("GGUF: unexpected end of file")
+        return b
+
+    def scalar(self, code: str, size: int):
+        return struct.unpack(code, self.read(size))[0]
+
+    def string(self) -> str:
+        n = self.scalar("<Q", 8)
+        return self.read(n).decode("utf-8")
+
+    def value(self, vtype: int):
+        if vtype in _SCALARS:
+            return self.scalar(*_SCALARS[vtype])
+        if vtype == _STRING:
+            return self.string()
+        if vtype == _ARRAY:
+            itype = self.scalar("<I", 4)
+            count = self.scalar("<Q", 8)
+            return [self.value(itype) for _ in range(count)]
+        raise ValueError(f"GGUF: unknown value type {vtype}")
+
+
+@dataclasses.dataclass
+class GGUFFile:
+    path: Path
+    version: int
+    fields: dict
+    tensors: dict[str, TensorInfo]
+    alignment: int
+
+
+def read_gguf(path: str | Path) -> GGUFFile:
+    """The metadata and tensor directory of a GGUF file."""
+    path = Path(path)
+    with open(path, "rb") as f:
+        c = _Cursor(f)
+        if c.read(4) != GGUF_MAGIC:
+            raise ValueError(f"{path}: not a GGUF file")
+        version = c.scalar("<I", 4)
+        if version not in (2, 3):
+            raise ValueError(f"{path}: GGUF version {version} (2 and 3 are read)")
+        n_tensors = c.scalar("<Q", 8)
+        n_kv = c.scalar("<Q", 8)
+        fields = {}
+        for _ in range(n_kv):
+            key = c.string()
+            fields[key] = c.value(c.scalar("<I", 4))
+        infos = []
+        for _ in range(n_tensors):
+            name = c.string()
+            n_dims = c.scalar("<I", 4)
+            dims = tuple(c.scalar("<Q", 8) for _ in range(n_dims))
+            gtype = c.scalar("<I", 4)
+            off = c.scalar("<Q", 8)
+            infos.append((name, dims, gtype, off))
+        alignment = int(fields.get("general.alignment", 32))
+        pos = f.tell()
+        data_start = (pos + alignment - 1) // alignment * alignment
+    tensors = {n: TensorInfo(n, d, t, data_start + o) for n, d, t, o in infos}
+    return GGUFFile(path, version, fields, tensors, alignment)

@@ -324,3 +324,35 @@ def test_forward_config4_full_size(cuda):
     G.assert_out_matches(got, FW.residual_add(G.bf16_bits(res)[sample], embs))
     del tabs, out, rows, res
     torch.cuda.empty_cache()
+
+
+def test_ple_table_from_gguf(cuda, tmp_path):
+    """PleTable(path) on a per-head IQ4_NL GGUF (engraft/table.py:40-109): the
+    hash parameters come from the metadata, read_rows_raw returns the file's
+    bytes, read_rows their IQ4_NL dequantisation, ngram_addresses the scalar
+    hash, and an all-zero-scale row reads as zero."""
+    from engraft_ngram_amd import table as T
+    from oracle import formats as F
+    from tests.gguf_util import ple_table_file
+    spec = fake_table_spec(5, head_vocab_size=300)
+    rng = np.random.default_rng(1)
+    raw = []
+    for h in range(16):
+        r = rng.integers(0, 256, size=(300, 90), dtype=np.uint8)
+        for b in range(5):  # finite fp16 scales
+            r[:, 18 * b:18 * b + 2] = np.frombuffer(
+                (rng.standard_normal(300) * 1e-3).astype(np.float16).tobytes(), np.uint8).reshape(300, 2)
+        raw.append(r)
+    raw[4][17, [0, 1, 18, 19, 36, 37, 54, 55, 72, 73]] = 0  # row 17 of head 4: zero scales
+    ple_table_file(tmp_path / "ple.gguf", spec, raw)
+    tab = T.PleTable(tmp_path / "ple.gguf")
+    assert tab.head_offsets == list(spec.head_offsets) and tab.layer_multipliers == list(spec.layer_multipliers)
+    assert tab.image_token_id == 151_655
+    for h in (0, 4, 15):
+        assert np.array_equal(tab.read_rows_raw(h, 10, 50), raw[h][10:60])
+        np.testing.assert_array_equal(tab.read_rows(h, 10, 50), F.dequant_iq4nl(raw[h][10:60]))
+    assert T.row_is_zero(tab.read_rows_raw(4, 17, 1))[0] and not tab.read_rows(4, 17, 1).any()
+    tokens = [1, 2, 3, spec.eos_token_id, 9, 9]
+    assert tab.ngram_addresses(tokens) == H.ngram_addresses_scalar(spec, tokens)
+    with pytest.raises(AssertionError):
+        tab.read_rows_raw(0, 299, 2)

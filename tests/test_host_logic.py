@@ -108,3 +108,31 @@ def test_iter_blocks_overlap():
     blocks = list(damage.iter_blocks(toks, block=4))
     assert [o for o, _ in blocks] == [0, 4, 8]
     assert [b.tolist() for _, b in blocks] == [[0, 1, 2, 3], [2, 3, 4, 5, 6, 7], [6, 7, 8, 9]]
+
+
+def test_gguf_reader_layout(tmp_path):
+    """The GGUF directory as the published format lays it out: typed metadata
+    (scalars, strings, arrays), tensor dims ne0-first, data offsets aligned to
+    general.alignment and pointing at each tensor's bytes."""
+    from engraft_ngram_amd.ggufio import read_gguf
+    from tests.gguf_util import ple_table_file
+    from tests.params import fake_table_spec
+
+    spec = fake_table_spec(3, head_vocab_size=7)
+    rng = np.random.default_rng(0)
+    raw = [rng.integers(0, 256, size=(7, 90), dtype=np.uint8) for _ in range(16)]
+    offs = ple_table_file(tmp_path / "t.gguf", spec, raw)
+    g = read_gguf(tmp_path / "t.gguf")
+    assert g.version == 3 and g.alignment == 32
+    assert g.fields["general.architecture"] == "qwen4exp"
+    assert g.fields["qwen4exp.ple.layer_multipliers"] == list(spec.layer_multipliers)
+    assert g.fields["qwen4exp.ple.head_offsets"] == list(spec.head_offsets)
+    data = (tmp_path / "t.gguf").read_bytes()
+    for h in range(16):
+        t = g.tensors[f"ple_ngram_embd.{h}.weight"]
+        assert t.shape == (160, 7) and t.ggml_type == 20 and t.data_offset == offs[h]
+        assert t.data_offset % 32 == 0
+        assert data[t.data_offset:t.data_offset + 630] == raw[h].tobytes()
+    (tmp_path / "bad.gguf").write_bytes(b"GGML" + b"\0" * 40)
+    with pytest.raises(ValueError):
+        read_gguf(tmp_path / "bad.gguf")
