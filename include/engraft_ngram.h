@@ -27,6 +27,10 @@
  *                                                    engraft/replica/seq.py:372-444
  *   eg_descent_step  scatter + torch.optim.Adam step on the overlay rows
  *                                                    engraft/descend_corpus.py:785-790,921-947
+ *   eg_forward_decode  the per-token gather of a decode step with the overlay
+ *                                                    engraft/replica/model.py:473-495
+ *   eg_ple_gate, eg_ple_conv  ple_forward after its two projections
+ *                                                    engraft/replica/layers.py:565-626
  */
 #ifndef ENGRAFT_NGRAM_H
 #define ENGRAFT_NGRAM_H
@@ -233,6 +237,26 @@ int eg_scatter_grad_slots(const void* d_out, int32_t d_out_f32, const int32_t* s
  * smallest shared exponent e that keeps amax*2^-e <= 448). */
 int eg_synth_table(const eg_table* table, uint64_t seed, const float* qtable,
                    int64_t row0, int64_t n_rows, void* stream);
+
+/* ---- the PLE block consuming the rows (engraft/replica/layers.py:565-626) --
+ * After the projections key = emb @ w_key^T [n_pos, hc*n_embd] and
+ * value = emb @ w_value^T [n_pos, n_embd] (library GEMMs), per position and
+ * stream j: RMS norms of key_j (norm_key) and hidden_j (norm_query),
+ * s = <key_j^, hidden_j^> / sqrt(n_embd), gate = sigmoid(sign(s) sqrt(max(|s|, 1e-6))),
+ * gated_j = value * gate, normed_j = rmsnorm(gated_j) * norm_conv.
+ * normed f32 [n_pos, hc*n_embd]; s_out, gate_out f32 [n_pos, hc]. */
+int eg_ple_gate(const float* key, const float* value, const float* hidden, const float* norm_key,
+                const float* norm_query, const float* norm_conv, int64_t n_pos, int32_t hc,
+                int32_t n_embd, float eps, float* normed, float* s_out, float* gate_out,
+                void* stream);
+
+/* out = (hidden + value*gate) + silu(conv), conv[t, c] = sum_k conv_w[c, k] *
+ * full[hist_rows + t - (taps-1-k)*dilation, c] over the rows that exist
+ * (causal_depthwise_conv, layers.py:257-293); full f32 [hist_rows + n_pos,
+ * hc*n_embd] = [history; normed]; conv_w f32 [hc*n_embd, taps]. */
+int eg_ple_conv(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
+                const float* conv_w, int32_t taps, int32_t dilation, const float* hidden,
+                const float* value, const float* gate, float* out, void* stream);
 
 #ifdef __cplusplus
 }

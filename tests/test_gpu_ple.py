@@ -1,0 +1,85 @@
+"""GPU parity of the PLE block (ple_forward) against the torch fp32 oracle on
+the CPU: the real dimensions (hc 4, n_embd 2560, 4 taps, dilation 3),
+a sequence in two chunks with the history carried, and the gradient.
+
+Bar (floating point, as the reference's own check of its two formulations,
+tests/test_replica_layers.py:282): |out - oracle| <= 1e-4; history 1e-5;
+gradients within 1e-4 relative of the largest entry."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ple as P
+from tests.test_oracle_ple import ple_weights
+
+pytestmark = pytest.mark.gpu
+
+
+class _HP:
+    hc_mult = 4
+    n_embd = 2560
+    f_norm_rms_eps = 1e-6
+    ple_ngram_size = 3
+
+
+def _dev_weights(w, dev):
+    from engraft_ngram_amd.ple import PleWeights
+    return PleWeights(**{k: v.to(dev) for k, v in w.items()})
+
+
+def test_ple_forward_against_oracle(cuda):
+    from engraft_ngram_amd import ple
+    print("[gpu-test] ple_forward", file=sys.stderr, flush=True)
+    hc, n, T = 4, 2560, 48
+    w = ple_weights(hc, n, seed=3)
+    wd = _dev_weights(w, cuda)
+    g = torch.Generator().manual_seed(4)
+    emb = torch.randn((T, n), generator=g) * 0.1
+    hidden = torch.randn((T, hc, n), generator=g) * 0.1
+    # two chunks, the history of the first fed to the second
+    hist_c = torch.zeros(0, hc, n)
+    hist_d = torch.zeros(0, hc, n, device=cuda)
+    diag = {}
+    for lo, hi in ((0, 30), (30, T)):
+        exp, hist_c, s_c, gate_c = P.ple_forward(emb[lo:hi], hidden[lo:hi], w, hist_c, hc, n, 1e-6, 3)
+        got, hist_d = ple.ple_forward(emb[lo:hi].to(cuda), hidden[lo:hi].to(cuda), wd, hist_d, _HP, diag=diag)
+        err = (got.cpu() - exp).abs().max().item()
+        assert err <= 1e-4, f"chunk [{lo},{hi}): max |diff| {err}"
+        assert torch.allclose(hist_d.cpu(), hist_c, atol=1e-5)
+        assert torch.allclose(diag["gate"].cpu(), gate_c, atol=1e-5)
+        assert torch.allclose(diag["s"].cpu(), s_c, atol=1e-4)
+    assert hist_d.shape == (9, hc, n)
+
+
+def test_ple_forward_gradient(cuda):
+    """d(sum(out * R))/d(emb, hidden) against torch autograd of the oracle on the
+    CPU; detach_gate keeps only the value path's share of the emb gradient."""
+    from engraft_ngram_amd import ple
+    hc, n, T = 4, 2560, 12
+    w = ple_weights(hc, n, seed=5)
+    wd = _dev_weights(w, cuda)
+    g = torch.Generator().manual_seed(6)
+    emb = torch.randn((T, n), generator=g) * 0.1
+    hidden = torch.randn((T, hc, n), generator=g) * 0.1
+    r = torch.randn((T, hc, n), generator=g)
+    e_c = emb.clone().requires_grad_(True)
+    h_c = hidden.clone().requires_grad_(True)
+    out_c, _, _, _ = P.ple_forward(e_c, h_c, w, torch.zeros(0, hc, n), hc, n, 1e-6, 3)
+    (out_c * r).sum().backward()
+    e_d = emb.to(cuda).requires_grad_(True)
+    h_d = hidden.to(cuda).requires_grad_(True)
+    out_d, _ = ple.ple_forward(e_d, h_d, wd, torch.zeros(0, hc, n, device=cuda), _HP)
+    (out_d * r.to(cuda)).sum().backward()
+    for got, exp in ((e_d.grad, e_c.grad), (h_d.grad, h_c.grad)):
+        scale = exp.abs().max().item()
+        assert (got.cpu() - exp).abs().max().item() <= 1e-4 * scale
+    # detach_gate: forward unchanged, the gate's share of the gradient removed
+    e2 = emb.to(cuda).requires_grad_(True)
+    out2, _ = ple.ple_forward(e2, hidden.to(cuda), wd, torch.zeros(0, hc, n, device=cuda), _HP, detach_gate=True)
+    assert torch.equal(out2, out_d.detach())
+    (out2 * r.to(cuda)).sum().backward()
+    assert not torch.allclose(e2.grad, e_d.grad)
