@@ -31,7 +31,7 @@ HBM_PEAK_GBS = 8000.0
 
 N_ROWS, DIM, BATCH, SEQ, VOCAB, WIDTH, SLOTS = 320_000_000, 128, 8, 2048, 151_936, 2048, 16
 TABLE_SEED, HASH_SEED, TOKEN_SEED, RES_SEED = 201, 200, 202, 203
-DECODE_SEED, C4_SEED = 300, 400
+DECODE_SEED, C4_SEED, PLE_SEED = 300, 400, 500
 Q8_ROW_BYTES = DIM + 2 * DIM // 32  # 128 B int8 + 4 fp16 scales = 136 B
 
 
@@ -256,6 +256,44 @@ def bench_config4(steps: int, warmup: int) -> dict:
             "frac_of_hbm_peak": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": nbytes}
 
 
+def bench_ple(steps: int, warmup: int) -> dict:
+    """The PLE block consuming the rows (engraft/replica/layers.py:565-626) at
+    the real model's dimensions: 2048 positions, 4 hyper-connection streams,
+    n_embd 2560, 4 conv taps with dilation 3; seeded random weights; fp32."""
+    import torch
+
+    from engraft_ngram_amd import ple
+
+    class HP:
+        hc_mult, n_embd, f_norm_rms_eps, ple_ngram_size = 4, 2560, 1e-6, 3
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(PLE_SEED)
+    hc, n, t_len = 4, 2560, 2048
+    rnd = lambda *shape, sc=1.0: torch.randn(shape, generator=g, device=dev) * sc
+    w = ple.PleWeights(w_key=rnd(hc * n, n, sc=n ** -0.5), w_value=rnd(n, n, sc=n ** -0.5),
+                       norm_key=1 + rnd(hc * n, sc=0.1), norm_query=1 + rnd(hc * n, sc=0.1),
+                       norm_conv=1 + rnd(hc * n, sc=0.1), conv1d=rnd(hc * n, 4, sc=0.5))
+    emb, hidden = rnd(t_len, n, sc=0.1), rnd(t_len, hc, n, sc=0.1)
+    hist = torch.zeros(0, hc, n, device=dev)
+    with torch.no_grad():
+        for _ in range(warmup):
+            ple.ple_forward(emb, hidden, w, hist, HP)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            ple.ple_forward(emb, hidden, w, hist, HP)
+        b.record()
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    flops = 2.0 * t_len * n * (hc * n + n)
+    return {"workload": "ple_forward: T 2048, hc 4, n_embd 2560, 4 taps, dilation 3, fp32 (key/value GEMMs on "
+                        "hipBLASLt through torch.matmul, gate/norm and conv in HIP)",
+            "us_per_step": ms * 1e3, "gemm_tflops": flops / (ms * 1e-3) / 1e12,
+            "fp32_mfma_peak_tflops": 157.3}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -392,6 +430,9 @@ def main() -> None:
         result["forward_config4"] = c4
         log(f"forward (config 4): {c4['us_per_launch']:.1f} us/launch, {c4['gb_per_s']:.0f} GB/s algorithmic "
             f"({100 * c4['frac_of_hbm_peak']:.1f}% of peak)")
+        pl = bench_ple(max(1, args.steps // 10), 3)
+        result["ple_forward"] = pl
+        log(f"ple_forward: {pl['us_per_step']:.0f} us/step, GEMMs at {pl['gemm_tflops']:.1f} TFLOP/s fp32")
 
     if not args.no_cpu:
         cb = cpu_baseline(hp, tokens_np, res[0].cpu(), args.cpu_seconds)
