@@ -100,16 +100,28 @@ __device__ inline void load_head_mult(const LayerHash& L, int h, uint64_t m[EG_M
   }
 }
 
-// Global (or local) row of head h from its context and multipliers.
+// The modulus constants of head h (kernel-argument arrays indexed per lane are
+// memory loads: a kernel loads them ahead of use, like the multipliers).
+struct HeadConst {
+  uint64_t magic;
+  uint32_t vocab;
+  int32_t offset;
+};
+
+__device__ inline HeadConst load_head_const(const LayerHash& L, int h) {
+  return HeadConst{L.magic[h], L.vocab[h], L.offset[h]};
+}
+
+// Global (or local) row of head h from its context, multipliers and constants.
 __device__ inline int32_t row_of(const LayerHash& L, int h, const uint64_t ctx[EG_MAX_NGRAM],
-                                 const uint64_t m[EG_MAX_NGRAM], bool global_ids) {
+                                 const uint64_t m[EG_MAX_NGRAM], const HeadConst& hc, bool global_ids) {
   const int order = 2 + h / L.heads_per_ngram;
   uint64_t mixed = 0;
 #pragma unroll
   for (int j = 0; j < EG_MAX_NGRAM; ++j)
     if (j < order) mixed ^= ctx[j] * m[j];
-  const uint32_t local = fastmod_u64(mixed, L.vocab[h], L.magic[h]);
-  return global_ids ? L.offset[h] + (int32_t)local : (int32_t)local;
+  const uint32_t local = fastmod_u64(mixed, hc.vocab, hc.magic);
+  return global_ids ? hc.offset + (int32_t)local : (int32_t)local;
 }
 
 // Global row of head h: offset + (XOR_{j<order} ctx[j]*m[j]) mod vocab.
@@ -117,7 +129,7 @@ __device__ inline int32_t head_row(const LayerHash& L, int h, const uint64_t ctx
                                    bool global_ids) {
   uint64_t m[EG_MAX_NGRAM];
   load_head_mult(L, h, m);
-  return row_of(L, h, ctx, m, global_ids);
+  return row_of(L, h, ctx, m, load_head_const(L, h), global_ids);
 }
 
 // Segment start of flat position p.

@@ -138,7 +138,12 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   const int cb = (int)(wid - pu * parts) * (NCH * 512);  // first column of this wavefront
   const int h_lo = cb / dim;                                // first head it touches
   const int nh = min(H, (cb + NCH * 512 + dim - 1) / dim) - h_lo;  // heads it touches
-  const int hh = h_lo + lane;                               // the head lane < nh hashes
+  // Lane `lane` hashes head hh; the lanes past the heads this wavefront touches
+  // repeat its last head, so every load below is issued by every lane without
+  // a branch (a load inside a lane-divergent branch is waited for inside it,
+  // which would serialise the wavefront's loads).
+  const bool own_head = lane < nh;
+  const int hh = h_lo + min(lane, nh - 1);
 
   // 1. Everything the row ids depend on (tokens, segment start, multipliers,
   //    or the caller's row ids) is loaded first: vmcnt retires loads in issue
@@ -146,68 +151,70 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   const int nl = a.n_layers;
   uint64_t raw[EG_MAX_NGRAM];
   uint64_t mult[EG_MAX_LAYERS][EG_MAX_NGRAM];
+  HeadConst hconst[EG_MAX_LAYERS];
   int64_t seg0 = 0;
   int64_t tp = p;  // index of position p's own token
   int32_t rid[EG_MAX_LAYERS] = {0, 0};
   static_assert(MAXL >= 1 && MAXL <= EG_MAX_LAYERS, "layer count");
-  const bool hashing = a.rows_in == nullptr;
-  if (lane < nh) {
-    if (hashing) {
-      tp = a.decode_ctx > 0 ? p * a.decode_ctx + (a.decode_ctx - 1) : p;
-      seg0 = a.decode_ctx > 0 ? p * a.decode_ctx : seg_start_of(p, a.seq_len, a.seg_start);
-      int ng = a.hash[0].ngram_size;
-      if (MAXL > 1 && nl > 1 && a.hash[1].ngram_size > ng) ng = a.hash[1].ngram_size;
-      load_ctx_tokens(a.tokens, tp, ng, raw);
+  const bool hashing = a.rows_in == nullptr;  // uniform
+  if (hashing) {
+    tp = a.decode_ctx > 0 ? p * a.decode_ctx + (a.decode_ctx - 1) : p;
+    seg0 = a.decode_ctx > 0 ? p * a.decode_ctx : seg_start_of(p, a.seq_len, a.seg_start);
+    int ng = a.hash[0].ngram_size;
+    if (MAXL > 1 && nl > 1 && a.hash[1].ngram_size > ng) ng = a.hash[1].ngram_size;
+    load_ctx_tokens(a.tokens, tp, ng, raw);
 #pragma unroll
-      for (int l = 0; l < MAXL; ++l)
-        if (l < nl) load_head_mult(a.hash[l], hh, mult[l]);
-    } else {
-      rid[0] = a.rows_in[p * H + hh];
-    }
+    for (int l = 0; l < MAXL; ++l)
+      if (l < nl) {
+        load_head_mult(a.hash[l], hh, mult[l]);
+        hconst[l] = load_head_const(a.hash[l], hh);
+      }
+  } else {
+    rid[0] = a.rows_in[p * H + hh];
   }
 
-  // 2. The residual stream is read once: streaming (non-temporal) loads.
+  // 2. The residual stream is read once: streaming (non-temporal) loads, issued
+  //    by every lane (a lane past W re-reads the last chunk and stores nothing).
+  //    Without a residual (F32OUT) the sum starts from -0: -0 + x == x for every x.
   u32x4 res[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int e0 = cb + (lane + 64 * c) * 8;
-    if (a.residual != nullptr && e0 < W)
+    if constexpr (F32OUT) {
+      res[c] = u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+    } else {
+      const int e0 = min(cb + (lane + 64 * c) * 8, W - 8);
       res[c] = __builtin_nontemporal_load((const u32x4*)(a.residual + p * W + e0));
-    else
-      res[c] = u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};  // -0 + x == x for every x
+    }
   }
 
   // 3. Row ids of head hh, one per layer.
-  if (lane < nh && hashing) {
+  if (hashing) {
 #pragma unroll
     for (int l = 0; l < MAXL; ++l) {
       if (l < nl) {
         uint64_t ctx[EG_MAX_NGRAM];
         ctx_from(a.hash[l], raw, tp, seg0, ctx);
-        rid[l] = row_of(a.hash[l], hh, ctx, mult[l], true);
+        rid[l] = row_of(a.hash[l], hh, ctx, mult[l], hconst[l], true);
       }
     }
   }
   // 4. Issue the table (or overlay) row loads of every layer and chunk.  Row
   //    ids handed in by the caller (gather mode) and overlay indices are
-  //    checked: an id outside its table reads NaN, never memory.
+  //    checked: an id outside its table reads NaN, never memory.  Base-table
+  //    loads are unconditional (an invalid id loads row 0 and is masked).
   RawChunk tr[MAXL][NCH];
   uint32_t src[MAXL][NCH];  // 0: base table, 1: overlay, 2: invalid id
 #pragma unroll
   for (int l = 0; l < MAXL; ++l) {
     if (l >= nl) break;
-    if (lane < nh && hh * dim >= cb && a.rows_out != nullptr)  // the part holding the head's first column
-      a.rows_out[((int64_t)l * a.n_pos + p) * H + hh] = rid[l];
     int32_t ovk = -1;
     const OverlayDev& ov = a.ov[l];
     if constexpr (OVL) {
-      if (lane < nh) {
-        if (a.slot_var != nullptr) {
-          ovk = a.slot_var[p * H + hh];
-        } else if (ov.n > 0) {
-          const int64_t k = sorted_find(ov.ids, ov.n, rid[l]);
-          if (k >= 0) ovk = ov.index ? ov.index[k] : (int32_t)k;
-        }
+      if (a.slot_var != nullptr) {
+        ovk = a.slot_var[p * H + hh];
+      } else if (ov.n > 0) {
+        const int64_t k = sorted_find(ov.ids, ov.n, rid[l]);
+        if (k >= 0) ovk = ov.index ? ov.index[k] : (int32_t)k;
       }
     }
 #pragma unroll
@@ -218,19 +225,29 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
       int32_t k = -1;
       if constexpr (OVL) k = __shfl(ovk, h - h_lo);
       const int off = e0 - h * dim;
-      src[l][c] = 2;
-      if (e0 < W) {
-        if (OVL && k >= 0) {
+      const bool in_w = e0 < W;
+      const bool base_ok = in_w && (uint32_t)row < (uint64_t)a.table[l].n_rows;
+      if constexpr (OVL) {
+        if (in_w && k >= 0) {
+          src[l][c] = 2;
           if (k < ov.rows.n_rows) {
             tr[l][c] = load_raw_rt(ov.rows, k, off);
             src[l][c] = 1;
           }
-        } else if ((uint32_t)row < (uint64_t)a.table[l].n_rows) {
-          tr[l][c] = load_raw<FMT>(a.table[l], dim, row, off);
-          src[l][c] = 0;
+          continue;
         }
       }
+      tr[l][c] = load_raw<FMT>(a.table[l], dim, base_ok ? row : 0, base_ok ? off : 0);
+      src[l][c] = base_ok ? 0u : 2u;
     }
+  }
+
+  // Row ids for the backward (stored after every load is issued: a store in
+  // between would make later loads wait for it and for all loads before it).
+  if (a.rows_out != nullptr && own_head && hh * dim >= cb) {  // the part holding the head's first column
+#pragma unroll
+    for (int l = 0; l < MAXL; ++l)
+      if (l < nl) a.rows_out[((int64_t)l * a.n_pos + p) * H + hh] = rid[l];
   }
 
   // 5. Residual + every layer, fp32, in layer order.
@@ -250,13 +267,14 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
       const int e0 = cb + (lane + 64 * c) * 8;
       const int off = e0 - (min(e0, W - 8) / dim) * dim;
       float v[8];
-      if (src[l][c] == 0) {
-        decode<FMT>(tr[l][c], off, v);
-      } else if (OVL && src[l][c] == 1) {
+      if (OVL && src[l][c] == 1) {
         decode_rt(a.ov[l].rows.fmt, tr[l][c], off, v);
       } else {
+        decode<FMT>(tr[l][c], src[l][c] == 0 ? off : 0, v);
+        if (src[l][c] != 0) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(0x7fc00000u);
+          for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(0x7fc00000u);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[c][i] += v[i];
@@ -514,6 +532,7 @@ int eg_gather_slots(const eg_table* table, const int32_t* rows, const int32_t* s
   memset(&a, 0, sizeof(a));
   int rc = make_table(table, &a.table[0], "table");
   if (rc != EG_OK) return rc;
+  EG_CHECK_ARG(table->n_rows >= 1, "table: n_rows=%lld (at least one row)", (long long)table->n_rows);
   a.ov[0].rows.payload = (const uint8_t*)vars;
   a.ov[0].rows.n_rows = n_vars;
   a.ov[0].rows.fmt = EG_FMT_F32;
@@ -539,6 +558,7 @@ int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* r
   memset(&a, 0, sizeof(a));
   int rc = make_table(table, &a.table[0], "table");
   if (rc != EG_OK) return rc;
+  EG_CHECK_ARG(table->n_rows >= 1, "table: n_rows=%lld (at least one row)", (long long)table->n_rows);
   rc = fill_overlay(overlay, a.table[0], &a.ov[0]);
   if (rc != EG_OK) return rc;
   a.rows_in = rows;
