@@ -345,7 +345,8 @@ static bool launch_special(const FwdArgs& a, bool ovl, hipStream_t st) {
   } else if (a.n_layers == 1) {
     launch_nch<FMT, 128, 2, 1, false, true>(a, st);
   } else if (!ovl) {
-    launch_nch<FMT, 128, 2, 2, false, false>(a, st);
+    if (W == 3072) launch_nch<FMT, 128, 3, 2, false, false, 2>(a, st);
+    else launch_nch<FMT, 128, 2, 2, false, false>(a, st);
   } else {
     launch_nch<FMT, 128, 2, 2, false, true>(a, st);
   }
