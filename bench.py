@@ -417,7 +417,7 @@ def main() -> None:
     }
 
     if not args.no_backward:
-        bw = bench_backward(tab, tokens, max(1, args.steps // 4), max(1, args.warmup // 4))
+        bw = bench_backward(tab, tokens, max(1, args.steps // 4), max(1, args.warmup))
         result["backward"] = bw
         log(f"backward: {bw['us_per_step']:.1f} us/step, {bw['touched_rows']} touched rows, "
             f"{bw['gb_per_s']:.0f} GB/s algorithmic ({100 * bw['frac_of_hbm_peak']:.1f}% of peak)")

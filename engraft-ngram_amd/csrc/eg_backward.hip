@@ -344,13 +344,13 @@ __device__ inline void store_f32(float* __restrict__ row, int sub, const float x
   }
 }
 
-// d_out slice of one slot (bf16 or f32), VPL values of this lane.
-template <int VPL, bool CONSEC>
+// d_out slice of one slot (F32: f32, else bf16), VPL values of this lane.
+template <int VPL, bool CONSEC, bool F32>
 __device__ inline void load_grad(const SegArgs& a, uint32_t slot, int sub, float x[VPL]) {
   const int64_t p = slot / (uint32_t)a.heads;
   const int h = (int)(slot - p * a.heads);
   const int64_t base = p * a.width + (int64_t)h * a.dim;
-  if (a.d_out_f32) {
+  if constexpr (F32) {
     load_f32<VPL, CONSEC>((const float*)a.d_out + base, sub, x);
   } else {
     const uint16_t* src = (const uint16_t*)a.d_out + base;
@@ -367,17 +367,20 @@ __device__ inline void load_grad(const SegArgs& a, uint32_t slot, int sub, float
   }
 }
 
-// Sums the d_out slices of `cnt` (<= 32) consecutive sorted slots whose slot
+// Sums the d_out slices of `cnt` (1..32) consecutive sorted slots whose slot
 // ids sit in lane (gbase + e) of `vl`, in order, onto g.  Loads go out kBatch
-// slots at a time; the additions stay in slot order.
-template <int VPL, bool CONSEC, int kBatch>
+// slots at a time, all of them issued (a slot past cnt re-reads the first one,
+// unused): a load inside a lane-divergent branch would be waited for there.
+// The additions stay in slot order.
+template <int VPL, bool CONSEC, int kBatch, bool F32>
 __device__ inline void sum_piece(const SegArgs& a, uint32_t vl, int gbase, int cnt, int sub, float g[VPL]) {
+  const uint32_t s0 = (uint32_t)__shfl((int)vl, gbase);
   for (int e0 = 0; e0 < cnt; e0 += kBatch) {
     float x[kBatch][VPL];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const uint32_t s = (uint32_t)__shfl((int)vl, gbase + ((e0 + u) & 31));
-      if (e0 + u < cnt) load_grad<VPL, CONSEC>(a, s, sub, x[u]);
+      load_grad<VPL, CONSEC, F32>(a, e0 + u < cnt ? s : s0, sub, x[u]);
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
@@ -525,7 +528,7 @@ __device__ inline uint32_t sort32(uint32_t v, int sub) {
 // in order.
 constexpr int kLongLds = kLongGroups * 512;  // slot ids a long range orders in LDS (the partial-sum buffer)
 
-template <int VPL, bool CONSEC, bool ADAM>
+template <int VPL, bool CONSEC, bool ADAM, bool F32>
 __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_long_blocks) {
   __shared__ uint32_t lds[kLongLds];
   float* part = (float*)lds;  // [kLongGroups][512] once the slot ids are no longer needed
@@ -562,7 +565,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
       float P[VPL];
 #pragma unroll
       for (int t = 0; t < VPL; ++t) P[t] = 0.0f;
-      sum_piece<VPL, CONSEC, 4>(a, vl, gbase, cnt, sub, P);
+      sum_piece<VPL, CONSEC, 4, F32>(a, vl, gbase, cnt, sub, P);
 #pragma unroll
       for (int t = 0; t < VPL; ++t) G[t] = G[t] + P[t];
     }
@@ -595,11 +598,12 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
     load_f32<VPL, CONSEC>(a.v + off, sub, v);
   }
   const int cnt = (int)len;
-  const uint32_t vl = sort32((sub < cnt) ? a.slots[lo + sub] : 0xffffffffu, sub);
+  const uint32_t sl = a.slots[lo + min(sub, cnt - 1)];  // every lane loads (no divergent load)
+  const uint32_t vl = sort32(sub < cnt ? sl : 0xffffffffu, sub);
   float g[VPL];
 #pragma unroll
   for (int t = 0; t < VPL; ++t) g[t] = 0.0f;
-  sum_piece<VPL, CONSEC, 4>(a, vl, gbase, cnt, sub, g);
+  sum_piece<VPL, CONSEC, 4, F32>(a, vl, gbase, cnt, sub, g);
   finish<VPL, CONSEC, ADAM>(a, k, sub, g, p, m, v);
 }
 
@@ -703,7 +707,10 @@ template <bool ADAM, int VPL, bool CONSEC>
 static void launch_reduce_t(const SegArgs& a, hipStream_t st) {
   const int64_t n_long_blocks = n_long_max(a.n);
   const dim3 grid((unsigned)(n_long_blocks + (a.n_var * 32 + 255) / 256));
-  hipLaunchKernelGGL((reduce_kernel<VPL, CONSEC, ADAM>), grid, dim3(256), 0, st, a, n_long_blocks);
+  if (a.d_out_f32)
+    hipLaunchKernelGGL((reduce_kernel<VPL, CONSEC, ADAM, true>), grid, dim3(256), 0, st, a, n_long_blocks);
+  else
+    hipLaunchKernelGGL((reduce_kernel<VPL, CONSEC, ADAM, false>), grid, dim3(256), 0, st, a, n_long_blocks);
 }
 
 template <bool ADAM>
