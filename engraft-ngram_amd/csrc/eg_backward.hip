@@ -83,15 +83,17 @@ __global__ __launch_bounds__(kTileThreads) void keys_count_kernel(
     for (int i = tid; i < ns; i += kTileThreads) spl[i] = ids[(int64_t)i << split_shift];
     __syncthreads();
   }
-  // The kTileIPT lookups of a thread run in lockstep (fixed-length branchless
-  // searches), so their memory latencies overlap.
+  // The kTileIPT lookups of a thread run in lockstep and every load is
+  // issued unconditionally (indices clamped in range, results masked): a load
+  // inside a lane-divergent branch would be waited for inside it, which would
+  // serialise the lookups.
   int32_t row[kTileIPT];
   bool ok[kTileIPT];
 #pragma unroll
   for (int r = 0; r < kTileIPT; ++r) {
     const int64_t idx = (int64_t)blockIdx.x * kTile + r * kTileThreads + tid;
     ok[r] = idx < n;
-    row[r] = ok[r] ? rows[idx] : 0;
+    row[r] = rows[ok[r] ? idx : n - 1];
   }
   uint32_t key[kTileIPT];
   if constexpr (MODE == 2) {
@@ -111,10 +113,13 @@ __global__ __launch_bounds__(kTileThreads) void keys_count_kernel(
     }
     for (uint64_t probe = 0; probe <= imask; ++probe) {
       bool any = false;
+      unsigned long long ent[kTileIPT];
+#pragma unroll
+      for (int r = 0; r < kTileIPT; ++r) ent[r] = index[hslot[r]];
 #pragma unroll
       for (int r = 0; r < kTileIPT; ++r) {
         if (done[r]) continue;
-        const unsigned long long e = index[hslot[r]];
+        const unsigned long long e = ent[r];
         if (e == kIndexEmpty) {
           done[r] = true;
         } else if ((uint32_t)(e >> 32) == (uint32_t)row[r]) {
@@ -146,13 +151,17 @@ __global__ __launch_bounds__(kTileThreads) void keys_count_kernel(
       end[r] = lo[r] > 0 ? min(pos[r] + win, n_var) : 0;
     }
     for (int64_t step = win >> 1; step >= 1; step >>= 1) {
+      int32_t probe[kTileIPT];
+#pragma unroll
+      for (int r = 0; r < kTileIPT; ++r) probe[r] = ids[min(pos[r] + step, n_var - 1)];
 #pragma unroll
       for (int r = 0; r < kTileIPT; ++r)
-        if (pos[r] + step < end[r] && ids[pos[r] + step] <= row[r]) pos[r] += step;
+        if (pos[r] + step < end[r] && probe[r] <= row[r]) pos[r] += step;
     }
 #pragma unroll
     for (int r = 0; r < kTileIPT; ++r) {
-      key[r] = (ok[r] && lo[r] > 0 && ids[pos[r]] == row[r]) ? (uint32_t)pos[r] : (uint32_t)n_var;
+      const int32_t at = ids[pos[r]];
+      key[r] = (ok[r] && lo[r] > 0 && at == row[r]) ? (uint32_t)pos[r] : (uint32_t)n_var;
     }
   }
 #pragma unroll
