@@ -2,12 +2,13 @@
 // 565-626): after the two projections key = emb @ w_key^T [T, hc*n] and
 // value = emb @ w_value^T [T, n] (library GEMMs on the matrix cores),
 //
-//   ple_gate_kernel   one workgroup per position: per stream j the RMS norms
+//   ple_gate_kernel   one workgroup per (position, stream j): the RMS norms
 //                     of key_j and hidden_j, s_j = <key_j^, hidden_j^>/sqrt(n),
 //                     gate_j = sigmoid(sign(s_j) sqrt(max(|s_j|, 1e-6))),
 //                     gated_j = value * gate_j and its RMS norm (norm_conv):
 //                     normed [T, hc*n], s and gate [T, hc]
-//   ple_conv_kernel   thread per (position, channel): the causal depthwise
+//   ple_conv_kernel   one workgroup per position, its channels strided over the
+//                     threads: the causal depthwise
 //                     convolution over [history; normed] with dilation d,
 //                     SiLU, and out = (hidden + gated) + conv
 //
@@ -43,60 +44,63 @@ __global__ __launch_bounds__(kPleThreads) void ple_gate_kernel(
     int hc, int n, float eps, float inv_sqrt_n, float* __restrict__ normed, float* __restrict__ s_out,
     float* __restrict__ gate_out) {
   __shared__ float red[kPleThreads / 64];
-  const int64_t t = blockIdx.x;
+  const int64_t t = blockIdx.x / hc;
+  const int j = (int)(blockIdx.x - t * hc);
   const int tid = threadIdx.x;
   const int per = (n + kPleThreads - 1) / kPleThreads;
-  float v[kPleMaxPer];
+  // Every load of the workgroup is issued before the first reduction (indices
+  // clamped into the row; entries past n are masked to zero).
+  const int64_t row = (t * hc + j) * n;
+  float v[kPleMaxPer], k[kPleMaxPer], h[kPleMaxPer], wk[kPleMaxPer], wq[kPleMaxPer];
+#pragma unroll
+  for (int m = 0; m < kPleMaxPer; ++m) {
+    if (m < per) {
+      const int i = min(tid + m * kPleThreads, n - 1);
+      v[m] = value[t * n + i];
+      k[m] = key[row + i];
+      h[m] = hidden[row + i];
+      wk[m] = norm_key[j * n + i];
+      wq[m] = norm_query[j * n + i];
+    }
+  }
+  float sk = 0.0f, sh = 0.0f;
+#pragma unroll
+  for (int m = 0; m < kPleMaxPer; ++m) {
+    const bool ok = m < per && tid + m * kPleThreads < n;
+    if (!ok) v[m] = k[m] = h[m] = 0.0f;
+    sk += k[m] * k[m];
+    sh += h[m] * h[m];
+  }
+  const float rk = 1.0f / sqrtf(block_sum(sk, red) / (float)n + eps);
+  const float rq = 1.0f / sqrtf(block_sum(sh, red) / (float)n + eps);
+  float dot = 0.0f;
+#pragma unroll
+  for (int m = 0; m < kPleMaxPer; ++m) {
+    if (m < per && tid + m * kPleThreads < n) {
+      const float kn = (k[m] * rk) * wk[m];
+      const float qn = (h[m] * rq) * wq[m];
+      dot += kn * qn;
+    }
+  }
+  const float s = block_sum(dot, red) * inv_sqrt_n;
+  const float mag = sqrtf(fmaxf(fabsf(s), 1e-6f));
+  const float sg = s > 0.0f ? mag : (s < 0.0f ? -mag : 0.0f);
+  const float gate = 1.0f / (1.0f + expf(-sg));
+  float sq = 0.0f;
+#pragma unroll
+  for (int m = 0; m < kPleMaxPer; ++m) {
+    const float g = v[m] * gate;
+    sq += g * g;
+  }
+  const float rg = 1.0f / sqrtf(block_sum(sq, red) / (float)n + eps);
 #pragma unroll
   for (int m = 0; m < kPleMaxPer; ++m) {
     const int i = tid + m * kPleThreads;
-    v[m] = (m < per && i < n) ? value[t * n + i] : 0.0f;
+    if (m < per && i < n) normed[row + i] = ((v[m] * gate) * rg) * norm_conv[j * n + i];
   }
-  for (int j = 0; j < hc; ++j) {
-    const int64_t row = (t * hc + j) * n;
-    float k[kPleMaxPer], h[kPleMaxPer];
-    float sk = 0.0f, sh = 0.0f;
-#pragma unroll
-    for (int m = 0; m < kPleMaxPer; ++m) {
-      const int i = tid + m * kPleThreads;
-      const bool ok = m < per && i < n;
-      k[m] = ok ? key[row + i] : 0.0f;
-      h[m] = ok ? hidden[row + i] : 0.0f;
-      sk += k[m] * k[m];
-      sh += h[m] * h[m];
-    }
-    const float rk = 1.0f / sqrtf(block_sum(sk, red) / (float)n + eps);
-    const float rq = 1.0f / sqrtf(block_sum(sh, red) / (float)n + eps);
-    float dot = 0.0f;
-#pragma unroll
-    for (int m = 0; m < kPleMaxPer; ++m) {
-      const int i = tid + m * kPleThreads;
-      if (m < per && i < n) {
-        const float kn = (k[m] * rk) * norm_key[j * n + i];
-        const float qn = (h[m] * rq) * norm_query[j * n + i];
-        dot += kn * qn;
-      }
-    }
-    const float s = block_sum(dot, red) * inv_sqrt_n;
-    const float mag = sqrtf(fmaxf(fabsf(s), 1e-6f));
-    const float sg = s > 0.0f ? mag : (s < 0.0f ? -mag : 0.0f);
-    const float gate = 1.0f / (1.0f + expf(-sg));
-    float sq = 0.0f;
-#pragma unroll
-    for (int m = 0; m < kPleMaxPer; ++m) {
-      const float g = v[m] * gate;
-      sq += g * g;
-    }
-    const float rg = 1.0f / sqrtf(block_sum(sq, red) / (float)n + eps);
-#pragma unroll
-    for (int m = 0; m < kPleMaxPer; ++m) {
-      const int i = tid + m * kPleThreads;
-      if (m < per && i < n) normed[row + i] = ((v[m] * gate) * rg) * norm_conv[j * n + i];
-    }
-    if (tid == 0) {
-      s_out[t * hc + j] = s;
-      gate_out[t * hc + j] = gate;
-    }
+  if (tid == 0) {
+    s_out[t * hc + j] = s;
+    gate_out[t * hc + j] = gate;
   }
 }
 
@@ -105,20 +109,22 @@ __global__ __launch_bounds__(256) void ple_conv_kernel(const float* __restrict__
                                                        int dil, const float* __restrict__ hidden,
                                                        const float* __restrict__ value,
                                                        const float* __restrict__ gate, float* __restrict__ out) {
-  const int64_t C = (int64_t)hc * n;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= T * C) return;
-  const int64_t t = idx / C;
-  const int64_t c = idx - t * C;
-  float acc = 0.0f;
-  for (int k = 0; k < taps; ++k) {
-    const int64_t src = hist_rows + t - (int64_t)(taps - 1 - k) * dil;
-    if (src >= 0) acc += full[src * C + c] * conv_w[c * taps + k];
+  const int C = hc * n;
+  const int64_t t = blockIdx.x;
+  for (int j = 0; j < hc; ++j) {
+    const float gj = gate[t * hc + j];
+    for (int i = threadIdx.x; i < n; i += 256) {
+      const int c = j * n + i;
+      float acc = 0.0f;
+      for (int k = 0; k < taps; ++k) {
+        const int64_t src = hist_rows + t - (int64_t)(taps - 1 - k) * dil;
+        if (src >= 0) acc += full[src * C + c] * conv_w[(int64_t)c * taps + k];
+      }
+      const float silu = acc / (1.0f + expf(-acc));
+      const int64_t o = t * C + c;
+      out[o] = (hidden[o] + value[t * n + i] * gj) + silu;
+    }
   }
-  const float silu = acc / (1.0f + expf(-acc));
-  const int j = (int)(c / n);
-  const float gated = value[t * n + (c - (int64_t)j * n)] * gate[t * hc + j];
-  out[idx] = (hidden[idx] + gated) + silu;
 }
 
 }  // namespace eg
@@ -130,15 +136,15 @@ extern "C" {
 int eg_ple_gate(const float* key, const float* value, const float* hidden, const float* norm_key,
                 const float* norm_query, const float* norm_conv, int64_t n_pos, int32_t hc, int32_t n_embd, float eps,
                 float* normed, float* s_out, float* gate_out, void* stream) {
-  EG_CHECK_ARG(n_pos >= 0 && n_pos < (1LL << 31), "n_pos=%lld", (long long)n_pos);
+  EG_CHECK_ARG(n_pos >= 0 && n_pos * hc < (1LL << 31), "n_pos=%lld", (long long)n_pos);
   EG_CHECK_ARG(hc >= 1 && hc <= 64 && n_embd >= 1 && n_embd <= kPleThreads * kPleMaxPer,
                "hc=%d n_embd=%d (n_embd <= %d)", hc, n_embd, kPleThreads * kPleMaxPer);
   EG_CHECK_ARG(n_pos == 0 || (key && value && hidden && norm_key && norm_query && norm_conv && normed && s_out &&
                               gate_out),
                "NULL argument");
   if (n_pos == 0) return EG_OK;
-  hipLaunchKernelGGL(ple_gate_kernel, dim3((unsigned)n_pos), dim3(kPleThreads), 0, (hipStream_t)stream, key, value,
-                     hidden, norm_key, norm_query, norm_conv, hc, n_embd, eps, (float)(1.0 / sqrt((double)n_embd)),
+  hipLaunchKernelGGL(ple_gate_kernel, dim3((unsigned)(n_pos * hc)), dim3(kPleThreads), 0, (hipStream_t)stream, key,
+                     value, hidden, norm_key, norm_query, norm_conv, hc, n_embd, eps, (float)(1.0 / sqrt((double)n_embd)),
                      normed, s_out, gate_out);
   return launch_status("ple_gate_kernel");
 }
@@ -149,11 +155,10 @@ int eg_ple_conv(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc,
   EG_CHECK_ARG(n_pos >= 0 && hist_rows >= 0 && hc >= 1 && n_embd >= 1 && taps >= 1 && dilation >= 1,
                "n_pos=%lld hist_rows=%lld hc=%d n_embd=%d taps=%d dilation=%d", (long long)n_pos,
                (long long)hist_rows, hc, n_embd, taps, dilation);
-  const int64_t total = n_pos * hc * (int64_t)n_embd;
-  EG_CHECK_ARG(total < (1LL << 40), "too many elements");
+  EG_CHECK_ARG(n_pos < (1LL << 31) && (int64_t)hc * n_embd < (1LL << 31), "too many elements");
   EG_CHECK_ARG(n_pos == 0 || (full && conv_w && hidden && value && gate && out), "NULL argument");
   if (n_pos == 0) return EG_OK;
-  hipLaunchKernelGGL(ple_conv_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, full,
+  hipLaunchKernelGGL(ple_conv_kernel, dim3((unsigned)n_pos), dim3(256), 0, (hipStream_t)stream, full,
                      hist_rows, n_pos, hc, n_embd, conv_w, taps, dilation, hidden, value, gate, out);
   return launch_status("ple_conv_kernel");
 }
