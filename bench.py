@@ -309,7 +309,8 @@ def main() -> None:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures the table path on one "
-              "GPU (every box here has one MI355X); see DESIGN.md for how the path shards.", file=sys.stderr)
+              "GPU (every box here has one MI355X). The path shards by positions (forward, table replicated) "
+              "and by variable owner (backward); that layout is not built here.", file=sys.stderr)
         sys.exit(2)
 
     import torch

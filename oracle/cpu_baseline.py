@@ -2,7 +2,7 @@
 ``bench.py``'s ``cpu_baseline`` (TEST INFRASTRUCTURE ONLY -- see
 oracle/__init__.py).
 
-This is BASELINE.md's "vectorized" CPU baseline: the numpy-uint64 hash of
+This is the vectorized form of the reference's CPU path: the numpy-uint64 hash of
 ``engraft/damage.py:68-104`` (``oracle.hash.ngram_rows_np``), then
 ``torch.index_select`` gathers from a host-resident table of the benchmark's
 full shape, Q8_0 dequantisation (``engraft/replica/dequant.py:86-93``), and an
