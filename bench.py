@@ -405,7 +405,7 @@ def main() -> None:
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profile("forward_q8_cfg1"),
-            "kernel": "eg::forward_kernel<Q8_0, 128, 4, bf16 out, no overlay>",
+            "kernel": "eg::forward_kernel<Q8_0, dim 128, 2 x 1024-column parts per position, bf16 out, no overlay>",
             "algorithmic_bytes_per_launch": fbytes, "avg_launch_us": kernel_ms * 1e3,
         },
         "forward": {

@@ -329,18 +329,19 @@ static void launch_nch(FwdArgs a, hipStream_t st) {
   EG_LAUNCH(FMT, DIM, NCH, MAXL, F32OUT, OVL, PARTS);
 }
 
-// Specialised residual-add shapes (dim 128): a whole W = 2048 row per
-// wavefront for one layer without overlay (the config-1 shape), W = 3072 in
-// two halves; two layers and overlay lookups take 1024-column parts, which
-// keeps their registers (and so their occupancy) close to the one-layer
-// kernel's.  Everything else goes through the generic kernel.
+// Specialised residual-add shapes (dim 128): one layer without overlay takes
+// W = 2048 in two 1024-column parts (the config-1 shape: 8 waves per SIMD
+// without spills; one 2048-column wavefront per position, at 6 waves, and four
+// 512-column parts both measured slower) and W = 3072 in two halves; two layers
+// take 1536-column parts at W = 3072, 1024-column parts otherwise, overlay
+// lookups 1024-column parts.  Everything else goes through the generic kernel.
 template <int FMT>
 static bool launch_special(const FwdArgs& a, bool ovl, hipStream_t st) {
   if (a.dim != 128) return false;
   const int W = a.heads * a.dim;
   if (W != 2048 && W != 3072) return false;
   if (a.n_layers == 1 && !ovl) {
-    if (W == 2048) launch_nch<FMT, 128, 4, 1, false, false, 1>(a, st);
+    if (W == 2048) launch_nch<FMT, 128, 2, 1, false, false, 2>(a, st);
     else launch_nch<FMT, 128, 3, 1, false, false, 2>(a, st);
   } else if (a.n_layers == 1) {
     launch_nch<FMT, 128, 2, 1, false, true>(a, st);
