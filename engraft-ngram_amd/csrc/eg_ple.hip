@@ -7,8 +7,8 @@
 //                     gate_j = sigmoid(sign(s_j) sqrt(max(|s_j|, 1e-6))),
 //                     gated_j = value * gate_j and its RMS norm (norm_conv):
 //                     normed [T, hc*n], s and gate [T, hc]
-//   ple_conv_kernel   one workgroup per position, its channels strided over the
-//                     threads: the causal depthwise
+//   ple_conv_kernel   one workgroup per 256 channels x 32 positions: the causal
+//                     depthwise
 //                     convolution over [history; normed] with dilation d,
 //                     SiLU, and out = (hidden + gated) + conv
 //
@@ -104,26 +104,52 @@ __global__ __launch_bounds__(kPleThreads) void ple_gate_kernel(
   }
 }
 
+// Workgroup = 256 channels x kConvRun consecutive positions: a tap reads a row
+// the same workgroup read a few positions earlier (L1), so every normed value
+// comes from HBM about once.
+constexpr int kConvRun = 32;
+
 __global__ __launch_bounds__(256) void ple_conv_kernel(const float* __restrict__ full, int64_t hist_rows, int64_t T,
                                                        int hc, int n, const float* __restrict__ conv_w, int taps,
                                                        int dil, const float* __restrict__ hidden,
                                                        const float* __restrict__ value,
                                                        const float* __restrict__ gate, float* __restrict__ out) {
   const int C = hc * n;
-  const int64_t t = blockIdx.x;
-  for (int j = 0; j < hc; ++j) {
-    const float gj = gate[t * hc + j];
-    for (int i = threadIdx.x; i < n; i += 256) {
-      const int c = j * n + i;
-      float acc = 0.0f;
-      for (int k = 0; k < taps; ++k) {
+  const int n_cblk = (C + 255) / 256;
+  const int cblk = (int)(blockIdx.x % n_cblk);
+  const int64_t t0 = (int64_t)(blockIdx.x / n_cblk) * kConvRun;
+  const int c = cblk * 256 + threadIdx.x;
+  if (c >= C) return;
+  const int j = c / n;
+  const int i = c - j * n;
+  constexpr int kMaxTaps = 8;
+  float w[kMaxTaps];
+#pragma unroll
+  for (int k = 0; k < kMaxTaps; ++k)
+    if (k < taps) w[k] = conv_w[(int64_t)c * taps + k];
+  const int64_t t_end = min(t0 + kConvRun, T);
+  for (int64_t t = t0; t < t_end; ++t) {
+    // a tap before the first row reads row 0 with its weight dropped (every load is issued)
+    float x[kMaxTaps];
+    bool ok[kMaxTaps];
+#pragma unroll
+    for (int k = 0; k < kMaxTaps; ++k) {
+      if (k < taps) {
         const int64_t src = hist_rows + t - (int64_t)(taps - 1 - k) * dil;
-        if (src >= 0) acc += full[src * C + c] * conv_w[(int64_t)c * taps + k];
+        ok[k] = src >= 0;
+        x[k] = full[(ok[k] ? src : 0) * C + c];
       }
-      const float silu = acc / (1.0f + expf(-acc));
-      const int64_t o = t * C + c;
-      out[o] = (hidden[o] + value[t * n + i] * gj) + silu;
     }
+    const int64_t o = t * C + c;
+    const float hv = hidden[o];
+    const float vv = value[t * n + i];
+    const float gj = gate[t * hc + j];
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMaxTaps; ++k)
+      if (k < taps && ok[k]) acc += x[k] * w[k];
+    const float silu = acc / (1.0f + expf(-acc));
+    out[o] = (hv + vv * gj) + silu;
   }
 }
 
@@ -152,13 +178,15 @@ int eg_ple_gate(const float* key, const float* value, const float* hidden, const
 int eg_ple_conv(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
                 const float* conv_w, int32_t taps, int32_t dilation, const float* hidden, const float* value,
                 const float* gate, float* out, void* stream) {
-  EG_CHECK_ARG(n_pos >= 0 && hist_rows >= 0 && hc >= 1 && n_embd >= 1 && taps >= 1 && dilation >= 1,
+  EG_CHECK_ARG(n_pos >= 0 && hist_rows >= 0 && hc >= 1 && n_embd >= 1 && taps >= 1 && taps <= 8 && dilation >= 1,
                "n_pos=%lld hist_rows=%lld hc=%d n_embd=%d taps=%d dilation=%d", (long long)n_pos,
                (long long)hist_rows, hc, n_embd, taps, dilation);
   EG_CHECK_ARG(n_pos < (1LL << 31) && (int64_t)hc * n_embd < (1LL << 31), "too many elements");
   EG_CHECK_ARG(n_pos == 0 || (full && conv_w && hidden && value && gate && out), "NULL argument");
   if (n_pos == 0) return EG_OK;
-  hipLaunchKernelGGL(ple_conv_kernel, dim3((unsigned)n_pos), dim3(256), 0, (hipStream_t)stream, full,
+  const int64_t blocks = (int64_t)((hc * n_embd + 255) / 256) * ((n_pos + kConvRun - 1) / kConvRun);
+  EG_CHECK_ARG(blocks < (1LL << 32), "too many elements");
+  hipLaunchKernelGGL(ple_conv_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, full,
                      hist_rows, n_pos, hc, n_embd, conv_w, taps, dilation, hidden, value, gate, out);
   return launch_status("ple_conv_kernel");
 }

@@ -253,7 +253,7 @@ int eg_ple_gate(const float* key, const float* value, const float* hidden, const
 /* out = (hidden + value*gate) + silu(conv), conv[t, c] = sum_k conv_w[c, k] *
  * full[hist_rows + t - (taps-1-k)*dilation, c] over the rows that exist
  * (causal_depthwise_conv, layers.py:257-293); full f32 [hist_rows + n_pos,
- * hc*n_embd] = [history; normed]; conv_w f32 [hc*n_embd, taps]. */
+ * hc*n_embd] = [history; normed]; conv_w f32 [hc*n_embd, taps], taps <= 8. */
 int eg_ple_conv(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
                 const float* conv_w, int32_t taps, int32_t dilation, const float* hidden,
                 const float* value, const float* gate, float* out, void* stream);
