@@ -23,3 +23,18 @@ def run() -> None:
     assert np.array_equal(rows[0].cpu().numpy(), exp_rows), "row ids differ from the oracle"
     G.assert_out_matches(G.bf16_bits(out), exp_out)
     print("smoke: forward (hash -> gather -> dequant -> residual add) matches the oracle", flush=True)
+
+    # one descent step on the rows just read: deterministic scatter + Adam + requant
+    from engraft_ngram_amd import descent as D
+    from oracle import backward as B
+
+    d = (torch.randn((tokens.size, 2048), generator=torch.Generator(device="cuda").manual_seed(5), device="cuda")
+         * 1e-3).to(torch.bfloat16)
+    st = D.DescentState.from_rows(tab, rows[0])
+    st.step(d, rows[0], lr=1e-3)
+    ids = st.ids.cpu().numpy()
+    grad, _ = B.scatter_grad(d.float().cpu().numpy(), exp_rows, ids)
+    p0 = G.synth_fetch("q8_0", 2, 128)(ids)
+    p1, _, _ = B.adam_step(p0, grad, np.zeros_like(p0), np.zeros_like(p0), 1, 1e-3)
+    assert np.array_equal(st.master.cpu().numpy(), p1), "descent step differs from the oracle"
+    print("smoke: descent step (scatter + Adam) matches the oracle", flush=True)
