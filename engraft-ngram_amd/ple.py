@@ -10,9 +10,10 @@ Forward:
 * ``eg_ple_conv``: the dilated causal depthwise convolution over
   ``[history; normed]``, SiLU, and ``out = hidden + gated + conv``.
 
-The result is differentiable.  The backward recomputes the block with torch
-operations on the device and differentiates that; the forward values are the
-HIP kernels'.  ``detach_value`` / ``detach_gate`` change only the backward,
+The result -- the output and the new history -- is differentiable in emb,
+hidden, the history and the weights.  The backward recomputes the block with
+torch operations on the device and differentiates that; the forward values are
+the HIP kernels'.  ``detach_value`` / ``detach_gate`` change only the backward,
 as in the reference.
 """
 from __future__ import annotations
@@ -42,7 +43,8 @@ def _rms(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
 
 
 def _block_torch(emb, hidden, w_key, w_value, nk, nq, nc, conv, hist, eps, dil, detach_value, detach_gate):
-    """The block in torch operations (the backward's recomputation)."""
+    """The block in torch operations (the backward's recomputation): ``(out,
+    new_hist)``."""
     t_len, hc, n = hidden.shape
     key = _rms((emb @ w_key.T).reshape(t_len, hc, n), nk.reshape(hc, n), eps)
     query = _rms(hidden, nq.reshape(hc, n), eps)
@@ -62,7 +64,10 @@ def _block_torch(emb, hidden, w_key, w_value, nk, nq, nc, conv, hist, eps, dil, 
         lo = max(0, back - h0)  # first position whose source row exists
         if lo < t_len:
             acc[lo:] = acc[lo:] + full[h0 + lo - back:h0 + t_len - back] * conv[:, k]
-    return hidden + gated + F.silu(acc).reshape(t_len, hc, n)
+    out = hidden + gated + F.silu(acc).reshape(t_len, hc, n)
+    hist_len = (taps - 1) * dil
+    new_hist = full[-hist_len:] if hist_len > 0 else full[:0]
+    return out, new_hist.reshape(-1, hc, n)
 
 
 class _PleFn(torch.autograd.Function):
@@ -89,21 +94,30 @@ class _PleFn(torch.autograd.Function):
         out = torch.empty((t_len, hc, n), **f32)
         _lib.call("eg_ple_conv", _lib.ptr(full), h0, t_len, hc, n, _lib.ptr(conv32), conv32.shape[1], int(dil),
                   _lib.ptr(hidden32), _lib.ptr(value), _lib.ptr(gate), _lib.ptr(out), st)
+        hist_len = (conv32.shape[1] - 1) * int(dil)
+        new_hist = (full[-hist_len:] if hist_len > 0 else full[:0]).reshape(-1, hc, n).to(hidden.dtype).clone()
         ctx.save_for_backward(emb, hidden, w_key, w_value, nk, nq, nc, conv, hist)
         ctx.cfg = (eps, dil, detach_value, detach_gate)
-        ctx.mark_non_differentiable(full, s, gate, value)
-        return out.to(hidden.dtype), full, s, gate, value
+        ctx.mark_non_differentiable(s, gate, value)
+        return out.to(hidden.dtype), new_hist, s, gate, value
 
     @staticmethod
-    def backward(ctx, d_out, _d_full, _d_s, _d_gate, _d_value):
+    def backward(ctx, d_out, d_hist, _d_s, _d_gate, _d_value):
         inputs = ctx.saved_tensors
         eps, dil, detach_value, detach_gate = ctx.cfg
         with torch.enable_grad():
             leaves = [x.detach().requires_grad_(need) for x, need in zip(inputs, ctx.needs_input_grad[:9])]
-            out = _block_torch(*leaves, eps, dil, detach_value, detach_gate)
+            out, new_hist = _block_torch(*leaves, eps, dil, detach_value, detach_gate)
             wrt = [x for x, need in zip(leaves, ctx.needs_input_grad[:9]) if need]
-            grads = iter(torch.autograd.grad(out, wrt, d_out) if wrt else [])
-        res = [next(grads) if need else None for need in ctx.needs_input_grad[:9]]
+            outs, grads_in = [out], [d_out]
+            if d_hist is not None and new_hist.numel():
+                outs.append(new_hist)
+                grads_in.append(d_hist)
+            grads = iter(torch.autograd.grad(outs, wrt, grads_in, allow_unused=True) if wrt else [])
+        res = []
+        for x, need in zip(leaves, ctx.needs_input_grad[:9]):
+            g = next(grads) if need else None
+            res.append(torch.zeros_like(x) if (need and g is None) else g)
         return (*res, None, None, None, None)
 
 
@@ -122,8 +136,8 @@ def ple_forward(emb: torch.Tensor, hidden: torch.Tensor, w: PleWeights, hist: to
         raise ValueError(f"emb [T, {n}] and hidden [T, {hc}, {n}] expected, got {tuple(emb.shape)}, "
                          f"{tuple(hidden.shape)}")
     hist = hist.reshape(-1, hc, n) if hist.numel() else hidden.new_zeros((0, hc, n))
-    out, full, s, gate, value = _PleFn.apply(emb, hidden, w.w_key, w.w_value, w.norm_key, w.norm_query,
-                                             w.norm_conv, w.conv1d, hist, eps, dil, detach_value, detach_gate)
+    out, new_hist, s, gate, value = _PleFn.apply(emb, hidden, w.w_key, w.w_value, w.norm_key, w.norm_query,
+                                                 w.norm_conv, w.conv1d, hist, eps, dil, detach_value, detach_gate)
     if diag is not None:
         gated_norm = value.norm(dim=-1, keepdim=True) * gate.abs()
         diag["s"] = s.clone()
@@ -131,6 +145,4 @@ def ple_forward(emb: torch.Tensor, hidden: torch.Tensor, w: PleWeights, hist: to
         diag["value_norm"] = value.norm(dim=-1).clone()
         diag["gated_norm"] = gated_norm.clone()
         diag["hidden_norm"] = hidden.detach().norm(dim=-1).clone()
-    hist_len = (w.conv1d.shape[1] - 1) * dil
-    new_hist = full[-hist_len:] if hist_len > 0 else full[:0]
-    return out, new_hist.reshape(-1, hc, n)
+    return out, new_hist

@@ -83,3 +83,29 @@ def test_ple_forward_gradient(cuda):
     assert torch.equal(out2, out_d.detach())
     (out2 * r.to(cuda)).sum().backward()
     assert not torch.allclose(e2.grad, e_d.grad)
+
+
+def test_ple_history_gradient_across_chunks(cuda):
+    """The history returned by one chunk carries the gradient into the next, as
+    the reference's differentiable ``new_hist`` (layers.py:623-626): the loss of
+    chunk 2 reaches chunk 1's emb."""
+    from engraft_ngram_amd import ple
+    hc, n = 4, 2560
+    w = ple_weights(hc, n, seed=8)
+    wd = _dev_weights(w, cuda)
+    g = torch.Generator().manual_seed(9)
+    emb = torch.randn((14, n), generator=g) * 0.1
+    hidden = torch.randn((14, hc, n), generator=g) * 0.1
+    r = torch.randn((6, hc, n), generator=g)
+    e_c = emb.clone().requires_grad_(True)
+    _, h1, _, _ = P.ple_forward(e_c[:8], hidden[:8], w, torch.zeros(0, hc, n), hc, n, 1e-6, 3)
+    out2, _, _, _ = P.ple_forward(e_c[8:], hidden[8:], w, h1, hc, n, 1e-6, 3)
+    (out2 * r).sum().backward()
+    e_d = emb.to(cuda).requires_grad_(True)
+    hd = hidden.to(cuda)
+    _, h1d = ple.ple_forward(e_d[:8], hd[:8], wd, torch.zeros(0, hc, n, device=cuda), _HP)
+    out2d, _ = ple.ple_forward(e_d[8:], hd[8:], wd, h1d, _HP)
+    (out2d * r.to(cuda)).sum().backward()
+    scale = e_c.grad.abs().max().item()
+    assert e_c.grad[:8].abs().max().item() > 0  # the first chunk does receive gradient
+    assert (e_d.grad.cpu() - e_c.grad).abs().max().item() <= 1e-4 * scale
