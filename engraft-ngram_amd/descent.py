@@ -158,10 +158,9 @@ class DescentState:
         n_pos, heads = rows.shape
         if d_out.numel() != n_pos * heads * self.dim or not d_out.is_contiguous() or d_out.device != dev:
             raise ValueError(f"d_out must be contiguous on {dev} with {n_pos}x{heads * self.dim} elements")
-        self.step_count += 1
         opt = _lib.EgAdam()
         opt.lr, opt.beta1, opt.beta2, opt.eps = float(lr), float(betas[0]), float(betas[1]), float(eps)
-        opt.step = self.step_count
+        opt.step = self.step_count + 1
         opt.dense = 1 if dense else 0
         base = None
         if mu != 0.0:
@@ -174,6 +173,7 @@ class DescentState:
         _lib.call("eg_descent_step", _lib.ptr(d_out), _dout_args(d_out), _lib.ptr(rows), n_pos, heads,
                   ctypes.byref(st), ctypes.byref(opt), ctypes.byref(base) if base is not None else None,
                   _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
+        self.step_count += 1  # only once the step is on its way (a rejected call leaves the count)
 
     def overlay(self, quantized: bool = True) -> DeviceOverlay:
         """The variables as a forward overlay: the requantised rows, or the fp32
