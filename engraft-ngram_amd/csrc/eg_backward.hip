@@ -400,6 +400,77 @@ __device__ inline void sum_piece(const SegArgs& a, uint32_t vl, int gbase, int c
   }
 }
 
+// Row k of the Q8_0 / MXFP8 store q from the fp32 values p this lane owns
+// (the 32 lanes of a row together): Q8_0 d = fp16(amax/127), q = rint(x/d)
+// clamped to +-127; MXFP8 the smallest shared exponent e with amax*2^-e <= 448.
+template <int VPL, bool CONSEC>
+__device__ void requant_row(const TableDev& q, int64_t k, int dim, int sub, const float p[VPL]) {
+  const int64_t off = k * dim;
+  const int nb = dim >> 5;
+  uint8_t* payload = (uint8_t*)q.payload;
+  if constexpr (CONSEC) {
+    // this lane's values all lie in block sub / (32 / VPL)
+    constexpr int kLanesPerBlock = 32 / VPL;
+    float amax = 0.0f;
+#pragma unroll
+    for (int t = 0; t < VPL; ++t) amax = fmaxf(amax, fabsf(p[t]));
+#pragma unroll
+    for (int o = kLanesPerBlock / 2; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+    const int blk = sub / kLanesPerBlock;
+    uint32_t packed = 0;
+    if (q.fmt == EG_FMT_Q8_0) {
+      const uint16_t dh = f32_to_f16(amax / 127.0f);
+      const float d = f16_to_f32(dh);
+#pragma unroll
+      for (int t = 0; t < VPL; ++t) {
+        float r = (d == 0.0f) ? 0.0f : rintf(p[t] / d);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        const uint32_t b = (uint32_t)(int32_t)r & 0xffu;
+        if constexpr (VPL == 4) packed |= b << (8 * t);
+        else payload[off + col_of<VPL, CONSEC>(sub, t)] = (uint8_t)b;
+      }
+      if (sub % kLanesPerBlock == 0) ((uint16_t*)q.scales)[k * nb + blk] = dh;
+    } else {  // EG_FMT_MXFP8
+      const int ebits = (int)((__float_as_uint(amax) >> 23) & 0xffu);
+      int e = (amax > 0.0f ? ebits - 127 : -127) - 8;
+      e = min(max(e, -127), 127);
+      if (amax * ldexpf(1.0f, -e) > 448.0f) e = min(e + 1, 127);
+      const float inv = ldexpf(1.0f, -e);
+#pragma unroll
+      for (int t = 0; t < VPL; ++t) {
+        const uint32_t b = f32_to_e4m3(fminf(fmaxf(p[t] * inv, -448.0f), 448.0f));
+        if constexpr (VPL == 4) packed |= b << (8 * t);
+        else payload[off + col_of<VPL, CONSEC>(sub, t)] = (uint8_t)b;
+      }
+      if (sub % kLanesPerBlock == 0) ((uint8_t*)q.scales)[k * nb + blk] = (uint8_t)(e + 127);
+    }
+    if constexpr (VPL == 4) *(uint32_t*)(payload + off + sub * 4) = packed;
+  } else {
+#pragma unroll
+    for (int t = 0; t < VPL; ++t) {
+      float amax = fabsf(p[t]);
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+      const int64_t qi = off + sub + 32 * t;
+      if (q.fmt == EG_FMT_Q8_0) {
+        const uint16_t dh = f32_to_f16(amax / 127.0f);
+        const float d = f16_to_f32(dh);
+        float r = (d == 0.0f) ? 0.0f : rintf(p[t] / d);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        payload[qi] = (uint8_t)(int32_t)r;
+        if (sub == 0) ((uint16_t*)q.scales)[k * nb + t] = dh;
+      } else {
+        const int ebits = (int)((__float_as_uint(amax) >> 23) & 0xffu);
+        int e = (amax > 0.0f ? ebits - 127 : -127) - 8;
+        e = min(max(e, -127), 127);
+        if (amax * ldexpf(1.0f, -e) > 448.0f) e = min(e + 1, 127);
+        payload[qi] = (uint8_t)f32_to_e4m3(fminf(fmaxf(p[t] * ldexpf(1.0f, -e), -448.0f), 448.0f));
+        if (sub == 0) ((uint8_t*)q.scales)[k * nb + t] = (uint8_t)(e + 127);
+      }
+    }
+  }
+}
+
 // Adam on variable k (torch's single-tensor order, no contractions):
 // m.lerp_(g, 1-b1); v.mul_(b2).addcmul_(g, g, 1-b2);
 // p.addcdiv_(m, sqrt(v)/sqrt(bc2) + eps, -lr/bc1); then the requantised copy.
@@ -426,70 +497,7 @@ __device__ void adam_apply(const SegArgs& a, int64_t k, int sub, const float g[V
   store_f32<VPL, CONSEC>(a.master + off, sub, p);
   store_f32<VPL, CONSEC>(a.m + off, sub, m);
   store_f32<VPL, CONSEC>(a.v + off, sub, v);
-  if (a.quant.fmt == 0) return;
-  const int nb = a.dim >> 5;
-  uint8_t* payload = (uint8_t*)a.quant.payload;
-  if constexpr (CONSEC) {
-    // this lane's values all lie in block sub / (32 / VPL)
-    constexpr int kLanesPerBlock = 32 / VPL;
-    float amax = 0.0f;
-#pragma unroll
-    for (int t = 0; t < VPL; ++t) amax = fmaxf(amax, fabsf(p[t]));
-#pragma unroll
-    for (int o = kLanesPerBlock / 2; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
-    const int blk = sub / kLanesPerBlock;
-    uint32_t packed = 0;
-    if (a.quant.fmt == EG_FMT_Q8_0) {
-      const uint16_t dh = f32_to_f16(amax / 127.0f);
-      const float d = f16_to_f32(dh);
-#pragma unroll
-      for (int t = 0; t < VPL; ++t) {
-        float r = (d == 0.0f) ? 0.0f : rintf(p[t] / d);
-        r = fminf(fmaxf(r, -127.0f), 127.0f);
-        const uint32_t b = (uint32_t)(int32_t)r & 0xffu;
-        if constexpr (VPL == 4) packed |= b << (8 * t);
-        else payload[off + col_of<VPL, CONSEC>(sub, t)] = (uint8_t)b;
-      }
-      if (sub % kLanesPerBlock == 0) ((uint16_t*)a.quant.scales)[k * nb + blk] = dh;
-    } else {  // EG_FMT_MXFP8
-      const int ebits = (int)((__float_as_uint(amax) >> 23) & 0xffu);
-      int e = (amax > 0.0f ? ebits - 127 : -127) - 8;
-      e = min(max(e, -127), 127);
-      if (amax * ldexpf(1.0f, -e) > 448.0f) e = min(e + 1, 127);
-      const float inv = ldexpf(1.0f, -e);
-#pragma unroll
-      for (int t = 0; t < VPL; ++t) {
-        const uint32_t b = f32_to_e4m3(fminf(fmaxf(p[t] * inv, -448.0f), 448.0f));
-        if constexpr (VPL == 4) packed |= b << (8 * t);
-        else payload[off + col_of<VPL, CONSEC>(sub, t)] = (uint8_t)b;
-      }
-      if (sub % kLanesPerBlock == 0) ((uint8_t*)a.quant.scales)[k * nb + blk] = (uint8_t)(e + 127);
-    }
-    if constexpr (VPL == 4) *(uint32_t*)(payload + off + sub * 4) = packed;
-  } else {
-#pragma unroll
-    for (int t = 0; t < VPL; ++t) {
-      float amax = fabsf(p[t]);
-#pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
-      const int64_t qi = off + sub + 32 * t;
-      if (a.quant.fmt == EG_FMT_Q8_0) {
-        const uint16_t dh = f32_to_f16(amax / 127.0f);
-        const float d = f16_to_f32(dh);
-        float r = (d == 0.0f) ? 0.0f : rintf(p[t] / d);
-        r = fminf(fmaxf(r, -127.0f), 127.0f);
-        payload[qi] = (uint8_t)(int32_t)r;
-        if (sub == 0) ((uint16_t*)a.quant.scales)[k * nb + t] = dh;
-      } else {
-        const int ebits = (int)((__float_as_uint(amax) >> 23) & 0xffu);
-        int e = (amax > 0.0f ? ebits - 127 : -127) - 8;
-        e = min(max(e, -127), 127);
-        if (amax * ldexpf(1.0f, -e) > 448.0f) e = min(e + 1, 127);
-        payload[qi] = (uint8_t)f32_to_e4m3(fminf(fmaxf(p[t] * ldexpf(1.0f, -e), -448.0f), 448.0f));
-        if (sub == 0) ((uint8_t*)a.quant.scales)[k * nb + t] = (uint8_t)(e + 127);
-      }
-    }
-  }
+  if (a.quant.fmt != 0) requant_row<VPL, CONSEC>(a.quant, k, a.dim, sub, p);
 }
 
 // The sum g of variable k is final: optimizer step, or accumulation into grad_out.
@@ -631,6 +639,21 @@ __global__ __launch_bounds__(256) void dense_kernel(const SegArgs a) {
   load_f32<VPL, CONSEC>(a.m + off, sub, m);
   load_f32<VPL, CONSEC>(a.v + off, sub, v);
   adam_apply<VPL, CONSEC>(a, k, sub, g, p, m, v);
+}
+
+// Requantisation on its own: src row i -> row dst_rows[i] (i when NULL) of q,
+// one 32-lane group per row; a destination outside q is skipped.
+template <int VPL, bool CONSEC>
+__global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ src, int64_t n, int dim,
+                                                       const int32_t* __restrict__ dst_rows, const TableDev q) {
+  const int sub = threadIdx.x & 31;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 5;
+  if (i >= n) return;
+  const int64_t k = dst_rows ? (int64_t)dst_rows[i] : i;
+  if (k < 0 || k >= q.n_rows) return;
+  float p[VPL];
+  load_f32<VPL, CONSEC>(src + i * dim, sub, p);
+  requant_row<VPL, CONSEC>(q, k, dim, sub, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -895,6 +918,31 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   }
   if (opt->dense) rc = launch_dense(a, st);
   return rc;
+}
+
+int eg_quantize_rows(const float* src, int64_t n, int32_t dim, const int32_t* dst_rows, const eg_table* dst,
+                     void* stream) {
+  EG_CHECK_ARG(dst != nullptr, "dst is NULL");
+  EG_CHECK_ARG(dst->fmt == EG_FMT_Q8_0 || dst->fmt == EG_FMT_MXFP8, "dst must be Q8_0 or MXFP8 (fmt %d)", dst->fmt);
+  EG_CHECK_ARG(dim == dst->dim, "dim %d != dst dim %d", dim, dst->dim);
+  EG_CHECK_ARG(n >= 0 && n < (1LL << 31), "n=%lld", (long long)n);
+  EG_CHECK_ARG(dst_rows != nullptr || n <= dst->n_rows, "n=%lld > dst rows %lld", (long long)n,
+               (long long)dst->n_rows);
+  EG_CHECK_ARG(n == 0 || src != nullptr, "src is NULL");
+  TableDev q;
+  int rc = make_table(dst, &q, "dst");
+  if (rc != EG_OK) return rc;
+  if (n == 0) return EG_OK;
+  const dim3 grid((unsigned)((n * 32 + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  switch (dim) {
+    case 128: hipLaunchKernelGGL((quantize_kernel<4, true>), grid, dim3(256), 0, st, src, n, dim, dst_rows, q); break;
+    case 64: hipLaunchKernelGGL((quantize_kernel<2, true>), grid, dim3(256), 0, st, src, n, dim, dst_rows, q); break;
+    case 256: hipLaunchKernelGGL((quantize_kernel<8, true>), grid, dim3(256), 0, st, src, n, dim, dst_rows, q); break;
+    case 160: hipLaunchKernelGGL((quantize_kernel<5, false>), grid, dim3(256), 0, st, src, n, dim, dst_rows, q); break;
+    default: return set_error(EG_ERR_UNSUPPORTED, "requantisation for dim %d (built: 64, 128, 160, 256)", dim);
+  }
+  return launch_status("quantize_kernel");
 }
 
 }  // extern "C"

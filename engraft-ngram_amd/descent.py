@@ -105,6 +105,9 @@ class DescentState:
         self.step_count = 0
         self.base = base
         self.quant = RowStore.empty(quant_fmt, ids.numel(), self.dim, dev) if quant_fmt else None
+        if self.quant is not None and ids.numel():
+            # every variable's quantised row is valid before its first step
+            self._requant(self.master, None)
         # open-addressing index of the ids for the backward's lookups (built once)
         cap = 64
         while cap < 2 * ids.numel():
@@ -148,14 +151,42 @@ class DescentState:
         s.index_capacity = self.index.numel()
         return s
 
+    def _requant(self, src: torch.Tensor, dst_rows: torch.Tensor | None) -> None:
+        tab = self.quant.c_table()
+        _lib.call("eg_quantize_rows", _lib.ptr(src), src.shape[0], self.dim,
+                  _lib.ptr(dst_rows) if dst_rows is not None else None, ctypes.byref(tab),
+                  _lib.stream_ptr(self.device))
+
     def step(self, d_out: torch.Tensor, rows: torch.Tensor, *, lr: float, betas=(0.9, 0.999), eps: float = 1e-8,
-             dense: bool = False, mu: float = 0.0) -> None:
+             dense: bool = False, mu: float = 0.0, frozen=None) -> None:
         """One optimizer step from ``d_out`` (bf16/f32 ``[n_pos, heads*D]``) and the
         slots' row ids ``rows`` (int32 ``[n_pos, heads]``).  ``mu``: the pull
-        term ``mu*||rows_var - rows0||^2/||rows0||^2`` (rows0 = the base table)."""
+        term ``mu*||rows_var - rows0||^2/||rows0||^2`` (rows0 = the base table).
+
+        ``frozen``: bool ``[R]``, the variables held at their true rows -- the
+        masked step of ``engraft/replica/descend.py:262-271`` (``row_mask`` =
+        ``~frozen``): their gradient, pull term included, is zero (Adam still
+        decays their moments in the dense mode) and their rows are the base
+        table's again after the step."""
         dev = self.device
         rows = rows.to(device=dev, dtype=torch.int32).contiguous()
         n_pos, heads = rows.shape
+        fidx = rows0_f = None
+        if frozen is not None:
+            fz = torch.as_tensor(np.asarray(frozen.cpu() if isinstance(frozen, torch.Tensor) else frozen, dtype=bool))
+            if fz.dim() != 1 or fz.numel() != self.n:
+                raise ValueError(f"frozen must be a bool mask over the {self.n} variables")
+            if self.base is None:
+                raise ValueError("frozen rows are restored from the base table (DescentState(base=...))")
+            fidx = fz.nonzero().reshape(-1).to(dev)
+            if fidx.numel():
+                frozen_ids = self.ids[fidx]
+                rows0_f = self.base.gather(frozen_ids.reshape(-1, 1)).reshape(-1, self.dim)
+                # at rows0 the pull gradient is exactly zero; slots that read a frozen row carry none
+                self.master[fidx] = rows0_f
+                rows = torch.where(torch.isin(rows, frozen_ids), torch.full_like(rows, -1), rows)
+            else:
+                fidx = None
         if d_out.numel() != n_pos * heads * self.dim or not d_out.is_contiguous() or d_out.device != dev:
             raise ValueError(f"d_out must be contiguous on {dev} with {n_pos}x{heads * self.dim} elements")
         opt = _lib.EgAdam()
@@ -174,6 +205,11 @@ class DescentState:
                   ctypes.byref(st), ctypes.byref(opt), ctypes.byref(base) if base is not None else None,
                   _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
         self.step_count += 1  # only once the step is on its way (a rejected call leaves the count)
+        if fidx is not None:
+            # engraft/replica/descend.py:269-271: the frozen rows are restored after the step
+            self.master[fidx] = rows0_f
+            if self.quant is not None:
+                self._requant(rows0_f.contiguous(), fidx.to(torch.int32))
 
     def overlay(self, quantized: bool = True) -> DeviceOverlay:
         """The variables as a forward overlay: the requantised rows, or the fp32

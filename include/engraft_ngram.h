@@ -209,6 +209,16 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
                     int32_t heads, const eg_descent_state* state, const eg_adam* opt,
                     const eg_table* base, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The requantisation eg_descent_step applies after its update, on its own:
+ * fp32 rows src [n, dim] -> rows dst_rows[i] (i when dst_rows is NULL) of dst
+ * (Q8_0 or MXFP8); a dst_rows entry outside dst is skipped.  No counterpart in
+ * the reference, whose overlays stay fp32 (engraft/lens.py:167-198): it makes
+ * a descent state's quantised overlay valid before its first step and
+ * restores the frozen rows of the masked step (engraft/replica/descend.py:
+ * 262-271). */
+int eg_quantize_rows(const float* src, int64_t n, int32_t dim, const int32_t* dst_rows,
+                     const eg_table* dst, void* stream);
+
 /* ---- per-slot variables (OverlayEmb) ---------------------------------------
  * Variable index of each row id: out[i] = index[k] (k when index is NULL) for
  * rows[i] == ids[k], else -1; counts (optional, int64 [n_ids], accumulated)

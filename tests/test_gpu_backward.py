@@ -194,3 +194,92 @@ def test_updated_rows_read_back_through_forward_overlay(cuda):
         _, _, exp = FW.forward(spec, tokens, G.synth_fetch("q8_0", 92, 128), G.bf16_bits(res),
                                overlay=(ids, vals))
         G.assert_out_matches(G.bf16_bits(out), exp)
+
+
+@pytest.mark.parametrize("fmt,dim", [("q8_0", 128), ("mxfp8", 128), ("q8_0", 160), ("mxfp8", 64)])
+def test_quantised_overlay_valid_before_first_step(cuda, fmt, dim):
+    """A new state's requantised rows are its master rows under the
+    requantisation rule (bit-exact), so the overlay is whole before any step;
+    eg_quantize_rows with destination rows writes exactly those rows."""
+    import ctypes
+
+    from engraft_ngram_amd import _lib
+    from engraft_ngram_amd import descent as D
+    _say(f"quantise fmt={fmt} dim={dim}")
+    g = torch.Generator(device=cuda).manual_seed(101)
+    n = 3000
+    master = torch.randn((n, dim), generator=g, device=cuda) * 0.02
+    master[7, :32] = 0.0  # an all-zero block
+    ids = torch.arange(0, 3 * n, 3, dtype=torch.int32, device=cuda)
+    st = D.DescentState(ids, master.clone(), quant_fmt=fmt)
+    rule = F.quant_q8_0 if fmt == "q8_0" else F.quant_mxfp8
+    q_exp, s_exp = rule(master.cpu().numpy())
+    q_got = st.quant.payload.view(torch.uint8).cpu().numpy().reshape(n, dim)
+    s_got = st.quant.scales.view(torch.uint8).cpu().numpy().reshape(n, -1)
+    assert np.array_equal(q_got, q_exp.view(np.uint8))
+    assert np.array_equal(s_got, np.ascontiguousarray(s_exp).view(np.uint8).reshape(n, -1))
+    # scatter form: rows 5, 0 and 2999 rewritten from new values; -1 and n are skipped
+    src = torch.randn((5, dim), generator=g, device=cuda) * 0.05
+    dst = torch.tensor([5, -1, 0, n, n - 1], dtype=torch.int32, device=cuda)
+    tab = st.quant.c_table()
+    _lib.call("eg_quantize_rows", _lib.ptr(src), 5, dim, _lib.ptr(dst), ctypes.byref(tab), _lib.stream_ptr(cuda))
+    q2, s2 = rule(src.cpu().numpy())
+    q_now = st.quant.payload.view(torch.uint8).cpu().numpy().reshape(n, dim)
+    s_now = st.quant.scales.view(torch.uint8).cpu().numpy().reshape(n, -1)
+    q_ref = q_exp.view(np.uint8).copy()
+    s_ref = np.ascontiguousarray(s_exp).view(np.uint8).reshape(n, -1).copy()
+    for i, r in ((0, 5), (2, 0), (4, n - 1)):
+        q_ref[r] = q2.view(np.uint8)[i]
+        s_ref[r] = np.ascontiguousarray(s2).view(np.uint8).reshape(5, -1)[i]
+    assert np.array_equal(q_now, q_ref)
+    assert np.array_equal(s_now, s_ref)
+
+
+def test_frozen_rows_masked_step_against_torch_adam(cuda):
+    """The masked step (engraft/replica/descend.py:262-271): dense Adam with the
+    pull term, the frozen rows' gradient zeroed after the pull's backward, the
+    frozen rows restored to rows0 after the step -- against torch on the CPU.
+    The mask is off for the first step, so a frozen row carries moments."""
+    from engraft_ngram_amd import descent as D
+    spec = synthetic_spec(n_rows=16 * 2000, seed=111)
+    tab = G.device_table(spec, "q8_0", 16 * 2000, 128, seed=112)
+    tokens = synth.zipf_tokens(113, 2048, 3000)
+    rows = H.ngram_rows_np(spec, tokens)
+    st = D.DescentState.from_rows(tab, torch.from_numpy(rows.astype(np.int32)))
+    ids = st.ids.cpu().numpy()
+    rows0 = G.synth_fetch("q8_0", 112, 128)(ids)
+    rv = torch.from_numpy(rows0.copy()).requires_grad_(True)
+    r0 = torch.from_numpy(rows0.copy())
+    opt = torch.optim.Adam([rv], lr=1e-3)
+    mu = 0.1
+    rng = np.random.default_rng(114)
+    row_mask = rng.random(ids.size) < 0.5  # True: the row moves
+    frozen_t = torch.from_numpy(~row_mask)
+    for k in range(3):
+        sub = rows[k * 600:(k + 1) * 600]
+        d = (torch.randn((600, 2048), device=cuda) * 1e-3).to(torch.bfloat16)
+        masked = k > 0
+        st.step(d, torch.from_numpy(sub.astype(np.int32)), lr=1e-3, dense=True, mu=mu,
+                frozen=~row_mask if masked else None)
+        grad, _ = B.scatter_grad(d.float().cpu().numpy(), sub, ids)
+        opt.zero_grad()
+        rv.grad = torch.from_numpy(grad)
+        reg = mu * ((rv - r0).pow(2).sum() / r0.pow(2).sum().clamp_min(1e-12))
+        reg.backward()
+        if masked:
+            rv.grad[frozen_t] = 0.0
+        opt.step()
+        if masked:
+            with torch.no_grad():
+                rv[frozen_t] = r0[frozen_t]
+    got = st.master.cpu().numpy()
+    exp = rv.detach().numpy()
+    _rel_ok(got, exp)
+    assert np.array_equal(got[~row_mask], rows0[~row_mask])
+    state = opt.state[rv]
+    _rel_ok(st.m.cpu().numpy(), state["exp_avg"].numpy(), tol=1e-4)
+    # the frozen rows' requantised copy is the rule applied to rows0
+    q_exp, s_exp = F.quant_q8_0(rows0[~row_mask])
+    fz = np.nonzero(~row_mask)[0]
+    assert np.array_equal(st.quant.payload.cpu().numpy().view(np.int8)[fz], q_exp)
+    assert np.array_equal(st.quant.scales.cpu().numpy().view(np.float16)[fz], s_exp)
