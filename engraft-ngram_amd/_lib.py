@@ -99,8 +99,9 @@ SIGNATURES = {
                              c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_gate": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32,
                               c_int32, ctypes.c_float, c_void_p, c_void_p, c_void_p, c_void_p]),
-    "eg_ple_conv": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32, c_void_p,
-                              c_void_p, c_void_p, c_void_p, c_void_p]),
+    "eg_ple_conv": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32,
+                              c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "eg_ple_rms": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, ctypes.c_float, c_void_p, c_void_p]),
     "eg_forward_decode": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,
                                     c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_forward_timed": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,

@@ -8,12 +8,18 @@
 //                     gated_j = value * gate_j and its RMS norm (norm_conv):
 //                     normed [T, hc*n], s and gate [T, hc]
 //   ple_conv_kernel   one workgroup per 256 channels x 32 positions: the causal
-//                     depthwise
-//                     convolution over [history; normed] with dilation d,
-//                     SiLU, and out = (hidden + gated) + conv
+//                     depthwise convolution over [history; normed] with
+//                     dilation d, SiLU, and out = (hidden + gated) + conv
+//                     (gated + conv without hidden, conv alone without value);
+//                     with a shared history every position is a one-token
+//                     continuation of the same history (the batch of
+//                     engraft/lens.py ple_out_at)
+//   ple_rms_kernel    one workgroup per (row, stream j): x * 1/sqrt(mean(x^2)
+//                     + eps) * w_j, the per-stream RMS norm on its own
 //
-// fp32 throughout, the reference's operation order within each element; the
-// reductions are workgroup tree sums (a different association from torch's).
+// fp32 throughout, the reference's operation order within each element and no
+// contracted multiply-adds; the reductions are workgroup tree sums (a
+// different association from torch's).
 #include <string.h>
 
 #include "eg_common.h"
@@ -43,6 +49,7 @@ __global__ __launch_bounds__(kPleThreads) void ple_gate_kernel(
     const float* __restrict__ norm_key, const float* __restrict__ norm_query, const float* __restrict__ norm_conv,
     int hc, int n, float eps, float inv_sqrt_n, float* __restrict__ normed, float* __restrict__ s_out,
     float* __restrict__ gate_out) {
+#pragma clang fp contract(off)
   __shared__ float red[kPleThreads / 64];
   const int64_t t = blockIdx.x / hc;
   const int j = (int)(blockIdx.x - t * hc);
@@ -109,11 +116,14 @@ __global__ __launch_bounds__(kPleThreads) void ple_gate_kernel(
 // comes from HBM about once.
 constexpr int kConvRun = 32;
 
+// MODE 0: out = (hidden + value*gate) + conv; 1: value*gate + conv; 2: conv.
+template <int MODE, bool SHARED>
 __global__ __launch_bounds__(256) void ple_conv_kernel(const float* __restrict__ full, int64_t hist_rows, int64_t T,
                                                        int hc, int n, const float* __restrict__ conv_w, int taps,
                                                        int dil, const float* __restrict__ hidden,
                                                        const float* __restrict__ value,
                                                        const float* __restrict__ gate, float* __restrict__ out) {
+#pragma clang fp contract(off)
   const int C = hc * n;
   const int n_cblk = (C + 255) / 256;
   const int cblk = (int)(blockIdx.x % n_cblk);
@@ -135,22 +145,65 @@ __global__ __launch_bounds__(256) void ple_conv_kernel(const float* __restrict__
 #pragma unroll
     for (int k = 0; k < kMaxTaps; ++k) {
       if (k < taps) {
-        const int64_t src = hist_rows + t - (int64_t)(taps - 1 - k) * dil;
+        const int64_t back = (int64_t)(taps - 1 - k) * dil;
+        const int64_t src = SHARED ? (back == 0 ? hist_rows + t : hist_rows - back) : hist_rows + t - back;
         ok[k] = src >= 0;
         x[k] = full[(ok[k] ? src : 0) * C + c];
       }
     }
     const int64_t o = t * C + c;
-    const float hv = hidden[o];
-    const float vv = value[t * n + i];
-    const float gj = gate[t * hc + j];
+    float hv = 0.0f, vv = 0.0f, gj = 0.0f;
+    if constexpr (MODE == 0) hv = hidden[o];
+    if constexpr (MODE <= 1) {
+      vv = value[t * n + i];
+      gj = gate[t * hc + j];
+    }
     float acc = 0.0f;
 #pragma unroll
     for (int k = 0; k < kMaxTaps; ++k)
       if (k < taps && ok[k]) acc += x[k] * w[k];
     const float silu = acc / (1.0f + expf(-acc));
-    out[o] = (hv + vv * gj) + silu;
+    if constexpr (MODE == 0) out[o] = (hv + vv * gj) + silu;
+    else if constexpr (MODE == 1) out[o] = vv * gj + silu;
+    else out[o] = silu;
   }
+}
+
+// The per-stream RMS norm, with the reductions of ple_gate_kernel (same thread
+// layout and tree), so it reproduces that kernel's normed values bit for bit.
+__global__ __launch_bounds__(kPleThreads) void ple_rms_kernel(const float* __restrict__ x, int hc, int n, float eps,
+                                                            const float* __restrict__ w, float* __restrict__ out) {
+#pragma clang fp contract(off)
+  __shared__ float red[kPleThreads / 64];
+  const int64_t t = blockIdx.x / hc;
+  const int j = (int)(blockIdx.x - t * hc);
+  const int tid = threadIdx.x;
+  const int per = (n + kPleThreads - 1) / kPleThreads;
+  const int64_t row = (t * hc + j) * n;
+  float v[kPleMaxPer];
+#pragma unroll
+  for (int m = 0; m < kPleMaxPer; ++m)
+    if (m < per) v[m] = x[row + min(tid + m * kPleThreads, n - 1)];
+  float sq = 0.0f;
+#pragma unroll
+  for (int m = 0; m < kPleMaxPer; ++m) {
+    if (!(m < per && tid + m * kPleThreads < n)) v[m] = 0.0f;
+    sq += v[m] * v[m];
+  }
+  const float r = 1.0f / sqrtf(block_sum(sq, red) / (float)n + eps);
+#pragma unroll
+  for (int m = 0; m < kPleMaxPer; ++m) {
+    const int i = tid + m * kPleThreads;
+    if (m < per && i < n) out[row + i] = (v[m] * r) * w[j * n + i];
+  }
+}
+
+template <int MODE, bool SHARED>
+static void launch_conv(dim3 grid, hipStream_t st, const float* full, int64_t hist_rows, int64_t n_pos, int hc, int n,
+                        const float* conv_w, int taps, int dil, const float* hidden, const float* value,
+                        const float* gate, float* out) {
+  hipLaunchKernelGGL((ple_conv_kernel<MODE, SHARED>), grid, dim3(256), 0, st, full, hist_rows, n_pos, hc, n, conv_w,
+                     taps, dil, hidden, value, gate, out);
 }
 
 }  // namespace eg
@@ -176,19 +229,41 @@ int eg_ple_gate(const float* key, const float* value, const float* hidden, const
 }
 
 int eg_ple_conv(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
-                const float* conv_w, int32_t taps, int32_t dilation, const float* hidden, const float* value,
-                const float* gate, float* out, void* stream) {
+                const float* conv_w, int32_t taps, int32_t dilation, int32_t shared_history, const float* hidden,
+                const float* value, const float* gate, float* out, void* stream) {
   EG_CHECK_ARG(n_pos >= 0 && hist_rows >= 0 && hc >= 1 && n_embd >= 1 && taps >= 1 && taps <= 8 && dilation >= 1,
                "n_pos=%lld hist_rows=%lld hc=%d n_embd=%d taps=%d dilation=%d", (long long)n_pos,
                (long long)hist_rows, hc, n_embd, taps, dilation);
   EG_CHECK_ARG(n_pos < (1LL << 31) && (int64_t)hc * n_embd < (1LL << 31), "too many elements");
-  EG_CHECK_ARG(n_pos == 0 || (full && conv_w && hidden && value && gate && out), "NULL argument");
+  EG_CHECK_ARG(n_pos == 0 || (full && conv_w && out), "NULL argument");
+  EG_CHECK_ARG(value != nullptr || hidden == nullptr, "hidden without value");
+  EG_CHECK_ARG(value == nullptr || gate != nullptr, "value without gate");
   if (n_pos == 0) return EG_OK;
   const int64_t blocks = (int64_t)((hc * n_embd + 255) / 256) * ((n_pos + kConvRun - 1) / kConvRun);
   EG_CHECK_ARG(blocks < (1LL << 32), "too many elements");
-  hipLaunchKernelGGL(ple_conv_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, full,
-                     hist_rows, n_pos, hc, n_embd, conv_w, taps, dilation, hidden, value, gate, out);
+  const dim3 grid((unsigned)blocks);
+  hipStream_t st = (hipStream_t)stream;
+  const int mode = hidden ? 0 : (value ? 1 : 2);
+  const bool sh = shared_history != 0;
+#define EG_CONV(M, S) launch_conv<M, S>(grid, st, full, hist_rows, n_pos, hc, n_embd, conv_w, taps, dilation, \
+                                          hidden, value, gate, out)
+  if (mode == 0) sh ? EG_CONV(0, true) : EG_CONV(0, false);
+  else if (mode == 1) sh ? EG_CONV(1, true) : EG_CONV(1, false);
+  else sh ? EG_CONV(2, true) : EG_CONV(2, false);
+#undef EG_CONV
   return launch_status("ple_conv_kernel");
+}
+
+int eg_ple_rms(const float* x, int64_t n_rows, int32_t hc, int32_t n_embd, const float* weight, float eps, float* out,
+               void* stream) {
+  EG_CHECK_ARG(n_rows >= 0 && n_rows * hc < (1LL << 31), "n_rows=%lld", (long long)n_rows);
+  EG_CHECK_ARG(hc >= 1 && hc <= 64 && n_embd >= 1 && n_embd <= kPleThreads * kPleMaxPer,
+               "hc=%d n_embd=%d (n_embd <= %d)", hc, n_embd, kPleThreads * kPleMaxPer);
+  EG_CHECK_ARG(n_rows == 0 || (x && weight && out), "NULL argument");
+  if (n_rows == 0) return EG_OK;
+  hipLaunchKernelGGL(ple_rms_kernel, dim3((unsigned)(n_rows * hc)), dim3(kPleThreads), 0, (hipStream_t)stream, x, hc,
+                     n_embd, eps, weight, out);
+  return launch_status("ple_rms_kernel");
 }
 
 }  // extern "C"

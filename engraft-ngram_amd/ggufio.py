@@ -10,14 +10,18 @@ the same file layout from the published GGUF format (v2/v3, little endian):
     padding to general.alignment (default 32), then the tensor data
 
 with ``string = u64 length + UTF-8 bytes`` and array values ``u32 item type +
-u64 count + items``.  Only the metadata is parsed; tensor data stays in the
-file and is read by offset.
+u64 count + items``.  ``read_gguf`` parses the metadata only (tensor data stays
+in the file, read by offset); ``read_tensor_f32`` reads one F32 / F16 / Q8_0
+tensor, ``read_rms_eps`` the RMS-norm epsilon of a (split) model file.
 """
 from __future__ import annotations
 
 import dataclasses
+import re
 import struct
 from pathlib import Path
+
+import numpy as np
 
 GGUF_MAGIC = b"GGUF"
 GGML_TYPE_IQ4_NL = 20
@@ -103,3 +107,61 @@ def read_gguf(path: str | Path) -> GGUFFile:
         data_start = (pos + alignment - 1) // alignment * alignment
     tensors = {n: TensorInfo(n, d, t, data_start + o) for n, d, t, o in infos}
     return GGUFFile(path, version, fields, tensors, alignment)
+
+
+# ggml tensor types read by read_tensor_f32: (block values, block bytes)
+GGML_TYPE_F32 = 0
+GGML_TYPE_F16 = 1
+GGML_TYPE_Q8_0 = 8
+_BLOCKS = {GGML_TYPE_F32: (1, 4), GGML_TYPE_F16: (1, 2), GGML_TYPE_Q8_0: (32, 34)}
+
+
+def read_tensor_f32(gf: GGUFFile, name: str, expected_type: int | None = None) -> np.ndarray:
+    """Tensor ``name`` as f32 numpy, shaped with ne0 last (``[ne1, ne0]`` for a
+    matrix).  F32, F16 and Q8_0 (blocks of an fp16 scale d and 32 int8 q,
+    value d*q) are read.  ``expected_type``: raise ValueError on another type
+    (``engraft/lens.py:236-244``)."""
+    if name not in gf.tensors:
+        raise KeyError(f"{name}: tensor missing in {gf.path}")
+    info = gf.tensors[name]
+    if expected_type is not None and info.ggml_type != expected_type:
+        raise ValueError(f"{name}: expected ggml type {expected_type}, got {info.ggml_type}")
+    if info.ggml_type not in _BLOCKS:
+        raise ValueError(f"{name}: ggml type {info.ggml_type} is not read (F32, F16, Q8_0)")
+    n = 1
+    for d in info.shape:
+        n *= int(d)
+    per, nbytes = _BLOCKS[info.ggml_type]
+    if n % per:
+        raise ValueError(f"{name}: {n} values are not whole blocks of {per}")
+    raw = np.fromfile(gf.path, dtype=np.uint8, count=n // per * nbytes, offset=info.data_offset)
+    if raw.size != n // per * nbytes:
+        raise ValueError(f"{name}: tensor data past the end of {gf.path}")
+    if info.ggml_type == GGML_TYPE_F32:
+        vals = raw.view("<f4").astype(np.float32)
+    elif info.ggml_type == GGML_TYPE_F16:
+        vals = raw.view("<f2").astype(np.float32)
+    else:
+        blocks = raw.reshape(-1, 34)
+        d = blocks[:, :2].copy().view("<f2").astype(np.float32)  # [n_blocks, 1]
+        q = blocks[:, 2:].view(np.int8).astype(np.float32)
+        vals = (q * d).reshape(-1)
+    return vals.reshape(tuple(int(x) for x in reversed(info.shape)))
+
+
+def read_rms_eps(path: str | Path) -> float:
+    """``qwen4exp.attention.layer_norm_rms_epsilon`` of a model file; for a
+    split file (``…-NNNNN-of-MMMMM.gguf``) it is read from shard 1, which alone
+    holds the model metadata (``engraft/lens.py:490-518``)."""
+    path = Path(path)
+    m = re.search(r"(\d{5})-of-(\d{5})", path.name)
+    src = path
+    if m is not None:
+        src = path.with_name(path.name[:m.start(1)] + "00001" + path.name[m.end(1):])
+        if not src.exists():
+            raise FileNotFoundError(f"eps not given explicitly and shard 1 not found: {src}")
+    key = "qwen4exp.attention.layer_norm_rms_epsilon"
+    fields = read_gguf(src).fields
+    if key not in fields:
+        raise KeyError(f"{key}: missing in {src}")
+    return float(fields[key])

@@ -11,7 +11,9 @@ Forward:
   ``[history; normed]``, SiLU, and ``out = hidden + gated + conv``.
 
 The result -- the output and the new history -- is differentiable in emb,
-hidden, the history and the weights.  The backward recomputes the block with
+hidden, the history and the weights.  ``PleReplica`` (below) is the same block
+with its weights read from the model GGUF, method for method as the
+reference's numpy replica.  The backward recomputes the block with
 torch operations on the device and differentiates that; the forward values are
 the HIP kernels'.  ``detach_value`` / ``detach_gate`` change only the backward,
 as in the reference.
@@ -20,6 +22,7 @@ from __future__ import annotations
 
 import dataclasses
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -92,7 +95,7 @@ class _PleFn(torch.autograd.Function):
         _lib.call("eg_ple_gate", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden32), _lib.ptr(nk32), _lib.ptr(nq32),
                   _lib.ptr(nc32), t_len, hc, n, float(eps), _lib.ptr(full[h0:]), _lib.ptr(s), _lib.ptr(gate), st)
         out = torch.empty((t_len, hc, n), **f32)
-        _lib.call("eg_ple_conv", _lib.ptr(full), h0, t_len, hc, n, _lib.ptr(conv32), conv32.shape[1], int(dil),
+        _lib.call("eg_ple_conv", _lib.ptr(full), h0, t_len, hc, n, _lib.ptr(conv32), conv32.shape[1], int(dil), 0,
                   _lib.ptr(hidden32), _lib.ptr(value), _lib.ptr(gate), _lib.ptr(out), st)
         hist_len = (conv32.shape[1] - 1) * int(dil)
         new_hist = (full[-hist_len:] if hist_len > 0 else full[:0]).reshape(-1, hc, n).to(hidden.dtype).clone()
@@ -146,3 +149,188 @@ def ple_forward(emb: torch.Tensor, hidden: torch.Tensor, w: PleWeights, hist: to
         diag["gated_norm"] = gated_norm.clone()
         diag["hidden_norm"] = hidden.detach().norm(dim=-1).clone()
     return out, new_hist
+
+
+# ---------------------------------------------------------------------------------------------
+# PleReplica (engraft/lens.py:221-415): the block with weights read from a model GGUF
+# ---------------------------------------------------------------------------------------------
+
+def _ple_tensor_types():
+    from .ggufio import GGML_TYPE_F32, GGML_TYPE_Q8_0
+    return {"ple_key": GGML_TYPE_Q8_0, "ple_value": GGML_TYPE_Q8_0, "ple_norm_key": GGML_TYPE_F32,
+            "ple_norm_query": GGML_TYPE_F32, "ple_norm_conv": GGML_TYPE_F32, "ple_conv1d": GGML_TYPE_F32}
+
+
+class PleReplica:
+    """The PLE block of one layer on the device, method for method as
+    ``engraft.lens.PleReplica`` (``engraft/lens.py:221-415``).
+
+    Inputs are numpy arrays or tensors; results are f32 tensors on the device
+    (the reference returns numpy: ``.cpu().numpy()`` gives the same layout).
+    ``key``/``value`` are library GEMMs plus ``eg_ple_rms``; ``gate``,
+    ``gated`` and ``ple_out`` run ``eg_ple_gate`` and ``eg_ple_conv``;
+    ``conv_out`` runs ``eg_ple_rms`` and ``eg_ple_conv``; ``ple_out_at`` runs
+    ``eg_ple_conv`` with one history shared by the batch.  The reference fixes
+    4 streams of 2560 values, 4 taps and dilation 3; here the widths come from
+    the tensors (``hc`` streams) and the dilation is a parameter.
+
+    Attributes as the reference's: ``w_key [hc*n, n]``, ``w_value [n, n]``,
+    ``norm_key``/``norm_query``/``norm_conv [hc, n]``, ``conv1d [hc, n, taps]``
+    (in place: zeroing it switches the convolution off, as
+    ``tests/test_lens.py:336-342`` does) and ``eps``."""
+
+    def __init__(self, gguf_path, eps: float | None = None, *, device="cuda", hc: int = 4, dilation: int = 3,
+                 layer: int = 1):
+        from .ggufio import read_gguf, read_rms_eps, read_tensor_f32
+        gf = read_gguf(gguf_path)
+        types = _ple_tensor_types()
+        ld = {k: read_tensor_f32(gf, f"blk.{layer}.{k}.weight", t) for k, t in types.items()}
+        if eps is None:
+            eps = read_rms_eps(gguf_path)
+        self._setup(ld["ple_key"], ld["ple_value"], ld["ple_norm_key"], ld["ple_norm_query"], ld["ple_norm_conv"],
+                    ld["ple_conv1d"], float(eps), hc, dilation, device)
+        self.gguf_path = gguf_path
+
+    @classmethod
+    def from_weights(cls, w: PleWeights, eps: float, *, hc: int = 4, dilation: int = 3, device="cuda"):
+        obj = cls.__new__(cls)
+        obj._setup(w.w_key, w.w_value, w.norm_key, w.norm_query, w.norm_conv, w.conv1d, float(eps), hc, dilation,
+                   device)
+        obj.gguf_path = None
+        return obj
+
+    def _setup(self, w_key, w_value, nk, nq, nc, conv, eps, hc, dilation, device):
+        f = lambda x: torch.as_tensor(x, dtype=torch.float32).to(device).contiguous()
+        w_value = f(w_value)
+        n = int(w_value.shape[0])
+        if w_value.dim() != 2 or w_value.shape[1] != n:
+            raise ValueError(f"ple_value: unexpected shape {tuple(w_value.shape)}")
+        w_key = f(w_key)
+        if tuple(w_key.shape) != (hc * n, n):
+            raise ValueError(f"ple_key: unexpected shape {tuple(w_key.shape)}, expected {(hc * n, n)}")
+        norms = []
+        for name, arr in (("ple_norm_key", nk), ("ple_norm_query", nq), ("ple_norm_conv", nc)):
+            a = f(arr)
+            if a.numel() != hc * n:
+                raise ValueError(f"{name}: unexpected shape {tuple(a.shape)}")
+            norms.append(a.reshape(hc, n))
+        conv = f(conv)
+        if conv.dim() not in (2, 3) or conv.numel() % (hc * n) or not 1 <= conv.numel() // (hc * n) <= 8:
+            raise ValueError(f"ple_conv1d: unexpected shape {tuple(conv.shape)}")
+        self.hc, self.n_embd, self.dilation, self.eps = hc, n, int(dilation), float(eps)
+        self.device = w_value.device
+        self.w_key, self.w_value = w_key, w_value
+        self.norm_key, self.norm_query, self.norm_conv = norms
+        self.conv1d = conv.reshape(hc, n, -1)  # [stream, channel, tap], the kernel's [hc*n, taps] memory
+
+    # ---- pieces ---------------------------------------------------------------------------
+    def _in(self, x, *shape_tail) -> torch.Tensor:
+        t = torch.as_tensor(x, dtype=torch.float32).to(self.device).contiguous()
+        if tuple(t.shape[1:]) != shape_tail:
+            raise ValueError(f"expected [T, {', '.join(map(str, shape_tail))}], got {tuple(t.shape)}")
+        return t
+
+    def _rms(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        out = torch.empty_like(x)
+        _lib.call("eg_ple_rms", _lib.ptr(x), x.shape[0], self.hc, self.n_embd, _lib.ptr(weight), self.eps,
+                  _lib.ptr(out), _lib.stream_ptr(self.device))
+        return out
+
+    def _gate_pass(self, emb: torch.Tensor, hidden: torch.Tensor):
+        """value [T, n], normed [T, hc*n], s and gate [T, hc] (eg_ple_gate)."""
+        t_len = emb.shape[0]
+        key = (emb @ self.w_key.T).contiguous()
+        value = (emb @ self.w_value.T).contiguous()
+        f32 = dict(dtype=torch.float32, device=self.device)
+        normed = torch.empty((t_len, self.hc * self.n_embd), **f32)
+        s = torch.empty((t_len, self.hc), **f32)
+        gate = torch.empty((t_len, self.hc), **f32)
+        _lib.call("eg_ple_gate", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden), _lib.ptr(self.norm_key),
+                  _lib.ptr(self.norm_query), _lib.ptr(self.norm_conv), t_len, self.hc, self.n_embd, self.eps,
+                  _lib.ptr(normed), _lib.ptr(s), _lib.ptr(gate), _lib.stream_ptr(self.device))
+        return value, normed, s, gate
+
+    def _conv(self, full: torch.Tensor, hist_rows: int, n_pos: int, value=None, gate=None,
+              shared: bool = False) -> torch.Tensor:
+        out = torch.empty((n_pos, self.hc, self.n_embd), dtype=torch.float32, device=self.device)
+        taps = self.conv1d.shape[2]
+        _lib.call("eg_ple_conv", _lib.ptr(full), hist_rows, n_pos, self.hc, self.n_embd, _lib.ptr(self.conv1d), taps,
+                  self.dilation, 1 if shared else 0, None, _lib.ptr(value), _lib.ptr(gate), _lib.ptr(out),
+                  _lib.stream_ptr(self.device))
+        return out
+
+    # ---- the reference's methods ----------------------------------------------------------
+    def key(self, emb) -> torch.Tensor:
+        """``[T, n] -> [T, hc, n]``, RMS-normalised per stream (``lens.py:289-294``)."""
+        emb = self._in(emb, self.n_embd)
+        raw = (emb @ self.w_key.T).contiguous()
+        return self._rms(raw, self.norm_key).reshape(-1, self.hc, self.n_embd)
+
+    def value(self, emb) -> torch.Tensor:
+        """``[T, n] -> [T, n]`` (``lens.py:296-299``)."""
+        return self._in(emb, self.n_embd) @ self.w_value.T
+
+    def gate(self, emb, hidden) -> torch.Tensor:
+        """``[T, hc]`` (``lens.py:301-312``)."""
+        return self._gate_pass(self._in(emb, self.n_embd), self._in(hidden, self.hc, self.n_embd))[3]
+
+    def gated(self, emb, hidden) -> torch.Tensor:
+        """``[T, hc, n]`` = value replicated over the streams x gate (``lens.py:314-318``)."""
+        value, _, _, gate = self._gate_pass(self._in(emb, self.n_embd), self._in(hidden, self.hc, self.n_embd))
+        return value[:, None, :] * gate[:, :, None]
+
+    def conv_out(self, gated_seq) -> torch.Tensor:
+        """norm_conv, the dilated causal convolution over zero history, SiLU
+        (``lens.py:320-339``)."""
+        g = self._in(gated_seq, self.hc, self.n_embd)
+        normed = self._rms(g, self.norm_conv)
+        return self._conv(normed, 0, g.shape[0])
+
+    def ple_out(self, emb_seq, hidden_seq) -> torch.Tensor:
+        """``gated + conv_out(gated)`` over a whole sequence (``lens.py:341-345``);
+        the caller adds ``hidden``."""
+        emb = self._in(emb_seq, self.n_embd)
+        value, normed, _, gate = self._gate_pass(emb, self._in(hidden_seq, self.hc, self.n_embd))
+        return self._conv(normed, 0, emb.shape[0], value, gate)
+
+    def ple_out_at(self, emb_t, emb_seq, hidden_seq, t: int) -> torch.Tensor:
+        """``[B, hc, n]``: ``ple_out[t]`` with ``emb_seq[t]`` replaced by each row of
+        ``emb_t [B, n]``, the convolution history from the true sequence
+        (``lens.py:347-385``)."""
+        emb_t = self._in(emb_t, self.n_embd)
+        emb_seq = self._in(emb_seq, self.n_embd)
+        hidden_seq = self._in(hidden_seq, self.hc, self.n_embd)
+        if not 0 <= t < emb_seq.shape[0]:
+            raise ValueError(f"t={t} outside the sequence of {emb_seq.shape[0]} positions")
+        b = emb_t.shape[0]
+        h0 = min(t, (self.conv1d.shape[2] - 1) * self.dilation)
+        hid_b = hidden_seq[t].expand(b, self.hc, self.n_embd).contiguous()
+        value, normed_b, _, gate = self._gate_pass(emb_t, hid_b)
+        if h0:
+            normed_h = self._gate_pass(emb_seq[t - h0:t].contiguous(), hidden_seq[t - h0:t].contiguous())[1]
+            full = torch.cat([normed_h, normed_b], dim=0)
+        else:
+            full = normed_b
+        return self._conv(full, h0, b, value, gate, shared=True)
+
+    def jacobian_out(self, emb_seq, hidden_seq, t: int, coords=None, step: float = 1e-3) -> torch.Tensor:
+        """f64 ``[hc*n, n_coords]``: d ple_out[t] / d emb[t][coords] by central
+        differences of ``ple_out_at``, 512 coordinates per batch
+        (``lens.py:387-415``)."""
+        emb_seq = self._in(emb_seq, self.n_embd)
+        hidden_seq = self._in(hidden_seq, self.hc, self.n_embd)
+        coords = torch.arange(self.n_embd) if coords is None else torch.as_tensor(np.asarray(coords),
+                                                                                   dtype=torch.int64)
+        coords = coords.to(self.device)
+        jac = torch.empty((self.hc * self.n_embd, coords.numel()), dtype=torch.float64, device=self.device)
+        for lo in range(0, coords.numel(), 512):
+            idx = coords[lo:lo + 512]
+            m = idx.numel()
+            plus = emb_seq[t].expand(m, self.n_embd).clone()
+            minus = plus.clone()
+            r = torch.arange(m, device=self.device)
+            plus[r, idx] += step
+            minus[r, idx] -= step
+            out = self.ple_out_at(torch.cat([plus, minus]), emb_seq, hidden_seq, t).reshape(2 * m, -1)
+            jac[:, lo:lo + m] = ((out[:m].double() - out[m:].double()) / (2.0 * step)).T
+        return jac

@@ -31,6 +31,7 @@
  *                                                    engraft/replica/model.py:473-495
  *   eg_ple_gate, eg_ple_conv  ple_forward after its two projections
  *                                                    engraft/replica/layers.py:565-626
+ *   eg_ple_rms, eg_ple_conv's other modes  PleReplica engraft/lens.py:221-385
  */
 #ifndef ENGRAFT_NGRAM_H
 #define ENGRAFT_NGRAM_H
@@ -263,10 +264,23 @@ int eg_ple_gate(const float* key, const float* value, const float* hidden, const
 /* out = (hidden + value*gate) + silu(conv), conv[t, c] = sum_k conv_w[c, k] *
  * full[hist_rows + t - (taps-1-k)*dilation, c] over the rows that exist
  * (causal_depthwise_conv, layers.py:257-293); full f32 [hist_rows + n_pos,
- * hc*n_embd] = [history; normed]; conv_w f32 [hc*n_embd, taps], taps <= 8. */
+ * hc*n_embd] = [history; normed]; conv_w f32 [hc*n_embd, taps], taps <= 8.
+ * hidden NULL: out = value*gate + silu(conv) (PleReplica.ple_out,
+ * engraft/lens.py:334-341); value (and hidden) NULL: out = silu(conv)
+ * (PleReplica.conv_out, lens.py:309-332).  shared_history != 0: every
+ * position t is its own one-token continuation of the history, the tap at
+ * distance 0 reading row hist_rows + t and the others row hist_rows - distance
+ * (PleReplica.ple_out_at, lens.py:341-385). */
 int eg_ple_conv(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
-                const float* conv_w, int32_t taps, int32_t dilation, const float* hidden,
-                const float* value, const float* gate, float* out, void* stream);
+                const float* conv_w, int32_t taps, int32_t dilation, int32_t shared_history,
+                const float* hidden, const float* value, const float* gate, float* out, void* stream);
+
+/* Per-stream RMS norm: out[r, j, :] = x[r, j, :] / sqrt(mean(x[r, j, :]^2) + eps)
+ * * weight[j, :], x and out f32 [n_rows, hc, n_embd], weight f32 [hc, n_embd]
+ * (PleReplica._rmsnorm_per_stream, engraft/lens.py:282-287; the reductions of
+ * eg_ple_gate, so applied to value*gate it gives eg_ple_gate's normed). */
+int eg_ple_rms(const float* x, int64_t n_rows, int32_t hc, int32_t n_embd, const float* weight, float eps,
+               float* out, void* stream);
 
 #ifdef __cplusplus
 }

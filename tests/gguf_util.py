@@ -66,3 +66,43 @@ def ple_table_file(path, spec, raw_heads: list[np.ndarray], image_token_id: int 
     tensors = [(f"ple_ngram_embd.{h}.weight", (160, int(r.shape[0])), 20, np.ascontiguousarray(r).tobytes())
                for h, r in enumerate(raw_heads)]
     return write_gguf(path, kv, tensors)
+
+
+def q8_0_blocks(x: np.ndarray) -> tuple[bytes, np.ndarray]:
+    """GGML Q8_0 bytes of ``x`` (blocks of 32 along the last axis: fp16 d, then
+    32 int8 q) and their value d*q, the closed form a reader must give."""
+    from oracle import formats as F
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    flat = x.reshape(-1, 32)
+    q, d16 = F.quant_q8_0(flat.reshape(-1, 32))  # one block per row
+    raw = np.concatenate([d16.reshape(-1, 1).view(np.uint8), q.view(np.uint8)], axis=1)  # [n_blocks, 34]
+    vals = (q.astype(np.float32) * d16.astype(np.float32)).reshape(x.shape)
+    return raw.tobytes(), vals
+
+
+def ple_model_files(dir_path, w: dict, eps: float, layer: int = 1, split: bool = True):
+    """A model GGUF holding ``blk.<layer>.ple_*`` (key/value Q8_0, the rest F32)
+    -- as shard 2 of a 2-shard split whose shard 1 holds the metadata, or one
+    file with both.  Returns (path to pass, dequantised weights dict)."""
+    from pathlib import Path
+    dir_path = Path(dir_path)
+    kb, kv_vals = q8_0_blocks(w["w_key"])
+    vb, vv_vals = q8_0_blocks(w["w_value"])
+    f32 = lambda a: np.ascontiguousarray(a, dtype=np.float32)
+    dims = lambda a: tuple(reversed(np.asarray(a).shape))  # ne0 first
+    tensors = [(f"blk.{layer}.ple_key.weight", dims(w["w_key"]), 8, kb),
+               (f"blk.{layer}.ple_value.weight", dims(w["w_value"]), 8, vb)]
+    for name in ("norm_key", "norm_query", "norm_conv", "conv1d"):
+        tensors.append((f"blk.{layer}.ple_{name}.weight", dims(w[name]), 0, f32(w[name]).tobytes()))
+    meta = [("general.architecture", STRING, "qwen4exp"),
+            ("qwen4exp.attention.layer_norm_rms_epsilon", F32, float(eps))]
+    if split:
+        write_gguf(dir_path / "m-00001-of-00002.gguf", meta + [("split.count", U16, 2)], [])
+        path = dir_path / "m-00002-of-00002.gguf"
+        write_gguf(path, [("split.count", U16, 2)], tensors)
+    else:
+        path = dir_path / "m.gguf"
+        write_gguf(path, meta, tensors)
+    vals = dict(w)
+    vals["w_key"], vals["w_value"] = kv_vals, vv_vals
+    return path, vals

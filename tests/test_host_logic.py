@@ -136,3 +136,41 @@ def test_gguf_reader_layout(tmp_path):
     (tmp_path / "bad.gguf").write_bytes(b"GGML" + b"\0" * 40)
     with pytest.raises(ValueError):
         read_gguf(tmp_path / "bad.gguf")
+
+
+def _ple_w(hc=4, n=64, taps=4, seed=0):
+    rng = np.random.default_rng(seed)
+    f = lambda *s, sc=1.0: (rng.standard_normal(s) * sc).astype(np.float32)
+    return {"w_key": f(hc * n, n, sc=n ** -0.5), "w_value": f(n, n, sc=n ** -0.5), "norm_key": 1 + f(hc * n, sc=0.1),
+            "norm_query": 1 + f(hc * n, sc=0.1), "norm_conv": 1 + f(hc * n, sc=0.1), "conv1d": f(hc * n, taps)}
+
+
+def test_gguf_ple_weights_reader(tmp_path):
+    """The PLE weights of a model GGUF (engraft/lens.py:229-266): Q8_0 and F32
+    tensors read to their closed-form values (d*q), the type check, and the
+    RMS epsilon from shard 1 of a split (lens.py:490-518)."""
+    from engraft_ngram_amd import ggufio
+    from tests import gguf_util as GU
+    w = _ple_w()
+    path, vals = GU.ple_model_files(tmp_path, w, 1e-6)
+    gf = ggufio.read_gguf(path)
+    for name, ref in vals.items():
+        got = ggufio.read_tensor_f32(gf, f"blk.1.ple_{name.replace('w_', '')}.weight")
+        assert got.shape == np.asarray(ref).shape
+        assert np.array_equal(got, ref)
+    # Q8_0 values are within half a step of the source
+    assert np.abs(vals["w_value"] - w["w_value"]).max() <= np.abs(w["w_value"]).max() / 127
+    with pytest.raises(ValueError):
+        ggufio.read_tensor_f32(gf, "blk.1.ple_key.weight", expected_type=ggufio.GGML_TYPE_F32)
+    with pytest.raises(KeyError):
+        ggufio.read_tensor_f32(gf, "blk.2.ple_key.weight")
+    assert ggufio.read_rms_eps(path) == np.float32(1e-6)
+    (tmp_path / "one").mkdir()
+    one, _ = GU.ple_model_files(tmp_path / "one", w, 1e-5, split=False)
+    assert ggufio.read_rms_eps(one) == np.float32(1e-5)
+    (tmp_path / "m-00001-of-00002.gguf").unlink()
+    with pytest.raises(FileNotFoundError):
+        ggufio.read_rms_eps(path)
+    GU.write_gguf(tmp_path / "m-00001-of-00002.gguf", [("general.architecture", GU.STRING, "qwen4exp")], [])
+    with pytest.raises(KeyError):
+        ggufio.read_rms_eps(path)
