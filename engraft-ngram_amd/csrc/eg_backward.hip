@@ -6,8 +6,9 @@
 //            given directly); every variable's slot count is accumulated
 //   offsets  exclusive scan of the counts; variables hit by more than 32
 //            slots are listed
-//   fill     every slot id is placed in its variable's range (CSR); the order
-//            inside a range is whatever the atomics gave
+//   fill     every slot id is written at its variable's range start plus the
+//            rank its counting atomic returned (CSR, no atomics); the order
+//            inside a range is whatever the counting atomics gave
 //   order    each range is put in ascending slot order inside the reduction:
 //            ranges of at most 32 slots by a 32-lane bitonic network on
 //            registers, longer ones by their workgroup (LDS bitonic network,
@@ -70,12 +71,13 @@ __global__ __launch_bounds__(256) void index_build_kernel(const int32_t* __restr
 // Keys + per-variable counts
 // ---------------------------------------------------------------------------
 // MODE 0: search the sorted ids; 1: probe the row index; 2: rows already hold
-// variable indices (< 0 or >= n_var: no variable).  cnt[k] += the slots of k.
+// variable indices (< 0 or >= n_var: no variable).  cnt[k] += the slots of k;
+// ranks[s] = the count of k before slot s was counted (its place in k's range).
 template <int MODE>
 __global__ __launch_bounds__(kTileThreads) void keys_count_kernel(
     const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ ids, int64_t n_var, int split_shift,
     const unsigned long long* __restrict__ index, int index_bits, uint32_t* __restrict__ keys,
-    uint32_t* __restrict__ cnt) {
+    uint32_t* __restrict__ ranks, uint32_t* __restrict__ cnt) {
   __shared__ int32_t spl[kSplitMax];
   const int tid = threadIdx.x;
   const int ns = MODE == 0 ? (int)((n_var + (1LL << split_shift) - 1) >> split_shift) : 0;
@@ -169,7 +171,7 @@ __global__ __launch_bounds__(kTileThreads) void keys_count_kernel(
     if (!ok[r]) continue;
     const int64_t idx = (int64_t)blockIdx.x * kTile + r * kTileThreads + tid;
     keys[idx] = key[r];
-    if ((int64_t)key[r] < n_var) atomicAdd(&cnt[key[r]], 1u);
+    if ((int64_t)key[r] < n_var) ranks[idx] = atomicAdd(&cnt[key[r]], 1u);
   }
 }
 
@@ -256,12 +258,13 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply(uint32_t* __restrict_
 // CSR fill and the ordering of long ranges
 // ---------------------------------------------------------------------------
 // off[k] enters as variable k's first position and leaves as its end.
-__global__ __launch_bounds__(256) void fill_kernel(const uint32_t* __restrict__ keys, int64_t n, int64_t n_var,
-                                                   uint32_t* __restrict__ off, uint32_t* __restrict__ slots) {
+__global__ __launch_bounds__(256) void fill_kernel(const uint32_t* __restrict__ keys,
+                                                   const uint32_t* __restrict__ ranks, int64_t n, int64_t n_var,
+                                                   const uint32_t* __restrict__ start, uint32_t* __restrict__ slots) {
   const int64_t s = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (s >= n) return;
   const uint32_t k = keys[s];
-  if ((int64_t)k < n_var) slots[atomicAdd(&off[k], 1u)] = (uint32_t)s;
+  if ((int64_t)k < n_var) slots[start[k] + ranks[s]] = (uint32_t)s;
 }
 
 // Ascending order of x[0, len) with the bitonic network in its one-direction
@@ -294,7 +297,7 @@ __device__ void bitonic_sort(Ptr x, int64_t len) {
 // Segmented reduction + optimizer
 // ---------------------------------------------------------------------------
 struct SegArgs {
-  const uint32_t* ends;       // [n_var] end of each variable's range in slots
+  const uint32_t* start;      // [n_var + 1] start of each variable's range in slots (then the total)
   const uint32_t* slots;      // slot ids grouped by variable (CSR)
   const uint32_t* long_list;  // variables with more than kPiece slots
   const uint32_t* n_long;     // their number
@@ -554,8 +557,8 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
     if (blockIdx.x >= *a.n_long) return;  // uniform per workgroup
     const int grp = threadIdx.x >> 5;
     const uint32_t key = a.long_list[blockIdx.x];
-    const int64_t lo = key == 0 ? 0 : a.ends[key - 1];
-    const int64_t hi = a.ends[key];
+    const int64_t lo = a.start[key];
+    const int64_t hi = a.start[key + 1];
     const int64_t len = hi - lo;
     float p[VPL], m[VPL], v[VPL];
     if (ADAM && grp == 0) {  // independent of the gradient: fetched first
@@ -604,8 +607,8 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
   }
   const int64_t k = (((int64_t)blockIdx.x - n_long_blocks) * 256 + threadIdx.x) >> 5;
   if (k >= a.n_var) return;  // uniform per group
-  const int64_t lo = k == 0 ? 0 : a.ends[k - 1];
-  const int64_t len = (int64_t)a.ends[k] - lo;
+  const int64_t lo = a.start[k];
+  const int64_t len = (int64_t)a.start[k + 1] - lo;
   if (len == 0 || len > kPiece) return;  // not hit, or a long range (its own workgroup)
   float p[VPL], m[VPL], v[VPL];
   if constexpr (ADAM) {  // the state rows do not depend on the gradient: fetch them first
@@ -661,8 +664,9 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
 // ---------------------------------------------------------------------------
 struct Workspace {
   uint32_t* keys;       // [n] variable of every slot (n_var: none)
+  uint32_t* ranks;      // [n] place of every slot in its variable's range
   uint32_t* slots;      // [n] slot ids grouped by variable
-  uint32_t* off;        // [n_var + 1] counts -> offsets -> ends; [n_var]: long-list length
+  uint32_t* off;        // [n_var + 2] counts -> range starts ([n_var]: the total); [n_var + 1]: long-list length
   uint32_t* partial;    // scan chunk totals
   uint32_t* long_list;  // variables of more than kPiece slots
 };
@@ -674,8 +678,8 @@ static int64_t n_long_max(int64_t n) { return n / (kPiece + 1) + 1; }
 static int64_t scan_chunks(int64_t n_var) { return (n_var + kScanChunk - 1) / kScanChunk; }
 
 static size_t workspace_bytes(int64_t n, int64_t n_var) {
-  return 2 * align256((size_t)n * 4) + align256((size_t)(n_var + 1) * 4) +
-         align256((size_t)(scan_chunks(n_var) + 1) * 4) + align256((size_t)n_long_max(n) * 4);
+  return 3 * align256((size_t)n * 4) + align256((size_t)(n_var + 2) * 4) +
+         align256((size_t)(scan_chunks(n_var + 1) + 1) * 4) + align256((size_t)n_long_max(n) * 4);
 }
 
 static Workspace carve(void* ws, int64_t n, int64_t n_var) {
@@ -683,12 +687,14 @@ static Workspace carve(void* ws, int64_t n, int64_t n_var) {
   char* p = (char*)ws;
   w.keys = (uint32_t*)p;
   p += align256((size_t)n * 4);
+  w.ranks = (uint32_t*)p;
+  p += align256((size_t)n * 4);
   w.slots = (uint32_t*)p;
   p += align256((size_t)n * 4);
   w.off = (uint32_t*)p;
-  p += align256((size_t)(n_var + 1) * 4);
+  p += align256((size_t)(n_var + 2) * 4);
   w.partial = (uint32_t*)p;
-  p += align256((size_t)(scan_chunks(n_var) + 1) * 4);
+  p += align256((size_t)(scan_chunks(n_var + 1) + 1) * 4);
   w.long_list = (uint32_t*)p;
   return w;
 }
@@ -703,34 +709,35 @@ static int group_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64
                        int64_t index_capacity, bool direct, const Workspace& w, hipStream_t st) {
   int split_shift = 0;
   while (((n_var + (1LL << split_shift) - 1) >> split_shift) > kSplitMax) ++split_shift;
-  hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n_var + 1, 256, 1024)), dim3(256), 0, st, w.off, n_var + 1);
+  hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n_var + 2, 256, 1024)), dim3(256), 0, st, w.off, n_var + 2);
   const dim3 kgrid((unsigned)((n + kTile - 1) / kTile));
   if (direct) {
     hipLaunchKernelGGL(keys_count_kernel<2>, kgrid, dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
-                       (const unsigned long long*)nullptr, 0, w.keys, w.off);
+                       (const unsigned long long*)nullptr, 0, w.keys, w.ranks, w.off);
   } else if (index != nullptr) {
     int ib = 0;
     while ((1LL << ib) < index_capacity) ++ib;
     hipLaunchKernelGGL(keys_count_kernel<1>, kgrid, dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
-                       (const unsigned long long*)index, ib, w.keys, w.off);
+                       (const unsigned long long*)index, ib, w.keys, w.ranks, w.off);
   } else {
     hipLaunchKernelGGL(keys_count_kernel<0>, kgrid, dim3(kTileThreads), 0, st, rows, n, ids, n_var, split_shift,
-                       (const unsigned long long*)nullptr, 0, w.keys, w.off);
+                       (const unsigned long long*)nullptr, 0, w.keys, w.ranks, w.off);
   }
-  const unsigned chunks = (unsigned)scan_chunks(n_var);
-  hipLaunchKernelGGL(scan_partials, dim3(chunks), dim3(kScanThreads), 0, st, w.off, n_var, w.partial);
-  hipLaunchKernelGGL(scan_apply, dim3(chunks), dim3(kScanThreads), 0, st, w.off, n_var, w.partial, w.long_list,
-                     w.off + n_var);
-  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w.keys, n, n_var, w.off,
-                     w.slots);
+  // the scan runs over n_var + 1 entries (the last count is zero), so off[n_var] is the total
+  const unsigned chunks = (unsigned)scan_chunks(n_var + 1);
+  hipLaunchKernelGGL(scan_partials, dim3(chunks), dim3(kScanThreads), 0, st, w.off, n_var + 1, w.partial);
+  hipLaunchKernelGGL(scan_apply, dim3(chunks), dim3(kScanThreads), 0, st, w.off, n_var + 1, w.partial, w.long_list,
+                     w.off + n_var + 1);
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w.keys, w.ranks, n, n_var,
+                     w.off, w.slots);
   return launch_status("slot grouping kernels");
 }
 
 static void fill_seg(SegArgs* a, const Workspace& w, int64_t n, int64_t n_var) {
-  a->ends = w.off;
+  a->start = w.off;
   a->slots = w.slots;
   a->long_list = w.long_list;
-  a->n_long = w.off + n_var;
+  a->n_long = w.off + n_var + 1;
   a->n = n;
   a->n_var = n_var;
 }
