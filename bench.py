@@ -297,8 +297,8 @@ def bench_ple(steps: int, warmup: int) -> dict:
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-backward", action="store_true", help="skip the config-2 descent step leg")
@@ -427,11 +427,11 @@ def main() -> None:
         dc = bench_decode(tab, 200)
         result["decode_config3"] = dc
         log(f"decode (config 3): p50 {dc['us_p50']:.1f} us, p99 {dc['us_p99']:.1f} us per call")
-        c4 = bench_config4(max(1, args.steps // 4), max(1, args.warmup // 4))
+        c4 = bench_config4(max(1, args.steps // 4), max(1, args.warmup))
         result["forward_config4"] = c4
         log(f"forward (config 4): {c4['us_per_launch']:.1f} us/launch, {c4['gb_per_s']:.0f} GB/s algorithmic "
             f"({100 * c4['frac_of_hbm_peak']:.1f}% of peak)")
-        pl = bench_ple(max(1, args.steps // 10), 3)
+        pl = bench_ple(max(1, args.steps // 10), max(1, args.warmup // 10))
         result["ple_forward"] = pl
         log(f"ple_forward: {pl['us_per_step']:.0f} us/step, GEMMs at {pl['gemm_tflops']:.1f} TFLOP/s fp32")
 

@@ -115,6 +115,7 @@ __global__ __launch_bounds__(kPleThreads) void ple_gate_kernel(
 // the same workgroup read a few positions earlier (L1), so every normed value
 // comes from HBM about once.
 constexpr int kConvRun = 32;
+constexpr int kConvBatch = 4;  // positions whose loads are issued together
 
 // MODE 0: out = (hidden + value*gate) + conv; 1: value*gate + conv; 2: conv.
 template <int MODE, bool SHARED>
@@ -138,34 +139,45 @@ __global__ __launch_bounds__(256) void ple_conv_kernel(const float* __restrict__
   for (int k = 0; k < kMaxTaps; ++k)
     if (k < taps) w[k] = conv_w[(int64_t)c * taps + k];
   const int64_t t_end = min(t0 + kConvRun, T);
-  for (int64_t t = t0; t < t_end; ++t) {
-    // a tap before the first row reads row 0 with its weight dropped (every load is issued)
-    float x[kMaxTaps];
-    bool ok[kMaxTaps];
+  // kConvBatch positions at a time: all their loads are issued before the first
+  // is used (a position past t_end re-reads the last one and stores nothing);
+  // a tap before the first row reads row 0 with its weight dropped.
+  for (int64_t t = t0; t < t_end; t += kConvBatch) {
+    float x[kConvBatch][kMaxTaps];
+    bool ok[kConvBatch][kMaxTaps];
+    float hv[kConvBatch], vv[kConvBatch], gj[kConvBatch];
 #pragma unroll
-    for (int k = 0; k < kMaxTaps; ++k) {
-      if (k < taps) {
-        const int64_t back = (int64_t)(taps - 1 - k) * dil;
-        const int64_t src = SHARED ? (back == 0 ? hist_rows + t : hist_rows - back) : hist_rows + t - back;
-        ok[k] = src >= 0;
-        x[k] = full[(ok[k] ? src : 0) * C + c];
+    for (int b = 0; b < kConvBatch; ++b) {
+      const int64_t tb = min(t + b, t_end - 1);
+#pragma unroll
+      for (int k = 0; k < kMaxTaps; ++k) {
+        if (k < taps) {
+          const int64_t back = (int64_t)(taps - 1 - k) * dil;
+          const int64_t src = SHARED ? (back == 0 ? hist_rows + tb : hist_rows - back) : hist_rows + tb - back;
+          ok[b][k] = src >= 0;
+          x[b][k] = full[(ok[b][k] ? src : 0) * C + c];
+        }
+      }
+      hv[b] = vv[b] = gj[b] = 0.0f;
+      if constexpr (MODE == 0) hv[b] = hidden[tb * C + c];
+      if constexpr (MODE <= 1) {
+        vv[b] = value[tb * n + i];
+        gj[b] = gate[tb * hc + j];
       }
     }
-    const int64_t o = t * C + c;
-    float hv = 0.0f, vv = 0.0f, gj = 0.0f;
-    if constexpr (MODE == 0) hv = hidden[o];
-    if constexpr (MODE <= 1) {
-      vv = value[t * n + i];
-      gj = gate[t * hc + j];
-    }
-    float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kMaxTaps; ++k)
-      if (k < taps && ok[k]) acc += x[k] * w[k];
-    const float silu = acc / (1.0f + expf(-acc));
-    if constexpr (MODE == 0) out[o] = (hv + vv * gj) + silu;
-    else if constexpr (MODE == 1) out[o] = vv * gj + silu;
-    else out[o] = silu;
+    for (int b = 0; b < kConvBatch; ++b) {
+      if (t + b >= t_end) break;
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kMaxTaps; ++k)
+        if (k < taps && ok[b][k]) acc += x[b][k] * w[k];
+      const float silu = acc / (1.0f + expf(-acc));
+      const int64_t o = (t + b) * C + c;
+      if constexpr (MODE == 0) out[o] = (hv[b] + vv[b] * gj[b]) + silu;
+      else if constexpr (MODE == 1) out[o] = vv[b] * gj[b] + silu;
+      else out[o] = silu;
+    }
   }
 }
 
