@@ -286,12 +286,34 @@ def bench_ple(steps: int, warmup: int) -> dict:
             ple.ple_forward(emb, hidden, w, hist, HP)
         b.record()
         torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / steps
+        ms = a.elapsed_time(b) / steps
+        # the two projections alone, for the GEMMs' own rate
+        a.record()
+        for _ in range(steps):
+            emb @ w.w_key.T
+            emb @ w.w_value.T
+        b.record()
+        torch.cuda.synchronize()
+        gemm_ms = a.elapsed_time(b) / steps
+    # forward + backward to emb (the descent's use: the weights stay fixed)
+    emb_v = emb.clone().requires_grad_(True)
+    d_out = rnd(t_len, hc, n, sc=1e-3)
+    bsteps = max(1, steps // 5)
+    for i in range(bsteps + 2):
+        if i == 2:
+            torch.cuda.synchronize()
+            a.record()
+        out, _ = ple.ple_forward(emb_v, hidden, w, hist, HP)
+        (d_gemm,) = torch.autograd.grad(out, emb_v, d_out)
+    b.record()
+    torch.cuda.synchronize()
+    fb_ms = a.elapsed_time(b) / bsteps
     flops = 2.0 * t_len * n * (hc * n + n)
     return {"workload": "ple_forward: T 2048, hc 4, n_embd 2560, 4 taps, dilation 3, fp32 (key/value GEMMs on "
                         "hipBLASLt through torch.matmul, gate/norm and conv in HIP)",
-            "us_per_step": ms * 1e3, "gemm_tflops": flops / (ms * 1e-3) / 1e12,
-            "fp32_mfma_peak_tflops": 157.3}
+            "us_per_step": ms * 1e3, "gemm_us": gemm_ms * 1e3, "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12,
+            "non_gemm_us": (ms - gemm_ms) * 1e3, "fp32_mfma_peak_tflops": 157.3,
+            "us_forward_backward_to_emb": fb_ms * 1e3}
 
 
 def main() -> None:
@@ -433,7 +455,9 @@ def main() -> None:
             f"({100 * c4['frac_of_hbm_peak']:.1f}% of peak)")
         pl = bench_ple(max(1, args.steps // 10), max(1, args.warmup // 10))
         result["ple_forward"] = pl
-        log(f"ple_forward: {pl['us_per_step']:.0f} us/step, GEMMs at {pl['gemm_tflops']:.1f} TFLOP/s fp32")
+        log(f"ple_forward: {pl['us_per_step']:.0f} us/step; its two GEMMs alone {pl['gemm_us']:.0f} us "
+            f"({pl['gemm_tflops']:.1f} TFLOP/s fp32), the rest {pl['non_gemm_us']:.0f} us; forward + backward "
+            f"to emb {pl['us_forward_backward_to_emb']:.0f} us")
 
     if not args.no_cpu:
         cb = cpu_baseline(hp, tokens_np, res[0].cpu(), args.cpu_seconds)

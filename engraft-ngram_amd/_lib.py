@@ -98,7 +98,12 @@ SIGNATURES = {
     "eg_forward": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,
                              c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_gate": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32,
-                              c_int32, ctypes.c_float, c_void_p, c_void_p, c_void_p, c_void_p]),
+                              c_int32, ctypes.c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "eg_ple_conv_backward": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32,
+                                       c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "eg_ple_gate_backward": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
+                                       c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_conv": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32,
                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_rms": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, ctypes.c_float, c_void_p, c_void_p]),

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(kPleThreads) void ple_gate_kernel(
     const float* __restrict__ key, const float* __restrict__ value, const float* __restrict__ hidden,
     const float* __restrict__ norm_key, const float* __restrict__ norm_query, const float* __restrict__ norm_conv,
     int hc, int n, float eps, float inv_sqrt_n, float* __restrict__ normed, float* __restrict__ s_out,
-    float* __restrict__ gate_out) {
+    float* __restrict__ gate_out, float* __restrict__ rstd_out) {
 #pragma clang fp contract(off)
   __shared__ float red[kPleThreads / 64];
   const int64_t t = blockIdx.x / hc;
@@ -108,6 +108,11 @@ __global__ __launch_bounds__(kPleThreads) void ple_gate_kernel(
   if (tid == 0) {
     s_out[t * hc + j] = s;
     gate_out[t * hc + j] = gate;
+    if (rstd_out != nullptr) {  // the three RMS factors, for the backward
+      rstd_out[(t * hc + j) * 3 + 0] = rk;
+      rstd_out[(t * hc + j) * 3 + 1] = rq;
+      rstd_out[(t * hc + j) * 3 + 2] = rg;
+    }
   }
 }
 
@@ -210,6 +215,244 @@ __global__ __launch_bounds__(kPleThreads) void ple_rms_kernel(const float* __res
   }
 }
 
+// ---------------------------------------------------------------------------
+// Backward (gradients to the GEMM outputs, the hidden state and the history;
+// the weights' gradients are not computed here)
+// ---------------------------------------------------------------------------
+// ple_conv_bwd_kernel: workgroup = 256 channels x kConvRun rows of full.
+//   d_acc[t] = d_out[t] * silu'(acc[t]), silu'(x) = sg (1 + x (1 - sg)), acc
+//   recomputed from the taps; the d_acc of the positions the rows need are
+//   staged in LDS (each thread its own channel column), then
+//   d_full[r] = sum_k w_k d_acc[r - hist_rows + back_k] (+ the gradient of the
+//   returned history tail).
+constexpr int kConvBwdMaxBack = 32;  // (taps - 1) * dilation the LDS window holds
+constexpr int kConvBwdRun = 16;      // rows of full per workgroup
+constexpr int kConvBwdBatch = 4;     // positions whose loads are issued together
+
+__global__ __launch_bounds__(256) void ple_conv_bwd_kernel(const float* __restrict__ full, int64_t hist_rows,
+                                                           int64_t T, int hc, int n,
+                                                           const float* __restrict__ conv_w, int taps, int dil,
+                                                           const float* __restrict__ d_out,
+                                                           const float* __restrict__ d_tail, int64_t tail_rows,
+                                                           float* __restrict__ d_full) {
+#pragma clang fp contract(off)
+  extern __shared__ float dacc[];  // [kConvBwdRun + (taps-1)*dil][256]
+  const int C = hc * n;
+  const int n_cblk = (C + 255) / 256;
+  const int cblk = (int)(blockIdx.x % n_cblk);
+  const int64_t r0 = (int64_t)(blockIdx.x / n_cblk) * kConvBwdRun;
+  const int tid = threadIdx.x;
+  const int c = cblk * 256 + tid;
+  if (c >= C) return;  // no barrier below: every thread reads only its own column
+  constexpr int kMaxTaps = 8;
+  float w[kMaxTaps];
+#pragma unroll
+  for (int k = 0; k < kMaxTaps; ++k)
+    if (k < taps) w[k] = conv_w[(int64_t)c * taps + k];
+  const int64_t R = hist_rows + T;
+  const int64_t r1 = min(r0 + kConvBwdRun, R);
+  const int64_t max_back = (int64_t)(taps - 1) * dil;
+  const int64_t ta = max(r0 - hist_rows, (int64_t)0);
+  const int64_t tb = min(r1 - hist_rows + max_back, T);
+  for (int64_t t = ta; t < tb; t += kConvBwdBatch) {
+    float x[kConvBwdBatch][kMaxTaps];
+    bool ok[kConvBwdBatch][kMaxTaps];
+    float dv[kConvBwdBatch];
+#pragma unroll
+    for (int b = 0; b < kConvBwdBatch; ++b) {
+      const int64_t tt = min(t + b, tb - 1);
+#pragma unroll
+      for (int k = 0; k < kMaxTaps; ++k) {
+        if (k < taps) {
+          const int64_t src = hist_rows + tt - (int64_t)(taps - 1 - k) * dil;
+          ok[b][k] = src >= 0;
+          x[b][k] = full[(ok[b][k] ? src : 0) * C + c];
+        }
+      }
+      dv[b] = d_out[tt * C + c];
+    }
+#pragma unroll
+    for (int b = 0; b < kConvBwdBatch; ++b) {
+      if (t + b >= tb) break;
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kMaxTaps; ++k)
+        if (k < taps && ok[b][k]) acc += x[b][k] * w[k];
+      const float sg = 1.0f / (1.0f + expf(-acc));
+      dacc[(t + b - ta) * 256 + tid] = dv[b] * (sg * (1.0f + acc * (1.0f - sg)));
+    }
+  }
+  const int64_t tail0 = R - tail_rows;
+  for (int64_t r = r0; r < r1; ++r) {
+    float g = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMaxTaps; ++k) {
+      if (k < taps) {
+        const int64_t t = r - hist_rows + (int64_t)(taps - 1 - k) * dil;
+        if (t >= 0 && t < T) g += w[k] * dacc[(t - ta) * 256 + tid];
+      }
+    }
+    if (d_tail != nullptr && r >= tail0) g += d_tail[(r - tail0) * C + c];
+    d_full[r * C + c] = g;
+  }
+}
+
+// ple_gate_bwd_kernel: one workgroup of 1024 threads per position, every
+// stream (hc <= 4, n <= 4096).  With x = value * gate_j (gated), y = normed,
+// dy = d_normed, r = the forward's RMS factors:
+//   d_gated = d_out + r_g nc dy - x r_g^3 / n * sum(dy nc x)
+//   d_value = sum_j d_gated_j gate_j;  d_gate_j = sum(d_gated_j value)
+//   d_s = d_gate g (1 - g) / (2 sqrt|s|) for |s| > 1e-6, else 0
+//   d_key_raw = r_k nk (d_s q^ / sqrt n) - k r_k^2 d_s s / n
+//   d_hidden  = d_out + r_q nq (d_s k^ / sqrt n) - h r_q^2 d_s s / n
+// (the key and query norms' sums close to d_s s / r: sum(k^ q^) = s sqrt n).
+constexpr int kGbThreads = 1024;
+constexpr int kGbMaxPer = 4;
+constexpr int kGbMaxHc = 4;
+
+__device__ inline void block_sum4(float v[kGbMaxHc], float* red) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kWaves = kGbThreads / 64;
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j)
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v[j] += __shfl_xor(v[j], o);
+  __syncthreads();  // the previous use of red is complete
+  if (lane == 0)
+#pragma unroll
+    for (int j = 0; j < kGbMaxHc; ++j) red[j * kWaves + wave] = v[j];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) {
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) t += red[j * kWaves + w];
+    v[j] = t;
+  }
+}
+
+__global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_kernel(
+    const float* __restrict__ key, const float* __restrict__ value, const float* __restrict__ hidden,
+    const float* __restrict__ norm_key, const float* __restrict__ norm_query, const float* __restrict__ norm_conv,
+    const float* __restrict__ s_in, const float* __restrict__ gate_in, const float* __restrict__ rstd,
+    const float* __restrict__ d_out, const float* __restrict__ d_normed, int hc, int n, float inv_sqrt_n,
+    int detach_value, int detach_gate, float* __restrict__ d_key, float* __restrict__ d_value,
+    float* __restrict__ d_hidden) {
+#pragma clang fp contract(off)
+  __shared__ float red[kGbMaxHc * (kGbThreads / 64)];
+  const int64_t t = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int per = (n + kGbThreads - 1) / kGbThreads;
+  const float inv_n = 1.0f / (float)n;
+  float sj[kGbMaxHc], gj[kGbMaxHc], rk[kGbMaxHc], rq[kGbMaxHc], rg[kGbMaxHc];
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) {
+    const int jj = min(j, hc - 1);
+    sj[j] = s_in[t * hc + jj];
+    gj[j] = gate_in[t * hc + jj];
+    rk[j] = rstd[(t * hc + jj) * 3 + 0];
+    rq[j] = rstd[(t * hc + jj) * 3 + 1];
+    rg[j] = rstd[(t * hc + jj) * 3 + 2];
+  }
+  float val[kGbMaxPer];
+#pragma unroll
+  for (int m = 0; m < kGbMaxPer; ++m)
+    if (m < per) val[m] = value[t * n + min(tid + m * kGbThreads, n - 1)];
+  // round 1: sum(dy nc x) per stream; d_gated without its last term
+  float dg[kGbMaxHc][kGbMaxPer], acc[kGbMaxHc];
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) {
+    acc[j] = 0.0f;
+    const int jj = min(j, hc - 1);
+    const int64_t row = (t * hc + jj) * n;
+#pragma unroll
+    for (int m = 0; m < kGbMaxPer; ++m) {
+      if (m < per) {
+        const int i = min(tid + m * kGbThreads, n - 1);
+        const bool ok = j < hc && tid + m * kGbThreads < n;
+        const float dy = d_normed[row + i];
+        const float wc = norm_conv[jj * n + i];
+        const float x = val[m] * gj[j];
+        dg[j][m] = d_out[row + i] + rg[j] * (wc * dy);
+        if (ok) acc[j] += (dy * wc) * x;
+      }
+    }
+  }
+  block_sum4(acc, red);
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) {
+    const float coef = ((rg[j] * rg[j]) * rg[j]) * inv_n * acc[j];
+#pragma unroll
+    for (int m = 0; m < kGbMaxPer; ++m)
+      if (m < per) dg[j][m] = dg[j][m] - (val[m] * gj[j]) * coef;
+  }
+  if (!detach_value && d_value != nullptr) {
+#pragma unroll
+    for (int m = 0; m < kGbMaxPer; ++m) {
+      const int i = tid + m * kGbThreads;
+      if (m < per && i < n) {
+        float dv = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kGbMaxHc; ++j)
+          if (j < hc) dv += dg[j][m] * gj[j];
+        d_value[t * n + i] = dv;
+      }
+    }
+  }
+  // round 2: d_gate per stream -> d_s
+  float ds[kGbMaxHc];
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) ds[j] = 0.0f;
+  if (!detach_gate) {  // uniform
+#pragma unroll
+    for (int j = 0; j < kGbMaxHc; ++j) {
+      acc[j] = 0.0f;
+#pragma unroll
+      for (int m = 0; m < kGbMaxPer; ++m)
+        if (m < per && j < hc && tid + m * kGbThreads < n) acc[j] += dg[j][m] * val[m];
+    }
+    block_sum4(acc, red);
+#pragma unroll
+    for (int j = 0; j < kGbMaxHc; ++j) {
+      const float du = acc[j] * (gj[j] * (1.0f - gj[j]));
+      const float as = fabsf(sj[j]);
+      ds[j] = as > 1e-6f ? du * (0.5f / sqrtf(as)) : 0.0f;
+    }
+  }
+  // the key and query norms' backward, and the hidden state's gradient
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) {
+    if (j >= hc) break;
+    const int64_t row = (t * hc + j) * n;
+    float k[kGbMaxPer], h[kGbMaxPer], wk[kGbMaxPer], wq[kGbMaxPer], dd[kGbMaxPer];
+#pragma unroll
+    for (int m = 0; m < kGbMaxPer; ++m) {
+      if (m < per) {
+        const int i = min(tid + m * kGbThreads, n - 1);
+        k[m] = key[row + i];
+        h[m] = hidden[row + i];
+        wk[m] = norm_key[j * n + i];
+        wq[m] = norm_query[j * n + i];
+        dd[m] = d_out[row + i];
+      }
+    }
+    const float ck = ((rk[j] * rk[j]) * ds[j]) * sj[j] * inv_n;
+    const float cq = ((rq[j] * rq[j]) * ds[j]) * sj[j] * inv_n;
+    const float dsn = ds[j] * inv_sqrt_n;
+#pragma unroll
+    for (int m = 0; m < kGbMaxPer; ++m) {
+      const int i = tid + m * kGbThreads;
+      if (m < per && i < n) {
+        const float kn = (k[m] * rk[j]) * wk[m];
+        const float qn = (h[m] * rq[j]) * wq[m];
+        if (d_key != nullptr) d_key[row + i] = (rk[j] * wk[m]) * (dsn * qn) - k[m] * ck;
+        if (d_hidden != nullptr) d_hidden[row + i] = dd[m] + ((rq[j] * wq[m]) * (dsn * kn) - h[m] * cq);
+      }
+    }
+  }
+}
+
+
 template <int MODE, bool SHARED>
 static void launch_conv(dim3 grid, hipStream_t st, const float* full, int64_t hist_rows, int64_t n_pos, int hc, int n,
                         const float* conv_w, int taps, int dil, const float* hidden, const float* value,
@@ -226,7 +469,7 @@ extern "C" {
 
 int eg_ple_gate(const float* key, const float* value, const float* hidden, const float* norm_key,
                 const float* norm_query, const float* norm_conv, int64_t n_pos, int32_t hc, int32_t n_embd, float eps,
-                float* normed, float* s_out, float* gate_out, void* stream) {
+                float* normed, float* s_out, float* gate_out, float* rstd_out, void* stream) {
   EG_CHECK_ARG(n_pos >= 0 && n_pos * hc < (1LL << 31), "n_pos=%lld", (long long)n_pos);
   EG_CHECK_ARG(hc >= 1 && hc <= 64 && n_embd >= 1 && n_embd <= kPleThreads * kPleMaxPer,
                "hc=%d n_embd=%d (n_embd <= %d)", hc, n_embd, kPleThreads * kPleMaxPer);
@@ -236,7 +479,7 @@ int eg_ple_gate(const float* key, const float* value, const float* hidden, const
   if (n_pos == 0) return EG_OK;
   hipLaunchKernelGGL(ple_gate_kernel, dim3((unsigned)(n_pos * hc)), dim3(kPleThreads), 0, (hipStream_t)stream, key,
                      value, hidden, norm_key, norm_query, norm_conv, hc, n_embd, eps, (float)(1.0 / sqrt((double)n_embd)),
-                     normed, s_out, gate_out);
+                     normed, s_out, gate_out, rstd_out);
   return launch_status("ple_gate_kernel");
 }
 
@@ -276,6 +519,49 @@ int eg_ple_rms(const float* x, int64_t n_rows, int32_t hc, int32_t n_embd, const
   hipLaunchKernelGGL(ple_rms_kernel, dim3((unsigned)(n_rows * hc)), dim3(kPleThreads), 0, (hipStream_t)stream, x, hc,
                      n_embd, eps, weight, out);
   return launch_status("ple_rms_kernel");
+}
+
+int eg_ple_conv_backward(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
+                         const float* conv_w, int32_t taps, int32_t dilation, const float* d_out, const float* d_tail,
+                         int64_t tail_rows, float* d_full, void* stream) {
+  EG_CHECK_ARG(n_pos >= 0 && hist_rows >= 0 && hc >= 1 && n_embd >= 1 && taps >= 1 && taps <= 8 && dilation >= 1,
+               "n_pos=%lld hist_rows=%lld hc=%d n_embd=%d taps=%d dilation=%d", (long long)n_pos,
+               (long long)hist_rows, hc, n_embd, taps, dilation);
+  if ((int64_t)(taps - 1) * dilation > kConvBwdMaxBack)
+    return set_error(EG_ERR_UNSUPPORTED, "convolution backward for (taps-1)*dilation = %lld > %d",
+                     (long long)(taps - 1) * dilation, kConvBwdMaxBack);
+  EG_CHECK_ARG(tail_rows >= 0 && tail_rows <= hist_rows + n_pos, "tail_rows=%lld", (long long)tail_rows);
+  EG_CHECK_ARG(n_pos < (1LL << 31) && (int64_t)hc * n_embd < (1LL << 31), "too many elements");
+  const int64_t rows = hist_rows + n_pos;
+  EG_CHECK_ARG(rows == 0 || (full && conv_w && d_full && (n_pos == 0 || d_out)), "NULL argument");
+  EG_CHECK_ARG(tail_rows == 0 || d_tail != nullptr, "d_tail is NULL");
+  if (rows == 0) return EG_OK;
+  const int64_t blocks = (int64_t)((hc * n_embd + 255) / 256) * ((rows + kConvBwdRun - 1) / kConvBwdRun);
+  EG_CHECK_ARG(blocks < (1LL << 32), "too many elements");
+  const size_t lds = (size_t)(kConvBwdRun + (taps - 1) * dilation) * 256 * sizeof(float);
+  hipLaunchKernelGGL(ple_conv_bwd_kernel, dim3((unsigned)blocks), dim3(256), lds, (hipStream_t)stream, full, hist_rows,
+                     n_pos, hc, n_embd, conv_w, taps, dilation, d_out, tail_rows ? d_tail : nullptr, tail_rows, d_full);
+  return launch_status("ple_conv_bwd_kernel");
+}
+
+int eg_ple_gate_backward(const float* key, const float* value, const float* hidden, const float* norm_key,
+                         const float* norm_query, const float* norm_conv, const float* s, const float* gate,
+                         const float* rstd, const float* d_out, const float* d_normed, int64_t n_pos, int32_t hc,
+                         int32_t n_embd, int32_t detach_value, int32_t detach_gate, float* d_key, float* d_value,
+                         float* d_hidden, void* stream) {
+  EG_CHECK_ARG(n_pos >= 0 && n_pos < (1LL << 31), "n_pos=%lld", (long long)n_pos);
+  if (hc < 1 || hc > kGbMaxHc || n_embd < 1 || n_embd > kGbThreads * kGbMaxPer)
+    return set_error(EG_ERR_UNSUPPORTED, "gate backward for hc=%d n_embd=%d (built: hc <= %d, n_embd <= %d)", hc,
+                     n_embd, kGbMaxHc, kGbThreads * kGbMaxPer);
+  EG_CHECK_ARG(n_pos == 0 || (key && value && hidden && norm_key && norm_query && norm_conv && s && gate && rstd &&
+                              d_out && d_normed),
+               "NULL argument");
+  if (n_pos == 0) return EG_OK;
+  hipLaunchKernelGGL(ple_gate_bwd_kernel, dim3((unsigned)n_pos), dim3(kGbThreads), 0, (hipStream_t)stream, key, value,
+                     hidden, norm_key, norm_query, norm_conv, s, gate, rstd, d_out, d_normed, hc, n_embd,
+                     (float)(1.0 / sqrt((double)n_embd)), detach_value, detach_gate, detach_gate ? nullptr : d_key,
+                     detach_value ? nullptr : d_value, d_hidden);
+  return launch_status("ple_gate_bwd_kernel");
 }
 
 }  // extern "C"

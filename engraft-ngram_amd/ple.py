@@ -11,12 +11,16 @@ Forward:
   ``[history; normed]``, SiLU, and ``out = hidden + gated + conv``.
 
 The result -- the output and the new history -- is differentiable in emb,
-hidden, the history and the weights.  ``PleReplica`` (below) is the same block
-with its weights read from the model GGUF, method for method as the
-reference's numpy replica.  The backward recomputes the block with
-torch operations on the device and differentiates that; the forward values are
-the HIP kernels'.  ``detach_value`` / ``detach_gate`` change only the backward,
-as in the reference.
+hidden, the history and the weights.  Without weight gradients (the descent's
+case) the backward runs ``eg_ple_conv_backward`` and ``eg_ple_gate_backward``
+on the forward's saved intermediates, then the projections' two GEMMs; with
+weight gradients, a torch recomputation of the block on the device,
+differentiated by autograd.  Either way the forward values are the HIP
+kernels'.  ``detach_value`` / ``detach_gate`` change only the backward, as in
+the reference.
+
+``PleReplica`` (below) is the same block with its weights read from the model
+GGUF, method for method as the reference's numpy replica.
 """
 from __future__ import annotations
 
@@ -73,15 +77,28 @@ def _block_torch(emb, hidden, w_key, w_value, nk, nq, nc, conv, hist, eps, dil, 
     return out, new_hist.reshape(-1, hc, n)
 
 
+def _native_backward_ok(hc: int, n: int, taps: int, dil: int) -> bool:
+    """The HIP backward's built limits (eg_ple_gate_backward, eg_ple_conv_backward)."""
+    return hc <= 4 and n <= 4096 and (taps - 1) * dil <= 32
+
+
 class _PleFn(torch.autograd.Function):
+    """Forward on the HIP kernels.  Backward: when no weight needs a gradient
+    (the descent's case: emb, hidden and the history only), the HIP backward
+    from the saved forward intermediates, so that the projections' GEMMs are
+    not run again; otherwise a torch recomputation of the block, differentiated
+    by autograd."""
+
     @staticmethod
     def forward(ctx, emb, hidden, w_key, w_value, nk, nq, nc, conv, hist, eps, dil, detach_value, detach_gate):
         t_len, hc, n = hidden.shape
         dev = hidden.device
         f32 = dict(dtype=torch.float32, device=dev)
         emb32 = emb.to(**f32).contiguous()
-        key = (emb32 @ w_key.to(**f32).T).contiguous()
-        value = (emb32 @ w_value.to(**f32).T).contiguous()
+        wk32 = w_key.to(**f32)
+        wv32 = w_value.to(**f32)
+        key = (emb32 @ wk32.T).contiguous()
+        value = (emb32 @ wv32.T).contiguous()
         hidden32 = hidden.to(**f32).contiguous()
         h0 = hist.shape[0]
         full = torch.empty((h0 + t_len, hc * n), **f32)
@@ -92,20 +109,33 @@ class _PleFn(torch.autograd.Function):
         st = _lib.stream_ptr(dev)
         nk32, nq32, nc32 = (x.to(**f32).contiguous() for x in (nk, nq, nc))
         conv32 = conv.to(**f32).contiguous()
+        taps = conv32.shape[1]
+        native = (not any(ctx.needs_input_grad[2:8]) and any(ctx.needs_input_grad)
+                  and _native_backward_ok(hc, n, taps, int(dil)))
+        rstd = torch.empty((t_len, hc, 3), **f32) if native else None
         _lib.call("eg_ple_gate", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden32), _lib.ptr(nk32), _lib.ptr(nq32),
-                  _lib.ptr(nc32), t_len, hc, n, float(eps), _lib.ptr(full[h0:]), _lib.ptr(s), _lib.ptr(gate), st)
+                  _lib.ptr(nc32), t_len, hc, n, float(eps), _lib.ptr(full[h0:]), _lib.ptr(s), _lib.ptr(gate),
+                  _lib.ptr(rstd), st)
         out = torch.empty((t_len, hc, n), **f32)
-        _lib.call("eg_ple_conv", _lib.ptr(full), h0, t_len, hc, n, _lib.ptr(conv32), conv32.shape[1], int(dil), 0,
+        _lib.call("eg_ple_conv", _lib.ptr(full), h0, t_len, hc, n, _lib.ptr(conv32), taps, int(dil), 0,
                   _lib.ptr(hidden32), _lib.ptr(value), _lib.ptr(gate), _lib.ptr(out), st)
-        hist_len = (conv32.shape[1] - 1) * int(dil)
+        hist_len = (taps - 1) * int(dil)
         new_hist = (full[-hist_len:] if hist_len > 0 else full[:0]).reshape(-1, hc, n).to(hidden.dtype).clone()
-        ctx.save_for_backward(emb, hidden, w_key, w_value, nk, nq, nc, conv, hist)
+        ctx.native = native
+        if native:
+            ctx.save_for_backward(key, value, hidden32, full, s, gate, rstd, nk32, nq32, nc32, conv32, wk32, wv32)
+            ctx.dtypes = (emb.dtype, hidden.dtype, hist.dtype)
+            ctx.tail_rows = new_hist.shape[0]
+        else:
+            ctx.save_for_backward(emb, hidden, w_key, w_value, nk, nq, nc, conv, hist)
         ctx.cfg = (eps, dil, detach_value, detach_gate)
         ctx.mark_non_differentiable(s, gate, value)
         return out.to(hidden.dtype), new_hist, s, gate, value
 
     @staticmethod
     def backward(ctx, d_out, d_hist, _d_s, _d_gate, _d_value):
+        if ctx.native:
+            return _PleFn._backward_native(ctx, d_out, d_hist)
         inputs = ctx.saved_tensors
         eps, dil, detach_value, detach_gate = ctx.cfg
         with torch.enable_grad():
@@ -122,6 +152,48 @@ class _PleFn(torch.autograd.Function):
             g = next(grads) if need else None
             res.append(torch.zeros_like(x) if (need and g is None) else g)
         return (*res, None, None, None, None)
+
+    @staticmethod
+    def _backward_native(ctx, d_out, d_hist):
+        key, value, hidden32, full, s, gate, rstd, nk32, nq32, nc32, conv32, wk32, wv32 = ctx.saved_tensors
+        _eps, dil, detach_value, detach_gate = ctx.cfg
+        emb_dt, hidden_dt, hist_dt = ctx.dtypes
+        t_len, hc, n = hidden32.shape
+        c_dim = hc * n
+        h0 = full.shape[0] - t_len
+        dev = full.device
+        f32 = dict(dtype=torch.float32, device=dev)
+        st = _lib.stream_ptr(dev)
+        need_emb, need_hidden, need_hist = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[8]
+        d_out32 = d_out.to(**f32).contiguous()
+        tail = ctx.tail_rows if (d_hist is not None and ctx.tail_rows > 0) else 0
+        d_tail = d_hist.to(**f32).reshape(tail, c_dim).contiguous() if tail else None
+        d_full = torch.empty((h0 + t_len, c_dim), **f32)
+        _lib.call("eg_ple_conv_backward", _lib.ptr(full), h0, t_len, hc, n, _lib.ptr(conv32), conv32.shape[1],
+                  int(dil), _lib.ptr(d_out32), _lib.ptr(d_tail), tail, _lib.ptr(d_full), st)
+        d_key = torch.empty((t_len, c_dim), **f32) if (need_emb and not detach_gate) else None
+        d_value = torch.empty((t_len, n), **f32) if (need_emb and not detach_value) else None
+        d_hidden = torch.empty((t_len, hc, n), **f32) if need_hidden else None
+        if d_key is not None or d_value is not None or d_hidden is not None:
+            _lib.call("eg_ple_gate_backward", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden32), _lib.ptr(nk32),
+                      _lib.ptr(nq32), _lib.ptr(nc32), _lib.ptr(s), _lib.ptr(gate), _lib.ptr(rstd), _lib.ptr(d_out32),
+                      _lib.ptr(d_full[h0:]), t_len, hc, n, int(bool(detach_value)), int(bool(detach_gate)),
+                      _lib.ptr(d_key), _lib.ptr(d_value), _lib.ptr(d_hidden), st)
+        d_emb = None
+        if need_emb:
+            # the projections' backward: d_emb = d_key @ w_key + d_value @ w_value
+            if d_key is not None:
+                d_emb = d_key @ wk32
+                if d_value is not None:
+                    d_emb.addmm_(d_value, wv32)
+            elif d_value is not None:
+                d_emb = d_value @ wv32
+            else:
+                d_emb = torch.zeros((t_len, n), **f32)
+            d_emb = d_emb.to(emb_dt)
+        d_hist_in = d_full[:h0].reshape(h0, hc, n).to(hist_dt) if need_hist else None
+        return (d_emb, d_hidden.to(hidden_dt) if d_hidden is not None else None, None, None, None, None, None, None,
+                d_hist_in, None, None, None, None)
 
 
 def ple_forward(emb: torch.Tensor, hidden: torch.Tensor, w: PleWeights, hist: torch.Tensor, hparams,
@@ -247,7 +319,7 @@ class PleReplica:
         gate = torch.empty((t_len, self.hc), **f32)
         _lib.call("eg_ple_gate", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden), _lib.ptr(self.norm_key),
                   _lib.ptr(self.norm_query), _lib.ptr(self.norm_conv), t_len, self.hc, self.n_embd, self.eps,
-                  _lib.ptr(normed), _lib.ptr(s), _lib.ptr(gate), _lib.stream_ptr(self.device))
+                  _lib.ptr(normed), _lib.ptr(s), _lib.ptr(gate), None, _lib.stream_ptr(self.device))
         return value, normed, s, gate
 
     def _conv(self, full: torch.Tensor, hist_rows: int, n_pos: int, value=None, gate=None,

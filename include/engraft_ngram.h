@@ -30,7 +30,7 @@
  *   eg_forward_decode  the per-token gather of a decode step with the overlay
  *                                                    engraft/replica/model.py:473-495
  *   eg_ple_gate, eg_ple_conv  ple_forward after its two projections
- *                                                    engraft/replica/layers.py:565-626
+ *   (+ _backward)    and the autograd of it          engraft/replica/layers.py:565-626
  *   eg_ple_rms, eg_ple_conv's other modes  PleReplica engraft/lens.py:221-385
  */
 #ifndef ENGRAFT_NGRAM_H
@@ -255,11 +255,13 @@ int eg_synth_table(const eg_table* table, uint64_t seed, const float* qtable,
  * stream j: RMS norms of key_j (norm_key) and hidden_j (norm_query),
  * s = <key_j^, hidden_j^> / sqrt(n_embd), gate = sigmoid(sign(s) sqrt(max(|s|, 1e-6))),
  * gated_j = value * gate, normed_j = rmsnorm(gated_j) * norm_conv.
- * normed f32 [n_pos, hc*n_embd]; s_out, gate_out f32 [n_pos, hc]. */
+ * normed f32 [n_pos, hc*n_embd]; s_out, gate_out f32 [n_pos, hc]; rstd_out
+ * (optional, f32 [n_pos, hc, 3]) the RMS factors 1/sqrt(mean(x^2) + eps) of
+ * key, hidden and gated, which eg_ple_gate_backward takes. */
 int eg_ple_gate(const float* key, const float* value, const float* hidden, const float* norm_key,
                 const float* norm_query, const float* norm_conv, int64_t n_pos, int32_t hc,
                 int32_t n_embd, float eps, float* normed, float* s_out, float* gate_out,
-                void* stream);
+                float* rstd_out, void* stream);
 
 /* out = (hidden + value*gate) + silu(conv), conv[t, c] = sum_k conv_w[c, k] *
  * full[hist_rows + t - (taps-1-k)*dilation, c] over the rows that exist
@@ -274,6 +276,32 @@ int eg_ple_gate(const float* key, const float* value, const float* hidden, const
 int eg_ple_conv(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
                 const float* conv_w, int32_t taps, int32_t dilation, int32_t shared_history,
                 const float* hidden, const float* value, const float* gate, float* out, void* stream);
+
+/* Backward of eg_ple_conv (mode 0, own history): d_full f32 [hist_rows + n_pos,
+ * hc*n_embd] = the gradient of [history; normed] given d_out f32 [n_pos,
+ * hc*n_embd] (the block's output gradient) and d_tail (optional, f32
+ * [tail_rows, hc*n_embd]: the gradient of the last tail_rows rows of full, the
+ * history the forward returned).  full and conv_w as the forward's.  The
+ * convolution weights' gradient is not computed.  (taps-1)*dilation <= 32.
+ * Replaces the autograd of causal_depthwise_conv + silu
+ * (engraft/replica/layers.py:257-293, 614-626). */
+int eg_ple_conv_backward(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
+                         const float* conv_w, int32_t taps, int32_t dilation, const float* d_out,
+                         const float* d_tail, int64_t tail_rows, float* d_full, void* stream);
+
+/* Backward of eg_ple_gate: from d_out and d_normed (the rows of d_full after
+ * the history), the gradients of the projections and of the hidden state:
+ * d_key f32 [n_pos, hc*n_embd] (of emb @ w_key^T), d_value f32 [n_pos, n_embd]
+ * (of emb @ w_value^T), d_hidden f32 [n_pos, hc*n_embd] (d_out included); any
+ * output may be NULL.  detach_value / detach_gate drop that factor of
+ * gated = value * gate from the gradient (engraft/replica/layers.py:600-604),
+ * leaving d_value / d_key untouched.  s, gate, rstd: the forward's outputs.
+ * hc <= 4, n_embd <= 4096.  The norm weights' gradients are not computed. */
+int eg_ple_gate_backward(const float* key, const float* value, const float* hidden, const float* norm_key,
+                         const float* norm_query, const float* norm_conv, const float* s, const float* gate,
+                         const float* rstd, const float* d_out, const float* d_normed, int64_t n_pos,
+                         int32_t hc, int32_t n_embd, int32_t detach_value, int32_t detach_gate,
+                         float* d_key, float* d_value, float* d_hidden, void* stream);
 
 /* Per-stream RMS norm: out[r, j, :] = x[r, j, :] / sqrt(mean(x[r, j, :]^2) + eps)
  * * weight[j, :], x and out f32 [n_rows, hc, n_embd], weight f32 [hc, n_embd]

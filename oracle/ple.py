@@ -55,8 +55,11 @@ def causal_depthwise_conv(x_new, history, weight, dilation=1):
     return acc
 
 
-def ple_forward(emb, hidden, w: dict, hist, hc: int, n_embd: int, eps: float, ngram_size: int):
-    """Returns ``(out [T, hc, n], new_hist, s [T, hc], gate [T, hc])``."""
+def ple_forward(emb, hidden, w: dict, hist, hc: int, n_embd: int, eps: float, ngram_size: int,
+                detach_value: bool = False, detach_gate: bool = False):
+    """Returns ``(out [T, hc, n], new_hist, s [T, hc], gate [T, hc])``;
+    ``detach_value`` / ``detach_gate`` detach that factor before ``gated =
+    value * gate`` (``layers.py:600-604``)."""
     t_len = emb.shape[0]
     key = (emb @ w["w_key"].T).reshape(t_len, hc, n_embd)
     key = rmsnorm_grouped(key, w["norm_key"], eps, hc)
@@ -65,7 +68,9 @@ def ple_forward(emb, hidden, w: dict, hist, hc: int, n_embd: int, eps: float, ng
     mag = torch.sqrt(torch.clamp(s.abs(), min=1e-6))
     gate = torch.sigmoid(torch.sign(s) * mag)
     value = emb @ w["w_value"].T
-    gated = value.unsqueeze(1) * gate.unsqueeze(-1)
+    g = gate.detach() if detach_gate else gate
+    v = value.detach() if detach_value else value
+    gated = v.unsqueeze(1) * g.unsqueeze(-1)
     normed = rmsnorm_grouped(gated, w["norm_conv"], eps, hc)
     normed_flat = normed.reshape(t_len, hc * n_embd)
     hist_flat = hist.reshape(hist.shape[0], hc * n_embd) if hist.numel() else hist.reshape(0, hc * n_embd)

@@ -356,3 +356,45 @@ def test_ple_table_from_gguf(cuda, tmp_path):
     assert tab.ngram_addresses(tokens) == H.ngram_addresses_scalar(spec, tokens)
     with pytest.raises(AssertionError):
         tab.read_rows_raw(0, 299, 2)
+
+
+def test_forward_graph_capture_replays(cuda):
+    """A PreparedForward captured in a HIP graph: three replays with the
+    program's own eager work between them (a new residual written in place, an
+    eager forward of the same inputs), every replay equal to the eager result
+    and to the oracle.  The forward records no memset."""
+    from engraft_ngram_amd import table as T
+    from engraft_ngram_amd.overlay import DeviceOverlay
+    _say("graph capture of the forward")
+    spec = synthetic_spec(n_rows=16 * 2000, seed=61)
+    tab = G.device_table(spec, "q8_0", 16 * 2000, 128, seed=62)
+    tokens = synth.zipf_tokens(63, 2048, 5000)
+    rows = H.ngram_rows_np(spec, tokens)
+    rng = np.random.default_rng(64)
+    ov_ids = np.unique(rng.choice(np.unique(rows), size=200, replace=False)).astype(np.int32)
+    ov_rows = (rng.standard_normal((ov_ids.size, 128)) * 0.05).astype(np.float32)
+    ov = DeviceOverlay.from_rows(ov_ids, ov_rows, device=cuda)
+    tok = torch.from_numpy(tokens).to(cuda)
+    res = G.residual(tokens.size, 2048, seed=65)
+    out = torch.empty_like(res)
+    call = T.PreparedForward([tab], tok, res, out=out, overlays=[ov], seq_len=1024)
+    side = torch.cuda.Stream(cuda)
+    side.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream(cuda).wait_stream(side)
+    torch.cuda.synchronize(cuda)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    fetch = G.synth_fetch("q8_0", 62, 128)
+    for k in range(3):
+        res.copy_(G.residual(tokens.size, 2048, seed=70 + k))
+        eager = tab.forward(tok, res, overlay=ov, seq_len=1024)
+        torch.cuda.synchronize(cuda)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize(cuda)
+        assert torch.equal(out, eager), f"replay {k}"
+        _, _, exp = FW.forward(spec, tokens, fetch, G.bf16_bits(res), overlay=(ov_ids, ov_rows), seq_len=1024)
+        G.assert_out_matches(G.bf16_bits(out), exp)

@@ -109,3 +109,71 @@ def test_ple_history_gradient_across_chunks(cuda):
     scale = e_c.grad.abs().max().item()
     assert e_c.grad[:8].abs().max().item() > 0  # the first chunk does receive gradient
     assert (e_d.grad.cpu() - e_c.grad).abs().max().item() <= 1e-4 * scale
+
+
+@pytest.mark.parametrize("dv,dg", [(False, False), (True, False), (False, True)])
+def test_ple_native_backward_against_oracle(cuda, dv, dg):
+    """The HIP backward (no weight gradients): d_emb, d_hidden and the incoming
+    history's gradient, with a gradient on the returned history too, against
+    autograd of the oracle on the CPU (T 40 after a 9-row history), for the
+    plain block and with either factor of gated detached."""
+    from engraft_ngram_amd import _lib, ple
+    print(f"[gpu-test] ple native backward detach_value={dv} detach_gate={dg}", file=sys.stderr, flush=True)
+    hc, n, T = 4, 2560, 40
+    w = ple_weights(hc, n, seed=31)
+    wd = _dev_weights(w, cuda)
+    g = torch.Generator().manual_seed(32)
+    emb = torch.randn((T, n), generator=g) * 0.1
+    hidden = torch.randn((T, hc, n), generator=g) * 0.1
+    hist = torch.randn((9, hc, n), generator=g) * 0.1
+    r = torch.randn((T, hc, n), generator=g)
+    rh = torch.randn((9, hc, n), generator=g)
+    leaves_c = [x.clone().requires_grad_(True) for x in (emb, hidden, hist)]
+    out_c, nh_c, _, _ = P.ple_forward(*leaves_c[:2], w, leaves_c[2], hc, n, 1e-6, 3, detach_value=dv, detach_gate=dg)
+    ((out_c * r).sum() + (nh_c * rh).sum()).backward()
+    leaves_d = [x.to(cuda).requires_grad_(True) for x in (emb, hidden, hist)]
+    called = []
+    real_call = _lib.call
+
+    def spy(name, *args):
+        called.append(name)
+        return real_call(name, *args)
+
+    _lib.call = spy
+    try:
+        out_d, nh_d = ple.ple_forward(leaves_d[0], leaves_d[1], wd, leaves_d[2], _HP, detach_value=dv,
+                                      detach_gate=dg)
+        ((out_d * r.to(cuda)).sum() + (nh_d * rh.to(cuda)).sum()).backward()
+    finally:
+        _lib.call = real_call
+    assert "eg_ple_conv_backward" in called and "eg_ple_gate_backward" in called
+    for name, got, exp in zip(("emb", "hidden", "hist"), (x.grad for x in leaves_d), (x.grad for x in leaves_c)):
+        scale = exp.abs().max().item()
+        err = (got.cpu() - exp).abs().max().item()
+        assert err <= 1e-4 * scale, f"d_{name}: {err} vs scale {scale}"
+
+
+def test_ple_weight_gradients_recompute_path(cuda):
+    """With weight gradients requested the backward recomputes the block with
+    torch on the device: the gradients of w_key, norm_conv and the taps, and
+    of emb, against autograd of the oracle on the CPU."""
+    from engraft_ngram_amd import ple
+    hc, n, T = 4, 2560, 12
+    w = ple_weights(hc, n, seed=41)
+    g = torch.Generator().manual_seed(42)
+    emb = torch.randn((T, n), generator=g) * 0.1
+    hidden = torch.randn((T, hc, n), generator=g) * 0.1
+    r = torch.randn((T, hc, n), generator=g)
+    wc = {k: (v.clone().requires_grad_(k in ("w_key", "norm_conv", "conv1d"))) for k, v in w.items()}
+    e_c = emb.clone().requires_grad_(True)
+    out_c, _, _, _ = P.ple_forward(e_c, hidden, wc, torch.zeros(0, hc, n), hc, n, 1e-6, 3)
+    (out_c * r).sum().backward()
+    wd = ple.PleWeights(**{k: v.to(cuda).requires_grad_(k in ("w_key", "norm_conv", "conv1d"))
+                           for k, v in w.items()})
+    e_d = emb.to(cuda).requires_grad_(True)
+    out_d, _ = ple.ple_forward(e_d, hidden.to(cuda), wd, torch.zeros(0, hc, n, device=cuda), _HP)
+    (out_d * r.to(cuda)).sum().backward()
+    for got, exp in ((e_d.grad, e_c.grad), (wd.w_key.grad, wc["w_key"].grad), (wd.norm_conv.grad, wc["norm_conv"].grad),
+                     (wd.conv1d.grad, wc["conv1d"].grad)):
+        scale = exp.abs().max().item()
+        assert (got.cpu() - exp).abs().max().item() <= 1e-4 * scale

@@ -110,3 +110,29 @@ def test_replica_jacobian_finite_differences_and_closed_form():
     jac = z.jacobian_out(emb, np.zeros((5, hc, n), dtype=np.float32), 2, coords=coords, step=1e-3)
     exp = np.tile(0.5 * z.w_value[:, coords], (hc, 1))
     assert np.linalg.norm(jac - exp) / np.linalg.norm(exp) <= 1e-3
+
+
+def test_detached_gradients_sum_to_the_full_gradient():
+    """layers.py:584-591: with detach_value the emb gradient flows through the
+    gate only, with detach_gate through the value only; emb reaches the output
+    only through gated = value * gate, so by the product rule the two add up to
+    the undetached emb gradient.  (hidden and the history also reach the output
+    directly, so for them the direct share would count twice.)"""
+    hc, n, T = 4, 256, 14
+    w = ple_weights(hc, n, seed=21)
+    g = torch.Generator().manual_seed(22)
+    emb = torch.randn((T, n), generator=g) * 0.1
+    hidden = torch.randn((T, hc, n), generator=g) * 0.1
+    hist = torch.randn((9, hc, n), generator=g) * 0.1
+    r = torch.randn((T, hc, n), generator=g)
+    grads = {}
+    for dv, dg in ((False, False), (True, False), (False, True)):
+        leaves = [x.clone().requires_grad_(True) for x in (emb, hidden, hist)]
+        out, new_hist, _, _ = P.ple_forward(leaves[0], leaves[1], w, leaves[2], hc, n, 1e-6, 3,
+                                            detach_value=dv, detach_gate=dg)
+        ((out * r).sum() + new_hist.sum()).backward()
+        grads[(dv, dg)] = [x.grad for x in leaves]
+    full, a, b = grads[(False, False)][0], grads[(True, False)][0], grads[(False, True)][0]
+    assert (a + b - full).abs().max().item() <= 1e-5 * full.abs().max().item()
+    # the value path and the gate path each carry a share of the emb gradient
+    assert grads[(True, False)][0].abs().max() > 0 and grads[(False, True)][0].abs().max() > 0
