@@ -47,3 +47,50 @@ def test_abi_version_and_error_string():
     rc = lib.eg_hash_rows(ctypes.byref(spec), None, 0, 0, None, 1, None, None)
     assert rc == _lib.EG_ERR_ARG
     assert b"ngram_size" in lib.eg_last_error()
+
+
+def _rejects(fn, *args) -> tuple[int, str]:
+    from engraft_ngram_amd import _lib
+    rc = fn(*args)
+    return rc, (_lib.load().eg_last_error() or b"").decode()
+
+
+def test_host_side_argument_checks():
+    """Every entry point rejects a bad argument on the host, before any launch,
+    with a status and a message (the Python layer raises ValueError for
+    EG_ERR_ARG, as the reference raises for bad shapes); these run without a GPU."""
+    from engraft_ngram_amd import _lib
+    lib = _lib.load()
+    spec = _lib.EgHashSpec()
+    spec.ngram_size, spec.heads_per_ngram = 3, 8
+    tab = _lib.EgTable()
+    tab.fmt, tab.dim, tab.n_rows = _lib.FMT_BF16, 128, 10
+    cases = [
+        ("n_layers", _lib.EG_ERR_ARG, lib.eg_forward, 3, ctypes.byref(spec), ctypes.byref(tab), None, None, 1, 0, None,
+         None, None, None, None),
+        ("NULL", _lib.EG_ERR_ARG, lib.eg_gather, None, None, None, 1, 1, None, None),
+        ("NULL", _lib.EG_ERR_ARG, lib.eg_descent_step, None, 0, None, 1, 16, None, None, None, None, 0, None),
+        ("Q8_0 or MXFP8", _lib.EG_ERR_ARG, lib.eg_quantize_rows, None, 1, 128, None, ctypes.byref(tab), None),
+        ("n_embd", _lib.EG_ERR_ARG, lib.eg_ple_gate, None, None, None, None, None, None, 1, 4, 5000, 1e-6, None,
+         None, None, None, None),
+        ("taps", _lib.EG_ERR_ARG, lib.eg_ple_conv, None, 0, 1, 4, 64, None, 9, 3, 0, None, None, None, None, None),
+        ("dilation", _lib.EG_ERR_UNSUPPORTED, lib.eg_ple_conv_backward, None, 0, 1, 4, 64, None, 4, 11, None, None,
+         0, None, None),
+        ("hc=5", _lib.EG_ERR_UNSUPPORTED, lib.eg_ple_gate_backward, *([None] * 11), 1, 5, 64, 0, 0, None, None,
+         None, None),
+        ("taps", _lib.EG_ERR_ARG, lib.eg_ple_conv_backward, None, 0, 1, 4, 64, None, 9, 1, None, None, 0, None,
+         None),
+    ]
+    for needle, code, fn, *args in cases:
+        rc, msg = _rejects(fn, *args)
+        assert rc == code, (fn.__name__, rc, msg)
+        assert needle in msg, (fn.__name__, msg)
+    # the workspace check: too small a workspace is its own status
+    need = lib.eg_backward_workspace_size(1000, 100)
+    assert need > 0 and lib.eg_backward_workspace_size(2000, 100) > need
+    ids = ctypes.c_int32(0)
+    rc, msg = _rejects(lib.eg_scatter_grad, ctypes.c_void_p(8), 0, ctypes.c_void_p(8), 10, 16, 128,
+                       ctypes.byref(ids), 1, ctypes.c_void_p(8), ctypes.c_void_p(8), 16, None)
+    assert rc == _lib.EG_ERR_WORKSPACE and "workspace" in msg
+    with pytest.raises(ValueError):
+        _lib.check(_lib.EG_ERR_ARG)
