@@ -140,10 +140,10 @@ def backward_bytes(positions: int, n_unique: int) -> int:
 
 def bench_backward(tab, tokens, steps: int, warmup: int) -> dict:
     """d_residual [16384, 2048] bf16 ~ N(0, 1e-3); scatter of
-    the per-slot row gradients into the fp32 overlay of the touched rows (stable
-    radix sort + segmented reduce), Adam (lr 1e-3, betas 0.9/0.999, eps 1e-8) on
-    the touched rows and requantisation to Q8_0 blocks.  One step = one
-    eg_descent_step call (a handful of launches)."""
+    the per-slot row gradients into the fp32 overlay of the touched rows (slots
+    grouped per row, CSR, then each row's slots summed in slot order), Adam (lr
+    1e-3, betas 0.9/0.999, eps 1e-8) on the touched rows and requantisation to
+    Q8_0 blocks.  One step = one eg_descent_step call (a handful of launches)."""
     import torch
 
     from engraft_ngram_amd import descent as D
@@ -169,8 +169,8 @@ def bench_backward(tab, tokens, steps: int, warmup: int) -> dict:
     return {"us_per_step": ms * 1e3, "touched_rows": state.n, "slot_gradients": rows.numel(),
             "algorithmic_bytes_per_step": nb, "gb_per_s": gbs, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
             "rows_per_s": rows.numel() / (ms * 1e-3),
-            "workload": "BASELINE config 2: scatter (sort + segmented reduce) + sparse Adam + Q8_0 requant, "
-                        "fp32 master/m/v kept"}
+            "workload": "BASELINE config 2: scatter (CSR grouping + slot-ordered segmented reduce) + sparse Adam + "
+                        "Q8_0 requant, fp32 master/m/v kept"}
 
 
 def bench_decode(tab, steps: int) -> dict:

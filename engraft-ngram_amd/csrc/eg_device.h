@@ -168,18 +168,19 @@ __device__ inline uint16_t f32_to_f16(float f) {
   return __builtin_bit_cast(uint16_t, v);
 }
 
-// OCP e4m3 (float8_e4m3fn): bias 7, subnormals m*2^-9, 0x7f/0xff NaN.
-__device__ inline float e4m3_to_f32(uint32_t b) {
-  const uint32_t e = (b >> 3) & 0xfu, m = b & 7u;
-  float v;
-  if ((b & 0x7fu) == 0x7fu) {
-    v = __uint_as_float(0x7fc00000u);
-  } else if (e == 0) {
-    v = (float)m * 0.001953125f;  // 2^-9
-  } else {
-    v = __uint_as_float(((e + 120u) << 23) | (m << 20));  // (1+m/8)*2^(e-7)
-  }
-  return (b & 0x80u) ? -v : v;
+// OCP e4m3 (float8_e4m3fn): bias 7, subnormals m*2^-9, 0x7f/0xff NaN.  gfx950's
+// v_cvt_pk_f32_fp8 converts two such bytes exactly (every code is checked
+// against the definition); byte 0 of b here.
+__device__ inline float e4m3_to_f32(uint32_t b) { return __builtin_amdgcn_cvt_pk_f32_fp8((int)b, false)[0]; }
+
+// The four e4m3 bytes of w, byte 0 first.
+__device__ inline void e4m3x4_to_f32(uint32_t w, float out[4]) {
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);  // bytes 0, 1
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);   // bytes 2, 3
+  out[0] = lo[0];
+  out[1] = lo[1];
+  out[2] = hi[0];
+  out[3] = hi[1];
 }
 
 // e8m0 scale 2^(e-127); 0xff is NaN.
@@ -274,8 +275,10 @@ __device__ inline void decode(const RawChunk& r, int off, float v[8]) {
     }
   } else if constexpr (FMT == EG_FMT_MXFP8) {
     const float sc = e8m0_to_f32(r.s);
+    e4m3x4_to_f32(r.w0[0], v);
+    e4m3x4_to_f32(r.w0[1], v + 4);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = e4m3_to_f32((r.w0[i >> 2] >> ((i & 3) * 8)) & 0xffu) * sc;
+    for (int i = 0; i < 8; ++i) v[i] = v[i] * sc;
   } else if constexpr (FMT == EG_FMT_IQ4_NL) {
     const float d = f16_to_f32((uint16_t)r.s);
     const int sh = ((off & 31) >= 16) ? 4 : 0;

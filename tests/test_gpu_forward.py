@@ -398,3 +398,24 @@ def test_forward_graph_capture_replays(cuda):
         assert torch.equal(out, eager), f"replay {k}"
         _, _, exp = FW.forward(spec, tokens, fetch, G.bf16_bits(res), overlay=(ov_ids, ov_rows), seq_len=1024)
         G.assert_out_matches(G.bf16_bits(out), exp)
+
+
+def test_mxfp8_every_code_decodes_exactly(cuda):
+    """Every e4m3 code (0..255) under e8m0 scales 2^0, 2^-7, 2^7 and 2^-126 (the
+    last giving subnormal products), through eg_gather -- gfx950's packed fp8
+    conversion -- against the oracle's definition of the format: bit-exact,
+    and NaN exactly where the code is 0x7f or 0xff."""
+    _say("mxfp8 every code")
+    spec = synthetic_spec(n_rows=16, seed=3)  # 16 heads of one row each
+    codes = np.arange(256, dtype=np.uint8).reshape(2, 128)
+    payload = np.zeros((16, 128), dtype=np.uint8)
+    scales = np.full((16, 4), 127, dtype=np.uint8)
+    for i, e in enumerate((127, 120, 134, 1)):
+        payload[2 * i:2 * i + 2] = codes
+        scales[2 * i:2 * i + 2] = e
+    tab = G.table_from_arrays(spec, "mxfp8", 128, payload, scales)
+    got = tab.gather(torch.arange(16, dtype=torch.int32).reshape(-1, 1)).cpu().numpy()
+    exp = G.F.dequant_mxfp8(payload, scales)
+    nan = np.isnan(exp)
+    assert nan.sum() == 4 * 2 and np.array_equal(np.isnan(got), nan)  # 0x7f and 0xff per scale
+    assert np.array_equal(got[~nan].view(np.uint32), exp[~nan].view(np.uint32))
