@@ -84,9 +84,9 @@ class _Events:
 
 def traffic_from_profile(kernel_key: str):
     """HBM bytes per launch of a kernel from the committed rocprofv3 PMC summary
-    (``profiles/pmc_traffic.md``: FETCH_SIZE x its copy-kernel factor +
+    (``profiles/hbm_traffic_forward_descent_kernels_cfg1-4.md``: FETCH_SIZE x its copy-kernel factor +
     WRITE_SIZE x its factor), or None when the summary is absent."""
-    path = ROOT / "profiles" / "pmc_traffic.md"
+    path = ROOT / "profiles" / "hbm_traffic_forward_descent_kernels_cfg1-4.md"
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
