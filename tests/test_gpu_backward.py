@@ -283,3 +283,29 @@ def test_frozen_rows_masked_step_against_torch_adam(cuda):
     fz = np.nonzero(~row_mask)[0]
     assert np.array_equal(st.quant.payload.cpu().numpy().view(np.int8)[fz], q_exp)
     assert np.array_equal(st.quant.scales.cpu().numpy().view(np.float16)[fz], s_exp)
+
+
+def test_descent_step_edge_cases(cuda):
+    """A step without slots (sparse: nothing moves; dense: the zero-gradient step,
+    whose pull term is zero at the start rows, leaves the rows as they are), and
+    slots that hit no variable."""
+    from engraft_ngram_amd import descent as D
+    _say("descent edge cases")
+    spec = synthetic_spec(n_rows=16 * 1000, seed=101)
+    tab = G.device_table(spec, "q8_0", 16 * 1000, 128, seed=102)
+    tokens = synth.zipf_tokens(103, 256, 2000)
+    rows = H.ngram_rows_np(spec, tokens).astype(np.int32)
+    st = D.DescentState.from_rows(tab, torch.from_numpy(rows))
+    p0, q0 = st.master.clone(), st.quant.payload.clone()
+    none_d = torch.zeros((0, 16 * 128), dtype=torch.bfloat16, device=cuda)
+    none_r = torch.zeros((0, 16), dtype=torch.int32)
+    st.step(none_d, none_r, lr=1e-3)
+    assert st.step_count == 1 and torch.equal(st.master, p0) and torch.equal(st.quant.payload, q0)
+    st.step(none_d, none_r, lr=1e-3, dense=True, mu=0.1)
+    assert st.step_count == 2 and torch.equal(st.master, p0) and float(st.m.abs().max()) == 0.0
+    # slots whose rows are not variables
+    ids = st.ids.cpu().numpy()
+    free = int(np.setdiff1d(np.arange(16 * 1000), ids)[0])
+    d = (torch.randn((256, 16 * 128), device=cuda) * 1e-3).to(torch.bfloat16)
+    st.step(d, torch.full((256, 16), free, dtype=torch.int32), lr=1e-3)
+    assert torch.equal(st.master, p0)

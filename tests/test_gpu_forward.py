@@ -419,3 +419,35 @@ def test_mxfp8_every_code_decodes_exactly(cuda):
     nan = np.isnan(exp)
     assert nan.sum() == 4 * 2 and np.array_equal(np.isnan(got), nan)  # 0x7f and 0xff per scale
     assert np.array_equal(got[~nan].view(np.uint32), exp[~nan].view(np.uint32))
+
+
+def test_forward_edge_cases(cuda):
+    """Empty input; one-token and ragged segments (the hash substitutes EOS for
+    missing predecessors and never looks across a segment start); a last
+    sequence shorter than seq_len; the residual updated in place."""
+    from engraft_ngram_amd import table as T
+    _say("forward edge cases")
+    spec = synthetic_spec(n_rows=16 * 1000, seed=91)
+    tab = G.device_table(spec, "q8_0", 16 * 1000, 128, seed=92)
+    fetch = G.synth_fetch("q8_0", 92, 128)
+    empty = tab.forward(torch.zeros(0, dtype=torch.int64), torch.zeros((0, 2048), dtype=torch.bfloat16, device=cuda))
+    assert empty.shape == (0, 2048)
+    rng = np.random.default_rng(93)
+    tokens = rng.integers(0, 40, size=37)
+    # ragged segments, including single-token ones
+    starts = np.array([0, 1, 2, 9, 10, 30, 36])
+    seg_start = np.zeros(37, dtype=np.int32)
+    for s in starts:
+        seg_start[s:] = s
+    res = G.residual(37, 2048, seed=94)
+    out = tab.forward(torch.from_numpy(tokens), res, seg_start=torch.from_numpy(seg_start))
+    _, _, exp = FW.forward(spec, tokens, fetch, G.bf16_bits(res), seg_start=seg_start)
+    G.assert_out_matches(G.bf16_bits(out), exp)
+    # seq_len 16 over 37 positions: the last sequence holds 5
+    out = tab.forward(torch.from_numpy(tokens), res, seq_len=16)
+    _, _, exp = FW.forward(spec, tokens, fetch, G.bf16_bits(res), seq_len=16)
+    G.assert_out_matches(G.bf16_bits(out), exp)
+    # in place: out is the residual
+    res2 = res.clone()
+    T.forward([tab], torch.from_numpy(tokens), res2, out=res2, seq_len=16)
+    assert torch.equal(res2, out)
