@@ -31,18 +31,24 @@ _POLICIES = ("all-read", "private", "entity", "t8-answer")
 
 
 class _Workspace:
-    """Grow-only device workspace for the backward kernels (per device)."""
+    """Grow-only device workspace for the backward kernels, one per (device,
+    stream): calls on one stream run in order and may share it; calls on
+    different streams get different buffers, so they never race on it.  A
+    buffer that is replaced by a larger one was allocated and used on the same
+    stream, so torch's allocator reuses its memory only after that stream's
+    earlier work."""
 
     def __init__(self):
-        self._buf: dict[torch.device, torch.Tensor] = {}
+        self._buf: dict[tuple[torch.device, int], torch.Tensor] = {}
 
     def get(self, n_slots: int, n_var: int, device) -> torch.Tensor:
         need = int(_lib.load().eg_backward_workspace_size(int(n_slots), int(n_var)))
         dev = torch.device(device)
-        buf = self._buf.get(dev)
+        key = (dev, int(torch.cuda.current_stream(dev).cuda_stream))
+        buf = self._buf.get(key)
         if buf is None or buf.numel() < need:
             buf = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
-            self._buf[dev] = buf
+            self._buf[key] = buf
         return buf
 
 
