@@ -6,9 +6,10 @@ reference (``engraft/replica/distill.py:378-453`` row variables,
   values, read from the device table (same names, arguments and errors).
 * ``scatter_grad`` -- the gradient of the variables from ``d_out`` and the slot
   row ids: the autograd of ``rows_var[idx_r]`` + ``index_put``
-  (``engraft/replica/seq.py:433-441``), computed by a stable radix sort of
-  (variable, slot) and a segmented reduction in ascending slot order on the
-  device -- bitwise repeatable.
+  (``engraft/replica/seq.py:433-441``), computed on the device by grouping
+  the slots per variable (counts, range starts, a scatter at start + rank)
+  and a reduction of each variable's slots in ascending slot order -- bitwise
+  repeatable.
 * ``DescentState`` -- ``rows_var`` (fp32 master rows), Adam moments and a
   requantised copy in HBM; ``step`` runs scatter + Adam (torch's single-tensor
   order, fp32) + requantisation in one call (``eg_descent_step``), in the

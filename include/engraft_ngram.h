@@ -156,9 +156,9 @@ int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* r
  * (engraft/replica/distill.py:401-453 row_map, ascending).  Every slot (p, h)
  * whose row id is one of them contributes d_out[p, h*dim:(h+1)*dim] to that
  * variable's gradient (the autograd of rows_var[idx_r] + index_put,
- * engraft/replica/seq.py:433-441).  Contributions are merged by a stable radix
- * sort of (variable, slot) and a segmented reduction in ascending slot order:
- * the result is bitwise repeatable and independent of scheduling. */
+ * engraft/replica/seq.py:433-441).  The slots are grouped per variable and
+ * each variable's contributions are summed in ascending slot order: the result
+ * is bitwise repeatable and independent of scheduling. */
 
 /* Adam hyper-parameters of one step (torch.optim.Adam, engraft/descend_corpus.py:785-790). */
 typedef struct eg_adam {

@@ -6,7 +6,7 @@
   gives ``grad[r] = sum over (t, h) with row_map[rows[t, h]] == r of
   d_emb[t, h, :]``.  The slots of a variable are taken in ascending slot order
   (``slot = t*n_heads + h``) and summed in fp32 with the association the
-  device's sort + segmented reduce fixes (``segment_sum``: sequential up to 32
+  device's slot-ordered reduction fixes (``segment_sum``: sequential up to 32
   slots, pieces of 32 grouped mod 8 beyond); ``scatter_grad_exact`` gives the
   fp64 sum.
 * ``adam_step``     -- ``torch.optim.Adam`` (``engraft/descend_corpus.py:
