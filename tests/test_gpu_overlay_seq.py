@@ -210,3 +210,29 @@ def test_sum_overlays_against_oracle(cuda, tmp_path, n_files):
     exp_rows, exp_data = OS.write_merged_rows(row_map, rv.numpy(), e_rows[:10].tolist(), fetch)
     assert np.array_equal(got_rows, exp_rows) and np.array_equal(got_data, exp_data)
     assert info["n_rows_frozen"] == 8
+
+
+def test_lookup_rows_sorted_search_edges(cuda):
+    """eg_lookup_rows' search of the sorted ids (the same search resolves the
+    forward's overlay ids) against numpy's searchsorted: every size from 1 to
+    40 ids and 500,000, keys present, absent between ids, below the first and
+    above the last; the read counts of the found ids."""
+    from engraft_ngram_amd import _lib
+    _say("sorted-id search edges")
+    rng = np.random.default_rng(41)
+    for n in list(range(1, 41)) + [500_000]:
+        ids = np.unique(rng.integers(0, 2**31 - 2, size=2 * n))[:n].astype(np.int32)
+        keys = np.concatenate([ids, ids - 1, ids + 1, [0, 2**31 - 1]]).astype(np.int32)
+        if n > 40:
+            keys = keys[rng.choice(keys.size, 20_000, replace=False)]
+        pos = np.searchsorted(ids, keys)
+        hit = (pos < n) & (ids[np.minimum(pos, n - 1)] == keys)
+        exp = np.where(hit, pos, -1).astype(np.int32)
+        ids_d = torch.from_numpy(ids).to(cuda)
+        keys_d = torch.from_numpy(keys).to(cuda)
+        out = torch.empty_like(keys_d)
+        counts = torch.zeros(n, dtype=torch.int64, device=cuda)
+        _lib.call("eg_lookup_rows", _lib.ptr(keys_d), keys.size, _lib.ptr(ids_d), None, n, _lib.ptr(out),
+                  _lib.ptr(counts), _lib.stream_ptr(cuda))
+        assert np.array_equal(out.cpu().numpy(), exp), n
+        assert np.array_equal(counts.cpu().numpy(), np.bincount(exp[exp >= 0], minlength=n)), n
