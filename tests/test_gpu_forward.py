@@ -451,3 +451,25 @@ def test_forward_edge_cases(cuda):
     res2 = res.clone()
     T.forward([tab], torch.from_numpy(tokens), res2, out=res2, seq_len=16)
     assert torch.equal(res2, out)
+
+
+def test_forward_on_two_streams(cuda):
+    """Calls on different streams are independent: two batches launched on two
+    non-default streams (default priority) give the results of the same calls
+    made one after the other on the default stream."""
+    _say("forward on two streams")
+    spec = synthetic_spec(n_rows=16 * 2000, seed=111)
+    tab = G.device_table(spec, "q8_0", 16 * 2000, 128, seed=112)
+    toks = [torch.from_numpy(synth.zipf_tokens(113 + k, 4096, 5000)) for k in range(2)]
+    res = [G.residual(4096, 2048, seed=115 + k) for k in range(2)]
+    exp = [tab.forward(toks[k], res[k], seq_len=1024) for k in range(2)]
+    torch.cuda.synchronize(cuda)
+    streams = [torch.cuda.Stream(cuda) for _ in range(2)]
+    got = [None, None]
+    for k in range(2):
+        streams[k].wait_stream(torch.cuda.current_stream(cuda))
+        with torch.cuda.stream(streams[k]):
+            got[k] = tab.forward(toks[k], res[k], seq_len=1024)
+    torch.cuda.synchronize(cuda)
+    for k in range(2):
+        assert torch.equal(got[k], exp[k])
