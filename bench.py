@@ -35,7 +35,7 @@ HBM_PEAK_GBS = 8000.0
 N_ROWS, DIM, BATCH, SEQ, VOCAB, WIDTH, SLOTS = 320_000_000, 128, 8, 2048, 151_936, 2048, 16
 TABLE_SEED, HASH_SEED, TOKEN_SEED, RES_SEED = 201, 200, 202, 203
 TOKEN_SETS, RES_SETS = 16, 4  # token batches and residual sets rotated in the timed loop
-DECODE_SEED, C4_SEED, PLE_SEED = 300, 400, 500
+DECODE_SEED, C4_SEED, PLE_SEED, REAL_SEED = 300, 400, 500, 600
 Q8_ROW_BYTES = DIM + 2 * DIM // 32  # 128 B int8 + 4 fp16 scales = 136 B
 
 
@@ -266,6 +266,67 @@ def bench_config4(steps: int, warmup: int) -> dict:
             "frac_of_hbm_peak": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": nbytes}
 
 
+def bench_real_format(steps: int, warmup: int) -> dict:
+    """The reference's own table format (the f4 path, engraft/table.py:40-169):
+    16 heads x 20,000,096 rows of 160 values in IQ4_NL blocks (90 B per row,
+    28.8 GB), the reference's hash mode (three multipliers shared by every head),
+    16,384 Zipf tokens per step into a bf16 residual [16384, 2560]; 16 token
+    batches and 4 residual sets rotate.  Rows: random nibbles, block scale
+    fp16(0.002)."""
+    import numpy as np
+    import torch
+
+    from engraft_ngram_amd import synthetic as S
+    from engraft_ngram_amd import table as T
+
+    dev = torch.device("cuda", 0)
+    per, heads, dim = 20_000_096, 16, 160
+    n_rows, width = per * heads, heads * dim
+    store = T.RowStore.empty("iq4_nl", n_rows, dim, dev)
+    g = torch.Generator(device=dev).manual_seed(REAL_SEED)
+    chunk = 1 << 26
+    scale = np.array([0.002], dtype=np.float16).view(np.uint8)
+    for r0 in range(0, n_rows, chunk):
+        blk = store.payload[r0:r0 + chunk]
+        blk.random_(0, 256, generator=g)
+        v = blk.view(-1, dim // 32, 18)
+        v[:, :, 0] = int(scale[0])
+        v[:, :, 1] = int(scale[1])
+    mults = [int(m) for m in S.odd_multipliers(REAL_SEED, 3)]
+    tab = T.DeviceTable(store, eos_token_id=S.QWEN_EOS, ngram_size=3, heads_per_ngram=8, layer_multipliers=mults,
+                        head_vocab_sizes=[per] * heads, head_offsets=[h * per for h in range(heads)])
+    n_pos = BATCH * SEQ
+    toks = [torch.from_numpy(S.zipf_tokens(REAL_SEED + 1 + 1000 * j, n_pos, VOCAB)).to(dev) for j in range(TOKEN_SETS)]
+    res = [S.residual(n_pos, width, seed=REAL_SEED + 50 + i, device=dev) for i in range(RES_SETS)]
+    outs = [torch.empty_like(r) for r in res]
+    n_sets = max(TOKEN_SETS, RES_SETS)
+    calls = [T.PreparedForward([tab], toks[i % TOKEN_SETS], res[i % RES_SETS], out=outs[i % RES_SETS], seq_len=SEQ)
+             for i in range(n_sets)]
+    for i in range(warmup):
+        calls[i % n_sets]()
+    ev = _Events(4)
+    torch.cuda.synchronize()
+    for i in range(steps):
+        c = calls[i % n_sets]
+        if i == 0:
+            c.timed(ev[0], ev[1] if steps > 1 else ev[3])
+        elif i == steps - 1:
+            c.timed(ev[2], ev[3])
+        else:
+            c()
+    torch.cuda.synchronize()
+    us = ev.elapsed_ms(0, 3) / steps * 1e3
+    ev.destroy()
+    nbytes = n_pos * (heads * 90 + 2 * 2 * width + 8)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del tab, store
+    torch.cuda.empty_cache()
+    return {"workload": "the reference's real table format: 16 heads x 20,000,096 IQ4_NL rows of 160 (90 B), "
+                        "shared multipliers, 16,384 Zipf tokens, residual width 2560",
+            "us_per_launch": us, "rows_per_s": n_pos * heads / (us * 1e-6), "gb_per_s": gbs,
+            "frac_of_hbm_peak": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": nbytes}
+
+
 def bench_ple(steps: int, warmup: int) -> dict:
     """The PLE block consuming the rows (engraft/replica/layers.py:565-626) at
     the real model's dimensions: 2048 positions, 4 hyper-connection streams,
@@ -470,6 +531,10 @@ def main() -> None:
         result["forward_config4"] = c4
         log(f"forward (config 4): {c4['us_per_launch']:.1f} us/launch, {c4['gb_per_s']:.0f} GB/s algorithmic "
             f"({100 * c4['frac_of_hbm_peak']:.1f}% of peak)")
+        rf = bench_real_format(max(1, args.steps // 4), max(1, args.warmup))
+        result["forward_real_format"] = rf
+        log(f"forward (real IQ4_NL format): {rf['us_per_launch']:.1f} us/launch, {rf['gb_per_s']:.0f} GB/s "
+            f"algorithmic ({100 * rf['frac_of_hbm_peak']:.1f}% of peak)")
         pl = bench_ple(max(1, args.steps // 10), max(1, args.warmup // 10))
         result["ple_forward"] = pl
         log(f"ple_forward: {pl['us_per_step']:.0f} us/step; its two GEMMs alone {pl['gemm_us']:.0f} us "

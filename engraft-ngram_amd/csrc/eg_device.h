@@ -207,12 +207,20 @@ __device__ inline uint32_t f32_to_e4m3(float x) {
   return code | sign;
 }
 
-// IQ4_NL codebook (GGML kvalues_iq4nl; engraft/table.py:26-29).
-__device__ inline float iq4nl_value(uint32_t nib) {
-  constexpr int8_t kv[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
-                             1,    13,   25,  38,  53,  69,  89,  113};
-  return (float)kv[nib & 15u];
+// IQ4_NL codebook (GGML kvalues_iq4nl; engraft/table.py:26-29):
+//   -127 -104 -83 -65 -49 -35 -22 -10 1 13 25 38 53 69 89 113
+// held in registers as int8 bytes.  iq4nl_lookup4 maps four nibbles at once
+// (one per byte of n, each < 16) to four int8 codebook bytes: v_perm_b32 picks
+// bytes of a 64-bit pair by a 3-bit index, and bit 3 chooses the half.
+__device__ inline uint32_t iq4nl_lookup4(uint32_t n) {
+  const uint32_t sel = n & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(0xF6EADDCFu, 0xBFAD9881u, sel);  // kvalues[0..7]
+  const uint32_t hi = __builtin_amdgcn_perm(0x71594535u, 0x26190D01u, sel);  // kvalues[8..15]
+  const uint32_t m = ((n >> 3) & 0x01010101u) * 0xffu;
+  return (hi & m) | (lo & ~m);
 }
+
+__device__ inline float iq4nl_value(uint32_t nib) { return (float)(int8_t)(iq4nl_lookup4(nib & 15u) & 0xffu); }
 
 // ---------------------------------------------------------------------------
 // Row chunk loads: 8 consecutive values [off, off+8) of a row, dequantised to
@@ -248,11 +256,18 @@ __device__ inline RawChunk load_raw(const TableDev& t, int dim, int64_t row, int
     r.w0 = *(const u32x4*)(t.payload + (row * dim + off) * 2);
   } else if constexpr (FMT == EG_FMT_IQ4_NL) {
     // 18-byte blocks: fp16 d, then 16 bytes of nibbles; value j < 16 is the low
-    // nibble of byte j, value j >= 16 the high nibble of byte j-16.
+    // nibble of byte j, value j >= 16 the high nibble of byte j-16.  The chunk's
+    // 8 nibble bytes start at an even address q: the aligned 8 bytes at q & ~3
+    // and the halfword at q + 6 hold them whatever q % 4 is, and no load reaches
+    // past the block.
     const uint8_t* blk = t.payload + row * (int64_t)((dim >> 5) * 18) + (off >> 5) * 18;
     r.s = *(const uint16_t*)blk;
-    const uint16_t* qs = (const uint16_t*)(blk + 2 + (off & 15));
-    r.w0 = u32x4{qs[0], qs[1], qs[2], qs[3]};
+    const uint8_t* q = blk + 2 + (off & 15);
+    const uint32_t mis = (uint32_t)(uintptr_t)q & 3u;  // 0 or 2
+    const uint32_t* al = (const uint32_t*)(q - mis);  // 4-byte aligned
+    const uint32_t d0 = al[0], d1 = al[1];
+    const uint32_t tail = *(const uint16_t*)(q + 6);
+    r.w0 = u32x4{__builtin_amdgcn_alignbyte(d1, d0, mis), __builtin_amdgcn_alignbyte(tail, d1, mis), 0u, 0u};
   } else {  // EG_FMT_F32
     const u32x4* src = (const u32x4*)(t.payload + (row * dim + off) * 4);
     r.w0 = src[0];
@@ -283,9 +298,10 @@ __device__ inline void decode(const RawChunk& r, int off, float v[8]) {
     const float d = f16_to_f32((uint16_t)r.s);
     const int sh = ((off & 31) >= 16) ? 4 : 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = iq4nl_value((r.w0[i] >> sh) & 15u) * d;
-      v[2 * i + 1] = iq4nl_value((r.w0[i] >> (8 + sh)) & 15u) * d;
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t q = iq4nl_lookup4((r.w0[w] >> sh) & 0x0f0f0f0fu);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[4 * w + i] = (float)(int8_t)(q >> (8 * i)) * d;
     }
   } else {
 #pragma unroll

@@ -354,6 +354,16 @@ static bool launch_special(const FwdArgs& a, bool ovl, hipStream_t st) {
   return true;
 }
 
+// The reference's real table shape (16 heads of 160 values, W = 2560, one
+// layer, no overlay): five 512-column chunks per position.
+constexpr int kRealNch = 5;
+template <int FMT>
+static bool launch_real(const FwdArgs& a, bool ovl, hipStream_t st) {
+  if (a.dim != 160 || a.heads * a.dim != 2560 || a.n_layers != 1 || ovl) return false;
+  launch_nch<FMT, 160, kRealNch, 1, false, false, 5 / kRealNch>(a, st);
+  return true;
+}
+
 // Any shape: runtime dim, 1024-column parts, overlays compiled in.
 template <int FMT, bool F32OUT>
 static void launch_generic(const FwdArgs& a, hipStream_t st) {
@@ -372,6 +382,7 @@ static int launch_forward(const FwdArgs& a, hipStream_t st) {
     if (fmt == EG_FMT_Q8_0) done = launch_special<EG_FMT_Q8_0>(a, ovl, st);
     else if (fmt == EG_FMT_BF16) done = launch_special<EG_FMT_BF16>(a, ovl, st);
     else if (fmt == EG_FMT_MXFP8) done = launch_special<EG_FMT_MXFP8>(a, ovl, st);
+    else if (fmt == EG_FMT_IQ4_NL) done = launch_real<EG_FMT_IQ4_NL>(a, ovl, st);
     if (done) return launch_status("forward_kernel");
   }
   switch (fmt) {
