@@ -35,7 +35,7 @@ HBM_PEAK_GBS = 8000.0
 N_ROWS, DIM, BATCH, SEQ, VOCAB, WIDTH, SLOTS = 320_000_000, 128, 8, 2048, 151_936, 2048, 16
 TABLE_SEED, HASH_SEED, TOKEN_SEED, RES_SEED = 201, 200, 202, 203
 TOKEN_SETS, RES_SETS = 16, 4  # token batches and residual sets rotated in the timed loop
-DECODE_SEED, C4_SEED, PLE_SEED, REAL_SEED = 300, 400, 500, 600
+DECODE_SEED, C4_SEED, PLE_SEED, REAL_SEED, SCAN_SEED = 300, 400, 500, 600, 700
 Q8_ROW_BYTES = DIM + 2 * DIM // 32  # 128 B int8 + 4 fp16 scales = 136 B
 
 
@@ -327,6 +327,63 @@ def bench_real_format(steps: int, warmup: int) -> dict:
             "frac_of_hbm_peak": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": nbytes}
 
 
+def bench_damage_scan(tab, steps: int) -> dict:
+    """The damage scan (the f3 path, engraft/damage.py:159-224): one corpus block
+    of 8,000,000 Zipf tokens (the reference's block size, damage.py:60) against
+    500,000 sorted overlay rows with their dnorm, on the config-1 table's hash:
+    the fused eg_scan_overlay launch on device-resident tokens (HIP events),
+    and damage.scan_hits end to end (tokens from the host, hit lists back)."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from engraft_ngram_amd import _lib, damage
+    from engraft_ngram_amd import synthetic as S
+
+    dev = tab.device
+    n = 8_000_000
+    tokens = S.zipf_tokens(SCAN_SEED, n, VOCAB)
+    rng = np.random.default_rng(SCAN_SEED + 1)
+    ids = np.unique(rng.integers(0, N_ROWS, size=520_000))[:500_000].astype(np.int32)
+    dnorm = rng.random(ids.size).astype(np.float32)
+    tok = torch.from_numpy(tokens).to(dev)
+    ids_d, dn_d = torch.from_numpy(ids).to(dev), torch.from_numpy(dnorm).to(dev)
+    n_hit = torch.empty(n, dtype=torch.int32, device=dev)
+    dmax, dsum = torch.empty(n, device=dev), torch.empty(n, device=dev)
+    counts = torch.zeros(ids.size, dtype=torch.int64, device=dev)
+    spec = tab.c_spec
+    n_bits = tab.n_rows
+    bitmap = torch.empty(2 * ((n_bits + 31) // 32), dtype=torch.int32, device=dev)
+    _lib.call("eg_build_id_bitmap", _lib.ptr(ids_d), ids.size, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(dev))
+
+    def timed(bm) -> float:
+        args = (ctypes.byref(spec), _lib.ptr(tok), n, 0, _lib.ptr(ids_d), ids.size, bm, n_bits, _lib.ptr(dn_d),
+                _lib.ptr(n_hit), _lib.ptr(dmax), _lib.ptr(dsum), _lib.ptr(counts), _lib.stream_ptr(dev))
+        for _ in range(3):
+            _lib.call("eg_scan_overlay", *args)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            _lib.call("eg_scan_overlay", *args)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / steps * 1e3
+
+    us_search = timed(None)
+    us = timed(_lib.ptr(bitmap))
+    damage.scan_hits(tokens[:100_000], tab, ids, dnorm)  # warm the host path
+    t0 = time.perf_counter()
+    res = damage.scan_hits(tokens, tab, ids, dnorm)
+    wall = time.perf_counter() - t0
+    lookups = n * tab.n_heads
+    return {"workload": "damage scan: 8,000,000 Zipf tokens x 16 rows against 500,000 sorted overlay rows",
+            "us_per_block_kernel": us, "us_per_block_kernel_search_only": us_search, "tokens_per_s_kernel": n / (us * 1e-6),
+            "lookups_per_s_kernel": lookups / (us * 1e-6), "s_per_block_end_to_end": wall,
+            "hit_positions": int(res["pos"].size)}
+
+
 def bench_ple(steps: int, warmup: int) -> dict:
     """The PLE block consuming the rows (engraft/replica/layers.py:565-626) at
     the real model's dimensions: 2048 positions, 4 hyper-connection streams,
@@ -531,6 +588,11 @@ def main() -> None:
         result["forward_config4"] = c4
         log(f"forward (config 4): {c4['us_per_launch']:.1f} us/launch, {c4['gb_per_s']:.0f} GB/s algorithmic "
             f"({100 * c4['frac_of_hbm_peak']:.1f}% of peak)")
+        ds = bench_damage_scan(tab, 20)
+        result["damage_scan"] = ds
+        log(f"damage scan: {ds['us_per_block_kernel']:.0f} us per 8M-token block on the device "
+            f"({ds['lookups_per_s_kernel'] / 1e9:.1f} G lookups/s), {ds['s_per_block_end_to_end'] * 1e3:.0f} ms end "
+            f"to end")
         rf = bench_real_format(max(1, args.steps // 4), max(1, args.warmup))
         result["forward_real_format"] = rf
         log(f"forward (real IQ4_NL format): {rf['us_per_launch']:.1f} us/launch, {rf['gb_per_s']:.0f} GB/s "

@@ -2,16 +2,17 @@
 ``ngram_rows`` / ``iter_blocks`` / ``scan_hits`` / ``compute_rows_delta``
 (``engraft/damage.py:68-224``).
 
-``scan_hits`` hashes a corpus block (``eg_hash_rows``, the whole block as one
-sequence, so every position sees its real predecessors), resolves each of the
-``n_heads`` rows of every position against the sorted overlay ids with
-``eg_lookup_rows`` (which also counts the reads of every overlay row), and
-reduces per position the number of overlay rows read and the max / sum of
-their ``dnorm``.  Blocks overlap by ``ngram_size - 1`` tokens, whose positions
-are dropped, so the result equals a scan of the whole corpus as one sequence.
+``scan_hits`` runs one fused launch per corpus block (``eg_scan_overlay``):
+every position hashes its ``n_heads`` rows (the whole block as one sequence,
+so every position sees its real predecessors), looks each up in the sorted
+overlay ids, counts the reads of every overlay row and reduces per position
+the number of overlay rows read and the max / sum of their ``dnorm``.  Blocks
+overlap by ``ngram_size - 1`` tokens, whose positions are dropped, so the
+result equals a scan of the whole corpus as one sequence.
 """
 from __future__ import annotations
 
+import ctypes
 import time
 from typing import Iterator
 
@@ -93,28 +94,36 @@ def scan_hits(tokens: np.ndarray, table, overlay_sorted: np.ndarray, dnorm_sorte
     hist = table.ngram_size - 1
     pos_parts, nh_parts, dmax_parts, dsum_parts = [], [], [], []
     t0 = time.time()
+    spec = table.c_spec
+    # membership bitmap over the table's rows: almost every lookup is a miss,
+    # settled by one bit instead of the binary search
+    n_bits = max(int(table.n_rows), 1)
+    bitmap = torch.empty(2 * ((n_bits + 31) // 32), dtype=torch.int32, device=dev)
+    if n_ov:
+        _lib.call("eg_build_id_bitmap", _lib.ptr(ids), n_ov, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(dev))
     for offset, blk in iter_blocks(tokens, block=block, overlap=hist):
         start_local = 0 if offset == 0 else hist
-        rows = table.rows(torch.as_tensor(np.asarray(blk, dtype=np.int64)))[start_local:].contiguous()
-        m = rows.shape[0]
-        if m == 0 or n_ov == 0:
+        tok = torch.as_tensor(np.asarray(blk, dtype=np.int64)).to(dev)
+        m = tok.numel() - start_local
+        if m <= 0 or n_ov == 0:
             continue
-        k = torch.empty_like(rows)
-        _lib.call("eg_lookup_rows", _lib.ptr(rows), rows.numel(), _lib.ptr(ids), None, n_ov, _lib.ptr(k),
-                  _lib.ptr(counts), _lib.stream_ptr(dev))
-        matched = k >= 0
-        n_hit = matched.sum(dim=1)
+        # one fused launch: hash, membership, per-position reductions, read counts
+        n_hit = torch.empty(m, dtype=torch.int32, device=dev)
+        dmax = torch.empty(m, dtype=torch.float32, device=dev)
+        dsum = torch.empty(m, dtype=torch.float32, device=dev)
+        _lib.call("eg_scan_overlay", ctypes.byref(spec), _lib.ptr(tok), tok.numel(), start_local, _lib.ptr(ids), n_ov,
+                  _lib.ptr(bitmap), n_bits, _lib.ptr(dn), _lib.ptr(n_hit), _lib.ptr(dmax), _lib.ptr(dsum), _lib.ptr(counts),
+                  _lib.stream_ptr(dev))
         hit_local = torch.nonzero(n_hit > 0).reshape(-1)
         pos_here = hit_local + offset
         keep = pos_here < (n - 1)
         hit_local = hit_local[keep]
         if hit_local.numel() == 0:
             continue
-        md = torch.where(matched[hit_local], dn[k[hit_local].clamp_min(0).long()], torch.zeros((), device=dev))
         pos_parts.append(pos_here[keep].cpu().numpy().astype(np.int64))
         nh_parts.append(n_hit[hit_local].cpu().numpy().astype(np.int32))
-        dmax_parts.append(md.max(dim=1).values.cpu().numpy().astype(np.float32))
-        dsum_parts.append(md.sum(dim=1).cpu().numpy().astype(np.float32))
+        dmax_parts.append(dmax[hit_local].cpu().numpy().astype(np.float32))
+        dsum_parts.append(dsum[hit_local].cpu().numpy().astype(np.float32))
     read_count = counts[:n_ov].cpu().numpy().astype(np.int64)
     dt = time.time() - t0
 

@@ -23,6 +23,7 @@
  *   eg_lookup_rows   row_map / sorted-overlay membership + read counts
  *                                                    engraft/replica/seq.py:412-417,
  *                                                    engraft/damage.py:192-197
+ *   eg_scan_overlay  the damage scan of a token block  engraft/damage.py:159-224
  *   eg_gather_slots  OverlayEmb.build's base gather + index_put
  *                                                    engraft/replica/seq.py:372-444
  *   eg_descent_step  scatter + torch.optim.Adam step on the overlay rows
@@ -226,6 +227,27 @@ int eg_quantize_rows(const float* src, int64_t n, int32_t dim, const int32_t* ds
  * += the number of reads of each id (engraft/damage.py:192-197 read_count). */
 int eg_lookup_rows(const int32_t* rows, int64_t n, const int32_t* ids, const int32_t* index,
                    int64_t n_ids, int32_t* out, int64_t* counts, void* stream);
+
+/* Damage scan of one token block (engraft/damage.py:159-224, fused): positions
+ * start..n_tokens-1 of tokens (device int64, the block as one sequence) hash
+ * their rows; each row is looked up in the sorted overlay ids (int32 [n_ids],
+ * n_ids >= 1) and, per position, n_hit int32 = the rows found, dnorm_max /
+ * dnorm_sum f32 = max / sum of dnorm[k] over them (0 when none); read_counts
+ * int64 [n_ids] += the reads of every overlay row.  Outputs have n_tokens -
+ * start entries.  No per-slot array is written.  bitmap (optional, from
+ * eg_build_id_bitmap over the same ids, n_bits covering every row id) replaces
+ * the binary search with a probe of the rank bitmap. */
+int eg_scan_overlay(const eg_hash_spec* spec, const int64_t* tokens, int64_t n_tokens, int64_t start,
+                    const int32_t* ids, int64_t n_ids, const uint32_t* bitmap, int64_t n_bits,
+                    const float* dnorm, int32_t* n_hit, float* dnorm_max, float* dnorm_sum,
+                    int64_t* read_counts, void* stream);
+
+/* Rank bitmap of sorted, unique overlay ids for eg_scan_overlay: bitmap is
+ * uint32 [2 * nw], nw = ceil(n_bits/32); word w < nw gets bit b set for every
+ * id 32 w + b < n_bits (all other bits cleared), and bitmap[nw + w] = the
+ * number of ids below 32 w.  No counterpart in the reference: it turns the
+ * scan's per-lookup binary search into one probe. */
+int eg_build_id_bitmap(const int32_t* ids, int64_t n_ids, uint32_t* bitmap, int64_t n_bits, void* stream);
 
 /* Gather with per-slot replacement rows (engraft/replica/seq.py:433-441):
  * out f32 [n_pos, heads*dim]; slot (p, h) reads vars[slot_var[p, h]] (f32

@@ -170,6 +170,54 @@ def test_scan_hits_against_oracle(cuda):
         np.testing.assert_allclose(got["dnorm_sum"], exp["dnorm_sum"], rtol=1e-6)
 
 
+def test_scan_overlay_rank_bitmap(cuda):
+    """eg_scan_overlay with and without the eg_build_id_bitmap rank bitmap:
+    the bits hold exactly the ids below n_bits (an id past the table's rows is
+    left out and still never hits), the ranks are the lower bounds of 32 w in
+    the ids, and both launches give the same per-position outputs and read
+    counts (bit-exact)."""
+    import ctypes
+
+    from engraft_ngram_amd import _lib
+    _say("scan rank bitmap")
+    spec = fake_table_spec(7)
+    tab, _ = G.f32_table(spec, 32, seed=52)
+    tokens = reference_corpus(30_000, seed=3, eos=spec.eos_token_id)
+    rows = H.ngram_rows_np(spec, tokens)
+    rng = np.random.default_rng(53)
+    n_bits = tab.n_rows
+    picked = set(rows[rng.integers(0, len(tokens), 40), rng.integers(0, rows.shape[1], 40)].tolist())
+    picked |= set(rng.integers(0, n_bits, 3000).tolist()) | {0, n_bits - 1, n_bits + 5}
+    ov = np.array(sorted(picked), dtype=np.int32)
+    ids = torch.from_numpy(ov).to(cuda)
+    dn = torch.from_numpy(rng.random(ov.size).astype(np.float32)).to(cuda)
+    bitmap = torch.full((2 * ((n_bits + 31) // 32),), -1, dtype=torch.int32, device=cuda)  # stale bits get cleared
+    _lib.call("eg_build_id_bitmap", _lib.ptr(ids), ov.size, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(cuda))
+    nw = (n_bits + 31) // 32
+    want = np.zeros(nw * 32, dtype=bool)
+    want[ov[ov < n_bits]] = True
+    bm = bitmap.cpu().numpy()
+    got_bits = np.unpackbits(bm[:nw].view(np.uint8), bitorder="little").astype(bool)
+    assert np.array_equal(got_bits, want)
+    assert np.array_equal(bm[nw:].astype(np.int64), np.searchsorted(ov, np.arange(nw, dtype=np.int64) * 32))
+    tok = torch.from_numpy(np.asarray(tokens, dtype=np.int64)).to(cuda)
+    spec_c = tab.c_spec
+    outs = []
+    for start in (0, 2):
+        for bm in (None, _lib.ptr(bitmap)):
+            m = tok.numel() - start
+            n_hit = torch.empty(m, dtype=torch.int32, device=cuda)
+            dmax, dsum = torch.empty(m, device=cuda), torch.empty(m, device=cuda)
+            counts = torch.zeros(ov.size, dtype=torch.int64, device=cuda)
+            _lib.call("eg_scan_overlay", ctypes.byref(spec_c), _lib.ptr(tok), tok.numel(), start, _lib.ptr(ids),
+                      ov.size, bm, n_bits, _lib.ptr(dn), _lib.ptr(n_hit), _lib.ptr(dmax), _lib.ptr(dsum),
+                      _lib.ptr(counts), _lib.stream_ptr(cuda))
+            outs.append([x.cpu().numpy() for x in (n_hit, dmax, dsum, counts)])
+        for a, b in zip(outs[-2], outs[-1]):
+            assert np.array_equal(a, b)
+    assert int(outs[0][0].sum()) > 0 and int(outs[0][3][-1]) == 0
+
+
 @pytest.mark.parametrize("n_files", [4, 40])
 def test_sum_overlays_against_oracle(cuda, tmp_path, n_files):
     """engraft/replica/overlay_sum.py:38-112 on the device: the union, the
