@@ -99,6 +99,31 @@ def traffic_from_profile(kernel_key: str):
     return None
 
 
+def oracle_spec(hp: dict):
+    from oracle import hash as OH
+    return OH.HashSpec(eos_token_id=hp["eos_token_id"], ngram_size=hp["ngram_size"],
+                       heads_per_ngram=hp["heads_per_ngram"], layer_multipliers=tuple(hp["layer_multipliers"]),
+                       head_vocab_sizes=tuple(hp["head_vocab_sizes"]), head_offsets=tuple(hp["head_offsets"]),
+                       head_multipliers=tuple(tuple(r) for r in hp["head_multipliers"]))
+
+
+def log_cpu_leg(name: str, leg: dict) -> None:
+    cb = leg.get("cpu_baseline")
+    if cb:
+        log(f"{name} cpu baseline: {cb['value']:.3g} {cb['unit']} on {cb['cores']} thread(s)")
+
+
+def repeat_for(fn, budget_s: float) -> tuple[int, float]:
+    """Calls fn until budget_s has passed (at least once): (calls, seconds)."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            return n, el
+
+
 def cpu_baseline(hp: dict, tokens_np, residual_cpu, budget_s: float) -> dict:
     """The oracle's vectorized CPU restatement on the same inputs (rank 0, N=1)."""
     import torch
@@ -106,10 +131,7 @@ def cpu_baseline(hp: dict, tokens_np, residual_cpu, budget_s: float) -> dict:
     from oracle import cpu_baseline as CB
     from oracle import hash as OH
 
-    spec = OH.HashSpec(eos_token_id=hp["eos_token_id"], ngram_size=hp["ngram_size"],
-                       heads_per_ngram=hp["heads_per_ngram"], layer_multipliers=tuple(hp["layer_multipliers"]),
-                       head_vocab_sizes=tuple(hp["head_vocab_sizes"]), head_offsets=tuple(hp["head_offsets"]),
-                       head_multipliers=tuple(tuple(r) for r in hp["head_multipliers"]))
+    spec = oracle_spec(hp)
     t0 = time.perf_counter()
     host = CB.HostTable(N_ROWS, DIM)
     rows = OH.ngram_rows_np(spec, tokens_np, seq_len=SEQ)
@@ -142,7 +164,7 @@ def backward_bytes(positions: int, n_unique: int) -> int:
     return positions * 2 * WIDTH + positions * SLOTS * 4 + n_unique * (2 * Q8_ROW_BYTES + 4 * 512 + 2 * 512)
 
 
-def bench_backward(tab, tokens, steps: int, warmup: int) -> dict:
+def bench_backward(tab, tokens, steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
     """d_residual [16384, 2048] bf16 ~ N(0, 1e-3); scatter of
     the per-slot row gradients into the fp32 overlay of the touched rows (slots
     grouped per row, CSR, then each row's slots summed in slot order), Adam (lr
@@ -172,11 +194,44 @@ def bench_backward(tab, tokens, steps: int, warmup: int) -> dict:
     ms = a.elapsed_time(b) / steps
     nb = backward_bytes(rows.shape[0], state.n)
     gbs = nb / (ms * 1e-3) / 1e9
-    return {"us_per_step": ms * 1e3, "touched_rows": state.n, "slot_gradients": rows.numel(),
-            "algorithmic_bytes_per_step": nb, "gb_per_s": gbs, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
-            "rows_per_s": rows.numel() / (ms * 1e-3),
-            "workload": "BASELINE config 2: scatter (CSR grouping + slot-ordered segmented reduce) + sparse Adam + "
-                        "Q8_0 requant, fp32 master/m/v kept"}
+    out = {"us_per_step": ms * 1e3, "touched_rows": state.n, "slot_gradients": rows.numel(),
+           "algorithmic_bytes_per_step": nb, "gb_per_s": gbs, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
+           "rows_per_s": rows.numel() / (ms * 1e-3),
+           "workload": "BASELINE config 2: scatter (CSR grouping + slot-ordered segmented reduce) + sparse Adam + "
+                       "Q8_0 requant, fp32 master/m/v kept"}
+    if cpu_s > 0:
+        out["cpu_baseline"] = cpu_descent(tab, rows, d_res[0], cpu_s)
+    return out
+
+
+def cpu_descent(tab, rows, d_res, budget_s: float) -> dict:
+    """The oracle's descent step on the host: slot-ordered scatter
+    (oracle.backward.scatter_grad), the sparse Adam step and the Q8_0
+    requantisation of the touched rows, over the first 2,048 positions of the
+    config-2 batch (32,768 slot gradients)."""
+    import numpy as np
+    import torch
+
+    from oracle import backward as OB
+    from oracle import formats as OF
+
+    p = 2048
+    r = rows[:p].cpu().numpy()
+    ids = np.unique(r)
+    d_emb = d_res[:p].float().cpu().numpy()
+    ids_d = torch.from_numpy(ids.astype(np.int32)).to(tab.device).reshape(-1, 1)
+    param = tab.gather(ids_d).float().cpu().numpy().reshape(ids.size, -1)
+    m, v = np.zeros_like(param), np.zeros_like(param)
+
+    def step():
+        grad, hits = OB.scatter_grad(d_emb, r, ids)
+        new_p, _, _ = OB.adam_step(param, grad, m, v, 1, 1e-3, touched=hits > 0)
+        OF.quant_q8_0(new_p)
+
+    n, el = repeat_for(step, budget_s)
+    return {"value": n * r.size / el, "unit": "slot gradients/s", "cores": 1, "kind": "port",
+            "sample": f"first {p} positions of the config-2 batch ({r.size} slots, {ids.size} rows) x {n} steps "
+                      f"in {el:.1f} s: oracle scatter (slot order) + Adam + Q8_0 requant, numpy"}
 
 
 def bench_decode(tab, steps: int) -> dict:
@@ -327,7 +382,7 @@ def bench_real_format(steps: int, warmup: int) -> dict:
             "frac_of_hbm_peak": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": nbytes}
 
 
-def bench_damage_scan(tab, steps: int) -> dict:
+def bench_damage_scan(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.0) -> dict:
     """The damage scan (the f3 path, engraft/damage.py:159-224): one corpus block
     of 8,000,000 Zipf tokens (the reference's block size, damage.py:60) against
     500,000 sorted overlay rows with their dnorm, on the config-1 table's hash:
@@ -378,13 +433,22 @@ def bench_damage_scan(tab, steps: int) -> dict:
     res = damage.scan_hits(tokens, tab, ids, dnorm)
     wall = time.perf_counter() - t0
     lookups = n * tab.n_heads
-    return {"workload": "damage scan: 8,000,000 Zipf tokens x 16 rows against 500,000 sorted overlay rows",
-            "us_per_block_kernel": us, "us_per_block_kernel_search_only": us_search, "tokens_per_s_kernel": n / (us * 1e-6),
-            "lookups_per_s_kernel": lookups / (us * 1e-6), "s_per_block_end_to_end": wall,
-            "hit_positions": int(res["pos"].size)}
+    out = {"workload": "damage scan: 8,000,000 Zipf tokens x 16 rows against 500,000 sorted overlay rows",
+           "us_per_block_kernel": us, "us_per_block_kernel_search_only": us_search,
+           "tokens_per_s_kernel": n / (us * 1e-6), "lookups_per_s_kernel": lookups / (us * 1e-6),
+           "s_per_block_end_to_end": wall, "hit_positions": int(res["pos"].size)}
+    if cpu_s > 0 and hp is not None:
+        from oracle import damage as OD
+        spec = oracle_spec(hp)
+        sample = tokens[:250_000]
+        k, el = repeat_for(lambda: OD.scan_hits(spec, sample, ids, dnorm, block=len(sample)), cpu_s)
+        out["cpu_baseline"] = {"value": k * sample.size / el, "unit": "tokens/s", "cores": 1, "kind": "port",
+                               "sample": f"first 250,000 tokens of the block x {k} in {el:.1f} s: oracle "
+                                         "scan_hits (numpy-uint64 hash, searchsorted, np.add.at)"}
+    return out
 
 
-def bench_ple(steps: int, warmup: int) -> dict:
+def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
     """The PLE block consuming the rows (engraft/replica/layers.py:565-626) at
     the real model's dimensions: 2048 positions, 4 hyper-connection streams,
     n_embd 2560, 4 conv taps with dilation 3; seeded random weights; fp32."""
@@ -437,11 +501,23 @@ def bench_ple(steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     fb_ms = a.elapsed_time(b) / bsteps
     flops = 2.0 * t_len * n * (hc * n + n)
-    return {"workload": "ple_forward: T 2048, hc 4, n_embd 2560, 4 taps, dilation 3, fp32 (key/value GEMMs on "
-                        "hipBLASLt through torch.matmul, gate/norm and conv in HIP)",
-            "us_per_step": ms * 1e3, "gemm_us": gemm_ms * 1e3, "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12,
-            "non_gemm_us": (ms - gemm_ms) * 1e3, "fp32_mfma_peak_tflops": 157.3,
-            "us_forward_backward_to_emb": fb_ms * 1e3}
+    out = {"workload": "ple_forward: T 2048, hc 4, n_embd 2560, 4 taps, dilation 3, fp32 (key/value GEMMs on "
+                       "hipBLASLt through torch.matmul, gate/norm and conv in HIP)",
+           "us_per_step": ms * 1e3, "positions_per_s": t_len / (ms * 1e-3), "gemm_us": gemm_ms * 1e3,
+           "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12, "non_gemm_us": (ms - gemm_ms) * 1e3,
+           "fp32_mfma_peak_tflops": 157.3, "us_forward_backward_to_emb": fb_ms * 1e3}
+    if cpu_s > 0:
+        from oracle import ple as OP
+        tc = 256
+        wc = {k: getattr(w, k).cpu() for k in ("w_key", "w_value", "norm_key", "norm_query", "norm_conv", "conv1d")}
+        ec, hcpu = emb[:tc].cpu(), hidden[:tc].cpu()
+        with torch.no_grad():
+            k, el = repeat_for(lambda: OP.ple_forward(ec, hcpu, wc, hist.cpu(), hc, n, 1e-6, 3), cpu_s)
+        out["cpu_baseline"] = {"value": k * tc / el, "unit": "positions/s", "cores": torch.get_num_threads(),
+                               "kind": "port",
+                               "sample": f"first {tc} positions x {k} in {el:.1f} s: oracle ple_forward (torch "
+                                         f"fp32 on the CPU, {torch.get_num_threads()} threads)"}
+    return out
 
 
 def main() -> None:
@@ -574,9 +650,12 @@ def main() -> None:
         },
     }
 
+    # the other legs' CPU baselines (the oracle on a bounded sample, a few seconds each)
+    cpu_leg_s = 0.0 if args.no_cpu else min(4.0, args.cpu_seconds)
     if not args.no_backward:
-        bw = bench_backward(tab, tokens, max(1, args.steps // 4), max(1, args.warmup))
+        bw = bench_backward(tab, tokens, max(1, args.steps // 4), max(1, args.warmup), cpu_leg_s)
         result["backward"] = bw
+        log_cpu_leg("backward", bw)
         log(f"backward: {bw['us_per_step']:.1f} us/step, {bw['touched_rows']} touched rows, "
             f"{bw['gb_per_s']:.0f} GB/s algorithmic ({100 * bw['frac_of_hbm_peak']:.1f}% of peak)")
 
@@ -588,8 +667,9 @@ def main() -> None:
         result["forward_config4"] = c4
         log(f"forward (config 4): {c4['us_per_launch']:.1f} us/launch, {c4['gb_per_s']:.0f} GB/s algorithmic "
             f"({100 * c4['frac_of_hbm_peak']:.1f}% of peak)")
-        ds = bench_damage_scan(tab, 20)
+        ds = bench_damage_scan(tab, 20, hp, cpu_leg_s)
         result["damage_scan"] = ds
+        log_cpu_leg("damage_scan", ds)
         log(f"damage scan: {ds['us_per_block_kernel']:.0f} us per 8M-token block on the device "
             f"({ds['lookups_per_s_kernel'] / 1e9:.1f} G lookups/s), {ds['s_per_block_end_to_end'] * 1e3:.0f} ms end "
             f"to end")
@@ -597,8 +677,9 @@ def main() -> None:
         result["forward_real_format"] = rf
         log(f"forward (real IQ4_NL format): {rf['us_per_launch']:.1f} us/launch, {rf['gb_per_s']:.0f} GB/s "
             f"algorithmic ({100 * rf['frac_of_hbm_peak']:.1f}% of peak)")
-        pl = bench_ple(max(1, args.steps // 10), max(1, args.warmup // 10))
+        pl = bench_ple(max(1, args.steps // 10), max(1, args.warmup // 10), cpu_leg_s)
         result["ple_forward"] = pl
+        log_cpu_leg("ple_forward", pl)
         log(f"ple_forward: {pl['us_per_step']:.0f} us/step; its two GEMMs alone {pl['gemm_us']:.0f} us "
             f"({pl['gemm_tflops']:.1f} TFLOP/s fp32), the rest {pl['non_gemm_us']:.0f} us; forward + backward "
             f"to emb {pl['us_forward_backward_to_emb']:.0f} us")
