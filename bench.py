@@ -113,6 +113,20 @@ def log_cpu_leg(name: str, leg: dict) -> None:
         log(f"{name} cpu baseline: {cb['value']:.3g} {cb['unit']} on {cb['cores']} thread(s)")
 
 
+def host_cpu() -> dict:
+    """The host the CPU legs ran on: CPU model, logical CPUs, CPUs this process may use."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0))}
+
+
 def repeat_for(fn, budget_s: float) -> tuple[int, float]:
     """Calls fn until budget_s has passed (at least once): (calls, seconds)."""
     n, t0 = 0, time.perf_counter()
@@ -125,7 +139,9 @@ def repeat_for(fn, budget_s: float) -> tuple[int, float]:
 
 
 def cpu_baseline(hp: dict, tokens_np, residual_cpu, budget_s: float) -> dict:
-    """The oracle's vectorized CPU restatement on the same inputs (rank 0, N=1)."""
+    """The oracle's vectorized CPU restatement on the same inputs (rank 0, N=1),
+    and the reference's per-position loop on the first 256 positions."""
+    import numpy as np
     import torch
 
     from oracle import cpu_baseline as CB
@@ -148,7 +164,19 @@ def cpu_baseline(hp: dict, tokens_np, residual_cpu, budget_s: float) -> dict:
         if el >= budget_s:
             break
     rows_per_s = n * tokens_np.size * SLOTS / el
-    return {"result": out, "value": rows_per_s, "unit": "rows/s", "cores": threads, "kind": "port",
+    # the reference's loop as written: position by position, each re-hashing its prefix
+    n_lit = 256
+    res_bits = residual_cpu[:n_lit].view(torch.int16).numpy().view(np.uint16)
+    t1 = time.perf_counter()
+    lit = CB.forward_q8_literal(spec, tokens_np, n_lit, host, res_bits)
+    el_lit = time.perf_counter() - t1
+    literal = {"value": n_lit * SLOTS / el_lit, "unit": "rows/s", "cores": 1, "kind": "port",
+               "sample": f"the first {n_lit} positions of sequence 0 in {el_lit:.2f} s: per position the scalar "
+                         "hash of its whole prefix (RowSet.from_position's O(T^2) re-hash), one row read + Q8_0 "
+                         "dequant per head, fp32 add -> bf16; pure Python/numpy",
+               "matches_vectorized": bool(np.array_equal(lit, out[:n_lit].view(torch.int16).numpy().view(np.uint16)))}
+    return {"result": out, "literal": literal, "host": host_cpu(), "value": rows_per_s, "unit": "rows/s",
+            "cores": threads, "kind": "port",
             "sample": (f"full config-1 step ({tokens_np.size} positions, {tokens_np.size * SLOTS} row reads) "
                        f"repeated {n}x in {el:.1f} s: numpy-uint64 hash + torch.index_select gather from a "
                        f"host table of the full 320M-row shape (touched rows materialised) + Q8_0 dequant + "
@@ -690,7 +718,11 @@ def main() -> None:
         cb = cpu_baseline(hp, tokens_np, res[0].cpu(), args.cpu_seconds)
         same = bool(torch.equal(cb.pop("result").view(torch.int16), outs[0].cpu().view(torch.int16)))
         cb["matches_gpu_output"] = same
+        result["cpu_baseline_literal"] = cb.pop("literal")
         result["cpu_baseline"] = cb
+        lit = result["cpu_baseline_literal"]
+        log(f"cpu baseline, the reference's per-position loop: {lit['value']:.3g} rows/s on 1 thread; "
+            f"identical output: {lit['matches_vectorized']}")
         log(f"cpu baseline: {cb['value']:.3g} rows/s on {cb['cores']} threads; identical output: {same}")
     else:
         result["cpu_baseline"] = None

@@ -11,7 +11,14 @@ is allocated at full size and only the rows the workload touches are written
 (the rest stay untouched zero pages), so the gather walks the same 43.5 GB
 address range as the device kernel.
 
-Pinned by tests/test_oracle_forward_backward.py (bit-identical to
+``forward_q8_literal`` is the reference's path as written: one position at a
+time, each re-hashing its whole prefix with the scalar hash
+(``RowSet.from_position``, ``engraft/lens.py:126-136``, whose
+``ngram_addresses(tokens[:t+1])`` makes the loop O(T^2)), one row read and
+dequantisation per head, the concatenated rows added into that position's
+residual row.
+
+Pinned by tests/test_oracle_forward_backward.py (both forms bit-identical to
 ``oracle.forward.forward`` on the same inputs).
 """
 from __future__ import annotations
@@ -19,6 +26,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
+from oracle import formats as F
 from oracle import hash as H
 from oracle import synth
 
@@ -57,3 +65,20 @@ def forward_q8(spec: H.HashSpec, tokens: np.ndarray, seq_len: int | None, table:
     emb = (q.view(p * hh, nb, 32).to(torch.float32) * d.to(torch.float32).unsqueeze(-1)).view(p, hh * table.dim)
     out = (residual.to(torch.float32) + emb).to(torch.bfloat16)
     return rows, out
+
+
+def forward_q8_literal(spec: H.HashSpec, tokens: np.ndarray, n_positions: int, table: HostTable,
+                       residual: np.ndarray) -> np.ndarray:
+    """The first ``n_positions`` positions of one sequence, position by position:
+    the scalar hash of ``tokens[:t+1]`` (O(t) per position), the 16 global ids,
+    a row read + Q8_0 dequantisation per head, fp32 add, RNE to bf16.  Returns
+    the bf16 bit patterns ``uint16 [n_positions, n_heads * dim]``."""
+    toks = [int(x) for x in np.asarray(tokens[:n_positions])]
+    out = np.empty((n_positions, spec.n_heads * table.dim), dtype=np.uint16)
+    for t in range(n_positions):
+        local = H.ngram_addresses_scalar(spec, toks[:t + 1])[t]
+        rows = [H.local_to_global(spec, h, r) for h, r in enumerate(local)]
+        emb = np.concatenate([F.dequant_q8_0(table.payload[r:r + 1], table.scales[r:r + 1])[0] for r in rows])
+        res = F.bf16_bits_to_f32(np.asarray(residual[t], dtype=np.uint16))
+        out[t] = F.f32_to_bf16_bits((res + emb).astype(np.float32))
+    return out

@@ -170,7 +170,8 @@ def test_adam_sparse_leaves_untouched_rows():
 
 
 def test_cpu_baseline_equals_oracle_forward():
-    """bench.py's cpu_baseline leg computes the same bits as oracle.forward."""
+    """bench.py's cpu_baseline leg computes the same bits as oracle.forward, in
+    both its vectorized and its literal per-position form."""
     from oracle import cpu_baseline as CB
     from tests.params import synthetic_spec
 
@@ -186,6 +187,9 @@ def test_cpu_baseline_equals_oracle_forward():
                                       seq_len=256)
     assert np.array_equal(rows, exp_rows)
     assert np.array_equal(out.view(torch.int16).numpy().view(np.uint16), exp_out)
+    # the literal per-position loop (scalar re-hash of every prefix) gives the same bits
+    lit = CB.forward_q8_literal(spec, tokens, 40, host, res[:40].view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(lit, exp_out[:40])
 
 
 def test_product_synthetic_params_equal_oracle_params():
