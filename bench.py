@@ -496,44 +496,45 @@ def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
                        norm_conv=1 + rnd(hc * n, sc=0.1), conv1d=rnd(hc * n, 4, sc=0.5))
     emb, hidden = rnd(t_len, n, sc=0.1), rnd(t_len, hc, n, sc=0.1)
     hist = torch.zeros(0, hc, n, device=dev)
-    with torch.no_grad():
-        for _ in range(warmup):
-            ple.ple_forward(emb, hidden, w, hist, HP)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, k: int) -> float:
         torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        for _ in range(steps):
-            ple.ple_forward(emb, hidden, w, hist, HP)
+        for _ in range(k):
+            fn()
         b.record()
         torch.cuda.synchronize()
-        ms = a.elapsed_time(b) / steps
-        # the two projections alone, for the GEMMs' own rate
-        a.record()
-        for _ in range(steps):
-            emb @ w.w_key.T
-            emb @ w.w_value.T
-        b.record()
-        torch.cuda.synchronize()
-        gemm_ms = a.elapsed_time(b) / steps
-    # forward + backward to emb (the descent's use: the weights stay fixed)
-    emb_v = emb.clone().requires_grad_(True)
-    d_out = rnd(t_len, hc, n, sc=1e-3)
-    bsteps = max(1, steps // 5)
-    for i in range(bsteps + 2):
-        if i == 2:
-            torch.cuda.synchronize()
-            a.record()
-        out, _ = ple.ple_forward(emb_v, hidden, w, hist, HP)
-        (d_gemm,) = torch.autograd.grad(out, emb_v, d_out)
-    b.record()
-    torch.cuda.synchronize()
-    fb_ms = a.elapsed_time(b) / bsteps
+        return a.elapsed_time(b) / k
+
     flops = 2.0 * t_len * n * (hc * n + n)
-    out = {"workload": "ple_forward: T 2048, hc 4, n_embd 2560, 4 taps, dilation 3, fp32 (key/value GEMMs on "
-                       "hipBLASLt through torch.matmul, gate/norm and conv in HIP)",
-           "us_per_step": ms * 1e3, "positions_per_s": t_len / (ms * 1e-3), "gemm_us": gemm_ms * 1e3,
-           "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12, "non_gemm_us": (ms - gemm_ms) * 1e3,
-           "fp32_mfma_peak_tflops": 157.3, "us_forward_backward_to_emb": fb_ms * 1e3}
+    d_out = rnd(t_len, hc, n, sc=1e-3)
+    emb_v = emb.clone().requires_grad_(True)
+    res = {}
+    for mode in ("fp32", "bf16x3"):
+        with torch.no_grad():
+            for _ in range(warmup):
+                ple.ple_forward(emb, hidden, w, hist, HP, gemm=mode)
+            ms = timed(lambda: ple.ple_forward(emb, hidden, w, hist, HP, gemm=mode), steps)
+            # the two projections alone, for the GEMMs' own rate
+            if mode == "fp32":
+                gemm_ms = timed(lambda: (emb @ w.w_key.T, emb @ w.w_value.T), steps)
+            else:
+                pk, pv = ple.SplitPlanes(w.w_key), ple.SplitPlanes(w.w_value)
+                gemm_ms = timed(lambda: (ple.gemm_x3(emb, pk), ple.gemm_x3(emb, pv)), steps)
+        # forward + backward to emb (the descent's use: the weights stay fixed)
+        fb = lambda: torch.autograd.grad(ple.ple_forward(emb_v, hidden, w, hist, HP, gemm=mode)[0], emb_v, d_out)
+        fb()
+        fb_ms = timed(fb, max(1, steps // 5))
+        res[mode] = {"us_per_step": ms * 1e3, "positions_per_s": t_len / (ms * 1e-3), "gemm_us": gemm_ms * 1e3,
+                     "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12, "non_gemm_us": (ms - gemm_ms) * 1e3,
+                     "us_forward_backward_to_emb": fb_ms * 1e3}
+    out = {"workload": "ple_forward: T 2048, hc 4, n_embd 2560, 4 taps, dilation 3, fp32 activations; key/value "
+                       "GEMMs either fp32 (hipBLASLt through torch.matmul; the reference's arithmetic) or bf16x3 "
+                       "(eg_gemm_bf16x3 on the bf16 matrix cores, 16 mantissa bits per operand); gate/norm and "
+                       "conv in HIP",
+           **res["fp32"], "bf16x3": res["bf16x3"], "fp32_mfma_peak_tflops": 157.3,
+           "bf16_mfma_peak_tflops": 2500.0}
     if cpu_s > 0:
         from oracle import ple as OP
         tc = 256
@@ -711,6 +712,10 @@ def main() -> None:
         log(f"ple_forward: {pl['us_per_step']:.0f} us/step; its two GEMMs alone {pl['gemm_us']:.0f} us "
             f"({pl['gemm_tflops']:.1f} TFLOP/s fp32), the rest {pl['non_gemm_us']:.0f} us; forward + backward "
             f"to emb {pl['us_forward_backward_to_emb']:.0f} us")
+        x3 = pl["bf16x3"]
+        log(f"ple_forward with bf16x3 GEMMs: {x3['us_per_step']:.0f} us/step; GEMMs {x3['gemm_us']:.0f} us "
+            f"({x3['gemm_tflops']:.1f} TFLOP/s fp32-equivalent); forward + backward to emb "
+            f"{x3['us_forward_backward_to_emb']:.0f} us")
 
     if not args.no_cpu:
         calls[0]()  # outs[0] = the step on token batch 0 and residual set 0, which the CPU repeats

@@ -89,6 +89,21 @@ class EgDescentState(ctypes.Structure):
     ]
 
 
+class EgGemmOperands(ctypes.Structure):
+    _fields_ = [
+        ("a_hi", c_void_p),
+        ("a_lo", c_void_p),
+        ("lda", c_int64),
+        ("b_hi", c_void_p),
+        ("b_lo", c_void_p),
+        ("ldb", c_int64),
+        ("b2_hi", c_void_p),
+        ("b2_lo", c_void_p),
+        ("ldb2", c_int64),
+        ("k", c_int64),
+    ]
+
+
 # name -> (restype, argtypes); every symbol the header declares.
 SIGNATURES = {
     "eg_last_error": (c_char_p, []),
@@ -107,6 +122,10 @@ SIGNATURES = {
     "eg_ple_conv": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32,
                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_rms": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, ctypes.c_float, c_void_p, c_void_p]),
+    "eg_split_bf16": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+    "eg_gemm_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int32]),
+    "eg_gemm_bf16x3": (c_int32, [POINTER(EgGemmOperands), c_int32, c_int64, c_int64, c_int64, c_void_p, c_int64,
+                                 c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_void_p]),
     "eg_forward_decode": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,
                                     c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_forward_timed": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,

@@ -4,7 +4,9 @@ for ``PleWeights`` / ``ple_forward`` (``engraft/replica/layers.py:555-626``).
 Forward:
 
 * ``key = emb @ w_key^T`` and ``value = emb @ w_value^T``: fp32 library GEMMs
-  (hipBLASLt / rocBLAS through ``torch.matmul``, on the matrix cores);
+  (hipBLASLt through ``torch.matmul``), or with ``gemm="bf16x3"`` the
+  ``gemm_x3`` kernel on the bf16 matrix cores (operands split into bf16 hi +
+  lo, three products accumulated in fp32: 16 mantissa bits per operand);
 * ``eg_ple_gate``: per position and stream, the RMS norms of key and hidden,
   the score ``s``, the gate, ``gated = value * gate`` and its RMS norm;
 * ``eg_ple_conv``: the dilated causal depthwise convolution over
@@ -13,7 +15,8 @@ Forward:
 The result -- the output and the new history -- is differentiable in emb,
 hidden, the history and the weights.  Without weight gradients (the descent's
 case) the backward runs ``eg_ple_conv_backward`` and ``eg_ple_gate_backward``
-on the forward's saved intermediates, then the projections' two GEMMs; with
+on the forward's saved intermediates, then the projections' backward (with
+``bf16x3``, one ``gemm_x3`` call over two K segments); with
 weight gradients, a torch recomputation of the block on the device,
 differentiated by autograd.  Either way the forward values are the HIP
 kernels'.  ``detach_value`` / ``detach_gate`` change only the backward, as in
@@ -79,9 +82,9 @@ def _block_torch(emb, hidden, w_key, w_value, nk, nq, nc, conv, hist, eps, dil, 
 
 class _TransposedCache:
     """Row-major copies of the projection weights' transposes, kept between
-    steps: hipBLASLt runs ``d_emb^T = w^T @ d^T`` about 10 % faster than
-    ``d @ w`` at these shapes.  An entry is used only for the same tensor
-    object (weak reference) at the same version counter, so a weight that is
+    steps: the backward's ``d_emb = d @ w`` is ``gemm_x3(d, w^T)``, whose B
+    operand is K-contiguous.  An entry is used only for the same tensor object
+    (weak reference) at the same version counter, so a weight that is
     modified in place or freed and replaced is transposed again."""
 
     def __init__(self, size: int = 4):
@@ -102,6 +105,118 @@ class _TransposedCache:
 _WT = _TransposedCache()
 
 
+class SplitPlanes:
+    """The bf16 hi / lo planes of an fp32 matrix ``[rows, cols]`` (``eg_split_bf16``),
+    each ``[rows, kp]`` with ``kp`` = cols rounded up to 32, zero-padded."""
+
+    def __init__(self, x: torch.Tensor):
+        if x.dim() != 2:
+            raise ValueError("SplitPlanes: a 2-D matrix expected")
+        x = x if x.dtype == torch.float32 else x.float()
+        if x.stride(-1) != 1:
+            x = x.contiguous()
+        rows, cols = x.shape
+        self.rows, self.cols, self.kp = rows, cols, (cols + 31) // 32 * 32
+        self.hi = torch.empty((rows, self.kp), dtype=torch.bfloat16, device=x.device)
+        self.lo = torch.empty_like(self.hi)
+        _lib.call("eg_split_bf16", _lib.ptr(x), rows, cols, max(x.stride(0), cols), _lib.ptr(self.hi),
+                  _lib.ptr(self.lo), _lib.stream_ptr(x.device))
+
+
+class _PlaneCache:
+    """Split planes of weights, kept between steps: an entry is used only for
+    the same tensor object (weak reference) at the same version counter."""
+
+    def __init__(self, size: int = 8):
+        self._entries: list = []
+        self._size = size
+
+    def get(self, w: torch.Tensor) -> SplitPlanes:
+        import weakref
+        for ref, version, planes in self._entries:
+            if ref() is w and version == w._version:
+                return planes
+        planes = SplitPlanes(w)
+        self._entries = [e for e in self._entries if e[0]() is not None][-(self._size - 1):]
+        self._entries.append((weakref.ref(w), w._version, planes))
+        return planes
+
+
+_PLANES = _PlaneCache()
+
+
+def _planes(x, cached: bool) -> SplitPlanes:
+    if isinstance(x, SplitPlanes):
+        return x
+    return _PLANES.get(x) if cached else SplitPlanes(x)
+
+
+def _k_slices(tiles: int, k_tiles: int) -> int:
+    """K slices for few output tiles: enough workgroups for two per CU on 256
+    CUs, each slice at least 16 K steps."""
+    s = 1
+    while tiles * s < 512 and k_tiles // (2 * s) >= 16 and s < 8:
+        s *= 2
+    return s
+
+
+def gemm_x3(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate: bool = False,
+            cache_b: bool = False, b_n2=None, b2_n2=None, out2: torch.Tensor | None = None,
+            k_slices: int | None = None):
+    """``a @ b.T (+ a2 @ b2.T)`` in fp32 on the bf16 matrix cores
+    (``eg_gemm_bf16x3``: every operand split into bf16 hi + lo planes, three
+    products accumulated in fp32; 16 mantissa bits per operand).  ``a [m, k]``, ``b [n, k]``, ``a2 [m, k2]``,
+    ``b2 [n, k2]``: fp32 tensors on one device, or their ``SplitPlanes``;
+    ``cache_b`` keeps the planes of the B operands between calls (weights).
+    ``b_n2`` (and ``b2_n2`` with a second segment) ``[n2, k]`` add a second
+    column group, ``a @ b_n2.T (+ a2 @ b2_n2.T)`` into ``out2``, in the same
+    launch.  ``k_slices`` (default: chosen from the tile count) cuts K into
+    slices summed in a fixed order.  Returns ``out`` (``[m, n]`` fp32,
+    allocated when not given; added to when ``accumulate``), or ``(out,
+    out2)`` with a second column group."""
+    segs = [(_planes(a, False), _planes(b, cache_b), None if b_n2 is None else _planes(b_n2, cache_b))]
+    if a2 is not None:
+        segs.append((_planes(a2, False), _planes(b2, cache_b), None if b2_n2 is None else _planes(b2_n2, cache_b)))
+    m, n = segs[0][0].rows, segs[0][1].rows
+    n2 = 0 if segs[0][2] is None else segs[0][2].rows
+    ops = (_lib.EgGemmOperands * 2)()
+    k_tiles = 0
+    for i, (pa, pb, pb2) in enumerate(segs):
+        if pa.rows != m or pb.rows != n or pb.cols != pa.cols:
+            raise ValueError(f"gemm_x3: segment {i}: a [m, k] and b [n, k] expected, got [{pa.rows}, {pa.cols}] "
+                             f"and [{pb.rows}, {pb.cols}]")
+        if (pb2 is None) != (n2 == 0) or (pb2 is not None and (pb2.rows != n2 or pb2.cols != pa.cols)):
+            raise ValueError(f"gemm_x3: segment {i}: the second column group needs b [n2, k] in every segment")
+        o = ops[i]
+        o.a_hi, o.a_lo, o.lda = _lib.ptr(pa.hi), _lib.ptr(pa.lo), pa.kp
+        o.b_hi, o.b_lo, o.ldb = _lib.ptr(pb.hi), _lib.ptr(pb.lo), pb.kp
+        if pb2 is not None:
+            o.b2_hi, o.b2_lo, o.ldb2 = _lib.ptr(pb2.hi), _lib.ptr(pb2.lo), pb2.kp
+        o.k = pa.kp
+        k_tiles += pa.kp // 32
+    dev = segs[0][0].hi.device
+
+    def _out(t, rows, cols, name):
+        if t is None:
+            if accumulate:
+                raise ValueError(f"gemm_x3: accumulate needs {name}")
+            return torch.empty((rows, cols), dtype=torch.float32, device=dev)
+        if t.dtype != torch.float32 or t.shape != (rows, cols) or t.stride(1) != 1:
+            raise ValueError(f"gemm_x3: {name} must be fp32 [{rows}, {cols}] with unit column stride")
+        return t
+
+    out = _out(out, m, n, "out")
+    out2 = _out(out2, m, n2, "out2") if n2 else None
+    tiles = -(-m // 128) * (-(-n // 128) + -(-n2 // 128))
+    slices = _k_slices(tiles, k_tiles) if k_slices is None else int(k_slices)
+    ws_bytes = int(_lib.load().eg_gemm_workspace_size(m, n, n2, slices))
+    ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=dev) if ws_bytes else None
+    _lib.call("eg_gemm_bf16x3", ops, len(segs), m, n, n2, _lib.ptr(out), max(out.stride(0), n),
+              _lib.ptr(out2), max(out2.stride(0), n2) if n2 else 0, int(accumulate), slices, _lib.ptr(ws),
+              ws_bytes, _lib.stream_ptr(dev))
+    return (out, out2) if n2 else out
+
+
 def _native_backward_ok(hc: int, n: int, taps: int, dil: int) -> bool:
     """The HIP backward's built limits (eg_ple_gate_backward, eg_ple_conv_backward)."""
     return hc <= 4 and n <= 4096 and (taps - 1) * dil <= 32
@@ -115,15 +230,21 @@ class _PleFn(torch.autograd.Function):
     by autograd."""
 
     @staticmethod
-    def forward(ctx, emb, hidden, w_key, w_value, nk, nq, nc, conv, hist, eps, dil, detach_value, detach_gate):
+    def forward(ctx, emb, hidden, w_key, w_value, nk, nq, nc, conv, hist, eps, dil, detach_value, detach_gate,
+                gemm):
         t_len, hc, n = hidden.shape
         dev = hidden.device
         f32 = dict(dtype=torch.float32, device=dev)
         emb32 = emb.to(**f32).contiguous()
         wk32 = w_key.to(**f32)
         wv32 = w_value.to(**f32)
-        key = (emb32 @ wk32.T).contiguous()
-        value = (emb32 @ wv32.T).contiguous()
+        if gemm == "bf16x3":
+            pe = SplitPlanes(emb32)
+            key = gemm_x3(pe, wk32, cache_b=True)
+            value = gemm_x3(pe, wv32, cache_b=True)
+        else:
+            key = (emb32 @ wk32.T).contiguous()
+            value = (emb32 @ wv32.T).contiguous()
         hidden32 = hidden.to(**f32).contiguous()
         h0 = hist.shape[0]
         full = torch.empty((h0 + t_len, hc * n), **f32)
@@ -154,6 +275,7 @@ class _PleFn(torch.autograd.Function):
         else:
             ctx.save_for_backward(emb, hidden, w_key, w_value, nk, nq, nc, conv, hist)
         ctx.cfg = (eps, dil, detach_value, detach_gate)
+        ctx.gemm = gemm
         ctx.mark_non_differentiable(s, gate, value)
         return out.to(hidden.dtype), new_hist, s, gate, value
 
@@ -176,7 +298,7 @@ class _PleFn(torch.autograd.Function):
         for x, need in zip(leaves, ctx.needs_input_grad[:9]):
             g = next(grads) if need else None
             res.append(torch.zeros_like(x) if (need and g is None) else g)
-        return (*res, None, None, None, None)
+        return (*res, None, None, None, None, None)
 
     @staticmethod
     def _backward_native(ctx, d_out, d_hist):
@@ -206,29 +328,36 @@ class _PleFn(torch.autograd.Function):
                       _lib.ptr(d_key), _lib.ptr(d_value), _lib.ptr(d_hidden), st)
         d_emb = None
         if need_emb:
-            # the projections' backward, transposed: d_emb^T = w_key^T d_key^T + w_value^T d_value^T
-            d_emb_t = None
-            if d_key is not None:
-                d_emb_t = _WT.get(wk32) @ d_key.T
-            if d_value is not None:
-                if d_emb_t is None:
-                    d_emb_t = _WT.get(wv32) @ d_value.T
-                else:
-                    d_emb_t.addmm_(_WT.get(wv32), d_value.T)
-            d_emb = d_emb_t.T.contiguous() if d_emb_t is not None else torch.zeros((t_len, n), **f32)
+            # the projections' backward, d_emb = d_key w_key + d_value w_value, as
+            # products with the weights' transposes (kept between steps)
+            parts = [(d, _WT.get(w)) for d, w in ((d_key, wk32), (d_value, wv32)) if d is not None]
+            if not parts:
+                d_emb = torch.zeros((t_len, n), **f32)
+            elif ctx.gemm == "bf16x3":
+                flat = [x for part in parts for x in part]
+                d_emb = gemm_x3(*flat, cache_b=True)
+            else:
+                d_emb = parts[0][0] @ parts[0][1].T
+                if len(parts) > 1:
+                    d_emb.addmm_(parts[1][0], parts[1][1].T)
             d_emb = d_emb.to(emb_dt)
         d_hist_in = d_full[:h0].reshape(h0, hc, n).to(hist_dt) if need_hist else None
         return (d_emb, d_hidden.to(hidden_dt) if d_hidden is not None else None, None, None, None, None, None, None,
-                d_hist_in, None, None, None, None)
+                d_hist_in, None, None, None, None, None)
 
 
 def ple_forward(emb: torch.Tensor, hidden: torch.Tensor, w: PleWeights, hist: torch.Tensor, hparams,
-                diag: dict | None = None, detach_value: bool = False,
-                detach_gate: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+                diag: dict | None = None, detach_value: bool = False, detach_gate: bool = False,
+                gemm: str = "fp32") -> tuple[torch.Tensor, torch.Tensor]:
     """``(hidden + gated + conv_out, new history)`` (``engraft/replica/layers.py:
     565-626``).  ``emb [T, n_embd]``, ``hidden [T, hc, n_embd]``, ``hist``
     ``[rows, hc, n_embd]`` (at most ``(K-1)*ple_ngram_size`` rows, empty at a
-    sequence start); all on the device."""
+    sequence start); all on the device.  ``gemm`` picks the projections' GEMM:
+    ``"fp32"`` (the reference's arithmetic, hipBLASLt fp32) or ``"bf16x3"``
+    (``gemm_x3`` on the bf16 matrix cores: 16 mantissa bits per operand, about
+    1e-5 relative per projection, 2x faster)."""
+    if gemm not in ("fp32", "bf16x3"):
+        raise ValueError(f"gemm must be 'fp32' or 'bf16x3', got {gemm!r}")
     hc = hparams.hc_mult
     n = hparams.n_embd
     eps = float(hparams.f_norm_rms_eps)
@@ -238,7 +367,8 @@ def ple_forward(emb: torch.Tensor, hidden: torch.Tensor, w: PleWeights, hist: to
                          f"{tuple(hidden.shape)}")
     hist = hist.reshape(-1, hc, n) if hist.numel() else hidden.new_zeros((0, hc, n))
     out, new_hist, s, gate, value = _PleFn.apply(emb, hidden, w.w_key, w.w_value, w.norm_key, w.norm_query,
-                                                 w.norm_conv, w.conv1d, hist, eps, dil, detach_value, detach_gate)
+                                                 w.norm_conv, w.conv1d, hist, eps, dil, detach_value, detach_gate,
+                                                 gemm)
     if diag is not None:
         gated_norm = value.norm(dim=-1, keepdim=True) * gate.abs()
         diag["s"] = s.clone()

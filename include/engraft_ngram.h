@@ -33,6 +33,9 @@
  *   eg_ple_gate, eg_ple_conv  ple_forward after its two projections
  *   (+ _backward)    and the autograd of it          engraft/replica/layers.py:565-626
  *   eg_ple_rms, eg_ple_conv's other modes  PleReplica engraft/lens.py:221-385
+ *   eg_split_bf16, eg_gemm_bf16x3 (+ _workspace_size)
+ *                    ple_forward's projections and their backward
+ *                                                    engraft/replica/layers.py:594-606
  */
 #ifndef ENGRAFT_NGRAM_H
 #define ENGRAFT_NGRAM_H
@@ -331,6 +334,47 @@ int eg_ple_gate_backward(const float* key, const float* value, const float* hidd
  * eg_ple_gate, so applied to value*gate it gives eg_ple_gate's normed). */
 int eg_ple_rms(const float* x, int64_t n_rows, int32_t hc, int32_t n_embd, const float* weight, float eps,
                float* out, void* stream);
+
+/* The bf16 hi / lo planes of an fp32 matrix for eg_gemm_bf16x3: x f32
+ * [rows, cols] with row stride ld -> hi, lo bf16 [rows, kp], kp = cols
+ * rounded up to a multiple of 32, hi = rne(x), lo = rne(x - hi), the padding
+ * zero.  No counterpart in the reference (part of its fp32 matmuls). */
+int eg_split_bf16(const float* x, int64_t rows, int64_t cols, int64_t ld, void* hi, void* lo, void* stream);
+
+/* One K segment of eg_gemm_bf16x3: the eg_split_bf16 planes of A [m, k]
+ * and of B [n, k] for each column group (b2_* only read when n2 > 0). */
+typedef struct eg_gemm_operands {
+  const void* a_hi;
+  const void* a_lo;
+  int64_t lda;
+  const void* b_hi;
+  const void* b_lo;
+  int64_t ldb;
+  const void* b2_hi;
+  const void* b2_lo;
+  int64_t ldb2;
+  int64_t k; /* multiple of 32 */
+} eg_gemm_operands;
+
+/* fp32 GEMM on the bf16 matrix cores over n_seg (1 or 2) K segments and two
+ * column groups:
+ *   C [m, n]   (+)= sum_s A_s B_s^T     C2 [m, n2] (+)= sum_s A_s B2_s^T
+ * every operand given as its eg_split_bf16 planes and hi*hi + hi*lo + lo*hi
+ * accumulated in fp32 (hi + lo keeps 16 mantissa bits: a relative error
+ * up to ~3 x 2^-18 per product, about 1e-5 of the result on random data; a
+ * non-finite operand gives NaN).  Planes 16-byte aligned, leading dimensions
+ * multiples of 8; accumulate = 1 adds to C / C2.  k_slices > 1 cuts the K
+ * range into that many slices run by separate workgroups, their partial
+ * products summed in slice order afterwards (deterministic), in a workspace
+ * of eg_gemm_workspace_size bytes.  The projections of ple_forward, key =
+ * emb w_key^T and value = emb w_value^T as the two column groups of one
+ * call, and their backward d_emb = d_key w_key + d_value w_value as two
+ * segments with the weights' transposes as B (engraft/replica/layers.py:
+ * 594-606, where they are torch fp32 matmuls). */
+int64_t eg_gemm_workspace_size(int64_t m, int64_t n, int64_t n2, int32_t k_slices);
+int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,
+                   int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate, int32_t k_slices,
+                   void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -4,7 +4,11 @@ a sequence in two chunks with the history carried, and the gradient.
 
 Bar (floating point, as the reference's own check of its two formulations,
 tests/test_replica_layers.py:282): |out - oracle| <= 1e-4; history 1e-5;
-gradients within 1e-4 relative of the largest entry."""
+gradients within 1e-4 relative of the largest entry.  With gemm="bf16x3" (the
+projections on the bf16 matrix cores, 16 mantissa bits per operand: about 1e-5
+relative per projection output) the output and gradient bars are the same and
+the history, gate and score bars are 1e-4, 5e-5 and 1e-4 (measured: 2.1e-5,
+7.8e-6 and 1.7e-5 on O(1)-O(5) values; the fp32 path: 3.6e-6, 5.1e-7, 1.4e-6)."""
 from __future__ import annotations
 
 import sys
@@ -31,9 +35,14 @@ def _dev_weights(w, dev):
     return PleWeights(**{k: v.to(dev) for k, v in w.items()})
 
 
-def test_ple_forward_against_oracle(cuda):
+_BARS = {"fp32": (1e-5, 1e-5, 1e-4), "bf16x3": (1e-4, 5e-5, 1e-4)}  # history, gate, score
+
+
+@pytest.mark.parametrize("gemm", ["fp32", "bf16x3"])
+def test_ple_forward_against_oracle(cuda, gemm):
     from engraft_ngram_amd import ple
-    print("[gpu-test] ple_forward", file=sys.stderr, flush=True)
+    print(f"[gpu-test] ple_forward gemm={gemm}", file=sys.stderr, flush=True)
+    bar_h, bar_g, bar_s = _BARS[gemm]
     hc, n, T = 4, 2560, 48
     w = ple_weights(hc, n, seed=3)
     wd = _dev_weights(w, cuda)
@@ -46,12 +55,13 @@ def test_ple_forward_against_oracle(cuda):
     diag = {}
     for lo, hi in ((0, 30), (30, T)):
         exp, hist_c, s_c, gate_c = P.ple_forward(emb[lo:hi], hidden[lo:hi], w, hist_c, hc, n, 1e-6, 3)
-        got, hist_d = ple.ple_forward(emb[lo:hi].to(cuda), hidden[lo:hi].to(cuda), wd, hist_d, _HP, diag=diag)
+        got, hist_d = ple.ple_forward(emb[lo:hi].to(cuda), hidden[lo:hi].to(cuda), wd, hist_d, _HP, diag=diag,
+                                      gemm=gemm)
         err = (got.cpu() - exp).abs().max().item()
         assert err <= 1e-4, f"chunk [{lo},{hi}): max |diff| {err}"
-        assert torch.allclose(hist_d.cpu(), hist_c, atol=1e-5)
-        assert torch.allclose(diag["gate"].cpu(), gate_c, atol=1e-5)
-        assert torch.allclose(diag["s"].cpu(), s_c, atol=1e-4)
+        assert (hist_d.cpu() - hist_c).abs().max().item() <= bar_h
+        assert (diag["gate"].cpu() - gate_c).abs().max().item() <= bar_g
+        assert (diag["s"].cpu() - s_c).abs().max().item() <= bar_s
     assert hist_d.shape == (9, hc, n)
 
 
@@ -111,14 +121,17 @@ def test_ple_history_gradient_across_chunks(cuda):
     assert (e_d.grad.cpu() - e_c.grad).abs().max().item() <= 1e-4 * scale
 
 
-@pytest.mark.parametrize("dv,dg", [(False, False), (True, False), (False, True)])
-def test_ple_native_backward_against_oracle(cuda, dv, dg):
+@pytest.mark.parametrize("dv,dg,gemm", [(False, False, "fp32"), (True, False, "fp32"), (False, True, "fp32"),
+                                        (False, False, "bf16x3"), (True, False, "bf16x3")])
+def test_ple_native_backward_against_oracle(cuda, dv, dg, gemm):
     """The HIP backward (no weight gradients): d_emb, d_hidden and the incoming
     history's gradient, with a gradient on the returned history too, against
     autograd of the oracle on the CPU (T 40 after a 9-row history), for the
-    plain block and with either factor of gated detached."""
+    plain block and with either factor of gated detached; with bf16x3 the
+    projections' backward runs as one gemm_x3 call over two K segments."""
     from engraft_ngram_amd import _lib, ple
-    print(f"[gpu-test] ple native backward detach_value={dv} detach_gate={dg}", file=sys.stderr, flush=True)
+    print(f"[gpu-test] ple native backward detach_value={dv} detach_gate={dg} gemm={gemm}", file=sys.stderr,
+          flush=True)
     hc, n, T = 4, 2560, 40
     w = ple_weights(hc, n, seed=31)
     wd = _dev_weights(w, cuda)
@@ -142,11 +155,12 @@ def test_ple_native_backward_against_oracle(cuda, dv, dg):
     _lib.call = spy
     try:
         out_d, nh_d = ple.ple_forward(leaves_d[0], leaves_d[1], wd, leaves_d[2], _HP, detach_value=dv,
-                                      detach_gate=dg)
+                                      detach_gate=dg, gemm=gemm)
         ((out_d * r.to(cuda)).sum() + (nh_d * rh.to(cuda)).sum()).backward()
     finally:
         _lib.call = real_call
     assert "eg_ple_conv_backward" in called and "eg_ple_gate_backward" in called
+    assert (called.count("eg_gemm_bf16x3") == 3) == (gemm == "bf16x3")  # key, value, then d_emb
     for name, got, exp in zip(("emb", "hidden", "hist"), (x.grad for x in leaves_d), (x.grad for x in leaves_c)):
         scale = exp.abs().max().item()
         err = (got.cpu() - exp).abs().max().item()
