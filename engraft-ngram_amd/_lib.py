@@ -115,12 +115,12 @@ SIGNATURES = {
     "eg_ple_gate": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32,
                               c_int32, ctypes.c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_conv_backward": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32,
-                                       c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+                                       c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "eg_ple_gate_backward": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
                                        c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_conv": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32,
-                              c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+                              c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_rms": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, ctypes.c_float, c_void_p, c_void_p]),
     "eg_split_bf16": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "eg_gemm_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int32]),

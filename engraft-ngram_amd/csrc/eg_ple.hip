@@ -128,7 +128,8 @@ __global__ __launch_bounds__(256) void ple_conv_kernel(const float* __restrict__
                                                        int hc, int n, const float* __restrict__ conv_w, int taps,
                                                        int dil, const float* __restrict__ hidden,
                                                        const float* __restrict__ value,
-                                                       const float* __restrict__ gate, float* __restrict__ out) {
+                                                       const float* __restrict__ gate, float* __restrict__ out,
+                                                       float* __restrict__ pre) {
 #pragma clang fp contract(off)
   const int C = hc * n;
   const int n_cblk = (C + 255) / 256;
@@ -179,6 +180,7 @@ __global__ __launch_bounds__(256) void ple_conv_kernel(const float* __restrict__
         if (k < taps && ok[b][k]) acc += x[b][k] * w[k];
       const float silu = acc / (1.0f + expf(-acc));
       const int64_t o = (t + b) * C + c;
+      if (pre != nullptr) pre[o] = acc;  // the backward's SiLU derivative
       if constexpr (MODE == 0) out[o] = (hv[b] + vv[b] * gj[b]) + silu;
       else if constexpr (MODE == 1) out[o] = vv[b] * gj[b] + silu;
       else out[o] = silu;
@@ -229,9 +231,11 @@ constexpr int kConvBwdMaxBack = 32;  // (taps - 1) * dilation the LDS window hol
 constexpr int kConvBwdRun = 16;      // rows of full per workgroup
 constexpr int kConvBwdBatch = 4;     // positions whose loads are issued together
 
+template <bool PRE>
 __global__ __launch_bounds__(256) void ple_conv_bwd_kernel(const float* __restrict__ full, int64_t hist_rows,
                                                            int64_t T, int hc, int n,
                                                            const float* __restrict__ conv_w, int taps, int dil,
+                                                           const float* __restrict__ pre,
                                                            const float* __restrict__ d_out,
                                                            const float* __restrict__ d_tail, int64_t tail_rows,
                                                            float* __restrict__ d_full) {
@@ -257,16 +261,20 @@ __global__ __launch_bounds__(256) void ple_conv_bwd_kernel(const float* __restri
   for (int64_t t = ta; t < tb; t += kConvBwdBatch) {
     float x[kConvBwdBatch][kMaxTaps];
     bool ok[kConvBwdBatch][kMaxTaps];
-    float dv[kConvBwdBatch];
+    float dv[kConvBwdBatch], pa[kConvBwdBatch];
 #pragma unroll
     for (int b = 0; b < kConvBwdBatch; ++b) {
       const int64_t tt = min(t + b, tb - 1);
+      if constexpr (PRE) {
+        pa[b] = pre[tt * C + c];  // the forward's pre-activation
+      } else {
 #pragma unroll
-      for (int k = 0; k < kMaxTaps; ++k) {
-        if (k < taps) {
-          const int64_t src = hist_rows + tt - (int64_t)(taps - 1 - k) * dil;
-          ok[b][k] = src >= 0;
-          x[b][k] = full[(ok[b][k] ? src : 0) * C + c];
+        for (int k = 0; k < kMaxTaps; ++k) {
+          if (k < taps) {
+            const int64_t src = hist_rows + tt - (int64_t)(taps - 1 - k) * dil;
+            ok[b][k] = src >= 0;
+            x[b][k] = full[(ok[b][k] ? src : 0) * C + c];
+          }
         }
       }
       dv[b] = d_out[tt * C + c];
@@ -275,9 +283,13 @@ __global__ __launch_bounds__(256) void ple_conv_bwd_kernel(const float* __restri
     for (int b = 0; b < kConvBwdBatch; ++b) {
       if (t + b >= tb) break;
       float acc = 0.0f;
+      if constexpr (PRE) {
+        acc = pa[b];
+      } else {
 #pragma unroll
-      for (int k = 0; k < kMaxTaps; ++k)
-        if (k < taps && ok[b][k]) acc += x[b][k] * w[k];
+        for (int k = 0; k < kMaxTaps; ++k)
+          if (k < taps && ok[b][k]) acc += x[b][k] * w[k];
+      }
       const float sg = 1.0f / (1.0f + expf(-acc));
       dacc[(t + b - ta) * 256 + tid] = dv[b] * (sg * (1.0f + acc * (1.0f - sg)));
     }
@@ -456,9 +468,9 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_kernel(
 template <int MODE, bool SHARED>
 static void launch_conv(dim3 grid, hipStream_t st, const float* full, int64_t hist_rows, int64_t n_pos, int hc, int n,
                         const float* conv_w, int taps, int dil, const float* hidden, const float* value,
-                        const float* gate, float* out) {
+                        const float* gate, float* out, float* pre) {
   hipLaunchKernelGGL((ple_conv_kernel<MODE, SHARED>), grid, dim3(256), 0, st, full, hist_rows, n_pos, hc, n, conv_w,
-                     taps, dil, hidden, value, gate, out);
+                     taps, dil, hidden, value, gate, out, pre);
 }
 
 }  // namespace eg
@@ -485,7 +497,7 @@ int eg_ple_gate(const float* key, const float* value, const float* hidden, const
 
 int eg_ple_conv(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
                 const float* conv_w, int32_t taps, int32_t dilation, int32_t shared_history, const float* hidden,
-                const float* value, const float* gate, float* out, void* stream) {
+                const float* value, const float* gate, float* out, float* pre, void* stream) {
   EG_CHECK_ARG(n_pos >= 0 && hist_rows >= 0 && hc >= 1 && n_embd >= 1 && taps >= 1 && taps <= 8 && dilation >= 1,
                "n_pos=%lld hist_rows=%lld hc=%d n_embd=%d taps=%d dilation=%d", (long long)n_pos,
                (long long)hist_rows, hc, n_embd, taps, dilation);
@@ -501,7 +513,7 @@ int eg_ple_conv(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc,
   const int mode = hidden ? 0 : (value ? 1 : 2);
   const bool sh = shared_history != 0;
 #define EG_CONV(M, S) launch_conv<M, S>(grid, st, full, hist_rows, n_pos, hc, n_embd, conv_w, taps, dilation, \
-                                          hidden, value, gate, out)
+                                          hidden, value, gate, out, pre)
   if (mode == 0) sh ? EG_CONV(0, true) : EG_CONV(0, false);
   else if (mode == 1) sh ? EG_CONV(1, true) : EG_CONV(1, false);
   else sh ? EG_CONV(2, true) : EG_CONV(2, false);
@@ -522,8 +534,8 @@ int eg_ple_rms(const float* x, int64_t n_rows, int32_t hc, int32_t n_embd, const
 }
 
 int eg_ple_conv_backward(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
-                         const float* conv_w, int32_t taps, int32_t dilation, const float* d_out, const float* d_tail,
-                         int64_t tail_rows, float* d_full, void* stream) {
+                         const float* conv_w, int32_t taps, int32_t dilation, const float* pre, const float* d_out,
+                         const float* d_tail, int64_t tail_rows, float* d_full, void* stream) {
   EG_CHECK_ARG(n_pos >= 0 && hist_rows >= 0 && hc >= 1 && n_embd >= 1 && taps >= 1 && taps <= 8 && dilation >= 1,
                "n_pos=%lld hist_rows=%lld hc=%d n_embd=%d taps=%d dilation=%d", (long long)n_pos,
                (long long)hist_rows, hc, n_embd, taps, dilation);
@@ -539,8 +551,14 @@ int eg_ple_conv_backward(const float* full, int64_t hist_rows, int64_t n_pos, in
   const int64_t blocks = (int64_t)((hc * n_embd + 255) / 256) * ((rows + kConvBwdRun - 1) / kConvBwdRun);
   EG_CHECK_ARG(blocks < (1LL << 32), "too many elements");
   const size_t lds = (size_t)(kConvBwdRun + (taps - 1) * dilation) * 256 * sizeof(float);
-  hipLaunchKernelGGL(ple_conv_bwd_kernel, dim3((unsigned)blocks), dim3(256), lds, (hipStream_t)stream, full, hist_rows,
-                     n_pos, hc, n_embd, conv_w, taps, dilation, d_out, tail_rows ? d_tail : nullptr, tail_rows, d_full);
+  if (pre != nullptr)
+    hipLaunchKernelGGL(ple_conv_bwd_kernel<true>, dim3((unsigned)blocks), dim3(256), lds, (hipStream_t)stream, full,
+                       hist_rows, n_pos, hc, n_embd, conv_w, taps, dilation, pre, d_out, tail_rows ? d_tail : nullptr,
+                       tail_rows, d_full);
+  else
+    hipLaunchKernelGGL(ple_conv_bwd_kernel<false>, dim3((unsigned)blocks), dim3(256), lds, (hipStream_t)stream, full,
+                       hist_rows, n_pos, hc, n_embd, conv_w, taps, dilation, pre, d_out, tail_rows ? d_tail : nullptr,
+                       tail_rows, d_full);
   return launch_status("ple_conv_bwd_kernel");
 }
 

@@ -263,13 +263,14 @@ class _PleFn(torch.autograd.Function):
                   _lib.ptr(nc32), t_len, hc, n, float(eps), _lib.ptr(full[h0:]), _lib.ptr(s), _lib.ptr(gate),
                   _lib.ptr(rstd), st)
         out = torch.empty((t_len, hc, n), **f32)
+        pre = torch.empty((t_len, hc * n), **f32) if native else None  # kept for the backward's SiLU derivative
         _lib.call("eg_ple_conv", _lib.ptr(full), h0, t_len, hc, n, _lib.ptr(conv32), taps, int(dil), 0,
-                  _lib.ptr(hidden32), _lib.ptr(value), _lib.ptr(gate), _lib.ptr(out), st)
+                  _lib.ptr(hidden32), _lib.ptr(value), _lib.ptr(gate), _lib.ptr(out), _lib.ptr(pre), st)
         hist_len = (taps - 1) * int(dil)
         new_hist = (full[-hist_len:] if hist_len > 0 else full[:0]).reshape(-1, hc, n).to(hidden.dtype).clone()
         ctx.native = native
         if native:
-            ctx.save_for_backward(key, value, hidden32, full, s, gate, rstd, nk32, nq32, nc32, conv32, wk32, wv32)
+            ctx.save_for_backward(key, value, hidden32, full, s, gate, rstd, nk32, nq32, nc32, conv32, wk32, wv32, pre)
             ctx.dtypes = (emb.dtype, hidden.dtype, hist.dtype)
             ctx.tail_rows = new_hist.shape[0]
         else:
@@ -302,7 +303,7 @@ class _PleFn(torch.autograd.Function):
 
     @staticmethod
     def _backward_native(ctx, d_out, d_hist):
-        key, value, hidden32, full, s, gate, rstd, nk32, nq32, nc32, conv32, wk32, wv32 = ctx.saved_tensors
+        key, value, hidden32, full, s, gate, rstd, nk32, nq32, nc32, conv32, wk32, wv32, pre = ctx.saved_tensors
         _eps, dil, detach_value, detach_gate = ctx.cfg
         emb_dt, hidden_dt, hist_dt = ctx.dtypes
         t_len, hc, n = hidden32.shape
@@ -317,7 +318,7 @@ class _PleFn(torch.autograd.Function):
         d_tail = d_hist.to(**f32).reshape(tail, c_dim).contiguous() if tail else None
         d_full = torch.empty((h0 + t_len, c_dim), **f32)
         _lib.call("eg_ple_conv_backward", _lib.ptr(full), h0, t_len, hc, n, _lib.ptr(conv32), conv32.shape[1],
-                  int(dil), _lib.ptr(d_out32), _lib.ptr(d_tail), tail, _lib.ptr(d_full), st)
+                  int(dil), _lib.ptr(pre), _lib.ptr(d_out32), _lib.ptr(d_tail), tail, _lib.ptr(d_full), st)
         d_key = torch.empty((t_len, c_dim), **f32) if (need_emb and not detach_gate) else None
         d_value = torch.empty((t_len, n), **f32) if (need_emb and not detach_value) else None
         d_hidden = torch.empty((t_len, hc, n), **f32) if need_hidden else None
@@ -483,7 +484,7 @@ class PleReplica:
         out = torch.empty((n_pos, self.hc, self.n_embd), dtype=torch.float32, device=self.device)
         taps = self.conv1d.shape[2]
         _lib.call("eg_ple_conv", _lib.ptr(full), hist_rows, n_pos, self.hc, self.n_embd, _lib.ptr(self.conv1d), taps,
-                  self.dilation, 1 if shared else 0, None, _lib.ptr(value), _lib.ptr(gate), _lib.ptr(out),
+                  self.dilation, 1 if shared else 0, None, _lib.ptr(value), _lib.ptr(gate), _lib.ptr(out), None,
                   _lib.stream_ptr(self.device))
         return out
 

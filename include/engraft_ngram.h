@@ -297,22 +297,26 @@ int eg_ple_gate(const float* key, const float* value, const float* hidden, const
  * (PleReplica.conv_out, lens.py:309-332).  shared_history != 0: every
  * position t is its own one-token continuation of the history, the tap at
  * distance 0 reading row hist_rows + t and the others row hist_rows - distance
- * (PleReplica.ple_out_at, lens.py:341-385). */
+ * (PleReplica.ple_out_at, lens.py:341-385).  pre (optional, f32 [n_pos,
+ * hc*n_embd]) receives conv before the SiLU, for eg_ple_conv_backward. */
 int eg_ple_conv(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
                 const float* conv_w, int32_t taps, int32_t dilation, int32_t shared_history,
-                const float* hidden, const float* value, const float* gate, float* out, void* stream);
+                const float* hidden, const float* value, const float* gate, float* out, float* pre,
+                void* stream);
 
 /* Backward of eg_ple_conv (mode 0, own history): d_full f32 [hist_rows + n_pos,
  * hc*n_embd] = the gradient of [history; normed] given d_out f32 [n_pos,
  * hc*n_embd] (the block's output gradient) and d_tail (optional, f32
  * [tail_rows, hc*n_embd]: the gradient of the last tail_rows rows of full, the
- * history the forward returned).  full and conv_w as the forward's.  The
- * convolution weights' gradient is not computed.  (taps-1)*dilation <= 32.
- * Replaces the autograd of causal_depthwise_conv + silu
- * (engraft/replica/layers.py:257-293, 614-626). */
+ * history the forward returned).  full and conv_w as the forward's; pre
+ * (optional) the forward's pre-activation, read in place of recomputing the
+ * convolution.  The convolution weights' gradient is not computed.
+ * (taps-1)*dilation <= 32.  Replaces the autograd of causal_depthwise_conv +
+ * silu (engraft/replica/layers.py:257-293, 614-626). */
 int eg_ple_conv_backward(const float* full, int64_t hist_rows, int64_t n_pos, int32_t hc, int32_t n_embd,
-                         const float* conv_w, int32_t taps, int32_t dilation, const float* d_out,
-                         const float* d_tail, int64_t tail_rows, float* d_full, void* stream);
+                         const float* conv_w, int32_t taps, int32_t dilation, const float* pre,
+                         const float* d_out, const float* d_tail, int64_t tail_rows, float* d_full,
+                         void* stream);
 
 /* Backward of eg_ple_gate: from d_out and d_normed (the rows of d_full after
  * the history), the gradients of the projections and of the hidden state:

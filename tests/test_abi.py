@@ -73,13 +73,14 @@ def test_host_side_argument_checks():
         ("Q8_0 or MXFP8", _lib.EG_ERR_ARG, lib.eg_quantize_rows, None, 1, 128, None, ctypes.byref(tab), None),
         ("n_embd", _lib.EG_ERR_ARG, lib.eg_ple_gate, None, None, None, None, None, None, 1, 4, 5000, 1e-6, None,
          None, None, None, None),
-        ("taps", _lib.EG_ERR_ARG, lib.eg_ple_conv, None, 0, 1, 4, 64, None, 9, 3, 0, None, None, None, None, None),
+        ("taps", _lib.EG_ERR_ARG, lib.eg_ple_conv, None, 0, 1, 4, 64, None, 9, 3, 0, None, None, None, None, None,
+         None),
         ("dilation", _lib.EG_ERR_UNSUPPORTED, lib.eg_ple_conv_backward, None, 0, 1, 4, 64, None, 4, 11, None, None,
-         0, None, None),
+         None, 0, None, None),
         ("hc=5", _lib.EG_ERR_UNSUPPORTED, lib.eg_ple_gate_backward, *([None] * 11), 1, 5, 64, 0, 0, None, None,
          None, None),
-        ("taps", _lib.EG_ERR_ARG, lib.eg_ple_conv_backward, None, 0, 1, 4, 64, None, 9, 1, None, None, 0, None,
-         None),
+        ("taps", _lib.EG_ERR_ARG, lib.eg_ple_conv_backward, None, 0, 1, 4, 64, None, 9, 1, None, None, None, 0,
+         None, None),
     ]
     for needle, code, fn, *args in cases:
         rc, msg = _rejects(fn, *args)

@@ -191,3 +191,42 @@ def test_ple_weight_gradients_recompute_path(cuda):
                      (wd.conv1d.grad, wc["conv1d"].grad)):
         scale = exp.abs().max().item()
         assert (got.cpu() - exp).abs().max().item() <= 1e-4 * scale
+
+
+def test_conv_backward_stored_preactivation_equals_recompute(cuda):
+    """eg_ple_conv_backward with the forward's stored pre-activation (what
+    ple_forward's backward uses) and without it (recomputing the convolution
+    from full): bit-identical, the forward and backward sum their taps in the
+    same order."""
+    from engraft_ngram_amd import _lib
+    _say = lambda m: print(f"[gpu-test] {m}", file=sys.stderr, flush=True)
+    _say("conv backward, stored pre-activation vs recompute")
+    g = torch.Generator(device=cuda).manual_seed(51)
+    hc, n, T, h0, taps, dil = 4, 256, 37, 9, 4, 3
+    C = hc * n
+    full = torch.randn(h0 + T, C, generator=g, device=cuda)
+    conv = torch.randn(C, taps, generator=g, device=cuda) * 0.5
+    hidden = torch.randn(T, C, generator=g, device=cuda)
+    value = torch.randn(T, n, generator=g, device=cuda)
+    gate = torch.rand(T, hc, generator=g, device=cuda)
+    out = torch.empty(T, C, device=cuda)
+    pre = torch.empty(T, C, device=cuda)
+    st = _lib.stream_ptr(cuda)
+    _lib.call("eg_ple_conv", _lib.ptr(full), h0, T, hc, n, _lib.ptr(conv), taps, dil, 0, _lib.ptr(hidden),
+              _lib.ptr(value), _lib.ptr(gate), _lib.ptr(out), _lib.ptr(pre), st)
+    d_out = torch.randn(T, C, generator=g, device=cuda)
+    d_tail = torch.randn(9, C, generator=g, device=cuda)
+    res = []
+    for p in (pre, None):
+        d_full = torch.empty(h0 + T, C, device=cuda)
+        _lib.call("eg_ple_conv_backward", _lib.ptr(full), h0, T, hc, n, _lib.ptr(conv), taps, dil, _lib.ptr(p),
+                  _lib.ptr(d_out), _lib.ptr(d_tail), 9, _lib.ptr(d_full), st)
+        res.append(d_full)
+    torch.cuda.synchronize()
+    assert torch.equal(res[0], res[1])
+    # the stored pre-activation is the convolution itself
+    ref = torch.zeros(T, C, device=cuda, dtype=torch.float64)
+    for k in range(taps):
+        back = (taps - 1 - k) * dil
+        ref += full[h0 - back:h0 + T - back].double() * conv[:, k].double()
+    assert float((pre.double() - ref).abs().max()) <= 1e-5
