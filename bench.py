@@ -437,7 +437,8 @@ def bench_damage_scan(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     counts = torch.zeros(ids.size, dtype=torch.int64, device=dev)
     spec = tab.c_spec
     n_bits = tab.n_rows
-    bitmap = torch.empty(2 * ((n_bits + 31) // 32), dtype=torch.int32, device=dev)
+    nw = (n_bits + 31) // 32
+    bitmap = torch.empty(2 * nw + (nw + 31) // 32, dtype=torch.int32, device=dev)
     _lib.call("eg_build_id_bitmap", _lib.ptr(ids_d), ids.size, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(dev))
 
     def timed(bm) -> float:

@@ -246,10 +246,11 @@ int eg_scan_overlay(const eg_hash_spec* spec, const int64_t* tokens, int64_t n_t
                     int64_t* read_counts, void* stream);
 
 /* Rank bitmap of sorted, unique overlay ids for eg_scan_overlay: bitmap is
- * uint32 [2 * nw], nw = ceil(n_bits/32); word w < nw gets bit b set for every
- * id 32 w + b < n_bits (all other bits cleared), and bitmap[nw + w] = the
- * number of ids below 32 w.  No counterpart in the reference: it turns the
- * scan's per-lookup binary search into one probe. */
+ * uint32 [2 * nw + ceil(nw/32)], nw = ceil(n_bits/32); word w < nw gets bit b
+ * set for every id 32 w + b < n_bits (all other bits cleared), bitmap[nw + w]
+ * = the number of ids below 32 w, and coarse word bitmap[2 nw + v] has bit u
+ * set when word 32 v + u is not zero.  No counterpart in the reference: it
+ * turns the scan's per-lookup binary search into one or two probes. */
 int eg_build_id_bitmap(const int32_t* ids, int64_t n_ids, uint32_t* bitmap, int64_t n_bits, void* stream);
 
 /* Gather with per-slot replacement rows (engraft/replica/seq.py:433-441):

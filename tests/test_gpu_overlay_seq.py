@@ -174,8 +174,8 @@ def test_scan_overlay_rank_bitmap(cuda):
     """eg_scan_overlay with and without the eg_build_id_bitmap rank bitmap:
     the bits hold exactly the ids below n_bits (an id past the table's rows is
     left out and still never hits), the ranks are the lower bounds of 32 w in
-    the ids, and both launches give the same per-position outputs and read
-    counts (bit-exact)."""
+    the ids, the coarse bits mark the nonempty words, and both launches give
+    the same per-position outputs and read counts (bit-exact)."""
     import ctypes
 
     from engraft_ngram_amd import _lib
@@ -191,15 +191,19 @@ def test_scan_overlay_rank_bitmap(cuda):
     ov = np.array(sorted(picked), dtype=np.int32)
     ids = torch.from_numpy(ov).to(cuda)
     dn = torch.from_numpy(rng.random(ov.size).astype(np.float32)).to(cuda)
-    bitmap = torch.full((2 * ((n_bits + 31) // 32),), -1, dtype=torch.int32, device=cuda)  # stale bits get cleared
-    _lib.call("eg_build_id_bitmap", _lib.ptr(ids), ov.size, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(cuda))
     nw = (n_bits + 31) // 32
+    bitmap = torch.full((2 * nw + (nw + 31) // 32,), -1, dtype=torch.int32, device=cuda)  # stale bits get cleared
+    _lib.call("eg_build_id_bitmap", _lib.ptr(ids), ov.size, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(cuda))
     want = np.zeros(nw * 32, dtype=bool)
     want[ov[ov < n_bits]] = True
     bm = bitmap.cpu().numpy()
     got_bits = np.unpackbits(bm[:nw].view(np.uint8), bitorder="little").astype(bool)
     assert np.array_equal(got_bits, want)
-    assert np.array_equal(bm[nw:].astype(np.int64), np.searchsorted(ov, np.arange(nw, dtype=np.int64) * 32))
+    assert np.array_equal(bm[nw:2 * nw].astype(np.int64), np.searchsorted(ov, np.arange(nw, dtype=np.int64) * 32))
+    coarse = np.unpackbits(bm[2 * nw:].view(np.uint8), bitorder="little").astype(bool)
+    want_c = np.zeros(coarse.size, dtype=bool)
+    want_c[:nw] = bm[:nw] != 0
+    assert np.array_equal(coarse, want_c)
     tok = torch.from_numpy(np.asarray(tokens, dtype=np.int64)).to(cuda)
     spec_c = tab.c_spec
     outs = []
