@@ -21,8 +21,11 @@
 // through registers.  A plane tile is rows x 32 bf16 (64 B rows, no padding);
 // the 16-byte chunk c of row r sits in slot c ^ ((r >> 1) & 3), which spreads
 // the fragment reads (32 rows at one chunk) over the banks.  Two stages (64 KB)
-// keep two workgroups on a CU; three or four stages (one workgroup) and
-// register-staged loads into a padded LDS tile measured slower.  With few
+// keep two workgroups on a CU.  Measured against it after a warm-up, launches
+// interleaved: 128 x 256 and 256 x 128 tiles with eight wavefronts, 256 x 256
+// with sixteen, three stages, and scheduling hints that interleave the LDS
+// reads with the MFMAs ran 3-5 % slower; register-staged loads into a padded
+// LDS tile ran 20 % slower.  With few
 // output tiles (the backward's 16 x 20) the K range is cut into slices whose
 // partial products go to a workspace and are summed in slice order by a
 // second kernel, so the result does not depend on scheduling.
