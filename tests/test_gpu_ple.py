@@ -230,3 +230,37 @@ def test_conv_backward_stored_preactivation_equals_recompute(cuda):
         back = (taps - 1 - k) * dil
         ref += full[h0 - back:h0 + T - back].double() * conv[:, k].double()
     assert float((pre.double() - ref).abs().max()) <= 1e-5
+
+
+@pytest.mark.parametrize("gemm", ["fp32", "bf16x3"])
+def test_ple_forward_checkpointed_bit_identical(cuda, gemm):
+    """As tests/test_seq.py:91-112 does for a whole layer: wrapping the block in
+    torch.utils.checkpoint (the forward recomputed during the backward) changes
+    nothing -- output, loss and the gradients of emb and hidden are torch.equal
+    with and without it (every kernel on the path is deterministic)."""
+    from torch.utils.checkpoint import checkpoint
+
+    from engraft_ngram_amd import ple
+    print(f"[gpu-test] ple_forward under checkpoint gemm={gemm}", file=sys.stderr, flush=True)
+    hc, n, T = 4, 2560, 24
+    w = ple_weights(hc, n, seed=61)
+    wd = _dev_weights(w, cuda)
+    g = torch.Generator().manual_seed(62)
+    emb = (torch.randn((T, n), generator=g) * 0.1).to(cuda)
+    hidden = (torch.randn((T, hc, n), generator=g) * 0.1).to(cuda)
+    r = torch.randn((T, hc, n), generator=g).to(cuda)
+    h0 = torch.zeros(0, hc, n, device=cuda)
+
+    def block(e, h):
+        return ple.ple_forward(e, h, wd, h0, _HP, gemm=gemm)[0]
+
+    res = []
+    for ckpt in (False, True):
+        e = emb.clone().requires_grad_(True)
+        h = hidden.clone().requires_grad_(True)
+        out = checkpoint(block, e, h, use_reentrant=False) if ckpt else block(e, h)
+        loss = (out * r).sum()
+        loss.backward()
+        res.append((out.detach(), loss.detach(), e.grad, h.grad))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
