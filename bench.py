@@ -99,6 +99,31 @@ def traffic_from_profile(kernel_key: str):
     return None
 
 
+def copy_ceiling_us(n_bytes_moved: int, dev) -> float:
+    """Time of a plain device copy (torch ``copy_``) that reads and writes
+    ``n_bytes_moved`` bytes in total, warmed up, four buffer pairs rotated (so
+    no repeat is served from the Infinity Cache): the practical ceiling for a
+    kernel that moves that many bytes of HBM traffic."""
+    import torch
+
+    n = max(1, n_bytes_moved // 8)  # floats per buffer: half the bytes read, half written
+    src = [torch.ones(n, device=dev) for _ in range(4)]
+    dst = [torch.empty(n, device=dev) for _ in range(4)]
+    for i in range(200):
+        dst[i % 4].copy_(src[i % 4])
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    best = float("inf")
+    for _ in range(5):
+        torch.cuda.synchronize()
+        a.record()
+        for i in range(50):
+            dst[i % 4].copy_(src[i % 4])
+        b.record()
+        torch.cuda.synchronize()
+        best = min(best, a.elapsed_time(b) / 50 * 1e3)
+    return best
+
+
 def oracle_spec(hp: dict):
     from oracle import hash as OH
     return OH.HashSpec(eos_token_id=hp["eos_token_id"], ngram_size=hp["ngram_size"],
@@ -640,6 +665,11 @@ def main() -> None:
 
     rows_per_step = n_pos * SLOTS
     fbytes = forward_bytes(n_pos)
+    # a plain device copy moving the kernel's measured HBM traffic (profiles/), for scale
+    traffic = traffic_from_profile("forward_q8_cfg1")
+    copy_us = copy_ceiling_us(traffic, dev) if traffic else None
+    if copy_us:
+        log(f"forward: a device copy moving the same {traffic / 1e6:.1f} MB takes {copy_us:.1f} us")
     achieved = fbytes / (kernel_ms * 1e-3) / 1e9
     log(f"forward: {ms_per_step * 1e3:.1f} us/step wall, {kernel_ms * 1e3:.1f} us/launch back to back "
         f"(first launch alone {first_ms * 1e3:.1f}), {achieved:.0f} GB/s algorithmic")
@@ -667,9 +697,11 @@ def main() -> None:
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profile("forward_q8_cfg1"),
+            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
             "kernel": "eg::forward_kernel<Q8_0, dim 128, 2 x 1024-column parts per position, bf16 out, no overlay>",
             "algorithmic_bytes_per_launch": fbytes, "avg_launch_us": kernel_ms * 1e3,
+            "copy_of_same_traffic_us": copy_us,
+            "launch_vs_copy_of_same_traffic": (kernel_ms * 1e3 / copy_us) if copy_us else None,
         },
         "forward": {
             "rows_per_s": rows_per_step / (kernel_ms * 1e-3),
