@@ -1,6 +1,6 @@
 // The PLE block that consumes the gathered rows (engraft/replica/layers.py:
 // 565-626): after the two projections key = emb @ w_key^T [T, hc*n] and
-// value = emb @ w_value^T [T, n] (library GEMMs on the matrix cores),
+// value = emb @ w_value^T [T, n] (fp32 library GEMMs, or eg_gemm_bf16x3),
 //
 //   ple_gate_kernel   one workgroup per (position, stream j): the RMS norms
 //                     of key_j and hidden_j, s_j = <key_j^, hidden_j^>/sqrt(n),
@@ -465,6 +465,139 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_kernel(
 }
 
 
+// Sum over the workgroup of up to kGbMaxHc values per thread, for any whole
+// number of wavefronts (the vector form below runs n/4 threads).
+__device__ inline void block_sum4_n(float v[kGbMaxHc], float* red) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j)
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v[j] += __shfl_xor(v[j], o);
+  __syncthreads();  // the previous use of red is complete
+  if (lane == 0)
+#pragma unroll
+    for (int j = 0; j < kGbMaxHc; ++j) red[j * (kGbThreads / 64) + wave] = v[j];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) {
+    float t = 0.0f;
+    for (int w = 0; w < nw; ++w) t += red[j * (kGbThreads / 64) + w];
+    v[j] = t;
+  }
+}
+
+// ple_gate_bwd_kernel with one float4 per thread: n/4 threads per position
+// (n a multiple of 256, so whole wavefronts), 16-byte loads and stores, the
+// same arithmetic per element.
+__global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_vec_kernel(
+    const float* __restrict__ key, const float* __restrict__ value, const float* __restrict__ hidden,
+    const float* __restrict__ norm_key, const float* __restrict__ norm_query, const float* __restrict__ norm_conv,
+    const float* __restrict__ s_in, const float* __restrict__ gate_in, const float* __restrict__ rstd,
+    const float* __restrict__ d_out, const float* __restrict__ d_normed, int hc, int n, float inv_sqrt_n,
+    int detach_value, int detach_gate, float* __restrict__ d_key, float* __restrict__ d_value,
+    float* __restrict__ d_hidden) {
+#pragma clang fp contract(off)
+  __shared__ float red[kGbMaxHc * (kGbThreads / 64)];
+  const int64_t t = blockIdx.x;
+  const int i0 = 4 * threadIdx.x;
+  const float inv_n = 1.0f / (float)n;
+  float sj[kGbMaxHc], gj[kGbMaxHc], rk[kGbMaxHc], rq[kGbMaxHc], rg[kGbMaxHc];
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) {
+    const int jj = min(j, hc - 1);
+    sj[j] = s_in[t * hc + jj];
+    gj[j] = gate_in[t * hc + jj];
+    rk[j] = rstd[(t * hc + jj) * 3 + 0];
+    rq[j] = rstd[(t * hc + jj) * 3 + 1];
+    rg[j] = rstd[(t * hc + jj) * 3 + 2];
+  }
+  const float4 v4 = *(const float4*)(value + t * n + i0);
+  const float val[4] = {v4.x, v4.y, v4.z, v4.w};
+  // round 1: sum(dy nc x) per stream; d_gated without its last term
+  float dg[kGbMaxHc][4], acc[kGbMaxHc];
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) {
+    acc[j] = 0.0f;
+    const int jj = min(j, hc - 1);
+    const int64_t row = (t * hc + jj) * n;
+    const float4 dy4 = *(const float4*)(d_normed + row + i0);
+    const float4 wc4 = *(const float4*)(norm_conv + (int64_t)jj * n + i0);
+    const float4 do4 = *(const float4*)(d_out + row + i0);
+    const float dy[4] = {dy4.x, dy4.y, dy4.z, dy4.w}, wc[4] = {wc4.x, wc4.y, wc4.z, wc4.w};
+    const float dd[4] = {do4.x, do4.y, do4.z, do4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x = val[e] * gj[j];
+      dg[j][e] = dd[e] + rg[j] * (wc[e] * dy[e]);
+      if (j < hc) acc[j] += (dy[e] * wc[e]) * x;
+    }
+  }
+  block_sum4_n(acc, red);
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) {
+    const float coef = ((rg[j] * rg[j]) * rg[j]) * inv_n * acc[j];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dg[j][e] = dg[j][e] - (val[e] * gj[j]) * coef;
+  }
+  if (!detach_value && d_value != nullptr) {
+    float dv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      dv[e] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kGbMaxHc; ++j)
+        if (j < hc) dv[e] += dg[j][e] * gj[j];
+    }
+    *(float4*)(d_value + t * n + i0) = make_float4(dv[0], dv[1], dv[2], dv[3]);
+  }
+  // round 2: d_gate per stream -> d_s
+  float ds[kGbMaxHc];
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) ds[j] = 0.0f;
+  if (!detach_gate) {  // uniform
+#pragma unroll
+    for (int j = 0; j < kGbMaxHc; ++j) {
+      acc[j] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (j < hc) acc[j] += dg[j][e] * val[e];
+    }
+    block_sum4_n(acc, red);
+#pragma unroll
+    for (int j = 0; j < kGbMaxHc; ++j) {
+      const float du = acc[j] * (gj[j] * (1.0f - gj[j]));
+      const float as = fabsf(sj[j]);
+      ds[j] = as > 1e-6f ? du * (0.5f / sqrtf(as)) : 0.0f;
+    }
+  }
+  // the key and query norms' backward, and the hidden state's gradient
+#pragma unroll
+  for (int j = 0; j < kGbMaxHc; ++j) {
+    if (j >= hc) break;
+    const int64_t row = (t * hc + j) * n;
+    const float4 k4 = *(const float4*)(key + row + i0), h4 = *(const float4*)(hidden + row + i0);
+    const float4 wk4 = *(const float4*)(norm_key + (int64_t)j * n + i0);
+    const float4 wq4 = *(const float4*)(norm_query + (int64_t)j * n + i0);
+    const float4 do4 = *(const float4*)(d_out + row + i0);
+    const float k[4] = {k4.x, k4.y, k4.z, k4.w}, h[4] = {h4.x, h4.y, h4.z, h4.w};
+    const float wk[4] = {wk4.x, wk4.y, wk4.z, wk4.w}, wq[4] = {wq4.x, wq4.y, wq4.z, wq4.w};
+    const float dd[4] = {do4.x, do4.y, do4.z, do4.w};
+    const float ck = ((rk[j] * rk[j]) * ds[j]) * sj[j] * inv_n;
+    const float cq = ((rq[j] * rq[j]) * ds[j]) * sj[j] * inv_n;
+    const float dsn = ds[j] * inv_sqrt_n;
+    float dk[4], dh[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float kn = (k[e] * rk[j]) * wk[e];
+      const float qn = (h[e] * rq[j]) * wq[e];
+      dk[e] = (rk[j] * wk[e]) * (dsn * qn) - k[e] * ck;
+      dh[e] = dd[e] + ((rq[j] * wq[e]) * (dsn * kn) - h[e] * cq);
+    }
+    if (d_key != nullptr) *(float4*)(d_key + row + i0) = make_float4(dk[0], dk[1], dk[2], dk[3]);
+    if (d_hidden != nullptr) *(float4*)(d_hidden + row + i0) = make_float4(dh[0], dh[1], dh[2], dh[3]);
+  }
+}
+
 template <int MODE, bool SHARED>
 static void launch_conv(dim3 grid, hipStream_t st, const float* full, int64_t hist_rows, int64_t n_pos, int hc, int n,
                         const float* conv_w, int taps, int dil, const float* hidden, const float* value,
@@ -575,10 +708,21 @@ int eg_ple_gate_backward(const float* key, const float* value, const float* hidd
                               d_out && d_normed),
                "NULL argument");
   if (n_pos == 0) return EG_OK;
-  hipLaunchKernelGGL(ple_gate_bwd_kernel, dim3((unsigned)n_pos), dim3(kGbThreads), 0, (hipStream_t)stream, key, value,
-                     hidden, norm_key, norm_query, norm_conv, s, gate, rstd, d_out, d_normed, hc, n_embd,
-                     (float)(1.0 / sqrt((double)n_embd)), detach_value, detach_gate, detach_gate ? nullptr : d_key,
-                     detach_value ? nullptr : d_value, d_hidden);
+  // the float4 form needs 16-byte aligned rows of whole wavefronts of float4
+  const bool vec = n_embd % 256 == 0 &&
+                   ((uintptr_t)key | (uintptr_t)value | (uintptr_t)hidden | (uintptr_t)norm_key |
+                    (uintptr_t)norm_query | (uintptr_t)norm_conv | (uintptr_t)d_out | (uintptr_t)d_normed |
+                    (uintptr_t)d_key | (uintptr_t)d_value | (uintptr_t)d_hidden) % 16 == 0;
+  if (vec)
+    hipLaunchKernelGGL(ple_gate_bwd_vec_kernel, dim3((unsigned)n_pos), dim3(n_embd / 4), 0, (hipStream_t)stream, key,
+                       value, hidden, norm_key, norm_query, norm_conv, s, gate, rstd, d_out, d_normed, hc, n_embd,
+                       (float)(1.0 / sqrt((double)n_embd)), detach_value, detach_gate, detach_gate ? nullptr : d_key,
+                       detach_value ? nullptr : d_value, d_hidden);
+  else
+    hipLaunchKernelGGL(ple_gate_bwd_kernel, dim3((unsigned)n_pos), dim3(kGbThreads), 0, (hipStream_t)stream, key,
+                       value, hidden, norm_key, norm_query, norm_conv, s, gate, rstd, d_out, d_normed, hc, n_embd,
+                       (float)(1.0 / sqrt((double)n_embd)), detach_value, detach_gate, detach_gate ? nullptr : d_key,
+                       detach_value ? nullptr : d_value, d_hidden);
   return launch_status("ple_gate_bwd_kernel");
 }
 
