@@ -336,7 +336,8 @@ int eg_ple_gate_backward(const float* key, const float* value, const float* hidd
 /* Per-stream RMS norm: out[r, j, :] = x[r, j, :] / sqrt(mean(x[r, j, :]^2) + eps)
  * * weight[j, :], x and out f32 [n_rows, hc, n_embd], weight f32 [hc, n_embd]
  * (PleReplica._rmsnorm_per_stream, engraft/lens.py:282-287; the reductions of
- * eg_ple_gate, so applied to value*gate it gives eg_ple_gate's normed). */
+ * eg_ple_gate, so applied to value*gate it gives eg_ple_gate's normed bit for
+ * bit when both calls' pointers are 16-byte aligned, or both are not). */
 int eg_ple_rms(const float* x, int64_t n_rows, int32_t hc, int32_t n_embd, const float* weight, float eps,
                float* out, void* stream);
 
