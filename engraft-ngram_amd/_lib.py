@@ -59,6 +59,8 @@ class EgOverlay(ctypes.Structure):
         ("ids", c_void_p),
         ("index", c_void_p),
         ("rows", EgTable),
+        ("bitmap", c_void_p),
+        ("n_bits", c_int64),
     ]
 
 

@@ -365,6 +365,23 @@ __device__ inline float load_value_rt(const TableDev& t, int64_t row, int col) {
 }
 
 // Index of `key` in the sorted array ids[0..n), or -1.
+// Index of row in the sorted ids behind an eg_build_id_bitmap rank bitmap
+// (fine words [0, nw), ranks [nw, 2 nw), coarse words from 2 nw), or -1: the
+// coarse bit of the row's 32-row word settles most misses, then the fine bit,
+// then rank + popcount of the word's lower bits.
+__device__ inline int64_t bitmap_find(const uint32_t* __restrict__ bm, int64_t n_bits, int32_t row) {
+  const int64_t nw = (n_bits + 31) >> 5;
+  const bool in = (int64_t)(uint32_t)row < n_bits;
+  const uint32_t w = in ? ((uint32_t)row >> 5) : 0u;
+  const uint32_t coarse = bm[2 * nw + (w >> 5)];
+  int64_t k = -1;
+  if (in && ((coarse >> (w & 31u)) & 1u)) {
+    const uint32_t word = bm[w], below = word & ((1u << ((uint32_t)row & 31u)) - 1u);
+    if ((word >> ((uint32_t)row & 31u)) & 1u) k = (int64_t)bm[nw + w] + __popc(below);
+  }
+  return k;
+}
+
 __device__ inline int64_t sorted_find(const int32_t* __restrict__ ids, int64_t n, int32_t key) {
   int64_t lo = 0, hi = n;
   while (lo < hi) {

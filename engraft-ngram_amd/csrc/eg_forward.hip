@@ -118,20 +118,7 @@ __global__ __launch_bounds__(256) void scan_kernel(const LayerHash L, const int6
   uint64_t ctx[EG_MAX_NGRAM];
   build_ctx(L, tokens, p, 0, ctx);
   const int32_t row = head_row(L, hh, ctx, true);
-  int64_t k;
-  if (bitmap != nullptr) {  // uniform
-    const int64_t nw = (n_bits + 31) >> 5;
-    const bool in = (int64_t)(uint32_t)row < n_bits;
-    const uint32_t w = in ? ((uint32_t)row >> 5) : 0u;
-    const uint32_t coarse = bitmap[2 * nw + (w >> 5)];
-    k = -1;
-    if (in && ((coarse >> (w & 31u)) & 1u)) {
-      const uint32_t word = bitmap[w], below = word & ((1u << ((uint32_t)row & 31u)) - 1u);
-      if ((word >> ((uint32_t)row & 31u)) & 1u) k = (int64_t)bitmap[nw + w] + __popc(below);
-    }
-  } else {
-    k = sorted_find(ids, n_ids, row);
-  }
+  const int64_t k = bitmap != nullptr ? bitmap_find(bitmap, n_bits, row) : sorted_find(ids, n_ids, row);
   const bool hit = h < L.n_heads && k >= 0;
   if (hit) atomicAdd(&counts[k], 1ull);
   const float d = hit ? dnorm[k] : 0.0f;
@@ -163,6 +150,8 @@ struct OverlayDev {
   const int32_t* index;
   int64_t n;
   TableDev rows;
+  const uint32_t* bitmap;  // optional rank bitmap of ids (eg_build_id_bitmap)
+  int64_t n_bits;
 };
 
 struct FwdArgs {
@@ -281,7 +270,7 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
       if (a.slot_var != nullptr) {
         ovk = a.slot_var[p * H + hh];
       } else if (ov.n > 0) {
-        const int64_t k = sorted_find(ov.ids, ov.n, rid[l]);
+        const int64_t k = ov.bitmap ? bitmap_find(ov.bitmap, ov.n_bits, rid[l]) : sorted_find(ov.ids, ov.n, rid[l]);
         if (k >= 0) ovk = ov.index ? ov.index[k] : (int32_t)k;
       }
     }
@@ -488,9 +477,13 @@ static int fill_overlay(const eg_overlay* o, const TableDev& base, OverlayDev* o
   EG_CHECK_ARG(o->rows.dim == base.dim, "overlay dim %d != table dim %d", o->rows.dim, base.dim);
   EG_CHECK_ARG(o->index != nullptr || o->rows.n_rows >= o->n, "overlay: %lld ids but %lld rows",
                (long long)o->n, (long long)o->rows.n_rows);
+  EG_CHECK_ARG(o->bitmap == nullptr || (o->n_bits >= 1 && o->n_bits <= (1LL << 31)),
+               "overlay: bitmap with n_bits=%lld", (long long)o->n_bits);
   out->ids = o->ids;
   out->index = o->index;
   out->n = o->n;
+  out->bitmap = o->bitmap;
+  out->n_bits = o->n_bits;
   return EG_OK;
 }
 

@@ -7,7 +7,9 @@ reference's overlay substitution (``Replica.ple_true_emb(tokens, t, overlay)``,
 ``DeviceOverlay`` holds a sorted, unique int32 id array plus the replacement
 rows (fp32 as in ``.pleo`` files, or block-quantised like the base table) in
 HBM; the forward kernels binary-search every slot's row id in it and read the
-replacement instead of the base row.
+replacement instead of the base row.  ``with_bitmap(n_rows)`` adds the
+two-level rank bitmap of the ids (``eg_build_id_bitmap``, about n_rows / 4
+bytes), with which a lookup costs one or two probes instead of the search.
 """
 from __future__ import annotations
 
@@ -40,6 +42,22 @@ class DeviceOverlay:
         self.ids = ids
         self.rows = rows
         self.index = index
+        self.bitmap = None
+        self.n_bits = 0
+
+    def with_bitmap(self, n_rows: int) -> "DeviceOverlay":
+        """Builds the rank bitmap of the ids over ``n_rows`` global rows (every
+        row id the table can produce: its ``n_rows``) and returns self; lookups
+        then resolve through it, with the same results."""
+        n_rows = int(n_rows)
+        if not 1 <= n_rows <= (1 << 31):
+            raise ValueError(f"n_rows={n_rows} out of range")
+        nw = (n_rows + 31) // 32
+        bm = torch.empty(2 * nw + (nw + 31) // 32, dtype=torch.int32, device=self.ids.device)
+        _lib.call("eg_build_id_bitmap", _lib.ptr(self.ids), self.n, _lib.ptr(bm), n_rows,
+                  _lib.stream_ptr(self.ids.device))
+        self.bitmap, self.n_bits = bm, n_rows
+        return self
 
     @property
     def n(self) -> int:
@@ -54,6 +72,8 @@ class DeviceOverlay:
         o.ids = _lib.ptr(self.ids)
         o.index = _lib.ptr(self.index)
         o.rows = self.rows.c_table()
+        o.bitmap = _lib.ptr(self.bitmap)
+        o.n_bits = self.n_bits
         return o
 
     # ---- construction ----------------------------------------------------------------------

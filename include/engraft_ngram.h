@@ -98,10 +98,14 @@ typedef struct eg_table {
  * a slot whose global row equals ids[k] reads row index[k] (or k when index is
  * NULL) of `rows` instead of the base table. */
 typedef struct eg_overlay {
-  int64_t n;            /* 0: no overlay */
-  const int32_t* ids;   /* device, sorted ascending, unique */
-  const int32_t* index; /* device or NULL */
-  eg_table rows;        /* rows.dim must equal the base table's dim */
+  int64_t n;               /* 0: no overlay */
+  const int32_t* ids;      /* device, sorted ascending, unique */
+  const int32_t* index;    /* device or NULL */
+  eg_table rows;           /* rows.dim must equal the base table's dim */
+  const uint32_t* bitmap;  /* device or NULL: eg_build_id_bitmap of ids over n_bits rows
+                              (covering every row id looked up); resolves the lookups
+                              in place of the binary search, same results */
+  int64_t n_bits;
 } eg_overlay;
 
 const char* eg_last_error(void);

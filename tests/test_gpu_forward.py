@@ -252,7 +252,8 @@ def _decode_expect(spec, tok2d, fetch, ov_ids, ov_fetch, res_bits):
 def test_decode_with_overlay_config3_shape(cuda):
     """BASELINE config 3's shape on a 1.6M-row table: 256 sequences x (2 context
     tokens + 1 new), a 500,000-row Q8_0 overlay resolved per id; the decode step
-    equals the oracle and the full forward's last positions."""
+    equals the oracle and the full forward's last positions, by binary search
+    and through the overlay's rank bitmap alike."""
     from engraft_ngram_amd import table as T
     c = CFG3
     spec = synthetic_spec(n_rows=16 * 100_000, seed=61)
@@ -274,6 +275,13 @@ def test_decode_with_overlay_config3_shape(cuda):
     res_full[c["ctx"] - 1::c["ctx"]] = res
     full = tab.forward(torch.from_numpy(tok.reshape(-1)), res_full, overlay=ov, seq_len=c["ctx"])
     assert torch.equal(full[c["ctx"] - 1::c["ctx"]], out)
+    # the overlay's rank bitmap in place of the binary search: the same bits
+    from engraft_ngram_amd.overlay import DeviceOverlay
+    ov_bm = DeviceOverlay(ov.ids, ov.rows).with_bitmap(tab.n_rows)
+    out_bm, rows_bm = T.forward_decode([tab], torch.from_numpy(tok), res, overlays=[ov_bm], return_rows=True)
+    assert torch.equal(out_bm, out) and torch.equal(rows_bm[0], rows[0])
+    full_bm = tab.forward(torch.from_numpy(tok.reshape(-1)), res_full, overlay=ov_bm, seq_len=c["ctx"])
+    assert torch.equal(full_bm, full)
 
 
 def test_decode_config3_full_size(cuda):
@@ -296,7 +304,12 @@ def test_decode_config3_full_size(cuda):
                                        G.bf16_bits(res))
     assert np.array_equal(rows[0].cpu().numpy(), exp_rows)
     G.assert_out_matches(G.bf16_bits(out), exp_out)
-    del tab, ov
+    # with the overlay's rank bitmap (81 MB over the 320M rows): the same bits
+    from engraft_ngram_amd.overlay import DeviceOverlay
+    ov_bm = DeviceOverlay(ov.ids, ov.rows).with_bitmap(c["n_rows"])
+    out_bm = T.forward_decode([tab], torch.from_numpy(tok), res, overlays=[ov_bm])
+    assert torch.equal(out_bm, out)
+    del tab, ov, ov_bm
     torch.cuda.empty_cache()
 
 
