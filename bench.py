@@ -254,6 +254,7 @@ def bench_backward(tab, tokens, steps: int, warmup: int, cpu_s: float = 0.0) -> 
                        "Q8_0 requant, fp32 master/m/v kept"}
     if cpu_s > 0:
         out["cpu_baseline"] = cpu_descent(tab, rows, d_res[0], cpu_s)
+        out["cpu_baseline"]["gpu_speedup"] = out["rows_per_s"] / out["cpu_baseline"]["value"]
     return out
 
 
@@ -507,6 +508,7 @@ def bench_damage_scan(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
         out["cpu_baseline"] = {"value": k * sample.size / el, "unit": "tokens/s", "cores": 1, "kind": "port",
                                "sample": f"first 250,000 tokens of the block x {k} in {el:.1f} s: oracle "
                                          "scan_hits (numpy-uint64 hash, searchsorted, np.add.at)"}
+        out["cpu_baseline"]["gpu_speedup"] = out["tokens_per_s_kernel"] / out["cpu_baseline"]["value"]
     return out
 
 
@@ -580,6 +582,7 @@ def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
                                "kind": "port",
                                "sample": f"first {tc} positions x {k} in {el:.1f} s: oracle ple_forward (torch "
                                          f"fp32 on the CPU, {torch.get_num_threads()} threads)"}
+        out["cpu_baseline"]["gpu_speedup"] = out["positions_per_s"] / out["cpu_baseline"]["value"]
     return out
 
 
@@ -766,6 +769,8 @@ def main() -> None:
         same = bool(torch.equal(cb.pop("result").view(torch.int16), outs[0].cpu().view(torch.int16)))
         cb["matches_gpu_output"] = same
         result["cpu_baseline_literal"] = cb.pop("literal")
+        cb["gpu_speedup"] = result["value"] / cb["value"]
+        result["cpu_baseline_literal"]["gpu_speedup"] = result["value"] / result["cpu_baseline_literal"]["value"]
         result["cpu_baseline"] = cb
         lit = result["cpu_baseline_literal"]
         log(f"cpu baseline, the reference's per-position loop: {lit['value']:.3g} rows/s on 1 thread; "
