@@ -121,6 +121,8 @@ SIGNATURES = {
     "eg_ple_gate_backward": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
                                        c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "eg_ple_gate_backward_planes": (c_int32, [c_void_p] * 11 + [c_int64, c_int32, c_int32, c_int32, c_int32] +
+                                    [c_void_p] * 6),
     "eg_ple_conv": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32,
                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_rms": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, ctypes.c_float, c_void_p, c_void_p]),

@@ -620,13 +620,29 @@ __device__ inline void block_sum4_n(float v[kGbMaxHc], float* red) {
 // ple_gate_bwd_kernel with one float4 per thread: n/4 threads per position
 // (n a multiple of 256, so whole wavefronts), 16-byte loads and stores, the
 // same arithmetic per element.
+// hi = rne(x), lo = rne(x - hi) of 4 values, stored at hi + o, lo + o.
+__device__ inline void store_planes4(const float* x, __bf16* hi, __bf16* lo, int64_t o) {
+  typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+  bf16x4 h, l;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    h[e] = (__bf16)x[e];
+    l[e] = (__bf16)(x[e] - (float)h[e]);
+  }
+  *(bf16x4*)(hi + o) = h;
+  *(bf16x4*)(lo + o) = l;
+}
+
+// PLANES: d_key and d_value are written as their bf16 hi / lo planes (the
+// operands of eg_gemm_bf16x3), d_key_lo / d_value_lo the lo planes.
+template <bool PLANES>
 __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_vec_kernel(
     const float* __restrict__ key, const float* __restrict__ value, const float* __restrict__ hidden,
     const float* __restrict__ norm_key, const float* __restrict__ norm_query, const float* __restrict__ norm_conv,
     const float* __restrict__ s_in, const float* __restrict__ gate_in, const float* __restrict__ rstd,
     const float* __restrict__ d_out, const float* __restrict__ d_normed, int hc, int n, float inv_sqrt_n,
     int detach_value, int detach_gate, float* __restrict__ d_key, float* __restrict__ d_value,
-    float* __restrict__ d_hidden) {
+    float* __restrict__ d_hidden, __bf16* __restrict__ d_key_lo, __bf16* __restrict__ d_value_lo) {
 #pragma clang fp contract(off)
   __shared__ float red[kGbMaxHc * (kGbThreads / 64)];
   const int64_t t = blockIdx.x;
@@ -679,7 +695,8 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_vec_kernel(
       for (int j = 0; j < kGbMaxHc; ++j)
         if (j < hc) dv[e] += dg[j][e] * gj[j];
     }
-    *(float4*)(d_value + t * n + i0) = make_float4(dv[0], dv[1], dv[2], dv[3]);
+    if constexpr (PLANES) store_planes4(dv, (__bf16*)d_value, d_value_lo, t * n + i0);
+    else *(float4*)(d_value + t * n + i0) = make_float4(dv[0], dv[1], dv[2], dv[3]);
   }
   // round 2: d_gate per stream -> d_s
   float ds[kGbMaxHc];
@@ -724,7 +741,10 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_vec_kernel(
       dk[e] = (rk[j] * wk[e]) * (dsn * qn) - k[e] * ck;
       dh[e] = dd[e] + ((rq[j] * wq[e]) * (dsn * kn) - h[e] * cq);
     }
-    if (d_key != nullptr) *(float4*)(d_key + row + i0) = make_float4(dk[0], dk[1], dk[2], dk[3]);
+    if (d_key != nullptr) {
+      if constexpr (PLANES) store_planes4(dk, (__bf16*)d_key, d_key_lo, row + i0);
+      else *(float4*)(d_key + row + i0) = make_float4(dk[0], dk[1], dk[2], dk[3]);
+    }
     if (d_hidden != nullptr) *(float4*)(d_hidden + row + i0) = make_float4(dh[0], dh[1], dh[2], dh[3]);
   }
 }
@@ -878,16 +898,45 @@ int eg_ple_gate_backward(const float* key, const float* value, const float* hidd
                     (uintptr_t)norm_query | (uintptr_t)norm_conv | (uintptr_t)d_out | (uintptr_t)d_normed |
                     (uintptr_t)d_key | (uintptr_t)d_value | (uintptr_t)d_hidden) % 16 == 0;
   if (vec)
-    hipLaunchKernelGGL(ple_gate_bwd_vec_kernel, dim3((unsigned)n_pos), dim3(n_embd / 4), 0, (hipStream_t)stream, key,
-                       value, hidden, norm_key, norm_query, norm_conv, s, gate, rstd, d_out, d_normed, hc, n_embd,
+    hipLaunchKernelGGL(ple_gate_bwd_vec_kernel<false>, dim3((unsigned)n_pos), dim3(n_embd / 4), 0, (hipStream_t)stream,
+                       key, value, hidden, norm_key, norm_query, norm_conv, s, gate, rstd, d_out, d_normed, hc, n_embd,
                        (float)(1.0 / sqrt((double)n_embd)), detach_value, detach_gate, detach_gate ? nullptr : d_key,
-                       detach_value ? nullptr : d_value, d_hidden);
+                       detach_value ? nullptr : d_value, d_hidden, nullptr, nullptr);
   else
     hipLaunchKernelGGL(ple_gate_bwd_kernel, dim3((unsigned)n_pos), dim3(kGbThreads), 0, (hipStream_t)stream, key,
                        value, hidden, norm_key, norm_query, norm_conv, s, gate, rstd, d_out, d_normed, hc, n_embd,
                        (float)(1.0 / sqrt((double)n_embd)), detach_value, detach_gate, detach_gate ? nullptr : d_key,
                        detach_value ? nullptr : d_value, d_hidden);
   return launch_status("ple_gate_bwd_kernel");
+}
+
+int eg_ple_gate_backward_planes(const float* key, const float* value, const float* hidden, const float* norm_key,
+                                const float* norm_query, const float* norm_conv, const float* s, const float* gate,
+                                const float* rstd, const float* d_out, const float* d_normed, int64_t n_pos,
+                                int32_t hc, int32_t n_embd, int32_t detach_value, int32_t detach_gate,
+                                void* d_key_hi, void* d_key_lo, void* d_value_hi, void* d_value_lo, float* d_hidden,
+                                void* stream) {
+  EG_CHECK_ARG(n_pos >= 0 && n_pos < (1LL << 31), "n_pos=%lld", (long long)n_pos);
+  if (hc < 1 || hc > kGbMaxHc || n_embd < 256 || n_embd > kGbThreads * 4 || n_embd % 256 != 0)
+    return set_error(EG_ERR_UNSUPPORTED, "gate backward to planes for hc=%d n_embd=%d (built: hc <= %d, n_embd a "
+                     "multiple of 256 up to %d)", hc, n_embd, kGbMaxHc, kGbThreads * 4);
+  EG_CHECK_ARG(n_pos == 0 || (key && value && hidden && norm_key && norm_query && norm_conv && s && gate && rstd &&
+                              d_out && d_normed),
+               "NULL argument");
+  EG_CHECK_ARG((d_key_hi == nullptr) == (d_key_lo == nullptr) && (d_value_hi == nullptr) == (d_value_lo == nullptr),
+               "hi and lo planes go together");
+  const bool aligned = ((uintptr_t)key | (uintptr_t)value | (uintptr_t)hidden | (uintptr_t)norm_key |
+                        (uintptr_t)norm_query | (uintptr_t)norm_conv | (uintptr_t)d_out | (uintptr_t)d_normed |
+                        (uintptr_t)d_hidden) % 16 == 0 &&
+                       ((uintptr_t)d_key_hi | (uintptr_t)d_key_lo | (uintptr_t)d_value_hi | (uintptr_t)d_value_lo) % 8 == 0;
+  EG_CHECK_ARG(aligned, "pointers must be 16-byte aligned (planes 8-byte)");
+  if (n_pos == 0) return EG_OK;
+  hipLaunchKernelGGL(ple_gate_bwd_vec_kernel<true>, dim3((unsigned)n_pos), dim3(n_embd / 4), 0, (hipStream_t)stream,
+                     key, value, hidden, norm_key, norm_query, norm_conv, s, gate, rstd, d_out, d_normed, hc, n_embd,
+                     (float)(1.0 / sqrt((double)n_embd)), detach_value, detach_gate,
+                     detach_gate ? nullptr : (float*)d_key_hi, detach_value ? nullptr : (float*)d_value_hi, d_hidden,
+                     (__bf16*)d_key_lo, (__bf16*)d_value_lo);
+  return launch_status("ple_gate_bwd_vec_kernel");
 }
 
 }  // extern "C"

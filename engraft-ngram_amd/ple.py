@@ -123,6 +123,16 @@ class SplitPlanes:
                   _lib.ptr(self.lo), _lib.stream_ptr(x.device))
 
 
+def _empty_planes(rows: int, cols: int, device) -> "SplitPlanes":
+    """Uninitialised planes of a [rows, cols] matrix, cols a multiple of 32 (no
+    padding), for a kernel that writes them directly."""
+    p = SplitPlanes.__new__(SplitPlanes)
+    p.rows, p.cols, p.kp = rows, cols, cols
+    p.hi = torch.empty((rows, cols), dtype=torch.bfloat16, device=device)
+    p.lo = torch.empty_like(p.hi)
+    return p
+
+
 class _PlaneCache:
     """Split planes of weights, kept between steps: an entry is used only for
     the same tensor object (weak reference) at the same version counter."""
@@ -319,9 +329,30 @@ class _PleFn(torch.autograd.Function):
         d_full = torch.empty((h0 + t_len, c_dim), **f32)
         _lib.call("eg_ple_conv_backward", _lib.ptr(full), h0, t_len, hc, n, _lib.ptr(conv32), conv32.shape[1],
                   int(dil), _lib.ptr(pre), _lib.ptr(d_out32), _lib.ptr(d_tail), tail, _lib.ptr(d_full), st)
+        d_hidden = torch.empty((t_len, hc, n), **f32) if need_hidden else None
+        if ctx.gemm == "bf16x3" and n % 256 == 0:
+            # d_key and d_value straight into the bf16 planes gemm_x3 takes
+            pk = _empty_planes(t_len, c_dim, dev) if (need_emb and not detach_gate) else None
+            pv = _empty_planes(t_len, n, dev) if (need_emb and not detach_value) else None
+            if pk is not None or pv is not None or d_hidden is not None:
+                _lib.call("eg_ple_gate_backward_planes", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden32),
+                          _lib.ptr(nk32), _lib.ptr(nq32), _lib.ptr(nc32), _lib.ptr(s), _lib.ptr(gate), _lib.ptr(rstd),
+                          _lib.ptr(d_out32), _lib.ptr(d_full[h0:]), t_len, hc, n, int(bool(detach_value)),
+                          int(bool(detach_gate)), _lib.ptr(pk.hi if pk else None), _lib.ptr(pk.lo if pk else None),
+                          _lib.ptr(pv.hi if pv else None), _lib.ptr(pv.lo if pv else None), _lib.ptr(d_hidden), st)
+            d_emb = None
+            if need_emb:
+                parts = [(d, _WT.get(w)) for d, w in ((pk, wk32), (pv, wv32)) if d is not None]
+                if parts:
+                    d_emb = gemm_x3(*[x for part in parts for x in part], cache_b=True)
+                else:
+                    d_emb = torch.zeros((t_len, n), **f32)
+                d_emb = d_emb.to(emb_dt)
+            d_hist_in = d_full[:h0].reshape(h0, hc, n).to(hist_dt) if need_hist else None
+            return (d_emb, d_hidden.to(hidden_dt) if d_hidden is not None else None, None, None, None, None, None,
+                    None, d_hist_in, None, None, None, None, None)
         d_key = torch.empty((t_len, c_dim), **f32) if (need_emb and not detach_gate) else None
         d_value = torch.empty((t_len, n), **f32) if (need_emb and not detach_value) else None
-        d_hidden = torch.empty((t_len, hc, n), **f32) if need_hidden else None
         if d_key is not None or d_value is not None or d_hidden is not None:
             _lib.call("eg_ple_gate_backward", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden32), _lib.ptr(nk32),
                       _lib.ptr(nq32), _lib.ptr(nc32), _lib.ptr(s), _lib.ptr(gate), _lib.ptr(rstd), _lib.ptr(d_out32),

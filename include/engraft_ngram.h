@@ -337,6 +337,18 @@ int eg_ple_gate_backward(const float* key, const float* value, const float* hidd
                          int32_t hc, int32_t n_embd, int32_t detach_value, int32_t detach_gate,
                          float* d_key, float* d_value, float* d_hidden, void* stream);
 
+/* eg_ple_gate_backward with d_key and d_value written as their bf16 hi / lo
+ * planes (hi = rne(x), lo = rne(x - hi); row strides hc*n_embd and n_embd,
+ * the layout of eg_split_bf16's output), ready as eg_gemm_bf16x3 operands:
+ * no fp32 gradient is stored and split again.  n_embd a multiple of 256;
+ * NULL planes skip that gradient. */
+int eg_ple_gate_backward_planes(const float* key, const float* value, const float* hidden,
+                                const float* norm_key, const float* norm_query, const float* norm_conv,
+                                const float* s, const float* gate, const float* rstd, const float* d_out,
+                                const float* d_normed, int64_t n_pos, int32_t hc, int32_t n_embd,
+                                int32_t detach_value, int32_t detach_gate, void* d_key_hi, void* d_key_lo,
+                                void* d_value_hi, void* d_value_lo, float* d_hidden, void* stream);
+
 /* Per-stream RMS norm: out[r, j, :] = x[r, j, :] / sqrt(mean(x[r, j, :]^2) + eps)
  * * weight[j, :], x and out f32 [n_rows, hc, n_embd], weight f32 [hc, n_embd]
  * (PleReplica._rmsnorm_per_stream, engraft/lens.py:282-287; the reductions of

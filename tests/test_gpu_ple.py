@@ -159,7 +159,8 @@ def test_ple_native_backward_against_oracle(cuda, dv, dg, gemm):
         ((out_d * r.to(cuda)).sum() + (nh_d * rh.to(cuda)).sum()).backward()
     finally:
         _lib.call = real_call
-    assert "eg_ple_conv_backward" in called and "eg_ple_gate_backward" in called
+    gate_bwd = "eg_ple_gate_backward_planes" if gemm == "bf16x3" else "eg_ple_gate_backward"
+    assert "eg_ple_conv_backward" in called and gate_bwd in called  # bf16x3: d_key, d_value written as planes
     assert (called.count("eg_gemm_bf16x3") == 3) == (gemm == "bf16x3")  # key, value, then d_emb
     for name, got, exp in zip(("emb", "hidden", "hist"), (x.grad for x in leaves_d), (x.grad for x in leaves_c)):
         scale = exp.abs().max().item()
