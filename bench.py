@@ -512,6 +512,80 @@ def bench_damage_scan(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     return out
 
 
+def bench_overlay_emb(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.0) -> dict:
+    """The differentiable overlay of the descent loop (a8, OverlayEmb,
+    engraft/replica/seq.py:237-444): one 2,048-token Zipf sequence on the
+    config-1 table, 14,032 of its rows as fp32 variables (the size of the
+    reference's Quail s0b overlay, docs/formats.md:120-124); a step is build()
+    (the cached plan's gather with the variables substituted) plus the backward
+    into the variables.  CPU: the oracle's build + slot-ordered scatter on the
+    first 256 positions."""
+    import numpy as np
+    import torch
+
+    from engraft_ngram_amd import synthetic as S
+    from engraft_ngram_amd.seq import OverlayEmb
+
+    dev = tab.device
+    t_len, n_var = 2048, 14_032
+    tokens = S.zipf_tokens(SCAN_SEED + 2, t_len, VOCAB)
+    rows = tab.rows(torch.from_numpy(tokens).to(dev), seq_len=t_len).cpu().numpy()
+    uniq = np.unique(rows.reshape(-1))
+    pick = np.sort(np.random.default_rng(SCAN_SEED + 3).choice(uniq, size=min(n_var, uniq.size), replace=False))
+    row_map = {int(g): i for i, g in enumerate(pick)}
+    rv = tab.gather(torch.from_numpy(pick.astype(np.int32)).to(dev).reshape(-1, 1)).float()
+    rv = rv.reshape(pick.size, -1).contiguous().requires_grad_(True)
+    oe = OverlayEmb(tab, tokens.tolist(), rv, row_map)
+    g = torch.randn((t_len, tab.n_heads * DIM), generator=torch.Generator(device=dev).manual_seed(5), device=dev)
+
+    def step():
+        rv.grad = None
+        emb = oe.build(t_len)
+        (emb.float() * g).sum().backward()
+
+    step()  # plans the sequence once, as the reference's overlay_cache does
+    for _ in range(20):
+        step()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        step()
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) / steps * 1e3
+    hits = int(oe.n_id_hits)
+    out = {"workload": "OverlayEmb: 2,048-token sequence, config-1 table, 14,032 fp32 variable rows; build + backward",
+           "us_per_step": us, "positions_per_s": t_len / (us * 1e-6), "slots_replaced": hits}
+    if cpu_s > 0 and hp is not None:
+        from oracle import backward as OB
+        from oracle import overlay_emb as OE
+        spec = oracle_spec(hp)
+        n_c = 256
+        rvc = rv.detach().cpu().numpy()
+        fetch = lambda r: tab.gather(torch.as_tensor(np.asarray(r, dtype=np.int32), device=dev).reshape(-1, 1)).float().cpu().numpy().reshape(len(r), -1)
+        gc = g[:n_c].cpu().numpy()
+
+        # the plan (the per-position re-hash and base gather) once, as the reference caches it
+        _, base, it, ih, ir, _, _ = OE.build_plan(spec, tokens[:n_c].tolist(), row_map, n_c, 0, None, fetch)
+        keys = OE.slot_keys(it, ih, ir, n_c, tab.n_heads)
+        it, ih, ir = np.array(it), np.array(ih), np.array(ir)
+
+        def cpu_step():
+            emb = base.copy()  # seq.py:428-444: base.index_put((idx_t, idx_h), rows_var[idx_r])
+            if it.size:
+                emb[it, ih] = rvc[ir]
+            OB.scatter_grad_keys(gc, keys, tab.n_heads, pick.size)
+
+        k, el = repeat_for(cpu_step, cpu_s)
+        out["cpu_baseline"] = {"value": k * n_c / el, "unit": "positions/s", "cores": 1, "kind": "port",
+                               "sample": f"first {n_c} positions x {k} in {el:.1f} s, plan cached as the reference "
+                                         "caches it: the substitution into the planned base gather + the "
+                                         "slot-ordered scatter of the gradient, numpy",
+                               "gpu_speedup": out["positions_per_s"] / (k * n_c / el)}
+    return out
+
+
 def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
     """The PLE block consuming the rows (engraft/replica/layers.py:565-626) at
     the real model's dimensions: 2048 positions, 4 hyper-connection streams,
@@ -747,6 +821,11 @@ def main() -> None:
         log(f"damage scan: {ds['us_per_block_kernel']:.0f} us per 8M-token block on the device "
             f"({ds['lookups_per_s_kernel'] / 1e9:.1f} G lookups/s), {ds['s_per_block_end_to_end'] * 1e3:.0f} ms end "
             f"to end")
+        oe = bench_overlay_emb(tab, 100, hp, cpu_leg_s)
+        result["overlay_emb"] = oe
+        log_cpu_leg("overlay_emb", oe)
+        log(f"OverlayEmb (a8): {oe['us_per_step']:.0f} us per build + backward of a 2,048-token sequence "
+            f"({oe['slots_replaced']} slots replaced)")
         rf = bench_real_format(max(1, args.steps // 4), max(1, args.warmup))
         result["forward_real_format"] = rf
         log(f"forward (real IQ4_NL format): {rf['us_per_launch']:.1f} us/launch, {rf['gb_per_s']:.0f} GB/s "
