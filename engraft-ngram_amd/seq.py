@@ -244,8 +244,8 @@ class OverlayEmb:
         if self.overlay_cache is not None and self._seg_ranges is not None and start == 0:
             plan = self._plan_fragments(n_positions)
         else:
-            seg_key = None if self._seg_starts is None else self._seg_starts[:n_positions].tobytes()
-            key = (tuple(self._tok[:n_positions]), start, n_positions, seg_key)
+            # the tokens and segments are fixed per instance: the range names the plan
+            key = (start, n_positions)
             plan = self._plans.get(key)
             if plan is None:
                 plan = self._plan_tokens(self._tok, self._seg_starts, start, n_positions)
