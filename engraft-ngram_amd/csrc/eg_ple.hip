@@ -501,7 +501,7 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_kernel(
 #pragma unroll
   for (int m = 0; m < kGbMaxPer; ++m)
     if (m < per) val[m] = value[t * n + min(tid + m * kGbThreads, n - 1)];
-  // round 1: sum(dy nc x) per stream; d_gated without its last term
+  // first reduction: sum(dy nc x) per stream; d_gated without its last term
   float dg[kGbMaxHc][kGbMaxPer], acc[kGbMaxHc];
 #pragma unroll
   for (int j = 0; j < kGbMaxHc; ++j) {
@@ -542,7 +542,7 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_kernel(
       }
     }
   }
-  // round 2: d_gate per stream -> d_s
+  // second reduction: d_gate per stream -> d_s
   float ds[kGbMaxHc];
 #pragma unroll
   for (int j = 0; j < kGbMaxHc; ++j) ds[j] = 0.0f;
@@ -660,7 +660,7 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_vec_kernel(
   }
   const float4 v4 = *(const float4*)(value + t * n + i0);
   const float val[4] = {v4.x, v4.y, v4.z, v4.w};
-  // round 1: sum(dy nc x) per stream; d_gated without its last term
+  // first reduction: sum(dy nc x) per stream; d_gated without its last term
   float dg[kGbMaxHc][4], acc[kGbMaxHc];
 #pragma unroll
   for (int j = 0; j < kGbMaxHc; ++j) {
@@ -698,7 +698,7 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_vec_kernel(
     if constexpr (PLANES) store_planes4(dv, (__bf16*)d_value, d_value_lo, t * n + i0);
     else *(float4*)(d_value + t * n + i0) = make_float4(dv[0], dv[1], dv[2], dv[3]);
   }
-  // round 2: d_gate per stream -> d_s
+  // second reduction: d_gate per stream -> d_s
   float ds[kGbMaxHc];
 #pragma unroll
   for (int j = 0; j < kGbMaxHc; ++j) ds[j] = 0.0f;
