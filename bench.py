@@ -476,7 +476,7 @@ def bench_damage_scan(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     _lib.call("eg_build_id_bitmap", _lib.ptr(ids_d), ids.size, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(dev))
 
     def timed(bm) -> float:
-        args = (ctypes.byref(spec), _lib.ptr(tok), n, 0, _lib.ptr(ids_d), ids.size, bm, n_bits, _lib.ptr(dn_d),
+        args = (ctypes.byref(spec), _lib.ptr(tok), 8, n, 0, _lib.ptr(ids_d), ids.size, bm, n_bits, _lib.ptr(dn_d),
                 _lib.ptr(n_hit), _lib.ptr(dmax), _lib.ptr(dsum), _lib.ptr(counts), _lib.stream_ptr(dev))
         for _ in range(3):
             _lib.call("eg_scan_overlay", *args)
@@ -495,11 +495,18 @@ def bench_damage_scan(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     t0 = time.perf_counter()
     res = damage.scan_hits(tokens, tab, ids, dnorm)
     wall = time.perf_counter() - t0
+    tokens32 = tokens.astype(np.int32)  # a tokenized corpus file's int32 ids
+    damage.scan_hits(tokens32[:100_000], tab, ids, dnorm)
+    t0 = time.perf_counter()
+    res32 = damage.scan_hits(tokens32, tab, ids, dnorm)
+    wall32 = time.perf_counter() - t0
+    assert np.array_equal(res32["pos"], res["pos"]) and np.array_equal(res32["read_count"], res["read_count"])
     lookups = n * tab.n_heads
     out = {"workload": "damage scan: 8,000,000 Zipf tokens x 16 rows against 500,000 sorted overlay rows",
            "us_per_block_kernel": us, "us_per_block_kernel_search_only": us_search,
            "tokens_per_s_kernel": n / (us * 1e-6), "lookups_per_s_kernel": lookups / (us * 1e-6),
-           "s_per_block_end_to_end": wall, "hit_positions": int(res["pos"].size)}
+           "s_per_block_end_to_end": wall, "s_per_block_end_to_end_int32_tokens": wall32,
+           "hit_positions": int(res["pos"].size)}
     if cpu_s > 0 and hp is not None:
         from oracle import damage as OD
         spec = oracle_spec(hp)
@@ -819,8 +826,8 @@ def main() -> None:
         result["damage_scan"] = ds
         log_cpu_leg("damage_scan", ds)
         log(f"damage scan: {ds['us_per_block_kernel']:.0f} us per 8M-token block on the device "
-            f"({ds['lookups_per_s_kernel'] / 1e9:.1f} G lookups/s), {ds['s_per_block_end_to_end'] * 1e3:.0f} ms end "
-            f"to end")
+            f"({ds['lookups_per_s_kernel'] / 1e9:.1f} G lookups/s), {ds['s_per_block_end_to_end'] * 1e3:.1f} ms end "
+            f"to end ({ds['s_per_block_end_to_end_int32_tokens'] * 1e3:.1f} ms from int32 tokens)")
         oe = bench_overlay_emb(tab, 100, hp, cpu_leg_s)
         result["overlay_emb"] = oe
         log_cpu_leg("overlay_emb", oe)

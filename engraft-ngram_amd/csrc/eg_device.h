@@ -50,7 +50,8 @@ __host__ __device__ inline uint32_t fastmod_u64(uint64_t x, uint32_t p, uint64_t
 // their use lets a kernel issue them before its bulk loads: vmcnt retires
 // vector memory operations in order, so a wait for the tokens then does not
 // wait for the bulk data.
-__device__ inline void load_ctx_tokens(const int64_t* __restrict__ tokens, int64_t p, int ngram_size,
+template <typename TOK>
+__device__ inline void load_ctx_tokens(const TOK* __restrict__ tokens, int64_t p, int ngram_size,
                                        uint64_t raw[EG_MAX_NGRAM]) {
 #pragma unroll
   for (int s = 0; s < EG_MAX_NGRAM; ++s) {
@@ -84,7 +85,8 @@ __device__ inline void ctx_from(const LayerHash& L, const uint64_t raw[EG_MAX_NG
   }
 }
 
-__device__ inline void build_ctx(const LayerHash& L, const int64_t* __restrict__ tokens, int64_t p, int64_t seg0,
+template <typename TOK>
+__device__ inline void build_ctx(const LayerHash& L, const TOK* __restrict__ tokens, int64_t p, int64_t seg0,
                                  uint64_t ctx[EG_MAX_NGRAM]) {
   uint64_t raw[EG_MAX_NGRAM];
   load_ctx_tokens(tokens, p, L.ngram_size, raw);

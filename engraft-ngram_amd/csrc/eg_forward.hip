@@ -103,8 +103,8 @@ __global__ __launch_bounds__(256) void hash_kernel(const LayerHash L, const int6
 // settle most misses; only rows in a nonempty 32-row group probe the fine word
 // (the 40 MB level, from the Infinity Cache) -- in place of the ~19 dependent
 // loads of the binary search.
-template <int G>
-__global__ __launch_bounds__(256) void scan_kernel(const LayerHash L, const int64_t* __restrict__ tokens, int64_t n,
+template <int G, typename TOK>
+__global__ __launch_bounds__(256) void scan_kernel(const LayerHash L, const TOK* __restrict__ tokens, int64_t n,
                                                    int64_t start, const int32_t* __restrict__ ids, int64_t n_ids,
                                                    const uint32_t* __restrict__ bitmap, int64_t n_bits,
                                                    const float* __restrict__ dnorm, int32_t* __restrict__ n_hit,
@@ -545,9 +545,10 @@ int eg_build_id_bitmap(const int32_t* ids, int64_t n_ids, uint32_t* bitmap, int6
   return launch_status("bitmap kernels");
 }
 
-int eg_scan_overlay(const eg_hash_spec* spec, const int64_t* tokens, int64_t n_tokens, int64_t start,
-                    const int32_t* ids, int64_t n_ids, const uint32_t* bitmap, int64_t n_bits, const float* dnorm,
-                    int32_t* n_hit, float* dnorm_max, float* dnorm_sum, int64_t* read_counts, void* stream) {
+int eg_scan_overlay(const eg_hash_spec* spec, const void* tokens, int32_t token_bytes, int64_t n_tokens,
+                    int64_t start, const int32_t* ids, int64_t n_ids, const uint32_t* bitmap, int64_t n_bits,
+                    const float* dnorm, int32_t* n_hit, float* dnorm_max, float* dnorm_sum, int64_t* read_counts,
+                    void* stream) {
   LayerHash L;
   int rc = make_layer_hash(spec, &L);
   if (rc != EG_OK) return rc;
@@ -558,17 +559,22 @@ int eg_scan_overlay(const eg_hash_spec* spec, const int64_t* tokens, int64_t n_t
   if (m == 0) return EG_OK;
   EG_CHECK_ARG(tokens && ids && dnorm && n_hit && dnorm_max && dnorm_sum && read_counts, "NULL argument");
   EG_CHECK_ARG(bitmap == nullptr || n_bits >= 1, "n_bits=%lld", (long long)n_bits);
+  EG_CHECK_ARG(token_bytes == 4 || token_bytes == 8, "token_bytes=%d (4: int32, 8: int64)", token_bytes);
   const int G = L.n_heads <= 16 ? 16 : 32;
   const int64_t threads = m * G;
   EG_CHECK_ARG((threads + 255) / 256 < (1LL << 31), "n_tokens=%lld too large for one launch", (long long)n_tokens);
   const dim3 grid((unsigned)((threads + 255) / 256));
   hipStream_t st = (hipStream_t)stream;
-  if (G == 16)
-    hipLaunchKernelGGL(scan_kernel<16>, grid, dim3(256), 0, st, L, tokens, n_tokens, start, ids, n_ids, bitmap, n_bits,
-                       dnorm, n_hit, dnorm_max, dnorm_sum, (unsigned long long*)read_counts);
-  else
-    hipLaunchKernelGGL(scan_kernel<32>, grid, dim3(256), 0, st, L, tokens, n_tokens, start, ids, n_ids, bitmap, n_bits,
-                       dnorm, n_hit, dnorm_max, dnorm_sum, (unsigned long long*)read_counts);
+  unsigned long long* rc64 = (unsigned long long*)read_counts;
+#define EG_SCAN(GG, T)                                                                                             \
+  hipLaunchKernelGGL((scan_kernel<GG, T>), grid, dim3(256), 0, st, L, (const T*)tokens, n_tokens, start, ids, n_ids, \
+                     bitmap, n_bits, dnorm, n_hit, dnorm_max, dnorm_sum, rc64)
+  if (token_bytes == 8) {
+    if (G == 16) EG_SCAN(16, int64_t); else EG_SCAN(32, int64_t);
+  } else {
+    if (G == 16) EG_SCAN(16, int32_t); else EG_SCAN(32, int32_t);
+  }
+#undef EG_SCAN
   return launch_status("scan_kernel");
 }
 

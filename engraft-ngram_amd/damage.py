@@ -102,9 +102,12 @@ def scan_hits(tokens: np.ndarray, table, overlay_sorted: np.ndarray, dnorm_sorte
     bitmap = torch.empty(2 * nw + (nw + 31) // 32, dtype=torch.int32, device=dev)
     if n_ov:
         _lib.call("eg_build_id_bitmap", _lib.ptr(ids), n_ov, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(dev))
+    # int32 token arrays (a tokenized corpus file) go to the device as they are
+    # (4 bytes a token); any other integer type as int64
+    narrow = tokens.dtype == np.int32
     for offset, blk in iter_blocks(tokens, block=block, overlap=hist):
         start_local = 0 if offset == 0 else hist
-        tok = torch.as_tensor(np.asarray(blk, dtype=np.int64)).to(dev)
+        tok = torch.as_tensor(np.ascontiguousarray(blk) if narrow else np.asarray(blk, dtype=np.int64)).to(dev)
         m = tok.numel() - start_local
         if m <= 0 or n_ov == 0:
             continue
@@ -112,7 +115,8 @@ def scan_hits(tokens: np.ndarray, table, overlay_sorted: np.ndarray, dnorm_sorte
         n_hit = torch.empty(m, dtype=torch.int32, device=dev)
         dmax = torch.empty(m, dtype=torch.float32, device=dev)
         dsum = torch.empty(m, dtype=torch.float32, device=dev)
-        _lib.call("eg_scan_overlay", ctypes.byref(spec), _lib.ptr(tok), tok.numel(), start_local, _lib.ptr(ids), n_ov,
+        _lib.call("eg_scan_overlay", ctypes.byref(spec), _lib.ptr(tok), tok.element_size(), tok.numel(), start_local,
+                  _lib.ptr(ids), n_ov,
                   _lib.ptr(bitmap), n_bits, _lib.ptr(dn), _lib.ptr(n_hit), _lib.ptr(dmax), _lib.ptr(dsum), _lib.ptr(counts),
                   _lib.stream_ptr(dev))
         hit_local = torch.nonzero(n_hit > 0).reshape(-1)

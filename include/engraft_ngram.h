@@ -236,7 +236,8 @@ int eg_lookup_rows(const int32_t* rows, int64_t n, const int32_t* ids, const int
                    int64_t n_ids, int32_t* out, int64_t* counts, void* stream);
 
 /* Damage scan of one token block (engraft/damage.py:159-224, fused): positions
- * start..n_tokens-1 of tokens (device int64, the block as one sequence) hash
+ * start..n_tokens-1 of tokens (device, int32 when token_bytes is 4, int64 when
+ * 8, the block as one sequence) hash
  * their rows; each row is looked up in the sorted overlay ids (int32 [n_ids],
  * n_ids >= 1) and, per position, n_hit int32 = the rows found, dnorm_max /
  * dnorm_sum f32 = max / sum of dnorm[k] over them (0 when none); read_counts
@@ -244,10 +245,10 @@ int eg_lookup_rows(const int32_t* rows, int64_t n, const int32_t* ids, const int
  * start entries.  No per-slot array is written.  bitmap (optional, from
  * eg_build_id_bitmap over the same ids, n_bits covering every row id) replaces
  * the binary search with a probe of the rank bitmap. */
-int eg_scan_overlay(const eg_hash_spec* spec, const int64_t* tokens, int64_t n_tokens, int64_t start,
-                    const int32_t* ids, int64_t n_ids, const uint32_t* bitmap, int64_t n_bits,
-                    const float* dnorm, int32_t* n_hit, float* dnorm_max, float* dnorm_sum,
-                    int64_t* read_counts, void* stream);
+int eg_scan_overlay(const eg_hash_spec* spec, const void* tokens, int32_t token_bytes, int64_t n_tokens,
+                    int64_t start, const int32_t* ids, int64_t n_ids, const uint32_t* bitmap,
+                    int64_t n_bits, const float* dnorm, int32_t* n_hit, float* dnorm_max,
+                    float* dnorm_sum, int64_t* read_counts, void* stream);
 
 /* Rank bitmap of sorted, unique overlay ids for eg_scan_overlay: bitmap is
  * uint32 [2 * nw + ceil(nw/32)], nw = ceil(n_bits/32); word w < nw gets bit b

@@ -164,10 +164,11 @@ def test_scan_hits_against_oracle(cuda):
     assert np.array_equal(np.concatenate([big, tri], axis=1), rows)
     exp = DM.scan_hits(spec, tokens, ov, dn, block=4_000)
     for block in (4_000, 7_777, 20_000):
-        got = damage.scan_hits(tokens, tab, ov, dn, block=block)
-        for k in ("pos", "n_hit_rows", "dnorm_max", "read_count"):
-            assert np.array_equal(got[k], exp[k]), k
-        np.testing.assert_allclose(got["dnorm_sum"], exp["dnorm_sum"], rtol=1e-6)
+        for toks in (tokens, np.asarray(tokens, dtype=np.int32)):  # int64 and int32 token arrays
+            got = damage.scan_hits(toks, tab, ov, dn, block=block)
+            for k in ("pos", "n_hit_rows", "dnorm_max", "read_count"):
+                assert np.array_equal(got[k], exp[k]), k
+            np.testing.assert_allclose(got["dnorm_sum"], exp["dnorm_sum"], rtol=1e-6)
 
 
 def test_scan_overlay_rank_bitmap(cuda):
@@ -213,7 +214,7 @@ def test_scan_overlay_rank_bitmap(cuda):
             n_hit = torch.empty(m, dtype=torch.int32, device=cuda)
             dmax, dsum = torch.empty(m, device=cuda), torch.empty(m, device=cuda)
             counts = torch.zeros(ov.size, dtype=torch.int64, device=cuda)
-            _lib.call("eg_scan_overlay", ctypes.byref(spec_c), _lib.ptr(tok), tok.numel(), start, _lib.ptr(ids),
+            _lib.call("eg_scan_overlay", ctypes.byref(spec_c), _lib.ptr(tok), 8, tok.numel(), start, _lib.ptr(ids),
                       ov.size, bm, n_bits, _lib.ptr(dn), _lib.ptr(n_hit), _lib.ptr(dmax), _lib.ptr(dsum),
                       _lib.ptr(counts), _lib.stream_ptr(cuda))
             outs.append([x.cpu().numpy() for x in (n_hit, dmax, dsum, counts)])
