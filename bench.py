@@ -200,13 +200,45 @@ def cpu_baseline(hp: dict, tokens_np, residual_cpu, budget_s: float) -> dict:
                          "hash of its whole prefix (RowSet.from_position's O(T^2) re-hash), one row read + Q8_0 "
                          "dequant per head, fp32 add -> bf16; pure Python/numpy",
                "matches_vectorized": bool(np.array_equal(lit, out[:n_lit].view(torch.int16).numpy().view(np.uint16)))}
-    return {"result": out, "literal": literal, "host": host_cpu(), "value": rows_per_s, "unit": "rows/s",
+    literal_cfg0 = cpu_literal_config0(n_lit)
+    return {"result": out, "literal": literal, "literal_config0": literal_cfg0, "host": host_cpu(),
+            "value": rows_per_s, "unit": "rows/s",
             "cores": threads, "kind": "port",
             "sample": (f"full config-1 step ({tokens_np.size} positions, {tokens_np.size * SLOTS} row reads) "
                        f"repeated {n}x in {el:.1f} s: numpy-uint64 hash + torch.index_select gather from a "
                        f"host table of the full 320M-row shape (touched rows materialised) + Q8_0 dequant + "
                        f"fp32 add -> bf16, {threads} torch threads"),
             "gb_per_s": n * forward_bytes(tokens_np.size) / el / 1e9, "steps": n, "seconds": el}
+
+
+def cpu_literal_config0(n_pos: int) -> dict:
+    """The reference's per-position loop on BASELINE config 0 (its CPU-runnable
+    case: 4,194,304 bf16 rows, uniform tokens over 151,936, 16 slots, residual
+    width 2048), first n_pos positions; the touched rows are generated before
+    the timed loop and read one at a time inside it."""
+    import numpy as np
+
+    from engraft_ngram_amd import synthetic as S
+    from oracle import cpu_baseline as CB
+    from oracle import hash as OH
+    from oracle import synth
+
+    n_rows, dim, seed = 4_194_304, 128, 11
+    spec = oracle_spec(S.hash_params(n_rows, seed))
+    tokens = np.random.default_rng(seed + 1).integers(0, VOCAB, size=n_pos)
+    rows = OH.ngram_rows_np(spec, tokens)
+    uniq = np.unique(rows)
+    vals = synth.synth_dequant("bf16", seed + 2, uniq, dim, 0.02)
+    store = dict(zip(uniq.tolist(), vals))
+    res_bits = np.random.default_rng(seed + 3).integers(0, 1 << 16, size=(n_pos, 16 * dim)).astype(np.uint16)
+    res_bits &= 0x7F7F  # finite bf16 values
+    t0 = time.perf_counter()
+    CB.forward_literal(spec, tokens, n_pos, store.__getitem__, dim, res_bits)
+    el = time.perf_counter() - t0
+    return {"value": n_pos * 16 / el, "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": f"BASELINE config 0 (4,194,304 bf16 rows, uniform tokens), the first {n_pos} positions in "
+                      f"{el:.2f} s: per position the scalar re-hash of its prefix, a row read + dequant per head, "
+                      "fp32 add -> bf16; pure Python/numpy"}
 
 
 def backward_bytes(positions: int, n_unique: int) -> int:
@@ -855,12 +887,14 @@ def main() -> None:
         same = bool(torch.equal(cb.pop("result").view(torch.int16), outs[0].cpu().view(torch.int16)))
         cb["matches_gpu_output"] = same
         result["cpu_baseline_literal"] = cb.pop("literal")
+        result["cpu_baseline_literal_config0"] = cb.pop("literal_config0")
         cb["gpu_speedup"] = result["value"] / cb["value"]
         result["cpu_baseline_literal"]["gpu_speedup"] = result["value"] / result["cpu_baseline_literal"]["value"]
         result["cpu_baseline"] = cb
         lit = result["cpu_baseline_literal"]
         log(f"cpu baseline, the reference's per-position loop: {lit['value']:.3g} rows/s on 1 thread; "
-            f"identical output: {lit['matches_vectorized']}")
+            f"identical output: {lit['matches_vectorized']}; on config 0: "
+            f"{result['cpu_baseline_literal_config0']['value']:.3g} rows/s")
         log(f"cpu baseline: {cb['value']:.3g} rows/s on {cb['cores']} threads; identical output: {same}")
     else:
         result["cpu_baseline"] = None

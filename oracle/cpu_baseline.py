@@ -67,6 +67,21 @@ def forward_q8(spec: H.HashSpec, tokens: np.ndarray, seq_len: int | None, table:
     return rows, out
 
 
+def forward_literal(spec: H.HashSpec, tokens: np.ndarray, n_positions: int, read_row, dim: int,
+                    residual: np.ndarray) -> np.ndarray:
+    """``forward_q8_literal`` for any row format: ``read_row(r)`` returns global
+    row ``r`` dequantised (f32 ``[dim]``), one call per head and position as the
+    reference reads a row at a time."""
+    toks = [int(x) for x in np.asarray(tokens[:n_positions])]
+    out = np.empty((n_positions, spec.n_heads * dim), dtype=np.uint16)
+    for t in range(n_positions):
+        local = H.ngram_addresses_scalar(spec, toks[:t + 1])[t]
+        emb = np.concatenate([read_row(H.local_to_global(spec, h, r)) for h, r in enumerate(local)])
+        res = F.bf16_bits_to_f32(np.asarray(residual[t], dtype=np.uint16))
+        out[t] = F.f32_to_bf16_bits((res + emb).astype(np.float32))
+    return out
+
+
 def forward_q8_literal(spec: H.HashSpec, tokens: np.ndarray, n_positions: int, table: HostTable,
                        residual: np.ndarray) -> np.ndarray:
     """The first ``n_positions`` positions of one sequence, position by position:

@@ -190,6 +190,10 @@ def test_cpu_baseline_equals_oracle_forward():
     # the literal per-position loop (scalar re-hash of every prefix) gives the same bits
     lit = CB.forward_q8_literal(spec, tokens, 40, host, res[:40].view(torch.int16).numpy().view(np.uint16))
     assert np.array_equal(lit, exp_out[:40])
+    # the format-generic form with a row reader gives the same bits
+    read = lambda r: FW.table_fetch("q8_0", host.payload, host.scales)(np.array([r]))[0]
+    lit2 = CB.forward_literal(spec, tokens, 40, read, 128, res[:40].view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(lit2, exp_out[:40])
 
 
 def test_product_synthetic_params_equal_oracle_params():
