@@ -71,6 +71,38 @@ def compute_rows_delta(table, rows_global: np.ndarray, data: np.ndarray) -> dict
             "true": true}
 
 
+_STAGING: dict = {}
+
+
+def _staging(dtype: torch.dtype, n: int) -> list:
+    """Two pinned host buffers of at least n tokens (kept for the next call):
+    one is filled while the other's copy to the device is in flight."""
+    have = _STAGING.get(dtype)
+    if have is None or have[0].numel() < n:
+        have = [torch.empty(max(n, 1), dtype=dtype, pin_memory=True) for _ in range(2)]
+        _STAGING[dtype] = have
+    return have
+
+
+_FILL_POOL = None
+
+
+def _fill(dst: np.ndarray, src: np.ndarray) -> None:
+    """dst[:] = src (converting to dst's type), in 1M-token pieces over four
+    threads: numpy's copy releases the GIL, and one thread moves an 8M-token
+    block at well under the host's memory bandwidth."""
+    global _FILL_POOL
+    piece = 1 << 20
+    if src.shape[0] <= piece:
+        dst[:] = src
+        return
+    if _FILL_POOL is None:
+        from concurrent.futures import ThreadPoolExecutor
+        _FILL_POOL = ThreadPoolExecutor(4, thread_name_prefix="eg-fill")
+    list(_FILL_POOL.map(lambda i: np.copyto(dst[i:i + piece], src[i:i + piece], casting="unsafe"),
+                        range(0, src.shape[0], piece)))
+
+
 def scan_hits(tokens: np.ndarray, table, overlay_sorted: np.ndarray, dnorm_sorted: np.ndarray,
               block: int = BLOCK_TOKENS) -> dict:
     """Positions of ``tokens`` that read at least one row of the sorted overlay
@@ -103,32 +135,57 @@ def scan_hits(tokens: np.ndarray, table, overlay_sorted: np.ndarray, dnorm_sorte
     if n_ov:
         _lib.call("eg_build_id_bitmap", _lib.ptr(ids), n_ov, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(dev))
     # int32 token arrays (a tokenized corpus file) go to the device as they are
-    # (4 bytes a token); any other integer type as int64
+    # (4 bytes a token); any other integer type as int64.  Blocks are uploaded
+    # on a second stream: block i+1 crosses PCIe while block i is scanned.
     narrow = tokens.dtype == np.int32
-    for offset, blk in iter_blocks(tokens, block=block, overlap=hist):
+    tdt = torch.int32 if narrow else torch.int64
+    main = torch.cuda.current_stream(dev)
+    upload_stream = torch.cuda.Stream(device=dev)
+    blocks = list(iter_blocks(tokens, block=block, overlap=hist))
+    staging = _staging(tdt, max((len(b) for _, b in blocks), default=0)) if n_ov else None
+    copied = [None, None]  # the last copy out of each pinned buffer
+
+    def upload(j):
+        blk = blocks[j][1]
+        host = staging[j % 2][:len(blk)]
+        if copied[j % 2] is not None:
+            copied[j % 2].synchronize()  # that buffer's previous block has left it
+        _fill(host.numpy(), blk)
+        with torch.cuda.stream(upload_stream):
+            t = torch.empty(len(blk), dtype=tdt, device=dev)
+            t.copy_(host, non_blocking=True)
+            copied[j % 2] = upload_stream.record_event()
+        return t, copied[j % 2]
+
+    nxt = upload(0) if blocks and n_ov else None
+    for i, (offset, blk) in enumerate(blocks):
+        if nxt is None:
+            break
+        tok, ready = nxt
+        main.wait_event(ready)
+        tok.record_stream(main)  # allocated on the upload stream, read on this one
         start_local = 0 if offset == 0 else hist
-        tok = torch.as_tensor(np.ascontiguousarray(blk) if narrow else np.asarray(blk, dtype=np.int64)).to(dev)
         m = tok.numel() - start_local
-        if m <= 0 or n_ov == 0:
+        if m > 0:
+            # one fused launch: hash, membership, per-position reductions, read
+            # counts; n_hit / dnorm_max / dnorm_sum land in the rows of one
+            # [3, m] buffer so the hits leave the device in one gather
+            out = torch.empty((3, m), dtype=torch.int32, device=dev)
+            _lib.call("eg_scan_overlay", ctypes.byref(spec), _lib.ptr(tok), tok.element_size(), tok.numel(),
+                      start_local, _lib.ptr(ids), n_ov, _lib.ptr(bitmap), n_bits, _lib.ptr(dn), _lib.ptr(out[0]),
+                      _lib.ptr(out[1]), _lib.ptr(out[2]), _lib.ptr(counts), _lib.stream_ptr(dev))
+        nxt = upload(i + 1) if i + 1 < len(blocks) else None  # while the scan runs
+        lim = min(m, n - 1 - offset)  # the corpus's last position is not a hit
+        if lim <= 0:
             continue
-        # one fused launch: hash, membership, per-position reductions, read counts
-        n_hit = torch.empty(m, dtype=torch.int32, device=dev)
-        dmax = torch.empty(m, dtype=torch.float32, device=dev)
-        dsum = torch.empty(m, dtype=torch.float32, device=dev)
-        _lib.call("eg_scan_overlay", ctypes.byref(spec), _lib.ptr(tok), tok.element_size(), tok.numel(), start_local,
-                  _lib.ptr(ids), n_ov,
-                  _lib.ptr(bitmap), n_bits, _lib.ptr(dn), _lib.ptr(n_hit), _lib.ptr(dmax), _lib.ptr(dsum), _lib.ptr(counts),
-                  _lib.stream_ptr(dev))
-        hit_local = torch.nonzero(n_hit > 0).reshape(-1)
-        pos_here = hit_local + offset
-        keep = pos_here < (n - 1)
-        hit_local = hit_local[keep]
+        hit_local = torch.nonzero(out[0, :lim] > 0).reshape(-1)
         if hit_local.numel() == 0:
             continue
-        pos_parts.append(pos_here[keep].cpu().numpy().astype(np.int64))
-        nh_parts.append(n_hit[hit_local].cpu().numpy().astype(np.int32))
-        dmax_parts.append(dmax[hit_local].cpu().numpy().astype(np.float32))
-        dsum_parts.append(dsum[hit_local].cpu().numpy().astype(np.float32))
+        vals = out[:, hit_local].cpu().numpy()
+        pos_parts.append(hit_local.cpu().numpy() + offset)
+        nh_parts.append(vals[0])
+        dmax_parts.append(vals[1].view(np.float32))
+        dsum_parts.append(vals[2].view(np.float32))
     read_count = counts[:n_ov].cpu().numpy().astype(np.int64)
     dt = time.time() - t0
 
