@@ -71,19 +71,6 @@ def compute_rows_delta(table, rows_global: np.ndarray, data: np.ndarray) -> dict
             "true": true}
 
 
-_STAGING: dict = {}
-
-
-def _staging(dtype: torch.dtype, n: int) -> list:
-    """Two pinned host buffers of at least n tokens (kept for the next call):
-    one is filled while the other's copy to the device is in flight."""
-    have = _STAGING.get(dtype)
-    if have is None or have[0].numel() < n:
-        have = [torch.empty(max(n, 1), dtype=dtype, pin_memory=True) for _ in range(2)]
-        _STAGING[dtype] = have
-    return have
-
-
 _FILL_POOL = None
 
 
@@ -142,7 +129,10 @@ def scan_hits(tokens: np.ndarray, table, overlay_sorted: np.ndarray, dnorm_sorte
     main = torch.cuda.current_stream(dev)
     upload_stream = torch.cuda.Stream(device=dev)
     blocks = list(iter_blocks(tokens, block=block, overlap=hist))
-    staging = _staging(tdt, max((len(b) for _, b in blocks), default=0)) if n_ov else None
+    # two pinned host buffers (torch's host allocator keeps them for the next
+    # call): one is filled while the other's copy to the device is in flight
+    cap = max((len(b) for _, b in blocks), default=0)
+    staging = [torch.empty(max(cap, 1), dtype=tdt, pin_memory=True) for _ in range(2)] if n_ov else None
     copied = [None, None]  # the last copy out of each pinned buffer
 
     def upload(j):
