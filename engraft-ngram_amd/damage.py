@@ -111,6 +111,10 @@ def scan_hits(tokens: np.ndarray, table, overlay_sorted: np.ndarray, dnorm_sorte
         raise ValueError("scan_hits: dnorm_sorted must match overlay_sorted")
     counts = torch.zeros(max(n_ov, 1), dtype=torch.int64, device=dev)
     hist = table.ngram_size - 1
+    if block < max(hist, 1):
+        # a later block's history would start before the corpus (the
+        # reference's loop reads a wrapped-around slice there)
+        raise ValueError(f"scan_hits: block ({block}) must be at least the n-gram history ({hist})")
     pos_parts, nh_parts, dmax_parts, dsum_parts = [], [], [], []
     t0 = time.time()
     spec = table.c_spec

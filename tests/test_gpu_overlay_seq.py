@@ -171,6 +171,34 @@ def test_scan_hits_against_oracle(cuda):
             np.testing.assert_allclose(got["dnorm_sum"], exp["dnorm_sum"], rtol=1e-6)
 
 
+def test_scan_hits_edges_against_oracle(cuda):
+    """Corpora shorter than the n-gram history, one block of exactly the
+    history, every position in its own block, an empty and a one-row overlay,
+    EOS runs; device scan vs oracle, and blocks below the history refused."""
+    from engraft_ngram_amd import damage
+    _say("damage scan edges")
+    spec = fake_table_spec(7)
+    tab, _ = G.f32_table(spec, 32, seed=52)
+    hist = spec.ngram_size - 1
+    corpus = reference_corpus(600, seed=3, eos=spec.eos_token_id)
+    corpus[40:45] = spec.eos_token_id
+    rows = H.ngram_rows_np(spec, corpus)
+    overlays = [np.zeros(0, dtype=np.int64), np.array([rows[7, 3]], dtype=np.int64),
+                np.unique(rows[::37].reshape(-1))]
+    for n_tok in (0, 1, 2, 3, 4, 600):
+        toks = corpus[:n_tok]
+        for ov in overlays:
+            dn = np.linspace(0.5, 2.0, ov.size).astype(np.float32)
+            for block in sorted({hist, 5, 600}):
+                exp = DM.scan_hits(spec, toks, ov, dn, block=block)
+                got = damage.scan_hits(toks, tab, ov, dn, block=block)
+                for k in ("pos", "n_hit_rows", "dnorm_max", "read_count"):
+                    assert np.array_equal(got[k], exp[k]), (n_tok, ov.size, block, k)
+                np.testing.assert_allclose(got["dnorm_sum"], exp["dnorm_sum"], rtol=1e-6)
+    with pytest.raises(ValueError, match="history"):
+        damage.scan_hits(corpus, tab, overlays[1], np.ones(1, np.float32), block=hist - 1)
+
+
 def test_scan_overlay_rank_bitmap(cuda):
     """eg_scan_overlay with and without the eg_build_id_bitmap rank bitmap:
     the bits hold exactly the ids below n_bits (an id past the table's rows is
