@@ -258,44 +258,48 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   // 4. Issue the table (or overlay) row loads of every layer and chunk.  Row
   //    ids handed in by the caller (gather mode) and overlay indices are
   //    checked: an id outside its table reads NaN, never memory.  Base-table
-  //    loads are unconditional (an invalid id loads row 0 and is masked).
+  //    loads are unconditional (an invalid id loads row 0 and is masked) and
+  //    go out before the overlay lookup: the lookup's dependent probes then
+  //    overlap the row's own latency, and a row the overlay replaces (rare)
+  //    costs one wasted load.
   RawChunk tr[MAXL][NCH];
+  RawChunk orow[OVL ? MAXL : 1][OVL ? NCH : 1];
   uint32_t src[MAXL][NCH];  // 0: base table, 1: overlay, 2: invalid id
 #pragma unroll
   for (int l = 0; l < MAXL; ++l) {
     if (l >= nl) break;
-    int32_t ovk = -1;
-    const OverlayDev& ov = a.ov[l];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int e0 = cb + (lane + 64 * c) * 8;
+      const int h = min(e0, W - 8) / dim;
+      const int32_t row = __shfl(rid[l], h - h_lo);
+      const int off = e0 - h * dim;
+      const bool base_ok = e0 < W && (uint32_t)row < (uint64_t)a.table[l].n_rows;
+      tr[l][c] = load_raw<FMT>(a.table[l], dim, base_ok ? row : 0, base_ok ? off : 0);
+      src[l][c] = base_ok ? 0u : 2u;
+    }
     if constexpr (OVL) {
+      int32_t ovk = -1;
+      const OverlayDev& ov = a.ov[l];
       if (a.slot_var != nullptr) {
         ovk = a.slot_var[p * H + hh];
       } else if (ov.n > 0) {
         const int64_t k = ov.bitmap ? bitmap_find(ov.bitmap, ov.n_bits, rid[l]) : sorted_find(ov.ids, ov.n, rid[l]);
         if (k >= 0) ovk = ov.index ? ov.index[k] : (int32_t)k;
       }
-    }
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int e0 = cb + (lane + 64 * c) * 8;
-      const int h = min(e0, W - 8) / dim;
-      const int32_t row = __shfl(rid[l], h - h_lo);
-      int32_t k = -1;
-      if constexpr (OVL) k = __shfl(ovk, h - h_lo);
-      const int off = e0 - h * dim;
-      const bool in_w = e0 < W;
-      const bool base_ok = in_w && (uint32_t)row < (uint64_t)a.table[l].n_rows;
-      if constexpr (OVL) {
-        if (in_w && k >= 0) {
+      for (int c = 0; c < NCH; ++c) {
+        const int e0 = cb + (lane + 64 * c) * 8;
+        const int h = min(e0, W - 8) / dim;
+        const int32_t k = __shfl(ovk, h - h_lo);
+        if (e0 < W && k >= 0) {
           src[l][c] = 2;
           if (k < ov.rows.n_rows) {
-            tr[l][c] = load_raw_rt(ov.rows, k, off);
+            orow[l][c] = load_raw_rt(ov.rows, k, e0 - h * dim);
             src[l][c] = 1;
           }
-          continue;
         }
       }
-      tr[l][c] = load_raw<FMT>(a.table[l], dim, base_ok ? row : 0, base_ok ? off : 0);
-      src[l][c] = base_ok ? 0u : 2u;
     }
   }
 
@@ -325,7 +329,7 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
       const int off = e0 - (min(e0, W - 8) / dim) * dim;
       float v[8];
       if (OVL && src[l][c] == 1) {
-        decode_rt(a.ov[l].rows.fmt, tr[l][c], off, v);
+        decode_rt(a.ov[l].rows.fmt, orow[OVL ? l : 0][OVL ? c : 0], off, v);
       } else {
         decode<FMT>(tr[l][c], src[l][c] == 0 ? off : 0, v);
         if (src[l][c] != 0) {
