@@ -190,6 +190,69 @@ __global__ __launch_bounds__(256) void ple_conv_kernel(const float* __restrict__
   }
 }
 
+// ple_conv_kernel for a fixed tap count and dilation, one position per row:
+// each thread keeps its channel's rows t0-H .. t0+kConvRun-1 in registers
+// (H = (TAPS-1)*DIL), so every row of `full` is read once per workgroup
+// instead of once per tap.  Same arithmetic in the same order as
+// ple_conv_kernel (bit-identical results).
+template <int MODE, int TAPS, int DIL>
+__global__ __launch_bounds__(256) void ple_conv_win_kernel(const float* __restrict__ full, int64_t hist_rows,
+                                                           int64_t T, int hc, int n, const float* __restrict__ conv_w,
+                                                           const float* __restrict__ hidden,
+                                                           const float* __restrict__ value,
+                                                           const float* __restrict__ gate, float* __restrict__ out,
+                                                           float* __restrict__ pre) {
+#pragma clang fp contract(off)
+  constexpr int H = (TAPS - 1) * DIL;
+  constexpr int RUN = kConvRun;
+  const int C = hc * n;
+  const int n_cblk = (C + 255) / 256;
+  const int cblk = (int)(blockIdx.x % n_cblk);
+  const int64_t t0 = (int64_t)(blockIdx.x / n_cblk) * RUN;
+  const int c = cblk * 256 + threadIdx.x;
+  if (c >= C) return;
+  const int j = c / n;
+  const int i = c - j * n;
+  float w[TAPS];
+#pragma unroll
+  for (int k = 0; k < TAPS; ++k) w[k] = conv_w[(int64_t)c * TAPS + k];
+  // window slot q holds row hist_rows + t0 - H + q; a row before the first is
+  // not read (its taps are dropped), a row past the last (positions >= T,
+  // never stored) re-reads the last
+  const int64_t last = hist_rows + T - 1;
+  float win[RUN + H];
+#pragma unroll
+  for (int q = 0; q < RUN + H; ++q) {
+    const int64_t r = hist_rows + t0 - H + q;
+    win[q] = full[(r < 0 ? 0 : (r > last ? last : r)) * C + c];
+  }
+  float hv[RUN], vv[RUN], gj[RUN];
+#pragma unroll
+  for (int b = 0; b < RUN; ++b) {
+    const int64_t tb = min(t0 + b, T - 1);
+    hv[b] = vv[b] = gj[b] = 0.0f;
+    if constexpr (MODE == 0) hv[b] = hidden[tb * C + c];
+    if constexpr (MODE <= 1) {
+      vv[b] = value[tb * n + i];
+      gj[b] = gate[tb * hc + j];
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < RUN; ++b) {
+    if (t0 + b >= T) break;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < TAPS; ++k)
+      if (hist_rows + t0 - H + b + k * DIL >= 0) acc += win[b + k * DIL] * w[k];
+    const float silu = acc / (1.0f + expf(-acc));
+    const int64_t o = (t0 + b) * C + c;
+    if (pre != nullptr) pre[o] = acc;
+    if constexpr (MODE == 0) out[o] = (hv[b] + vv[b] * gj[b]) + silu;
+    else if constexpr (MODE == 1) out[o] = vv[b] * gj[b] + silu;
+    else out[o] = silu;
+  }
+}
+
 // The per-stream RMS norm, with the reductions of ple_gate_kernel (same thread
 // layout and tree), so it reproduces that kernel's normed values bit for bit.
 __global__ __launch_bounds__(kPleThreads) void ple_rms_kernel(const float* __restrict__ x, int hc, int n, float eps,
@@ -768,6 +831,11 @@ template <int MODE, bool SHARED>
 static void launch_conv(dim3 grid, hipStream_t st, const float* full, int64_t hist_rows, int64_t n_pos, int hc, int n,
                         const float* conv_w, int taps, int dil, const float* hidden, const float* value,
                         const float* gate, float* out, float* pre) {
+  if (!SHARED && taps == 4 && dil == 3) {  // the model's shape
+    hipLaunchKernelGGL((ple_conv_win_kernel<MODE, 4, 3>), grid, dim3(256), 0, st, full, hist_rows, n_pos, hc, n,
+                       conv_w, hidden, value, gate, out, pre);
+    return;
+  }
   hipLaunchKernelGGL((ple_conv_kernel<MODE, SHARED>), grid, dim3(256), 0, st, full, hist_rows, n_pos, hc, n, conv_w,
                      taps, dil, hidden, value, gate, out, pre);
 }
