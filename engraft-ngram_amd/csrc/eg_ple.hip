@@ -13,8 +13,10 @@
 //                     (gated + conv without hidden, conv alone without value);
 //                     with a shared history every position is a one-token
 //                     continuation of the same history (the batch of
-//                     engraft/lens.py ple_out_at)
-//   ple_rms_kernel    one workgroup per (row, stream j): x * 1/sqrt(mean(x^2)
+//                     engraft/lens.py ple_out_at); ple_conv_win_kernel is
+//                     the same for 4 taps at dilation 3 with each channel's
+//                     rows held in registers (every row read once)
+//   ple_rms_kernel   one workgroup per (row, stream j): x * 1/sqrt(mean(x^2)
 //                     + eps) * w_j, the per-stream RMS norm on its own
 //
 // fp32 throughout, the reference's operation order within each element and no
