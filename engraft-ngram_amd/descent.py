@@ -28,7 +28,15 @@ from . import _lib
 from .overlay import DeviceOverlay
 from .table import DeviceTable, RowStore
 
-_POLICIES = ("all-read", "private", "entity", "t8-answer")
+# Locality policies of the variable rows (engraft/replica/distill.py:401-437):
+# policy -> (row-set keys whose union is taken, row-set keys removed from it).
+_POLICY_RULES: dict[str, tuple[tuple[str, ...], tuple[str, ...]]] = {
+    "all-read": (("all_read",), ()),
+    "private": (("all_read",), ("neutral_read",)),
+    "entity": (("entity", "terme"), ()),
+    "t8-answer": (("t8_answer",), ()),
+}
+_POLICIES = tuple(_POLICY_RULES)
 
 
 class _Workspace:
@@ -122,8 +130,13 @@ class DescentState:
         self.index = torch.empty(cap, dtype=torch.int64, device=dev)
         _lib.call("eg_build_row_index", _lib.ptr(self.ids), ids.numel(), _lib.ptr(self.index), cap,
                   _lib.stream_ptr(dev))
-        # ||rows0||^2 of the start rows (engraft/descend_corpus.py:936), for the pull term
-        self.rows0_sq = float(self.master.pow(2).sum().clamp_min(1e-12).item()) if ids.numel() else 0.0
+        # ||rows0||^2 (engraft/descend_corpus.py:936) for the pull term.  rows0 are
+        # the true rows, which the step kernel reads from the base table as the
+        # anchor, so the denominator comes from the same rows (the master may
+        # start elsewhere, e.g. from a resumed overlay); without a base table
+        # the pull term is unavailable and the master stands in.
+        rows0 = base.gather(self.ids.reshape(-1, 1)) if (base is not None and ids.numel()) else self.master
+        self.rows0_sq = float(rows0.pow(2).sum().clamp_min(1e-12).item()) if ids.numel() else 0.0
 
     @property
     def n(self) -> int:
@@ -222,8 +235,8 @@ class DescentState:
         """The variables as a forward overlay: the requantised rows, or the fp32
         master rows (the reference's ``.pleo`` semantics)."""
         if quantized and self.quant is not None:
-            return DeviceOverlay(self.ids, self.quant)
-        return DeviceOverlay(self.ids, RowStore("f32", self.dim, self.master))
+            return DeviceOverlay(self.ids, self.quant, ids_checked=True)
+        return DeviceOverlay(self.ids, RowStore("f32", self.dim, self.master), ids_checked=True)
 
 
 # ---------------------------------------------------------------------------------------------
@@ -259,30 +272,24 @@ def build_rows_var(table: DeviceTable, sequences: list[list[int]], policy: str, 
     position; ``row_map`` = ``{global_row: index}`` in ascending row order;
     ``rows_var`` f32 ``[R, row_len]`` (CPU, like the reference) holding the TRUE
     values."""
-    if policy not in _POLICIES:
+    rule = _POLICY_RULES.get(policy)
+    if rule is None:
         raise ValueError(f"build_rows_var: unknown policy {policy!r} (expected: {_POLICIES})")
+    include, subtract = rule
 
-    def rows_of(key: str) -> set[int]:
-        return {int(r) for r in row_sets[key]}
+    def ids(keys: tuple[str, ...]) -> np.ndarray:
+        return np.unique(np.concatenate([np.asarray(row_sets[k], dtype=np.int64).reshape(-1) for k in keys]
+                                        + [np.zeros(0, dtype=np.int64)]))
 
-    if policy == "all-read":
-        candidate = rows_of("all_read")
-    elif policy == "private":
-        candidate = rows_of("all_read") - rows_of("neutral_read")
-    elif policy == "entity":
-        candidate = rows_of("entity") | rows_of("terme")
-    else:
-        candidate = rows_of("t8_answer")
-    excluded: set[int] = set()
+    # rows read at an excluded position (every head of it), hashed on the device
+    excluded = [np.zeros(0, dtype=np.int64)]
     for seq_idx, positions in (exclude_positions or {}).items():
-        if not positions:
-            continue
-        ids = table.rows(sequences[seq_idx]).cpu().numpy()
-        for p in positions:
-            excluded.update(int(g) for g in ids[p])
-    selected = sorted(candidate - excluded)
-    row_map = {g: i for i, g in enumerate(selected)}
-    if not selected:
+        if len(positions):
+            excluded.append(table.rows(sequences[seq_idx]).cpu().numpy()[list(positions)].reshape(-1))
+    drop = np.union1d(ids(subtract), np.concatenate(excluded))
+    selected = np.setdiff1d(ids(include), drop)  # ascending, unique
+    row_map = {int(g): i for i, g in enumerate(selected.tolist())}
+    if selected.size == 0:
         return row_map, torch.zeros(0, table.row_len, dtype=torch.float32)
     return row_map, torch.from_numpy(_read_true_rows(table, selected).copy())
 

@@ -23,6 +23,7 @@ from pathlib import Path
 import numpy as np
 
 from .overlay import DeviceOverlay
+from .table import ROW_LEN
 
 PLEO_MAGIC = b"PLEO"
 
@@ -93,60 +94,75 @@ class RowSet:
         data = table.gather(table_rows_tensor(table, rows)).cpu().numpy().reshape(table.n_heads, table.row_len)
         return cls(table=table, rows_global=rows, data=data)
 
-    # -- variants: each returns a new float32 array [n_heads, row_len] --
+    # -- variants of the true rows (engraft/lens.py:138-165): each a new float32
+    #    array of the same [n_heads, row_len] shape --
     def identity(self) -> np.ndarray:
-        return self.data.copy()
+        return np.array(self.data, dtype=np.float32, copy=True)
 
     def zero(self) -> np.ndarray:
-        return np.zeros_like(self.data)
+        return np.zeros(self.data.shape, dtype=np.float32)
 
     def scale(self, k: float) -> np.ndarray:
-        return (self.data * k).astype(np.float32)
+        return np.multiply(self.data, np.float32(k), dtype=np.float32)
 
     def random_matched(self, rng: np.random.Generator) -> np.ndarray:
-        """Independent Gaussian per row, renormalised to the true row's norm."""
-        norms = np.linalg.norm(self.data, axis=1, keepdims=True)
-        g = rng.standard_normal(self.data.shape).astype(np.float32)
-        g_norms = np.linalg.norm(g, axis=1, keepdims=True)
-        g_norms = np.where(g_norms == 0.0, 1.0, g_norms)
-        return (g / g_norms * norms).astype(np.float32)
+        """Gaussian rows with the true rows' norms.  One ``standard_normal`` draw
+        of the whole [n_heads, row_len] block, so the same generator state gives
+        the reference's numbers; an all-zero draw row keeps norm 1."""
+        target = np.linalg.norm(self.data, axis=1, keepdims=True)
+        draw = rng.standard_normal(self.data.shape).astype(np.float32)
+        drawn = np.linalg.norm(draw, axis=1, keepdims=True)
+        drawn = drawn + (drawn == 0.0)  # 0 -> 1, every other norm unchanged
+        return ((draw / drawn) * target).astype(np.float32)
 
     def swap(self, other: "RowSet") -> np.ndarray:
+        """The other position's rows in place of these (shapes must agree)."""
         if other.data.shape != self.data.shape:
             raise ValueError("swap: RowSet of different shape")
-        return other.data.copy()
+        return np.array(other.data, dtype=np.float32, copy=True)
 
     def isolate(self, h: int) -> np.ndarray:
-        out = np.zeros_like(self.data)
-        out[h] = self.data[h]
-        return out
+        """Head ``h``'s row kept, every other head zeroed (negative ``h`` counts
+        from the end, like an index)."""
+        keep = range(self.data.shape[0])[h]
+        mask = (np.arange(self.data.shape[0]) == keep)[:, None]
+        return np.where(mask, self.data, np.float32(0.0)).astype(np.float32)
 
     @staticmethod
     def build_overlay(parts: list[tuple[np.ndarray, np.ndarray]]) -> tuple[np.ndarray, np.ndarray]:
-        """Merges several ``(rows_global, data[n, D])`` sets by global row,
-        deduplicating; ``ValueError`` if one row receives two different vectors
-        (``engraft/lens.py:167-198``).  Returns ascending rows."""
-        seen: dict[int, np.ndarray] = {}
+        """One overlay from several ``(rows_global, data[n, D])`` sets
+        (``engraft/lens.py:167-198``): rows ascending, each once.  A row listed
+        more than once must carry equal vectors every time (``ValueError``
+        otherwise: NaN never equals itself, -0.0 equals 0.0).
+
+        All parts are concatenated and stably sorted by row; a run of equal
+        rows is compared against its first member and keeps it."""
+        rows_parts, data_parts = [], []
         dim = None
         for rows_global, data in parts:
-            rows_global = np.asarray(rows_global)
-            data = np.asarray(data, dtype=np.float32)
-            if rows_global.shape[0] != data.shape[0]:
+            r = np.asarray(rows_global).reshape(-1)
+            d = np.asarray(data, dtype=np.float32)
+            if r.shape[0] != d.shape[0]:
                 raise ValueError("build_overlay: rows_global and data of different length")
-            if data.ndim == 2:
-                dim = data.shape[1]
-            for i in range(rows_global.shape[0]):
-                r = int(rows_global[i])
-                vec = data[i]
-                if r in seen:
-                    if not np.array_equal(seen[r], vec):
-                        raise ValueError(f"build_overlay: global row {r} receives two different vectors")
-                else:
-                    seen[r] = vec
-        if not seen:
-            return np.empty(0, dtype=np.int32), np.empty((0, dim or 0), dtype=np.float32)
-        rows_sorted = sorted(seen.keys())
-        return np.array(rows_sorted, dtype=np.int32), np.stack([seen[r] for r in rows_sorted]).astype(np.float32)
+            if d.ndim == 2:
+                dim = d.shape[1]
+            rows_parts.append(r.astype(np.int64))
+            data_parts.append(d.reshape(d.shape[0], -1))
+        n = sum(r.shape[0] for r in rows_parts)
+        if n == 0:
+            return np.empty(0, dtype=np.int32), np.empty((0, ROW_LEN if dim is None else dim), dtype=np.float32)
+        rows = np.concatenate(rows_parts)
+        data = np.concatenate(data_parts, axis=0)
+        order = np.argsort(rows, kind="stable")
+        rows, data = rows[order], data[order]
+        head = np.ones(n, dtype=bool)
+        head[1:] = rows[1:] != rows[:-1]
+        first = np.flatnonzero(head)[np.cumsum(head) - 1]  # each entry's run head
+        clash = ~(data == data[first]).all(axis=1)
+        if clash.any():
+            raise ValueError(f"build_overlay: global row {int(rows[np.flatnonzero(clash)[0]])} "
+                             "receives two different vectors")
+        return rows[head].astype(np.int32), np.ascontiguousarray(data[head])
 
 
 def table_rows_tensor(table, rows: np.ndarray):

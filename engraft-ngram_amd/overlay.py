@@ -32,9 +32,16 @@ class DeviceOverlay:
     ``index`` (optional, int32 ``[n]``): row of ``rows`` holding the k-th id;
     without it the k-th id reads row k."""
 
-    def __init__(self, ids: torch.Tensor, rows: RowStore, index: torch.Tensor | None = None):
+    def __init__(self, ids: torch.Tensor, rows: RowStore, index: torch.Tensor | None = None, *,
+                 ids_checked: bool = False):
         if ids.dtype != torch.int32 or ids.dim() != 1 or not ids.is_contiguous():
             raise ValueError("overlay ids must be a contiguous 1-D int32 tensor")
+        # Both lookups (binary search, rank bitmap) need strictly ascending ids;
+        # ids_checked: the caller has already established that.
+        if not ids_checked and ids.numel() > 1 and not bool((ids[1:] > ids[:-1]).all()):
+            raise ValueError("overlay ids must be sorted ascending and unique")
+        if ids.numel() and not ids_checked and int(ids[0]) < 0:
+            raise ValueError("overlay ids must be global rows >= 0")
         if index is None and rows.n_rows < ids.numel():
             raise ValueError(f"{ids.numel()} overlay ids but only {rows.n_rows} rows")
         if index is not None and (index.dtype != torch.int32 or index.shape != ids.shape):
@@ -52,6 +59,10 @@ class DeviceOverlay:
         n_rows = int(n_rows)
         if not 1 <= n_rows <= (1 << 31):
             raise ValueError(f"n_rows={n_rows} out of range")
+        if self.n and int(self.ids[-1]) >= n_rows:
+            # the bitmap holds rows below n_rows only: a larger id would be
+            # found by the binary search and missed through the bitmap
+            raise ValueError(f"overlay id {int(self.ids[-1])} >= n_rows={n_rows}")
         nw = (n_rows + 31) // 32
         bm = torch.empty(2 * nw + (nw + 31) // 32, dtype=torch.int32, device=self.ids.device)
         _lib.call("eg_build_id_bitmap", _lib.ptr(self.ids), self.n, _lib.ptr(bm), n_rows,
@@ -99,7 +110,7 @@ class DeviceOverlay:
         if data.ndim != 2 or data.shape[0] != s.size:
             raise ValueError(f"data must be [n, D] with n={s.size}")
         payload = torch.from_numpy(np.ascontiguousarray(data[order])).to(dev)
-        return cls(torch.from_numpy(s).to(dev), RowStore("f32", data.shape[1], payload))
+        return cls(torch.from_numpy(s).to(dev), RowStore("f32", data.shape[1], payload), ids_checked=True)
 
     @classmethod
     def from_dict(cls, overlay: dict, dim: int, device=None) -> "DeviceOverlay":
@@ -133,7 +144,7 @@ class DeviceOverlay:
         if ss is not None:
             sc = np.ascontiguousarray(np.asarray(scales)[order])
             st = torch.from_numpy(sc.view(np.uint8).reshape(n, -1)).view(ss[1]).reshape(ss[0]).to(dev)
-        return cls(torch.from_numpy(s).to(dev), RowStore(fmt, dim, p, st))
+        return cls(torch.from_numpy(s).to(dev), RowStore(fmt, dim, p, st), ids_checked=True)
 
     @classmethod
     def from_store(cls, ids: torch.Tensor, rows: RowStore, index: torch.Tensor | None = None) -> "DeviceOverlay":

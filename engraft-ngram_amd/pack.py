@@ -48,42 +48,51 @@ def seg_starts_from_segment_ids(segment_ids) -> np.ndarray:
     return starts[np.cumsum(change) - 1].astype(np.int32)
 
 
+def _bin_ranges(lengths: np.ndarray, max_len: int) -> list[tuple[int, int]]:
+    """``[first, end)`` fragment ranges of the bins.  A bin keeps taking the
+    next fragment while the total canonical length stays within ``max_len``;
+    the first fragment that does not fit opens the next bin (no reordering)."""
+    ranges: list[tuple[int, int]] = []
+    first, used = 0, 0
+    for i, ln in enumerate(lengths.tolist()):
+        if i > first and used + ln > max_len:
+            ranges.append((first, i))
+            first, used = i, 0
+        used += ln
+    if lengths.size > first:
+        ranges.append((first, int(lengths.size)))
+    return ranges
+
+
 def pack_fragments(frags: list[list[int]], eos: int, max_len: int) -> list[Packed]:
-    """``engraft/replica/pack.py:99-161``: greedy, in order, no reordering."""
-    canon = [[eos] + list(f) for f in frags]
-    lengths = [len(c) for c in canon]
-    for i, ln in enumerate(lengths):
-        if ln > max_len:
-            raise ValueError(f"pack_fragments: fragment {i} (canonical length {ln}, with EOS) "
-                             f"exceeds max_len={max_len} on its own")
-    bins: list[list[int]] = []
-    cur: list[int] = []
-    cur_len = 0
-    for i, ln in enumerate(lengths):
-        if cur and cur_len + ln > max_len:
-            bins.append(cur)
-            cur, cur_len = [], 0
-        cur.append(i)
-        cur_len += ln
-    if cur:
-        bins.append(cur)
+    """Greedy in-order packing of ``[eos] + frag`` fragments into bins of at
+    most ``max_len`` tokens (``engraft/replica/pack.py:99-161``).
+
+    Per bin, fragment k occupies tokens ``[off_k, off_k + len_k)``; every prefix
+    position (``len(tokens) - 1`` of them) carries its fragment index and its
+    offset inside the fragment, and ``frag_slices[k] = (off_k, off_k + len_k - 1)``
+    leaves out the fragment's last position (the boundary, or the bin's final
+    label).  ``ValueError`` when one fragment alone exceeds ``max_len``."""
+    lengths = np.fromiter((len(f) + 1 for f in frags), dtype=np.int64, count=len(frags))
+    too_long = np.flatnonzero(lengths > max_len)
+    if too_long.size:
+        i = int(too_long[0])
+        raise ValueError(f"pack_fragments: fragment {i} (canonical length {int(lengths[i])}, with EOS) "
+                         f"exceeds max_len={max_len} on its own")
     out: list[Packed] = []
-    for bin_idxs in bins:
-        tok_offsets: list[int] = []
+    for first, end in _bin_ranges(lengths, max_len):
+        lens = lengths[first:end]
+        offs = np.cumsum(lens) - lens
+        total = int(lens.sum())
+        n_prefix = total - 1
         tokens: list[int] = []
-        for fi in bin_idxs:
-            tok_offsets.append(len(tokens))
-            tokens.extend(canon[fi])
-        n_prefix = len(tokens) - 1
-        seg = torch.zeros(n_prefix, dtype=torch.int64)
-        pos = torch.zeros(n_prefix, dtype=torch.float64)
-        frag_slices: list[tuple[int, int]] = []
-        for local_seg, fi in enumerate(bin_idxs):
-            off, ln = tok_offsets[local_seg], lengths[fi]
-            end_all = min(off + ln, n_prefix)
-            if end_all > off:
-                seg[off:end_all] = local_seg
-                pos[off:end_all] = torch.arange(end_all - off, dtype=torch.float64)
-            frag_slices.append((off, off + ln - 1))
-        out.append(Packed(tokens=tokens, segment_ids=seg, positions=pos, frag_slices=frag_slices))
+        for f in frags[first:end]:
+            tokens.append(eos)
+            tokens.extend(f)
+        local = np.arange(end - first, dtype=np.int64)
+        seg = np.repeat(local, lens)[:n_prefix]
+        pos = (np.arange(total, dtype=np.int64) - np.repeat(offs, lens))[:n_prefix]
+        out.append(Packed(tokens=tokens, segment_ids=torch.from_numpy(seg.copy()),
+                          positions=torch.from_numpy(pos.astype(np.float64)),
+                          frag_slices=[(int(o), int(o + ln - 1)) for o, ln in zip(offs, lens)]))
     return out

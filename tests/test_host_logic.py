@@ -45,6 +45,69 @@ def test_pack_greedy_bins_and_oversize():
     assert pack.pack_fragments([], 0, max_len=10) == []
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_pack_invariants_random(seed):
+    """Invariants that fix greedy in-order packing whatever the implementation:
+    the bins concatenate to ``[eos]+frag`` for every fragment in order; no bin
+    exceeds ``max_len``; the next bin's first fragment would not have fitted;
+    every prefix position's segment id and offset point back at its
+    fragment's leading EOS; each frag slice spans the fragment's ``len(frag)``
+    significant positions."""
+    _, pack, _, _ = _pkg()
+    rng = np.random.default_rng(seed)
+    max_len = int(rng.integers(4, 40))
+    frags = [rng.integers(1, 50, size=int(rng.integers(0, max_len))).tolist()
+             for _ in range(int(rng.integers(0, 30)))]
+    eos = 0
+    bins = pack.pack_fragments(frags, eos, max_len)
+    flat = [t for b in bins for t in b.tokens]
+    assert flat == [t for f in frags for t in [eos] + f]
+    k = 0  # fragments consumed so far
+    for i, b in enumerate(bins):
+        assert len(b.tokens) <= max_len
+        n_frag = len(b.frag_slices)
+        assert n_frag >= 1
+        if i + 1 < len(bins):
+            assert len(b.tokens) + len(frags[k + n_frag]) + 1 > max_len
+        n_prefix = len(b.tokens) - 1
+        seg = b.segment_ids.numpy()
+        pos = b.positions.numpy()
+        assert seg.shape == (n_prefix,) and pos.shape == (n_prefix,)
+        for j in range(n_prefix):
+            start = j - int(pos[j])
+            assert b.tokens[start] == eos
+            assert b.frag_slices[int(seg[j])][0] == start
+        for s_i, (a, e) in enumerate(b.frag_slices):
+            assert e - a == len(frags[k + s_i])
+            assert b.tokens[a] == eos
+        k += n_frag
+    assert k == len(frags)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_build_overlay_matches_first_wins_dedup(seed):
+    """build_overlay against the plain specification: every row once,
+    ascending, with the vector it was given (all copies equal)."""
+    lens, _, _, _ = _pkg()
+    rng = np.random.default_rng(seed)
+    truth = {int(r): rng.standard_normal(8).astype(np.float32) for r in rng.choice(1000, 40, replace=False)}
+    keys = list(truth)
+    parts = []
+    for _ in range(int(rng.integers(1, 5))):
+        pick = rng.choice(keys, int(rng.integers(0, 30)))
+        parts.append((np.array(pick, dtype=np.int64), np.stack([truth[int(r)] for r in pick])
+                      if len(pick) else np.zeros((0, 8), np.float32)))
+    rows, data = lens.RowSet.build_overlay(parts)
+    want = sorted({int(x) for r, _ in parts for x in r})
+    assert rows.tolist() == want and rows.dtype == np.int32
+    for r, v in zip(rows.tolist(), data):
+        np.testing.assert_array_equal(v, truth[r])
+    if want:
+        bad = np.stack([truth[want[0]] + 1.0])
+        with pytest.raises(ValueError):
+            lens.RowSet.build_overlay(parts + [(np.array([want[0]]), bad)])
+
+
 def test_pleo_roundtrip_and_bad_magic(tmp_path):
     """tests/test_lens.py:57-72."""
     lens, _, _, _ = _pkg()
