@@ -25,6 +25,8 @@
 // oracle reproduces them exactly.
 #include <string.h>
 
+#include <mutex>
+
 #include "eg_common.h"
 
 namespace eg {
@@ -792,6 +794,39 @@ static int check_common(const void* d_out, const int32_t* rows, int64_t n_pos, i
   return EG_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Static scratch of eg_descent_step_noalloc: the grouping workspace in a
+// file-scope device array, so that callers that may not allocate (code under
+// stream capture, serving loops) still get a descent step.  Every GPU holds its
+// own copy of the array at its own address, for the life of the process.
+// ---------------------------------------------------------------------------
+constexpr size_t kStaticScratchBytes = (size_t)16 << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on the current device, looked up once per
+// device.  The array's name is only a host-side stand-in: kernels must get
+// this address, never the name.
+static int static_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(EG_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(EG_ERR_UNSUPPORTED, "device %d >= %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(EG_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return EG_OK;
+}
+
 }  // namespace eg
 
 using namespace eg;
@@ -925,6 +960,29 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   }
   if (opt->dense) rc = launch_dense(a, st);
   return rc;
+}
+
+size_t eg_descent_step_noalloc_max_bytes(void) { return kStaticScratchBytes; }
+
+int eg_descent_step_noalloc(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos, int32_t heads,
+                            const eg_descent_state* state, const eg_adam* opt, const eg_table* base, void* stream) {
+  EG_CHECK_ARG(state != nullptr && opt != nullptr, "state/opt is NULL");
+  EG_CHECK_ARG(n_pos >= 0 && heads >= 1 && heads <= EG_MAX_HEADS, "n_pos=%lld heads=%d", (long long)n_pos, heads);
+  EG_CHECK_ARG(state->n >= 0 && state->n < (1LL << 31), "n_var=%lld", (long long)state->n);
+  const int64_t n = n_pos * heads;
+  EG_CHECK_ARG(n < (1LL << 31), "n_pos*heads=%lld slots exceed 2^31", (long long)n);
+  const size_t need = workspace_bytes(n, state->n);
+  if (need > kStaticScratchBytes)
+    return set_error(EG_ERR_WORKSPACE,
+                     "eg_descent_step_noalloc: %lld slots and %lld variables need %zu bytes of scratch, more than "
+                     "its static %zu; use eg_descent_step with a workspace",
+                     (long long)n, (long long)state->n, need, kStaticScratchBytes);
+  void* ws = nullptr;
+  const int rc = static_scratch(&ws);
+  if (rc != EG_OK) return rc;
+  // every kernel that reads a part of the scratch first writes or clears it in
+  // this same call (counts by a fill kernel, never hipMemsetAsync)
+  return eg_descent_step(d_out, d_out_f32, rows, n_pos, heads, state, opt, base, ws, kStaticScratchBytes, stream);
 }
 
 int eg_quantize_rows(const float* src, int64_t n, int32_t dim, const int32_t* dst_rows, const eg_table* dst,

@@ -178,7 +178,7 @@ class DescentState:
                   _lib.stream_ptr(self.device))
 
     def step(self, d_out: torch.Tensor, rows: torch.Tensor, *, lr: float, betas=(0.9, 0.999), eps: float = 1e-8,
-             dense: bool = False, mu: float = 0.0, frozen=None) -> None:
+             dense: bool = False, mu: float = 0.0, frozen=None, no_alloc: bool = False) -> None:
         """One optimizer step from ``d_out`` (bf16/f32 ``[n_pos, heads*D]``) and the
         slots' row ids ``rows`` (int32 ``[n_pos, heads]``).  ``mu``: the pull
         term ``mu*||rows_var - rows0||^2/||rows0||^2`` (rows0 = the base table).
@@ -187,7 +187,11 @@ class DescentState:
         masked step of ``engraft/replica/descend.py:262-271`` (``row_mask`` =
         ``~frozen``): their gradient, pull term included, is zero (Adam still
         decays their moments in the dense mode) and their rows are the base
-        table's again after the step."""
+        table's again after the step.
+
+        ``no_alloc``: the step's C call is ``eg_descent_step_noalloc``, which
+        allocates nothing (its scratch is a static 16 MiB array per GPU; larger
+        steps raise ``EgError``)."""
         dev = self.device
         rows = rows.to(device=dev, dtype=torch.int32).contiguous()
         n_pos, heads = rows.shape
@@ -219,11 +223,18 @@ class DescentState:
                 raise ValueError("the pull term needs the base table (DescentState(base=...))")
             opt.l2_coef = float(np.float32(mu) / np.float32(self.rows0_sq))
             base = self.base.c_table
-        ws = _WS.get(n_pos * heads, self.n, dev)
         st = self.c_state()
-        _lib.call("eg_descent_step", _lib.ptr(d_out), _dout_args(d_out), _lib.ptr(rows), n_pos, heads,
-                  ctypes.byref(st), ctypes.byref(opt), ctypes.byref(base) if base is not None else None,
-                  _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
+        if no_alloc:
+            # eg_descent_step_noalloc: the grouping scratch is the library's
+            # static per-GPU array (calls overlapping on one GPU race)
+            _lib.call("eg_descent_step_noalloc", _lib.ptr(d_out), _dout_args(d_out), _lib.ptr(rows), n_pos, heads,
+                      ctypes.byref(st), ctypes.byref(opt), ctypes.byref(base) if base is not None else None,
+                      _lib.stream_ptr(dev))
+        else:
+            ws = _WS.get(n_pos * heads, self.n, dev)
+            _lib.call("eg_descent_step", _lib.ptr(d_out), _dout_args(d_out), _lib.ptr(rows), n_pos, heads,
+                      ctypes.byref(st), ctypes.byref(opt), ctypes.byref(base) if base is not None else None,
+                      _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
         self.step_count += 1  # only once the step is on its way (a rejected call leaves the count)
         if fidx is not None:
             # engraft/replica/descend.py:269-271: the frozen rows are restored after the step

@@ -218,6 +218,21 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
                     int32_t heads, const eg_descent_state* state, const eg_adam* opt,
                     const eg_table* base, void* workspace, size_t workspace_bytes, void* stream);
 
+/* eg_descent_step without a workspace argument: it allocates nothing (no
+ * hipMalloc, no library allocation).  No counterpart in the reference; it is
+ * for callers that cannot allocate device memory (code under HIP stream
+ * capture, tight serving loops).  The grouping scratch is a static device array
+ * of eg_descent_step_noalloc_max_bytes() (16 MiB) per GPU, held until the
+ * process ends; a call whose n_pos*heads slots and state->n variables need more
+ * (eg_backward_workspace_size) fails with EG_ERR_WORKSPACE.  Every call on one
+ * GPU shares that array: calls that overlap on one GPU (two streams, two
+ * threads) race and must be serialised by the caller.  Results are bitwise
+ * those of eg_descent_step. */
+int eg_descent_step_noalloc(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos,
+                            int32_t heads, const eg_descent_state* state, const eg_adam* opt,
+                            const eg_table* base, void* stream);
+size_t eg_descent_step_noalloc_max_bytes(void);
+
 /* The requantisation eg_descent_step applies after its update, on its own:
  * fp32 rows src [n, dim] -> rows dst_rows[i] (i when dst_rows is NULL) of dst
  * (Q8_0 or MXFP8); a dst_rows entry outside dst is skipped.  No counterpart in
