@@ -17,6 +17,7 @@ Prints ONE JSON line on stdout; progress goes to stderr.
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import os
 import sys
@@ -99,29 +100,61 @@ def traffic_from_profile(kernel_key: str):
     return None
 
 
-def copy_ceiling_us(n_bytes_moved: int, dev) -> float:
-    """Time of a plain device copy (torch ``copy_``) that reads and writes
-    ``n_bytes_moved`` bytes in total, warmed up, four buffer pairs rotated (so
-    no repeat is served from the Infinity Cache): the practical ceiling for a
-    kernel that moves that many bytes of HBM traffic."""
+def ramp(fn, seconds: float = 0.3, min_calls: int = 20) -> int:
+    """Untimed launches of ``fn`` for at least ``seconds`` of wall time and
+    ``min_calls`` calls, so that the shader clock has ramped up before a leg is
+    timed whatever ``--warmup`` says; returns the number of calls."""
     import torch
 
-    n = max(1, n_bytes_moved // 8)  # floats per buffer: half the bytes read, half written
-    src = [torch.ones(n, device=dev) for _ in range(4)]
-    dst = [torch.empty(n, device=dev) for _ in range(4)]
-    for i in range(200):
-        dst[i % 4].copy_(src[i % 4])
+    t0 = time.perf_counter()
+    k = 0
+    while k < min_calls or time.perf_counter() - t0 < seconds:
+        fn()
+        k += 1
+        if k % 64 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return k
+
+
+def copy_ceiling_us(n_bytes_moved: int, dev) -> float:
+    """Time of the library's own streaming copy (``eg_stream_copy``: 16-byte
+    non-temporal loads and stores) that reads and writes ``n_bytes_moved``
+    bytes in total, warmed up, four buffer pairs rotated (so no repeat is
+    served from the Infinity Cache): the practical ceiling for a kernel that
+    moves that many bytes of HBM traffic."""
+    import torch
+
+    from engraft_ngram_amd import table as T
+
+    n = max(16, (n_bytes_moved // 2) // 16 * 16)  # bytes per buffer: half read, half written
+    sets = 4 if n < (256 << 20) else 1
+    src = [torch.ones(n // 4, dtype=torch.int32, device=dev) for _ in range(sets)]
+    dst = [torch.empty_like(src[0]) for _ in range(sets)]
+    ramp(lambda: [T.stream_copy(src[i], dst[i]) for i in range(sets)], 0.2)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     best = float("inf")
     for _ in range(5):
         torch.cuda.synchronize()
         a.record()
-        for i in range(50):
-            dst[i % 4].copy_(src[i % 4])
+        for i in range(40):
+            T.stream_copy(src[i % sets], dst[i % sets])
         b.record()
         torch.cuda.synchronize()
-        best = min(best, a.elapsed_time(b) / 50 * 1e3)
+        best = min(best, a.elapsed_time(b) / 40 * 1e3)
     return best
+
+
+def stream_ceilings(dev) -> dict:
+    """The streaming copy's rate at the residual stream alone (134.2 MB), at the
+    forward's HBM traffic (198.4 MB) and at 1 GiB: the ceilings the forward is
+    read against."""
+    out = {}
+    for name, nb in (("residual_stream_134MB", 2 * 67_108_864), ("forward_traffic_198MB", 198_385_667),
+                     ("copy_1GiB", 2 * 536_870_912)):
+        us = copy_ceiling_us(nb, dev)
+        out[name] = {"bytes_moved": nb, "us": us, "tb_per_s": nb / (us * 1e-6) / 1e12}
+    return out
 
 
 def oracle_spec(hp: dict):
@@ -269,7 +302,8 @@ def bench_backward(tab, tokens, steps: int, warmup: int, cpu_s: float = 0.0) -> 
     torch.cuda.synchronize()
     for i in range(warmup):
         state.step(d_res[i % RES_SETS], rows, lr=1e-3)
-    torch.cuda.synchronize()
+    rot = itertools.count()
+    ramp(lambda: state.step(d_res[next(rot) % RES_SETS], rows, lr=1e-3), 0.3)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for i in range(steps):
@@ -291,33 +325,37 @@ def bench_backward(tab, tokens, steps: int, warmup: int, cpu_s: float = 0.0) -> 
 
 
 def cpu_descent(tab, rows, d_res, budget_s: float) -> dict:
-    """The oracle's descent step on the host: slot-ordered scatter
-    (oracle.backward.scatter_grad), the sparse Adam step and the Q8_0
-    requantisation of the touched rows, over the first 2,048 positions of the
-    config-2 batch (32,768 slot gradients)."""
+    """The descent step on the host as the reference's CPU torch path runs it,
+    on the full config-2 inputs (all 16,384 positions): ``index_add_`` of the
+    slot gradients into the touched rows, ``torch.optim.Adam``, Q8_0
+    requantisation, on every thread torch uses; its first step is compared with
+    the device's first step from the same rows (relative error per row)."""
     import numpy as np
     import torch
 
-    from oracle import backward as OB
-    from oracle import formats as OF
+    from engraft_ngram_amd import descent as D
+    from oracle import cpu_baseline as CB
 
-    p = 2048
-    r = rows[:p].cpu().numpy()
-    ids = np.unique(r)
-    d_emb = d_res[:p].float().cpu().numpy()
-    ids_d = torch.from_numpy(ids.astype(np.int32)).to(tab.device).reshape(-1, 1)
-    param = tab.gather(ids_d).float().cpu().numpy().reshape(ids.size, -1)
-    m, v = np.zeros_like(param), np.zeros_like(param)
-
-    def step():
-        grad, hits = OB.scatter_grad(d_emb, r, ids)
-        new_p, _, _ = OB.adam_step(param, grad, m, v, 1, 1e-3, touched=hits > 0)
-        OF.quant_q8_0(new_p)
-
-    n, el = repeat_for(step, budget_s)
-    return {"value": n * r.size / el, "unit": "slot gradients/s", "cores": 1, "kind": "port",
-            "sample": f"first {p} positions of the config-2 batch ({r.size} slots, {ids.size} rows) x {n} steps "
-                      f"in {el:.1f} s: oracle scatter (slot order) + Adam + Q8_0 requant, numpy"}
+    rows_c = rows.cpu()
+    d_c = d_res.cpu()
+    ids = torch.unique(rows_c.reshape(-1).to(torch.int64))
+    param0 = tab.gather(ids.to(torch.int32).to(tab.device).reshape(-1, 1)).float().cpu().reshape(ids.numel(), -1)
+    td = CB.TorchDescent(rows_c, param0, lr=1e-3)
+    td.step(d_c)
+    fresh = D.DescentState.from_rows(tab, rows)
+    fresh.step(d_res, rows, lr=1e-3)
+    dev_p = fresh.master.cpu().numpy()
+    cpu_p = td.param.detach().numpy()
+    scale = np.maximum(np.abs(dev_p).max(axis=1, keepdims=True), 1e-30)
+    rel = float((np.abs(cpu_p - dev_p) / scale).max())
+    del fresh
+    td = CB.TorchDescent(rows_c, param0, lr=1e-3)
+    n, el = repeat_for(lambda: td.step(d_c), budget_s)
+    threads = torch.get_num_threads()
+    return {"value": n * rows_c.numel() / el, "unit": "slot gradients/s", "cores": threads, "kind": "port",
+            "host": host_cpu(), "first_step_max_rel_err_vs_gpu": rel,
+            "sample": f"full config-2 step ({rows_c.numel()} slots, {ids.numel()} rows) x {n} in {el:.1f} s: "
+                      f"torch index_add_ + torch.optim.Adam + Q8_0 requant on {threads} threads"}
 
 
 def bench_decode(tab, steps: int) -> dict:
@@ -344,27 +382,47 @@ def bench_decode(tab, steps: int) -> dict:
     out = torch.empty_like(res)
     ov_bm = DeviceOverlay(ov.ids, store).with_bitmap(tab.n_rows)
 
-    def latencies(overlay) -> list:
+    def latencies(overlay, graphs: bool = False) -> list:
         calls = [T.PreparedForward([tab], tk, res, out=out, overlays=[overlay], decode_ctx=ctx) for tk in toks]
+        run = [c for c in calls]
+        if graphs:
+            # one HIP graph per token set (the decode step captured once, replayed per call)
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for c in calls:
+                    c()
+            torch.cuda.current_stream().wait_stream(side)
+            gs = []
+            for c in calls:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    c()
+                gs.append(g)
+            run = [g.replay for g in gs]
         for i in range(200):
-            calls[i % 64]()
-        torch.cuda.synchronize()
+            run[i % 64]()
+        rot = itertools.count()
+        ramp(lambda: run[next(rot) % 64](), 0.2)
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
         for i, (a, b) in enumerate(evs):
             a.record()
-            calls[i % 64]()
+            run[i % 64]()
             b.record()
         torch.cuda.synchronize()
         return sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
 
     lat_search = latencies(ov)
     lat = latencies(ov_bm)
+    lat_graph = latencies(ov_bm, graphs=True)
     pct = lambda v, q: v[min(len(v) - 1, int(len(v) * q))]
     nbytes = n_seq * (SLOTS * Q8_ROW_BYTES + 2 * 2 * WIDTH + ctx * 8)
     return {"workload": "BASELINE config 3: 256 sequences x (2 context + 1 new token), config-1 table + "
                         "500,000-row Q8_0 overlay resolved per id through its two-level rank bitmap",
             "calls": steps, "us_p50": pct(lat, 0.5), "us_p99": pct(lat, 0.99), "us_min": lat[0],
             "us_p50_binary_search": pct(lat_search, 0.5), "us_p99_binary_search": pct(lat_search, 0.99),
+            "us_p50_graph_replay": pct(lat_graph, 0.5), "us_p99_graph_replay": pct(lat_graph, 0.99),
+            "us_min_graph_replay": lat_graph[0],
             "lookups_per_call": n_seq * SLOTS, "algorithmic_bytes_per_call": nbytes}
 
 
@@ -392,6 +450,8 @@ def bench_config4(steps: int, warmup: int) -> dict:
     calls = [T.PreparedForward(tabs, toks[i], res[i % 2], out=outs[i % 2]) for i in range(8)]
     for i in range(warmup):
         calls[i % 8]()
+    rot = itertools.count()
+    ramp(lambda: calls[next(rot) % 8](), 0.3)
     ev = _Events(4)
     torch.cuda.synchronize()
     for i in range(steps):
@@ -453,6 +513,8 @@ def bench_real_format(steps: int, warmup: int) -> dict:
              for i in range(n_sets)]
     for i in range(warmup):
         calls[i % n_sets]()
+    rot = itertools.count()
+    ramp(lambda: calls[next(rot) % n_sets](), 0.3)
     ev = _Events(4)
     torch.cuda.synchronize()
     for i in range(steps):
@@ -524,6 +586,11 @@ def bench_damage_scan(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
 
     us_search = timed(None)
     us = timed(_lib.ptr(bitmap))
+    counts.zero_()
+    _lib.call("eg_scan_overlay", ctypes.byref(spec), _lib.ptr(tok), 8, n, 0, _lib.ptr(ids_d), ids.size,
+              _lib.ptr(bitmap), n_bits, _lib.ptr(dn_d), _lib.ptr(n_hit), _lib.ptr(dmax), _lib.ptr(dsum),
+              _lib.ptr(counts), _lib.stream_ptr(dev))
+    counts_ref = counts.cpu().numpy()
     # end to end over a four-block corpus (32M tokens): block i+1 uploads while block i is scanned.
     # The first full call pins the host staging buffers (kept by torch's host allocator); the
     # median of three calls after it is the steady state of a long corpus.
@@ -549,13 +616,19 @@ def bench_damage_scan(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
            "s_per_block_end_to_end": wall, "s_per_block_end_to_end_int32_tokens": wall32,
            "hit_positions": int(res["pos"].size)}
     if cpu_s > 0 and hp is not None:
-        from oracle import damage as OD
+        from concurrent.futures import ThreadPoolExecutor
+
+        from oracle import cpu_baseline as CB
         spec = oracle_spec(hp)
-        sample = tokens[:250_000]
-        k, el = repeat_for(lambda: OD.scan_hits(spec, sample, ids, dnorm, block=len(sample)), cpu_s)
-        out["cpu_baseline"] = {"value": k * sample.size / el, "unit": "tokens/s", "cores": 1, "kind": "port",
-                               "sample": f"first 250,000 tokens of the block x {k} in {el:.1f} s: oracle "
-                                         "scan_hits (numpy-uint64 hash, searchsorted, np.add.at)"}
+        threads = torch.get_num_threads()
+        with ThreadPoolExecutor(threads) as pool:
+            k, el = repeat_for(lambda: CB.scan_block_threads(spec, tokens, ids, dnorm, threads, pool), cpu_s)
+            r = CB.scan_block_threads(spec, tokens, ids, dnorm, threads, pool)
+        same = bool(np.array_equal(r["read_count"], counts_ref)) if counts_ref is not None else None
+        out["cpu_baseline"] = {"value": k * n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+                               "host": host_cpu(), "read_counts_match_gpu": same,
+                               "sample": f"the full 8,000,000-token block x {k} in {el:.1f} s: vectorized numpy "
+                                         f"hash + searchsorted + bincount, split over {threads} threads"}
         out["cpu_baseline"]["gpu_speedup"] = out["tokens_per_s_kernel"] / out["cpu_baseline"]["value"]
     return out
 
@@ -673,6 +746,7 @@ def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
         with torch.no_grad():
             for _ in range(warmup):
                 ple.ple_forward(emb, hidden, w, hist, HP, gemm=mode)
+            ramp(lambda: ple.ple_forward(emb, hidden, w, hist, HP, gemm=mode), 0.3)
             ms = timed(lambda: ple.ple_forward(emb, hidden, w, hist, HP, gemm=mode), steps)
             # the two projections alone, for the GEMMs' own rate
             if mode == "fp32":
@@ -683,7 +757,8 @@ def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
         # forward + backward to emb (the descent's use: the weights stay fixed)
         fb = lambda: torch.autograd.grad(ple.ple_forward(emb_v, hidden, w, hist, HP, gemm=mode)[0], emb_v, d_out)
         fb()
-        fb_ms = timed(fb, max(1, steps // 5))
+        ramp(fb, 0.2, 3)
+        fb_ms = timed(fb, max(10, steps // 2))
         res[mode] = {"us_per_step": ms * 1e3, "positions_per_s": t_len / (ms * 1e-3), "gemm_us": gemm_ms * 1e3,
                      "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12, "non_gemm_us": (ms - gemm_ms) * 1e3,
                      "us_forward_backward_to_emb": fb_ms * 1e3}
@@ -769,6 +844,9 @@ def main() -> None:
                                seq_len=SEQ) for i in range(n_sets)]
     torch.cuda.synchronize()
 
+    # clock ramp (time-based, whatever --warmup is), then the W warm-up steps
+    rot = itertools.count()
+    ramp_calls = ramp(lambda: calls[next(rot) % n_sets](), 0.5)
     for i in range(args.warmup):
         calls[i % n_sets]()
     torch.cuda.synchronize()
@@ -798,11 +876,27 @@ def main() -> None:
 
     rows_per_step = n_pos * SLOTS
     fbytes = forward_bytes(n_pos)
-    # a plain device copy moving the kernel's measured HBM traffic (profiles/), for scale
+    # the library's streaming copy moving the kernel's measured HBM traffic (profiles/), for scale
     traffic = traffic_from_profile("forward_q8_cfg1")
     copy_us = copy_ceiling_us(traffic, dev) if traffic else None
     if copy_us:
-        log(f"forward: a device copy moving the same {traffic / 1e6:.1f} MB takes {copy_us:.1f} us")
+        log(f"forward: the streaming copy moving the same {traffic / 1e6:.1f} MB takes {copy_us:.1f} us")
+    ceilings = stream_ceilings(dev)
+    # the same step with the row ids given (eg_forward_rows): the forward without its hash
+    rows_sets = [T.forward([tab], tok_sets[j], res[0], out=outs[0], seq_len=SEQ, return_rows=True)[1]
+                 for j in range(TOKEN_SETS)]
+    rcalls = [T.PreparedForwardRows([tab], rows_sets[i % TOKEN_SETS], res[i % RES_SETS], out=outs[i % RES_SETS])
+              for i in range(n_sets)]
+    rot = itertools.count()
+    ramp(lambda: rcalls[next(rot) % n_sets](), 0.2)
+    start.record()
+    for i in range(args.steps):
+        rcalls[i % n_sets]()
+    end.record()
+    torch.cuda.synchronize()
+    hash_free_us = start.elapsed_time(end) / args.steps * 1e3
+    del rcalls, rows_sets
+    log(f"forward with the row ids given (no hash): {hash_free_us:.1f} us/launch")
     achieved = fbytes / (kernel_ms * 1e-3) / 1e9
     log(f"forward: {ms_per_step * 1e3:.1f} us/step wall, {kernel_ms * 1e3:.1f} us/launch back to back "
         f"(first launch alone {first_ms * 1e3:.1f}), {achieved:.0f} GB/s algorithmic")
@@ -835,6 +929,10 @@ def main() -> None:
             "algorithmic_bytes_per_launch": fbytes, "avg_launch_us": kernel_ms * 1e3,
             "copy_of_same_traffic_us": copy_us,
             "launch_vs_copy_of_same_traffic": (kernel_ms * 1e3 / copy_us) if copy_us else None,
+            "hash_free_us": hash_free_us,
+            "hash_free_frac": fbytes / (hash_free_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "stream_ceilings": ceilings,
+            "clock_ramp_calls": ramp_calls,
         },
         "forward": {
             "rows_per_s": rows_per_step / (kernel_ms * 1e-3),
@@ -848,7 +946,7 @@ def main() -> None:
     # the other legs' CPU baselines (the oracle on a bounded sample, a few seconds each)
     cpu_leg_s = 0.0 if args.no_cpu else min(4.0, args.cpu_seconds)
     if not args.no_backward:
-        bw = bench_backward(tab, tokens, max(1, args.steps // 4), max(1, args.warmup), cpu_leg_s)
+        bw = bench_backward(tab, tokens, max(50, args.steps // 4), max(20, args.warmup // 4), cpu_leg_s)
         result["backward"] = bw
         log_cpu_leg("backward", bw)
         log(f"backward: {bw['us_per_step']:.1f} us/step, {bw['touched_rows']} touched rows, "
@@ -858,8 +956,9 @@ def main() -> None:
         dc = bench_decode(tab, 200)
         result["decode_config3"] = dc
         log(f"decode (config 3): p50 {dc['us_p50']:.1f} us, p99 {dc['us_p99']:.1f} us per call (binary search in "
-            f"place of the bitmap: p50 {dc['us_p50_binary_search']:.1f} us)")
-        c4 = bench_config4(max(1, args.steps // 4), max(1, args.warmup))
+            f"place of the bitmap: p50 {dc['us_p50_binary_search']:.1f} us); as a HIP-graph replay: p50 "
+            f"{dc['us_p50_graph_replay']:.1f} us, p99 {dc['us_p99_graph_replay']:.1f} us")
+        c4 = bench_config4(max(50, args.steps // 4), max(20, args.warmup // 4))
         result["forward_config4"] = c4
         log(f"forward (config 4): {c4['us_per_launch']:.1f} us/launch, {c4['gb_per_s']:.0f} GB/s algorithmic "
             f"({100 * c4['frac_of_hbm_peak']:.1f}% of peak)")
@@ -874,11 +973,11 @@ def main() -> None:
         log_cpu_leg("overlay_emb", oe)
         log(f"OverlayEmb (a8): {oe['us_per_step']:.0f} us per build + backward of a 2,048-token sequence "
             f"({oe['slots_replaced']} slots replaced)")
-        rf = bench_real_format(max(1, args.steps // 4), max(1, args.warmup))
+        rf = bench_real_format(max(50, args.steps // 4), max(20, args.warmup // 4))
         result["forward_real_format"] = rf
         log(f"forward (real IQ4_NL format): {rf['us_per_launch']:.1f} us/launch, {rf['gb_per_s']:.0f} GB/s "
             f"algorithmic ({100 * rf['frac_of_hbm_peak']:.1f}% of peak)")
-        pl = bench_ple(max(1, args.steps // 10), max(1, args.warmup // 10), cpu_leg_s)
+        pl = bench_ple(max(20, args.steps // 10), max(3, args.warmup // 20), cpu_leg_s)
         result["ple_forward"] = pl
         log_cpu_leg("ple_forward", pl)
         log(f"ple_forward: {pl['us_per_step']:.0f} us/step; its two GEMMs alone {pl['gemm_us']:.0f} us "

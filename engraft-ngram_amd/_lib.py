@@ -114,6 +114,9 @@ SIGNATURES = {
                                c_void_p]),
     "eg_forward": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,
                              c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "eg_forward_rows": (c_int32, [c_int32, POINTER(EgTable), POINTER(EgOverlay), c_void_p, c_int64, c_int32,
+                                  c_void_p, c_void_p, c_void_p]),
+    "eg_stream_copy": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p]),
     "eg_ple_gate": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32,
                               c_int32, ctypes.c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_conv_backward": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32,

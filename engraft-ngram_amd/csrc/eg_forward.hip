@@ -227,7 +227,10 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
         hconst[l] = load_head_const(a.hash[l], hh);
       }
   } else {
-    rid[0] = a.rows_in[p * H + hh];
+    // caller's ids, [n_layers, n_pos, heads] (eg_forward's rows_out layout)
+#pragma unroll
+    for (int l = 0; l < MAXL; ++l)
+      if (l < nl) rid[l] = a.rows_in[((int64_t)l * a.n_pos + p) * H + hh];
   }
 
   // 2. The residual stream is read once: streaming (non-temporal) loads, issued
@@ -666,6 +669,39 @@ int eg_forward_timed(int32_t n_layers, const eg_hash_spec* specs, const eg_table
   g_ev_start = nullptr;
   g_ev_stop = nullptr;
   return rc;
+}
+
+int eg_forward_rows(int32_t n_layers, const eg_table* tables, const eg_overlay* overlays, const int32_t* rows,
+                    int64_t n_pos, int32_t heads, const uint16_t* residual, uint16_t* out, void* stream) {
+  EG_CHECK_ARG(n_layers >= 1 && n_layers <= EG_MAX_LAYERS, "n_layers=%d outside [1, %d]", n_layers,
+               EG_MAX_LAYERS);
+  EG_CHECK_ARG(tables != nullptr, "tables is NULL");
+  EG_CHECK_ARG(heads >= 1 && heads <= EG_MAX_HEADS, "heads=%d outside [1, %d]", heads, EG_MAX_HEADS);
+  EG_CHECK_ARG(n_pos >= 0 && n_pos < (1LL << 30), "n_pos=%lld outside [0, 2^30)", (long long)n_pos);
+  EG_CHECK_ARG(n_pos == 0 || (rows != nullptr && residual != nullptr && out != nullptr),
+               "rows/residual/out is NULL");
+  FwdArgs a;
+  memset(&a, 0, sizeof(a));
+  for (int l = 0; l < n_layers; ++l) {
+    int rc = make_table(&tables[l], &a.table[l], "table");
+    if (rc != EG_OK) return rc;
+    EG_CHECK_ARG(tables[l].fmt == tables[0].fmt && tables[l].dim == tables[0].dim,
+                 "layer %d: format/dim differ from layer 0", l);
+    EG_CHECK_ARG(tables[l].n_rows >= 1, "layer %d: n_rows=%lld (at least one row)", l,
+                 (long long)tables[l].n_rows);
+    rc = fill_overlay(overlays ? &overlays[l] : nullptr, a.table[l], &a.ov[l]);
+    if (rc != EG_OK) return rc;
+  }
+  a.rows_in = rows;
+  a.residual = residual;
+  a.out = out;
+  a.n_pos = n_pos;
+  a.n_layers = n_layers;
+  a.heads = heads;
+  a.dim = tables[0].dim;
+  const int W = heads * a.dim;
+  EG_CHECK_ARG(W <= kMaxWidth, "row width %d > %d", W, kMaxWidth);
+  return launch_forward<false>(a, (hipStream_t)stream);
 }
 
 int eg_lookup_rows(const int32_t* rows, int64_t n, const int32_t* ids, const int32_t* index, int64_t n_ids,

@@ -475,6 +475,68 @@ def forward(tables: list[DeviceTable], tokens, residual: torch.Tensor | None = N
     return (call.out, call.rows) if return_rows else call.out
 
 
+class PreparedForwardRows:
+    """``eg_forward_rows`` with its arguments marshalled once: the forward's
+    residual add from row ids already known (int32 ``[n_layers, n, n_heads]``,
+    the layout ``forward(..., return_rows=True)`` returns)."""
+
+    def __init__(self, tables: list[DeviceTable], rows: torch.Tensor, residual: torch.Tensor, *,
+                 out: torch.Tensor | None = None, overlays=None):
+        if not 1 <= len(tables) <= _lib.EG_MAX_LAYERS:
+            raise ValueError(f"{len(tables)} table layers (1..{_lib.EG_MAX_LAYERS} supported)")
+        t0 = tables[0]
+        dev = t0.device
+        nl = len(tables)
+        if rows.dtype != torch.int32 or rows.device != dev or not rows.is_contiguous():
+            raise ValueError("rows must be a contiguous int32 tensor on the table's device")
+        if rows.dim() == 2:
+            rows = rows.unsqueeze(0)
+        if rows.dim() != 3 or rows.shape[0] != nl or rows.shape[2] != t0.n_heads:
+            raise ValueError(f"rows must be [{nl}, n, {t0.n_heads}]")
+        n = int(rows.shape[1])
+        w = t0.n_heads * t0.row_len
+        if residual.dtype != torch.bfloat16 or residual.device != dev or residual.numel() != n * w \
+                or not residual.is_contiguous():
+            raise ValueError(f"residual must be a contiguous bf16 tensor with {n}x{w} elements on {dev}")
+        if out is None:
+            out = torch.empty_like(residual)
+        if out.dtype != torch.bfloat16 or out.numel() != n * w or not out.is_contiguous() or out.device != dev:
+            raise ValueError(f"out must be a contiguous bf16 tensor with {n}x{w} elements")
+        self._ctabs = (_lib.EgTable * nl)(*[t.c_table for t in tables])
+        self._ovs = None
+        if overlays is not None and any(o is not None for o in overlays):
+            self._ovs = (_lib.EgOverlay * nl)(*[(o.c_overlay() if o is not None else _lib.EgOverlay())
+                                                for o in overlays])
+        self.out = out
+        self._keep = (tables, rows, residual, overlays)
+        self._fn = _lib.load().eg_forward_rows
+        self._args = (nl, self._ctabs, self._ovs, _lib.ptr(rows), n, t0.n_heads, _lib.ptr(residual), _lib.ptr(out))
+        self.device = dev
+
+    def __call__(self, stream: int | None = None) -> None:
+        st = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
+        rc = self._fn(*self._args, st)
+        if rc != _lib.EG_OK:
+            _lib.check(rc)
+
+
+def forward_rows(tables: list[DeviceTable], rows: torch.Tensor, residual: torch.Tensor, *,
+                 out: torch.Tensor | None = None, overlays=None) -> torch.Tensor:
+    """The residual add of ``forward`` from known row ids (``eg_forward_rows``)."""
+    call = PreparedForwardRows(tables, rows, residual, out=out, overlays=overlays)
+    call()
+    return call.out
+
+
+def stream_copy(src: torch.Tensor, dst: torch.Tensor) -> None:
+    """``dst[:] = src`` by the library's streaming copy kernel (``eg_stream_copy``):
+    the streaming ceiling the forward's roofline is read against."""
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes or not (src.is_contiguous() and dst.is_contiguous()):
+        raise ValueError("src and dst must be contiguous with the same number of bytes")
+    _lib.call("eg_stream_copy", _lib.ptr(src), _lib.ptr(dst), nbytes, _lib.stream_ptr(src.device))
+
+
 def forward_decode(tables: list[DeviceTable], tokens, residual: torch.Tensor | None = None, *,
                    out: torch.Tensor | None = None, overlays=None, return_rows: bool = False):
     """One decode step: ``tokens`` int ``[n_seq, ctx]`` (each sequence's last

@@ -143,6 +143,24 @@ int eg_forward_decode(int32_t n_layers, const eg_hash_spec* specs, const eg_tabl
                       int32_t ctx_len, const uint16_t* residual, void* out, int32_t* rows_out,
                       void* stream);
 
+/* eg_forward with the row ids given: rows int32 [n_layers, n_pos, heads]
+ * global ids (eg_forward's rows_out layout, e.g. ids hashed once and read
+ * again after an overlay update), the rows read, dequantised, substituted by
+ * the overlays and added to the bf16 residual exactly as eg_forward does; an
+ * id outside its table reads NaN.  It replaces the row reads of
+ * RowSet.from_position for known addresses (engraft/lens.py:133-135,
+ * engraft/table.py:90-109); with the hash left out it is also the hash-free
+ * reference point of eg_forward's time. */
+int eg_forward_rows(int32_t n_layers, const eg_table* tables, const eg_overlay* overlays,
+                    const int32_t* rows, int64_t n_pos, int32_t heads, const uint16_t* residual,
+                    uint16_t* out, void* stream);
+
+/* Streaming copy of `bytes` (a multiple of 16, 16-byte aligned pointers) with
+ * the library's own non-temporal 16-byte load/store kernel.  No counterpart in
+ * the reference: it measures the device's streaming ceiling that the forward
+ * kernels' rooflines are read against. */
+int eg_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
 /* eg_forward with the kernel launched through hipExtLaunchKernelGGL, so that
  * start_event / stop_event (hipEvent_t, created by the caller) hold the
  * dispatch's own start and end timestamps.  No counterpart in the reference:

@@ -19,7 +19,10 @@ dequantisation per head, the concatenated rows added into that position's
 residual row.
 
 Pinned by tests/test_oracle_forward_backward.py (both forms bit-identical to
-``oracle.forward.forward`` on the same inputs).
+``oracle.forward.forward`` on the same inputs) and tests/test_cpu_baselines.py
+(``scan_block_threads`` equal to ``oracle.damage.scan_hits``; ``TorchDescent``
+within 1e-5 of the oracle's scatter + Adam, its requantisation equal to
+``oracle.formats.quant_q8_0``).
 """
 from __future__ import annotations
 
@@ -97,3 +100,83 @@ def forward_q8_literal(spec: H.HashSpec, tokens: np.ndarray, n_positions: int, t
         res = F.bf16_bits_to_f32(np.asarray(residual[t], dtype=np.uint16))
         out[t] = F.f32_to_bf16_bits((res + emb).astype(np.float32))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Descent step and damage scan on every host thread
+# ---------------------------------------------------------------------------
+class TorchDescent:
+    """The descent step as the reference's CPU torch path would run it on the
+    full config-2 inputs (``engraft/replica/seq.py:433-441`` autograd of the
+    ``index_put``, i.e. an ``index_add_`` over the slots; ``torch.optim.Adam``
+    of ``engraft/descend_corpus.py:785-790, 921-947``), then the Q8_0
+    requantisation of the updated rows, on every thread torch uses.
+
+    ``rows`` int ``[P, H]`` global ids; ``param0`` f32 ``[U, dim]`` the true rows
+    of the sorted unique ids; ``lr`` as the GPU leg."""
+
+    def __init__(self, rows: torch.Tensor, param0: torch.Tensor, lr: float):
+        flat = rows.reshape(-1).to(torch.int64)
+        self.ids, self.inv = torch.unique(flat, sorted=True, return_inverse=True)
+        self.dim = int(param0.shape[1])
+        self.param = param0.clone().requires_grad_(True)
+        self.opt = torch.optim.Adam([self.param], lr=lr)
+
+    def step(self, d_res: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        d = d_res.to(torch.float32).reshape(-1, self.dim)
+        grad = torch.zeros_like(self.param, requires_grad=False)
+        grad.index_add_(0, self.inv, d)
+        self.param.grad = grad
+        self.opt.step()
+        with torch.no_grad():
+            blocks = self.param.detach().reshape(-1, self.dim // 32, 32)
+            dq = (blocks.abs().amax(dim=-1) / 127.0).to(torch.float16)
+            d32 = dq.to(torch.float32).unsqueeze(-1)
+            q = torch.where(d32 == 0, torch.zeros_like(blocks), torch.round(blocks / d32))
+            q = q.clamp_(-127, 127).to(torch.int8)
+        return q.reshape(-1, self.dim), dq
+
+
+def _scan_chunk(spec: H.HashSpec, tokens: np.ndarray, lo: int, hi: int, ov: np.ndarray, dnorm: np.ndarray):
+    """Positions [lo, hi) of one block (the block is one sequence): hits per
+    position, their dnorm max and sum, and the overlay indices hit."""
+    hist = spec.ngram_size - 1
+    s0 = max(0, lo - hist)
+    rows = H.ngram_rows_np(spec, tokens[s0:hi])[lo - s0:]
+    idx = np.searchsorted(ov, rows)
+    idx_c = np.minimum(idx, ov.size - 1)
+    matched = ov[idx_c] == rows
+    md = np.where(matched, dnorm[idx_c], np.float32(0.0)).astype(np.float32)
+    n_hit = matched.sum(axis=1).astype(np.int32)
+    dmax = np.where(n_hit > 0, md.max(axis=1), np.float32(0.0)).astype(np.float32)
+    dsum = md.sum(axis=1, dtype=np.float64).astype(np.float32)
+    return n_hit, dmax, dsum, idx_c[matched]
+
+
+def scan_block_threads(spec: H.HashSpec, tokens, ov_sorted, dnorm_sorted, threads: int, pool=None) -> dict:
+    """The damage scan of one token block (``engraft/damage.py:168-224``:
+    vectorized numpy-uint64 hash, ``searchsorted`` membership, per-position
+    count / max / sum, read counts) split into ``threads`` chunks run on a
+    thread pool (numpy releases the GIL inside its array operations).  Returns
+    every position's ``n_hit``, ``dnorm_max``, ``dnorm_sum`` and the overlay
+    rows' ``read_count``."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    tokens = np.asarray(tokens)
+    ov = np.asarray(ov_sorted, dtype=np.int64)
+    dn = np.asarray(dnorm_sorted, dtype=np.float32)
+    n = tokens.shape[0]
+    bounds = np.linspace(0, n, threads + 1).astype(np.int64)
+    own = pool is None
+    pool = pool or ThreadPoolExecutor(threads)
+    try:
+        parts = list(pool.map(lambda i: _scan_chunk(spec, tokens, int(bounds[i]), int(bounds[i + 1]), ov, dn),
+                              range(threads)))
+    finally:
+        if own:
+            pool.shutdown()
+    read_count = np.zeros(ov.size, dtype=np.int64)
+    for p in parts:
+        read_count += np.bincount(p[3], minlength=ov.size)
+    return {"n_hit": np.concatenate([p[0] for p in parts]), "dnorm_max": np.concatenate([p[1] for p in parts]),
+            "dnorm_sum": np.concatenate([p[2] for p in parts]), "read_count": read_count}

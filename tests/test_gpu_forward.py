@@ -204,6 +204,63 @@ def test_forward_two_layer_mxfp8_4gram(cuda):
     G.assert_out_matches(G.bf16_bits(out), FW.residual_add(G.bf16_bits(res), embs))
 
 
+def test_forward_rows_equals_hashed_forward(cuda):
+    """eg_forward_rows (ids given) against the oracle and against eg_forward on
+    the same ids: one Q8_0 layer (the config-1 shape), one layer with an f32
+    overlay, two MXFP8 4-gram layers (width 3072); an id outside the table reads
+    NaN in its head's columns only."""
+    from engraft_ngram_amd import table as T
+    from engraft_ngram_amd.overlay import DeviceOverlay
+    _say("forward_rows")
+    spec = synthetic_spec(n_rows=16 * 3000, seed=121)
+    tab = G.device_table(spec, "q8_0", 16 * 3000, 128, seed=122)
+    tokens = synth.zipf_tokens(123, 2048, 5000)
+    res = G.residual(2048, 2048, seed=124)
+    out, rows = T.forward([tab], torch.from_numpy(tokens), res, return_rows=True)
+    got = T.forward_rows([tab], rows, res)
+    _, _, exp = FW.forward(spec, tokens, G.synth_fetch("q8_0", 122, 128), G.bf16_bits(res))
+    G.assert_out_matches(G.bf16_bits(got), exp)
+    assert torch.equal(got.view(torch.int16), out.view(torch.int16))
+    # overlay resolved per id, as in eg_forward
+    rng = np.random.default_rng(125)
+    r_np = rows[0].cpu().numpy()
+    ov_ids = np.unique(rng.choice(np.unique(r_np), size=200, replace=False)).astype(np.int32)
+    ov = DeviceOverlay.from_rows(ov_ids, (rng.standard_normal((ov_ids.size, 128)) * 0.05).astype(np.float32),
+                                 device=cuda)
+    out_ov = tab.forward(torch.from_numpy(tokens), res, overlay=ov)
+    got_ov = T.forward_rows([tab], rows, res, overlays=[ov])
+    assert torch.equal(got_ov.view(torch.int16), out_ov.view(torch.int16))
+    # an id outside the table: NaN in that head's 128 columns, the rest unchanged
+    bad = rows.clone()
+    bad[0, 5, 3] = 16 * 3000 + 7
+    got_bad = T.forward_rows([tab], bad, res).float().cpu()
+    assert torch.isnan(got_bad[5, 3 * 128:4 * 128]).all()
+    ref = out.float().cpu()
+    keep = torch.ones_like(ref, dtype=torch.bool)
+    keep[5, 3 * 128:4 * 128] = False
+    assert torch.equal(got_bad[keep], ref[keep])
+    # two MXFP8 layers of 24 heads (2-, 3-, 4-grams)
+    specs = [synthetic_spec(n_rows=24 * 3000, seed=126 + l, ngram_size=4) for l in range(2)]
+    tabs = [G.device_table(specs[l], "mxfp8", 24 * 3000, 128, seed=128 + l) for l in range(2)]
+    tok4 = synth.zipf_tokens(130, 1024, 129_280)
+    res4 = G.residual(1024, 3072, seed=131)
+    out4, rows4 = T.forward(tabs, torch.from_numpy(tok4), res4, return_rows=True)
+    got4 = T.forward_rows(tabs, rows4, res4)
+    assert torch.equal(got4.view(torch.int16), out4.view(torch.int16))
+
+
+def test_stream_copy(cuda):
+    """eg_stream_copy: byte-exact copies of several sizes; misaligned sizes refused."""
+    from engraft_ngram_amd import table as T
+    for n in (16, 4096 + 16, 3 * 1024 * 1024 + 48):
+        src = torch.randint(0, 256, (n,), dtype=torch.uint8, device=cuda)
+        dst = torch.zeros_like(src)
+        T.stream_copy(src, dst)
+        assert torch.equal(src, dst)
+    with pytest.raises(ValueError):
+        T.stream_copy(torch.zeros(20, dtype=torch.uint8, device=cuda), torch.zeros(20, dtype=torch.uint8, device=cuda))
+
+
 def test_forward_config1_full_size(cuda):
     """BASELINE config 1 at its own size: 320,000,000-row Q8_0 table (43.5 GB),
     batch 8 x 2048 Zipf(1.1) tokens, residual [16384, 2048] bf16.  Every one of
