@@ -25,6 +25,7 @@
 // oracle reproduces them exactly.
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "eg_common.h"
@@ -72,56 +73,48 @@ __global__ __launch_bounds__(256) void index_build_kernel(const int32_t* __restr
 // ---------------------------------------------------------------------------
 // Keys + per-variable counts
 // ---------------------------------------------------------------------------
-// MODE 0: search the sorted ids; 1: probe the row index; 2: rows already hold
-// variable indices (< 0 or >= n_var: no variable).  cnt[k] += the slots of k;
-// ranks[s] = the count of k before slot s was counted (its place in k's range).
-template <int MODE>
-__global__ __launch_bounds__(kTileThreads) void keys_count_kernel(
-    const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ ids, int64_t n_var, int split_shift,
-    const unsigned long long* __restrict__ index, int index_bits, uint32_t* __restrict__ keys,
-    uint32_t* __restrict__ ranks, uint32_t* __restrict__ cnt) {
-  __shared__ int32_t spl[kSplitMax];
-  const int tid = threadIdx.x;
-  const int ns = MODE == 0 ? (int)((n_var + (1LL << split_shift) - 1) >> split_shift) : 0;
-  if constexpr (MODE == 0) {
-    for (int i = tid; i < ns; i += kTileThreads) spl[i] = ids[(int64_t)i << split_shift];
-    __syncthreads();
-  }
-  // The kTileIPT lookups of a thread run in lockstep and every load is
-  // issued unconditionally (indices clamped in range, results masked): a load
-  // inside a lane-divergent branch would be waited for inside it, which would
-  // serialise the lookups.
-  int32_t row[kTileIPT];
-  bool ok[kTileIPT];
+// Variable index (key) of IPT slots per thread, the slots of thread tid of a
+// block of NT threads at base + r*NT + tid.  MODE 0: search the sorted ids
+// (level 1 in the LDS splitters spl[0, ns)); 1: probe the row index; 2: rows
+// already hold variable indices.  key = n_var: no variable (or idx >= n).
+// The IPT lookups of a thread run in lockstep and every load is issued
+// unconditionally (indices clamped in range, results masked): a load inside a
+// lane-divergent branch would be waited for inside it, which would serialise
+// the lookups.
+template <int MODE, int IPT, int NT>
+__device__ inline void slot_keys(const int32_t* __restrict__ rows, int64_t n, int64_t base, int tid,
+                                 const int32_t* __restrict__ ids, int64_t n_var, int split_shift, const int32_t* spl,
+                                 int ns, const unsigned long long* __restrict__ index, int index_bits,
+                                 uint32_t key[IPT], bool ok[IPT]) {
+  int32_t row[IPT];
 #pragma unroll
-  for (int r = 0; r < kTileIPT; ++r) {
-    const int64_t idx = (int64_t)blockIdx.x * kTile + r * kTileThreads + tid;
+  for (int r = 0; r < IPT; ++r) {
+    const int64_t idx = base + r * NT + tid;
     ok[r] = idx < n;
     row[r] = rows[ok[r] ? idx : n - 1];
   }
-  uint32_t key[kTileIPT];
   if constexpr (MODE == 2) {
 #pragma unroll
-    for (int r = 0; r < kTileIPT; ++r)
-      key[r] = (row[r] >= 0 && (int64_t)row[r] < n_var) ? (uint32_t)row[r] : (uint32_t)n_var;
+    for (int r = 0; r < IPT; ++r)
+      key[r] = (ok[r] && row[r] >= 0 && (int64_t)row[r] < n_var) ? (uint32_t)row[r] : (uint32_t)n_var;
   } else if constexpr (MODE == 1) {
     // probe the row index; the items' probes advance in lockstep
     const uint64_t imask = (1ull << index_bits) - 1ull;
-    uint64_t hslot[kTileIPT];
-    bool done[kTileIPT];
+    uint64_t hslot[IPT];
+    bool done[IPT];
 #pragma unroll
-    for (int r = 0; r < kTileIPT; ++r) {
+    for (int r = 0; r < IPT; ++r) {
       hslot[r] = index_slot(row[r], index_bits);
       done[r] = !ok[r];
       key[r] = (uint32_t)n_var;
     }
     for (uint64_t probe = 0; probe <= imask; ++probe) {
       bool any = false;
-      unsigned long long ent[kTileIPT];
+      unsigned long long ent[IPT];
 #pragma unroll
-      for (int r = 0; r < kTileIPT; ++r) ent[r] = index[hslot[r]];
+      for (int r = 0; r < IPT; ++r) ent[r] = index[hslot[r]];
 #pragma unroll
-      for (int r = 0; r < kTileIPT; ++r) {
+      for (int r = 0; r < IPT; ++r) {
         if (done[r]) continue;
         const unsigned long long e = ent[r];
         if (e == kIndexEmpty) {
@@ -138,42 +131,313 @@ __global__ __launch_bounds__(kTileThreads) void keys_count_kernel(
     }
   } else {
     // level 1 (LDS): lo = number of splitters <= row
-    int lo[kTileIPT];
+    int lo[IPT];
 #pragma unroll
-    for (int r = 0; r < kTileIPT; ++r) lo[r] = 0;
+    for (int r = 0; r < IPT; ++r) lo[r] = 0;
     for (int step = kSplitMax; step >= 1; step >>= 1) {
 #pragma unroll
-      for (int r = 0; r < kTileIPT; ++r)
+      for (int r = 0; r < IPT; ++r)
         if (lo[r] + step <= ns && spl[lo[r] + step - 1] <= row[r]) lo[r] += step;
     }
     // level 2 (global): the last id <= row inside that splitter's window
     const int64_t win = 1LL << split_shift;
-    int64_t pos[kTileIPT], end[kTileIPT];
+    int64_t pos[IPT], end[IPT];
 #pragma unroll
-    for (int r = 0; r < kTileIPT; ++r) {
+    for (int r = 0; r < IPT; ++r) {
       pos[r] = lo[r] > 0 ? ((int64_t)(lo[r] - 1) << split_shift) : 0;
       end[r] = lo[r] > 0 ? min(pos[r] + win, n_var) : 0;
     }
     for (int64_t step = win >> 1; step >= 1; step >>= 1) {
-      int32_t probe[kTileIPT];
+      int32_t probe[IPT];
 #pragma unroll
-      for (int r = 0; r < kTileIPT; ++r) probe[r] = ids[min(pos[r] + step, n_var - 1)];
+      for (int r = 0; r < IPT; ++r) probe[r] = ids[min(pos[r] + step, n_var - 1)];
 #pragma unroll
-      for (int r = 0; r < kTileIPT; ++r)
+      for (int r = 0; r < IPT; ++r)
         if (pos[r] + step < end[r] && probe[r] <= row[r]) pos[r] += step;
     }
 #pragma unroll
-    for (int r = 0; r < kTileIPT; ++r) {
+    for (int r = 0; r < IPT; ++r) {
       const int32_t at = ids[pos[r]];
       key[r] = (ok[r] && lo[r] > 0 && at == row[r]) ? (uint32_t)pos[r] : (uint32_t)n_var;
     }
   }
+}
+
+// Splitters of the sorted ids for slot_keys<0>: every 2^split_shift-th id.
+__device__ inline int load_splitters(const int32_t* __restrict__ ids, int64_t n_var, int split_shift, int32_t* spl,
+                                     int tid, int nt) {
+  const int ns = (int)((n_var + (1LL << split_shift) - 1) >> split_shift);
+  for (int i = tid; i < ns; i += nt) spl[i] = ids[(int64_t)i << split_shift];
+  return ns;
+}
+
+// Keys + per-variable counts (the grouping for more than kBucketsMax buckets).
+// cnt[k] += the slots of k; ranks[s] = the count of k before slot s was
+// counted (its place in k's range).
+template <int MODE>
+__global__ __launch_bounds__(kTileThreads) void keys_count_kernel(
+    const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ ids, int64_t n_var, int split_shift,
+    const unsigned long long* __restrict__ index, int index_bits, uint32_t* __restrict__ keys,
+    uint32_t* __restrict__ ranks, uint32_t* __restrict__ cnt) {
+  __shared__ int32_t spl[kSplitMax];
+  const int tid = threadIdx.x;
+  int ns = 0;
+  if constexpr (MODE == 0) {
+    ns = load_splitters(ids, n_var, split_shift, spl, tid, kTileThreads);
+    __syncthreads();
+  }
+  uint32_t key[kTileIPT];
+  bool ok[kTileIPT];
+  slot_keys<MODE, kTileIPT, kTileThreads>(rows, n, (int64_t)blockIdx.x * kTile, tid, ids, n_var, split_shift, spl, ns,
+                                          index, index_bits, key, ok);
 #pragma unroll
   for (int r = 0; r < kTileIPT; ++r) {
     if (!ok[r]) continue;
     const int64_t idx = (int64_t)blockIdx.x * kTile + r * kTileThreads + tid;
     keys[idx] = key[r];
     if ((int64_t)key[r] < n_var) ranks[idx] = atomicAdd(&cnt[key[r]], 1u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Bucketed grouping: two launches, one global atomic per bucket
+// ---------------------------------------------------------------------------
+// Bucket b holds the variables [b << bs, (b + 1) << bs).
+// tile_sort_kernel: tile t (kGroupTile slots) computes its slots' keys and
+//   counting-sorts its (key, slot) pairs by bucket in LDS into its own region
+//   pairs[t * kGroupTile, ...), writing per bucket the segment seg[t][b] =
+//   (count, tile-local offset).
+// bucket_ranges_kernel: bucket b gathers its pairs from every tile, counts
+//   its keys in LDS and writes every variable's range [start, end) and its
+//   slot ids (in no particular order inside a range: the reduction orders
+//   them), and lists the variables of more than kPiece slots.  Its region of
+//   the slots array, and of the list, follows those of the earlier buckets:
+//   every bucket publishes its totals, tagged with the call's epoch, and adds
+//   up the earlier buckets' (no same-address atomics, which serialise).
+constexpr int kGroupThreads = 512;
+constexpr int kGroupIPT = 2;
+constexpr int kGroupTile = kGroupThreads * kGroupIPT;  // slots per tile
+constexpr int kBucketsMax = 1024;
+constexpr int kBucketKeysLog2Max = 11;                 // at most 2048 variables per bucket
+constexpr int kRangeThreads = 256;
+constexpr int kRangeTilesMax = 4 * kRangeThreads;   // tiles bucket_ranges_kernel reads (4 per thread)
+
+// Exclusive scan of x[0, len) in LDS by a block of NT threads (len <= PER * NT).
+template <int NT, int PER>
+__device__ inline void lds_exclusive_scan(uint32_t* x, int len, uint32_t* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t v[PER];
+  uint32_t t = 0;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = tid * PER + u;
+    v[u] = i < len ? x[i] : 0u;
+    t += v[u];
+  }
+  uint32_t incl = t;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  uint32_t before = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w)
+    if (w < wave) before += wsum[w];
+  uint32_t run = before + incl - t;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = tid * PER + u;
+    if (i < len) x[i] = run;
+    run += v[u];
+  }
+  __syncthreads();
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kGroupThreads) void tile_sort_kernel(
+    const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ ids, int64_t n_var, int split_shift,
+    const unsigned long long* __restrict__ index, int index_bits, int bs, int nb, int64_t n_tiles,
+    unsigned long long* __restrict__ pairs, u32x2* __restrict__ seg) {
+  __shared__ int32_t spl[MODE == 0 ? kSplitMax : 1];
+  __shared__ uint32_t bh[kBucketsMax];
+  __shared__ uint32_t wsum[kGroupThreads / 64];
+  const int tid = threadIdx.x;
+  const int64_t t = blockIdx.x;
+  for (int i = tid; i < nb; i += kGroupThreads) bh[i] = 0u;
+  int ns = 0;
+  if constexpr (MODE == 0) ns = load_splitters(ids, n_var, split_shift, spl, tid, kGroupThreads);
+  __syncthreads();
+  uint32_t key[kGroupIPT];
+  bool ok[kGroupIPT];
+  slot_keys<MODE, kGroupIPT, kGroupThreads>(rows, n, t * kGroupTile, tid, ids, n_var, split_shift, spl, ns, index,
+                                            index_bits, key, ok);
+  uint32_t rank[kGroupIPT];
+#pragma unroll
+  for (int r = 0; r < kGroupIPT; ++r) {
+    rank[r] = 0u;
+    if (ok[r] && (int64_t)key[r] < n_var) rank[r] = atomicAdd(&bh[key[r] >> bs], 1u);
+  }
+  __syncthreads();
+  uint32_t cnt_b[kBucketsMax / kGroupThreads];
+#pragma unroll
+  for (int u = 0; u < kBucketsMax / kGroupThreads; ++u) {
+    const int b = tid + u * kGroupThreads;
+    cnt_b[u] = b < nb ? bh[b] : 0u;
+  }
+  __syncthreads();
+  lds_exclusive_scan<kGroupThreads, kBucketsMax / kGroupThreads>(bh, nb, wsum);
+#pragma unroll
+  for (int u = 0; u < kBucketsMax / kGroupThreads; ++u) {
+    const int b = tid + u * kGroupThreads;
+    if (b < nb) seg[t * nb + b] = u32x2{cnt_b[u], bh[b]};
+  }
+#pragma unroll
+  for (int r = 0; r < kGroupIPT; ++r) {
+    if (ok[r] && (int64_t)key[r] < n_var) {
+      const int64_t s = t * kGroupTile + r * kGroupThreads + tid;
+      pairs[t * kGroupTile + bh[key[r] >> bs] + rank[r]] = ((unsigned long long)key[r] << 32) | (uint32_t)s;
+    }
+  }
+}
+
+// Sum over buckets [0, b) of the values they publish in pub[] tagged with this
+// call's epoch (the high 32 bits), read coherently across XCDs.  Only earlier
+// buckets are waited for: workgroups are dispatched in order, so those are
+// already resident and publish without waiting on this one.  The wait is
+// bounded; past the bound the value read is used as it is.
+__device__ inline uint32_t sum_published(const unsigned long long* pub, int64_t b, uint32_t epoch, uint32_t* wsum) {
+  const int tid = threadIdx.x;
+  uint32_t part = 0;
+  for (int64_t i = tid; i < b; i += kRangeThreads) {
+    unsigned long long v = 0;
+    for (int spin = 0; spin < (1 << 22); ++spin) {
+      v = __hip_atomic_load(&pub[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((uint32_t)(v >> 32) == epoch) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    part += (uint32_t)v;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
+  __syncthreads();
+  if ((tid & 63) == 0) wsum[tid >> 6] = part;
+  __syncthreads();
+  uint32_t total = 0;
+#pragma unroll
+  for (int w = 0; w < kRangeThreads / 64; ++w) total += wsum[w];
+  __syncthreads();
+  return total;
+}
+
+__global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
+    const unsigned long long* __restrict__ pairs, const u32x2* __restrict__ seg, int64_t n_tiles, int nb, int bs,
+    int64_t n_var, uint32_t epoch, unsigned long long* __restrict__ pub_total,
+    unsigned long long* __restrict__ pub_long, uint32_t* __restrict__ n_long, uint32_t* __restrict__ start,
+    uint32_t* __restrict__ end, uint32_t* __restrict__ slots, uint32_t* __restrict__ long_list) {
+  constexpr int kKeys = 1 << kBucketKeysLog2Max;
+  constexpr int kKeep = 4;                         // pairs of one tile a thread holds in registers
+  __shared__ uint32_t cnt[kKeys];                  // pairs held in registers, per variable
+  __shared__ uint32_t over[kKeys];                 // pairs beyond kKeep of a tile, per variable
+  __shared__ uint32_t lst[kKeys];
+  __shared__ uint32_t lng[kKeys];                  // the bucket's variables of more than kPiece slots
+  __shared__ uint32_t wsum[kRangeThreads / 64];
+  __shared__ uint32_t n_long_b;
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  const int64_t key0 = b << bs;
+  const int nkeys = (int)min((int64_t)1 << bs, n_var - key0);
+  for (int i = tid; i < nkeys; i += kRangeThreads) {
+    cnt[i] = 0u;
+    over[i] = 0u;
+  }
+  // this thread's tiles: (count, offset) of the bucket's segment in each
+  constexpr int kTilesPerThread = 4;  // n_tiles <= kTilesPerThread * kRangeThreads (host checks)
+  u32x2 sg[kTilesPerThread];
+  uint32_t part = 0;
+#pragma unroll
+  for (int j = 0; j < kTilesPerThread; ++j) {
+    const int64_t t = tid + (int64_t)j * kRangeThreads;
+    sg[j] = t < n_tiles ? seg[t * nb + b] : u32x2{0u, 0u};
+    part += sg[j].x;
+  }
+  // the bucket's slot total, published for the later buckets; its region of
+  // the slots array starts at the totals of the earlier buckets
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
+  if ((tid & 63) == 0) wsum[tid >> 6] = part;
+  if (tid == 0) n_long_b = 0u;
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t total = 0;
+#pragma unroll
+    for (int w = 0; w < kRangeThreads / 64; ++w) total += wsum[w];
+    __hip_atomic_store(&pub_total[b], ((unsigned long long)epoch << 32) | total, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // the first kKeep pairs of each tile segment: loaded together, counted, and
+  // given their rank among the variable's register-held pairs
+  unsigned long long pr[kTilesPerThread][kKeep];
+  uint32_t rk[kTilesPerThread][kKeep];
+#pragma unroll
+  for (int j = 0; j < kTilesPerThread; ++j) {
+    const int64_t t = tid + (int64_t)j * kRangeThreads;
+    // an empty segment's offset may equal the tile's size: read the tile's first pair instead (unused)
+    const unsigned long long* src = pairs + (t < n_tiles ? t : 0) * kGroupTile + (sg[j].x ? sg[j].y : 0u);
+#pragma unroll
+    for (int e = 0; e < kKeep; ++e) pr[j][e] = src[(uint32_t)e < sg[j].x ? e : 0];
+  }
+#pragma unroll
+  for (int j = 0; j < kTilesPerThread; ++j)
+#pragma unroll
+    for (int e = 0; e < kKeep; ++e)
+      rk[j][e] = ((uint32_t)e < sg[j].x) ? atomicAdd(&cnt[(uint32_t)(pr[j][e] >> 32) - (uint32_t)key0], 1u) : 0u;
+  // the rest of a long segment (a variable hit many times in one tile): counted apart
+#pragma unroll
+  for (int j = 0; j < kTilesPerThread; ++j) {
+    if (sg[j].x <= (uint32_t)kKeep) continue;
+    const unsigned long long* src = pairs + (tid + (int64_t)j * kRangeThreads) * kGroupTile + sg[j].y;
+    for (uint32_t e = kKeep; e < sg[j].x; ++e) atomicAdd(&over[(uint32_t)(src[e] >> 32) - (uint32_t)key0], 1u);
+  }
+  const uint32_t base = sum_published(pub_total, b, epoch, wsum);  // (its barriers also close the counting)
+  for (int i = tid; i < nkeys; i += kRangeThreads) lst[i] = cnt[i] + over[i];
+  __syncthreads();
+  lds_exclusive_scan<kRangeThreads, kKeys / kRangeThreads>(lst, nkeys, wsum);
+  for (int i = tid; i < nkeys; i += kRangeThreads) {
+    const uint32_t c = cnt[i] + over[i];
+    start[key0 + i] = base + lst[i];
+    end[key0 + i] = base + lst[i] + c;
+    if (c > (uint32_t)kPiece) lng[atomicAdd(&n_long_b, 1u)] = (uint32_t)(key0 + i);
+    over[i] = lst[i] + cnt[i];  // where the variable's overflow pairs go
+  }
+  __syncthreads();
+  // the variables of more than kPiece slots, listed after the earlier buckets' ones
+  if (tid == 0)
+    __hip_atomic_store(&pub_long[b], ((unsigned long long)epoch << 32) | n_long_b, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t lbase = sum_published(pub_long, b, epoch, wsum);
+  if (b == nb - 1 && tid == 0) *n_long = lbase + n_long_b;
+  for (uint32_t j = tid; j < n_long_b; j += kRangeThreads) long_list[lbase + j] = lng[j];
+  // every slot id at its variable's place (the order inside a range is free)
+#pragma unroll
+  for (int j = 0; j < kTilesPerThread; ++j)
+#pragma unroll
+    for (int e = 0; e < kKeep; ++e)
+      if ((uint32_t)e < sg[j].x) {
+        const uint32_t i = (uint32_t)(pr[j][e] >> 32) - (uint32_t)key0;
+        slots[base + lst[i] + rk[j][e]] = (uint32_t)pr[j][e];
+      }
+#pragma unroll
+  for (int j = 0; j < kTilesPerThread; ++j) {
+    if (sg[j].x <= (uint32_t)kKeep) continue;
+    const unsigned long long* src = pairs + (tid + (int64_t)j * kRangeThreads) * kGroupTile + sg[j].y;
+    for (uint32_t e = kKeep; e < sg[j].x; ++e) {
+      const unsigned long long q = src[e];
+      const uint32_t i = (uint32_t)(q >> 32) - (uint32_t)key0;
+      slots[base + atomicAdd(&over[i], 1u)] = (uint32_t)q;
+    }
   }
 }
 
@@ -299,7 +563,8 @@ __device__ void bitonic_sort(Ptr x, int64_t len) {
 // Segmented reduction + optimizer
 // ---------------------------------------------------------------------------
 struct SegArgs {
-  const uint32_t* start;      // [n_var + 1] start of each variable's range in slots (then the total)
+  const uint32_t* start;      // [n_var] start of each variable's range in slots
+  const uint32_t* end;        // [n_var] its end
   const uint32_t* slots;      // slot ids grouped by variable (CSR)
   const uint32_t* long_list;  // variables with more than kPiece slots
   const uint32_t* n_long;     // their number
@@ -560,7 +825,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
     const int grp = threadIdx.x >> 5;
     const uint32_t key = a.long_list[blockIdx.x];
     const int64_t lo = a.start[key];
-    const int64_t hi = a.start[key + 1];
+    const int64_t hi = a.end[key];
     const int64_t len = hi - lo;
     float p[VPL], m[VPL], v[VPL];
     if (ADAM && grp == 0) {  // independent of the gradient: fetched first
@@ -610,7 +875,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
   const int64_t k = (((int64_t)blockIdx.x - n_long_blocks) * 256 + threadIdx.x) >> 5;
   if (k >= a.n_var) return;  // uniform per group
   const int64_t lo = a.start[k];
-  const int64_t len = (int64_t)a.start[k + 1] - lo;
+  const int64_t len = (int64_t)a.end[k] - lo;
   if (len == 0 || len > kPiece) return;  // not hit, or a long range (its own workgroup)
   float p[VPL], m[VPL], v[VPL];
   if constexpr (ADAM) {  // the state rows do not depend on the gradient: fetch them first
@@ -664,13 +929,48 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+// How a call groups its slots: the bucketed path (two launches) whenever the
+// variables fit kBucketsMax buckets of at most 2^kBucketKeysLog2Max, the
+// counting path (counts by global atomics, scan, fill) otherwise.
+struct GroupPlan {
+  bool bucketed;
+  int bs;           // bucket b holds the variables [b << bs, (b + 1) << bs)
+  int nb;           // buckets
+  int64_t n_tiles;  // tiles of kGroupTile slots
+};
+
+static std::atomic<uint32_t> g_epoch{0u};
+
+static GroupPlan plan_for(int64_t n, int64_t n_var) {
+  GroupPlan g{false, 0, 0, 0};
+  if (n_var < 1 || n_var > ((int64_t)kBucketsMax << kBucketKeysLog2Max)) return g;
+  if ((n + kGroupTile - 1) / kGroupTile > kRangeTilesMax) return g;
+  int bs = 0;
+  while (((n_var + (1LL << bs) - 1) >> bs) > kBucketsMax) ++bs;
+  g.bucketed = true;
+  g.bs = bs;
+  g.nb = (int)((n_var + (1LL << bs) - 1) >> bs);
+  g.n_tiles = (n + kGroupTile - 1) / kGroupTile;
+  return g;
+}
+
 struct Workspace {
+  // both paths
+  uint32_t* slots;      // [n] slot ids grouped by variable
+  uint32_t* start;      // [n_var] range start of every variable
+  uint32_t* end;        // [n_var] range end (the counting path: start + 1)
+  uint32_t* long_list;  // variables of more than kPiece slots
+  uint32_t* n_long;     // their number
+  // the counting path
   uint32_t* keys;       // [n] variable of every slot (n_var: none)
   uint32_t* ranks;      // [n] place of every slot in its variable's range
-  uint32_t* slots;      // [n] slot ids grouped by variable
   uint32_t* off;        // [n_var + 2] counts -> range starts ([n_var]: the total); [n_var + 1]: long-list length
   uint32_t* partial;    // scan chunk totals
-  uint32_t* long_list;  // variables of more than kPiece slots
+  // the bucketed path
+  unsigned long long* pairs;  // [n_tiles * kGroupTile] (key << 32 | slot), bucket-sorted per tile
+  u32x2* seg;                 // [n_tiles, nb] (slots of bucket b in tile t, their offset in t's region)
+  uint32_t* counters;         // [1]: the long-list length
+  unsigned long long* pub;    // [2 * nb]: every bucket's slot total, then its long-list length (epoch-tagged)
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -679,48 +979,83 @@ static int64_t n_long_max(int64_t n) { return n / (kPiece + 1) + 1; }
 
 static int64_t scan_chunks(int64_t n_var) { return (n_var + kScanChunk - 1) / kScanChunk; }
 
-static size_t workspace_bytes(int64_t n, int64_t n_var) {
-  return 3 * align256((size_t)n * 4) + align256((size_t)(n_var + 2) * 4) +
-         align256((size_t)(scan_chunks(n_var + 1) + 1) * 4) + align256((size_t)n_long_max(n) * 4);
+// Lays the workspace out (ws == nullptr: only measures it); returns its size.
+static size_t carve(void* ws, int64_t n, int64_t n_var, Workspace* out) {
+  const GroupPlan g = plan_for(n, n_var);
+  Workspace w;
+  memset(&w, 0, sizeof(w));
+  char* base = (char*)ws;
+  size_t at = 0;
+  auto take = [&](size_t bytes) {
+    void* p = base ? (void*)(base + at) : nullptr;
+    at += align256(bytes);
+    return p;
+  };
+  w.slots = (uint32_t*)take((size_t)n * 4);
+  w.long_list = (uint32_t*)take((size_t)n_long_max(n) * 4);
+  if (g.bucketed) {
+    w.start = (uint32_t*)take((size_t)n_var * 4);
+    w.end = (uint32_t*)take((size_t)n_var * 4);
+    w.pairs = (unsigned long long*)take((size_t)g.n_tiles * kGroupTile * 8);
+    w.seg = (u32x2*)take((size_t)g.n_tiles * g.nb * 8);
+    w.counters = (uint32_t*)take(4);
+    w.n_long = w.counters;
+    w.pub = (unsigned long long*)take((size_t)2 * g.nb * 8);
+  } else {
+    w.keys = (uint32_t*)take((size_t)n * 4);
+    w.ranks = (uint32_t*)take((size_t)n * 4);
+    w.off = (uint32_t*)take((size_t)(n_var + 2) * 4);
+    w.partial = (uint32_t*)take((size_t)(scan_chunks(n_var + 1) + 1) * 4);
+    w.start = w.off;
+    w.end = w.off ? w.off + 1 : nullptr;
+    w.n_long = w.off ? w.off + n_var + 1 : nullptr;
+  }
+  if (out) *out = w;
+  return at;
 }
 
-static Workspace carve(void* ws, int64_t n, int64_t n_var) {
-  Workspace w;
-  char* p = (char*)ws;
-  w.keys = (uint32_t*)p;
-  p += align256((size_t)n * 4);
-  w.ranks = (uint32_t*)p;
-  p += align256((size_t)n * 4);
-  w.slots = (uint32_t*)p;
-  p += align256((size_t)n * 4);
-  w.off = (uint32_t*)p;
-  p += align256((size_t)(n_var + 2) * 4);
-  w.partial = (uint32_t*)p;
-  p += align256((size_t)(scan_chunks(n_var + 1) + 1) * 4);
-  w.long_list = (uint32_t*)p;
-  return w;
-}
+static size_t workspace_bytes(int64_t n, int64_t n_var) { return carve(nullptr, n, n_var, nullptr); }
 
 static unsigned grid_for(int64_t items, int64_t per_block, int64_t cap) {
   const int64_t b = (items + per_block - 1) / per_block;
   return (unsigned)(b < 1 ? 1 : (b > cap ? cap : b));
 }
 
-// Keys, counts, offsets and the CSR fill.
+// Every variable's range [start, end) of slot ids, and the long list.
 static int group_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64_t n_var, const int64_t* index,
                        int64_t index_capacity, bool direct, const Workspace& w, hipStream_t st) {
   int split_shift = 0;
   while (((n_var + (1LL << split_shift) - 1) >> split_shift) > kSplitMax) ++split_shift;
+  int ib = 0;
+  while ((1LL << ib) < index_capacity) ++ib;
+  const int mode = direct ? 2 : (index != nullptr ? 1 : 0);
+  const unsigned long long* idx = (const unsigned long long*)index;
+  const GroupPlan g = plan_for(n, n_var);
+  if (g.bucketed) {
+    const dim3 tgrid((unsigned)g.n_tiles);
+#define EG_TILE_SORT(M)                                                                                            \
+  hipLaunchKernelGGL(tile_sort_kernel<M>, tgrid, dim3(kGroupThreads), 0, st, rows, n, ids, n_var, split_shift, idx, \
+                     ib, g.bs, g.nb, g.n_tiles, w.pairs, w.seg)
+    if (mode == 2) EG_TILE_SORT(2);
+    else if (mode == 1) EG_TILE_SORT(1);
+    else EG_TILE_SORT(0);
+#undef EG_TILE_SORT
+    // a fresh epoch per call: the published values of earlier calls never match
+    uint32_t epoch = g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
+    if (epoch == 0u) epoch = g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
+    hipLaunchKernelGGL(bucket_ranges_kernel, dim3((unsigned)g.nb), dim3(kRangeThreads), 0, st, w.pairs, w.seg,
+                       g.n_tiles, g.nb, g.bs, n_var, epoch, w.pub, w.pub + g.nb, w.n_long, w.start, w.end, w.slots,
+                       w.long_list);
+    return launch_status("slot grouping kernels");
+  }
   hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n_var + 2, 256, 1024)), dim3(256), 0, st, w.off, n_var + 2);
   const dim3 kgrid((unsigned)((n + kTile - 1) / kTile));
-  if (direct) {
+  if (mode == 2) {
     hipLaunchKernelGGL(keys_count_kernel<2>, kgrid, dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
                        (const unsigned long long*)nullptr, 0, w.keys, w.ranks, w.off);
-  } else if (index != nullptr) {
-    int ib = 0;
-    while ((1LL << ib) < index_capacity) ++ib;
-    hipLaunchKernelGGL(keys_count_kernel<1>, kgrid, dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
-                       (const unsigned long long*)index, ib, w.keys, w.ranks, w.off);
+  } else if (mode == 1) {
+    hipLaunchKernelGGL(keys_count_kernel<1>, kgrid, dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0, idx, ib,
+                       w.keys, w.ranks, w.off);
   } else {
     hipLaunchKernelGGL(keys_count_kernel<0>, kgrid, dim3(kTileThreads), 0, st, rows, n, ids, n_var, split_shift,
                        (const unsigned long long*)nullptr, 0, w.keys, w.ranks, w.off);
@@ -736,10 +1071,11 @@ static int group_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64
 }
 
 static void fill_seg(SegArgs* a, const Workspace& w, int64_t n, int64_t n_var) {
-  a->start = w.off;
+  a->start = w.start;
+  a->end = w.end;
   a->slots = w.slots;
   a->long_list = w.long_list;
-  a->n_long = w.off + n_var + 1;
+  a->n_long = w.n_long;
   a->n = n;
   a->n_var = n_var;
 }
@@ -864,7 +1200,8 @@ static int scatter_grad_impl(const void* d_out, int32_t d_out_f32, const int32_t
   const int64_t n = n_pos * heads;
   if (n == 0 || n_var == 0) return EG_OK;
   hipStream_t st = (hipStream_t)stream;
-  const Workspace w = carve(workspace, n, n_var);
+  Workspace w;
+  carve(workspace, n, n_var, &w);
   rc = group_slots(rows, n, ids, n_var, nullptr, 0, direct, w, st);
   if (rc != EG_OK) return rc;
   SegArgs a;
@@ -926,7 +1263,8 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   const int64_t n = n_pos * heads;
   if (state->n == 0) return EG_OK;
   hipStream_t st = (hipStream_t)stream;
-  const Workspace w = carve(workspace, n, state->n);
+  Workspace w;
+  carve(workspace, n, state->n, &w);
   if (n > 0) {
     rc = group_slots(rows, n, state->ids, state->n, state->index, state->index_capacity, false, w, st);
     if (rc != EG_OK) return rc;
