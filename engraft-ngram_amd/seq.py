@@ -1,7 +1,9 @@
 """The differentiable sequence overlay and the per-position true embedding, on
 the device: the drop-ins for ``OverlayEmb`` / ``overlay_key_len``
 (``engraft/replica/seq.py:222-444``) and ``Replica.ple_true_emb``
-(``engraft/replica/model.py:473-495``).
+(``engraft/replica/model.py:473-495``), and the sequence seam around the
+model: ``PatchStats``, ``ple_emb_patched``, ``seq_forward``, ``seq_step``
+(``engraft/replica/seq.py:453-637, 809-921, 1340-1470``).
 
 ``OverlayEmb.build`` does in a few launches what the reference does with a
 per-position Python loop:
@@ -26,8 +28,10 @@ step's scatter).
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import dataclasses
+import time
 
 import numpy as np
 import torch
@@ -285,3 +289,120 @@ def ple_true_emb_range(table, tokens, start: int, end: int, overlay=None, seg_st
     tok = tokens if isinstance(tokens, torch.Tensor) else torch.as_tensor(np.asarray(tokens, dtype=np.int64))
     rows = table.rows(tok[:end], seg_start=None if seg_start is None else np.asarray(seg_start)[:end])
     return table.gather(rows[start:end].contiguous(), overlay=_as_overlay(table, overlay))
+
+
+# ---------------------------------------------------------------------------------------------
+# The sequence seam: the model reads its PLE rows through replica.ple_true_emb
+# (engraft/replica/model.py:845-853); a sequence forward shadows that method with
+# slices of one precomputed OverlayEmb (engraft/replica/seq.py:570-637, 809-921,
+# 1340-1470).  Only the table path's half is here: the model's own patches (MoE
+# experts, routing, attention masking of packed segments) belong to the model.
+# ---------------------------------------------------------------------------------------------
+@dataclasses.dataclass
+class PatchStats:
+    """Counters proving the ``ple_true_emb`` patch took
+    (``engraft/replica/seq.py:453-500``): ``n_ple_calls`` must equal the
+    number of new positions ``n_prefix - start``; ``n_key_hits`` /
+    ``n_id_hits`` echo the very ``OverlayEmb`` that produced the forward."""
+
+    n_ple_calls: int = 0
+    n_key_hits: int = 0
+    n_id_hits: int = 0
+
+
+@contextlib.contextmanager
+def ple_emb_patched(replica, precomputed_emb: torch.Tensor, stats: PatchStats, start: int = 0):
+    """For the duration of the ``with`` block, ``replica.ple_true_emb`` (an
+    instance attribute, shadowing the class method) returns
+    ``precomputed_emb[t - start]`` as ``[1, n_embd]`` and counts the call;
+    the instance's own attribute (or its absence) is restored in ``finally``
+    (the ``ple_true_emb`` part of ``expert_op_patched``,
+    ``engraft/replica/seq.py:570-637``)."""
+    had = "ple_true_emb" in replica.__dict__
+    orig = replica.__dict__.get("ple_true_emb")
+
+    def patched_ple_true_emb(tokens_arg, t, overlay=None):
+        stats.n_ple_calls += 1
+        return precomputed_emb[t - start].unsqueeze(0)
+
+    replica.ple_true_emb = patched_ple_true_emb
+    try:
+        yield
+    finally:
+        if had:
+            replica.__dict__["ple_true_emb"] = orig
+        else:
+            del replica.__dict__["ple_true_emb"]
+
+
+def _new_positions_start(base_state, cache, tokens) -> tuple[int, object]:
+    """``start`` of the new positions (``engraft/replica/seq.py:893-906``): a
+    cache hit's or the given ``base_state``'s ``n_prefix``, else 0."""
+    n_prefix = len(tokens) - 1
+    if cache is not None:
+        hit = cache.lookup(list(tokens[:n_prefix]), {})
+        if hit is not None:
+            return int(hit[0].n_prefix), hit[0]
+    if base_state is not None:
+        return int(base_state.n_prefix), base_state
+    return 0, None
+
+
+def seq_forward(replica, tokens, rows_var: torch.Tensor, row_map: dict, return_logits: bool = True, *,
+                grad_proxy: bool = True, base_state=None, cache=None, segment_ids=None, overlay_cache=None,
+                **prefix_kwargs):
+    """Sequence forward (``engraft/replica/seq.py:809-921``): ``OverlayEmb``
+    over the new positions ``start..n_prefix-1`` (on the device,
+    differentiable in ``rows_var``), then ``replica.prefix(tokens, ...)`` with
+    ``replica.ple_true_emb`` reading slices of it.  ``ValueError`` with fewer
+    than 2 tokens.  Returns ``(state, stats)``; ``stats.n_ple_calls`` is
+    ``n_prefix - start`` when the model read every new position through the
+    patch.  Further keyword arguments go to ``replica.prefix``."""
+    n_prefix = len(tokens) - 1
+    if n_prefix <= 0:
+        raise ValueError("seq_forward: need at least 2 tokens")
+    start, _ = _new_positions_start(base_state, cache, tokens)
+    overlay_emb = OverlayEmb(replica.table, tokens, rows_var, row_map, segment_ids=segment_ids,
+                             overlay_cache=overlay_cache)
+    precomputed = overlay_emb.build(n_prefix, start=start)
+    stats = PatchStats(n_key_hits=overlay_emb.n_key_hits, n_id_hits=overlay_emb.n_id_hits)
+    with ple_emb_patched(replica, precomputed, stats, start=start):
+        state = replica.prefix(tokens, grad_proxy=grad_proxy, return_logits=return_logits, base_state=base_state,
+                               cache=cache, **prefix_kwargs)
+    return state, stats
+
+
+def seq_step(replica, tokens, rows_var: torch.Tensor, row_map: dict, loss_fn, *, base_state=None, cache=None,
+             segment_ids=None, overlay_cache=None, **prefix_kwargs):
+    """Sequence forward + backward with the patch active through
+    ``loss.backward()`` (``engraft/replica/seq.py:1340-1470``): the gradient
+    reaches ``rows_var`` through the device scatter of ``OverlayEmb``.
+    Returns ``(loss, timings, stats)``; ``AssertionError`` when
+    ``stats.n_ple_calls != n_prefix - start`` (the patch did not take)."""
+    t_entry = time.perf_counter()
+    n_prefix = len(tokens) - 1
+    if n_prefix <= 0:
+        raise ValueError("seq_step_triton: need at least 2 tokens")
+    start, _ = _new_positions_start(base_state, cache, tokens)
+    overlay_emb = OverlayEmb(replica.table, tokens, rows_var, row_map, segment_ids=segment_ids,
+                             overlay_cache=overlay_cache)
+    precomputed = overlay_emb.build(n_prefix, start=start)
+    stats = PatchStats(n_key_hits=overlay_emb.n_key_hits, n_id_hits=overlay_emb.n_id_hits)
+    dev = rows_var.device
+    sync = (lambda: torch.cuda.synchronize(dev)) if dev.type == "cuda" else (lambda: None)
+    with ple_emb_patched(replica, precomputed, stats, start=start):
+        sync()
+        t0 = time.perf_counter()
+        state = replica.prefix(tokens, grad_proxy=True, return_logits=True, base_state=base_state, cache=cache,
+                               **prefix_kwargs)
+        sync()
+        t_fwd = time.perf_counter() - t0
+        loss = loss_fn(state)
+        t1 = time.perf_counter()
+        loss.backward()
+        sync()
+        t_bwd = time.perf_counter() - t1
+    assert stats.n_ple_calls == n_prefix - start, (
+        f"seq_step_triton: n_ple_calls={stats.n_ple_calls} != n_prefix-start={n_prefix - start} "
+        "(the ple_true_emb patch did not take -- see PatchStats)")
+    return loss, {"fwd_s": t_fwd, "bwd_s": t_bwd, "pre_s": t0 - t_entry}, stats
