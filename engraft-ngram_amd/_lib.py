@@ -123,9 +123,12 @@ SIGNATURES = {
                                        c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "eg_ple_gate_backward": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
-                                       c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
+                                       c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_gate_backward_planes": (c_int32, [c_void_p] * 11 + [c_int64, c_int32, c_int32, c_int32, c_int32] +
-                                    [c_void_p] * 6),
+                                    [c_void_p] * 7),
+    "eg_ple_weight_grads_workspace_size": (ctypes.c_size_t, [c_int64, c_int32, c_int32, c_int32]),
+    "eg_ple_weight_grads": (c_int32, [c_void_p] * 11 + [c_int64, c_void_p, c_int64, c_int32, c_int32, c_int32,
+                                                        c_int32] + [c_void_p] * 5 + [ctypes.c_size_t, c_void_p]),
     "eg_ple_conv": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32,
                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_rms": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, ctypes.c_float, c_void_p, c_void_p]),

@@ -545,7 +545,7 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_kernel(
     const float* __restrict__ s_in, const float* __restrict__ gate_in, const float* __restrict__ rstd,
     const float* __restrict__ d_out, const float* __restrict__ d_normed, int hc, int n, float inv_sqrt_n,
     int detach_value, int detach_gate, float* __restrict__ d_key, float* __restrict__ d_value,
-    float* __restrict__ d_hidden) {
+    float* __restrict__ d_hidden, float* __restrict__ d_s) {
 #pragma clang fp contract(off)
   __shared__ float red[kGbMaxHc * (kGbThreads / 64)];
   const int64_t t = blockIdx.x;
@@ -627,6 +627,10 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_kernel(
       ds[j] = as > 1e-6f ? du * (0.5f / sqrtf(as)) : 0.0f;
     }
   }
+  if (d_s != nullptr && threadIdx.x == 0)  // the score gradient, for the norm weights' gradients
+#pragma unroll
+    for (int j = 0; j < kGbMaxHc; ++j)
+      if (j < hc) d_s[t * hc + j] = ds[j];
   // the key and query norms' backward, and the hidden state's gradient
 #pragma unroll
   for (int j = 0; j < kGbMaxHc; ++j) {
@@ -707,7 +711,8 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_vec_kernel(
     const float* __restrict__ s_in, const float* __restrict__ gate_in, const float* __restrict__ rstd,
     const float* __restrict__ d_out, const float* __restrict__ d_normed, int hc, int n, float inv_sqrt_n,
     int detach_value, int detach_gate, float* __restrict__ d_key, float* __restrict__ d_value,
-    float* __restrict__ d_hidden, __bf16* __restrict__ d_key_lo, __bf16* __restrict__ d_value_lo) {
+    float* __restrict__ d_hidden, __bf16* __restrict__ d_key_lo, __bf16* __restrict__ d_value_lo,
+    float* __restrict__ d_s) {
 #pragma clang fp contract(off)
   __shared__ float red[kGbMaxHc * (kGbThreads / 64)];
   const int64_t t = blockIdx.x;
@@ -783,6 +788,10 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_vec_kernel(
       ds[j] = as > 1e-6f ? du * (0.5f / sqrtf(as)) : 0.0f;
     }
   }
+  if (d_s != nullptr && threadIdx.x == 0)  // the score gradient, for the norm weights' gradients
+#pragma unroll
+    for (int j = 0; j < kGbMaxHc; ++j)
+      if (j < hc) d_s[t * hc + j] = ds[j];
   // the key and query norms' backward, and the hidden state's gradient
 #pragma unroll
   for (int j = 0; j < kGbMaxHc; ++j) {
@@ -812,6 +821,81 @@ __global__ __launch_bounds__(kGbThreads) void ple_gate_bwd_vec_kernel(
     }
     if (d_hidden != nullptr) *(float4*)(d_hidden + row + i0) = make_float4(dh[0], dh[1], dh[2], dh[3]);
   }
+}
+
+// Gradients of the norm and convolution weights: sums over the positions of
+// per-element products, column c = j*n + i per thread (j the stream).  With
+// the forward's RMS factors r and d_s the score gradient:
+//   d_norm_key[c]   = sum_t (d_s_j / sqrt n) q^[t,c] * key[t,c] r_k
+//   d_norm_query[c] = sum_t (d_s_j / sqrt n) k^[t,c] * hidden[t,c] r_q
+//   d_norm_conv[c]  = sum_t d_normed[t,c] * value[t,i] gate_j r_g
+//   d_conv[c,k]     = sum_t d_acc[t,c] * full[hist + t - (taps-1-k) dil, c]
+// with d_acc = d_out silu'(pre).  Each workgroup sums kWgChunk positions of
+// 256 columns; the chunks' partial sums are then added in chunk order (fixed
+// association, no float atomics).
+constexpr int kWgChunk = 64;
+constexpr int kWgMaxTaps = 8;
+
+template <int TAPS>
+__global__ __launch_bounds__(256) void ple_wgrad_part_kernel(
+    const float* __restrict__ key, const float* __restrict__ value, const float* __restrict__ hidden,
+    const float* __restrict__ gate, const float* __restrict__ rstd, const float* __restrict__ d_s,
+    const float* __restrict__ norm_key, const float* __restrict__ norm_query, const float* __restrict__ d_out,
+    const float* __restrict__ d_normed, const float* __restrict__ full, int64_t hist_rows,
+    const float* __restrict__ pre, int64_t T, int hc, int n, int dil, float inv_sqrt_n, float* __restrict__ part) {
+#pragma clang fp contract(off)
+  const int C = hc * n;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;  // no barrier: a thread touches its own column only
+  const int j = c / n, i = c - j * n;
+  const int64_t t0 = (int64_t)blockIdx.y * kWgChunk;
+  const int64_t t1 = min(t0 + kWgChunk, T);
+  const float nk = norm_key[c], nq = norm_query[c];
+  float a_nk = 0.0f, a_nq = 0.0f, a_nc = 0.0f, a_w[TAPS];
+#pragma unroll
+  for (int k = 0; k < TAPS; ++k) a_w[k] = 0.0f;
+  for (int64_t t = t0; t < t1; ++t) {
+    const int64_t pj = t * hc + j;
+    const float rk = rstd[pj * 3 + 0], rq = rstd[pj * 3 + 1], rg = rstd[pj * 3 + 2];
+    const float g = gate[pj], dsn = d_s[pj] * inv_sqrt_n;
+    const int64_t e = t * C + c;
+    const float kr = key[e] * rk, hr = hidden[e] * rq;
+    a_nk += (dsn * (hr * nq)) * kr;
+    a_nq += (dsn * (kr * nk)) * hr;
+    a_nc += d_normed[e] * ((value[t * n + i] * g) * rg);
+    const float x = pre[e];
+    const float sg = 1.0f / (1.0f + expf(-x));
+    const float da = d_out[e] * (sg * (1.0f + x * (1.0f - sg)));
+#pragma unroll
+    for (int k = 0; k < TAPS; ++k) {
+      const int64_t src = hist_rows + t - (int64_t)(TAPS - 1 - k) * dil;
+      if (src >= 0) a_w[k] += da * full[src * C + c];
+    }
+  }
+  constexpr int Q = 3 + TAPS;
+  float* out = part + (int64_t)blockIdx.y * Q * C + c;
+  out[0] = a_nk;
+  out[C] = a_nq;
+  out[2 * (int64_t)C] = a_nc;
+#pragma unroll
+  for (int k = 0; k < TAPS; ++k) out[(3 + (int64_t)k) * C] = a_w[k];
+}
+
+// Chunk partial sums added in chunk order; q < 3: the norm weights, else conv tap q-3.
+__global__ __launch_bounds__(256) void ple_wgrad_sum_kernel(const float* __restrict__ part, int64_t n_chunks,
+                                                           int Q, int C, int taps, float* __restrict__ d_norm_key,
+                                                           float* __restrict__ d_norm_query,
+                                                           float* __restrict__ d_norm_conv,
+                                                           float* __restrict__ d_conv) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)Q * C) return;
+  const int q = (int)(idx / C), c = (int)(idx - (int64_t)q * C);
+  float acc = 0.0f;
+  for (int64_t ch = 0; ch < n_chunks; ++ch) acc += part[(ch * Q + q) * C + c];
+  if (q == 0) { if (d_norm_key) d_norm_key[c] = acc; }
+  else if (q == 1) { if (d_norm_query) d_norm_query[c] = acc; }
+  else if (q == 2) { if (d_norm_conv) d_norm_conv[c] = acc; }
+  else if (d_conv) d_conv[(int64_t)c * taps + (q - 3)] = acc;
 }
 
 // Calls f with std::integral_constant<int, p> for p = 1..kVecMaxP.
@@ -953,7 +1037,7 @@ int eg_ple_gate_backward(const float* key, const float* value, const float* hidd
                          const float* norm_query, const float* norm_conv, const float* s, const float* gate,
                          const float* rstd, const float* d_out, const float* d_normed, int64_t n_pos, int32_t hc,
                          int32_t n_embd, int32_t detach_value, int32_t detach_gate, float* d_key, float* d_value,
-                         float* d_hidden, void* stream) {
+                         float* d_hidden, float* d_s, void* stream) {
   EG_CHECK_ARG(n_pos >= 0 && n_pos < (1LL << 31), "n_pos=%lld", (long long)n_pos);
   if (hc < 1 || hc > kGbMaxHc || n_embd < 1 || n_embd > kGbThreads * kGbMaxPer)
     return set_error(EG_ERR_UNSUPPORTED, "gate backward for hc=%d n_embd=%d (built: hc <= %d, n_embd <= %d)", hc,
@@ -971,12 +1055,12 @@ int eg_ple_gate_backward(const float* key, const float* value, const float* hidd
     hipLaunchKernelGGL(ple_gate_bwd_vec_kernel<false>, dim3((unsigned)n_pos), dim3(n_embd / 4), 0, (hipStream_t)stream,
                        key, value, hidden, norm_key, norm_query, norm_conv, s, gate, rstd, d_out, d_normed, hc, n_embd,
                        (float)(1.0 / sqrt((double)n_embd)), detach_value, detach_gate, detach_gate ? nullptr : d_key,
-                       detach_value ? nullptr : d_value, d_hidden, nullptr, nullptr);
+                       detach_value ? nullptr : d_value, d_hidden, nullptr, nullptr, d_s);
   else
     hipLaunchKernelGGL(ple_gate_bwd_kernel, dim3((unsigned)n_pos), dim3(kGbThreads), 0, (hipStream_t)stream, key,
                        value, hidden, norm_key, norm_query, norm_conv, s, gate, rstd, d_out, d_normed, hc, n_embd,
                        (float)(1.0 / sqrt((double)n_embd)), detach_value, detach_gate, detach_gate ? nullptr : d_key,
-                       detach_value ? nullptr : d_value, d_hidden);
+                       detach_value ? nullptr : d_value, d_hidden, d_s);
   return launch_status("ple_gate_bwd_kernel");
 }
 
@@ -985,7 +1069,7 @@ int eg_ple_gate_backward_planes(const float* key, const float* value, const floa
                                 const float* rstd, const float* d_out, const float* d_normed, int64_t n_pos,
                                 int32_t hc, int32_t n_embd, int32_t detach_value, int32_t detach_gate,
                                 void* d_key_hi, void* d_key_lo, void* d_value_hi, void* d_value_lo, float* d_hidden,
-                                void* stream) {
+                                float* d_s, void* stream) {
   EG_CHECK_ARG(n_pos >= 0 && n_pos < (1LL << 31), "n_pos=%lld", (long long)n_pos);
   if (hc < 1 || hc > kGbMaxHc || n_embd < 256 || n_embd > kGbThreads * 4 || n_embd % 256 != 0)
     return set_error(EG_ERR_UNSUPPORTED, "gate backward to planes for hc=%d n_embd=%d (built: hc <= %d, n_embd a "
@@ -1005,8 +1089,63 @@ int eg_ple_gate_backward_planes(const float* key, const float* value, const floa
                      key, value, hidden, norm_key, norm_query, norm_conv, s, gate, rstd, d_out, d_normed, hc, n_embd,
                      (float)(1.0 / sqrt((double)n_embd)), detach_value, detach_gate,
                      detach_gate ? nullptr : (float*)d_key_hi, detach_value ? nullptr : (float*)d_value_hi, d_hidden,
-                     (__bf16*)d_key_lo, (__bf16*)d_value_lo);
+                     (__bf16*)d_key_lo, (__bf16*)d_value_lo, d_s);
   return launch_status("ple_gate_bwd_vec_kernel");
+}
+
+size_t eg_ple_weight_grads_workspace_size(int64_t n_pos, int32_t hc, int32_t n_embd, int32_t taps) {
+  if (n_pos <= 0 || hc < 1 || n_embd < 1 || taps < 1) return 0;
+  return (size_t)((n_pos + kWgChunk - 1) / kWgChunk) * (size_t)(3 + taps) * (size_t)hc * (size_t)n_embd * 4;
+}
+
+int eg_ple_weight_grads(const float* key, const float* value, const float* hidden, const float* gate,
+                        const float* rstd, const float* d_s, const float* norm_key, const float* norm_query,
+                        const float* d_out, const float* d_normed, const float* full, int64_t hist_rows,
+                        const float* pre, int64_t n_pos, int32_t hc, int32_t n_embd, int32_t taps, int32_t dilation,
+                        float* d_norm_key, float* d_norm_query, float* d_norm_conv, float* d_conv_w, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  EG_CHECK_ARG(n_pos >= 0 && n_pos < (1LL << 31) && hist_rows >= 0 && hc >= 1 && n_embd >= 1 && dilation >= 1,
+               "n_pos=%lld hist_rows=%lld hc=%d n_embd=%d dilation=%d", (long long)n_pos, (long long)hist_rows, hc,
+               n_embd, dilation);
+  if (taps < 1 || taps > kWgMaxTaps)
+    return set_error(EG_ERR_UNSUPPORTED, "weight gradients for %d taps (built: 1..%d)", taps, kWgMaxTaps);
+  EG_CHECK_ARG((int64_t)hc * n_embd < (1LL << 31), "too many columns");
+  const int C = hc * n_embd;
+  const int64_t n_chunks = (n_pos + kWgChunk - 1) / kWgChunk;
+  const int Q = 3 + taps;
+  hipStream_t st = (hipStream_t)stream;
+  EG_CHECK_ARG(n_pos >= 1, "eg_ple_weight_grads needs at least one position");
+  EG_CHECK_ARG(key && value && hidden && gate && rstd && d_s && norm_key && norm_query && d_out && d_normed && full &&
+                   pre,
+               "NULL argument");
+  const size_t need = eg_ple_weight_grads_workspace_size(n_pos, hc, n_embd, taps);
+  if (workspace_bytes < need)
+    return set_error(EG_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, need);
+  EG_CHECK_ARG(need == 0 || workspace != nullptr, "workspace is NULL");
+  float* part = (float*)workspace;
+  {
+    const dim3 grid((unsigned)((C + 255) / 256), (unsigned)n_chunks);
+    const float isn = (float)(1.0 / sqrt((double)n_embd));
+#define EG_WG(TP)                                                                                                  \
+  hipLaunchKernelGGL(ple_wgrad_part_kernel<TP>, grid, dim3(256), 0, st, key, value, hidden, gate, rstd, d_s,       \
+                     norm_key, norm_query, d_out, d_normed, full, hist_rows, pre, n_pos, hc, n_embd, dilation, isn, \
+                     part)
+    switch (taps) {
+      case 1: EG_WG(1); break;
+      case 2: EG_WG(2); break;
+      case 3: EG_WG(3); break;
+      case 4: EG_WG(4); break;
+      case 5: EG_WG(5); break;
+      case 6: EG_WG(6); break;
+      case 7: EG_WG(7); break;
+      default: EG_WG(8); break;
+    }
+#undef EG_WG
+  }
+  const int64_t total = (int64_t)Q * C;
+  hipLaunchKernelGGL(ple_wgrad_sum_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, part, n_chunks, Q,
+                     C, taps, d_norm_key, d_norm_query, d_norm_conv, d_conv_w);
+  return launch_status("ple_wgrad kernels");
 }
 
 }  // extern "C"

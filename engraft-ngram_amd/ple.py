@@ -13,13 +13,15 @@ Forward:
   ``[history; normed]``, SiLU, and ``out = hidden + gated + conv``.
 
 The result -- the output and the new history -- is differentiable in emb,
-hidden, the history and the weights.  Without weight gradients (the descent's
-case) the backward runs ``eg_ple_conv_backward`` and ``eg_ple_gate_backward``
-on the forward's saved intermediates, then the projections' backward (with
-``bf16x3``, one ``gemm_x3`` call over two K segments); with
-weight gradients, a torch recomputation of the block on the device,
-differentiated by autograd.  Either way the forward values are the HIP
-kernels'.  ``detach_value`` / ``detach_gate`` change only the backward, as in
+hidden, the history and the weights.  The backward runs
+``eg_ple_conv_backward`` and ``eg_ple_gate_backward`` on the forward's saved
+intermediates, then the projections' backward (with ``bf16x3``, one
+``gemm_x3`` call over two K segments); when weights need gradients, also the
+two weight GEMMs (fp32) and ``eg_ple_weight_grads`` for the norm and
+convolution weights.  Only shapes beyond the HIP kernels' limits (more than 4
+streams, ``n_embd`` > 4096, a convolution reaching back more than 32 rows)
+fall back to a torch recomputation of the block, differentiated by
+autograd.  Either way the forward values are the HIP kernels'.  ``detach_value`` / ``detach_gate`` change only the backward, as in
 the reference.
 
 ``PleReplica`` (below) is the same block with its weights read from the model
@@ -246,11 +248,10 @@ def _native_backward_ok(hc: int, n: int, taps: int, dil: int) -> bool:
 
 
 class _PleFn(torch.autograd.Function):
-    """Forward on the HIP kernels.  Backward: when no weight needs a gradient
-    (the descent's case: emb, hidden and the history only), the HIP backward
-    from the saved forward intermediates, so that the projections' GEMMs are
-    not run again; otherwise a torch recomputation of the block, differentiated
-    by autograd."""
+    """Forward on the HIP kernels.  Backward: the HIP backward from the saved
+    forward intermediates (the projections' GEMMs are not run again), with the
+    weights' gradients when they are asked for; beyond the HIP kernels' limits,
+    a torch recomputation of the block, differentiated by autograd."""
 
     @staticmethod
     def forward(ctx, emb, hidden, w_key, w_value, nk, nq, nc, conv, hist, eps, dil, detach_value, detach_gate,
@@ -279,8 +280,7 @@ class _PleFn(torch.autograd.Function):
         nk32, nq32, nc32 = (x.to(**f32).contiguous() for x in (nk, nq, nc))
         conv32 = conv.to(**f32).contiguous()
         taps = conv32.shape[1]
-        native = (not any(ctx.needs_input_grad[2:8]) and any(ctx.needs_input_grad)
-                  and _native_backward_ok(hc, n, taps, int(dil)))
+        native = any(ctx.needs_input_grad) and _native_backward_ok(hc, n, taps, int(dil))
         rstd = torch.empty((t_len, hc, 3), **f32) if native else None
         _lib.call("eg_ple_gate", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden32), _lib.ptr(nk32), _lib.ptr(nq32),
                   _lib.ptr(nc32), t_len, hc, n, float(eps), _lib.ptr(full[h0:]), _lib.ptr(s), _lib.ptr(gate),
@@ -293,8 +293,12 @@ class _PleFn(torch.autograd.Function):
         new_hist = (full[-hist_len:] if hist_len > 0 else full[:0]).reshape(-1, hc, n).to(hidden.dtype).clone()
         ctx.native = native
         if native:
-            ctx.save_for_backward(key, value, hidden32, full, s, gate, rstd, nk32, nq32, nc32, conv32, wk32, wv32, pre)
+            # emb for the projection weights' gradients
+            emb_w = emb32 if any(ctx.needs_input_grad[2:4]) else None
+            ctx.save_for_backward(key, value, hidden32, full, s, gate, rstd, nk32, nq32, nc32, conv32, wk32, wv32, pre,
+                                  emb_w)
             ctx.dtypes = (emb.dtype, hidden.dtype, hist.dtype)
+            ctx.w_dtypes = tuple(x.dtype for x in (w_key, w_value, nk, nq, nc, conv))
             ctx.tail_rows = new_hist.shape[0]
         else:
             ctx.save_for_backward(emb, hidden, w_key, w_value, nk, nq, nc, conv, hist)
@@ -326,7 +330,7 @@ class _PleFn(torch.autograd.Function):
 
     @staticmethod
     def _backward_native(ctx, d_out, d_hist):
-        key, value, hidden32, full, s, gate, rstd, nk32, nq32, nc32, conv32, wk32, wv32, pre = ctx.saved_tensors
+        key, value, hidden32, full, s, gate, rstd, nk32, nq32, nc32, conv32, wk32, wv32, pre, emb32 = ctx.saved_tensors
         _eps, dil, detach_value, detach_gate = ctx.cfg
         emb_dt, hidden_dt, hist_dt = ctx.dtypes
         t_len, hc, n = hidden32.shape
@@ -343,6 +347,9 @@ class _PleFn(torch.autograd.Function):
         _lib.call("eg_ple_conv_backward", _lib.ptr(full), h0, t_len, hc, n, _lib.ptr(conv32), conv32.shape[1],
                   int(dil), _lib.ptr(pre), _lib.ptr(d_out32), _lib.ptr(d_tail), tail, _lib.ptr(d_full), st)
         d_hidden = torch.empty((t_len, hc, n), **f32) if need_hidden else None
+        need_w = ctx.needs_input_grad[2:8]
+        if any(need_w):
+            return _PleFn._backward_with_weights(ctx, d_out32, d_full, d_hidden)
         if ctx.gemm == "bf16x3" and n % 256 == 0:
             # d_key and d_value straight into the bf16 planes gemm_x3 takes
             pk = _empty_planes(t_len, c_dim, dev) if (need_emb and not detach_gate) else None
@@ -352,7 +359,8 @@ class _PleFn(torch.autograd.Function):
                           _lib.ptr(nk32), _lib.ptr(nq32), _lib.ptr(nc32), _lib.ptr(s), _lib.ptr(gate), _lib.ptr(rstd),
                           _lib.ptr(d_out32), _lib.ptr(d_full[h0:]), t_len, hc, n, int(bool(detach_value)),
                           int(bool(detach_gate)), _lib.ptr(pk.hi if pk else None), _lib.ptr(pk.lo if pk else None),
-                          _lib.ptr(pv.hi if pv else None), _lib.ptr(pv.lo if pv else None), _lib.ptr(d_hidden), st)
+                          _lib.ptr(pv.hi if pv else None), _lib.ptr(pv.lo if pv else None), _lib.ptr(d_hidden), None,
+                          st)
             d_emb = None
             if need_emb:
                 parts = [(d, _WT.get(w)) for d, w in ((pk, wk32), (pv, wv32)) if d is not None]
@@ -370,7 +378,7 @@ class _PleFn(torch.autograd.Function):
             _lib.call("eg_ple_gate_backward", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden32), _lib.ptr(nk32),
                       _lib.ptr(nq32), _lib.ptr(nc32), _lib.ptr(s), _lib.ptr(gate), _lib.ptr(rstd), _lib.ptr(d_out32),
                       _lib.ptr(d_full[h0:]), t_len, hc, n, int(bool(detach_value)), int(bool(detach_gate)),
-                      _lib.ptr(d_key), _lib.ptr(d_value), _lib.ptr(d_hidden), st)
+                      _lib.ptr(d_key), _lib.ptr(d_value), _lib.ptr(d_hidden), None, st)
         d_emb = None
         if need_emb:
             # the projections' backward, d_emb = d_key w_key + d_value w_value, as
@@ -388,6 +396,70 @@ class _PleFn(torch.autograd.Function):
             d_emb = d_emb.to(emb_dt)
         d_hist_in = d_full[:h0].reshape(h0, hc, n).to(hist_dt) if need_hist else None
         return (d_emb, d_hidden.to(hidden_dt) if d_hidden is not None else None, None, None, None, None, None, None,
+                d_hist_in, None, None, None, None, None)
+
+
+    @staticmethod
+    def _backward_with_weights(ctx, d_out32, d_full, d_hidden):
+        """The HIP backward with the weights' gradients too: the gate backward
+        in fp32 (its d_key / d_value also feed the projection weights'
+        gradients, and its score gradient d_s the norm weights'), the two
+        weight GEMMs ``d_w_key = d_key^T emb`` and ``d_w_value = d_value^T emb``,
+        and ``eg_ple_weight_grads`` for the norms and the convolution."""
+        key, value, hidden32, full, s, gate, rstd, nk32, nq32, nc32, conv32, wk32, wv32, pre, emb32 = ctx.saved_tensors
+        _eps, dil, detach_value, detach_gate = ctx.cfg
+        emb_dt, hidden_dt, hist_dt = ctx.dtypes
+        t_len, hc, n = hidden32.shape
+        c_dim = hc * n
+        h0 = full.shape[0] - t_len
+        dev = full.device
+        f32 = dict(dtype=torch.float32, device=dev)
+        st = _lib.stream_ptr(dev)
+        need = ctx.needs_input_grad
+        need_emb, need_hist = need[0], need[8]
+        need_wk, need_wv, need_nk, need_nq, need_nc, need_cv = need[2:8]
+        d_key = torch.empty((t_len, c_dim), **f32) if ((need_emb or need_wk) and not detach_gate) else None
+        d_value = torch.empty((t_len, n), **f32) if ((need_emb or need_wv) and not detach_value) else None
+        d_s = torch.empty((t_len, hc), **f32)
+        _lib.call("eg_ple_gate_backward", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden32), _lib.ptr(nk32),
+                  _lib.ptr(nq32), _lib.ptr(nc32), _lib.ptr(s), _lib.ptr(gate), _lib.ptr(rstd), _lib.ptr(d_out32),
+                  _lib.ptr(d_full[h0:]), t_len, hc, n, int(bool(detach_value)), int(bool(detach_gate)),
+                  _lib.ptr(d_key), _lib.ptr(d_value), _lib.ptr(d_hidden), _lib.ptr(d_s), st)
+        d_emb = None
+        if need_emb:
+            parts = [(d, _WT.get(w)) for d, w in ((d_key, wk32), (d_value, wv32)) if d is not None]
+            if not parts:
+                d_emb = torch.zeros((t_len, n), **f32)
+            elif ctx.gemm == "bf16x3":
+                d_emb = gemm_x3(*[x for part in parts for x in part], cache_b=True)
+            else:
+                d_emb = parts[0][0] @ parts[0][1].T
+                if len(parts) > 1:
+                    d_emb.addmm_(parts[1][0], parts[1][1].T)
+            d_emb = d_emb.to(emb_dt)
+        wdt = ctx.w_dtypes
+        d_wk = d_wv = None
+        if need_wk:
+            d_wk = (d_key.T @ emb32 if d_key is not None else torch.zeros_like(wk32)).to(wdt[0])
+        if need_wv:
+            d_wv = (d_value.T @ emb32 if d_value is not None else torch.zeros_like(wv32)).to(wdt[1])
+        d_nk = d_nq = d_nc = d_cv = None
+        if need_nk or need_nq or need_nc or need_cv:
+            taps = conv32.shape[1]
+            outs = [torch.zeros(c_dim, **f32) for _ in range(3)] + [torch.zeros((c_dim, taps), **f32)]
+            if t_len > 0:
+                ws_bytes = int(_lib.load().eg_ple_weight_grads_workspace_size(t_len, hc, n, taps))
+                ws = torch.empty(max(ws_bytes // 4, 1), **f32)
+                _lib.call("eg_ple_weight_grads", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden32), _lib.ptr(gate),
+                          _lib.ptr(rstd), _lib.ptr(d_s), _lib.ptr(nk32), _lib.ptr(nq32), _lib.ptr(d_out32),
+                          _lib.ptr(d_full[h0:]), _lib.ptr(full), h0, _lib.ptr(pre), t_len, hc, n, taps, int(dil),
+                          *[_lib.ptr(o) for o in outs], _lib.ptr(ws), ws_bytes, st)
+            d_nk = outs[0].to(wdt[2]) if need_nk else None
+            d_nq = outs[1].to(wdt[3]) if need_nq else None
+            d_nc = outs[2].to(wdt[4]) if need_nc else None
+            d_cv = outs[3].to(wdt[5]) if need_cv else None
+        d_hist_in = d_full[:h0].reshape(h0, hc, n).to(hist_dt) if need_hist else None
+        return (d_emb, d_hidden.to(hidden_dt) if d_hidden is not None else None, d_wk, d_wv, d_nk, d_nq, d_nc, d_cv,
                 d_hist_in, None, None, None, None, None)
 
 

@@ -364,12 +364,13 @@ int eg_ple_conv_backward(const float* full, int64_t hist_rows, int64_t n_pos, in
  * output may be NULL.  detach_value / detach_gate drop that factor of
  * gated = value * gate from the gradient (engraft/replica/layers.py:600-604),
  * leaving d_value / d_key untouched.  s, gate, rstd: the forward's outputs.
- * hc <= 4, n_embd <= 4096.  The norm weights' gradients are not computed. */
+ * d_s (NULL: not written) f32 [n_pos, hc] receives the score gradient, which
+ * eg_ple_weight_grads takes.  hc <= 4, n_embd <= 4096. */
 int eg_ple_gate_backward(const float* key, const float* value, const float* hidden, const float* norm_key,
                          const float* norm_query, const float* norm_conv, const float* s, const float* gate,
                          const float* rstd, const float* d_out, const float* d_normed, int64_t n_pos,
                          int32_t hc, int32_t n_embd, int32_t detach_value, int32_t detach_gate,
-                         float* d_key, float* d_value, float* d_hidden, void* stream);
+                         float* d_key, float* d_value, float* d_hidden, float* d_s, void* stream);
 
 /* eg_ple_gate_backward with d_key and d_value written as their bf16 hi / lo
  * planes (hi = rne(x), lo = rne(x - hi); row strides hc*n_embd and n_embd,
@@ -381,7 +382,26 @@ int eg_ple_gate_backward_planes(const float* key, const float* value, const floa
                                 const float* s, const float* gate, const float* rstd, const float* d_out,
                                 const float* d_normed, int64_t n_pos, int32_t hc, int32_t n_embd,
                                 int32_t detach_value, int32_t detach_gate, void* d_key_hi, void* d_key_lo,
-                                void* d_value_hi, void* d_value_lo, float* d_hidden, void* stream);
+                                void* d_value_hi, void* d_value_lo, float* d_hidden, float* d_s, void* stream);
+
+/* The weight gradients of the PLE block's norms and convolution (the part of
+ * ple_forward's autograd that reaches norm_key, norm_query, norm_conv and
+ * conv1d, engraft/replica/layers.py:565-626), from the forward's key, value,
+ * hidden, gate, rstd, full and pre-activation, eg_ple_gate_backward's d_s and
+ * eg_ple_conv_backward's d_normed (= d_full after the history):
+ *   d_norm_key[c], d_norm_query[c], d_norm_conv[c]  f32 [hc*n_embd]
+ *   d_conv_w[c, k]                                   f32 [hc*n_embd, taps]
+ * each sum over the n_pos positions taken in fixed 64-position chunks added in
+ * order (deterministic).  Any output may be NULL.  taps <= 8, n_pos >= 1;
+ * workspace of eg_ple_weight_grads_workspace_size bytes. */
+size_t eg_ple_weight_grads_workspace_size(int64_t n_pos, int32_t hc, int32_t n_embd, int32_t taps);
+int eg_ple_weight_grads(const float* key, const float* value, const float* hidden, const float* gate,
+                        const float* rstd, const float* d_s, const float* norm_key,
+                        const float* norm_query, const float* d_out, const float* d_normed,
+                        const float* full, int64_t hist_rows, const float* pre, int64_t n_pos,
+                        int32_t hc, int32_t n_embd, int32_t taps, int32_t dilation,
+                        float* d_norm_key, float* d_norm_query, float* d_norm_conv,
+                        float* d_conv_w, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Per-stream RMS norm: out[r, j, :] = x[r, j, :] / sqrt(mean(x[r, j, :]^2) + eps)
  * * weight[j, :], x and out f32 [n_rows, hc, n_embd], weight f32 [hc, n_embd]

@@ -78,7 +78,11 @@ def test_host_side_argument_checks():
         ("dilation", _lib.EG_ERR_UNSUPPORTED, lib.eg_ple_conv_backward, None, 0, 1, 4, 64, None, 4, 11, None, None,
          None, 0, None, None),
         ("hc=5", _lib.EG_ERR_UNSUPPORTED, lib.eg_ple_gate_backward, *([None] * 11), 1, 5, 64, 0, 0, None, None,
-         None, None),
+         None, None, None),
+        ("taps", _lib.EG_ERR_UNSUPPORTED, lib.eg_ple_weight_grads, *([None] * 11), 0, None, 4, 4, 64, 9, 3,
+         None, None, None, None, None, 0, None),
+        ("at least one position", _lib.EG_ERR_ARG, lib.eg_ple_weight_grads, *([None] * 11), 0, None, 0, 4, 64, 4,
+         3, None, None, None, None, None, 0, None),
         ("taps", _lib.EG_ERR_ARG, lib.eg_ple_conv_backward, None, 0, 1, 4, 64, None, 9, 1, None, None, None, 0,
          None, None),
     ]

@@ -23,6 +23,10 @@ from tests.test_oracle_ple import ple_weights
 pytestmark = pytest.mark.gpu
 
 
+def _say(msg: str) -> None:
+    print(f"[gpu-test] {msg}", file=sys.stderr, flush=True)
+
+
 class _HP:
     hc_mult = 4
     n_embd = 2560
@@ -168,12 +172,70 @@ def test_ple_native_backward_against_oracle(cuda, dv, dg, gemm):
         assert err <= 1e-4 * scale, f"d_{name}: {err} vs scale {scale}"
 
 
-def test_ple_weight_gradients_recompute_path(cuda):
-    """With weight gradients requested the backward recomputes the block with
-    torch on the device: the gradients of w_key, norm_conv and the taps, and
-    of emb, against autograd of the oracle on the CPU."""
+_WEIGHTS = ("w_key", "w_value", "norm_key", "norm_query", "norm_conv", "conv1d")
+
+
+def _grad_close(got, exp, tol, name):
+    """``got`` within ``tol`` of ``exp``'s largest entry; a gradient the
+    oracle's autograd never reached (``None``) must be absent or zero."""
+    if exp is None:
+        assert got is None or float(got.abs().max()) == 0.0, name
+        return
+    assert got is not None, name
+    scale = max(exp.abs().max().item(), 1e-30)
+    err = (got.detach().cpu().float() - exp).abs().max().item()
+    assert err <= tol * scale, f"{name}: {err / scale:.2e} of its largest entry"
+
+
+@pytest.mark.parametrize("gemm,dv,dg", [("fp32", False, False), ("bf16x3", False, False), ("fp32", True, False),
+                                        ("fp32", False, True)])
+def test_ple_weight_gradients_native(cuda, gemm, dv, dg):
+    """Every weight's gradient (w_key, w_value, the three norms, the conv taps)
+    together with emb's, hidden's and the history's, from the HIP backward
+    (eg_ple_gate_backward's d_s, the weight GEMMs, eg_ple_weight_grads)
+    against autograd of the oracle on the CPU: 150 positions after a 9-row
+    history (three 64-position partial sums), a gradient on the new history
+    too, with detach_value / detach_gate."""
     from engraft_ngram_amd import ple
-    hc, n, T = 4, 2560, 12
+    _say(f"PLE weight gradients {gemm} dv={dv} dg={dg}")
+    hc, n, T, H = 4, 2560, 150, 9
+    w = ple_weights(hc, n, seed=41)
+    g = torch.Generator().manual_seed(42)
+    emb = torch.randn((T, n), generator=g) * 0.1
+    hidden = torch.randn((T, hc, n), generator=g) * 0.1
+    hist = torch.randn((H, hc, n), generator=g) * 0.5
+    r = torch.randn((T, hc, n), generator=g)
+    rh = torch.randn((H, hc, n), generator=g)
+    wc = {k: v.clone().requires_grad_(True) for k, v in w.items()}
+    xc = [x.clone().requires_grad_(True) for x in (emb, hidden, hist)]
+    out_c, nh_c, _, _ = P.ple_forward(*xc[:2], wc, xc[2], hc, n, 1e-6, 3, dv, dg)
+    ((out_c * r).sum() + (nh_c * rh).sum()).backward()
+    wd = ple.PleWeights(**{k: v.to(cuda).requires_grad_(True) for k, v in w.items()})
+    xd = [x.to(cuda).requires_grad_(True) for x in (emb, hidden, hist)]
+    out_d, nh_d = ple.ple_forward(xd[0], xd[1], wd, xd[2], _HP, detach_value=dv, detach_gate=dg, gemm=gemm)
+    ((out_d * r.to(cuda)).sum() + (nh_d * rh.to(cuda)).sum()).backward()
+    # fp32 projections: the 1e-4 gradient bar.  bf16x3: the score's gradient
+    # goes through the gate's 1/sqrt|s| derivative, which at a position with a
+    # small |s| amplifies the projections' 16-bit-mantissa error (150
+    # positions reach such a position; the hidden gradient measured 6.8e-4)
+    tol = 1e-4 if gemm == "fp32" else 2e-3
+    for name, got, exp in zip(("emb", "hidden", "hist"), (x.grad for x in xd), (x.grad for x in xc)):
+        _grad_close(got, exp, tol, name)
+    for k in _WEIGHTS:
+        _grad_close(getattr(wd, k).grad, wc[k].grad, tol, k)
+
+
+def test_ple_weight_gradients_recompute_path(cuda):
+    """A convolution reaching back beyond the HIP backward's 32 rows (4 taps at
+    dilation 12) goes through the torch recomputation of the block: the
+    gradients of w_key, norm_conv and the taps, and of emb, against autograd
+    of the oracle on the CPU."""
+    from engraft_ngram_amd import ple
+
+    class HP12(_HP):
+        ple_ngram_size = 12
+
+    hc, n, T = 4, 2560, 40
     w = ple_weights(hc, n, seed=41)
     g = torch.Generator().manual_seed(42)
     emb = torch.randn((T, n), generator=g) * 0.1
@@ -181,12 +243,13 @@ def test_ple_weight_gradients_recompute_path(cuda):
     r = torch.randn((T, hc, n), generator=g)
     wc = {k: (v.clone().requires_grad_(k in ("w_key", "norm_conv", "conv1d"))) for k, v in w.items()}
     e_c = emb.clone().requires_grad_(True)
-    out_c, _, _, _ = P.ple_forward(e_c, hidden, wc, torch.zeros(0, hc, n), hc, n, 1e-6, 3)
+    out_c, _, _, _ = P.ple_forward(e_c, hidden, wc, torch.zeros(0, hc, n), hc, n, 1e-6, 12)
     (out_c * r).sum().backward()
+    assert not ple._native_backward_ok(hc, n, 4, 12)
     wd = ple.PleWeights(**{k: v.to(cuda).requires_grad_(k in ("w_key", "norm_conv", "conv1d"))
                            for k, v in w.items()})
     e_d = emb.to(cuda).requires_grad_(True)
-    out_d, _ = ple.ple_forward(e_d, hidden.to(cuda), wd, torch.zeros(0, hc, n, device=cuda), _HP)
+    out_d, _ = ple.ple_forward(e_d, hidden.to(cuda), wd, torch.zeros(0, hc, n, device=cuda), HP12)
     (out_d * r.to(cuda)).sum().backward()
     for got, exp in ((e_d.grad, e_c.grad), (wd.w_key.grad, wc["w_key"].grad), (wd.norm_conv.grad, wc["norm_conv"].grad),
                      (wd.conv1d.grad, wc["conv1d"].grad)):
@@ -265,3 +328,44 @@ def test_ple_forward_checkpointed_bit_identical(cuda, gemm):
         res.append((out.detach(), loss.detach(), e.grad, h.grad))
     for a, b in zip(*res):
         assert torch.equal(a, b)
+
+
+def _conv_pre(full, h0, T, hc, n, w, dil, dev):
+    """eg_ple_conv's pre-activation (no hidden / value: out = silu(conv))."""
+    from engraft_ngram_amd import _lib
+    full = full.to(dev).contiguous()
+    w = w.to(dev).contiguous()
+    out = torch.empty((T, hc * n), device=dev)
+    pre = torch.empty((T, hc * n), device=dev)
+    _lib.call("eg_ple_conv", _lib.ptr(full), h0, T, hc, n, _lib.ptr(w), w.shape[1], dil, 0, None, None, None,
+              _lib.ptr(out), _lib.ptr(pre), _lib.stream_ptr(dev))
+    return out.cpu(), pre.cpu()
+
+
+@pytest.mark.parametrize("taps,dil,h0", [(3, 2, 0), (3, 2, 3), (2, 5, 1), (6, 1, 2)])
+def test_generic_conv_other_shapes_against_oracle(cuda, taps, dil, h0):
+    """The generic convolution kernel (every tap count and dilation other than
+    the model's 4 taps at dilation 3), with an empty, short or partial
+    history, against the oracle's causal_depthwise_conv; out = silu(pre)."""
+    hc, n, T = 2, 640, 70
+    g = torch.Generator().manual_seed(60 + taps * 10 + dil)
+    full = torch.randn((h0 + T, hc * n), generator=g)
+    w = torch.randn((hc * n, taps), generator=g) * 0.5
+    out, pre = _conv_pre(full, h0, T, hc, n, w, dil, cuda)
+    exp = P.causal_depthwise_conv(full[h0:], full[:h0], w, dilation=dil)
+    assert (pre - exp).abs().max().item() <= 1e-6 * max(exp.abs().max().item(), 1.0)
+    assert (out - torch.nn.functional.silu(pre)).abs().max().item() <= 1e-6
+
+
+def test_window_conv_equals_generic_conv(cuda):
+    """The model's shape (4 taps, dilation 3) runs on the register-window
+    kernel; the same convolution as 5 taps whose oldest tap is zero runs on the
+    generic kernel.  Both give the same pre-activation."""
+    hc, n, T, h0 = 4, 2560, 100, 9
+    g = torch.Generator().manual_seed(71)
+    full = torch.randn((h0 + T, hc * n), generator=g)
+    w4 = torch.randn((hc * n, 4), generator=g) * 0.5
+    w5 = torch.cat([torch.zeros((hc * n, 1)), w4], dim=1)
+    _, pre4 = _conv_pre(full, h0, T, hc, n, w4, 3, cuda)
+    _, pre5 = _conv_pre(full, h0, T, hc, n, w5, 3, cuda)
+    assert (pre4 - pre5).abs().max().item() <= 1e-6 * pre4.abs().max().item()
