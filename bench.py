@@ -748,12 +748,17 @@ def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
                 ple.ple_forward(emb, hidden, w, hist, HP, gemm=mode)
             ramp(lambda: ple.ple_forward(emb, hidden, w, hist, HP, gemm=mode), 0.3)
             ms = timed(lambda: ple.ple_forward(emb, hidden, w, hist, HP, gemm=mode), steps)
-            # the two projections alone, for the GEMMs' own rate
+            # the two projections alone (one launch, as ple_forward runs them), for the GEMMs' own rate
             if mode == "fp32":
-                gemm_ms = timed(lambda: (emb @ w.w_key.T, emb @ w.w_value.T), steps)
+                gemm_ms = timed(lambda: ple.gemm_f32(emb, w.w_key, b_n2=w.w_value), steps)
+                # the same products through hipBLASLt (torch.matmul, no TF32), for reference
+                allow = torch.backends.cuda.matmul.allow_tf32
+                torch.backends.cuda.matmul.allow_tf32 = False
+                lib_ms = timed(lambda: (emb @ w.w_key.T, emb @ w.w_value.T), steps)
+                torch.backends.cuda.matmul.allow_tf32 = allow
             else:
                 pk, pv = ple.SplitPlanes(w.w_key), ple.SplitPlanes(w.w_value)
-                gemm_ms = timed(lambda: (ple.gemm_x3(emb, pk), ple.gemm_x3(emb, pv)), steps)
+                gemm_ms = timed(lambda: ple.gemm_x3(emb, pk, b_n2=pv), steps)
         # forward + backward to emb (the descent's use: the weights stay fixed)
         fb = lambda: torch.autograd.grad(ple.ple_forward(emb_v, hidden, w, hist, HP, gemm=mode)[0], emb_v, d_out)
         fb()
@@ -762,10 +767,13 @@ def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
         res[mode] = {"us_per_step": ms * 1e3, "positions_per_s": t_len / (ms * 1e-3), "gemm_us": gemm_ms * 1e3,
                      "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12, "non_gemm_us": (ms - gemm_ms) * 1e3,
                      "us_forward_backward_to_emb": fb_ms * 1e3}
+        if mode == "fp32":
+            res[mode]["hipblaslt_gemm_us"] = lib_ms * 1e3
+            res[mode]["hipblaslt_gemm_tflops"] = flops / (lib_ms * 1e-3) / 1e12
     out = {"workload": "ple_forward: T 2048, hc 4, n_embd 2560, 4 taps, dilation 3, fp32 activations; key/value "
-                       "GEMMs either fp32 (hipBLASLt through torch.matmul; the reference's arithmetic) or bf16x3 "
-                       "(eg_gemm_bf16x3 on the bf16 matrix cores, 16 mantissa bits per operand); gate/norm and "
-                       "conv in HIP",
+                       "GEMMs (one launch) either fp32 (eg_gemm_f32 on the fp32 matrix cores; the reference's "
+                       "arithmetic; hipBLASLt's time for the same products beside it) or bf16x3 (eg_gemm_bf16x3 "
+                       "on the bf16 matrix cores, 16 mantissa bits per operand); gate/norm and conv in HIP",
            **res["fp32"], "bf16x3": res["bf16x3"], "fp32_mfma_peak_tflops": 157.3,
            "bf16_mfma_peak_tflops": 2500.0}
     if cpu_s > 0:
@@ -981,8 +989,8 @@ def main() -> None:
         result["ple_forward"] = pl
         log_cpu_leg("ple_forward", pl)
         log(f"ple_forward: {pl['us_per_step']:.0f} us/step; its two GEMMs alone {pl['gemm_us']:.0f} us "
-            f"({pl['gemm_tflops']:.1f} TFLOP/s fp32), the rest {pl['non_gemm_us']:.0f} us; forward + backward "
-            f"to emb {pl['us_forward_backward_to_emb']:.0f} us")
+            f"({pl['gemm_tflops']:.1f} TFLOP/s fp32; hipBLASLt {pl['hipblaslt_gemm_us']:.0f} us), the rest "
+            f"{pl['non_gemm_us']:.0f} us; forward + backward to emb {pl['us_forward_backward_to_emb']:.0f} us")
         x3 = pl["bf16x3"]
         log(f"ple_forward with bf16x3 GEMMs: {x3['us_per_step']:.0f} us/step; GEMMs {x3['gemm_us']:.0f} us "
             f"({x3['gemm_tflops']:.1f} TFLOP/s fp32-equivalent); forward + backward to emb "

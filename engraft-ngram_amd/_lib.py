@@ -106,6 +106,18 @@ class EgGemmOperands(ctypes.Structure):
     ]
 
 
+class EgGemmF32Operands(ctypes.Structure):
+    _fields_ = [
+        ("a", c_void_p),
+        ("lda", c_int64),
+        ("b", c_void_p),
+        ("ldb", c_int64),
+        ("b2", c_void_p),
+        ("ldb2", c_int64),
+        ("k", c_int64),
+    ]
+
+
 # name -> (restype, argtypes); every symbol the header declares.
 SIGNATURES = {
     "eg_last_error": (c_char_p, []),
@@ -133,9 +145,11 @@ SIGNATURES = {
                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_rms": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, ctypes.c_float, c_void_p, c_void_p]),
     "eg_split_bf16": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
-    "eg_gemm_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int32]),
+    "eg_gemm_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int32]),
     "eg_gemm_bf16x3": (c_int32, [POINTER(EgGemmOperands), c_int32, c_int64, c_int64, c_int64, c_void_p, c_int64,
                                  c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_void_p]),
+    "eg_gemm_f32": (c_int32, [POINTER(EgGemmF32Operands), c_int32, c_int64, c_int64, c_int64, c_void_p, c_int64,
+                              c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_void_p]),
     "eg_forward_decode": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,
                                     c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_forward_timed": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,

@@ -1,39 +1,57 @@
-// fp32 GEMM on the bf16 matrix cores, three products per operand pair:
+// The PLE block's projections (engraft/replica/layers.py:594-606: key = emb
+// w_key^T and value = emb w_value^T, as two column groups over the same A in
+// one launch, and their backward d_emb = d_key w_key + d_value w_value as two
+// K segments with the weights' transposes kept row-major):
 //
 //   C[M, N] (+)= A[M, K] B[N, K]^T  (+ A2[M, K2] B2[N, K2]^T)
 //
-// Each fp32 operand is split once (eg_split_bf16) into bf16 planes hi = rne(x)
-// and lo = rne(x - hi) (x - hi is exact in fp32), and C accumulates
-// hi*hi + hi*lo + lo*hi in fp32 on v_mfma_f32_32x32x16_bf16.  hi + lo keeps
-// 16 of fp32's 24 mantissa bits, so each product carries a relative error up
-// to ~3 x 2^-18 (fp32's own is 2^-24): about 1e-5 of the result on random
-// data, at the bf16 rate.  This runs the PLE block's
-// projections (engraft/replica/layers.py:594-606: key = emb w_key^T and
-// value = emb w_value^T in one launch, as two column groups over the same A,
-// and their backward d_emb = d_key w_key + d_value w_value as two K segments
-// with the weights' transposes kept row-major).
+// in two arithmetics.
 //
-// Tiling: 128 x 128 output tile per 256-thread workgroup (four wavefronts,
-// 64 x 64 each as 2 x 2 MFMA tiles), K in steps of 32 through a two-stage LDS
-// ring filled by direct-to-LDS loads (global_load_lds_dwordx4: lane i of a
-// wavefront writes 16 bytes at the wavefront's LDS base + 16 i), so the next
-// step's loads are in flight during the current step's MFMAs without passing
-// through registers.  A plane tile is rows x 32 bf16 (64 B rows, no padding);
-// the 16-byte chunk c of row r sits in slot c ^ ((r >> 1) & 3), which spreads
-// the fragment reads (32 rows at one chunk) over the banks.  Two stages (64 KB)
-// keep two workgroups on a CU.  Measured against it after a warm-up, launches
+// gemm_x3_kernel, fp32 on the bf16 matrix cores: each fp32 operand is split
+// once (eg_split_bf16) into bf16 planes hi = rne(x) and lo = rne(x - hi)
+// (x - hi is exact in fp32), and C accumulates hi*hi + hi*lo + lo*hi in fp32
+// on v_mfma_f32_32x32x16_bf16.  hi + lo keeps 16 of fp32's 24 mantissa bits,
+// so each product carries a relative error up to ~3 x 2^-18 (fp32's own is
+// 2^-24): about 1e-5 of the result on random data, at the bf16 rate.
+//
+// gemm_f32_kernel, fp32 arithmetic on the fp32 matrix cores
+// (v_mfma_f32_32x32x2_f32): the products of an fp32 matmul, each operand
+// read once as fp32.
+//
+// Tiling, both: 128 x 128 output tile per 256-thread workgroup (four
+// wavefronts, 64 x 64 each as 2 x 2 MFMA tiles), K in steps of 32 through a
+// two-stage LDS ring filled by direct-to-LDS loads (global_load_lds_dwordx4:
+// lane i of a wavefront writes 16 bytes at the wavefront's LDS base + 16 i),
+// so the next step's loads are in flight during the current step's MFMAs
+// without passing through registers.  Two stages (64 KB) keep two workgroups
+// on a CU.  For gemm_x3, measured against it after a warm-up, launches
 // interleaved: 128 x 256 and 256 x 128 tiles with eight wavefronts, 256 x 256
 // with sixteen, three stages, and scheduling hints that interleave the LDS
 // reads with the MFMAs ran 3-5 % slower; register-staged loads into a padded
-// LDS tile ran 20 % slower.  With few
-// output tiles (the backward's 16 x 20) the K range is cut into slices whose
-// partial products go to a workspace and are summed in slice order by a
-// second kernel, so the result does not depend on scheduling.
+// LDS tile ran 20 % slower; fragments of the next half step read during the
+// current one's MFMAs, and a swizzle free of LDS bank conflicts (counted by
+// SQ_LDS_BANK_CONFLICT), changed the key projection by under 1 %.
 //
-// Workgroups are dispatched round-robin over the 8 XCDs; the tile order is
+// The last round.  The grid is a run of whole tiles followed by pieces: when
+// the tile count leaves the last round of workgroups (two a CU) partly empty,
+// the tiles of that round are cut along K into pieces that fill it, the
+// pieces' partial products go to a workspace, and piece_sum_kernel adds each
+// tile's pieces in K order into C, so the result does not depend on
+// scheduling.  On MI355X (512 workgroup slots): the key projection's 1280
+// tiles run as 1024 whole tiles and 256 tiles in halves, the forward's key +
+// value (1600 tiles) as 1536 and 64 in eighths, the backward's 320 tiles of
+// 400 K steps in thirds (1, 2, 3, 4, 6 pieces: 527, 486, 422, 436, 461 us
+// there).  An explicit k_slices cuts every tile the same way.
+//
+// Workgroups are dispatched round-robin over the 8 XCDs; the whole tiles are
 // remapped so that each XCD takes a contiguous run of tiles, grouped 8 row
 // tiles deep, whose A and B panels its own L2 shares.
 #include "eg_common.h"
+
+#include <algorithm>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 namespace eg {
 namespace {
@@ -45,10 +63,34 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 constexpr int kBM = 128, kBN = 128, kBK = 32;
-constexpr int kPlane = 128 * kBK;   // bf16 per plane tile
-constexpr int kStage = 4 * kPlane;  // ah, al, bh, bl
+constexpr int kTileElems = kBM * kBN;  // floats of one piece's partial product
 constexpr int kStages = 2;
+constexpr int kSlotsPerCu = 2;         // workgroups a CU holds (64 KB of LDS each)
+
+// bf16x3: a plane tile is 128 rows x 32 bf16 (64 B rows)
+constexpr int kPlane = 128 * kBK;
+constexpr int kStage = 4 * kPlane;  // ah, al, bh, bl
 constexpr size_t kLds = (size_t)kStages * kStage * 2;  // 64 KB
+
+// fp32: A and B tiles of 128 rows x 32 floats (128 B rows)
+constexpr int kF32Tile = 128 * kBK;
+constexpr int kF32Stage = 2 * kF32Tile;
+constexpr size_t kF32Lds = (size_t)kStages * kF32Stage * 4;  // 64 KB
+
+// What both kernels share: output, tiles and the whole-tile / piece split.
+struct Plan {
+  int64_t kt0;            // K steps of segment 0
+  int64_t kt_total;
+  int64_t kt_per_piece;
+  int dp_tiles;           // blocks [0, dp_tiles) run whole tiles (logical tiles 0 .. dp_tiles-1)
+  int pieces;             // pieces per remaining tile; block dp_tiles + q runs piece q
+  float* c[2];            // per column group
+  int64_t ldc[2];
+  float* ws;              // [tiles - dp_tiles][pieces][128 x 128] partial products
+  int64_t m, n[2];
+  int tiles_m, tiles_n0, tiles_n;
+  int accumulate;         // 1: C += result
+};
 
 struct GemmSeg {
   const __bf16* a_hi;
@@ -62,16 +104,20 @@ struct GemmSeg {
 struct GemmArgs {
   GemmSeg seg[2];
   int n_seg;
-  int64_t kt0;            // K tiles of segment 0
-  int64_t kt_total;
-  int64_t kt_per_slice;
-  int slices;
-  float* c[2];            // per column group (slices == 1)
-  int64_t ldc[2];
-  float* ws;              // slices > 1: [slices, m, n[0] + n[1]] partial products
-  int64_t m, n[2];
-  int tiles_m, tiles_n0, tiles_n;
-  int accumulate;         // 1: C += result (slices == 1)
+  Plan p;
+};
+
+struct F32Seg {
+  const float* a;
+  const float* b[2];      // per column group
+  int64_t lda, ldb[2];    // in floats, multiples of 4
+  int64_t ktiles;         // K / 32
+};
+
+struct F32Args {
+  F32Seg seg[2];
+  int n_seg;
+  Plan p;
 };
 
 // hi = rne(x), lo = rne(x - hi) for 4 values.
@@ -112,11 +158,9 @@ __global__ __launch_bounds__(256) void split_kernel(const float* __restrict__ x,
   }
 }
 
-// Workgroup b -> output tile: XCD-contiguous runs, then groups of kGroupM row tiles.
-__device__ inline void tile_of(int b, int nb, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int x = b % kXcds, i = b / kXcds;
-  const int per = nb / kXcds, extra = nb % kXcds;
-  const int logical = x * per + (x < extra ? x : extra) + i;
+// Logical tile -> (row tile, column tile): groups of kGroupM row tiles, each
+// group walked column tile by column tile.
+__device__ inline void grouped(int logical, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int in_group = kGroupM * tiles_n;
   const int g = logical / in_group;
   const int first_m = g * kGroupM;
@@ -126,20 +170,93 @@ __device__ inline void tile_of(int b, int nb, int tiles_m, int tiles_n, int& tm,
   tn = r / gsize;
 }
 
+// The block's work: a whole tile (piece < 0) or piece `piece` of a tile of the
+// last round, its K steps [kv0, kv1), and where its output goes.
+struct Work {
+  int64_t m0, n0, kv0, kv1;
+  int grp, piece;
+};
+
+__device__ inline Work work_of(const Plan& p) {
+  Work w;
+  const int b = blockIdx.x;
+  int logical;
+  if (b < p.dp_tiles) {
+    // XCD-contiguous runs: block b runs on XCD b % 8
+    const int x = b % kXcds, i = b / kXcds;
+    const int per = p.dp_tiles / kXcds, extra = p.dp_tiles % kXcds;
+    logical = x * per + (x < extra ? x : extra) + i;
+    w.piece = -1;
+    w.kv0 = 0;
+    w.kv1 = p.kt_total;
+  } else {
+    const int q = b - p.dp_tiles;
+    logical = p.dp_tiles + q / p.pieces;
+    w.piece = q;
+    w.kv0 = (int64_t)(q % p.pieces) * p.kt_per_piece;
+    w.kv1 = w.kv0 + p.kt_per_piece < p.kt_total ? w.kv0 + p.kt_per_piece : p.kt_total;
+  }
+  int tm, tn;
+  grouped(logical, p.tiles_m, p.tiles_n, tm, tn);
+  w.grp = tn < p.tiles_n0 ? 0 : 1;
+  w.m0 = (int64_t)tm * kBM;
+  w.n0 = (int64_t)(w.grp ? tn - p.tiles_n0 : tn) * kBN;
+  return w;
+}
+
+// D of a 32 x 32 MFMA tile: lane l holds column l % 32 and rows
+// 8 (r / 4) + 4 (l / 32) + r % 4.  A whole tile goes to C (bounded by m and
+// n, added to when accumulating); a piece to its 128 x 128 workspace slot.
+__device__ inline void store_acc(const Plan& p, const Work& w, const f32x16 (&acc)[2][2], int wm, int wn,
+                                 int lane) {
+  if (w.piece >= 0) {
+    float* t = p.ws + (int64_t)w.piece * kTileElems;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int lc = wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          t[(wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kBN + lc] = acc[i][j][r];
+      }
+    return;
+  }
+  float* out = p.c[w.grp];
+  const int64_t ld = p.ldc[w.grp], n_grp = p.n[w.grp];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = w.n0 + wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = w.m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row < p.m && col < n_grp) {
+          float* q = out + row * ld + col;
+          *q = p.accumulate ? *q + acc[i][j][r] : acc[i][j][r];
+        }
+      }
+    }
+}
+
 __device__ inline int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
+__device__ inline int swz8(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 // s_waitcnt vmcnt(0), leaving the other counters alone.
 __device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
 
+// A bf16 plane tile is rows x 32 bf16 (64 B rows, no padding); the 16-byte
+// chunk c of row r sits in slot c ^ ((r >> 1) & 3), which spreads the
+// fragment reads (32 rows at one chunk) over the banks.
 __global__ __launch_bounds__(256) void gemm_x3_kernel(const GemmArgs args) {
   extern __shared__ __attribute__((aligned(16))) __bf16 lds[];
+  const Plan& p = args.p;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  int tm, tn;
-  tile_of(blockIdx.x, gridDim.x, args.tiles_m, args.tiles_n, tm, tn);
-  const int grp = tn < args.tiles_n0 ? 0 : 1;
-  const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)(grp ? tn - args.tiles_n0 : tn) * kBN;
-  const int64_t n_grp = args.n[grp];
+  const Work w = work_of(p);
+  const int grp = w.grp;
+  const int64_t n_grp = p.n[grp];
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -160,17 +277,15 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const GemmArgs args) {
   for (int j = 0; j < 8; ++j) {
     const int q = uwave + 4 * j, plane = q >> 3, row = 16 * (q & 7) + (lane >> 2);
     const bool is_a = plane < 2;
-    const int64_t gr = (is_a ? m0 : n0) + row, lim = is_a ? args.m : n_grp;
+    const int64_t gr = (is_a ? w.m0 : w.n0) + row, lim = is_a ? p.m : n_grp;
     row_of[j] = gr < lim ? gr : lim - 1;
     col_of[j] = swz(row, lane & 3) * 8;
   }
 
-  // the slice's K steps, segment by segment (the ring drains at a segment change)
-  const int64_t kv0 = (int64_t)blockIdx.y * args.kt_per_slice;
-  const int64_t kv1 = kv0 + args.kt_per_slice < args.kt_total ? kv0 + args.kt_per_slice : args.kt_total;
+  // the block's K steps, segment by segment (the ring drains at a segment change)
   for (int s = 0; s < args.n_seg; ++s) {
-    const int64_t seg0 = s ? args.kt0 : 0, seg1 = s ? args.kt_total : args.kt0;
-    const int64_t lo = kv0 > seg0 ? kv0 : seg0, hi = kv1 < seg1 ? kv1 : seg1;
+    const int64_t seg0 = s ? p.kt0 : 0, seg1 = s ? p.kt_total : p.kt0;
+    const int64_t lo = w.kv0 > seg0 ? w.kv0 : seg0, hi = w.kv1 < seg1 ? w.kv1 : seg1;
     if (lo >= hi) continue;
     const GemmSeg& sg = args.seg[s];
     const __bf16* src[8];
@@ -235,41 +350,271 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const GemmArgs args) {
     }
     __builtin_amdgcn_s_barrier();  // the ring is refilled by the next segment
   }
+  store_acc(p, w, acc, wm, wn, lane);
+}
 
-  // D of a 32 x 32 tile: lane l holds column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4
-  const int64_t n_all = args.n[0] + args.n[1];
-  float* out = args.slices > 1 ? args.ws + (int64_t)blockIdx.y * args.m * n_all + (grp ? args.n[0] : 0)
-                               : args.c[grp];
-  const int64_t ld_out = args.slices > 1 ? n_all : args.ldc[grp];
-  const bool add = args.slices == 1 && args.accumulate;
+// One MFMA takes one A and one B value per lane (lane l: row / column l % 32,
+// k = l / 32), so each lane half works through its own 16 k of a step: lane
+// half h reads k 16 h .. 16 h + 15 of its row as four 16-byte chunks and the
+// 16 MFMAs of the step pair k = kk (half 0) with k = 16 + kk (half 1).  The
+// 16-byte chunk c of tile row r sits in slot c ^ ((r >> 1) & 7): a fragment
+// read (16 lanes at one chunk of 16 consecutive rows per LDS cycle) then
+// touches 16 distinct 16-byte bank groups.  64 MFMAs of 64 cycles a step
+// against 16 KB of LDS reads: the matrix cores, not the LDS, bound it.
+__global__ __launch_bounds__(256) void gemm_f32_kernel(const F32Args args) {
+  extern __shared__ __attribute__((aligned(16))) float ldsf[];
+  const Plan& p = args.p;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const Work w = work_of(p);
+  const int grp = w.grp;
+  const int64_t n_grp = p.n[grp];
+
+  f32x16 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < args.m && col < n_grp) {
-          float* p = out + row * ld_out + col;
-          *p = add ? *p + acc[i][j][r] : acc[i][j][r];
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // this wavefront's 8 loads per stage: load q = wave + 4 j covers tile rows
+  // 8 (q % 16) .. +7 of A (j < 4) or B (j >= 4); lane i fills row 8 (q % 16) +
+  // i / 8, slot i % 8.  Rows past m or n read row m-1 or n-1 (not stored).
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);
+  int64_t row_of[8];
+  int col_of[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int q = uwave + 4 * j, row = 8 * (q & 15) + (lane >> 3);
+    const int64_t gr = (j < 4 ? w.m0 : w.n0) + row, lim = j < 4 ? p.m : n_grp;
+    row_of[j] = gr < lim ? gr : lim - 1;
+    col_of[j] = swz8(row, lane & 7) * 4;
+  }
+
+  for (int s = 0; s < args.n_seg; ++s) {
+    const int64_t seg0 = s ? p.kt0 : 0, seg1 = s ? p.kt_total : p.kt0;
+    const int64_t lo = w.kv0 > seg0 ? w.kv0 : seg0, hi = w.kv1 < seg1 ? w.kv1 : seg1;
+    if (lo >= hi) continue;
+    const F32Seg& sg = args.seg[s];
+    const float* src[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      src[j] = (j < 4 ? sg.a : sg.b[grp]) + row_of[j] * (j < 4 ? sg.lda : sg.ldb[grp]) + col_of[j];
+    auto issue = [&](int64_t kt) {
+      float* st = ldsf + (kt & 1) * kF32Stage;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int q = uwave + 4 * j;
+        __builtin_amdgcn_global_load_lds((const void*)(src[j] + kt * kBK),
+                                         (__attribute__((address_space(3))) void*)(st + (j < 4 ? 0 : kF32Tile) +
+                                                                                   8 * (q & 15) * kBK),
+                                         16, 0, 0);
+      }
+    };
+    issue(lo - seg0);
+    for (int64_t kv = lo; kv < hi; ++kv) {
+      const int64_t kt = kv - seg0;
+      wait_vm0();
+      __builtin_amdgcn_s_barrier();
+      if (kv + 1 < hi) issue(kt + 1);
+      const float* st = ldsf + (kt & 1) * kF32Stage;
+      float4 fa[2][4], fb[2][4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int ar = wm * 64 + i * 32 + (lane & 31);
+        const int br = wn * 64 + i * 32 + (lane & 31);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int chunk = 4 * (lane >> 5) + c;
+          fa[i][c] = *(const float4*)(st + ar * kBK + swz8(ar, chunk) * 4);
+          fb[i][c] = *(const float4*)(st + kF32Tile + br * kBK + swz8(br, chunk) * 4);
         }
       }
+#pragma unroll
+      for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const float4& av = fa[i][kk >> 2];
+            const float4& bv = fb[j][kk >> 2];
+            const float x = (kk & 3) == 0 ? av.x : (kk & 3) == 1 ? av.y : (kk & 3) == 2 ? av.z : av.w;
+            const float y = (kk & 3) == 0 ? bv.x : (kk & 3) == 1 ? bv.y : (kk & 3) == 2 ? bv.z : bv.w;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc[i][j], 0, 0, 0);
+          }
     }
+    __builtin_amdgcn_s_barrier();
+  }
+  store_acc(p, w, acc, wm, wn, lane);
 }
 
-// C (+)= the sum of the slices' partial products, in slice order.
-__global__ __launch_bounds__(256) void slice_sum_kernel(const float* __restrict__ ws, int slices, int64_t m,
-                                                        int64_t n0, int64_t n1, float* c0, int64_t ldc0, float* c1,
-                                                        int64_t ldc1, int accumulate) {
-  const int64_t n_all = n0 + n1, total = m * n_all;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int64_t row = i / n_all, col = i % n_all;
-    float v = ws[i];
-    for (int s = 1; s < slices; ++s) v += ws[s * total + i];
-    float* p = col < n0 ? c0 + row * ldc0 + col : c1 + row * ldc1 + (col - n0);
-    *p = accumulate ? *p + v : v;
+// C (+)= the sum of a last-round tile's pieces, in K order: 16 blocks a tile,
+// each thread four consecutive columns of one row.
+__global__ __launch_bounds__(256) void piece_sum_kernel(const Plan p) {
+  const int q = blockIdx.x >> 4;
+  const int e = (blockIdx.x & 15) * 256 + threadIdx.x;  // float4 of the 128 x 128 tile
+  const int lr = e >> 5, lc = (e & 31) * 4;
+  int tm, tn;
+  grouped(p.dp_tiles + q, p.tiles_m, p.tiles_n, tm, tn);
+  const int grp = tn < p.tiles_n0 ? 0 : 1;
+  const int64_t row = (int64_t)tm * kBM + lr;
+  if (row >= p.m) return;
+  const float4* ws = (const float4*)(p.ws + (int64_t)q * p.pieces * kTileElems) + e;
+  float4 v = ws[0];
+  for (int s = 1; s < p.pieces; ++s) {
+    const float4 u = ws[(int64_t)s * (kTileElems / 4)];
+    v.x += u.x;
+    v.y += u.y;
+    v.z += u.z;
+    v.w += u.w;
   }
+  const int64_t n_grp = p.n[grp], col0 = (int64_t)(grp ? tn - p.tiles_n0 : tn) * kBN + lc;
+  float* out = p.c[grp] + row * p.ldc[grp];
+  const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int64_t col = col0 + t;
+    if (col < n_grp) out[col] = p.accumulate ? out[col] + vv[t] : vv[t];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+
+struct PiecePlan {
+  int dp;              // whole tiles
+  int pieces;          // pieces per remaining tile
+  int64_t kt_per_piece;
+};
+
+// k_slices >= 1: every tile in k_slices pieces (1: whole tiles).  0: the
+// tiles of a partly filled last round (of `slots` workgroups) in the piece
+// count that minimises the time of that round in tile units, ceil(R s /
+// slots) / s, plus the cost of summing the pieces (R s slots' worth of 64 KB
+// partial products, ~0.08 of a tile of 80 K steps per round of pieces); at
+// least 8 K steps a piece, and only for a gain of 10 % or more.
+PiecePlan plan_pieces(int64_t tiles, int64_t kt_total, int k_slices, int slots) {
+  PiecePlan pp{(int)tiles, 1, kt_total > 0 ? kt_total : 1};
+  int s = 1;
+  if (k_slices >= 1) {
+    s = k_slices;
+  } else {
+    const int64_t r = tiles % slots;
+    if (r == 0 || kt_total < 16) return pp;
+    double best = 1.0;
+    for (int c = 2; c <= 8 && kt_total / c >= 8; ++c) {
+      const double t = (double)((r * c + slots - 1) / slots) / c + 6.4 / (double)kt_total * (double)(r * c) / slots;
+      if (t < best) {
+        best = t;
+        s = c;
+      }
+    }
+    if (best > 0.9) return pp;
+  }
+  if (kt_total < s) s = kt_total > 0 ? (int)kt_total : 1;
+  if (s <= 1) return pp;
+  pp.kt_per_piece = (kt_total + s - 1) / s;
+  pp.pieces = (int)((kt_total + pp.kt_per_piece - 1) / pp.kt_per_piece);
+  if (pp.pieces <= 1) {
+    pp.pieces = 1;
+    pp.kt_per_piece = kt_total;
+    return pp;
+  }
+  pp.dp = k_slices >= 1 ? 0 : (int)(tiles - tiles % slots);
+  return pp;
+}
+
+// Workgroup slots of the current device: kSlotsPerCu per CU.
+int device_slots(int* slots) {
+  static std::mutex mu;
+  static std::vector<std::pair<int, int>> known;  // (device, CU count)
+  int dev = 0;
+  EG_CHECK_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  for (const auto& k : known)
+    if (k.first == dev) {
+      *slots = kSlotsPerCu * k.second;
+      return EG_OK;
+    }
+  int cus = 0;
+  EG_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  EG_CHECK_ARG(cus > 0, "device %d reports %d CUs", dev, cus);
+  known.emplace_back(dev, cus);
+  *slots = kSlotsPerCu * cus;
+  return EG_OK;
+}
+
+int64_t tiles_of(int64_t m, int64_t n, int64_t n2) {
+  return ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN + (n2 + kBN - 1) / kBN);
+}
+
+int64_t piece_bytes(int64_t tiles, const PiecePlan& pp) {
+  return pp.pieces > 1 ? (tiles - pp.dp) * pp.pieces * (int64_t)kTileElems * (int64_t)sizeof(float) : 0;
+}
+
+// The part of both entry points after their operands are checked: the plan,
+// the LDS attribute, the launch and the pieces' sum.
+template <typename Args>
+int launch_gemm(void (*kernel)(const Args), size_t lds, const char* name, Args& g, int64_t m, int64_t n, int64_t n2,
+                float* c, int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate, int32_t k_slices,
+                void* workspace, int64_t workspace_bytes, void* stream) {
+  EG_CHECK_ARG(m >= 0 && n >= 0 && n2 >= 0 && k_slices >= 0, "m=%lld n=%lld n2=%lld k_slices=%d", (long long)m,
+               (long long)n, (long long)n2, k_slices);
+  EG_CHECK_ARG(n == 0 || (c != nullptr && ldc >= n), "c / ldc");
+  EG_CHECK_ARG(n2 == 0 || (c2 != nullptr && ldc2 >= n2), "c2 / ldc2");
+  if (m == 0 || n + n2 == 0) return 0;
+  Plan& p = g.p;
+  p.kt0 = g.n_seg > 0 ? g.seg[0].ktiles : 0;
+  p.kt_total = p.kt0 + (g.n_seg > 1 ? g.seg[1].ktiles : 0);
+  const int64_t tiles = tiles_of(m, n, n2);
+  EG_CHECK_ARG(tiles < (1LL << 24), "too many tiles");
+  int slots = 0;
+  int rc = device_slots(&slots);
+  if (rc != EG_OK) return rc;
+  const PiecePlan pp = plan_pieces(tiles, p.kt_total, k_slices, slots);
+  const int64_t need = piece_bytes(tiles, pp);
+  if (need > 0) {
+    EG_CHECK_ARG(workspace != nullptr && ((uintptr_t)workspace & 15) == 0 && workspace_bytes >= need,
+                 "this call needs a 16-byte aligned workspace of %lld bytes (eg_gemm_workspace_size)",
+                 (long long)need);
+    p.ws = (float*)workspace;
+  }
+  p.dp_tiles = pp.dp;
+  p.pieces = pp.pieces;
+  p.kt_per_piece = pp.kt_per_piece;
+  p.c[0] = c;
+  p.c[1] = c2;
+  p.ldc[0] = ldc;
+  p.ldc[1] = ldc2;
+  p.m = m;
+  p.n[0] = n;
+  p.n[1] = n2;
+  p.tiles_m = (int)((m + kBM - 1) / kBM);
+  p.tiles_n0 = (int)((n + kBN - 1) / kBN);
+  p.tiles_n = p.tiles_n0 + (int)((n2 + kBN - 1) / kBN);
+  p.accumulate = accumulate ? 1 : 0;
+  const int64_t blocks = pp.dp + (tiles - pp.dp) * pp.pieces;
+  EG_CHECK_ARG(blocks < (1LL << 31), "too many workgroups");
+  hipStream_t st = (hipStream_t)stream;
+  // the dynamic LDS attribute, once per device and kernel
+  static std::mutex mu;
+  static std::vector<std::pair<const void*, int>> done;
+  int dev = 0;
+  EG_CHECK_HIP(hipGetDevice(&dev));
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    const std::pair<const void*, int> key((const void*)kernel, dev);
+    if (std::find(done.begin(), done.end(), key) == done.end()) {
+      EG_CHECK_HIP(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+      done.push_back(key);
+    }
+  }
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(256), lds, st, g);
+  rc = launch_status(name);
+  if (rc != 0 || pp.dp == tiles) return rc;
+  hipLaunchKernelGGL(piece_sum_kernel, dim3((unsigned)((tiles - pp.dp) * 16)), dim3(256), 0, st, p);
+  return launch_status("piece_sum_kernel");
 }
 
 }  // namespace
@@ -296,8 +641,13 @@ int eg_split_bf16(const float* x, int64_t rows, int64_t cols, int64_t ld, void* 
   return launch_status("split_kernel");
 }
 
-int64_t eg_gemm_workspace_size(int64_t m, int64_t n, int64_t n2, int32_t k_slices) {
-  return k_slices > 1 ? (int64_t)k_slices * m * (n + n2) * (int64_t)sizeof(float) : 0;
+int64_t eg_gemm_workspace_size(int64_t m, int64_t n, int64_t n2, int64_t k, int32_t k_slices) {
+  using namespace eg;
+  if (m <= 0 || n < 0 || n2 < 0 || n + n2 == 0 || k < 0 || k_slices < 0) return 0;
+  int slots = 0;
+  if (device_slots(&slots) != EG_OK) return -1;
+  const int64_t tiles = tiles_of(m, n, n2);
+  return piece_bytes(tiles, plan_pieces(tiles, k / 32, k_slices, slots));
 }
 
 int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,
@@ -305,11 +655,6 @@ int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_
                    int64_t workspace_bytes, void* stream) {
   using namespace eg;
   EG_CHECK_ARG(ops != nullptr && n_seg >= 0 && n_seg <= 2, "n_seg=%d", n_seg);
-  EG_CHECK_ARG(m >= 0 && n >= 0 && n2 >= 0 && k_slices >= 1, "m=%lld n=%lld n2=%lld k_slices=%d", (long long)m,
-               (long long)n, (long long)n2, k_slices);
-  EG_CHECK_ARG(n == 0 || (c != nullptr && ldc >= n), "c / ldc");
-  EG_CHECK_ARG(n2 == 0 || (c2 != nullptr && ldc2 >= n2), "c2 / ldc2");
-  if (m == 0 || n + n2 == 0) return 0;
   GemmArgs g{};
   for (int s = 0; s < n_seg; ++s) {
     const eg_gemm_operands& o = ops[s];
@@ -337,49 +682,41 @@ int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_
     sg.ktiles = o.k / 32;
     ++g.n_seg;
   }
-  g.kt0 = g.n_seg > 0 ? g.seg[0].ktiles : 0;
-  g.kt_total = g.kt0 + (g.n_seg > 1 ? g.seg[1].ktiles : 0);
-  int slices = k_slices;
-  if (g.kt_total < slices) slices = g.kt_total > 0 ? (int)g.kt_total : 1;
-  g.kt_per_slice = (g.kt_total + slices - 1) / slices;
-  if (g.kt_total > 0) slices = (int)((g.kt_total + g.kt_per_slice - 1) / g.kt_per_slice);
-  g.slices = slices;
-  g.c[0] = c;
-  g.c[1] = c2;
-  g.ldc[0] = ldc;
-  g.ldc[1] = ldc2;
-  g.m = m;
-  g.n[0] = n;
-  g.n[1] = n2;
-  g.accumulate = accumulate ? 1 : 0;
-  if (slices > 1) {
-    EG_CHECK_ARG(workspace != nullptr && ((uintptr_t)workspace & 15) == 0 &&
-                     workspace_bytes >= eg_gemm_workspace_size(m, n, n2, slices),
-                 "k_slices=%d needs a 16-byte aligned workspace of %lld bytes", slices,
-                 (long long)eg_gemm_workspace_size(m, n, n2, slices));
-    g.ws = (float*)workspace;
+  return launch_gemm(gemm_x3_kernel, kLds, "gemm_x3_kernel", g, m, n, n2, c, ldc, c2, ldc2, accumulate, k_slices,
+                     workspace, workspace_bytes, stream);
+}
+
+int eg_gemm_f32(const eg_gemm_f32_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,
+                int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate, int32_t k_slices, void* workspace,
+                int64_t workspace_bytes, void* stream) {
+  using namespace eg;
+  EG_CHECK_ARG(ops != nullptr && n_seg >= 0 && n_seg <= 2, "n_seg=%d", n_seg);
+  F32Args g{};
+  for (int s = 0; s < n_seg; ++s) {
+    const eg_gemm_f32_operands& o = ops[s];
+    EG_CHECK_ARG(o.k >= 0 && o.k % 32 == 0, "segment %d: k must be a multiple of 32 (k=%lld)", s, (long long)o.k);
+    if (o.k == 0) continue;
+    const float* mats[3] = {o.a, o.b, o.b2};
+    for (int q = 0; q < 3; ++q) {
+      if (q == 2 && n2 == 0) break;
+      EG_CHECK_ARG(mats[q] != nullptr && ((uintptr_t)mats[q] & 15) == 0,
+                   "segment %d: operand %d is NULL or not 16-byte aligned", s, q);
+    }
+    EG_CHECK_ARG(o.lda % 4 == 0 && o.ldb % 4 == 0 && o.lda >= o.k && o.ldb >= o.k &&
+                     (n2 == 0 || (o.ldb2 % 4 == 0 && o.ldb2 >= o.k)),
+                 "segment %d: leading dimensions must be multiples of 4 and >= k", s);
+    F32Seg& sg = g.seg[g.n_seg];
+    sg.a = o.a;
+    sg.b[0] = o.b;
+    sg.b[1] = n2 ? o.b2 : o.b;
+    sg.lda = o.lda;
+    sg.ldb[0] = o.ldb;
+    sg.ldb[1] = n2 ? o.ldb2 : o.ldb;
+    sg.ktiles = o.k / 32;
+    ++g.n_seg;
   }
-  g.tiles_m = (int)((m + kBM - 1) / kBM);
-  g.tiles_n0 = (int)((n + kBN - 1) / kBN);
-  g.tiles_n = g.tiles_n0 + (int)((n2 + kBN - 1) / kBN);
-  const int64_t blocks = (int64_t)g.tiles_m * g.tiles_n;
-  EG_CHECK_ARG(blocks < (1LL << 31), "too many tiles");
-  hipStream_t st = (hipStream_t)stream;
-  static bool lds_set[64] = {};
-  int dev = 0;
-  EG_CHECK_HIP(hipGetDevice(&dev));
-  if (dev < 64 && !lds_set[dev]) {
-    EG_CHECK_HIP(hipFuncSetAttribute((const void*)gemm_x3_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds));
-    lds_set[dev] = true;
-  }
-  hipLaunchKernelGGL(gemm_x3_kernel, dim3((unsigned)blocks, (unsigned)slices), dim3(256), kLds, st, g);
-  int rc = launch_status("gemm_x3_kernel");
-  if (rc != 0 || slices == 1) return rc;
-  const int64_t total = m * (n + n2);
-  const int64_t sb = (total + 255) / 256 < 16384 ? (total + 255) / 256 : 16384;
-  hipLaunchKernelGGL(slice_sum_kernel, dim3((unsigned)sb), dim3(256), 0, st, (const float*)g.ws, slices, m, n, n2, c,
-                     ldc, c2, ldc2, g.accumulate);
-  return launch_status("slice_sum_kernel");
+  return launch_gemm(gemm_f32_kernel, kF32Lds, "gemm_f32_kernel", g, m, n, n2, c, ldc, c2, ldc2, accumulate,
+                     k_slices, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

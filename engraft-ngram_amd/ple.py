@@ -3,10 +3,11 @@ for ``PleWeights`` / ``ple_forward`` (``engraft/replica/layers.py:555-626``).
 
 Forward:
 
-* ``key = emb @ w_key^T`` and ``value = emb @ w_value^T``: fp32 library GEMMs
-  (hipBLASLt through ``torch.matmul``), or with ``gemm="bf16x3"`` the
-  ``gemm_x3`` kernel on the bf16 matrix cores (operands split into bf16 hi +
-  lo, three products accumulated in fp32: 16 mantissa bits per operand);
+* ``key = emb @ w_key^T`` and ``value = emb @ w_value^T``, one launch of the
+  ``gemm_f32`` kernel on the fp32 matrix cores (fp32 arithmetic, as the
+  reference's torch matmuls), or with ``gemm="bf16x3"`` of the ``gemm_x3``
+  kernel on the bf16 matrix cores (operands split into bf16 hi + lo, three
+  products accumulated in fp32: 16 mantissa bits per operand);
 * ``eg_ple_gate``: per position and stream, the RMS norms of key and hidden,
   the score ``s``, the gate, ``gated = value * gate`` and its RMS norm;
 * ``eg_ple_conv``: the dilated causal depthwise convolution over
@@ -15,10 +16,10 @@ Forward:
 The result -- the output and the new history -- is differentiable in emb,
 hidden, the history and the weights.  The backward runs
 ``eg_ple_conv_backward`` and ``eg_ple_gate_backward`` on the forward's saved
-intermediates, then the projections' backward (with ``bf16x3``, one
+intermediates, then the projections' backward (one ``gemm_f32`` or
 ``gemm_x3`` call over two K segments); when weights need gradients, also the
-two weight GEMMs (fp32) and ``eg_ple_weight_grads`` for the norm and
-convolution weights.  Only shapes beyond the HIP kernels' limits (more than 4
+two weight GEMMs (fp32, ``torch.matmul``) and ``eg_ple_weight_grads`` for the
+norm and convolution weights.  Only shapes beyond the HIP kernels' limits (more than 4
 streams, ``n_embd`` > 4096, a convolution reaching back more than 32 rows)
 fall back to a torch recomputation of the block, differentiated by
 autograd.  Either way the forward values are the HIP kernels'.  ``detach_value`` / ``detach_gate`` change only the backward, as in
@@ -163,26 +164,18 @@ def _planes(x, cached: bool) -> SplitPlanes:
     return _PLANES.get(x) if cached else SplitPlanes(x)
 
 
-def _k_slices(tiles: int, k_tiles: int) -> int:
-    """K slices for few output tiles (two 128 x 128 workgroups fit a CU, 512
-    on the chip): the fewest slices, each at least 16 K steps, whose
-    workgroups fill their last round of 512 to 90 %; slices cost a pass over
-    the partial products.  Measured on the backward's 320 tiles: 1, 2, 3, 4,
-    6 slices take 527, 486, 422, 436, 461 us."""
-    rounds = 512
-    if tiles >= rounds:
-        return 1
-    best, best_eff = 1, tiles / rounds
-    for s in range(2, 9):
-        if k_tiles // s < 16:
-            break
-        work = tiles * s / rounds
-        eff = work / -(-work // 1)
-        if eff >= 0.9:
-            return s
-        if eff > best_eff:
-            best, best_eff = s, eff
-    return best
+def _gemm_workspace(m: int, n: int, n2: int, k: int, k_slices: int | None, dev):
+    """The K-slice argument for the GEMM entry points (0: the library plans the
+    pieces of a partly filled last round) and the workspace that plan needs."""
+    slices = 0 if k_slices is None else int(k_slices)
+    if slices < 0:
+        raise ValueError(f"k_slices must be >= 0, got {slices}")
+    with torch.cuda.device(dev):
+        ws_bytes = int(_lib.load().eg_gemm_workspace_size(m, n, n2, k, slices))
+    if ws_bytes < 0:
+        raise RuntimeError("eg_gemm_workspace_size: device query failed")
+    ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=dev) if ws_bytes else None
+    return slices, ws, ws_bytes
 
 
 def gemm_x3(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate: bool = False,
@@ -195,8 +188,9 @@ def gemm_x3(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate:
     ``cache_b`` keeps the planes of the B operands between calls (weights).
     ``b_n2`` (and ``b2_n2`` with a second segment) ``[n2, k]`` add a second
     column group, ``a @ b_n2.T (+ a2 @ b2_n2.T)`` into ``out2``, in the same
-    launch.  ``k_slices`` (default: chosen from the tile count) cuts K into
-    slices summed in a fixed order.  Returns ``out`` (``[m, n]`` fp32,
+    launch.  ``k_slices`` (default: the library's plan, which cuts the tiles
+    of a partly filled last round of workgroups along K) cuts every 128 x 128
+    tile into that many K pieces, summed in a fixed order.  Returns ``out`` (``[m, n]`` fp32,
     allocated when not given; added to when ``accumulate``), or ``(out,
     out2)`` with a second column group."""
     segs = [(_planes(a, False), _planes(b, cache_b), None if b_n2 is None else _planes(b_n2, cache_b))]
@@ -232,11 +226,74 @@ def gemm_x3(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate:
 
     out = _out(out, m, n, "out")
     out2 = _out(out2, m, n2, "out2") if n2 else None
-    tiles = -(-m // 128) * (-(-n // 128) + -(-n2 // 128))
-    slices = _k_slices(tiles, k_tiles) if k_slices is None else int(k_slices)
-    ws_bytes = int(_lib.load().eg_gemm_workspace_size(m, n, n2, slices))
-    ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=dev) if ws_bytes else None
+    slices, ws, ws_bytes = _gemm_workspace(m, n, n2, 32 * k_tiles, k_slices, dev)
     _lib.call("eg_gemm_bf16x3", ops, len(segs), m, n, n2, _lib.ptr(out), max(out.stride(0), n),
+              _lib.ptr(out2), max(out2.stride(0), n2) if n2 else 0, int(accumulate), slices, _lib.ptr(ws),
+              ws_bytes, _lib.stream_ptr(dev))
+    return (out, out2) if n2 else out
+
+
+def _f32_operand(x: torch.Tensor, kp: int) -> torch.Tensor:
+    """``x [rows, k]`` fp32 as eg_gemm_f32 reads it: unit column stride, row
+    stride a multiple of 4, 16-byte aligned, ``k`` a multiple of 32; otherwise
+    a copy with the columns zero-padded to ``kp``."""
+    if x.dtype != torch.float32:
+        x = x.float()
+    rows, cols = x.shape
+    if (cols == kp and x.stride(1) == 1 and x.stride(0) % 4 == 0 and x.stride(0) >= cols
+            and x.data_ptr() % 16 == 0):
+        return x
+    y = torch.zeros((rows, kp), dtype=torch.float32, device=x.device)
+    y[:, :cols] = x
+    return y
+
+
+def gemm_f32(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate: bool = False,
+             b_n2=None, b2_n2=None, out2: torch.Tensor | None = None, k_slices: int | None = None):
+    """``a @ b.T (+ a2 @ b2.T)`` in fp32 arithmetic on the fp32 matrix cores
+    (``eg_gemm_f32``): the products of an fp32 matmul, accumulated in fp32.
+    Operands and the column groups, K segments and K slices as
+    :func:`gemm_x3`, every operand an fp32 tensor (a ``k`` not a multiple of
+    32 is zero-padded in a copy).  Returns ``out``, or ``(out, out2)`` with a
+    second column group."""
+    raw = [(a, b, b_n2)] + ([(a2, b2, b2_n2)] if a2 is not None else [])
+    m, n = a.shape[0], b.shape[0]
+    n2 = 0 if b_n2 is None else b_n2.shape[0]
+    ops = (_lib.EgGemmF32Operands * 2)()
+    keep = []
+    k_tiles = 0
+    for i, (xa, xb, xb2) in enumerate(raw):
+        if xa.dim() != 2 or xb.dim() != 2 or xa.shape[0] != m or xb.shape[0] != n or xb.shape[1] != xa.shape[1]:
+            raise ValueError(f"gemm_f32: segment {i}: a [m, k] and b [n, k] expected, got {list(xa.shape)} and "
+                             f"{list(xb.shape)}")
+        if (xb2 is None) != (n2 == 0) or (xb2 is not None and (xb2.dim() != 2 or xb2.shape[0] != n2
+                                                                or xb2.shape[1] != xa.shape[1])):
+            raise ValueError(f"gemm_f32: segment {i}: the second column group needs b [n2, k] in every segment")
+        kp = (xa.shape[1] + 31) // 32 * 32
+        ta, tb = _f32_operand(xa, kp), _f32_operand(xb, kp)
+        tb2 = _f32_operand(xb2, kp) if xb2 is not None else None
+        keep += [ta, tb, tb2]
+        o = ops[i]
+        o.a, o.lda, o.b, o.ldb = _lib.ptr(ta), ta.stride(0), _lib.ptr(tb), tb.stride(0)
+        if tb2 is not None:
+            o.b2, o.ldb2 = _lib.ptr(tb2), tb2.stride(0)
+        o.k = kp
+        k_tiles += kp // 32
+    dev = a.device
+
+    def _out(t, rows, cols, name):
+        if t is None:
+            if accumulate:
+                raise ValueError(f"gemm_f32: accumulate needs {name}")
+            return torch.empty((rows, cols), dtype=torch.float32, device=dev)
+        if t.dtype != torch.float32 or t.shape != (rows, cols) or t.stride(1) != 1:
+            raise ValueError(f"gemm_f32: {name} must be fp32 [{rows}, {cols}] with unit column stride")
+        return t
+
+    out = _out(out, m, n, "out")
+    out2 = _out(out2, m, n2, "out2") if n2 else None
+    slices, ws, ws_bytes = _gemm_workspace(m, n, n2, 32 * k_tiles, k_slices, dev)
+    _lib.call("eg_gemm_f32", ops, len(raw), m, n, n2, _lib.ptr(out), max(out.stride(0), n),
               _lib.ptr(out2), max(out2.stride(0), n2) if n2 else 0, int(accumulate), slices, _lib.ptr(ws),
               ws_bytes, _lib.stream_ptr(dev))
     return (out, out2) if n2 else out
@@ -263,12 +320,9 @@ class _PleFn(torch.autograd.Function):
         wk32 = w_key.to(**f32)
         wv32 = w_value.to(**f32)
         if gemm == "bf16x3":
-            pe = SplitPlanes(emb32)
-            key = gemm_x3(pe, wk32, cache_b=True)
-            value = gemm_x3(pe, wv32, cache_b=True)
+            key, value = gemm_x3(SplitPlanes(emb32), wk32, cache_b=True, b_n2=wv32)
         else:
-            key = (emb32 @ wk32.T).contiguous()
-            value = (emb32 @ wv32.T).contiguous()
+            key, value = gemm_f32(emb32, wk32, b_n2=wv32)
         hidden32 = hidden.to(**f32).contiguous()
         h0 = hist.shape[0]
         full = torch.empty((h0 + t_len, hc * n), **f32)
@@ -390,9 +444,7 @@ class _PleFn(torch.autograd.Function):
                 flat = [x for part in parts for x in part]
                 d_emb = gemm_x3(*flat, cache_b=True)
             else:
-                d_emb = parts[0][0] @ parts[0][1].T
-                if len(parts) > 1:
-                    d_emb.addmm_(parts[1][0], parts[1][1].T)
+                d_emb = gemm_f32(*[x for part in parts for x in part])
             d_emb = d_emb.to(emb_dt)
         d_hist_in = d_full[:h0].reshape(h0, hc, n).to(hist_dt) if need_hist else None
         return (d_emb, d_hidden.to(hidden_dt) if d_hidden is not None else None, None, None, None, None, None, None,
@@ -433,9 +485,7 @@ class _PleFn(torch.autograd.Function):
             elif ctx.gemm == "bf16x3":
                 d_emb = gemm_x3(*[x for part in parts for x in part], cache_b=True)
             else:
-                d_emb = parts[0][0] @ parts[0][1].T
-                if len(parts) > 1:
-                    d_emb.addmm_(parts[1][0], parts[1][1].T)
+                d_emb = gemm_f32(*[x for part in parts for x in part])
             d_emb = d_emb.to(emb_dt)
         wdt = ctx.w_dtypes
         d_wk = d_wv = None
@@ -470,9 +520,9 @@ def ple_forward(emb: torch.Tensor, hidden: torch.Tensor, w: PleWeights, hist: to
     565-626``).  ``emb [T, n_embd]``, ``hidden [T, hc, n_embd]``, ``hist``
     ``[rows, hc, n_embd]`` (at most ``(K-1)*ple_ngram_size`` rows, empty at a
     sequence start); all on the device.  ``gemm`` picks the projections' GEMM:
-    ``"fp32"`` (the reference's arithmetic, hipBLASLt fp32) or ``"bf16x3"``
-    (``gemm_x3`` on the bf16 matrix cores: 16 mantissa bits per operand, about
-    1e-5 relative per projection, 2x faster)."""
+    ``"fp32"`` (the reference's arithmetic: ``gemm_f32`` on the fp32 matrix
+    cores) or ``"bf16x3"`` (``gemm_x3`` on the bf16 matrix cores: 16 mantissa
+    bits per operand, about 1e-5 relative per projection, 2.5x faster)."""
     if gemm not in ("fp32", "bf16x3"):
         raise ValueError(f"gemm must be 'fp32' or 'bf16x3', got {gemm!r}")
     hc = hparams.hc_mult

@@ -33,7 +33,7 @@
  *   eg_ple_gate, eg_ple_conv  ple_forward after its two projections
  *   (+ _backward)    and the autograd of it          engraft/replica/layers.py:565-626
  *   eg_ple_rms, eg_ple_conv's other modes  PleReplica engraft/lens.py:221-385
- *   eg_split_bf16, eg_gemm_bf16x3 (+ _workspace_size)
+ *   eg_split_bf16, eg_gemm_bf16x3 (+ _workspace_size), eg_gemm_f32
  *                    ple_forward's projections and their backward
  *                                                    engraft/replica/layers.py:594-606
  */
@@ -439,18 +439,44 @@ typedef struct eg_gemm_operands {
  * accumulated in fp32 (hi + lo keeps 16 mantissa bits: a relative error
  * up to ~3 x 2^-18 per product, about 1e-5 of the result on random data; a
  * non-finite operand gives NaN).  Planes 16-byte aligned, leading dimensions
- * multiples of 8; accumulate = 1 adds to C / C2.  k_slices > 1 cuts the K
- * range into that many slices run by separate workgroups, their partial
- * products summed in slice order afterwards (deterministic), in a workspace
- * of eg_gemm_workspace_size bytes.  The projections of ple_forward, key =
- * emb w_key^T and value = emb w_value^T as the two column groups of one
- * call, and their backward d_emb = d_key w_key + d_value w_value as two
- * segments with the weights' transposes as B (engraft/replica/layers.py:
- * 594-606, where they are torch fp32 matmuls). */
-int64_t eg_gemm_workspace_size(int64_t m, int64_t n, int64_t n2, int32_t k_slices);
+ * multiples of 8; accumulate = 1 adds to C / C2.  k_slices = 0 cuts the
+ * tiles of a partly filled last round of workgroups along K into pieces that
+ * fill it; k_slices >= 1 cuts every 128 x 128 output tile into that many K
+ * pieces (1: none).  Pieces' partial products go to a workspace of
+ * eg_gemm_workspace_size(m, n, n2, k, k_slices) bytes, k the sum of the
+ * segments' k (asked on the device that runs the GEMM: the plan follows its
+ * CU count), and are summed in K order afterwards (deterministic).  The
+ * projections of ple_forward, key = emb w_key^T and value = emb w_value^T as
+ * the two column groups of one call, and their backward d_emb = d_key w_key +
+ * d_value w_value as two segments with the weights' transposes as B
+ * (engraft/replica/layers.py:594-606, where they are torch fp32 matmuls). */
+int64_t eg_gemm_workspace_size(int64_t m, int64_t n, int64_t n2, int64_t k, int32_t k_slices);
 int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,
                    int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate, int32_t k_slices,
                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* One K segment of eg_gemm_f32: A [m, k] and B [n, k] (and B2 [n2, k] for
+ * the second column group, only read when n2 > 0), fp32, row-major. */
+typedef struct eg_gemm_f32_operands {
+  const float* a;
+  int64_t lda;
+  const float* b;
+  int64_t ldb;
+  const float* b2;
+  int64_t ldb2;
+  int64_t k; /* multiple of 32 */
+} eg_gemm_f32_operands;
+
+/* The same GEMM as eg_gemm_bf16x3 (two K segments, two column groups, K
+ * slices in the same workspace) in fp32 arithmetic on the fp32 matrix cores
+ * (v_mfma_f32_32x32x2_f32): every product exact-rounded as an fp32 matmul's,
+ * accumulated in fp32.  Operands 16-byte aligned, leading dimensions
+ * multiples of 4, k a multiple of 32.  ple_forward's projections with
+ * gemm="fp32", the arithmetic of the reference's torch fp32 matmuls
+ * (engraft/replica/layers.py:594-606). */
+int eg_gemm_f32(const eg_gemm_f32_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,
+                int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate, int32_t k_slices, void* workspace,
+                int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }
