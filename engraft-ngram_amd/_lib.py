@@ -146,6 +146,7 @@ SIGNATURES = {
     "eg_ple_rms": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, ctypes.c_float, c_void_p, c_void_p]),
     "eg_split_bf16": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "eg_gemm_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int32]),
+    "eg_gemm_f32_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int32]),
     "eg_gemm_bf16x3": (c_int32, [POINTER(EgGemmOperands), c_int32, c_int64, c_int64, c_int64, c_void_p, c_int64,
                                  c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_void_p]),
     "eg_gemm_f32": (c_int32, [POINTER(EgGemmF32Operands), c_int32, c_int64, c_int64, c_int64, c_void_p, c_int64,

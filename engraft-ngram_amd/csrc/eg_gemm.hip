@@ -18,30 +18,33 @@
 // (v_mfma_f32_32x32x2_f32): the products of an fp32 matmul, each operand
 // read once as fp32.
 //
-// Tiling, both: 128 x 128 output tile per 256-thread workgroup (four
-// wavefronts, 64 x 64 each as 2 x 2 MFMA tiles), K in steps of 32 through a
-// two-stage LDS ring filled by direct-to-LDS loads (global_load_lds_dwordx4:
-// lane i of a wavefront writes 16 bytes at the wavefront's LDS base + 16 i),
-// so the next step's loads are in flight during the current step's MFMAs
-// without passing through registers.  Two stages (64 KB) keep two workgroups
-// on a CU.  For gemm_x3, measured against it after a warm-up, launches
-// interleaved: 128 x 256 and 256 x 128 tiles with eight wavefronts, 256 x 256
-// with sixteen, three stages, and scheduling hints that interleave the LDS
-// reads with the MFMAs ran 3-5 % slower; register-staged loads into a padded
-// LDS tile ran 20 % slower; fragments of the next half step read during the
-// current one's MFMAs, and a swizzle free of LDS bank conflicts (counted by
-// SQ_LDS_BANK_CONFLICT), changed the key projection by under 1 %.
+// Tiling, both: K in steps of 32 through a two-stage LDS ring filled by
+// direct-to-LDS loads (global_load_lds_dwordx4: lane i of a wavefront writes
+// 16 bytes at the wavefront's LDS base + 16 i), so the next step's loads are
+// in flight during the current step's MFMAs without passing through
+// registers; wavefronts of 64 x 64 outputs (2 x 2 MFMA tiles of 32 x 32).
+// gemm_x3: 128 x 128 tiles of four wavefronts, 64 KB of LDS, two workgroups
+// a CU.  Measured against it after a warm-up, launches interleaved: 128 x 256
+// and 256 x 128 tiles with eight wavefronts, 256 x 256 with sixteen, three
+// stages, and scheduling hints that interleave the LDS reads with the MFMAs
+// ran 3-5 % slower; register-staged loads into a padded LDS tile ran 20 %
+// slower; fragments of the next half step read during the current one's
+// MFMAs, and a swizzle free of LDS bank conflicts (counted by
+// SQ_LDS_BANK_CONFLICT), changed the key projection by under 1 %.  gemm_f32:
+// 256 x 256 tiles of sixteen wavefronts, 128 KB of LDS, one workgroup a CU:
+// 88.8 % of the fp32 MFMA peak where the tiles fill whole rounds, against
+// 83.3 % for 128 x 128 tiles of four.
 //
 // The last round.  The grid is a run of whole tiles followed by pieces: when
-// the tile count leaves the last round of workgroups (two a CU) partly empty,
-// the tiles of that round are cut along K into pieces that fill it, the
-// pieces' partial products go to a workspace, and piece_sum_kernel adds each
-// tile's pieces in K order into C, so the result does not depend on
-// scheduling.  On MI355X (512 workgroup slots): the key projection's 1280
-// tiles run as 1024 whole tiles and 256 tiles in halves, the forward's key +
-// value (1600 tiles) as 1536 and 64 in eighths, the backward's 320 tiles of
-// 400 K steps in thirds (1, 2, 3, 4, 6 pieces: 527, 486, 422, 436, 461 us
-// there).  An explicit k_slices cuts every tile the same way.
+// the tile count leaves the last round (one tile a CU) partly empty, the
+// tiles of that round are cut along K into pieces that fill it, the pieces'
+// partial products go to a workspace, and piece_sum_kernel adds each tile's
+// pieces in K order into C, so the result does not depend on scheduling.  On
+// MI355X (256 CUs): the bf16x3 backward's 320 tiles run as 256 whole tiles
+// and 64 in quarters (412 us against 517 us whole and 483 us in thirds), the
+// forward's key + value (1600 tiles) as 1536 and 64 in quarters; the fp32
+// key + value's 400 tiles as 256 whole and 144 in sevenths (1126 us against
+// 1262 us whole).  An explicit k_slices cuts every tile the same way.
 //
 // Workgroups are dispatched round-robin over the 8 XCDs; the whole tiles are
 // remapped so that each XCD takes a contiguous run of tiles, grouped 8 row
@@ -63,19 +66,12 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 constexpr int kBM = 128, kBN = 128, kBK = 32;
-constexpr int kTileElems = kBM * kBN;  // floats of one piece's partial product
 constexpr int kStages = 2;
-constexpr int kSlotsPerCu = 2;         // workgroups a CU holds (64 KB of LDS each)
 
 // bf16x3: a plane tile is 128 rows x 32 bf16 (64 B rows)
 constexpr int kPlane = 128 * kBK;
 constexpr int kStage = 4 * kPlane;  // ah, al, bh, bl
 constexpr size_t kLds = (size_t)kStages * kStage * 2;  // 64 KB
-
-// fp32: A and B tiles of 128 rows x 32 floats (128 B rows)
-constexpr int kF32Tile = 128 * kBK;
-constexpr int kF32Stage = 2 * kF32Tile;
-constexpr size_t kF32Lds = (size_t)kStages * kF32Stage * 4;  // 64 KB
 
 // What both kernels share: output, tiles and the whole-tile / piece split.
 struct Plan {
@@ -86,7 +82,7 @@ struct Plan {
   int pieces;             // pieces per remaining tile; block dp_tiles + q runs piece q
   float* c[2];            // per column group
   int64_t ldc[2];
-  float* ws;              // [tiles - dp_tiles][pieces][128 x 128] partial products
+  float* ws;              // [tiles - dp_tiles][pieces][tile] partial products
   int64_t m, n[2];
   int tiles_m, tiles_n0, tiles_n;
   int accumulate;         // 1: C += result
@@ -177,6 +173,7 @@ struct Work {
   int grp, piece;
 };
 
+template <int BM, int BN>
 __device__ inline Work work_of(const Plan& p) {
   Work w;
   const int b = blockIdx.x;
@@ -199,18 +196,20 @@ __device__ inline Work work_of(const Plan& p) {
   int tm, tn;
   grouped(logical, p.tiles_m, p.tiles_n, tm, tn);
   w.grp = tn < p.tiles_n0 ? 0 : 1;
-  w.m0 = (int64_t)tm * kBM;
-  w.n0 = (int64_t)(w.grp ? tn - p.tiles_n0 : tn) * kBN;
+  w.m0 = (int64_t)tm * BM;
+  w.n0 = (int64_t)(w.grp ? tn - p.tiles_n0 : tn) * BN;
   return w;
 }
 
 // D of a 32 x 32 MFMA tile: lane l holds column l % 32 and rows
-// 8 (r / 4) + 4 (l / 32) + r % 4.  A whole tile goes to C (bounded by m and
-// n, added to when accumulating); a piece to its 128 x 128 workspace slot.
+// 8 (r / 4) + 4 (l / 32) + r % 4; wavefront (wm, wn) holds the 64 x 64 block
+// at (64 wm, 64 wn) of the tile.  A whole tile goes to C (bounded by m and n,
+// added to when accumulating); a piece to its BM x BN workspace slot.
+template <int BM, int BN>
 __device__ inline void store_acc(const Plan& p, const Work& w, const f32x16 (&acc)[2][2], int wm, int wn,
                                  int lane) {
   if (w.piece >= 0) {
-    float* t = p.ws + (int64_t)w.piece * kTileElems;
+    float* t = p.ws + (int64_t)w.piece * (BM * BN);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -218,7 +217,7 @@ __device__ inline void store_acc(const Plan& p, const Work& w, const f32x16 (&ac
         const int lc = wn * 64 + j * 32 + (lane & 31);
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          t[(wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kBN + lc] = acc[i][j][r];
+          t[(wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * BN + lc] = acc[i][j][r];
       }
     return;
   }
@@ -254,7 +253,7 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const GemmArgs args) {
   const Plan& p = args.p;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const Work w = work_of(p);
+  const Work w = work_of<kBM, kBN>(p);
   const int grp = w.grp;
   const int64_t n_grp = p.n[grp];
 
@@ -350,7 +349,7 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const GemmArgs args) {
     }
     __builtin_amdgcn_s_barrier();  // the ring is refilled by the next segment
   }
-  store_acc(p, w, acc, wm, wn, lane);
+  store_acc<kBM, kBN>(p, w, acc, wm, wn, lane);
 }
 
 // One MFMA takes one A and one B value per lane (lane l: row / column l % 32,
@@ -360,13 +359,21 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const GemmArgs args) {
 // 16-byte chunk c of tile row r sits in slot c ^ ((r >> 1) & 7): a fragment
 // read (16 lanes at one chunk of 16 consecutive rows per LDS cycle) then
 // touches 16 distinct 16-byte bank groups.  64 MFMAs of 64 cycles a step
-// against 16 KB of LDS reads: the matrix cores, not the LDS, bound it.
-__global__ __launch_bounds__(256) void gemm_f32_kernel(const F32Args args) {
+// against 16 KB of LDS reads per wavefront: the matrix cores, not the LDS,
+// bound it.  BM x BN tile, (BM / 64) x (BN / 64) wavefronts of 64 x 64; A and
+// B tiles of BM and BN rows x 128 B a stage.
+template <int BM, int BN>
+__global__ __launch_bounds__(BM * BN / 64) void gemm_f32_kernel(const F32Args args) {
+  constexpr int WN = BN / 64, NW = (BM / 64) * WN;
+  constexpr int STAGE = (BM + BN) * kBK;           // floats
+  constexpr int LPW = (BM + BN) / 8 / NW;          // 8-row loads per wavefront per stage
+  constexpr int LA = BM / 8 / NW;                  // of which on A
+  static_assert((BM / 8) % NW == 0 && (BN / 8) % NW == 0, "loads per wavefront");
   extern __shared__ __attribute__((aligned(16))) float ldsf[];
   const Plan& p = args.p;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const Work w = work_of(p);
+  const int wm = wave / WN, wn = wave % WN;
+  const Work w = work_of<BM, BN>(p);
   const int grp = w.grp;
   const int64_t n_grp = p.n[grp];
 
@@ -378,16 +385,16 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const F32Args args) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // this wavefront's 8 loads per stage: load q = wave + 4 j covers tile rows
-  // 8 (q % 16) .. +7 of A (j < 4) or B (j >= 4); lane i fills row 8 (q % 16) +
-  // i / 8, slot i % 8.  Rows past m or n read row m-1 or n-1 (not stored).
+  // this wavefront's loads per stage: load q = wave + NW j covers rows 8 q' ..
+  // 8 q' + 7 of A (j < LA, q' = q) or B (q' = q - BM / 8); lane i fills row
+  // 8 q' + i / 8, slot i % 8.  Rows past m or n read row m-1 or n-1 (not stored).
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
-  int64_t row_of[8];
-  int col_of[8];
+  int64_t row_of[LPW];
+  int col_of[LPW];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int q = uwave + 4 * j, row = 8 * (q & 15) + (lane >> 3);
-    const int64_t gr = (j < 4 ? w.m0 : w.n0) + row, lim = j < 4 ? p.m : n_grp;
+  for (int j = 0; j < LPW; ++j) {
+    const int q = uwave + NW * j, row = 8 * (j < LA ? q : q - BM / 8) + (lane >> 3);
+    const int64_t gr = (j < LA ? w.m0 : w.n0) + row, lim = j < LA ? p.m : n_grp;
     row_of[j] = gr < lim ? gr : lim - 1;
     col_of[j] = swz8(row, lane & 7) * 4;
   }
@@ -397,19 +404,17 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const F32Args args) {
     const int64_t lo = w.kv0 > seg0 ? w.kv0 : seg0, hi = w.kv1 < seg1 ? w.kv1 : seg1;
     if (lo >= hi) continue;
     const F32Seg& sg = args.seg[s];
-    const float* src[8];
+    const float* src[LPW];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      src[j] = (j < 4 ? sg.a : sg.b[grp]) + row_of[j] * (j < 4 ? sg.lda : sg.ldb[grp]) + col_of[j];
+    for (int j = 0; j < LPW; ++j)
+      src[j] = (j < LA ? sg.a : sg.b[grp]) + row_of[j] * (j < LA ? sg.lda : sg.ldb[grp]) + col_of[j];
     auto issue = [&](int64_t kt) {
-      float* st = ldsf + (kt & 1) * kF32Stage;
+      float* st = ldsf + (kt & 1) * STAGE;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int q = uwave + 4 * j;
+      for (int j = 0; j < LPW; ++j) {
+        const int q = uwave + NW * j;
         __builtin_amdgcn_global_load_lds((const void*)(src[j] + kt * kBK),
-                                         (__attribute__((address_space(3))) void*)(st + (j < 4 ? 0 : kF32Tile) +
-                                                                                   8 * (q & 15) * kBK),
-                                         16, 0, 0);
+                                         (__attribute__((address_space(3))) void*)(st + 8 * q * kBK), 16, 0, 0);
       }
     };
     issue(lo - seg0);
@@ -418,7 +423,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const F32Args args) {
       wait_vm0();
       __builtin_amdgcn_s_barrier();
       if (kv + 1 < hi) issue(kt + 1);
-      const float* st = ldsf + (kt & 1) * kF32Stage;
+      const float* st = ldsf + (kt & 1) * STAGE;
       float4 fa[2][4], fb[2][4];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -428,7 +433,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const F32Args args) {
         for (int c = 0; c < 4; ++c) {
           const int chunk = 4 * (lane >> 5) + c;
           fa[i][c] = *(const float4*)(st + ar * kBK + swz8(ar, chunk) * 4);
-          fb[i][c] = *(const float4*)(st + kF32Tile + br * kBK + swz8(br, chunk) * 4);
+          fb[i][c] = *(const float4*)(st + BM * kBK + br * kBK + swz8(br, chunk) * 4);
         }
       }
 #pragma unroll
@@ -446,30 +451,32 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const F32Args args) {
     }
     __builtin_amdgcn_s_barrier();
   }
-  store_acc(p, w, acc, wm, wn, lane);
+  store_acc<BM, BN>(p, w, acc, wm, wn, lane);
 }
 
-// C (+)= the sum of a last-round tile's pieces, in K order: 16 blocks a tile,
-// each thread four consecutive columns of one row.
+// C (+)= the sum of a last-round tile's pieces, in K order: BM BN / 1024
+// blocks a tile, each thread four consecutive columns of one row.
+template <int BM, int BN>
 __global__ __launch_bounds__(256) void piece_sum_kernel(const Plan p) {
-  const int q = blockIdx.x >> 4;
-  const int e = (blockIdx.x & 15) * 256 + threadIdx.x;  // float4 of the 128 x 128 tile
-  const int lr = e >> 5, lc = (e & 31) * 4;
+  constexpr int kBlocks = BM * BN / 1024;
+  const int q = blockIdx.x / kBlocks;
+  const int e = (blockIdx.x % kBlocks) * 256 + threadIdx.x;  // float4 of the BM x BN tile
+  const int lr = e / (BN / 4), lc = (e % (BN / 4)) * 4;
   int tm, tn;
   grouped(p.dp_tiles + q, p.tiles_m, p.tiles_n, tm, tn);
   const int grp = tn < p.tiles_n0 ? 0 : 1;
-  const int64_t row = (int64_t)tm * kBM + lr;
+  const int64_t row = (int64_t)tm * BM + lr;
   if (row >= p.m) return;
-  const float4* ws = (const float4*)(p.ws + (int64_t)q * p.pieces * kTileElems) + e;
+  const float4* ws = (const float4*)(p.ws + (int64_t)q * p.pieces * (BM * BN)) + e;
   float4 v = ws[0];
   for (int s = 1; s < p.pieces; ++s) {
-    const float4 u = ws[(int64_t)s * (kTileElems / 4)];
+    const float4 u = ws[(int64_t)s * (BM * BN / 4)];
     v.x += u.x;
     v.y += u.y;
     v.z += u.z;
     v.w += u.w;
   }
-  const int64_t n_grp = p.n[grp], col0 = (int64_t)(grp ? tn - p.tiles_n0 : tn) * kBN + lc;
+  const int64_t n_grp = p.n[grp], col0 = (int64_t)(grp ? tn - p.tiles_n0 : tn) * BN + lc;
   float* out = p.c[grp] + row * p.ldc[grp];
   const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -488,13 +495,32 @@ struct PiecePlan {
   int64_t kt_per_piece;
 };
 
+// A kernel's tile: BM x BN outputs of `threads` threads and `lds` bytes of
+// LDS.  The plan counts `rounds_per_cu` tiles a CU as one round: gemm_x3's
+// second workgroup on a CU adds little throughput to the first (it is bound
+// by its own LDS and load latency, not the CU's matrix cores), so a round of
+// its 128 x 128 tiles is one a CU, as for gemm_f32's 256 x 256 tiles.
+// `sum_cost` / (K steps) is the time of summing one round of pieces against
+// the time of one round of tiles: 4 bytes read per output and piece at ~5
+// TB/s against 192 (bf16 products, ~1 PFLOP/s reached) or 64 (fp32, ~130
+// TFLOP/s) flops per output and K step.
+struct Shape {
+  int bm, bn, threads, rounds_per_cu;
+  size_t lds;
+  double sum_cost;
+};
+
+constexpr Shape kX3Shape{kBM, kBN, 256, 1, kLds, 4.2};
+constexpr int kF32BM = 256, kF32BN = 256;
+constexpr Shape kF32Shape{kF32BM, kF32BN, kF32BM * kF32BN / 64, 1,
+                          (size_t)kStages * (kF32BM + kF32BN) * kBK * 4, 1.6};
+
 // k_slices >= 1: every tile in k_slices pieces (1: whole tiles).  0: the
-// tiles of a partly filled last round (of `slots` workgroups) in the piece
-// count that minimises the time of that round in tile units, ceil(R s /
-// slots) / s, plus the cost of summing the pieces (R s slots' worth of 64 KB
-// partial products, ~0.08 of a tile of 80 K steps per round of pieces); at
-// least 8 K steps a piece, and only for a gain of 10 % or more.
-PiecePlan plan_pieces(int64_t tiles, int64_t kt_total, int k_slices, int slots) {
+// tiles of a partly filled last round (of `slots` tiles) in the piece count
+// that minimises the time of that round in tile units, ceil(R s / slots) / s,
+// plus the cost of summing the pieces, sum_cost / (K steps) per round of
+// pieces.  At least 8 K steps a piece, and only for a gain of 10 % or more.
+PiecePlan plan_pieces(int64_t tiles, int64_t kt_total, int k_slices, int slots, double sum_cost) {
   PiecePlan pp{(int)tiles, 1, kt_total > 0 ? kt_total : 1};
   int s = 1;
   if (k_slices >= 1) {
@@ -502,9 +528,10 @@ PiecePlan plan_pieces(int64_t tiles, int64_t kt_total, int k_slices, int slots) 
   } else {
     const int64_t r = tiles % slots;
     if (r == 0 || kt_total < 16) return pp;
+    const double per_round = sum_cost / (double)kt_total;
     double best = 1.0;
     for (int c = 2; c <= 8 && kt_total / c >= 8; ++c) {
-      const double t = (double)((r * c + slots - 1) / slots) / c + 6.4 / (double)kt_total * (double)(r * c) / slots;
+      const double t = (double)((r * c + slots - 1) / slots) / c + per_round * (double)(r * c) / slots;
       if (t < best) {
         best = t;
         s = c;
@@ -525,8 +552,8 @@ PiecePlan plan_pieces(int64_t tiles, int64_t kt_total, int k_slices, int slots) 
   return pp;
 }
 
-// Workgroup slots of the current device: kSlotsPerCu per CU.
-int device_slots(int* slots) {
+// CUs of the current device.
+int device_cus(int* cus_out) {
   static std::mutex mu;
   static std::vector<std::pair<int, int>> known;  // (device, CU count)
   int dev = 0;
@@ -534,30 +561,48 @@ int device_slots(int* slots) {
   std::lock_guard<std::mutex> lock(mu);
   for (const auto& k : known)
     if (k.first == dev) {
-      *slots = kSlotsPerCu * k.second;
+      *cus_out = k.second;
       return EG_OK;
     }
   int cus = 0;
   EG_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   EG_CHECK_ARG(cus > 0, "device %d reports %d CUs", dev, cus);
   known.emplace_back(dev, cus);
-  *slots = kSlotsPerCu * cus;
+  *cus_out = cus;
   return EG_OK;
 }
 
-int64_t tiles_of(int64_t m, int64_t n, int64_t n2) {
-  return ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN + (n2 + kBN - 1) / kBN);
+int64_t tiles_of(const Shape& sh, int64_t m, int64_t n, int64_t n2) {
+  return ((m + sh.bm - 1) / sh.bm) * ((n + sh.bn - 1) / sh.bn + (n2 + sh.bn - 1) / sh.bn);
 }
 
-int64_t piece_bytes(int64_t tiles, const PiecePlan& pp) {
-  return pp.pieces > 1 ? (tiles - pp.dp) * pp.pieces * (int64_t)kTileElems * (int64_t)sizeof(float) : 0;
+int64_t piece_bytes(const Shape& sh, int64_t tiles, const PiecePlan& pp) {
+  return pp.pieces > 1 ? (tiles - pp.dp) * pp.pieces * (int64_t)sh.bm * sh.bn * (int64_t)sizeof(float) : 0;
+}
+
+int plan_for(const Shape& sh, int64_t m, int64_t n, int64_t n2, int64_t kt_total, int k_slices, int64_t* tiles,
+             PiecePlan* pp) {
+  int cus = 0;
+  const int rc = device_cus(&cus);
+  if (rc != EG_OK) return rc;
+  *tiles = tiles_of(sh, m, n, n2);
+  *pp = plan_pieces(*tiles, kt_total, k_slices, sh.rounds_per_cu * cus, sh.sum_cost);
+  return EG_OK;
+}
+
+int64_t workspace_size(const Shape& sh, int64_t m, int64_t n, int64_t n2, int64_t k, int32_t k_slices) {
+  if (m <= 0 || n < 0 || n2 < 0 || n + n2 == 0 || k < 0 || k_slices < 0) return 0;
+  int64_t tiles = 0;
+  PiecePlan pp{};
+  if (plan_for(sh, m, n, n2, k / 32, k_slices, &tiles, &pp) != EG_OK) return -1;
+  return piece_bytes(sh, tiles, pp);
 }
 
 // The part of both entry points after their operands are checked: the plan,
 // the LDS attribute, the launch and the pieces' sum.
-template <typename Args>
-int launch_gemm(void (*kernel)(const Args), size_t lds, const char* name, Args& g, int64_t m, int64_t n, int64_t n2,
-                float* c, int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate, int32_t k_slices,
+template <int BM, int BN, typename Args>
+int launch_gemm(const Shape& sh, void (*kernel)(const Args), const char* name, Args& g, int64_t m, int64_t n,
+                int64_t n2, float* c, int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate, int32_t k_slices,
                 void* workspace, int64_t workspace_bytes, void* stream) {
   EG_CHECK_ARG(m >= 0 && n >= 0 && n2 >= 0 && k_slices >= 0, "m=%lld n=%lld n2=%lld k_slices=%d", (long long)m,
                (long long)n, (long long)n2, k_slices);
@@ -567,16 +612,15 @@ int launch_gemm(void (*kernel)(const Args), size_t lds, const char* name, Args& 
   Plan& p = g.p;
   p.kt0 = g.n_seg > 0 ? g.seg[0].ktiles : 0;
   p.kt_total = p.kt0 + (g.n_seg > 1 ? g.seg[1].ktiles : 0);
-  const int64_t tiles = tiles_of(m, n, n2);
-  EG_CHECK_ARG(tiles < (1LL << 24), "too many tiles");
-  int slots = 0;
-  int rc = device_slots(&slots);
+  int64_t tiles = 0;
+  PiecePlan pp{};
+  int rc = plan_for(sh, m, n, n2, p.kt_total, k_slices, &tiles, &pp);
   if (rc != EG_OK) return rc;
-  const PiecePlan pp = plan_pieces(tiles, p.kt_total, k_slices, slots);
-  const int64_t need = piece_bytes(tiles, pp);
+  EG_CHECK_ARG(tiles < (1LL << 24), "too many tiles");
+  const int64_t need = piece_bytes(sh, tiles, pp);
   if (need > 0) {
     EG_CHECK_ARG(workspace != nullptr && ((uintptr_t)workspace & 15) == 0 && workspace_bytes >= need,
-                 "this call needs a 16-byte aligned workspace of %lld bytes (eg_gemm_workspace_size)",
+                 "this call needs a 16-byte aligned workspace of %lld bytes (its _workspace_size function)",
                  (long long)need);
     p.ws = (float*)workspace;
   }
@@ -590,9 +634,9 @@ int launch_gemm(void (*kernel)(const Args), size_t lds, const char* name, Args& 
   p.m = m;
   p.n[0] = n;
   p.n[1] = n2;
-  p.tiles_m = (int)((m + kBM - 1) / kBM);
-  p.tiles_n0 = (int)((n + kBN - 1) / kBN);
-  p.tiles_n = p.tiles_n0 + (int)((n2 + kBN - 1) / kBN);
+  p.tiles_m = (int)((m + BM - 1) / BM);
+  p.tiles_n0 = (int)((n + BN - 1) / BN);
+  p.tiles_n = p.tiles_n0 + (int)((n2 + BN - 1) / BN);
   p.accumulate = accumulate ? 1 : 0;
   const int64_t blocks = pp.dp + (tiles - pp.dp) * pp.pieces;
   EG_CHECK_ARG(blocks < (1LL << 31), "too many workgroups");
@@ -606,14 +650,16 @@ int launch_gemm(void (*kernel)(const Args), size_t lds, const char* name, Args& 
     std::lock_guard<std::mutex> lock(mu);
     const std::pair<const void*, int> key((const void*)kernel, dev);
     if (std::find(done.begin(), done.end(), key) == done.end()) {
-      EG_CHECK_HIP(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+      EG_CHECK_HIP(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)sh.lds));
       done.push_back(key);
     }
   }
-  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(256), lds, st, g);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(sh.threads), sh.lds, st, g);
   rc = launch_status(name);
   if (rc != 0 || pp.dp == tiles) return rc;
-  hipLaunchKernelGGL(piece_sum_kernel, dim3((unsigned)((tiles - pp.dp) * 16)), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((piece_sum_kernel<BM, BN>), dim3((unsigned)((tiles - pp.dp) * (BM * BN / 1024))), dim3(256),
+                     0, st, p);
   return launch_status("piece_sum_kernel");
 }
 
@@ -642,12 +688,11 @@ int eg_split_bf16(const float* x, int64_t rows, int64_t cols, int64_t ld, void* 
 }
 
 int64_t eg_gemm_workspace_size(int64_t m, int64_t n, int64_t n2, int64_t k, int32_t k_slices) {
-  using namespace eg;
-  if (m <= 0 || n < 0 || n2 < 0 || n + n2 == 0 || k < 0 || k_slices < 0) return 0;
-  int slots = 0;
-  if (device_slots(&slots) != EG_OK) return -1;
-  const int64_t tiles = tiles_of(m, n, n2);
-  return piece_bytes(tiles, plan_pieces(tiles, k / 32, k_slices, slots));
+  return eg::workspace_size(eg::kX3Shape, m, n, n2, k, k_slices);
+}
+
+int64_t eg_gemm_f32_workspace_size(int64_t m, int64_t n, int64_t n2, int64_t k, int32_t k_slices) {
+  return eg::workspace_size(eg::kF32Shape, m, n, n2, k, k_slices);
 }
 
 int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,
@@ -682,8 +727,8 @@ int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_
     sg.ktiles = o.k / 32;
     ++g.n_seg;
   }
-  return launch_gemm(gemm_x3_kernel, kLds, "gemm_x3_kernel", g, m, n, n2, c, ldc, c2, ldc2, accumulate, k_slices,
-                     workspace, workspace_bytes, stream);
+  return launch_gemm<kBM, kBN>(kX3Shape, gemm_x3_kernel, "gemm_x3_kernel", g, m, n, n2, c, ldc, c2, ldc2,
+                               accumulate, k_slices, workspace, workspace_bytes, stream);
 }
 
 int eg_gemm_f32(const eg_gemm_f32_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,
@@ -715,8 +760,8 @@ int eg_gemm_f32(const eg_gemm_f32_operands* ops, int32_t n_seg, int64_t m, int64
     sg.ktiles = o.k / 32;
     ++g.n_seg;
   }
-  return launch_gemm(gemm_f32_kernel, kF32Lds, "gemm_f32_kernel", g, m, n, n2, c, ldc, c2, ldc2, accumulate,
-                     k_slices, workspace, workspace_bytes, stream);
+  return launch_gemm<kF32BM, kF32BN>(kF32Shape, gemm_f32_kernel<kF32BM, kF32BN>, "gemm_f32_kernel", g, m, n, n2,
+                                     c, ldc, c2, ldc2, accumulate, k_slices, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

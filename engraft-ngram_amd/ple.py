@@ -164,14 +164,15 @@ def _planes(x, cached: bool) -> SplitPlanes:
     return _PLANES.get(x) if cached else SplitPlanes(x)
 
 
-def _gemm_workspace(m: int, n: int, n2: int, k: int, k_slices: int | None, dev):
+def _gemm_workspace(m: int, n: int, n2: int, k: int, k_slices: int | None, dev, size_fn: str):
     """The K-slice argument for the GEMM entry points (0: the library plans the
-    pieces of a partly filled last round) and the workspace that plan needs."""
+    pieces of a partly filled last round) and the workspace that plan needs
+    (``size_fn``: the entry point's workspace-size function)."""
     slices = 0 if k_slices is None else int(k_slices)
     if slices < 0:
         raise ValueError(f"k_slices must be >= 0, got {slices}")
     with torch.cuda.device(dev):
-        ws_bytes = int(_lib.load().eg_gemm_workspace_size(m, n, n2, k, slices))
+        ws_bytes = int(getattr(_lib.load(), size_fn)(m, n, n2, k, slices))
     if ws_bytes < 0:
         raise RuntimeError("eg_gemm_workspace_size: device query failed")
     ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=dev) if ws_bytes else None
@@ -226,7 +227,7 @@ def gemm_x3(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate:
 
     out = _out(out, m, n, "out")
     out2 = _out(out2, m, n2, "out2") if n2 else None
-    slices, ws, ws_bytes = _gemm_workspace(m, n, n2, 32 * k_tiles, k_slices, dev)
+    slices, ws, ws_bytes = _gemm_workspace(m, n, n2, 32 * k_tiles, k_slices, dev, "eg_gemm_workspace_size")
     _lib.call("eg_gemm_bf16x3", ops, len(segs), m, n, n2, _lib.ptr(out), max(out.stride(0), n),
               _lib.ptr(out2), max(out2.stride(0), n2) if n2 else 0, int(accumulate), slices, _lib.ptr(ws),
               ws_bytes, _lib.stream_ptr(dev))
@@ -292,7 +293,7 @@ def gemm_f32(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate
 
     out = _out(out, m, n, "out")
     out2 = _out(out2, m, n2, "out2") if n2 else None
-    slices, ws, ws_bytes = _gemm_workspace(m, n, n2, 32 * k_tiles, k_slices, dev)
+    slices, ws, ws_bytes = _gemm_workspace(m, n, n2, 32 * k_tiles, k_slices, dev, "eg_gemm_f32_workspace_size")
     _lib.call("eg_gemm_f32", ops, len(raw), m, n, n2, _lib.ptr(out), max(out.stride(0), n),
               _lib.ptr(out2), max(out2.stride(0), n2) if n2 else 0, int(accumulate), slices, _lib.ptr(ws),
               ws_bytes, _lib.stream_ptr(dev))

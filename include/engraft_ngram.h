@@ -33,7 +33,7 @@
  *   eg_ple_gate, eg_ple_conv  ple_forward after its two projections
  *   (+ _backward)    and the autograd of it          engraft/replica/layers.py:565-626
  *   eg_ple_rms, eg_ple_conv's other modes  PleReplica engraft/lens.py:221-385
- *   eg_split_bf16, eg_gemm_bf16x3 (+ _workspace_size), eg_gemm_f32
+ *   eg_split_bf16, eg_gemm_bf16x3, eg_gemm_f32 (+ _workspace_size)
  *                    ple_forward's projections and their backward
  *                                                    engraft/replica/layers.py:594-606
  */
@@ -471,9 +471,12 @@ typedef struct eg_gemm_f32_operands {
  * slices in the same workspace) in fp32 arithmetic on the fp32 matrix cores
  * (v_mfma_f32_32x32x2_f32): every product exact-rounded as an fp32 matmul's,
  * accumulated in fp32.  Operands 16-byte aligned, leading dimensions
- * multiples of 4, k a multiple of 32.  ple_forward's projections with
+ * multiples of 4, k a multiple of 32.  Its tiles are 256 x 256 (one
+ * workgroup a CU), so its pieces and workspace follow
+ * eg_gemm_f32_workspace_size.  ple_forward's projections with
  * gemm="fp32", the arithmetic of the reference's torch fp32 matmuls
  * (engraft/replica/layers.py:594-606). */
+int64_t eg_gemm_f32_workspace_size(int64_t m, int64_t n, int64_t n2, int64_t k, int32_t k_slices);
 int eg_gemm_f32(const eg_gemm_f32_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,
                 int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate, int32_t k_slices, void* workspace,
                 int64_t workspace_bytes, void* stream);
