@@ -181,7 +181,9 @@ constexpr int kWavesPerBlock = 4;
 // columns [q*NCH*512, (q+1)*NCH*512) of the position's W, NCH 8-value chunks
 // per lane, and hashes the heads those columns touch (a head whose row spans
 // two parts is hashed by both).  OVL: overlay lookups compiled in.
-template <int FMT, int DIM, int NCH, int MAXL, bool F32OUT, bool OVL, int PARTS>
+// ROWS: the caller's row ids in place of the hash (a separate instantiation, so
+// that a profile tells the two forms apart).
+template <int FMT, int DIM, int NCH, int MAXL, bool F32OUT, bool OVL, int PARTS, bool ROWS>
 __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   const int lane = threadIdx.x & 63;
   const uint32_t wid = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);  // n_pos * parts < 2^32
@@ -213,7 +215,7 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   int64_t tp = p;  // index of position p's own token
   int32_t rid[EG_MAX_LAYERS] = {0, 0};
   static_assert(MAXL >= 1 && MAXL <= EG_MAX_LAYERS, "layer count");
-  const bool hashing = a.rows_in == nullptr;  // uniform
+  const bool hashing = !ROWS;
   if (hashing) {
     tp = a.decode_ctx > 0 ? p * a.decode_ctx + (a.decode_ctx - 1) : p;
     seg0 = a.decode_ctx > 0 ? p * a.decode_ctx : seg_start_of(p, a.seq_len, a.seg_start);
@@ -385,12 +387,12 @@ static thread_local hipEvent_t g_ev_stop = nullptr;
 
 // One launch: parts = ceil(W / (NCH * 512)) wavefronts per position (PARTS:
 // the same number when the caller's shape fixes it, 0 otherwise).
-template <int FMT, int DIM, int NCH, int MAXL, bool F32OUT, bool OVL, int PARTS = 0>
+template <int FMT, int DIM, int NCH, int MAXL, bool F32OUT, bool OVL, int PARTS, bool ROWS>
 static void launch_nch(FwdArgs a, hipStream_t st) {
   a.parts = (a.heads * a.dim + NCH * 512 - 1) / (NCH * 512);
   const int64_t waves = a.n_pos * a.parts;
   const dim3 grid((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock));
-  EG_LAUNCH(FMT, DIM, NCH, MAXL, F32OUT, OVL, PARTS);
+  EG_LAUNCH(FMT, DIM, NCH, MAXL, F32OUT, OVL, PARTS, ROWS);
 }
 
 // Specialised residual-add shapes (dim 128): one layer without overlay takes
@@ -399,21 +401,21 @@ static void launch_nch(FwdArgs a, hipStream_t st) {
 // 512-column parts both measured slower) and W = 3072 in two halves; two layers
 // take 1536-column parts at W = 3072, 1024-column parts otherwise, overlay
 // lookups 1024-column parts.  Everything else goes through the generic kernel.
-template <int FMT>
+template <int FMT, bool ROWS>
 static bool launch_special(const FwdArgs& a, bool ovl, hipStream_t st) {
   if (a.dim != 128) return false;
   const int W = a.heads * a.dim;
   if (W != 2048 && W != 3072) return false;
   if (a.n_layers == 1 && !ovl) {
-    if (W == 2048) launch_nch<FMT, 128, 2, 1, false, false, 2>(a, st);
-    else launch_nch<FMT, 128, 3, 1, false, false, 2>(a, st);
+    if (W == 2048) launch_nch<FMT, 128, 2, 1, false, false, 2, ROWS>(a, st);
+    else launch_nch<FMT, 128, 3, 1, false, false, 2, ROWS>(a, st);
   } else if (a.n_layers == 1) {
-    launch_nch<FMT, 128, 2, 1, false, true>(a, st);
+    launch_nch<FMT, 128, 2, 1, false, true, 0, ROWS>(a, st);
   } else if (!ovl) {
-    if (W == 3072) launch_nch<FMT, 128, 3, 2, false, false, 2>(a, st);
-    else launch_nch<FMT, 128, 2, 2, false, false>(a, st);
+    if (W == 3072) launch_nch<FMT, 128, 3, 2, false, false, 2, ROWS>(a, st);
+    else launch_nch<FMT, 128, 2, 2, false, false, 0, ROWS>(a, st);
   } else {
-    launch_nch<FMT, 128, 2, 2, false, true>(a, st);
+    launch_nch<FMT, 128, 2, 2, false, true, 0, ROWS>(a, st);
   }
   return true;
 }
@@ -421,43 +423,48 @@ static bool launch_special(const FwdArgs& a, bool ovl, hipStream_t st) {
 // The reference's real table shape (16 heads of 160 values, W = 2560, one
 // layer, no overlay): five 512-column chunks per position.
 constexpr int kRealNch = 5;
-template <int FMT>
+template <int FMT, bool ROWS>
 static bool launch_real(const FwdArgs& a, bool ovl, hipStream_t st) {
   if (a.dim != 160 || a.heads * a.dim != 2560 || a.n_layers != 1 || ovl) return false;
-  launch_nch<FMT, 160, kRealNch, 1, false, false, 5 / kRealNch>(a, st);
+  launch_nch<FMT, 160, kRealNch, 1, false, false, 5 / kRealNch, ROWS>(a, st);
   return true;
 }
 
 // Any shape: runtime dim, 1024-column parts, overlays compiled in.
-template <int FMT, bool F32OUT>
+template <int FMT, bool F32OUT, bool ROWS>
 static void launch_generic(const FwdArgs& a, hipStream_t st) {
-  if (a.n_layers == 1) launch_nch<FMT, 0, 2, 1, F32OUT, true>(a, st);
-  else launch_nch<FMT, 0, 2, 2, F32OUT, true>(a, st);
+  if (a.n_layers == 1) launch_nch<FMT, 0, 2, 1, F32OUT, true, 0, ROWS>(a, st);
+  else launch_nch<FMT, 0, 2, 2, F32OUT, true, 0, ROWS>(a, st);
 }
 
-template <bool F32OUT>
-static int launch_forward(const FwdArgs& a, hipStream_t st) {
+template <bool F32OUT, bool ROWS>
+static int launch_forward_as(const FwdArgs& a, hipStream_t st) {
   if (a.n_pos == 0) return EG_OK;
   bool ovl = a.slot_var != nullptr;
   for (int l = 0; l < a.n_layers; ++l) ovl = ovl || a.ov[l].n > 0;
   const int fmt = a.table[0].fmt;
   if (!F32OUT) {
     bool done = false;
-    if (fmt == EG_FMT_Q8_0) done = launch_special<EG_FMT_Q8_0>(a, ovl, st);
-    else if (fmt == EG_FMT_BF16) done = launch_special<EG_FMT_BF16>(a, ovl, st);
-    else if (fmt == EG_FMT_MXFP8) done = launch_special<EG_FMT_MXFP8>(a, ovl, st);
-    else if (fmt == EG_FMT_IQ4_NL) done = launch_real<EG_FMT_IQ4_NL>(a, ovl, st);
+    if (fmt == EG_FMT_Q8_0) done = launch_special<EG_FMT_Q8_0, ROWS>(a, ovl, st);
+    else if (fmt == EG_FMT_BF16) done = launch_special<EG_FMT_BF16, ROWS>(a, ovl, st);
+    else if (fmt == EG_FMT_MXFP8) done = launch_special<EG_FMT_MXFP8, ROWS>(a, ovl, st);
+    else if (fmt == EG_FMT_IQ4_NL) done = launch_real<EG_FMT_IQ4_NL, ROWS>(a, ovl, st);
     if (done) return launch_status("forward_kernel");
   }
   switch (fmt) {
-    case EG_FMT_Q8_0: launch_generic<EG_FMT_Q8_0, F32OUT>(a, st); break;
-    case EG_FMT_BF16: launch_generic<EG_FMT_BF16, F32OUT>(a, st); break;
-    case EG_FMT_MXFP8: launch_generic<EG_FMT_MXFP8, F32OUT>(a, st); break;
-    case EG_FMT_IQ4_NL: launch_generic<EG_FMT_IQ4_NL, F32OUT>(a, st); break;
-    case EG_FMT_F32: launch_generic<EG_FMT_F32, F32OUT>(a, st); break;
+    case EG_FMT_Q8_0: launch_generic<EG_FMT_Q8_0, F32OUT, ROWS>(a, st); break;
+    case EG_FMT_BF16: launch_generic<EG_FMT_BF16, F32OUT, ROWS>(a, st); break;
+    case EG_FMT_MXFP8: launch_generic<EG_FMT_MXFP8, F32OUT, ROWS>(a, st); break;
+    case EG_FMT_IQ4_NL: launch_generic<EG_FMT_IQ4_NL, F32OUT, ROWS>(a, st); break;
+    case EG_FMT_F32: launch_generic<EG_FMT_F32, F32OUT, ROWS>(a, st); break;
     default: return set_error(EG_ERR_UNSUPPORTED, "row format %d", fmt);
   }
   return launch_status("forward_kernel");
+}
+
+template <bool F32OUT>
+static int launch_forward(const FwdArgs& a, hipStream_t st) {
+  return a.rows_in != nullptr ? launch_forward_as<F32OUT, true>(a, st) : launch_forward_as<F32OUT, false>(a, st);
 }
 
 #undef EG_LAUNCH
