@@ -291,6 +291,18 @@ def ple_true_emb_range(table, tokens, start: int, end: int, overlay=None, seg_st
     return table.gather(rows[start:end].contiguous(), overlay=_as_overlay(table, overlay))
 
 
+class ReplicaTableMixin:
+    """``Replica.ple_true_emb`` as a method (``engraft/replica/model.py:473-495``):
+    a model class that keeps its table in ``self.table``, as the reference's
+    ``Replica`` does, inherits it and reads its PLE rows from the device
+    table (the rows come back on the table's device, not the CPU)."""
+
+    table = None
+
+    def ple_true_emb(self, tokens: list[int], t: int, overlay=None) -> torch.Tensor:
+        return ple_true_emb(self.table, tokens, t, overlay)
+
+
 # ---------------------------------------------------------------------------------------------
 # The sequence seam: the model reads its PLE rows through replica.ple_true_emb
 # (engraft/replica/model.py:845-853); a sequence forward shadows that method with

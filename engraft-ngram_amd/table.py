@@ -318,52 +318,54 @@ class DeviceTable:
                    head_offsets=head_offsets, head_multipliers=head_multipliers)
 
 
-def PleTable(path, device=None, chunk_bytes: int = 1 << 28) -> DeviceTable:
+class PleTable(DeviceTable):
     """The per-head IQ4_NL table of a Qwen4Exp GGUF file, loaded into HBM
     (``engraft/table.py:40-88``): hash parameters from the
     ``qwen4exp.ple.*`` metadata, head h's rows from tensor
     ``ple_ngram_embd.{h}.weight`` (IQ4_NL, shape ``[160, p_h]``) placed at
     global rows ``head_offsets[h] .. + p_h``.  The file is streamed in
-    ``chunk_bytes`` stripes; same ``AssertionError``s as the reference."""
-    from pathlib import Path
+    ``chunk_bytes`` stripes; same ``AssertionError``s as the reference.  A
+    ``DeviceTable`` with the file's ``path``."""
 
-    from .ggufio import GGML_TYPE_IQ4_NL, read_gguf
+    def __init__(self, path, device=None, chunk_bytes: int = 1 << 28):
+        from pathlib import Path
 
-    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
-    g = read_gguf(path)
-    f = g.fields
-    eos = int(f["qwen4exp.ple.eos_token_id"])
-    image = int(f["qwen4exp.ple.image_token_id"])
-    ngram = int(f["qwen4exp.ple.ngram_size"])
-    hpn = int(f["qwen4exp.ple.heads_per_ngram"])
-    mults = [int(m) for m in f["qwen4exp.ple.layer_multipliers"]]
-    vocab = [int(v) for v in f["qwen4exp.ple.head_vocab_sizes"]]
-    offsets = [int(o) for o in f["qwen4exp.ple.head_offsets"]]
-    n_rows = max(o + v for o, v in zip(offsets, vocab))
-    store = RowStore.empty("iq4_nl", n_rows, ROW_LEN, dev)
-    flat = store.payload.view(-1)
-    with open(Path(path), "rb") as fh:
-        for h, (o, v) in enumerate(zip(offsets, vocab)):
-            name = f"ple_ngram_embd.{h}.weight"
-            t = g.tensors[name]
-            assert t.ggml_type == GGML_TYPE_IQ4_NL, f"{name}: expected IQ4_NL, got {t.ggml_type}"
-            assert int(t.shape[0]) == ROW_LEN, f"{name}: shape[0]={t.shape[0]} != {ROW_LEN}"
-            assert int(t.shape[1]) == v, f"{name}: shape[1]={t.shape[1]} != head_vocab_sizes[{h}]={v}"
-            total = v * ROW_BYTES
-            fh.seek(t.data_offset)
-            done = 0
-            while done < total:
-                n = min(chunk_bytes, total - done)
-                buf = np.frombuffer(fh.read(n), dtype=np.uint8)
-                if buf.size != n:
-                    raise ValueError(f"{path}: {name} is truncated")
-                dst0 = o * ROW_BYTES + done
-                flat[dst0:dst0 + n].copy_(torch.from_numpy(buf.copy()))
-                done += n
-    tab = DeviceTable(store, eos_token_id=eos, ngram_size=ngram, heads_per_ngram=hpn, layer_multipliers=mults,
-                      head_vocab_sizes=vocab, head_offsets=offsets, image_token_id=image)
-    tab.path = Path(path)
-    return tab
+        from .ggufio import GGML_TYPE_IQ4_NL, read_gguf
+
+        dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        g = read_gguf(path)
+        f = g.fields
+        eos = int(f["qwen4exp.ple.eos_token_id"])
+        image = int(f["qwen4exp.ple.image_token_id"])
+        ngram = int(f["qwen4exp.ple.ngram_size"])
+        hpn = int(f["qwen4exp.ple.heads_per_ngram"])
+        mults = [int(m) for m in f["qwen4exp.ple.layer_multipliers"]]
+        vocab = [int(v) for v in f["qwen4exp.ple.head_vocab_sizes"]]
+        offsets = [int(o) for o in f["qwen4exp.ple.head_offsets"]]
+        n_rows = max(o + v for o, v in zip(offsets, vocab))
+        store = RowStore.empty("iq4_nl", n_rows, ROW_LEN, dev)
+        flat = store.payload.view(-1)
+        with open(Path(path), "rb") as fh:
+            for h, (o, v) in enumerate(zip(offsets, vocab)):
+                name = f"ple_ngram_embd.{h}.weight"
+                t = g.tensors[name]
+                assert t.ggml_type == GGML_TYPE_IQ4_NL, f"{name}: expected IQ4_NL, got {t.ggml_type}"
+                assert int(t.shape[0]) == ROW_LEN, f"{name}: shape[0]={t.shape[0]} != {ROW_LEN}"
+                assert int(t.shape[1]) == v, f"{name}: shape[1]={t.shape[1]} != head_vocab_sizes[{h}]={v}"
+                total = v * ROW_BYTES
+                fh.seek(t.data_offset)
+                done = 0
+                while done < total:
+                    n = min(chunk_bytes, total - done)
+                    buf = np.frombuffer(fh.read(n), dtype=np.uint8)
+                    if buf.size != n:
+                        raise ValueError(f"{path}: {name} is truncated")
+                    dst0 = o * ROW_BYTES + done
+                    flat[dst0:dst0 + n].copy_(torch.from_numpy(buf.copy()))
+                    done += n
+        super().__init__(store, eos_token_id=eos, ngram_size=ngram, heads_per_ngram=hpn, layer_multipliers=mults,
+                         head_vocab_sizes=vocab, head_offsets=offsets, image_token_id=image)
+        self.path = Path(path)
 
 
 def quantile_table(sigma: float) -> np.ndarray:

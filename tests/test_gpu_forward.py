@@ -373,8 +373,10 @@ def test_decode_config3_full_size(cuda):
 def test_forward_config4_full_size(cuda):
     """BASELINE config 4 at its own size: 2 layers x 160,000,000 MXFP8 rows
     (42.2 GB), 2-/3-/4-gram hashes (24 slots per layer), 32,768 Zipf tokens over
-    129,280, residual width 3,072.  Every row id is compared; the output on 4,096
-    sampled positions (the oracle regenerates those rows)."""
+    129,280, residual width 3,072.  Every row id is compared.  The rows the
+    device gathers (eg_gather) equal the oracle's regenerated rows on 4,096
+    sampled positions, and the whole output equals the oracle's fp32 residual
+    add of the device-gathered rows at every position."""
     from engraft_ngram_amd import table as T
     _say("forward cfg4 (2 x 21 GB MXFP8 tables)")
     c = CFG4
@@ -385,14 +387,18 @@ def test_forward_config4_full_size(cuda):
     out, rows = T.forward(tabs, torch.from_numpy(tokens), res, return_rows=True)
     sample = np.sort(np.random.default_rng(422).choice(c["seq"], size=4096, replace=False))
     sample[:2] = [0, 1]  # the EOS-padded first positions
-    embs = []
+    embs, embs_all = [], []
     for l in range(2):
         r = H.ngram_rows_np(specs[l], tokens)
         assert np.array_equal(rows[l].cpu().numpy(), r)
         embs.append(FW.gather(r[sample], G.synth_fetch("mxfp8", 410 + l, 128)))
-    got = G.bf16_bits(out)[sample]
-    G.assert_out_matches(got, FW.residual_add(G.bf16_bits(res)[sample], embs))
-    del tabs, out, rows, res
+        dev_rows = tabs[l].gather(rows[l]).cpu().numpy()  # every position, through eg_gather
+        assert np.array_equal(dev_rows[sample], embs[l])
+        embs_all.append(dev_rows)
+    got = G.bf16_bits(out)
+    G.assert_out_matches(got[sample], FW.residual_add(G.bf16_bits(res)[sample], embs))
+    G.assert_out_matches(got, FW.residual_add(G.bf16_bits(res), embs_all))
+    del tabs, out, rows, res, embs_all
     torch.cuda.empty_cache()
 
 
@@ -416,6 +422,7 @@ def test_ple_table_from_gguf(cuda, tmp_path):
     raw[4][17, [0, 1, 18, 19, 36, 37, 54, 55, 72, 73]] = 0  # row 17 of head 4: zero scales
     ple_table_file(tmp_path / "ple.gguf", spec, raw)
     tab = T.PleTable(tmp_path / "ple.gguf")
+    assert isinstance(tab, T.PleTable) and isinstance(tab, T.DeviceTable) and tab.path == tmp_path / "ple.gguf"
     assert tab.head_offsets == list(spec.head_offsets) and tab.layer_multipliers == list(spec.layer_multipliers)
     assert tab.image_token_id == 151_655
     for h in (0, 4, 15):

@@ -133,6 +133,15 @@ def test_ple_true_emb_and_rowset(cuda):
     rng_all = seq.ple_true_emb_range(tab, tokens, 0, len(tokens), overlay=ov).cpu().numpy()
     for t in range(len(tokens)):
         assert np.array_equal(rng_all[t:t + 1], OE.ple_true_emb(spec, tokens, t, fetch, ov))
+    # the same as a method of a model class that keeps its table in self.table
+
+    class Model(seq.ReplicaTableMixin):
+        def __init__(self, table):
+            self.table = table
+
+    m = Model(tab)
+    for t in (0, 3, len(tokens) - 1):
+        assert torch.equal(m.ple_true_emb(tokens, t, overlay=ov), seq.ple_true_emb(tab, tokens, t, overlay=ov))
 
 
 def test_pleo_overlay_substitutes_real_rows(cuda):
