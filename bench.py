@@ -412,9 +412,40 @@ def bench_decode(tab, steps: int) -> dict:
         torch.cuda.synchronize()
         return sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
 
+    def per_step_in_graphs(overlay, k: int = 16) -> list:
+        """A decode loop of k steps (k token sets in turn) captured as one HIP
+        graph; per-step time of each replay (replay time / k)."""
+        calls = [T.PreparedForward([tab], tk, res, out=out, overlays=[overlay], decode_ctx=ctx) for tk in toks]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for c in calls:
+                c()
+        torch.cuda.current_stream().wait_stream(side)
+        gs = []
+        for j in range(0, len(calls), k):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for c in calls[j:j + k]:
+                    c()
+            gs.append(g)
+        for i in range(20):
+            gs[i % len(gs)].replay()
+        rot = itertools.count()
+        ramp(lambda: gs[next(rot) % len(gs)].replay(), 0.2, 5)
+        n_rep = max(20, steps // k)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_rep)]
+        for i, (a, b) in enumerate(evs):
+            a.record()
+            gs[i % len(gs)].replay()
+            b.record()
+        torch.cuda.synchronize()
+        return sorted(a.elapsed_time(b) * 1e3 / k for a, b in evs)
+
     lat_search = latencies(ov)
     lat = latencies(ov_bm)
     lat_graph = latencies(ov_bm, graphs=True)
+    lat_graph16 = per_step_in_graphs(ov_bm)
     pct = lambda v, q: v[min(len(v) - 1, int(len(v) * q))]
     nbytes = n_seq * (SLOTS * Q8_ROW_BYTES + 2 * 2 * WIDTH + ctx * 8)
     return {"workload": "BASELINE config 3: 256 sequences x (2 context + 1 new token), config-1 table + "
@@ -423,6 +454,8 @@ def bench_decode(tab, steps: int) -> dict:
             "us_p50_binary_search": pct(lat_search, 0.5), "us_p99_binary_search": pct(lat_search, 0.99),
             "us_p50_graph_replay": pct(lat_graph, 0.5), "us_p99_graph_replay": pct(lat_graph, 0.99),
             "us_min_graph_replay": lat_graph[0],
+            "us_per_step_p50_graph_of_16_steps": pct(lat_graph16, 0.5),
+            "us_per_step_p99_graph_of_16_steps": pct(lat_graph16, 0.99),
             "lookups_per_call": n_seq * SLOTS, "algorithmic_bytes_per_call": nbytes}
 
 
@@ -976,7 +1009,8 @@ def main() -> None:
         result["decode_config3"] = dc
         log(f"decode (config 3): p50 {dc['us_p50']:.1f} us, p99 {dc['us_p99']:.1f} us per call (binary search in "
             f"place of the bitmap: p50 {dc['us_p50_binary_search']:.1f} us); as a HIP-graph replay: p50 "
-            f"{dc['us_p50_graph_replay']:.1f} us, p99 {dc['us_p99_graph_replay']:.1f} us")
+            f"{dc['us_p50_graph_replay']:.1f} us, p99 {dc['us_p99_graph_replay']:.1f} us; 16 steps captured as one "
+            f"graph: p50 {dc['us_per_step_p50_graph_of_16_steps']:.1f} us per step")
         c4 = bench_config4(max(50, args.steps // 4), max(20, args.warmup // 4))
         result["forward_config4"] = c4
         log(f"forward (config 4): {c4['us_per_launch']:.1f} us/launch, {c4['gb_per_s']:.0f} GB/s algorithmic "
