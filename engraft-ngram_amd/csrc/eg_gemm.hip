@@ -42,9 +42,15 @@
 // pieces in K order into C, so the result does not depend on scheduling.  On
 // MI355X (256 CUs): the bf16x3 backward's 320 tiles run as 256 whole tiles
 // and 64 in quarters (412 us against 517 us whole and 483 us in thirds), the
-// forward's key + value (1600 tiles) as 1536 and 64 in quarters; the fp32
-// key + value's 400 tiles as 256 whole and 144 in sevenths (1126 us against
-// 1262 us whole).  An explicit k_slices cuts every tile the same way.
+// forward's key + value (1600 tiles) as 1536 and 64 in quarters.  gemm_f32
+// takes its last round as contiguous ranges instead: the (tile, K step)
+// units of that round's tiles cut into one equal range a CU, each range's
+// parts (one or two tiles) summed per tile in K order by sk_sum_kernel.  The
+// fp32 key + value's 400 tiles run as 256 whole and 144 in 256 ranges of 45
+// of a tile's 80 K steps (1040 us against 1249 us whole and 1126 us with the
+// 144 in sevenths), the backward's 80 tiles of 400 K steps in 256 ranges of
+// 125 (1018 us against 1091 us in thirds).  An explicit k_slices cuts every
+// tile into that many equal pieces.
 //
 // Workgroups are dispatched round-robin over the 8 XCDs; the whole tiles are
 // remapped so that each XCD takes a contiguous run of tiles, grouped 8 row
@@ -80,9 +86,11 @@ struct Plan {
   int64_t kt_per_piece;
   int dp_tiles;           // blocks [0, dp_tiles) run whole tiles (logical tiles 0 .. dp_tiles-1)
   int pieces;             // pieces per remaining tile; block dp_tiles + q runs piece q
+  int sk_groups;          // > 0: the remaining tiles' K steps in sk_groups contiguous ranges instead
+  int64_t sk_units;       //      (tiles - dp_tiles) x kt_total (tile, K step) units split among them
   float* c[2];            // per column group
   int64_t ldc[2];
-  float* ws;              // [tiles - dp_tiles][pieces][tile] partial products
+  float* ws;              // [tiles - dp_tiles][pieces][tile] partial products, or [2 sk_groups][tile]
   int64_t m, n[2];
   int tiles_m, tiles_n0, tiles_n;
   int accumulate;         // 1: C += result
@@ -173,16 +181,21 @@ struct Work {
   int grp, piece;
 };
 
+// Block b of nb whole-tile blocks -> logical tile: block b runs on XCD b % 8,
+// and each XCD takes a contiguous run of tiles.
+__device__ inline int xcd_order(int b, int nb) {
+  const int x = b % kXcds, i = b / kXcds;
+  const int per = nb / kXcds, extra = nb % kXcds;
+  return x * per + (x < extra ? x : extra) + i;
+}
+
 template <int BM, int BN>
 __device__ inline Work work_of(const Plan& p) {
   Work w;
   const int b = blockIdx.x;
   int logical;
   if (b < p.dp_tiles) {
-    // XCD-contiguous runs: block b runs on XCD b % 8
-    const int x = b % kXcds, i = b / kXcds;
-    const int per = p.dp_tiles / kXcds, extra = p.dp_tiles % kXcds;
-    logical = x * per + (x < extra ? x : extra) + i;
+    logical = xcd_order(b, p.dp_tiles);
     w.piece = -1;
     w.kv0 = 0;
     w.kv1 = p.kt_total;
@@ -201,6 +214,24 @@ __device__ inline Work work_of(const Plan& p) {
   return w;
 }
 
+// The work of one tile (logical index) over K steps [kv0, kv1).
+template <int BM, int BN>
+__device__ inline Work tile_work(const Plan& p, int logical, int64_t kv0, int64_t kv1, int piece) {
+  Work w;
+  int tm, tn;
+  grouped(logical, p.tiles_m, p.tiles_n, tm, tn);
+  w.grp = tn < p.tiles_n0 ? 0 : 1;
+  w.m0 = (int64_t)tm * BM;
+  w.n0 = (int64_t)(w.grp ? tn - p.tiles_n0 : tn) * BN;
+  w.kv0 = kv0;
+  w.kv1 = kv1;
+  w.piece = piece;
+  return w;
+}
+
+// Range s of the last round's (tile, K step) units: [U s / G, U (s + 1) / G).
+__device__ inline int64_t sk_start(const Plan& p, int64_t s) { return p.sk_units * s / p.sk_groups; }
+
 // D of a 32 x 32 MFMA tile: lane l holds column l % 32 and rows
 // 8 (r / 4) + 4 (l / 32) + r % 4; wavefront (wm, wn) holds the 64 x 64 block
 // at (64 wm, 64 wn) of the tile.  A whole tile goes to C (bounded by m and n,
@@ -208,6 +239,10 @@ __device__ inline Work work_of(const Plan& p) {
 template <int BM, int BN>
 __device__ inline void store_acc(const Plan& p, const Work& w, const f32x16 (&acc)[2][2], int wm, int wn,
                                  int lane) {
+  // the store addresses depend on the lane only; an opaque copy of it keeps the
+  // compiler from computing them once ahead of a loop over tiles and holding
+  // them (in scratch) across the K loops
+  asm volatile("" : "+v"(lane));
   if (w.piece >= 0) {
     float* t = p.ws + (int64_t)w.piece * (BM * BN);
 #pragma unroll
@@ -362,18 +397,17 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const GemmArgs args) {
 // against 16 KB of LDS reads per wavefront: the matrix cores, not the LDS,
 // bound it.  BM x BN tile, (BM / 64) x (BN / 64) wavefronts of 64 x 64; A and
 // B tiles of BM and BN rows x 128 B a stage.
+// One tile's (or piece's) K steps [w.kv0, w.kv1) and its store.
 template <int BM, int BN>
-__global__ __launch_bounds__(BM * BN / 64) void gemm_f32_kernel(const F32Args args) {
+__device__ inline void f32_tile(const F32Args& args, const Work& w, float* ldsf) {
   constexpr int WN = BN / 64, NW = (BM / 64) * WN;
   constexpr int STAGE = (BM + BN) * kBK;           // floats
   constexpr int LPW = (BM + BN) / 8 / NW;          // 8-row loads per wavefront per stage
   constexpr int LA = BM / 8 / NW;                  // of which on A
   static_assert((BM / 8) % NW == 0 && (BN / 8) % NW == 0, "loads per wavefront");
-  extern __shared__ __attribute__((aligned(16))) float ldsf[];
   const Plan& p = args.p;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const Work w = work_of<BM, BN>(p);
   const int grp = w.grp;
   const int64_t n_grp = p.n[grp];
 
@@ -424,34 +458,98 @@ __global__ __launch_bounds__(BM * BN / 64) void gemm_f32_kernel(const F32Args ar
       __builtin_amdgcn_s_barrier();
       if (kv + 1 < hi) issue(kt + 1);
       const float* st = ldsf + (kt & 1) * STAGE;
-      float4 fa[2][4], fb[2][4];
+      // two halves of the step's 16 k a lane half owns: 8 k (two chunks) of
+      // each fragment in registers at a time
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int ar = wm * 64 + i * 32 + (lane & 31);
-        const int br = wn * 64 + i * 32 + (lane & 31);
+      for (int half = 0; half < 2; ++half) {
+        float4 fa[2][2], fb[2][2];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int chunk = 4 * (lane >> 5) + c;
-          fa[i][c] = *(const float4*)(st + ar * kBK + swz8(ar, chunk) * 4);
-          fb[i][c] = *(const float4*)(st + BM * kBK + br * kBK + swz8(br, chunk) * 4);
-        }
-      }
+        for (int i = 0; i < 2; ++i) {
+          const int ar = wm * 64 + i * 32 + (lane & 31);
+          const int br = wn * 64 + i * 32 + (lane & 31);
 #pragma unroll
-      for (int kk = 0; kk < 16; ++kk)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const float4& av = fa[i][kk >> 2];
-            const float4& bv = fb[j][kk >> 2];
-            const float x = (kk & 3) == 0 ? av.x : (kk & 3) == 1 ? av.y : (kk & 3) == 2 ? av.z : av.w;
-            const float y = (kk & 3) == 0 ? bv.x : (kk & 3) == 1 ? bv.y : (kk & 3) == 2 ? bv.z : bv.w;
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc[i][j], 0, 0, 0);
+          for (int c = 0; c < 2; ++c) {
+            const int chunk = 4 * (lane >> 5) + 2 * half + c;
+            fa[i][c] = *(const float4*)(st + ar * kBK + swz8(ar, chunk) * 4);
+            fb[i][c] = *(const float4*)(st + BM * kBK + br * kBK + swz8(br, chunk) * 4);
           }
+        }
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const float4& av = fa[i][kk >> 2];
+              const float4& bv = fb[j][kk >> 2];
+              const float x = (kk & 3) == 0 ? av.x : (kk & 3) == 1 ? av.y : (kk & 3) == 2 ? av.z : av.w;
+              const float y = (kk & 3) == 0 ? bv.x : (kk & 3) == 1 ? bv.y : (kk & 3) == 2 ? bv.z : bv.w;
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc[i][j], 0, 0, 0);
+            }
+      }
     }
-    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_s_barrier();  // the ring is refilled by the next segment or tile
   }
   store_acc<BM, BN>(p, w, acc, wm, wn, lane);
+}
+
+// One MFMA takes one A and one B value per lane (lane l: row / column l % 32,
+// k = l / 32), so each lane half works through its own 16 k of a step: lane
+// half h reads k 16 h .. 16 h + 15 of its row as four 16-byte chunks and the
+// 16 MFMAs of the step pair k = kk (half 0) with k = 16 + kk (half 1).  The
+// 16-byte chunk c of tile row r sits in slot c ^ ((r >> 1) & 7): a fragment
+// read (16 lanes at one chunk of 16 consecutive rows per LDS cycle) then
+// touches 16 distinct 16-byte bank groups.  64 MFMAs of 64 cycles a step
+// against 16 KB of LDS reads per wavefront: the matrix cores, not the LDS,
+// bound it.  BM x BN tile, (BM / 64) x (BN / 64) wavefronts of 64 x 64; A and
+// B tiles of BM and BN rows x 128 B a stage.
+//
+// With ranges (sk_groups > 0), the last round's (tile, K step) units are cut
+// into sk_groups contiguous ranges, one per workgroup slot of the round. A
+// range is shorter than a tile's K steps (the last round has fewer tiles than
+// there are ranges), so it meets one or two tiles, and its workgroup runs the
+// two parts one after the other.  The stores' lane addresses are recomputed
+// for each part (see store_acc): held across both K loops they spilled 62
+// VGPRs to scratch and cost 4 % on whole tiles.
+template <int BM, int BN>
+__global__ __launch_bounds__(BM * BN / 64) void gemm_f32_kernel(const F32Args args) {
+  extern __shared__ __attribute__((aligned(16))) float ldsf[];
+  const Plan& p = args.p;
+  // Every block walks a range [u0, u1) of (tile, K step) units from tile
+  // `base` on: a whole tile is [0, kt) of its own tile; piece q of the equal
+  // cuts is its K steps of tile dp_tiles + q / pieces; range s of the last
+  // round covers units [start(s), start(s + 1)) of the tiles from dp_tiles on.
+  // A part of a tile goes to workspace slot `slot0` + (its tile - the range's
+  // first tile).
+  const int64_t kt = p.kt_total;
+  const int b = (int)blockIdx.x;
+  int base, slot0 = 0;
+  int64_t u0 = 0, u1 = kt;
+  if (b < p.dp_tiles) {
+    base = xcd_order(b, p.dp_tiles);
+  } else if (p.sk_groups == 0) {
+    const int q = b - p.dp_tiles;
+    base = p.dp_tiles + q / p.pieces;
+    u0 = (int64_t)(q % p.pieces) * p.kt_per_piece;
+    u1 = u0 + p.kt_per_piece < kt ? u0 + p.kt_per_piece : kt;
+    slot0 = q;
+  } else {
+    const int s = b - p.dp_tiles;
+    base = p.dp_tiles;
+    u0 = sk_start(p, s);
+    u1 = sk_start(p, s + 1);
+    slot0 = 2 * s;
+  }
+  if (u0 >= u1 && !(u0 == 0 && kt == 0)) return;  // an empty range (a tile with no K steps still stores zeros)
+  const int64_t t0 = kt > 0 ? u0 / kt : 0, t1 = kt > 0 ? (u1 - 1) / kt : 0;  // t1 <= t0 + 1
+#pragma unroll 1
+  for (int64_t t = t0; t <= t1; ++t) {
+    const int64_t k0 = (u0 > t * kt ? u0 : t * kt) - t * kt;
+    const int64_t k1 = (u1 < (t + 1) * kt ? u1 : (t + 1) * kt) - t * kt;
+    // whole: a tile of the full rounds, or one that a range covers from end to end
+    const bool whole = (b < p.dp_tiles || p.sk_groups > 0) && k0 == 0 && k1 == kt;
+    f32_tile<BM, BN>(args, tile_work<BM, BN>(p, base + (int)t, k0, k1, whole ? -1 : slot0 + (int)(t - t0)), ldsf);
+  }
 }
 
 // C (+)= the sum of a last-round tile's pieces, in K order: BM BN / 1024
@@ -486,6 +584,55 @@ __global__ __launch_bounds__(256) void piece_sum_kernel(const Plan p) {
   }
 }
 
+// C (+)= the sum, in K order, of the parts of a last-round tile that the
+// ranges of gemm_f32_kernel computed: the ranges meeting the tile, in
+// increasing order (a tile one range covers whole was stored directly).
+// BM BN / 1024 blocks a tile, four columns a thread.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void sk_sum_kernel(const Plan p) {
+  constexpr int kBlocks = BM * BN / 1024;
+  const int q = blockIdx.x / kBlocks;  // last-round tile
+  const int e = (blockIdx.x % kBlocks) * 256 + threadIdx.x;
+  const int lr = e / (BN / 4), lc = (e % (BN / 4)) * 4;
+  const int64_t kt = p.kt_total, x0 = (int64_t)q * kt, x1 = x0 + kt;
+  // the range holding unit x0: the last s with start(s) <= x0 (skips empty ranges)
+  int64_t s = x0 * p.sk_groups / p.sk_units;
+  while (s > 0 && sk_start(p, s) > x0) --s;
+  while (s + 1 < p.sk_groups && sk_start(p, s + 1) <= x0) ++s;
+  if (sk_start(p, s + 1) >= x1) return;  // one range covers the tile: stored directly
+  int tm, tn;
+  grouped(p.dp_tiles + q, p.tiles_m, p.tiles_n, tm, tn);
+  const int grp = tn < p.tiles_n0 ? 0 : 1;
+  const int64_t row = (int64_t)tm * BM + lr;
+  if (row >= p.m) return;
+  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  bool first = true;
+  for (; s < p.sk_groups; ++s) {
+    const int64_t a = sk_start(p, s);
+    if (a >= x1) break;
+    if (a == sk_start(p, s + 1)) continue;  // empty range
+    const int slot = 2 * (int)s + (int)(q - a / kt);
+    const float4 u = *((const float4*)(p.ws + (int64_t)slot * (BM * BN)) + e);
+    if (first) {
+      v = u;
+      first = false;
+    } else {
+      v.x += u.x;
+      v.y += u.y;
+      v.z += u.z;
+      v.w += u.w;
+    }
+  }
+  const int64_t n_grp = p.n[grp], col0 = (int64_t)(grp ? tn - p.tiles_n0 : tn) * BN + lc;
+  float* out = p.c[grp] + row * p.ldc[grp];
+  const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int64_t col = col0 + t;
+    if (col < n_grp) out[col] = p.accumulate ? out[col] + vv[t] : vv[t];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 
@@ -493,6 +640,7 @@ struct PiecePlan {
   int dp;              // whole tiles
   int pieces;          // pieces per remaining tile
   int64_t kt_per_piece;
+  int sk_groups;       // > 0: the remaining tiles' K steps in this many contiguous ranges instead of pieces
 };
 
 // A kernel's tile: BM x BN outputs of `threads` threads and `lds` bytes of
@@ -504,16 +652,20 @@ struct PiecePlan {
 // the time of one round of tiles: 4 bytes read per output and piece at ~5
 // TB/s against 192 (bf16 products, ~1 PFLOP/s reached) or 64 (fp32, ~130
 // TFLOP/s) flops per output and K step.
+// `ranges`: the kernel can take the last round as contiguous K ranges, one per
+// workgroup of the round (gemm_f32_kernel), rather than as equal pieces of each
+// tile.
 struct Shape {
   int bm, bn, threads, rounds_per_cu;
   size_t lds;
   double sum_cost;
+  bool ranges;
 };
 
-constexpr Shape kX3Shape{kBM, kBN, 256, 1, kLds, 4.2};
+constexpr Shape kX3Shape{kBM, kBN, 256, 1, kLds, 4.2, false};
 constexpr int kF32BM = 256, kF32BN = 256;
 constexpr Shape kF32Shape{kF32BM, kF32BN, kF32BM * kF32BN / 64, 1,
-                          (size_t)kStages * (kF32BM + kF32BN) * kBK * 4, 1.6};
+                          (size_t)kStages * (kF32BM + kF32BN) * kBK * 4, 1.6, true};
 
 // k_slices >= 1: every tile in k_slices pieces (1: whole tiles).  0: the
 // tiles of a partly filled last round (of `slots` tiles) in the piece count
@@ -521,7 +673,7 @@ constexpr Shape kF32Shape{kF32BM, kF32BN, kF32BM * kF32BN / 64, 1,
 // plus the cost of summing the pieces, sum_cost / (K steps) per round of
 // pieces.  At least 8 K steps a piece, and only for a gain of 10 % or more.
 PiecePlan plan_pieces(int64_t tiles, int64_t kt_total, int k_slices, int slots, double sum_cost) {
-  PiecePlan pp{(int)tiles, 1, kt_total > 0 ? kt_total : 1};
+  PiecePlan pp{(int)tiles, 1, kt_total > 0 ? kt_total : 1, 0};
   int s = 1;
   if (k_slices >= 1) {
     s = k_slices;
@@ -577,7 +729,9 @@ int64_t tiles_of(const Shape& sh, int64_t m, int64_t n, int64_t n2) {
 }
 
 int64_t piece_bytes(const Shape& sh, int64_t tiles, const PiecePlan& pp) {
-  return pp.pieces > 1 ? (tiles - pp.dp) * pp.pieces * (int64_t)sh.bm * sh.bn * (int64_t)sizeof(float) : 0;
+  const int64_t tile = (int64_t)sh.bm * sh.bn * (int64_t)sizeof(float);
+  if (pp.sk_groups > 0) return 2 * (int64_t)pp.sk_groups * tile;
+  return pp.pieces > 1 ? (tiles - pp.dp) * pp.pieces * tile : 0;
 }
 
 int plan_for(const Shape& sh, int64_t m, int64_t n, int64_t n2, int64_t kt_total, int k_slices, int64_t* tiles,
@@ -586,7 +740,18 @@ int plan_for(const Shape& sh, int64_t m, int64_t n, int64_t n2, int64_t kt_total
   const int rc = device_cus(&cus);
   if (rc != EG_OK) return rc;
   *tiles = tiles_of(sh, m, n, n2);
-  *pp = plan_pieces(*tiles, kt_total, k_slices, sh.rounds_per_cu * cus, sh.sum_cost);
+  const int slots = sh.rounds_per_cu * cus;
+  *pp = plan_pieces(*tiles, kt_total, k_slices, slots, sh.sum_cost);
+  // a kernel that takes ranges: the last round that the plan cuts runs as one
+  // contiguous range of its (tile, K step) units per workgroup slot, at least
+  // 8 K steps a range (fewer pieces than equal cuts, and no tile cut more
+  // often than the ranges meeting it)
+  const int64_t r = *tiles - pp->dp;
+  if (sh.ranges && k_slices == 0 && pp->pieces > 1 && r < slots && r * kt_total >= 8 * (int64_t)slots) {
+    pp->pieces = 1;
+    pp->kt_per_piece = kt_total;
+    pp->sk_groups = slots;
+  }
   return EG_OK;
 }
 
@@ -627,6 +792,8 @@ int launch_gemm(const Shape& sh, void (*kernel)(const Args), const char* name, A
   p.dp_tiles = pp.dp;
   p.pieces = pp.pieces;
   p.kt_per_piece = pp.kt_per_piece;
+  p.sk_groups = pp.sk_groups;
+  p.sk_units = pp.sk_groups > 0 ? (tiles - pp.dp) * p.kt_total : 0;
   p.c[0] = c;
   p.c[1] = c2;
   p.ldc[0] = ldc;
@@ -638,7 +805,7 @@ int launch_gemm(const Shape& sh, void (*kernel)(const Args), const char* name, A
   p.tiles_n0 = (int)((n + BN - 1) / BN);
   p.tiles_n = p.tiles_n0 + (int)((n2 + BN - 1) / BN);
   p.accumulate = accumulate ? 1 : 0;
-  const int64_t blocks = pp.dp + (tiles - pp.dp) * pp.pieces;
+  const int64_t blocks = pp.dp + (pp.sk_groups > 0 ? (int64_t)pp.sk_groups : (tiles - pp.dp) * pp.pieces);
   EG_CHECK_ARG(blocks < (1LL << 31), "too many workgroups");
   hipStream_t st = (hipStream_t)stream;
   // the dynamic LDS attribute, once per device and kernel
@@ -658,8 +825,12 @@ int launch_gemm(const Shape& sh, void (*kernel)(const Args), const char* name, A
   hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(sh.threads), sh.lds, st, g);
   rc = launch_status(name);
   if (rc != 0 || pp.dp == tiles) return rc;
-  hipLaunchKernelGGL((piece_sum_kernel<BM, BN>), dim3((unsigned)((tiles - pp.dp) * (BM * BN / 1024))), dim3(256),
-                     0, st, p);
+  const dim3 sum_grid((unsigned)((tiles - pp.dp) * (BM * BN / 1024)));
+  if (pp.sk_groups > 0) {
+    hipLaunchKernelGGL((sk_sum_kernel<BM, BN>), sum_grid, dim3(256), 0, st, p);
+    return launch_status("sk_sum_kernel");
+  }
+  hipLaunchKernelGGL((piece_sum_kernel<BM, BN>), sum_grid, dim3(256), 0, st, p);
   return launch_status("piece_sum_kernel");
 }
 

@@ -473,7 +473,9 @@ typedef struct eg_gemm_f32_operands {
  * accumulated in fp32.  Operands 16-byte aligned, leading dimensions
  * multiples of 4, k a multiple of 32.  Its tiles are 256 x 256 (one
  * workgroup a CU), so its pieces and workspace follow
- * eg_gemm_f32_workspace_size.  ple_forward's projections with
+ * eg_gemm_f32_workspace_size; with k_slices 0, a partly filled last round
+ * runs as one contiguous range of (tile, K step) units a CU, the parts of a
+ * tile summed in K order afterwards.  ple_forward's projections with
  * gemm="fp32", the arithmetic of the reference's torch fp32 matmuls
  * (engraft/replica/layers.py:594-606). */
 int64_t eg_gemm_f32_workspace_size(int64_t m, int64_t n, int64_t n2, int64_t k, int32_t k_slices);

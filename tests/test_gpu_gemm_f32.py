@@ -190,24 +190,39 @@ def test_gemm_f32_argument_errors(cuda):
         _lib.call("eg_gemm_f32", ops, 1, 8, 8, 0, _lib.ptr(c), 8, None, 0, 0, 1, None, 0, st)
 
 
-@pytest.mark.parametrize("kind", ["f32", "bf16x3"])
-def test_gemm_last_round_in_pieces(cuda, kind):
-    """A tile count that leaves the last round of workgroups mostly empty (on
-    256 CUs: 288 tiles of 256 x 256 at one a CU for fp32, 1152 of 128 x 128 at
-    two a CU for bf16x3): the library's plan runs that round's tiles in K
-    pieces summed afterwards.  Within the bar, equal to itself on a second
-    call, and refused with a workspace one byte short."""
+# (kind, m, n, k, plan on 256 CUs, workspace bytes of that plan).  fp32, one
+# 256 x 256 tile a CU: 288 tiles, 32 of them in 256 ranges of 8 K steps (each
+# inside one tile); 280 tiles, 24 in ranges of 9-10 of their 100 K steps (most
+# ranges meet two tiles); 264 tiles of 16 K steps, too short for ranges, the 8
+# past the first round in halves after 256 whole tiles.  bf16x3, 128 x 128
+# tiles: 1152 tiles, the 128 past the whole rounds in pieces.
+_LAST_ROUND = [
+    ("f32", 1024, 18432, 2048, "ranges", 2 * 256 * 256 * 256 * 4),
+    ("f32", 1024, 17920, 3200, "ranges", 2 * 256 * 256 * 256 * 4),
+    ("f32", 2048, 8448, 512, "halves", 8 * 2 * 256 * 256 * 4),
+    ("bf16x3", 1024, 18432, 2048, "pieces", None),
+]
+
+
+@pytest.mark.parametrize("kind,m,n,k,plan,ws_bytes", _LAST_ROUND, ids=[f"{c[0]}-{c[4]}-k{c[3]}" for c in _LAST_ROUND])
+def test_gemm_last_round_in_pieces(cuda, kind, m, n, k, plan, ws_bytes):
+    """Tile counts that leave the last round of workgroups mostly empty: the
+    library's plan runs that round's tiles as K ranges or K pieces whose
+    partial products are summed afterwards in K order.  Within the bar, equal
+    to itself on a second call, refused with a workspace one byte short, and
+    with accumulate on exactly twice the product."""
     from engraft_ngram_amd import _lib
     from engraft_ngram_amd.ple import gemm_f32, gemm_x3
-    _say(f"gemm last round in pieces ({kind})")
+    _say(f"gemm last round ({kind}, {plan}, m {m} n {n} k {k})")
     g = torch.Generator(device=cuda).manual_seed(21)
-    m, n, k = 1024, 18432, 2048
     a = torch.randn(m, k, generator=g, device=cuda)
     b = torch.randn(n, k, generator=g, device=cuda) * 0.05
     size_fn = "eg_gemm_f32_workspace_size" if kind == "f32" else "eg_gemm_workspace_size"
     need = int(getattr(_lib.load(), size_fn)(m, n, 0, k, 0))
     if torch.cuda.get_device_properties(cuda).multi_processor_count == 256:
-        assert need > 0, "the mostly empty last round should be cut into pieces"
+        assert need > 0, "the mostly empty last round should be cut"
+        if ws_bytes is not None:
+            assert need == ws_bytes, f"workspace {need} B, the {plan} plan takes {ws_bytes} B"
     fn = gemm_f32 if kind == "f32" else gemm_x3
     got = fn(a, b)
     if kind == "f32":
@@ -233,3 +248,9 @@ def test_gemm_last_round_in_pieces(cuda, kind):
                   _lib.stream_ptr(cuda))
         torch.cuda.synchronize()
         assert torch.equal(out, got)
+        # accumulate: every output, whole tile or summed parts, adds the same
+        # sum again, and doubling is exact
+        _lib.call("eg_gemm_f32", ops, 1, m, n, 0, _lib.ptr(out), n, None, 0, 1, 0, _lib.ptr(ws), need,
+                  _lib.stream_ptr(cuda))
+        torch.cuda.synchronize()
+        assert torch.equal(out, 2 * got)
