@@ -25,7 +25,6 @@
 // oracle reproduces them exactly.
 #include <string.h>
 
-#include <atomic>
 #include <mutex>
 
 #include "eg_common.h"
@@ -200,24 +199,29 @@ __global__ __launch_bounds__(kTileThreads) void keys_count_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Bucketed grouping: two launches, one global atomic per bucket
+// Bucketed grouping: two launches, no global atomics, no waits between workgroups
 // ---------------------------------------------------------------------------
 // Bucket b holds the variables [b << bs, (b + 1) << bs).
 // tile_sort_kernel: tile t (kGroupTile slots) computes its slots' keys and
 //   counting-sorts its (key, slot) pairs by bucket in LDS into its own region
-//   pairs[t * kGroupTile, ...), writing per bucket the segment seg[t][b] =
-//   (count, tile-local offset).
+//   pairs[t * kGroupTile, ...), writing per bucket the segment
+//   seg[b][t] = count << 16 | offset, the offset being the slots of t in
+//   the buckets before b (bucket-major: a bucket reads its segments of every
+//   tile as one contiguous run).
 // bucket_ranges_kernel: bucket b gathers its pairs from every tile, counts
 //   its keys in LDS and writes every variable's range [start, end) and its
 //   slot ids (in no particular order inside a range: the reduction orders
-//   them), and lists the variables of more than kPiece slots.  Its region of
-//   the slots array, and of the list, follows those of the earlier buckets:
-//   every bucket publishes its totals, tagged with the call's epoch, and adds
-//   up the earlier buckets' (no same-address atomics, which serialise).
+//   them).  Its region of the slots array starts at the slots of every tile
+//   in the earlier buckets, which is the sum over t of its own segments'
+//   offsets: each bucket finds it alone.  Its variables of more than kPiece
+//   slots go to its region of the long list, [start / (kPiece + 1),
+//   end / (kPiece + 1)) (room for every variable of more than kPiece slots in
+//   [start, end)), the rest of the region holds kNoVar.
 constexpr int kGroupThreads = 512;
 constexpr int kGroupIPT = 2;
 constexpr int kGroupTile = kGroupThreads * kGroupIPT;  // slots per tile
 constexpr int kBucketsMax = 1024;
+constexpr uint32_t kNoVar = 0xffffffffu;                // an unused entry of the long list
 constexpr int kBucketKeysLog2Max = 11;                 // at most 2048 variables per bucket
 constexpr int kRangeThreads = 256;
 constexpr int kRangeTilesMax = 4 * kRangeThreads;   // tiles bucket_ranges_kernel reads (4 per thread)
@@ -260,7 +264,7 @@ template <int MODE>
 __global__ __launch_bounds__(kGroupThreads) void tile_sort_kernel(
     const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ ids, int64_t n_var, int split_shift,
     const unsigned long long* __restrict__ index, int index_bits, int bs, int nb, int64_t n_tiles,
-    unsigned long long* __restrict__ pairs, u32x2* __restrict__ seg) {
+    unsigned long long* __restrict__ pairs, uint32_t* __restrict__ seg) {
   __shared__ int32_t spl[MODE == 0 ? kSplitMax : 1];
   __shared__ uint32_t bh[kBucketsMax];
   __shared__ uint32_t wsum[kGroupThreads / 64];
@@ -292,7 +296,7 @@ __global__ __launch_bounds__(kGroupThreads) void tile_sort_kernel(
 #pragma unroll
   for (int u = 0; u < kBucketsMax / kGroupThreads; ++u) {
     const int b = tid + u * kGroupThreads;
-    if (b < nb) seg[t * nb + b] = u32x2{cnt_b[u], bh[b]};
+    if (b < nb) seg[(int64_t)b * n_tiles + t] = cnt_b[u] << 16 | bh[b];  // both <= kGroupTile
   }
 #pragma unroll
   for (int r = 0; r < kGroupIPT; ++r) {
@@ -303,47 +307,17 @@ __global__ __launch_bounds__(kGroupThreads) void tile_sort_kernel(
   }
 }
 
-// Sum over buckets [0, b) of the values they publish in pub[] tagged with this
-// call's epoch (the high 32 bits), read coherently across XCDs.  Only earlier
-// buckets are waited for: workgroups are dispatched in order, so those are
-// already resident and publish without waiting on this one.  The wait is
-// bounded; past the bound the value read is used as it is.
-__device__ inline uint32_t sum_published(const unsigned long long* pub, int64_t b, uint32_t epoch, uint32_t* wsum) {
-  const int tid = threadIdx.x;
-  uint32_t part = 0;
-  for (int64_t i = tid; i < b; i += kRangeThreads) {
-    unsigned long long v = 0;
-    for (int spin = 0; spin < (1 << 22); ++spin) {
-      v = __hip_atomic_load(&pub[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((uint32_t)(v >> 32) == epoch) break;
-      __builtin_amdgcn_s_sleep(2);
-    }
-    part += (uint32_t)v;
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
-  __syncthreads();
-  if ((tid & 63) == 0) wsum[tid >> 6] = part;
-  __syncthreads();
-  uint32_t total = 0;
-#pragma unroll
-  for (int w = 0; w < kRangeThreads / 64; ++w) total += wsum[w];
-  __syncthreads();
-  return total;
-}
-
 __global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
-    const unsigned long long* __restrict__ pairs, const u32x2* __restrict__ seg, int64_t n_tiles, int nb, int bs,
-    int64_t n_var, uint32_t epoch, unsigned long long* __restrict__ pub_total,
-    unsigned long long* __restrict__ pub_long, uint32_t* __restrict__ n_long, uint32_t* __restrict__ start,
-    uint32_t* __restrict__ end, uint32_t* __restrict__ slots, uint32_t* __restrict__ long_list) {
+    const unsigned long long* __restrict__ pairs, const uint32_t* __restrict__ seg, int64_t n_tiles, int nb, int bs,
+    int64_t n_var, int64_t long_len, uint32_t* __restrict__ start, uint32_t* __restrict__ end,
+    uint32_t* __restrict__ slots, uint32_t* __restrict__ long_list) {
   constexpr int kKeys = 1 << kBucketKeysLog2Max;
   constexpr int kKeep = 4;                         // pairs of one tile a thread holds in registers
   __shared__ uint32_t cnt[kKeys];                  // pairs held in registers, per variable
   __shared__ uint32_t over[kKeys];                 // pairs beyond kKeep of a tile, per variable
   __shared__ uint32_t lst[kKeys];
   __shared__ uint32_t lng[kKeys];                  // the bucket's variables of more than kPiece slots
-  __shared__ uint32_t wsum[kRangeThreads / 64];
+  __shared__ uint32_t wsum[2][kRangeThreads / 64];
   __shared__ uint32_t n_long_b;
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
@@ -353,29 +327,19 @@ __global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
     cnt[i] = 0u;
     over[i] = 0u;
   }
-  // this thread's tiles: (count, offset) of the bucket's segment in each
+  if (tid == 0) n_long_b = 0u;
+  // this thread's tiles: (count, offset) of the bucket's segment in each; the
+  // offsets add up to the bucket's place in the slots array
   constexpr int kTilesPerThread = 4;  // n_tiles <= kTilesPerThread * kRangeThreads (host checks)
   u32x2 sg[kTilesPerThread];
-  uint32_t part = 0;
+  uint32_t tot = 0, pre = 0;
 #pragma unroll
   for (int j = 0; j < kTilesPerThread; ++j) {
     const int64_t t = tid + (int64_t)j * kRangeThreads;
-    sg[j] = t < n_tiles ? seg[t * nb + b] : u32x2{0u, 0u};
-    part += sg[j].x;
-  }
-  // the bucket's slot total, published for the later buckets; its region of
-  // the slots array starts at the totals of the earlier buckets
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
-  if ((tid & 63) == 0) wsum[tid >> 6] = part;
-  if (tid == 0) n_long_b = 0u;
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t total = 0;
-#pragma unroll
-    for (int w = 0; w < kRangeThreads / 64; ++w) total += wsum[w];
-    __hip_atomic_store(&pub_total[b], ((unsigned long long)epoch << 32) | total, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t e = t < n_tiles ? seg[b * n_tiles + t] : 0u;
+    sg[j] = u32x2{e >> 16, e & 0xffffu};
+    tot += sg[j].x;
+    pre += sg[j].y;
   }
   // the first kKeep pairs of each tile segment: loaded together, counted, and
   // given their rank among the variable's register-held pairs
@@ -390,6 +354,16 @@ __global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
     for (int e = 0; e < kKeep; ++e) pr[j][e] = src[(uint32_t)e < sg[j].x ? e : 0];
   }
 #pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    tot += __shfl_xor(tot, o);
+    pre += __shfl_xor(pre, o);
+  }
+  if ((tid & 63) == 0) {
+    wsum[0][tid >> 6] = tot;
+    wsum[1][tid >> 6] = pre;
+  }
+  __syncthreads();  // (also closes the zeroing of the counts)
+#pragma unroll
   for (int j = 0; j < kTilesPerThread; ++j)
 #pragma unroll
     for (int e = 0; e < kKeep; ++e)
@@ -401,10 +375,16 @@ __global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
     const unsigned long long* src = pairs + (tid + (int64_t)j * kRangeThreads) * kGroupTile + sg[j].y;
     for (uint32_t e = kKeep; e < sg[j].x; ++e) atomicAdd(&over[(uint32_t)(src[e] >> 32) - (uint32_t)key0], 1u);
   }
-  const uint32_t base = sum_published(pub_total, b, epoch, wsum);  // (its barriers also close the counting)
+  uint32_t total = 0, base = 0;
+#pragma unroll
+  for (int w = 0; w < kRangeThreads / 64; ++w) {
+    total += wsum[0][w];
+    base += wsum[1][w];
+  }
+  __syncthreads();
   for (int i = tid; i < nkeys; i += kRangeThreads) lst[i] = cnt[i] + over[i];
   __syncthreads();
-  lds_exclusive_scan<kRangeThreads, kKeys / kRangeThreads>(lst, nkeys, wsum);
+  lds_exclusive_scan<kRangeThreads, kKeys / kRangeThreads>(lst, nkeys, wsum[0]);
   for (int i = tid; i < nkeys; i += kRangeThreads) {
     const uint32_t c = cnt[i] + over[i];
     start[key0 + i] = base + lst[i];
@@ -413,13 +393,10 @@ __global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
     over[i] = lst[i] + cnt[i];  // where the variable's overflow pairs go
   }
   __syncthreads();
-  // the variables of more than kPiece slots, listed after the earlier buckets' ones
-  if (tid == 0)
-    __hip_atomic_store(&pub_long[b], ((unsigned long long)epoch << 32) | n_long_b, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t lbase = sum_published(pub_long, b, epoch, wsum);
-  if (b == nb - 1 && tid == 0) *n_long = lbase + n_long_b;
-  for (uint32_t j = tid; j < n_long_b; j += kRangeThreads) long_list[lbase + j] = lng[j];
+  // the bucket's region of the long list: its long variables, then kNoVar
+  const int64_t l0 = base / (kPiece + 1);
+  const int64_t l1 = b == nb - 1 ? long_len : (int64_t)(base + total) / (kPiece + 1);
+  for (int64_t j = tid; j < l1 - l0; j += kRangeThreads) long_list[l0 + j] = j < n_long_b ? lng[j] : kNoVar;
   // every slot id at its variable's place (the order inside a range is free)
 #pragma unroll
   for (int j = 0; j < kTilesPerThread; ++j)
@@ -441,8 +418,11 @@ __global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
   }
 }
 
-__global__ __launch_bounds__(256) void zero_kernel(uint32_t* __restrict__ a, int64_t len) {
+// a[0, len) = 0 and l[0, l_len) = kNoVar.
+__global__ __launch_bounds__(256) void clear_kernel(uint32_t* __restrict__ a, int64_t len, uint32_t* __restrict__ l,
+                                                    int64_t l_len) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < len; i += (int64_t)gridDim.x * 256) a[i] = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < l_len; i += (int64_t)gridDim.x * 256) l[i] = kNoVar;
 }
 
 // ---------------------------------------------------------------------------
@@ -566,8 +546,7 @@ struct SegArgs {
   const uint32_t* start;      // [n_var] start of each variable's range in slots
   const uint32_t* end;        // [n_var] its end
   const uint32_t* slots;      // slot ids grouped by variable (CSR)
-  const uint32_t* long_list;  // variables with more than kPiece slots
-  const uint32_t* n_long;     // their number
+  const uint32_t* long_list;  // variables with more than kPiece slots, unused entries kNoVar
   int64_t n;
   int64_t n_var;
   const void* d_out;
@@ -821,9 +800,9 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
   float* part = (float*)lds;  // [kLongGroups][512] once the slot ids are no longer needed
   const int lane = threadIdx.x & 63, sub = lane & 31, gbase = lane & 32;
   if ((int64_t)blockIdx.x < n_long_blocks) {
-    if (blockIdx.x >= *a.n_long) return;  // uniform per workgroup
-    const int grp = threadIdx.x >> 5;
     const uint32_t key = a.long_list[blockIdx.x];
+    if (key == kNoVar) return;  // uniform per workgroup
+    const int grp = threadIdx.x >> 5;
     const int64_t lo = a.start[key];
     const int64_t hi = a.end[key];
     const int64_t len = hi - lo;
@@ -939,7 +918,6 @@ struct GroupPlan {
   int64_t n_tiles;  // tiles of kGroupTile slots
 };
 
-static std::atomic<uint32_t> g_epoch{0u};
 
 static GroupPlan plan_for(int64_t n, int64_t n_var) {
   GroupPlan g{false, 0, 0, 0};
@@ -959,8 +937,7 @@ struct Workspace {
   uint32_t* slots;      // [n] slot ids grouped by variable
   uint32_t* start;      // [n_var] range start of every variable
   uint32_t* end;        // [n_var] range end (the counting path: start + 1)
-  uint32_t* long_list;  // variables of more than kPiece slots
-  uint32_t* n_long;     // their number
+  uint32_t* long_list;  // [n / (kPiece + 1) + 1] variables of more than kPiece slots, the rest kNoVar
   // the counting path
   uint32_t* keys;       // [n] variable of every slot (n_var: none)
   uint32_t* ranks;      // [n] place of every slot in its variable's range
@@ -968,9 +945,7 @@ struct Workspace {
   uint32_t* partial;    // scan chunk totals
   // the bucketed path
   unsigned long long* pairs;  // [n_tiles * kGroupTile] (key << 32 | slot), bucket-sorted per tile
-  u32x2* seg;                 // [n_tiles, nb] (slots of bucket b in tile t, their offset in t's region)
-  uint32_t* counters;         // [1]: the long-list length
-  unsigned long long* pub;    // [2 * nb]: every bucket's slot total, then its long-list length (epoch-tagged)
+  uint32_t* seg;              // [nb, n_tiles] slots of bucket b in tile t << 16 | the slots of t before b
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -997,10 +972,7 @@ static size_t carve(void* ws, int64_t n, int64_t n_var, Workspace* out) {
     w.start = (uint32_t*)take((size_t)n_var * 4);
     w.end = (uint32_t*)take((size_t)n_var * 4);
     w.pairs = (unsigned long long*)take((size_t)g.n_tiles * kGroupTile * 8);
-    w.seg = (u32x2*)take((size_t)g.n_tiles * g.nb * 8);
-    w.counters = (uint32_t*)take(4);
-    w.n_long = w.counters;
-    w.pub = (unsigned long long*)take((size_t)2 * g.nb * 8);
+    w.seg = (uint32_t*)take((size_t)g.n_tiles * g.nb * 4);
   } else {
     w.keys = (uint32_t*)take((size_t)n * 4);
     w.ranks = (uint32_t*)take((size_t)n * 4);
@@ -1008,7 +980,6 @@ static size_t carve(void* ws, int64_t n, int64_t n_var, Workspace* out) {
     w.partial = (uint32_t*)take((size_t)(scan_chunks(n_var + 1) + 1) * 4);
     w.start = w.off;
     w.end = w.off ? w.off + 1 : nullptr;
-    w.n_long = w.off ? w.off + n_var + 1 : nullptr;
   }
   if (out) *out = w;
   return at;
@@ -1040,15 +1011,12 @@ static int group_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64
     else if (mode == 1) EG_TILE_SORT(1);
     else EG_TILE_SORT(0);
 #undef EG_TILE_SORT
-    // a fresh epoch per call: the published values of earlier calls never match
-    uint32_t epoch = g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
-    if (epoch == 0u) epoch = g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
     hipLaunchKernelGGL(bucket_ranges_kernel, dim3((unsigned)g.nb), dim3(kRangeThreads), 0, st, w.pairs, w.seg,
-                       g.n_tiles, g.nb, g.bs, n_var, epoch, w.pub, w.pub + g.nb, w.n_long, w.start, w.end, w.slots,
-                       w.long_list);
+                       g.n_tiles, g.nb, g.bs, n_var, n_long_max(n), w.start, w.end, w.slots, w.long_list);
     return launch_status("slot grouping kernels");
   }
-  hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n_var + 2, 256, 1024)), dim3(256), 0, st, w.off, n_var + 2);
+  hipLaunchKernelGGL(clear_kernel, dim3(grid_for(n_var + 2, 256, 1024)), dim3(256), 0, st, w.off, n_var + 2,
+                     w.long_list, n_long_max(n));
   const dim3 kgrid((unsigned)((n + kTile - 1) / kTile));
   if (mode == 2) {
     hipLaunchKernelGGL(keys_count_kernel<2>, kgrid, dim3(kTileThreads), 0, st, rows, n, ids, n_var, 0,
@@ -1075,7 +1043,6 @@ static void fill_seg(SegArgs* a, const Workspace& w, int64_t n, int64_t n_var) {
   a->end = w.end;
   a->slots = w.slots;
   a->long_list = w.long_list;
-  a->n_long = w.n_long;
   a->n = n;
   a->n_var = n_var;
 }

@@ -123,9 +123,11 @@ class DescentState:
         if self.quant is not None and ids.numel():
             # every variable's quantised row is valid before its first step
             self._requant(self.master, None)
-        # open-addressing index of the ids for the backward's lookups (built once)
+        # open-addressing index of the ids for the backward's lookups (built
+        # once), at most a quarter full: a wavefront's lookups probe in
+        # lockstep, so the longest probe chain of 64 lanes sets their time
         cap = 64
-        while cap < 2 * ids.numel():
+        while cap < 4 * ids.numel():
             cap *= 2
         self.index = torch.empty(cap, dtype=torch.int64, device=dev)
         _lib.call("eg_build_row_index", _lib.ptr(self.ids), ids.numel(), _lib.ptr(self.index), cap,
