@@ -78,6 +78,30 @@ def test_scatter_grad_edge_cases(cuda):
         assert np.array_equal(got, exp)
 
 
+@pytest.mark.parametrize("n_slots,n_var", [(1_100_000, 300_000), (1_000_000, 1_500_000)],
+                         ids=["counting-1075-tiles", "buckets-of-2048-variables"])
+def test_scatter_grad_large_groupings(cuda, n_slots, n_var):
+    """The two groupings past the common case, bit-exact against the oracle:
+    more than 1,024 tiles of 1,024 slots (the counting grouping: per-variable
+    atomics, scan, fill), and more than 1M variables (the tile sort with
+    buckets of 2,048 variables).  Zipf-drawn rows give long segments; a twentieth
+    of the slots hit no variable."""
+    from engraft_ngram_amd import descent as D
+    _say(f"scatter_grad grouping, {n_slots} slots over {n_var} variables")
+    rng = np.random.default_rng(71)
+    ids = np.sort(rng.choice(np.arange(0, 8 * n_var, 2, dtype=np.int64), size=n_var, replace=False)).astype(np.int32)
+    pick = (rng.zipf(1.2, size=n_slots) - 1) % n_var
+    rows = ids[pick].astype(np.int64)
+    rows[rng.random(n_slots) < 0.05] += 1  # odd: no variable
+    rows = rows.astype(np.int32).reshape(-1, 1)
+    d = torch.from_numpy(rng.standard_normal((n_slots, 64), dtype=np.float32)).to(cuda)
+    got = D.scatter_grad(d, torch.from_numpy(rows), torch.from_numpy(ids), 64).cpu().numpy()
+    exp, hits = B.scatter_grad(d.cpu().numpy(), rows, ids)
+    _say(f"longest segment {hits.max()}, variables hit {(hits > 0).sum()}")
+    assert hits.max() > 1000
+    assert np.array_equal(got, exp)
+
+
 def test_descent_step_config2_full_size(cuda):
     """BASELINE config 2 at its own size: the config-1 table and batch, d_residual
     [16384, 2048] bf16 ~ N(0, 1e-3), duplicates merged deterministically, Adam
