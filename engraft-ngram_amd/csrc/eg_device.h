@@ -160,6 +160,16 @@ __host__ __device__ inline uint32_t f32_to_bf16(float f) {
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
+// Two fp32 values to bf16 packed lo | hi << 16, in one gfx950
+// v_cvt_pk_bf16_f32 (round to nearest even, NaN quieted): bit-identical to
+// f32_to_bf16 on all 2^32 fp32 inputs (checked exhaustively on an MI355X).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 __device__ inline float f16_to_f32(uint16_t h) {
   _Float16 v = __builtin_bit_cast(_Float16, h);
   return (float)v;

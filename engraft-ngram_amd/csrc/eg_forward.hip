@@ -186,7 +186,10 @@ constexpr int kWavesPerBlock = 4;
 template <int FMT, int DIM, int NCH, int MAXL, bool F32OUT, bool OVL, int PARTS, bool ROWS>
 __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   const int lane = threadIdx.x & 63;
-  const uint32_t wid = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);  // n_pos * parts < 2^32
+  // Wavefront index (n_pos * parts < 2^32), read as wavefront-uniform: the
+  // position, column part and head range then live in scalar registers and
+  // their address arithmetic leaves the vector ALU.
+  const uint32_t wid = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6));
   const uint32_t parts = PARTS ? (uint32_t)PARTS : (uint32_t)a.parts;     // PARTS: known at compile time
   const uint32_t pu = parts == 1 ? wid : wid / parts;
   const int64_t p = pu;
@@ -221,7 +224,12 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
     seg0 = a.decode_ctx > 0 ? p * a.decode_ctx : seg_start_of(p, a.seq_len, a.seg_start);
     int ng = a.hash[0].ngram_size;
     if (MAXL > 1 && nl > 1 && a.hash[1].ngram_size > ng) ng = a.hash[1].ngram_size;
-    load_ctx_tokens(a.tokens, tp, ng, raw);
+    // The token index is uniform, but held in a vector register: the tokens are
+    // then vector loads, retired in issue order ahead of the residual (scalar
+    // loads would be waited for before the residual loads are issued).
+    int64_t tpv = tp;
+    asm volatile("" : "+v"(tpv));
+    load_ctx_tokens(a.tokens, tpv, ng, raw);
 #pragma unroll
     for (int l = 0; l < MAXL; ++l)
       if (l < nl) {
@@ -364,7 +372,7 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
       } else {
         u32x4 o;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = f32_to_bf16(acc[c][2 * i]) | (f32_to_bf16(acc[c][2 * i + 1]) << 16);
+        for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(acc[c][2 * i], acc[c][2 * i + 1]);
         __builtin_nontemporal_store(o, (u32x4*)((uint16_t*)a.out + p * W + e0));
       }
     }

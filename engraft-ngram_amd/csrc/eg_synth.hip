@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void synth_kernel(uint8_t* __restrict__ payloa
       for (int w = 0; w < 4; ++w) {
         u32x4 o;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = f32_to_bf16(x[w * 8 + 2 * i]) | (f32_to_bf16(x[w * 8 + 2 * i + 1]) << 16);
+        for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(x[w * 8 + 2 * i], x[w * 8 + 2 * i + 1]);
         dst[w] = o;
       }
     } else if constexpr (FMT == EG_FMT_Q8_0) {
