@@ -170,6 +170,10 @@ SIGNATURES = {
                                   c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     "eg_descent_step": (c_int32, [c_void_p, c_int32, c_void_p, c_int64, c_int32, POINTER(EgDescentState),
                                   POINTER(EgAdam), POINTER(EgTable), c_void_p, ctypes.c_size_t, c_void_p]),
+    "eg_descent_plan": (c_int32, [c_void_p, c_int64, c_int32, POINTER(EgDescentState), c_void_p, ctypes.c_size_t,
+                                  c_void_p]),
+    "eg_descent_apply": (c_int32, [c_void_p, c_int32, c_int64, c_int32, POINTER(EgDescentState), POINTER(EgAdam),
+                                   POINTER(EgTable), c_void_p, ctypes.c_size_t, c_void_p]),
     "eg_descent_step_noalloc": (c_int32, [c_void_p, c_int32, c_void_p, c_int64, c_int32, POINTER(EgDescentState),
                                           POINTER(EgAdam), POINTER(EgTable), c_void_p]),
     "eg_descent_step_noalloc_max_bytes": (ctypes.c_size_t, []),

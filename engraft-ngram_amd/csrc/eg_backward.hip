@@ -1081,15 +1081,18 @@ static int launch_dense(const SegArgs& a, hipStream_t st) {
   return launch_status("dense_kernel");
 }
 
-static int check_common(const void* d_out, const int32_t* rows, int64_t n_pos, int32_t heads, int32_t dim,
-                        const int32_t* ids, int64_t n_var, void* ws, size_t ws_bytes) {
+// d_out and rows as the call uses them: a plan has no d_out, an apply no rows.
+static int check_common(const void* d_out, bool use_dout, const int32_t* rows, bool use_rows, int64_t n_pos,
+                        int32_t heads, int32_t dim, const int32_t* ids, int64_t n_var, const void* ws,
+                        size_t ws_bytes) {
   EG_CHECK_ARG(n_pos >= 0 && heads >= 1 && heads <= EG_MAX_HEADS, "n_pos=%lld heads=%d", (long long)n_pos, heads);
   EG_CHECK_ARG(dim == 64 || dim == 128 || dim == 160 || dim == 256, "backward dim=%d (built: 64, 128, 160, 256)",
                dim);
   EG_CHECK_ARG(n_var >= 0 && n_var < (1LL << 31), "n_var=%lld", (long long)n_var);
   const int64_t n = n_pos * heads;
   EG_CHECK_ARG(n < (1LL << 31), "n_pos*heads=%lld slots exceed 2^31", (long long)n);
-  EG_CHECK_ARG(n == 0 || (d_out != nullptr && rows != nullptr), "d_out/rows is NULL");
+  EG_CHECK_ARG(n == 0 || !use_dout || d_out != nullptr, "d_out is NULL");
+  EG_CHECK_ARG(n == 0 || !use_rows || rows != nullptr, "rows is NULL");
   EG_CHECK_ARG(n_var == 0 || ids != nullptr, "ids is NULL");
   if (ws_bytes < workspace_bytes(n, n_var))
     return set_error(EG_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", ws_bytes, workspace_bytes(n, n_var));
@@ -1160,8 +1163,8 @@ int eg_build_row_index(const int32_t* ids, int64_t n, int64_t* table, int64_t ca
 static int scatter_grad_impl(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos,
                              int32_t heads, int32_t dim, const int32_t* ids, int64_t n_var, bool direct,
                              float* grad_out, void* workspace, size_t workspace_bytes_, void* stream) {
-  int rc = check_common(d_out, rows, n_pos, heads, dim, direct ? (const int32_t*)rows : ids, n_var, workspace,
-                        workspace_bytes_);
+  int rc = check_common(d_out, true, rows, true, n_pos, heads, dim, direct ? (const int32_t*)rows : ids, n_var,
+                        workspace, workspace_bytes_);
   if (rc != EG_OK) return rc;
   EG_CHECK_ARG(n_var == 0 || grad_out != nullptr, "grad_out is NULL");
   const int64_t n = n_pos * heads;
@@ -1197,22 +1200,46 @@ int eg_scatter_grad_slots(const void* d_out, int32_t d_out_f32, const int32_t* s
                            workspace_bytes_, stream);
 }
 
-int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos, int32_t heads,
-                    const eg_descent_state* state, const eg_adam* opt, const eg_table* base, void* workspace,
-                    size_t workspace_bytes_, void* stream) {
-  EG_CHECK_ARG(state != nullptr && opt != nullptr, "state/opt is NULL");
-  int rc = check_common(d_out, rows, n_pos, heads, state->dim, state->ids, state->n, workspace, workspace_bytes_);
-  if (rc != EG_OK) return rc;
+// The descent state's own checks (every entry point of the step).
+static int check_state(const eg_descent_state* state) {
+  EG_CHECK_ARG(state != nullptr, "state is NULL");
   EG_CHECK_ARG(state->n == 0 || (state->master && state->m && state->v && state->stamp),
                "state master/m/v/stamp is NULL");
-  EG_CHECK_ARG(opt->step >= 1 && opt->step < (1LL << 31), "step=%lld", (long long)opt->step);
-  EG_CHECK_ARG(opt->lr >= 0.0 && opt->beta1 >= 0.0 && opt->beta1 < 1.0 && opt->beta2 >= 0.0 && opt->beta2 < 1.0 &&
-                   opt->eps >= 0.0,
-               "invalid Adam hyper-parameters");
   if (state->index != nullptr)
     EG_CHECK_ARG(state->index_capacity >= 2 * state->n && state->index_capacity >= 2 &&
                      (state->index_capacity & (state->index_capacity - 1)) == 0 && state->index_capacity <= (1LL << 32),
                  "index_capacity=%lld must be a power of two >= 2*n", (long long)state->index_capacity);
+  return EG_OK;
+}
+
+int eg_descent_plan(const int32_t* rows, int64_t n_pos, int32_t heads, const eg_descent_state* state,
+                    void* workspace, size_t workspace_bytes_, void* stream) {
+  int rc = check_state(state);
+  if (rc != EG_OK) return rc;
+  rc = check_common(nullptr, false, rows, true, n_pos, heads, state->dim, state->ids, state->n, workspace,
+                    workspace_bytes_);
+  if (rc != EG_OK) return rc;
+  const int64_t n = n_pos * heads;
+  if (state->n == 0 || n == 0) return EG_OK;
+  Workspace w;
+  carve(workspace, n, state->n, &w);
+  return group_slots(rows, n, state->ids, state->n, state->index, state->index_capacity, false, w,
+                     (hipStream_t)stream);
+}
+
+int eg_descent_apply(const void* d_out, int32_t d_out_f32, int64_t n_pos, int32_t heads,
+                     const eg_descent_state* state, const eg_adam* opt, const eg_table* base, const void* workspace,
+                     size_t workspace_bytes_, void* stream) {
+  int rc = check_state(state);
+  if (rc != EG_OK) return rc;
+  EG_CHECK_ARG(opt != nullptr, "opt is NULL");
+  rc = check_common(d_out, true, nullptr, false, n_pos, heads, state->dim, state->ids, state->n, workspace,
+                    workspace_bytes_);
+  if (rc != EG_OK) return rc;
+  EG_CHECK_ARG(opt->step >= 1 && opt->step < (1LL << 31), "step=%lld", (long long)opt->step);
+  EG_CHECK_ARG(opt->lr >= 0.0 && opt->beta1 >= 0.0 && opt->beta1 < 1.0 && opt->beta2 >= 0.0 && opt->beta2 < 1.0 &&
+                   opt->eps >= 0.0,
+               "invalid Adam hyper-parameters");
   SegArgs a;
   memset(&a, 0, sizeof(a));
   if (state->quant.payload != nullptr) {
@@ -1231,11 +1258,7 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   if (state->n == 0) return EG_OK;
   hipStream_t st = (hipStream_t)stream;
   Workspace w;
-  carve(workspace, n, state->n, &w);
-  if (n > 0) {
-    rc = group_slots(rows, n, state->ids, state->n, state->index, state->index_capacity, false, w, st);
-    if (rc != EG_OK) return rc;
-  }
+  carve((void*)workspace, n, state->n, &w);
   fill_seg(&a, w, n, state->n);
   a.d_out = d_out;
   a.d_out_f32 = d_out_f32;
@@ -1265,6 +1288,25 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
   }
   if (opt->dense) rc = launch_dense(a, st);
   return rc;
+}
+
+int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos, int32_t heads,
+                    const eg_descent_state* state, const eg_adam* opt, const eg_table* base, void* workspace,
+                    size_t workspace_bytes_, void* stream) {
+  int rc = check_state(state);
+  if (rc != EG_OK) return rc;
+  EG_CHECK_ARG(opt != nullptr, "opt is NULL");
+  // both halves' argument checks before either launches anything
+  rc = check_common(d_out, true, rows, true, n_pos, heads, state->dim, state->ids, state->n, workspace,
+                    workspace_bytes_);
+  if (rc != EG_OK) return rc;
+  EG_CHECK_ARG(opt->step >= 1 && opt->step < (1LL << 31), "step=%lld", (long long)opt->step);
+  EG_CHECK_ARG(opt->lr >= 0.0 && opt->beta1 >= 0.0 && opt->beta1 < 1.0 && opt->beta2 >= 0.0 && opt->beta2 < 1.0 &&
+                   opt->eps >= 0.0,
+               "invalid Adam hyper-parameters");
+  rc = eg_descent_plan(rows, n_pos, heads, state, workspace, workspace_bytes_, stream);
+  if (rc != EG_OK) return rc;
+  return eg_descent_apply(d_out, d_out_f32, n_pos, heads, state, opt, base, workspace, workspace_bytes_, stream);
 }
 
 size_t eg_descent_step_noalloc_max_bytes(void) { return kStaticScratchBytes; }

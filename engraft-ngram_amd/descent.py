@@ -179,8 +179,30 @@ class DescentState:
                   _lib.ptr(dst_rows) if dst_rows is not None else None, ctypes.byref(tab),
                   _lib.stream_ptr(self.device))
 
-    def step(self, d_out: torch.Tensor, rows: torch.Tensor, *, lr: float, betas=(0.9, 0.999), eps: float = 1e-8,
-             dense: bool = False, mu: float = 0.0, frozen=None, no_alloc: bool = False) -> None:
+    def plan(self, rows: torch.Tensor, plan: "DescentPlan | None" = None) -> "DescentPlan":
+        """The slot grouping of a step over ``rows`` (int32 ``[n_pos, heads]``),
+        made now on the current stream (``eg_descent_plan``) for a later
+        ``step(..., plan=...)``.  It depends only on the row ids, which the hash
+        fixes from the tokens, so a loop can plan the next batch on a second
+        stream while the current step runs.  ``plan``: an earlier plan whose
+        buffer is reused (its step must have been issued, and ordered before
+        this call by the caller when the streams differ)."""
+        dev = self.device
+        rows = rows.to(device=dev, dtype=torch.int32).contiguous()
+        if rows.dim() != 2:
+            raise ValueError("rows must be [n_pos, heads]")
+        n_pos, heads = rows.shape
+        need = int(_lib.load().eg_backward_workspace_size(n_pos * heads, self.n))
+        ws = plan.workspace if plan is not None and plan.workspace.numel() >= need else \
+            torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+        st = self.c_state()
+        _lib.call("eg_descent_plan", _lib.ptr(rows), n_pos, heads, ctypes.byref(st), _lib.ptr(ws), ws.numel(),
+                  _lib.stream_ptr(dev))
+        return DescentPlan(self, rows, ws)
+
+    def step(self, d_out: torch.Tensor, rows: torch.Tensor | None = None, *, lr: float, betas=(0.9, 0.999),
+             eps: float = 1e-8, dense: bool = False, mu: float = 0.0, frozen=None, no_alloc: bool = False,
+             plan: "DescentPlan | None" = None) -> None:
         """One optimizer step from ``d_out`` (bf16/f32 ``[n_pos, heads*D]``) and the
         slots' row ids ``rows`` (int32 ``[n_pos, heads]``).  ``mu``: the pull
         term ``mu*||rows_var - rows0||^2/||rows0||^2`` (rows0 = the base table).
@@ -193,8 +215,23 @@ class DescentState:
 
         ``no_alloc``: the step's C call is ``eg_descent_step_noalloc``, which
         allocates nothing (its scratch is a static 16 MiB array per GPU; larger
-        steps raise ``EgError``)."""
+        steps raise ``EgError``).
+
+        ``plan``: the grouping made by ``plan(rows)`` of this state (``rows``
+        may then be omitted); the step is then ``eg_descent_apply`` on it,
+        bitwise the same as a step that groups the slots itself.  The caller
+        orders the plan's stream before this one."""
         dev = self.device
+        if plan is not None:
+            if plan.state is not self:
+                raise ValueError("the plan was made for another DescentState")
+            if frozen is not None or no_alloc:
+                raise ValueError("a planned step takes neither frozen rows nor no_alloc")
+            if rows is not None and (tuple(rows.shape) != tuple(plan.rows.shape)):
+                raise ValueError("rows differ in shape from the plan's")
+            rows = plan.rows
+        if rows is None:
+            raise ValueError("rows (or a plan) are required")
         rows = rows.to(device=dev, dtype=torch.int32).contiguous()
         n_pos, heads = rows.shape
         fidx = rows0_f = None
@@ -226,7 +263,13 @@ class DescentState:
             opt.l2_coef = float(np.float32(mu) / np.float32(self.rows0_sq))
             base = self.base.c_table
         st = self.c_state()
-        if no_alloc:
+        if plan is not None:
+            ws = plan.workspace
+            ws.record_stream(torch.cuda.current_stream(dev))  # freed only after this stream's use
+            _lib.call("eg_descent_apply", _lib.ptr(d_out), _dout_args(d_out), n_pos, heads, ctypes.byref(st),
+                      ctypes.byref(opt), ctypes.byref(base) if base is not None else None, _lib.ptr(ws), ws.numel(),
+                      _lib.stream_ptr(dev))
+        elif no_alloc:
             # eg_descent_step_noalloc: the grouping scratch is the library's
             # static per-GPU array (calls overlapping on one GPU race)
             _lib.call("eg_descent_step_noalloc", _lib.ptr(d_out), _dout_args(d_out), _lib.ptr(rows), n_pos, heads,
@@ -250,6 +293,17 @@ class DescentState:
         if quantized and self.quant is not None:
             return DeviceOverlay(self.ids, self.quant, ids_checked=True)
         return DeviceOverlay(self.ids, RowStore("f32", self.dim, self.master), ids_checked=True)
+
+
+class DescentPlan:
+    """The slot grouping of one descent step (``DescentState.plan``): the rows
+    it was made from and the device buffer holding it.  A buffer holds one plan;
+    ``DescentState.plan(rows, plan=this)`` regroups into it."""
+
+    def __init__(self, state: DescentState, rows: torch.Tensor, workspace: torch.Tensor):
+        self.state = state
+        self.rows = rows
+        self.workspace = workspace
 
 
 # ---------------------------------------------------------------------------------------------

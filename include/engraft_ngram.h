@@ -27,7 +27,7 @@
  *   eg_gather_slots  OverlayEmb.build's base gather + index_put
  *                                                    engraft/replica/seq.py:372-444
  *   eg_descent_step  scatter + torch.optim.Adam step on the overlay rows
- *                                                    engraft/descend_corpus.py:785-790,921-947
+ *   (= eg_descent_plan + eg_descent_apply)           engraft/descend_corpus.py:785-790,921-947
  *   eg_forward_decode  the per-token gather of a decode step with the overlay
  *                                                    engraft/replica/model.py:473-495
  *   eg_ple_gate, eg_ple_conv  ple_forward after its two projections
@@ -235,6 +235,24 @@ int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
 int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos,
                     int32_t heads, const eg_descent_state* state, const eg_adam* opt,
                     const eg_table* base, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The two halves of eg_descent_step, for a descent loop that groups the next
+ * step's slots while the current step runs (the grouping depends only on the
+ * row ids, which the hash fixes from the tokens: the reference's loop packs a
+ * whole pass before its first step, engraft/descend_corpus.py:855-870).
+ * eg_descent_plan groups the slots of rows int32 [n_pos, heads] by variable of
+ * `state` into `workspace` (eg_backward_workspace_size(n_pos*heads, state->n)
+ * bytes); eg_descent_apply is the rest of eg_descent_step (segmented reduce in
+ * slot order, Adam, requantisation) from a workspace holding the plan of the
+ * same n_pos, heads and state, made on the same stream or ordered before it by
+ * the caller.  A workspace holds one plan: it must not be planned into again
+ * before the apply that reads it has run.  plan + apply on one workspace is
+ * eg_descent_step, bitwise. */
+int eg_descent_plan(const int32_t* rows, int64_t n_pos, int32_t heads, const eg_descent_state* state,
+                    void* workspace, size_t workspace_bytes, void* stream);
+int eg_descent_apply(const void* d_out, int32_t d_out_f32, int64_t n_pos, int32_t heads,
+                     const eg_descent_state* state, const eg_adam* opt, const eg_table* base,
+                     const void* workspace, size_t workspace_bytes, void* stream);
 
 /* eg_descent_step without a workspace argument: it allocates nothing (no
  * hipMalloc, no library allocation).  No counterpart in the reference; it is

@@ -333,3 +333,55 @@ def test_descent_step_edge_cases(cuda):
     d = (torch.randn((256, 16 * 128), device=cuda) * 1e-3).to(torch.bfloat16)
     st.step(d, torch.full((256, 16), free, dtype=torch.int32), lr=1e-3)
     assert torch.equal(st.master, p0)
+
+
+def test_planned_steps_on_a_second_stream(cuda):
+    """A descent loop that groups the next batch's slots on a second stream
+    while the current step runs (DescentState.plan + step(plan=...), i.e.
+    eg_descent_plan + eg_descent_apply, two plan buffers alternating): every
+    step bitwise the step that groups its own slots, over batches whose rows
+    differ, and the plan's misuse refused."""
+    from engraft_ngram_amd import descent as D
+    _say("planned descent steps on a second stream")
+    spec = synthetic_spec(n_rows=16 * 4000, seed=81)
+    tab = G.device_table(spec, "q8_0", 16 * 4000, 128, seed=82)
+    batches = [synth.zipf_tokens(83 + k, 1024, 5000) for k in range(5)]
+    all_rows = [torch.from_numpy(H.ngram_rows_np(spec, b).astype(np.int32)).to(cuda) for b in batches]
+    union = torch.cat(all_rows)
+    ref = D.DescentState.from_rows(tab, union)
+    st = D.DescentState.from_rows(tab, union)
+    g = torch.Generator(device=cuda).manual_seed(84)
+    d_res = [(torch.randn((1024, 2048), generator=g, device=cuda) * 1e-3).to(torch.bfloat16) for _ in batches]
+    for d, r in zip(d_res, all_rows):
+        ref.step(d, r, lr=2e-3)
+    main = torch.cuda.current_stream(cuda)
+    side = torch.cuda.Stream(cuda)  # default priority
+    side.wait_stream(main)  # the row ids were made on the main stream
+    plans = [None, None]
+    planned = [torch.cuda.Event(), torch.cuda.Event()]
+    applied = [torch.cuda.Event(), torch.cuda.Event()]
+    plans[0] = st.plan(all_rows[0])
+    planned[0].record(main)
+    for i in range(len(batches)):
+        if i + 1 < len(batches):
+            j = (i + 1) % 2
+            with torch.cuda.stream(side):
+                if plans[j] is not None:
+                    side.wait_event(applied[j])  # the buffer's previous step has read it
+                plans[j] = st.plan(all_rows[i + 1], plan=plans[j])
+                planned[j].record(side)
+        main.wait_event(planned[i % 2])
+        st.step(d_res[i], plan=plans[i % 2], lr=2e-3)
+        applied[i % 2].record(main)
+    torch.cuda.synchronize()
+    assert st.step_count == ref.step_count == len(batches)
+    assert torch.equal(st.master, ref.master) and torch.equal(st.m, ref.m) and torch.equal(st.v, ref.v)
+    assert torch.equal(st.quant.payload, ref.quant.payload) and torch.equal(st.quant.scales, ref.quant.scales)
+    other = D.DescentState.from_rows(tab, union)
+    p = other.plan(all_rows[0])
+    with pytest.raises(ValueError):
+        st.step(d_res[0], plan=p, lr=2e-3)
+    with pytest.raises(ValueError):
+        other.step(d_res[0], all_rows[0][:512], plan=p, lr=2e-3)
+    with pytest.raises(ValueError):
+        other.step(d_res[0], plan=p, lr=2e-3, no_alloc=True)
