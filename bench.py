@@ -511,10 +511,12 @@ def bench_config4(steps: int, warmup: int) -> dict:
 def bench_real_format(steps: int, warmup: int) -> dict:
     """The reference's own table format (the f4 path, engraft/table.py:40-169):
     16 heads x 20,000,096 rows of 160 values in IQ4_NL blocks (90 B per row,
-    28.8 GB), the reference's hash mode (three multipliers shared by every head),
+    28.8 GB as the file holds them), the reference's hash mode (three multipliers shared by every head),
     16,384 Zipf tokens per step into a bf16 residual [16384, 2560]; 16 token
     batches and 4 residual sets rotate.  Rows: random nibbles, block scale
-    fp16(0.002)."""
+    fp16(0.002).  The rows sit in 128-byte lines of their own (PleTable's
+    default layout): one line per random row read.  Algorithmic bytes count
+    the 90 bytes of a row."""
     import numpy as np
     import torch
 
@@ -524,14 +526,14 @@ def bench_real_format(steps: int, warmup: int) -> dict:
     dev = torch.device("cuda", 0)
     per, heads, dim = 20_000_096, 16, 160
     n_rows, width = per * heads, heads * dim
-    store = T.RowStore.empty("iq4_nl", n_rows, dim, dev)
+    store = T.RowStore.empty("iq4_nl", n_rows, dim, dev, row_stride=T.RowStore.padded_stride("iq4_nl", dim))
     g = torch.Generator(device=dev).manual_seed(REAL_SEED)
     chunk = 1 << 26
     scale = np.array([0.002], dtype=np.float16).view(np.uint8)
     for r0 in range(0, n_rows, chunk):
         blk = store.payload[r0:r0 + chunk]
         blk.random_(0, 256, generator=g)
-        v = blk.view(-1, dim // 32, 18)
+        v = blk[:, :store.row_bytes].unflatten(1, (dim // 32, 18))
         v[:, :, 0] = int(scale[0])
         v[:, :, 1] = int(scale[1])
     mults = [int(m) for m in S.odd_multipliers(REAL_SEED, 3)]
@@ -565,7 +567,8 @@ def bench_real_format(steps: int, warmup: int) -> dict:
     gbs = nbytes / (us * 1e-6) / 1e9
     del tab, store
     torch.cuda.empty_cache()
-    return {"workload": "the reference's real table format: 16 heads x 20,000,096 IQ4_NL rows of 160 (90 B), "
+    return {"workload": "the reference's real table format: 16 heads x 20,000,096 IQ4_NL rows of 160 (90 B, each in "
+                        "a 128-byte line of its own), "
                         "shared multipliers, 16,384 Zipf tokens, residual width 2560",
             "us_per_launch": us, "rows_per_s": n_pos * heads / (us * 1e-6), "gb_per_s": gbs,
             "frac_of_hbm_peak": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": nbytes}

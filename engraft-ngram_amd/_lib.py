@@ -50,6 +50,7 @@ class EgTable(ctypes.Structure):
         ("n_rows", c_int64),
         ("payload", c_void_p),
         ("scales", c_void_p),
+        ("row_stride", c_int64),
     ]
 
 

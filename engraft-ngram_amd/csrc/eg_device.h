@@ -244,6 +244,7 @@ struct TableDev {
   int64_t n_rows;
   int32_t fmt;
   int32_t dim;
+  int64_t stride;  // IQ4_NL: bytes from one row to the next (its 18-byte blocks, or padded lines)
 };
 
 // Raw bytes of one chunk, loaded apart from their decoding so that a kernel can
@@ -272,7 +273,7 @@ __device__ inline RawChunk load_raw(const TableDev& t, int dim, int64_t row, int
     // 8 nibble bytes start at an even address q: the aligned 8 bytes at q & ~3
     // and the halfword at q + 6 hold them whatever q % 4 is, and no load reaches
     // past the block.
-    const uint8_t* blk = t.payload + row * (int64_t)((dim >> 5) * 18) + (off >> 5) * 18;
+    const uint8_t* blk = t.payload + row * t.stride + (off >> 5) * 18;
     r.s = *(const uint16_t*)blk;
     const uint8_t* q = blk + 2 + (off & 15);
     const uint32_t mis = (uint32_t)(uintptr_t)q & 3u;  // 0 or 2
@@ -366,7 +367,7 @@ __device__ inline float load_value_rt(const TableDev& t, int64_t row, int col) {
     case EG_FMT_MXFP8:
       return e4m3_to_f32(t.payload[row * t.dim + col]) * e8m0_to_f32(t.scales[row * nb + (col >> 5)]);
     case EG_FMT_IQ4_NL: {
-      const uint8_t* blk = t.payload + row * (int64_t)(nb * 18) + (col >> 5) * 18;
+      const uint8_t* blk = t.payload + row * t.stride + (col >> 5) * 18;
       const int j = col & 31;
       const uint32_t byte = blk[2 + (j & 15)];
       return iq4nl_value(j < 16 ? (byte & 15u) : (byte >> 4)) * f16_to_f32(*(const uint16_t*)blk);

@@ -68,6 +68,16 @@ int make_table(const eg_table* t, TableDev* out, const char* what) {
   out->n_rows = t->n_rows;
   out->fmt = t->fmt;
   out->dim = t->dim;
+  const int64_t own = t->fmt == EG_FMT_IQ4_NL ? (int64_t)(t->dim / 32) * 18 : 0;
+  if (t->fmt == EG_FMT_IQ4_NL) {
+    EG_CHECK_ARG(t->row_stride == 0 || (t->row_stride >= own && t->row_stride % 2 == 0),
+                 "%s: row_stride=%lld (IQ4_NL: 0, or an even count >= %lld)", what, (long long)t->row_stride,
+                 (long long)own);
+  } else {
+    EG_CHECK_ARG(t->row_stride == 0, "%s: row_stride=%lld (format %d takes 0)", what, (long long)t->row_stride,
+                 t->fmt);
+  }
+  out->stride = t->row_stride ? t->row_stride : own;
   return EG_OK;
 }
 

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define EG_ABI_VERSION 1
+#define EG_ABI_VERSION 2
 
 #define EG_MAX_NGRAM 4   /* context slots per hash (2-, 3- and 4-grams) */
 #define EG_MAX_HEADS 32  /* row slots per position and table layer */
@@ -92,6 +92,10 @@ typedef struct eg_table {
   int64_t n_rows;
   const void* payload;  /* device */
   const void* scales;   /* device; Q8_0 and MXFP8 only, NULL otherwise */
+  int64_t row_stride;   /* bytes from one row of payload to the next; 0: the
+                           format's own row size.  IQ4_NL may take more (rows
+                           padded to whole 128-byte lines, so that a random row
+                           read is one line); every other format 0 */
 } eg_table;
 
 /* Replacement rows resolved per id (engraft/replica/model.py:473-495):

@@ -550,3 +550,55 @@ def test_forward_on_two_streams(cuda):
     torch.cuda.synchronize(cuda)
     for k in range(2):
         assert torch.equal(got[k], exp[k])
+
+
+def test_iq4nl_rows_in_padded_lines(cuda, tmp_path):
+    """IQ4_NL rows each in a 128-byte line (PleTable's default): the forward,
+    the gather, the raw and dequantised row reads and the hash match the same
+    table in its packed 90-byte rows bit for bit; the C boundary refuses a
+    stride for another format or an odd one."""
+    import ctypes
+
+    from engraft_ngram_amd import _lib
+    from engraft_ngram_amd import table as T
+    from tests.gguf_util import ple_table_file
+    spec = fake_table_spec(7, head_vocab_size=400)
+    assert list(spec.head_offsets) == [400 * h for h in range(16)]
+    rng = np.random.default_rng(2)
+    raw = []
+    for h in range(16):
+        r = rng.integers(0, 256, size=(400, 90), dtype=np.uint8)
+        for b in range(5):
+            r[:, 18 * b:18 * b + 2] = np.frombuffer(
+                (rng.standard_normal(400) * 1e-3).astype(np.float16).tobytes(), np.uint8).reshape(400, 2)
+        raw.append(r)
+    ple_table_file(tmp_path / "ple.gguf", spec, raw)
+    padded = T.PleTable(tmp_path / "ple.gguf")
+    packed = T.PleTable(tmp_path / "ple.gguf", pad_rows=False, chunk_bytes=90 * 7)
+    assert padded.store.row_stride == 128 and tuple(padded.store.payload.shape)[1] == 128
+    assert packed.store.row_stride == 0 and tuple(packed.store.payload.shape)[1] == 90
+    for h in (0, 9, 15):
+        assert np.array_equal(padded.read_rows_raw(h, 3, 100), raw[h][3:103])
+        assert np.array_equal(packed.read_rows_raw(h, 3, 100), raw[h][3:103])
+        assert np.array_equal(padded.read_rows(h, 3, 100), packed.read_rows(h, 3, 100))
+    tokens = synth.zipf_tokens(3, 4096, 6000)
+    res = G.residual(tokens.size, 16 * 160, seed=4)
+    a = padded.forward(torch.from_numpy(tokens), res, seq_len=1024)
+    b = packed.forward(torch.from_numpy(tokens), res, seq_len=1024)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    rows = padded.rows(torch.from_numpy(tokens), seq_len=1024)
+    assert torch.equal(padded.gather(rows), packed.gather(rows))
+    fetch = lambda ids: G.F.dequant_iq4nl(np.concatenate(raw)[np.asarray(ids).reshape(-1)])  # noqa: E731
+    _, _, exp = FW.forward(spec, tokens[:512], fetch, G.bf16_bits(res[:512]), seq_len=1024)
+    G.assert_out_matches(G.bf16_bits(a[:512]), exp)
+    # the boundary's checks (host side, before any launch)
+    q8 = T.RowStore.empty("q8_0", 16, 128, cuda).c_table()
+    q8.row_stride = 256
+    out = torch.empty((1, 128), dtype=torch.float32, device=cuda)
+    one = torch.zeros((1, 1), dtype=torch.int32, device=cuda)
+    rc = _lib.load().eg_gather(ctypes.byref(q8), None, _lib.ptr(one), 1, 1, _lib.ptr(out), _lib.stream_ptr(cuda))
+    assert rc == _lib.EG_ERR_ARG
+    odd = padded.store.c_table()
+    odd.row_stride = 127
+    rc = _lib.load().eg_gather(ctypes.byref(odd), None, _lib.ptr(one), 1, 1, _lib.ptr(out), _lib.stream_ptr(cuda))
+    assert rc == _lib.EG_ERR_ARG

@@ -237,3 +237,30 @@ def test_gguf_ple_weights_reader(tmp_path):
     GU.write_gguf(tmp_path / "m-00001-of-00002.gguf", [("general.architecture", GU.STRING, "qwen4exp")], [])
     with pytest.raises(KeyError):
         ggufio.read_rms_eps(path)
+
+
+def test_rowstore_padded_iq4nl_rows():
+    """IQ4_NL rows in 128-byte lines: the payload's wider rows are accepted
+    (even strides only), the C table carries the stride, raw rows drop the
+    padding, and no other format takes a stride."""
+    import torch
+
+    from engraft_ngram_amd import table as T
+    assert T.RowStore.padded_stride("iq4_nl", 160) == 128
+    assert T.RowStore.padded_stride("iq4_nl", 256) == 256  # 144 bytes -> two lines
+    assert T.RowStore.padded_stride("q8_0", 128) == 128
+    st = T.RowStore.empty("iq4_nl", 6, 160, "cpu", row_stride=128)
+    assert tuple(st.payload.shape) == (6, 128) and st.row_bytes == 90 and st.row_stride == 128
+    assert st.c_table().row_stride == 128
+    rng = np.random.default_rng(5)
+    st.payload.copy_(torch.from_numpy(rng.integers(0, 256, size=(6, 128), dtype=np.uint8)))
+    got = st.raw_rows(torch.tensor([4, 1]))
+    assert got.shape == (2, 90) and np.array_equal(got, st.payload.numpy()[[4, 1], :90])
+    plain = T.RowStore.empty("iq4_nl", 6, 160, "cpu")
+    assert plain.row_stride == 0 and plain.c_table().row_stride == 0 and plain.row_bytes == 90
+    with pytest.raises(ValueError):
+        T.RowStore("iq4_nl", 160, torch.zeros((6, 127), dtype=torch.uint8))
+    with pytest.raises(ValueError):
+        T.RowStore("iq4_nl", 160, torch.zeros((6, 88), dtype=torch.uint8))
+    with pytest.raises(ValueError):
+        T.RowStore.empty("q8_0", 6, 128, "cpu", row_stride=256)
