@@ -313,8 +313,38 @@ def bench_backward(tab, tokens, steps: int, warmup: int, cpu_s: float = 0.0) -> 
     ms = a.elapsed_time(b) / steps
     nb = backward_bytes(rows.shape[0], state.n)
     gbs = nb / (ms * 1e-3) / 1e9
+    # the same step from the slots' variables, as the forward over the state's
+    # overlay writes them (eg_forward_slots; OverlayEmb's idx_r): no row lookup
+    from engraft_ngram_amd import table as T
+    fwd = T.PreparedForward([tab], tokens, None, overlays=[state.overlay()], seq_len=SEQ, return_slot_vars=True)
+    fwd()
+    sv = fwd.slot_vars[0]
+    del fwd
+    rot = itertools.count()
+    ramp(lambda: state.step(d_res[next(rot) % RES_SETS], slot_var=sv, lr=1e-3), 0.3)
+    a.record()
+    for i in range(steps):
+        state.step(d_res[i % RES_SETS], slot_var=sv, lr=1e-3)
+    b.record()
+    torch.cuda.synchronize()
+    ms_sv = a.elapsed_time(b) / steps
+    s1 = D.DescentState(state.ids, state.master.clone(), base=state.base)
+    s2 = D.DescentState(state.ids, state.master.clone(), base=state.base)
+    for i in range(2):
+        s1.step(d_res[i], slot_var=sv, lr=1e-3)
+        s2.step(d_res[i], rows, lr=1e-3)
+    torch.cuda.synchronize()
+    sv_same = bool(torch.equal(s1.master, s2.master) and torch.equal(s1.m, s2.m) and torch.equal(s1.v, s2.v)
+                   and torch.equal(s1.quant.payload, s2.quant.payload))
+    del s1, s2
     out = {"us_per_step": ms * 1e3, "touched_rows": state.n, "slot_gradients": rows.numel(),
            "algorithmic_bytes_per_step": nb, "gb_per_s": gbs, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
+           "us_per_step_from_slot_vars": ms_sv * 1e3,
+           "frac_of_hbm_peak_from_slot_vars": nb / (ms_sv * 1e-3) / 1e9 / HBM_PEAK_GBS,
+           "slot_vars_step_matches_rows_step": sv_same,
+           "from_slot_vars": "the same step with each slot's variable given (what the forward over the state's "
+                             "overlay writes, eg_forward_slots; the reference's OverlayEmb backward scatters by "
+                             "these idx_r): the grouping needs no row lookup (eg_descent_plan_slots)",
            "rows_per_s": rows.numel() / (ms * 1e-3),
            "workload": "BASELINE config 2: scatter (CSR grouping + slot-ordered segmented reduce) + sparse Adam + "
                        "Q8_0 requant, fp32 master/m/v kept"}
@@ -1005,7 +1035,10 @@ def main() -> None:
         result["backward"] = bw
         log_cpu_leg("backward", bw)
         log(f"backward: {bw['us_per_step']:.1f} us/step, {bw['touched_rows']} touched rows, "
-            f"{bw['gb_per_s']:.0f} GB/s algorithmic ({100 * bw['frac_of_hbm_peak']:.1f}% of peak)")
+            f"{bw['gb_per_s']:.0f} GB/s algorithmic ({100 * bw['frac_of_hbm_peak']:.1f}% of peak); from the "
+            f"forward's slot variables {bw['us_per_step_from_slot_vars']:.1f} us/step "
+            f"({100 * bw['frac_of_hbm_peak_from_slot_vars']:.1f}% of peak, same bits: "
+            f"{bw['slot_vars_step_matches_rows_step']})")
 
     if not args.no_extra:
         dc = bench_decode(tab, 200)

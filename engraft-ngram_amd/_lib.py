@@ -127,6 +127,8 @@ SIGNATURES = {
                                c_void_p]),
     "eg_forward": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,
                              c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "eg_forward_slots": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,
+                                   c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_forward_rows": (c_int32, [c_int32, POINTER(EgTable), POINTER(EgOverlay), c_void_p, c_int64, c_int32,
                                   c_void_p, c_void_p, c_void_p]),
     "eg_stream_copy": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p]),
@@ -171,6 +173,8 @@ SIGNATURES = {
                                   c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     "eg_descent_step": (c_int32, [c_void_p, c_int32, c_void_p, c_int64, c_int32, POINTER(EgDescentState),
                                   POINTER(EgAdam), POINTER(EgTable), c_void_p, ctypes.c_size_t, c_void_p]),
+    "eg_descent_plan_slots": (c_int32, [c_void_p, c_int64, c_int32, POINTER(EgDescentState), c_void_p,
+                                        ctypes.c_size_t, c_void_p]),
     "eg_descent_plan": (c_int32, [c_void_p, c_int64, c_int32, POINTER(EgDescentState), c_void_p, ctypes.c_size_t,
                                   c_void_p]),
     "eg_descent_apply": (c_int32, [c_void_p, c_int32, c_int64, c_int32, POINTER(EgDescentState), POINTER(EgAdam),

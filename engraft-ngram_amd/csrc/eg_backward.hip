@@ -1227,6 +1227,21 @@ int eg_descent_plan(const int32_t* rows, int64_t n_pos, int32_t heads, const eg_
                      (hipStream_t)stream);
 }
 
+int eg_descent_plan_slots(const int32_t* slot_var, int64_t n_pos, int32_t heads, const eg_descent_state* state,
+                          void* workspace, size_t workspace_bytes_, void* stream) {
+  int rc = check_state(state);
+  if (rc != EG_OK) return rc;
+  rc = check_common(nullptr, false, slot_var, true, n_pos, heads, state->dim, state->ids, state->n, workspace,
+                    workspace_bytes_);
+  if (rc != EG_OK) return rc;
+  const int64_t n = n_pos * heads;
+  if (state->n == 0 || n == 0) return EG_OK;
+  Workspace w;
+  carve(workspace, n, state->n, &w);
+  // the slots' variables are given: no row lookup (values outside [0, n) hit no variable)
+  return group_slots(slot_var, n, state->ids, state->n, nullptr, 0, true, w, (hipStream_t)stream);
+}
+
 int eg_descent_apply(const void* d_out, int32_t d_out_f32, int64_t n_pos, int32_t heads,
                      const eg_descent_state* state, const eg_adam* opt, const eg_table* base, const void* workspace,
                      size_t workspace_bytes_, void* stream) {

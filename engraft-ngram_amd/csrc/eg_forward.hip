@@ -175,6 +175,7 @@ struct FwdArgs {
   const uint16_t* residual; // bf16 [n_pos, W] or nullptr
   void* out;
   int32_t* rows_out;
+  int32_t* vars_out;        // overlay row each slot read (-1: base table); overlay kernels only
   int64_t seq_len;
   int64_t n_pos;
   int32_t n_layers;
@@ -287,6 +288,7 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
   //    costs one wasted load.
   RawChunk tr[MAXL][NCH];
   RawChunk orow[OVL ? MAXL : 1][OVL ? NCH : 1];
+  int32_t ovk_keep[OVL ? MAXL : 1];
   uint32_t src[MAXL][NCH];  // 0: base table, 1: overlay, 2: invalid id
 #pragma unroll
   for (int l = 0; l < MAXL; ++l) {
@@ -304,12 +306,14 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
     if constexpr (OVL) {
       int32_t ovk = -1;
       const OverlayDev& ov = a.ov[l];
+      ovk_keep[l] = -1;
       if (a.slot_var != nullptr) {
         ovk = a.slot_var[p * H + hh];
       } else if (ov.n > 0) {
         const int64_t k = ov.bitmap ? bitmap_find(ov.bitmap, ov.n_bits, rid[l]) : sorted_find(ov.ids, ov.n, rid[l]);
         if (k >= 0) ovk = ov.index ? ov.index[k] : (int32_t)k;
       }
+      ovk_keep[l] = ovk;
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         const int e0 = cb + (lane + 64 * c) * 8;
@@ -332,6 +336,13 @@ __global__ __launch_bounds__(256) void forward_kernel(const FwdArgs a) {
 #pragma unroll
     for (int l = 0; l < MAXL; ++l)
       if (l < nl) a.rows_out[((int64_t)l * a.n_pos + p) * H + hh] = rid[l];
+  }
+  if constexpr (OVL) {
+    if (a.vars_out != nullptr && own_head && hh * dim >= cb) {
+#pragma unroll
+      for (int l = 0; l < MAXL; ++l)
+        if (l < nl) a.vars_out[((int64_t)l * a.n_pos + p) * H + hh] = ovk_keep[l];
+    }
   }
 
   // 5. Residual + every layer, fp32, in layer order.
@@ -458,7 +469,7 @@ static void launch_generic(const FwdArgs& a, hipStream_t st) {
 template <bool F32OUT, bool ROWS>
 static int launch_forward_as(const FwdArgs& a, hipStream_t st) {
   if (a.n_pos == 0) return EG_OK;
-  bool ovl = a.slot_var != nullptr;
+  bool ovl = a.slot_var != nullptr || a.vars_out != nullptr;
   for (int l = 0; l < a.n_layers; ++l) ovl = ovl || a.ov[l].n > 0;
   const int fmt = a.table[0].fmt;
   if (!F32OUT) {
@@ -627,7 +638,7 @@ int eg_hash_rows(const eg_hash_spec* spec, const int64_t* tokens, int64_t n_pos,
 static int forward_entry(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,
                          const eg_overlay* overlays, const int64_t* tokens, int64_t n_pos, int64_t seq_len,
                          const int32_t* seg_start, int32_t decode_ctx, const uint16_t* residual, void* out,
-                         int32_t* rows_out, void* stream) {
+                         int32_t* rows_out, int32_t* vars_out, void* stream) {
   EG_CHECK_ARG(n_layers >= 1 && n_layers <= EG_MAX_LAYERS, "n_layers=%d outside [1, %d]", n_layers,
                EG_MAX_LAYERS);
   EG_CHECK_ARG(decode_ctx >= 0, "decode_ctx < 0");
@@ -656,6 +667,7 @@ static int forward_entry(int32_t n_layers, const eg_hash_spec* specs, const eg_t
   a.residual = residual;
   a.out = out;
   a.rows_out = rows_out;
+  a.vars_out = vars_out;
   a.seq_len = seq_len;
   a.n_pos = n_pos;
   a.n_layers = n_layers;
@@ -671,7 +683,16 @@ int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tabl
                const int64_t* tokens, int64_t n_pos, int64_t seq_len, const int32_t* seg_start,
                const uint16_t* residual, void* out, int32_t* rows_out, void* stream) {
   return forward_entry(n_layers, specs, tables, overlays, tokens, n_pos, seq_len, seg_start, 0, residual, out,
-                       rows_out, stream);
+                       rows_out, nullptr, stream);
+}
+
+int eg_forward_slots(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,
+                     const eg_overlay* overlays, const int64_t* tokens, int64_t n_pos, int64_t seq_len,
+                     const int32_t* seg_start, const uint16_t* residual, void* out, int32_t* rows_out,
+                     int32_t* slot_var_out, void* stream) {
+  EG_CHECK_ARG(slot_var_out != nullptr, "slot_var_out is NULL");
+  return forward_entry(n_layers, specs, tables, overlays, tokens, n_pos, seq_len, seg_start, 0, residual, out,
+                       rows_out, slot_var_out, stream);
 }
 
 int eg_forward_decode(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,
@@ -679,7 +700,7 @@ int eg_forward_decode(int32_t n_layers, const eg_hash_spec* specs, const eg_tabl
                       const uint16_t* residual, void* out, int32_t* rows_out, void* stream) {
   EG_CHECK_ARG(ctx_len >= 1, "ctx_len=%d < 1", ctx_len);
   return forward_entry(n_layers, specs, tables, overlays, tokens, n_seq, 0, nullptr, ctx_len, residual, out,
-                       rows_out, stream);
+                       rows_out, nullptr, stream);
 }
 
 int eg_forward_timed(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,

@@ -179,30 +179,39 @@ class DescentState:
                   _lib.ptr(dst_rows) if dst_rows is not None else None, ctypes.byref(tab),
                   _lib.stream_ptr(self.device))
 
-    def plan(self, rows: torch.Tensor, plan: "DescentPlan | None" = None) -> "DescentPlan":
+    def plan(self, rows: torch.Tensor | None = None, plan: "DescentPlan | None" = None, *,
+             slot_var: torch.Tensor | None = None) -> "DescentPlan":
         """The slot grouping of a step over ``rows`` (int32 ``[n_pos, heads]``),
         made now on the current stream (``eg_descent_plan``) for a later
         ``step(..., plan=...)``.  It depends only on the row ids, which the hash
         fixes from the tokens, so a loop can plan the next batch on a second
         stream while the current step runs.  ``plan``: an earlier plan whose
         buffer is reused (its step must have been issued, and ordered before
-        this call by the caller when the streams differ)."""
+        this call by the caller when the streams differ).
+
+        ``slot_var`` in place of ``rows``: each slot's variable (a row of
+        ``ids``; any other value for none), as ``PreparedForward(...,
+        return_slot_vars=True)`` writes them for ``self.overlay()`` -- the
+        grouping then needs no row lookup (``eg_descent_plan_slots``)."""
         dev = self.device
-        rows = rows.to(device=dev, dtype=torch.int32).contiguous()
+        if (rows is None) == (slot_var is None):
+            raise ValueError("give rows or slot_var")
+        direct = slot_var is not None
+        rows = (slot_var if direct else rows).to(device=dev, dtype=torch.int32).contiguous()
         if rows.dim() != 2:
-            raise ValueError("rows must be [n_pos, heads]")
+            raise ValueError("rows / slot_var must be [n_pos, heads]")
         n_pos, heads = rows.shape
         need = int(_lib.load().eg_backward_workspace_size(n_pos * heads, self.n))
         ws = plan.workspace if plan is not None and plan.workspace.numel() >= need else \
             torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
         st = self.c_state()
-        _lib.call("eg_descent_plan", _lib.ptr(rows), n_pos, heads, ctypes.byref(st), _lib.ptr(ws), ws.numel(),
-                  _lib.stream_ptr(dev))
+        _lib.call("eg_descent_plan_slots" if direct else "eg_descent_plan", _lib.ptr(rows), n_pos, heads,
+                  ctypes.byref(st), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
         return DescentPlan(self, rows, ws)
 
     def step(self, d_out: torch.Tensor, rows: torch.Tensor | None = None, *, lr: float, betas=(0.9, 0.999),
              eps: float = 1e-8, dense: bool = False, mu: float = 0.0, frozen=None, no_alloc: bool = False,
-             plan: "DescentPlan | None" = None) -> None:
+             plan: "DescentPlan | None" = None, slot_var: torch.Tensor | None = None) -> None:
         """One optimizer step from ``d_out`` (bf16/f32 ``[n_pos, heads*D]``) and the
         slots' row ids ``rows`` (int32 ``[n_pos, heads]``).  ``mu``: the pull
         term ``mu*||rows_var - rows0||^2/||rows0||^2`` (rows0 = the base table).
@@ -220,8 +229,15 @@ class DescentState:
         ``plan``: the grouping made by ``plan(rows)`` of this state (``rows``
         may then be omitted); the step is then ``eg_descent_apply`` on it,
         bitwise the same as a step that groups the slots itself.  The caller
-        orders the plan's stream before this one."""
+        orders the plan's stream before this one.
+
+        ``slot_var`` in place of ``rows``: the slots' variables (see ``plan``);
+        the step groups them without a row lookup."""
         dev = self.device
+        if slot_var is not None:
+            if rows is not None or plan is not None or frozen is not None or no_alloc:
+                raise ValueError("slot_var takes neither rows, a plan, frozen rows nor no_alloc")
+            plan = self.plan(slot_var=slot_var)
         if plan is not None:
             if plan.state is not self:
                 raise ValueError("the plan was made for another DescentState")

@@ -427,7 +427,7 @@ class PreparedForward:
 
     def __init__(self, tables: list[DeviceTable], tokens, residual: torch.Tensor | None = None, *,
                  out: torch.Tensor | None = None, overlays=None, seq_len: int | None = None, seg_start=None,
-                 return_rows: bool = False, decode_ctx: int | None = None):
+                 return_rows: bool = False, decode_ctx: int | None = None, return_slot_vars: bool = False):
         if not 1 <= len(tables) <= _lib.EG_MAX_LAYERS:
             raise ValueError(f"{len(tables)} table layers (1..{_lib.EG_MAX_LAYERS} supported)")
         t0 = tables[0]
@@ -463,9 +463,20 @@ class PreparedForward:
             self._ovs = (_lib.EgOverlay * nl)(*[(o.c_overlay() if o is not None else _lib.EgOverlay())
                                                 for o in overlays])
         self.rows = torch.empty((nl, n, t0.n_heads), dtype=torch.int32, device=dev) if return_rows else None
+        # return_slot_vars: the overlay row each slot read (-1: base table), eg_forward_slots
+        self.slot_vars = None
+        if return_slot_vars:
+            if decode_ctx is not None:
+                raise ValueError("slot variables are written by eg_forward_slots, not the decode step")
+            self.slot_vars = torch.empty((nl, n, t0.n_heads), dtype=torch.int32, device=dev)
         self.out = out
         self._keep = (tables, tok, residual, seg)
-        if decode_ctx is None:
+        if self.slot_vars is not None:
+            self._fn = _lib.load().eg_forward_slots
+            self._args = (nl, self._specs, self._ctabs, self._ovs, _lib.ptr(tok), n, int(seq_len or 0),
+                          _lib.ptr(seg), _lib.ptr(residual), _lib.ptr(out), _lib.ptr(self.rows),
+                          _lib.ptr(self.slot_vars))
+        elif decode_ctx is None:
             self._fn = _lib.load().eg_forward
             self._args = (nl, self._specs, self._ctabs, self._ovs, _lib.ptr(tok), n, int(seq_len or 0),
                           _lib.ptr(seg), _lib.ptr(residual), _lib.ptr(out), _lib.ptr(self.rows))
@@ -486,7 +497,7 @@ class PreparedForward:
     def timed(self, start_event: int, stop_event: int, stream: int | None = None) -> None:
         """The same launch through ``eg_forward_timed``: the two hipEvent_t
         handles receive the kernel dispatch's own start / end timestamps."""
-        if self._decode:
+        if self._decode or self.slot_vars is not None:
             raise ValueError("timed launches are for eg_forward")
         st = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
         rc = _lib.load().eg_forward_timed(*self._args, start_event, stop_event, st)

@@ -136,6 +136,18 @@ int eg_forward(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tabl
                int64_t seq_len, const int32_t* seg_start, const uint16_t* residual,
                void* out, int32_t* rows_out, void* stream);
 
+/* eg_forward that also writes, per slot, the overlay row it read:
+ * slot_var_out int32 [n_layers, n_pos, n_heads], the row of overlays[l]'s store
+ * (its index entry, or the rank of the id among overlays[l].ids when index is
+ * NULL), -1 where the slot read the base table.  Over a descent state's
+ * overlay (ids = the variables, no index) these are the slots' variables, the
+ * idx_r of the reference's OverlayEmb (engraft/replica/seq.py:401-441), which
+ * eg_descent_plan_slots groups without a row lookup. */
+int eg_forward_slots(int32_t n_layers, const eg_hash_spec* specs, const eg_table* tables,
+                     const eg_overlay* overlays, const int64_t* tokens, int64_t n_pos,
+                     int64_t seq_len, const int32_t* seg_start, const uint16_t* residual,
+                     void* out, int32_t* rows_out, int32_t* slot_var_out, void* stream);
+
 /* Decode step: one new position per sequence.  tokens int64 [n_seq, ctx_len]
  * holds each sequence's last ctx_len tokens (the new one last; the hash never
  * looks before the first); residual / out / rows_out as eg_forward with
@@ -254,6 +266,15 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
  * eg_descent_step, bitwise. */
 int eg_descent_plan(const int32_t* rows, int64_t n_pos, int32_t heads, const eg_descent_state* state,
                     void* workspace, size_t workspace_bytes, void* stream);
+/* eg_descent_plan from the slots' variables instead of their rows: slot_var
+ * int32 [n_pos, heads], the variable (row of state->ids) each slot read, any
+ * value outside [0, state->n) for none -- what eg_forward_slots writes for the
+ * state's overlay.  The reference's backward scatters by the forward's
+ * variable indices the same way (engraft/replica/seq.py:433-441, the autograd
+ * of index_put by idx_r); no row lookup is needed. */
+int eg_descent_plan_slots(const int32_t* slot_var, int64_t n_pos, int32_t heads,
+                          const eg_descent_state* state, void* workspace, size_t workspace_bytes,
+                          void* stream);
 int eg_descent_apply(const void* d_out, int32_t d_out_f32, int64_t n_pos, int32_t heads,
                      const eg_descent_state* state, const eg_adam* opt, const eg_table* base,
                      const void* workspace, size_t workspace_bytes, void* stream);

@@ -385,3 +385,43 @@ def test_planned_steps_on_a_second_stream(cuda):
         other.step(d_res[0], all_rows[0][:512], plan=p, lr=2e-3)
     with pytest.raises(ValueError):
         other.step(d_res[0], plan=p, lr=2e-3, no_alloc=True)
+
+
+def test_descent_from_the_forwards_slot_variables(cuda):
+    """The forward over the state's overlay writes each slot's variable
+    (eg_forward_slots: the rank of its row among the ids, -1 for base rows,
+    as the oracle's binary search finds it); the step grouped from those
+    (eg_descent_plan_slots, no row lookup) is bitwise the step from the rows,
+    including slots that hit no variable."""
+    from engraft_ngram_amd import descent as D
+    from engraft_ngram_amd import table as T
+    _say("descent from the forward's slot variables")
+    spec = synthetic_spec(n_rows=16 * 4000, seed=91)
+    tab = G.device_table(spec, "q8_0", 16 * 4000, 128, seed=92)
+    tokens = synth.zipf_tokens(93, 4096, 5000)
+    rows_np = H.ngram_rows_np(spec, tokens, seq_len=1024).astype(np.int32)
+    # variables: the rows of the first half of the batch only, so the second half has misses
+    st = D.DescentState.from_rows(tab, torch.from_numpy(rows_np[:2048]))
+    ref = D.DescentState.from_rows(tab, torch.from_numpy(rows_np[:2048]))
+    ids = st.ids.cpu().numpy()
+    res = G.residual(tokens.size, 2048, seed=94)
+    call = T.PreparedForward([tab], torch.from_numpy(tokens), res, overlays=[st.overlay()], seq_len=1024,
+                             return_rows=True, return_slot_vars=True)
+    call()
+    torch.cuda.synchronize()
+    sv = call.slot_vars[0].cpu().numpy()
+    assert np.array_equal(call.rows[0].cpu().numpy(), rows_np)
+    pos = np.searchsorted(ids, rows_np)
+    hit = (pos < ids.size) & (ids[np.minimum(pos, ids.size - 1)] == rows_np)
+    exp = np.where(hit, pos, -1)
+    assert np.array_equal(sv, exp) and (sv == -1).any() and (sv >= 0).any()
+    g = torch.Generator(device=cuda).manual_seed(95)
+    for k in range(2):
+        d = (torch.randn((4096, 2048), generator=g, device=cuda) * 1e-3).to(torch.bfloat16)
+        st.step(d, slot_var=call.slot_vars[0], lr=1e-3)
+        ref.step(d, torch.from_numpy(rows_np), lr=1e-3)
+    torch.cuda.synchronize()
+    assert torch.equal(st.master, ref.master) and torch.equal(st.m, ref.m) and torch.equal(st.v, ref.v)
+    assert torch.equal(st.quant.payload, ref.quant.payload) and torch.equal(st.quant.scales, ref.quant.scales)
+    with pytest.raises(ValueError):
+        st.step(d, torch.from_numpy(rows_np), slot_var=call.slot_vars[0], lr=1e-3)
