@@ -766,10 +766,12 @@ __device__ inline void finish(const SegArgs& a, int64_t k, int sub, const float 
   }
 }
 
-// 32-lane ascending sort of one value per lane (bitonic, one-direction form).
-__device__ inline uint32_t sort32(uint32_t v, int sub) {
-#pragma unroll
-  for (int k = 2; k <= 32; k <<= 1) {
+// Ascending sort of one value per lane over the first `span` lanes of each
+// 32-lane group (bitonic, one-direction form; span a wavefront-uniform power
+// of two in [1, 32]; the lanes from span on already hold the largest values
+// and stay in place).
+__device__ inline uint32_t sort32(uint32_t v, int sub, int span = 32) {
+  for (int k = 2; k <= span; k <<= 1) {
     {
       const uint32_t o = (uint32_t)__shfl_xor((int)v, k - 1, 32);
       v = (sub < (sub ^ (k - 1))) ? min(v, o) : max(v, o);
@@ -865,11 +867,23 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
   }
   const int cnt = (int)len;
   const uint32_t sl = a.slots[lo + min(sub, cnt - 1)];  // every lane loads (no divergent load)
-  const uint32_t vl = sort32(sub < cnt ? sl : 0xffffffffu, sub);
+  // the network only as wide as the longest of the wavefront's two ranges needs
+  // (most ranges hold one or two slots); lanes past a range hold 0xffffffff
+  // (the other group's count is read from its lanes; a group that has already
+  // returned leaves an arbitrary value there, which only widens the network)
+  const int other = __shfl_xor(cnt, 32);
+  const int cmax = max(cnt, (other >= 1 && other <= kPiece) ? other : 1);
+  const int span = cmax <= 1 ? 1 : 1 << (32 - __clz(cmax - 1));
+  const uint32_t vl = sort32(sub < cnt ? sl : 0xffffffffu, sub, __builtin_amdgcn_readfirstlane(span));
   float g[VPL];
 #pragma unroll
   for (int t = 0; t < VPL; ++t) g[t] = 0.0f;
-  sum_piece<VPL, CONSEC, 4, F32>(a, vl, gbase, cnt, sub, g);
+  // loads go out as many slots at a time as the wavefront's longer range has,
+  // up to four (a batch re-reads its first slot past the range's end)
+  const int cw = __builtin_amdgcn_readfirstlane(cmax);
+  if (cw == 1) sum_piece<VPL, CONSEC, 1, F32>(a, vl, gbase, cnt, sub, g);
+  else if (cw == 2) sum_piece<VPL, CONSEC, 2, F32>(a, vl, gbase, cnt, sub, g);
+  else sum_piece<VPL, CONSEC, 4, F32>(a, vl, gbase, cnt, sub, g);
   finish<VPL, CONSEC, ADAM>(a, k, sub, g, p, m, v);
 }
 
