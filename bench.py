@@ -705,8 +705,10 @@ def bench_overlay_emb(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     config-1 table, 14,032 of its rows as fp32 variables (the size of the
     reference's Quail s0b overlay, docs/formats.md:120-124); a step is build()
     (the cached plan's gather with the variables substituted) plus the backward
-    into the variables.  CPU: the reference's step with the plan cached (torch
-    index_put into the base rows + autograd backward) on every host thread."""
+    of a given upstream gradient into the variables (what the model's backward
+    hands the embedding).  CPU: the reference's step with the plan cached
+    (torch index_put into the base rows + autograd backward of the same
+    gradient) on every host thread."""
 
     import numpy as np
     import torch
@@ -728,8 +730,7 @@ def bench_overlay_emb(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
 
     def step():
         rv.grad = None
-        emb = oe.build(t_len)
-        (emb.float() * g).sum().backward()
+        oe.build(t_len).backward(g)
 
     step()  # plans the sequence once, as the reference's overlay_cache does
     for _ in range(20):
@@ -762,8 +763,7 @@ def bench_overlay_emb(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
 
         def cpu_step():
             rv_c.grad = None
-            emb = base.index_put((it_t, ih_t), rv_c[ir_t])
-            (emb * g_c).sum().backward()
+            base.index_put((it_t, ih_t), rv_c[ir_t]).backward(g_c)
 
         cpu_step()
         step()

@@ -456,10 +456,12 @@ __device__ inline void f32_tile(const F32Args& args, const Work& w, float* ldsf)
       const int64_t kt = kv - seg0;
       wait_vm0();
       __builtin_amdgcn_s_barrier();
-      if (kv + 1 < hi) issue(kt + 1);
       const float* st = ldsf + (kt & 1) * STAGE;
       // two halves of the step's 16 k a lane half owns: 8 k (two chunks) of
-      // each fragment in registers at a time
+      // each fragment in registers at a time.  The next step's loads go out
+      // after the first half's fragment reads: the wait for them that the
+      // compiler puts before the next LDS read (it cannot tell the stages
+      // apart) then falls after the first half's MFMAs, not before them.
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         float4 fa[2][2], fb[2][2];
@@ -474,6 +476,7 @@ __device__ inline void f32_tile(const F32Args& args, const Work& w, float* ldsf)
             fb[i][c] = *(const float4*)(st + BM * kBK + br * kBK + swz8(br, chunk) * 4);
           }
         }
+        if (half == 0 && kv + 1 < hi) issue(kt + 1);
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
