@@ -602,3 +602,46 @@ def test_iq4nl_rows_in_padded_lines(cuda, tmp_path):
     odd.row_stride = 127
     rc = _lib.load().eg_gather(ctypes.byref(odd), None, _lib.ptr(one), 1, 1, _lib.ptr(out), _lib.stream_ptr(cuda))
     assert rc == _lib.EG_ERR_ARG
+
+
+def test_forward_slots_two_layers_with_overlays(cuda):
+    """eg_forward_slots over two table layers, each with its own overlay (one
+    with an index into a larger store): per layer, every slot's overlay row
+    (the index entry, or the id's rank) or -1, as the oracle's search finds
+    it; the output equals eg_forward's bit for bit."""
+    from engraft_ngram_amd import table as T
+    from engraft_ngram_amd.overlay import DeviceOverlay
+    specs = [synthetic_spec(n_rows=16 * 3000, seed=131 + l) for l in range(2)]
+    tabs = [G.device_table(specs[l], "q8_0", 16 * 3000, 128, seed=133 + l) for l in range(2)]
+    tokens = synth.zipf_tokens(135, 2048, 4000)
+    rng = np.random.default_rng(136)
+    ovs, exp = [], []
+    for l in range(2):
+        rows = H.ngram_rows_np(specs[l], tokens, seq_len=1024)
+        ids = np.unique(rng.choice(np.unique(rows), size=400, replace=False)).astype(np.int32)
+        vals = (rng.standard_normal((ids.size, 128)) * 0.05).astype(np.float32)
+        if l == 0:
+            ov = DeviceOverlay.from_rows(ids, vals, device=cuda)
+            slot_row = np.arange(ids.size)
+        else:
+            # an index into a store with the rows in reverse order
+            store_rows = torch.from_numpy(vals[::-1].copy()).to(cuda)
+            index = np.arange(ids.size)[::-1].astype(np.int32).copy()
+            ov = DeviceOverlay(torch.from_numpy(ids).to(cuda), T.RowStore("f32", 128, store_rows),
+                               index=torch.from_numpy(index).to(cuda))
+            slot_row = index
+        pos = np.searchsorted(ids, rows)
+        hit = (pos < ids.size) & (ids[np.minimum(pos, ids.size - 1)] == rows)
+        exp.append(np.where(hit, slot_row[np.minimum(pos, ids.size - 1)], -1))
+        ovs.append(ov)
+    res = G.residual(tokens.size, 2048, seed=137)
+    call = T.PreparedForward(tabs, torch.from_numpy(tokens), res, overlays=ovs, seq_len=1024,
+                             return_slot_vars=True)
+    call()
+    plain = T.forward(tabs, torch.from_numpy(tokens), res, overlays=ovs, seq_len=1024)
+    torch.cuda.synchronize()
+    sv = call.slot_vars.cpu().numpy()
+    for l in range(2):
+        assert np.array_equal(sv[l], exp[l]), l
+    assert (sv >= 0).any() and (sv == -1).any()
+    assert torch.equal(call.out.view(torch.int16), plain.view(torch.int16))
