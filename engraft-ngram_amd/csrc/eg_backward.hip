@@ -1257,7 +1257,7 @@ int eg_descent_plan_slots(const int32_t* slot_var, int64_t n_pos, int32_t heads,
 }
 
 int eg_descent_apply(const void* d_out, int32_t d_out_f32, int64_t n_pos, int32_t heads,
-                     const eg_descent_state* state, const eg_adam* opt, const eg_table* base, const void* workspace,
+                     const eg_descent_state* state, const eg_adam* opt, const eg_table* base, void* workspace,
                      size_t workspace_bytes_, void* stream) {
   int rc = check_state(state);
   if (rc != EG_OK) return rc;
@@ -1287,7 +1287,7 @@ int eg_descent_apply(const void* d_out, int32_t d_out_f32, int64_t n_pos, int32_
   if (state->n == 0) return EG_OK;
   hipStream_t st = (hipStream_t)stream;
   Workspace w;
-  carve((void*)workspace, n, state->n, &w);
+  carve(workspace, n, state->n, &w);
   fill_seg(&a, w, n, state->n);
   a.d_out = d_out;
   a.d_out_f32 = d_out_f32;

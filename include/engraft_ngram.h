@@ -261,9 +261,12 @@ int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
  * bytes); eg_descent_apply is the rest of eg_descent_step (segmented reduce in
  * slot order, Adam, requantisation) from a workspace holding the plan of the
  * same n_pos, heads and state, made on the same stream or ordered before it by
- * the caller.  A workspace holds one plan: it must not be planned into again
- * before the apply that reads it has run.  plan + apply on one workspace is
- * eg_descent_step, bitwise. */
+ * the caller.  A workspace holds one plan.  The apply writes it too: it sorts
+ * each variable's range of more than 4,096 slot ids in place, into the order
+ * the slots are summed in, which leaves the grouping as it was (an apply again
+ * from the same plan sums the same way), but applies of one workspace that
+ * overlap race.  Plan into a workspace only after the apply that reads it has
+ * run.  plan + apply on one workspace is eg_descent_step, bitwise. */
 int eg_descent_plan(const int32_t* rows, int64_t n_pos, int32_t heads, const eg_descent_state* state,
                     void* workspace, size_t workspace_bytes, void* stream);
 /* eg_descent_plan from the slots' variables instead of their rows: slot_var
@@ -277,7 +280,7 @@ int eg_descent_plan_slots(const int32_t* slot_var, int64_t n_pos, int32_t heads,
                           void* stream);
 int eg_descent_apply(const void* d_out, int32_t d_out_f32, int64_t n_pos, int32_t heads,
                      const eg_descent_state* state, const eg_adam* opt, const eg_table* base,
-                     const void* workspace, size_t workspace_bytes, void* stream);
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* eg_descent_step without a workspace argument: it allocates nothing (no
  * hipMalloc, no library allocation).  No counterpart in the reference; it is
