@@ -18,39 +18,36 @@
 // (v_mfma_f32_32x32x2_f32): the products of an fp32 matmul, each operand
 // read once as fp32.
 //
-// Tiling, both: K in steps of 32 through a two-stage LDS ring filled by
-// direct-to-LDS loads (global_load_lds_dwordx4: lane i of a wavefront writes
-// 16 bytes at the wavefront's LDS base + 16 i), so the next step's loads are
-// in flight during the current step's MFMAs without passing through
-// registers; wavefronts of 64 x 64 outputs (2 x 2 MFMA tiles of 32 x 32).
-// gemm_x3: 128 x 128 tiles of four wavefronts, 64 KB of LDS, two workgroups
-// a CU.  Measured against it after a warm-up, launches interleaved: 128 x 256
-// and 256 x 128 tiles with eight wavefronts, 256 x 256 with sixteen, three
-// stages, and scheduling hints that interleave the LDS reads with the MFMAs
-// ran 3-5 % slower; register-staged loads into a padded LDS tile ran 20 %
-// slower; fragments of the next half step read during the current one's
-// MFMAs, and a swizzle free of LDS bank conflicts (counted by
-// SQ_LDS_BANK_CONFLICT), changed the key projection by under 1 %.  gemm_f32:
-// 256 x 256 tiles of sixteen wavefronts, 128 KB of LDS, one workgroup a CU:
-// 88.8 % of the fp32 MFMA peak where the tiles fill whole rounds, against
-// 83.3 % for 128 x 128 tiles of four.
+// Tiling, both: 256 x 256 output tiles, one workgroup a CU; K in steps of 32
+// through a two-stage LDS ring filled by direct-to-LDS loads
+// (global_load_lds_dwordx4: lane i of a wavefront writes 16 bytes at the
+// wavefront's LDS base + 16 i), so the next step's loads are in flight during
+// the current step's MFMAs without passing through registers.
+// gemm_x3: eight wavefronts of 128 x 64 outputs (4 x 2 MFMA tiles of 32 x 32),
+// 128 KB of LDS (four bf16 planes a stage), software-pipelined: a half step's
+// fragments are read during the other half step's MFMAs, one barrier a step.
+// On the key projection (M 2048, N 10240, K 2560) 290 us against 319 us for
+// the 128 x 128 tiles of four wavefronts it replaces (two workgroups a CU,
+// the last round in K quarters), and the backward's d_emb 400 against 470 us;
+// sixteen wavefronts of 64 x 64 or eight of 64 x 128 ran 1-4 % slower, the
+// same tile without the pipelining 2 % slower.  Measured earlier on the
+// 128 x 128 tile and dropped: three stages, scheduling hints, register-staged
+// loads into a padded LDS tile (20 % slower), a swizzle free of LDS bank
+// conflicts (under 1 %).  gemm_f32: sixteen wavefronts of 64 x 64, 128 KB of
+// LDS: 88.8 % of the fp32 MFMA peak where the tiles fill whole rounds,
+// against 83.3 % for 128 x 128 tiles of four.
 //
-// The last round.  The grid is a run of whole tiles followed by pieces: when
-// the tile count leaves the last round (one tile a CU) partly empty, the
-// tiles of that round are cut along K into pieces that fill it, the pieces'
-// partial products go to a workspace, and piece_sum_kernel adds each tile's
-// pieces in K order into C, so the result does not depend on scheduling.  On
-// MI355X (256 CUs): the bf16x3 backward's 320 tiles run as 256 whole tiles
-// and 64 in quarters (412 us against 517 us whole and 483 us in thirds), the
-// forward's key + value (1600 tiles) as 1536 and 64 in quarters.  gemm_f32
-// takes its last round as contiguous ranges instead: the (tile, K step)
-// units of that round's tiles cut into one equal range a CU, each range's
-// parts (one or two tiles) summed per tile in K order by sk_sum_kernel.  The
-// fp32 key + value's 400 tiles run as 256 whole and 144 in 256 ranges of 45
-// of a tile's 80 K steps (1040 us against 1249 us whole and 1126 us with the
-// 144 in sevenths), the backward's 80 tiles of 400 K steps in 256 ranges of
-// 125 (1018 us against 1091 us in thirds).  An explicit k_slices cuts every
-// tile into that many equal pieces.
+// The last round.  When the tile count leaves the last round (one tile a CU)
+// partly empty, the (tile, K step) units of that round's tiles are cut into
+// one contiguous range a CU, each range's parts (one or two tiles) go to a
+// workspace, and sk_sum_kernel adds each tile's parts in K order into C, so
+// the result does not depend on scheduling.  On MI355X (256 CUs): the fp32
+// key + value's 400 tiles run as 256 whole and 144 in 256 ranges of 45 of a
+// tile's 80 K steps (1040 us against 1249 us whole and 1126 us with the 144
+// in sevenths), the backward's 80 tiles of 400 K steps in 256 ranges of 125
+// (1018 us against 1091 us in thirds); the bf16x3 key projection's 320 tiles
+// as 256 whole and 64 in 256 ranges of 20.  An explicit k_slices cuts every
+// tile into that many equal pieces instead (piece_sum_kernel adds them).
 //
 // Workgroups are dispatched round-robin over the 8 XCDs; the whole tiles are
 // remapped so that each XCD takes a contiguous run of tiles, grouped 8 row
@@ -71,13 +68,12 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
-constexpr int kBM = 128, kBN = 128, kBK = 32;
+constexpr int kBK = 32;
 constexpr int kStages = 2;
 
-// bf16x3: a plane tile is 128 rows x 32 bf16 (64 B rows)
-constexpr int kPlane = 128 * kBK;
-constexpr int kStage = 4 * kPlane;  // ah, al, bh, bl
-constexpr size_t kLds = (size_t)kStages * kStage * 2;  // 64 KB
+// gemm_x3's tile: 256 x 256 outputs of 2 x 4 wavefronts of 128 x 64; two
+// stages of four 256 x 32 bf16 planes, 128 KB of LDS
+constexpr int kX3BM = 256, kX3BN = 256, kX3WM = 2, kX3WN = 4;
 
 // What both kernels share: output, tiles and the whole-tile / piece split.
 struct Plan {
@@ -189,31 +185,6 @@ __device__ inline int xcd_order(int b, int nb) {
   return x * per + (x < extra ? x : extra) + i;
 }
 
-template <int BM, int BN>
-__device__ inline Work work_of(const Plan& p) {
-  Work w;
-  const int b = blockIdx.x;
-  int logical;
-  if (b < p.dp_tiles) {
-    logical = xcd_order(b, p.dp_tiles);
-    w.piece = -1;
-    w.kv0 = 0;
-    w.kv1 = p.kt_total;
-  } else {
-    const int q = b - p.dp_tiles;
-    logical = p.dp_tiles + q / p.pieces;
-    w.piece = q;
-    w.kv0 = (int64_t)(q % p.pieces) * p.kt_per_piece;
-    w.kv1 = w.kv0 + p.kt_per_piece < p.kt_total ? w.kv0 + p.kt_per_piece : p.kt_total;
-  }
-  int tm, tn;
-  grouped(logical, p.tiles_m, p.tiles_n, tm, tn);
-  w.grp = tn < p.tiles_n0 ? 0 : 1;
-  w.m0 = (int64_t)tm * BM;
-  w.n0 = (int64_t)(w.grp ? tn - p.tiles_n0 : tn) * BN;
-  return w;
-}
-
 // The work of one tile (logical index) over K steps [kv0, kv1).
 template <int BM, int BN>
 __device__ inline Work tile_work(const Plan& p, int logical, int64_t kv0, int64_t kv1, int piece) {
@@ -233,39 +204,41 @@ __device__ inline Work tile_work(const Plan& p, int logical, int64_t kv0, int64_
 __device__ inline int64_t sk_start(const Plan& p, int64_t s) { return p.sk_units * s / p.sk_groups; }
 
 // D of a 32 x 32 MFMA tile: lane l holds column l % 32 and rows
-// 8 (r / 4) + 4 (l / 32) + r % 4; wavefront (wm, wn) holds the 64 x 64 block
-// at (64 wm, 64 wn) of the tile.  A whole tile goes to C (bounded by m and n,
-// added to when accumulating); a piece to its BM x BN workspace slot.
-template <int BM, int BN>
-__device__ inline void store_acc(const Plan& p, const Work& w, const f32x16 (&acc)[2][2], int wm, int wn,
+// 8 (r / 4) + 4 (l / 32) + r % 4; wavefront (wm, wn) holds TI x TJ such
+// tiles, the block of 32 TI x 32 TJ outputs at (32 TI wm, 32 TJ wn) of the
+// tile.  A whole tile goes to C (bounded by m and n, added to when
+// accumulating); a piece to its BM x BN workspace slot.
+template <int BM, int BN, int TI, int TJ>
+__device__ inline void store_acc(const Plan& p, const Work& w, const f32x16 (&acc)[TI][TJ], int wm, int wn,
                                  int lane) {
   // the store addresses depend on the lane only; an opaque copy of it keeps the
   // compiler from computing them once ahead of a loop over tiles and holding
   // them (in scratch) across the K loops
   asm volatile("" : "+v"(lane));
+  const int r0 = wm * 32 * TI, c0 = wn * 32 * TJ;
   if (w.piece >= 0) {
     float* t = p.ws + (int64_t)w.piece * (BM * BN);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int lc = wn * 64 + j * 32 + (lane & 31);
+      for (int j = 0; j < TJ; ++j) {
+        const int lc = c0 + j * 32 + (lane & 31);
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          t[(wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * BN + lc] = acc[i][j][r];
+          t[(r0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * BN + lc] = acc[i][j][r];
       }
     return;
   }
   float* out = p.c[w.grp];
   const int64_t ld = p.ldc[w.grp], n_grp = p.n[w.grp];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = w.n0 + wn * 64 + j * 32 + (lane & 31);
+    for (int j = 0; j < TJ; ++j) {
+      const int64_t col = w.n0 + c0 + j * 32 + (lane & 31);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = w.m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int64_t row = w.m0 + r0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (row < p.m && col < n_grp) {
           float* q = out + row * ld + col;
           *q = p.accumulate ? *q + acc[i][j][r] : acc[i][j][r];
@@ -279,38 +252,98 @@ __device__ inline int swz8(int row, int chunk) { return chunk ^ ((row >> 1) & 7)
 
 // s_waitcnt vmcnt(0), leaving the other counters alone.
 __device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+// s_waitcnt vmcnt(N) (N < 16) and s_waitcnt lgkmcnt(0), each alone.
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8) | N);
+}
+__device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) | (3 << 14)); }
 
-// A bf16 plane tile is rows x 32 bf16 (64 B rows, no padding); the 16-byte
-// chunk c of row r sits in slot c ^ ((r >> 1) & 3), which spreads the
-// fragment reads (32 rows at one chunk) over the banks.
-__global__ __launch_bounds__(256) void gemm_x3_kernel(const GemmArgs args) {
-  extern __shared__ __attribute__((aligned(16))) __bf16 lds[];
+// Both GEMM kernels walk their blocks the same way: every block covers a range
+// [u0, u1) of (tile, K step) units from tile `base` on.  A whole tile is
+// [0, kt) of its own tile; piece q of the equal cuts is its K steps of tile
+// dp_tiles + q / pieces; with ranges (sk_groups > 0), range s of the last
+// round covers units [start(s), start(s + 1)) of the tiles from dp_tiles on.
+// A range is shorter than a tile's K steps (the last round has fewer tiles
+// than there are ranges), so it meets one or two tiles, t0 and t1 = t0 + 1
+// from base, and the block runs the two parts one after the other.  A part of
+// a tile goes to workspace slot `slot0` + (its tile - t0).  (Written out in
+// each kernel: as a shared helper the fp32 kernel ran 10 % slower.)
+#define EG_GEMM_WALK(...)                                                                               \
+  const Plan& p = args.p;                                                                               \
+  const int64_t kt = p.kt_total;                                                                        \
+  const int b = (int)blockIdx.x;                                                                        \
+  int base, slot0 = 0;                                                                                  \
+  int64_t u0 = 0, u1 = kt;                                                                              \
+  if (b < p.dp_tiles) {                                                                                 \
+    base = xcd_order(b, p.dp_tiles);                                                                    \
+  } else if (p.sk_groups == 0) {                                                                        \
+    const int q = b - p.dp_tiles;                                                                       \
+    base = p.dp_tiles + q / p.pieces;                                                                   \
+    u0 = (int64_t)(q % p.pieces) * p.kt_per_piece;                                                      \
+    u1 = u0 + p.kt_per_piece < kt ? u0 + p.kt_per_piece : kt;                                           \
+    slot0 = q;                                                                                          \
+  } else {                                                                                              \
+    const int s = b - p.dp_tiles;                                                                       \
+    base = p.dp_tiles;                                                                                  \
+    u0 = sk_start(p, s);                                                                                \
+    u1 = sk_start(p, s + 1);                                                                            \
+    slot0 = 2 * s;                                                                                      \
+  }                                                                                                     \
+  if (u0 >= u1 && !(u0 == 0 && kt == 0)) return; /* an empty range (no K steps still stores zeros) */  \
+  const int64_t t0 = kt > 0 ? u0 / kt : 0, t1 = kt > 0 ? (u1 - 1) / kt : 0;                            \
+  _Pragma("unroll 1") for (int64_t t = t0; t <= t1; ++t) {                                              \
+    const int64_t k0 = (u0 > t * kt ? u0 : t * kt) - t * kt;                                            \
+    const int64_t k1 = (u1 < (t + 1) * kt ? u1 : (t + 1) * kt) - t * kt;                                \
+    /* whole: a tile of the full rounds, or one that a range covers from end to end */                  \
+    const bool whole = (b < p.dp_tiles || p.sk_groups > 0) && k0 == 0 && k1 == kt;                      \
+    const Work w = tile_work<BM, BN>(p, base + (int)t, k0, k1, whole ? -1 : slot0 + (int)(t - t0));     \
+    __VA_ARGS__;                                                                                        \
+  }
+
+// gemm_x3: one tile's (or piece's) K steps [w.kv0, w.kv1) and its store.
+// BM x BN tile of WMW x WNW wavefronts, each 32 TI x 32 TJ outputs (TI x TJ
+// MFMA tiles).  A stage holds the four bf16 planes ah, al (BM rows) and bh, bl
+// (BN rows) of 32 k each, 64 B rows, one after the other; the 16-byte chunk c
+// of plane row r sits in slot c ^ ((r >> 1) & 3), which spreads the fragment
+// reads (32 rows at one chunk) over the banks.  A direct-to-LDS load fills 16
+// rows of a plane (1 KB), so load q of a stage lands at 16 q rows from the
+// stage's start.
+template <int BM, int BN, int WMW, int WNW>
+__device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds) {
+  constexpr int NW = WMW * WNW, TI = BM / WMW / 32, TJ = BN / WNW / 32;
+  constexpr int LA = BM / 16, LB = BN / 16;         // loads per A / B plane
+  constexpr int LPW = 2 * (LA + LB) / NW;           // loads per wavefront per stage
+  constexpr int STAGE = 2 * (BM + BN) * kBK;        // bf16
+  static_assert(LA % NW == 0 && LB % NW == 0, "a wavefront's j-th load stays in one plane");
   const Plan& p = args.p;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const Work w = work_of<kBM, kBN>(p);
+  const int r0 = (wave / WNW) * (BM / WMW), c0 = (wave % WNW) * (BN / WNW);
   const int grp = w.grp;
   const int64_t n_grp = p.n[grp];
 
-  f32x16 acc[2][2];
+  f32x16 acc[TI][TJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // this wavefront's 8 loads per stage: load q = wave + 4 j covers plane q / 8
-  // (ah, al, bh, bl), rows 16 (q % 8) .. +15; lane i fills row 16 (q % 8) + i / 4,
-  // slot i % 4.  Rows past m or n read row m-1 or n-1: their products only reach
-  // outputs that are not stored.
+  // this wavefront's loads per stage: load q = wave + NW j covers plane
+  // plane_of(j) (0 ah, 1 al, 2 bh, 3 bl), rows 16 (q - the plane's first load)
+  // .. +15; lane i fills row 16 (..) + i / 4, slot i % 4.  Rows past m or n read
+  // row m-1 or n-1: their products only reach outputs that are not stored.
+  auto plane_of = [](int j) { return NW * j < LA ? 0 : NW * j < 2 * LA ? 1 : NW * j < 2 * LA + LB ? 2 : 3; };
+  auto first_of = [](int pl) { return pl == 0 ? 0 : pl == 1 ? LA : pl == 2 ? 2 * LA : 2 * LA + LB; };
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
-  int64_t row_of[8];
-  int col_of[8];
+  int64_t row_of[LPW];
+  int col_of[LPW];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int q = uwave + 4 * j, plane = q >> 3, row = 16 * (q & 7) + (lane >> 2);
-    const bool is_a = plane < 2;
+  for (int j = 0; j < LPW; ++j) {
+    const int pl = plane_of(j), q = uwave + NW * j, row = 16 * (q - first_of(pl)) + (lane >> 2);
+    const bool is_a = pl < 2;
     const int64_t gr = (is_a ? w.m0 : w.n0) + row, lim = is_a ? p.m : n_grp;
     row_of[j] = gr < lim ? gr : lim - 1;
     col_of[j] = swz(row, lane & 3) * 8;
@@ -322,69 +355,110 @@ __global__ __launch_bounds__(256) void gemm_x3_kernel(const GemmArgs args) {
     const int64_t lo = w.kv0 > seg0 ? w.kv0 : seg0, hi = w.kv1 < seg1 ? w.kv1 : seg1;
     if (lo >= hi) continue;
     const GemmSeg& sg = args.seg[s];
-    const __bf16* src[8];
+    // a load's address: the plane's base (uniform) + a 32-bit byte offset
+    // (the host keeps every plane under 4 GiB), one VGPR a load
+    uint32_t off[LPW];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int plane = (uwave + 4 * j) >> 3;
-      const __bf16* base = plane == 0 ? sg.a_hi : plane == 1 ? sg.a_lo : plane == 2 ? sg.b_hi[grp] : sg.b_lo[grp];
-      const int64_t ld = plane < 2 ? sg.lda : sg.ldb[grp];
-      src[j] = base + row_of[j] * ld + col_of[j];
+    for (int j = 0; j < LPW; ++j) {
+      const int pl = plane_of(j);
+      off[j] = (uint32_t)((row_of[j] * (pl < 2 ? sg.lda : sg.ldb[grp]) + col_of[j]) * 2);
     }
     auto issue = [&](int64_t kt) {  // K step kt of the segment
-      __bf16* st = lds + (kt & 1) * kStage;
+      __bf16* st = lds + (kt & 1) * STAGE;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int q = uwave + 4 * j;
-        __builtin_amdgcn_global_load_lds((const void*)(src[j] + kt * kBK),
-                                         (__attribute__((address_space(3))) void*)(st + (q >> 3) * kPlane +
-                                                                                   16 * (q & 7) * kBK),
-                                         16, 0, 0);
+      for (int j = 0; j < LPW; ++j) {
+        const int pl = plane_of(j), q = uwave + NW * j;
+        const __bf16* base = pl == 0 ? sg.a_hi : pl == 1 ? sg.a_lo : pl == 2 ? sg.b_hi[grp] : sg.b_lo[grp];
+        __builtin_amdgcn_global_load_lds((const void*)((const char*)(base + kt * kBK) + off[j]),
+                                         (__attribute__((address_space(3))) void*)(st + 16 * q * kBK), 16, 0, 0);
       }
     };
-    issue(lo - seg0);
-    for (int64_t kv = lo; kv < hi; ++kv) {
-      const int64_t kt = kv - seg0;
-      wait_vm0();  // this wavefront's part of step kt is in LDS
-      // every wavefront's part is in, and step kt-1 is no longer read.  A bare
-      // s_barrier: no other memory operation needs ordering here.
-      __builtin_amdgcn_s_barrier();
-      if (kv + 1 < hi) issue(kt + 1);
-      const __bf16* st = lds + (kt & 1) * kStage;
+    // fragments of half step ks (16 k) of stage kt into set f
+    bf16x8 ah[2][TI], al[2][TI], bh[2][TJ], bl[2][TJ];
+    auto read = [&](int f, int64_t kt, int ks) {
+      const __bf16* st = lds + (kt & 1) * STAGE;
+      const int c = ks * 2 + (lane >> 5);
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int c = ks * 2 + (lane >> 5);
-        bf16x8 ah[2], al[2], bh[2], bl[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int ar = wm * 64 + i * 32 + (lane & 31);
-          const int ao = ar * kBK + swz(ar, c) * 8;
-          ah[i] = *(const bf16x8*)(st + ao);
-          al[i] = *(const bf16x8*)(st + kPlane + ao);
-          const int br = wn * 64 + i * 32 + (lane & 31);
-          const int bo = br * kBK + swz(br, c) * 8;
-          bh[i] = *(const bf16x8*)(st + 2 * kPlane + bo);
-          bl[i] = *(const bf16x8*)(st + 3 * kPlane + bo);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < TI; ++i) {
+        const int ar = r0 + i * 32 + (lane & 31);
+        const int ao = ar * kBK + swz(ar, c) * 8;
+        ah[f][i] = *(const bf16x8*)(st + ao);
+        al[f][i] = *(const bf16x8*)(st + BM * kBK + ao);
       }
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const int br = c0 + j * 32 + (lane & 31);
+        const int bo = br * kBK + swz(br, c) * 8;
+        bh[f][j] = *(const bf16x8*)(st + 2 * BM * kBK + bo);
+        bl[f][j] = *(const bf16x8*)(st + (2 * BM + BN) * kBK + bo);
+      }
+    };
+    // the products of set f: lo*hi, hi*lo, hi*hi (the small ones first), as
+    // three passes over the TI x TJ tiles
+    auto mfma = [&](int f, int pass) {
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pass == 0 ? al[f][i] : ah[f][i],
+                                                               pass == 1 ? bl[f][j] : bh[f][j], acc[i][j], 0, 0, 0);
+    };
+    // Software pipeline, one barrier a step.  The fragments of one half step
+    // are read during the other half step's MFMAs, after its first pass: the
+    // compiler's wait for a half step's fragments (it waits for every LDS read
+    // issued before it) then comes before the first pass, when only that half
+    // step's reads, long issued, are outstanding; and the next reads reuse the
+    // registers of the lo*hi pass's lo planes.  The loads of step kt + 2 are
+    // issued once every wavefront has read step kt (the barrier in the middle
+    // of step kt), a step ahead of their use.
+    issue(lo - seg0);
+    if (lo + 1 < hi) {
+      issue(lo + 1 - seg0);
+      wait_vm<LPW>();  // this wavefront's part of the first step is in LDS
+    } else {
+      wait_vm<0>();
     }
-    __builtin_amdgcn_s_barrier();  // the ring is refilled by the next segment
+    __builtin_amdgcn_s_barrier();
+    read(0, lo - seg0, 0);
+    // every step but the last (no branch around the reads)
+    for (int64_t kv = lo; kv + 1 < hi; ++kv) {
+      const int64_t kt = kv - seg0;
+      mfma(0, 0);
+      __builtin_amdgcn_sched_barrier(0);  // the reads stay between the passes
+      read(1, kt, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(0, 1);
+      mfma(0, 2);
+      __builtin_amdgcn_sched_barrier(0);
+      // this wavefront's part of step kt + 1 is in LDS and its reads of step kt
+      // are in registers; after the barrier, every wavefront's are
+      wait_vm<0>();
+      wait_lgkm0();
+      __builtin_amdgcn_s_barrier();
+      if (kv + 2 < hi) issue(kt + 2);
+      mfma(1, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      read(0, kt + 1, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(1, 1);
+      mfma(1, 2);
+    }
+    mfma(0, 0);
+    read(1, hi - 1 - seg0, 1);
+    mfma(0, 1);
+    mfma(0, 2);
+    mfma(1, 0);
+    mfma(1, 1);
+    mfma(1, 2);
+    __builtin_amdgcn_s_barrier();  // the ring is refilled by the next segment or tile
   }
-  store_acc<kBM, kBN>(p, w, acc, wm, wn, lane);
+  store_acc<BM, BN, TI, TJ>(p, w, acc, wave / WNW, wave % WNW, lane);
+}
+
+template <int BM, int BN, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * 64) void gemm_x3_kernel(const GemmArgs args) {
+  extern __shared__ __attribute__((aligned(16))) __bf16 lds[];
+  EG_GEMM_WALK(x3_tile<BM, BN, WMW, WNW>(args, w, lds))
 }
 
 // One MFMA takes one A and one B value per lane (lane l: row / column l % 32,
@@ -493,66 +567,16 @@ __device__ inline void f32_tile(const F32Args& args, const Work& w, float* ldsf)
     }
     __builtin_amdgcn_s_barrier();  // the ring is refilled by the next segment or tile
   }
-  store_acc<BM, BN>(p, w, acc, wm, wn, lane);
+  store_acc<BM, BN, 2, 2>(p, w, acc, wm, wn, lane);
 }
 
-// One MFMA takes one A and one B value per lane (lane l: row / column l % 32,
-// k = l / 32), so each lane half works through its own 16 k of a step: lane
-// half h reads k 16 h .. 16 h + 15 of its row as four 16-byte chunks and the
-// 16 MFMAs of the step pair k = kk (half 0) with k = 16 + kk (half 1).  The
-// 16-byte chunk c of tile row r sits in slot c ^ ((r >> 1) & 7): a fragment
-// read (16 lanes at one chunk of 16 consecutive rows per LDS cycle) then
-// touches 16 distinct 16-byte bank groups.  64 MFMAs of 64 cycles a step
-// against 16 KB of LDS reads per wavefront: the matrix cores, not the LDS,
-// bound it.  BM x BN tile, (BM / 64) x (BN / 64) wavefronts of 64 x 64; A and
-// B tiles of BM and BN rows x 128 B a stage.
-//
-// With ranges (sk_groups > 0), the last round's (tile, K step) units are cut
-// into sk_groups contiguous ranges, one per workgroup slot of the round. A
-// range is shorter than a tile's K steps (the last round has fewer tiles than
-// there are ranges), so it meets one or two tiles, and its workgroup runs the
-// two parts one after the other.  The stores' lane addresses are recomputed
-// for each part (see store_acc): held across both K loops they spilled 62
-// VGPRs to scratch and cost 4 % on whole tiles.
+// gemm_f32 over the walk.  The stores' lane addresses are recomputed for
+// each part of a range (see store_acc): held across both K loops they spilled
+// 62 VGPRs to scratch and cost 4 % on whole tiles.
 template <int BM, int BN>
 __global__ __launch_bounds__(BM * BN / 64) void gemm_f32_kernel(const F32Args args) {
   extern __shared__ __attribute__((aligned(16))) float ldsf[];
-  const Plan& p = args.p;
-  // Every block walks a range [u0, u1) of (tile, K step) units from tile
-  // `base` on: a whole tile is [0, kt) of its own tile; piece q of the equal
-  // cuts is its K steps of tile dp_tiles + q / pieces; range s of the last
-  // round covers units [start(s), start(s + 1)) of the tiles from dp_tiles on.
-  // A part of a tile goes to workspace slot `slot0` + (its tile - the range's
-  // first tile).
-  const int64_t kt = p.kt_total;
-  const int b = (int)blockIdx.x;
-  int base, slot0 = 0;
-  int64_t u0 = 0, u1 = kt;
-  if (b < p.dp_tiles) {
-    base = xcd_order(b, p.dp_tiles);
-  } else if (p.sk_groups == 0) {
-    const int q = b - p.dp_tiles;
-    base = p.dp_tiles + q / p.pieces;
-    u0 = (int64_t)(q % p.pieces) * p.kt_per_piece;
-    u1 = u0 + p.kt_per_piece < kt ? u0 + p.kt_per_piece : kt;
-    slot0 = q;
-  } else {
-    const int s = b - p.dp_tiles;
-    base = p.dp_tiles;
-    u0 = sk_start(p, s);
-    u1 = sk_start(p, s + 1);
-    slot0 = 2 * s;
-  }
-  if (u0 >= u1 && !(u0 == 0 && kt == 0)) return;  // an empty range (a tile with no K steps still stores zeros)
-  const int64_t t0 = kt > 0 ? u0 / kt : 0, t1 = kt > 0 ? (u1 - 1) / kt : 0;  // t1 <= t0 + 1
-#pragma unroll 1
-  for (int64_t t = t0; t <= t1; ++t) {
-    const int64_t k0 = (u0 > t * kt ? u0 : t * kt) - t * kt;
-    const int64_t k1 = (u1 < (t + 1) * kt ? u1 : (t + 1) * kt) - t * kt;
-    // whole: a tile of the full rounds, or one that a range covers from end to end
-    const bool whole = (b < p.dp_tiles || p.sk_groups > 0) && k0 == 0 && k1 == kt;
-    f32_tile<BM, BN>(args, tile_work<BM, BN>(p, base + (int)t, k0, k1, whole ? -1 : slot0 + (int)(t - t0)), ldsf);
-  }
+  EG_GEMM_WALK(f32_tile<BM, BN>(args, w, ldsf))
 }
 
 // C (+)= the sum of a last-round tile's pieces, in K order: BM BN / 1024
@@ -647,10 +671,8 @@ struct PiecePlan {
 };
 
 // A kernel's tile: BM x BN outputs of `threads` threads and `lds` bytes of
-// LDS.  The plan counts `rounds_per_cu` tiles a CU as one round: gemm_x3's
-// second workgroup on a CU adds little throughput to the first (it is bound
-// by its own LDS and load latency, not the CU's matrix cores), so a round of
-// its 128 x 128 tiles is one a CU, as for gemm_f32's 256 x 256 tiles.
+// LDS.  The plan counts `rounds_per_cu` tiles a CU as one round (one for
+// both kernels' 256 x 256 tiles, whose LDS holds one workgroup a CU).
 // `sum_cost` / (K steps) is the time of summing one round of pieces against
 // the time of one round of tiles: 4 bytes read per output and piece at ~5
 // TB/s against 192 (bf16 products, ~1 PFLOP/s reached) or 64 (fp32, ~130
@@ -665,7 +687,8 @@ struct Shape {
   bool ranges;
 };
 
-constexpr Shape kX3Shape{kBM, kBN, 256, 1, kLds, 4.2, false};
+constexpr Shape kX3Shape{kX3BM, kX3BN, kX3WM * kX3WN * 64, 1, (size_t)kStages * 2 * (kX3BM + kX3BN) * kBK * 2, 4.2,
+                         true};
 constexpr int kF32BM = 256, kF32BN = 256;
 constexpr Shape kF32Shape{kF32BM, kF32BN, kF32BM * kF32BN / 64, 1,
                           (size_t)kStages * (kF32BM + kF32BN) * kBK * 4, 1.6, true};
@@ -888,6 +911,10 @@ int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_
     EG_CHECK_ARG(o.lda % 8 == 0 && o.ldb % 8 == 0 && o.lda >= o.k && o.ldb >= o.k &&
                      (n2 == 0 || (o.ldb2 % 8 == 0 && o.ldb2 >= o.k)),
                  "segment %d: leading dimensions must be multiples of 8 and >= k", s);
+    // the kernel addresses a row's 16-byte chunks by 32-bit byte offsets from the plane's start
+    auto fits = [](int64_t rows, int64_t ld) { return rows <= 0 || ((rows - 1) * ld + 32) * 2 <= 0xffffffffLL; };
+    EG_CHECK_ARG(fits(m, o.lda) && fits(n, o.ldb) && (n2 == 0 || fits(n2, o.ldb2)),
+                 "segment %d: a bf16 plane spans 4 GiB or more", s);
     GemmSeg& sg = g.seg[g.n_seg];
     sg.a_hi = (const __bf16*)o.a_hi;
     sg.a_lo = (const __bf16*)o.a_lo;
@@ -901,8 +928,9 @@ int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_
     sg.ktiles = o.k / 32;
     ++g.n_seg;
   }
-  return launch_gemm<kBM, kBN>(kX3Shape, gemm_x3_kernel, "gemm_x3_kernel", g, m, n, n2, c, ldc, c2, ldc2,
-                               accumulate, k_slices, workspace, workspace_bytes, stream);
+  return launch_gemm<kX3BM, kX3BN>(kX3Shape, gemm_x3_kernel<kX3BM, kX3BN, kX3WM, kX3WN>, "gemm_x3_kernel", g, m, n,
+                                   n2, c, ldc, c2, ldc2, accumulate, k_slices, workspace, workspace_bytes,
+                                   stream);
 }
 
 int eg_gemm_f32(const eg_gemm_f32_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,

@@ -190,7 +190,7 @@ def gemm_x3(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate:
     ``b_n2`` (and ``b2_n2`` with a second segment) ``[n2, k]`` add a second
     column group, ``a @ b_n2.T (+ a2 @ b2_n2.T)`` into ``out2``, in the same
     launch.  ``k_slices`` (default: the library's plan, which cuts the tiles
-    of a partly filled last round of workgroups along K) cuts every 128 x 128
+    of a partly filled last round of workgroups along K) cuts every 256 x 256
     tile into that many K pieces, summed in a fixed order.  Returns ``out`` (``[m, n]`` fp32,
     allocated when not given; added to when ``accumulate``), or ``(out,
     out2)`` with a second column group."""

@@ -485,10 +485,11 @@ typedef struct eg_gemm_operands {
  * accumulated in fp32 (hi + lo keeps 16 mantissa bits: a relative error
  * up to ~3 x 2^-18 per product, about 1e-5 of the result on random data; a
  * non-finite operand gives NaN).  Planes 16-byte aligned, leading dimensions
- * multiples of 8; accumulate = 1 adds to C / C2.  k_slices = 0 cuts the
- * tiles of a partly filled last round of workgroups along K into pieces that
- * fill it; k_slices >= 1 cuts every 128 x 128 output tile into that many K
- * pieces (1: none).  Pieces' partial products go to a workspace of
+ * multiples of 8, each plane under 4 GiB ((rows - 1) * ld + 32 bf16);
+ * accumulate = 1 adds to C / C2.  k_slices = 0 cuts the tiles of a partly
+ * filled last round of workgroups along K into ranges that fill it;
+ * k_slices >= 1 cuts every 256 x 256 output tile into that many K pieces
+ * (1: none).  Pieces' partial products go to a workspace of
  * eg_gemm_workspace_size(m, n, n2, k, k_slices) bytes, k the sum of the
  * segments' k (asked on the device that runs the GEMM: the plan follows its
  * CU count), and are summed in K order afterwards (deterministic).  The

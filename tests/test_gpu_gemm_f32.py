@@ -194,13 +194,14 @@ def test_gemm_f32_argument_errors(cuda):
 # 256 x 256 tile a CU: 288 tiles, 32 of them in 256 ranges of 8 K steps (each
 # inside one tile); 280 tiles, 24 in ranges of 9-10 of their 100 K steps (most
 # ranges meet two tiles); 264 tiles of 16 K steps, too short for ranges, the 8
-# past the first round in halves after 256 whole tiles.  bf16x3, 128 x 128
-# tiles: 1152 tiles, the 128 past the whole rounds in pieces.
+# past the first round in halves after 256 whole tiles.  bf16x3, the same
+# tiles and plans: ranges inside one tile and ranges across two.
 _LAST_ROUND = [
     ("f32", 1024, 18432, 2048, "ranges", 2 * 256 * 256 * 256 * 4),
     ("f32", 1024, 17920, 3200, "ranges", 2 * 256 * 256 * 256 * 4),
     ("f32", 2048, 8448, 512, "halves", 8 * 2 * 256 * 256 * 4),
-    ("bf16x3", 1024, 18432, 2048, "pieces", None),
+    ("bf16x3", 1024, 18432, 2048, "ranges", 2 * 256 * 256 * 256 * 4),
+    ("bf16x3", 1024, 17920, 3200, "ranges", 2 * 256 * 256 * 256 * 4),
 ]
 
 
