@@ -30,10 +30,12 @@
 // the 128 x 128 tiles of four wavefronts it replaces (two workgroups a CU,
 // the last round in K quarters), and the backward's d_emb 400 against 470 us;
 // sixteen wavefronts of 64 x 64 or eight of 64 x 128 ran 1-4 % slower, the
-// same tile without the pipelining 2 % slower.  Measured earlier on the
-// 128 x 128 tile and dropped: three stages, scheduling hints, register-staged
-// loads into a padded LDS tile (20 % slower), a swizzle free of LDS bank
-// conflicts (under 1 %).  gemm_f32: sixteen wavefronts of 64 x 64, 128 KB of
+// same tile without the pipelining 2 % slower, with 2-way LDS bank conflicts
+// on the fragment reads 2-3 % slower.  Measured earlier on the 128 x 128 tile
+// and dropped: three stages, scheduling hints, register-staged loads into a
+// padded LDS tile (20 % slower).  Counters on the key projection: the matrix
+// cores busy 55 % of the cycles (SQ_VALU_MFMA_BUSY_CYCLES) at a shader clock
+// of ~1.8 GHz under this load.  gemm_f32: sixteen wavefronts of 64 x 64, 128 KB of
 // LDS: 88.8 % of the fp32 MFMA peak where the tiles fill whole rounds,
 // against 83.3 % for 128 x 128 tiles of four.
 //
@@ -247,7 +249,7 @@ __device__ inline void store_acc(const Plan& p, const Work& w, const f32x16 (&ac
     }
 }
 
-__device__ inline int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
+__device__ inline int swz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
 __device__ inline int swz8(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 // s_waitcnt vmcnt(0), leaving the other counters alone.
@@ -306,8 +308,11 @@ __device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) 
 // BM x BN tile of WMW x WNW wavefronts, each 32 TI x 32 TJ outputs (TI x TJ
 // MFMA tiles).  A stage holds the four bf16 planes ah, al (BM rows) and bh, bl
 // (BN rows) of 32 k each, 64 B rows, one after the other; the 16-byte chunk c
-// of plane row r sits in slot c ^ ((r >> 1) & 3), which spreads the fragment
-// reads (32 rows at one chunk) over the banks.  A direct-to-LDS load fills 16
+// of plane row r sits in slot c ^ ((r >> 2) & 3): a fragment read (16 lanes
+// at one chunk of 16 consecutive rows per LDS cycle) then touches 16
+// distinct 16-byte bank groups (the counter SQ_LDS_BANK_CONFLICT read half of
+// SQ_LDS_IDX_ACTIVE with c ^ ((r >> 1) & 3); 2-3 % faster without the
+// conflicts).  A direct-to-LDS load fills 16
 // rows of a plane (1 KB), so load q of a stage lands at 16 q rows from the
 // stage's start.
 template <int BM, int BN, int WMW, int WNW>
