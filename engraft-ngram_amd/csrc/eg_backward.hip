@@ -776,7 +776,6 @@ __device__ inline uint32_t sort32(uint32_t v, int sub, int span = 32) {
       const uint32_t o = (uint32_t)__shfl_xor((int)v, k - 1, 32);
       v = (sub < (sub ^ (k - 1))) ? min(v, o) : max(v, o);
     }
-#pragma unroll
     for (int j = k >> 2; j > 0; j >>= 1) {
       const uint32_t o = (uint32_t)__shfl_xor((int)v, j, 32);
       v = ((sub & j) == 0) ? min(v, o) : max(v, o);
