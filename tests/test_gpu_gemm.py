@@ -160,3 +160,8 @@ def test_gemm_x3_argument_errors(cuda):
     with pytest.raises(ValueError, match="workspace"):
         _lib.call("eg_gemm_bf16x3", ops, 1, 8, 8, 0, _lib.ptr(c), 8, None, 0, 0, 1 + 1, None, 0,
                   _lib.stream_ptr(cuda))
+    # the kernel's 32-bit byte offsets: a plane of 4 GiB or more is refused
+    # before anything is launched (only the leading dimension is large here)
+    ops[0].lda = 1 << 31
+    with pytest.raises(ValueError, match="4 GiB"):
+        _lib.call("eg_gemm_bf16x3", ops, 1, 8, 8, 0, _lib.ptr(c), 8, None, 0, 0, 1, None, 0, _lib.stream_ptr(cuda))
