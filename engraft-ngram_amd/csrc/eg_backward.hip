@@ -41,8 +41,11 @@ constexpr int kLongGroups = 8;   // 32-lane groups per long-segment workgroup
 
 // ---------------------------------------------------------------------------
 // Row index: open addressing over a power-of-two table of (row << 32 | k)
-// entries, Fibonacci hashing, linear probing.  Lookups are deterministic
-// whatever order the entries were inserted in.
+// entries (at least 8), Fibonacci hashing, linear probing from the start of the
+// aligned group of 8 entries (64 bytes) that holds the hash slot: a lookup reads
+// whole groups, and at most a quarter full a row's group holds it (or an empty
+// entry) for all but ~1e-4 of the lookups.  Lookups are deterministic whatever
+// order the entries were inserted in.
 // ---------------------------------------------------------------------------
 constexpr unsigned long long kIndexEmpty = ~0ull;
 
@@ -62,7 +65,7 @@ __global__ __launch_bounds__(256) void index_build_kernel(const int32_t* __restr
   const int32_t row = ids[k];
   const uint64_t mask = (1ull << bits) - 1ull;
   const unsigned long long packed = ((unsigned long long)(uint32_t)row << 32) | (uint32_t)k;
-  uint64_t h = index_slot(row, bits);
+  uint64_t h = index_slot(row, bits) & ~7ull;
   for (uint64_t probe = 0; probe <= mask; ++probe) {  // the table is at most half full
     if (atomicCAS(&tab[h], kIndexEmpty, packed) == kIndexEmpty) return;
     h = (h + 1) & mask;
@@ -97,32 +100,46 @@ __device__ inline void slot_keys(const int32_t* __restrict__ rows, int64_t n, in
     for (int r = 0; r < IPT; ++r)
       key[r] = (ok[r] && row[r] >= 0 && (int64_t)row[r] < n_var) ? (uint32_t)row[r] : (uint32_t)n_var;
   } else if constexpr (MODE == 1) {
-    // probe the row index; the items' probes advance in lockstep
+    // probe the row index a group of 8 entries at a time, the row's group
+    // first (the linear probe's order): one round of loads settles a
+    // wavefront's lookups but for ~1 % of the wavefronts.  The items' probes
+    // advance in lockstep.
     const uint64_t imask = (1ull << index_bits) - 1ull;
-    uint64_t hslot[IPT];
+    uint64_t grp[IPT];
     bool done[IPT];
 #pragma unroll
     for (int r = 0; r < IPT; ++r) {
-      hslot[r] = index_slot(row[r], index_bits);
+      grp[r] = index_slot(row[r], index_bits) & ~7ull;
       done[r] = !ok[r];
       key[r] = (uint32_t)n_var;
     }
-    for (uint64_t probe = 0; probe <= imask; ++probe) {
+    for (uint64_t probe = 0; probe <= (imask >> 3); ++probe) {  // every group once
       bool any = false;
-      unsigned long long ent[IPT];
+      ulonglong2 e[IPT][4];
 #pragma unroll
-      for (int r = 0; r < IPT; ++r) ent[r] = index[hslot[r]];
+      for (int r = 0; r < IPT; ++r)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) e[r][q] = ((const ulonglong2*)(index + grp[r]))[q];
 #pragma unroll
       for (int r = 0; r < IPT; ++r) {
         if (done[r]) continue;
-        const unsigned long long e = ent[r];
-        if (e == kIndexEmpty) {
-          done[r] = true;
-        } else if ((uint32_t)(e >> 32) == (uint32_t)row[r]) {
-          key[r] = (uint32_t)e;
+        bool fin = false;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const unsigned long long ent = (j & 1) ? e[r][j >> 1].y : e[r][j >> 1].x;
+          if (!fin) {
+            if (ent == kIndexEmpty) {
+              fin = true;
+            } else if ((uint32_t)(ent >> 32) == (uint32_t)row[r]) {
+              key[r] = (uint32_t)ent;
+              fin = true;
+            }
+          }
+        }
+        if (fin) {
           done[r] = true;
         } else {
-          hslot[r] = (hslot[r] + 1) & imask;
+          grp[r] = (grp[r] + 8) & imask;
           any = true;
         }
       }
@@ -1158,9 +1175,10 @@ size_t eg_backward_workspace_size(int64_t n_slots, int64_t n_var) {
 
 int eg_build_row_index(const int32_t* ids, int64_t n, int64_t* table, int64_t capacity, void* stream) {
   EG_CHECK_ARG(n >= 0 && n < (1LL << 31), "n=%lld", (long long)n);
-  EG_CHECK_ARG(capacity >= 2 && capacity >= 2 * n && (capacity & (capacity - 1)) == 0 && capacity <= (1LL << 32),
-               "capacity=%lld must be a power of two >= 2*n", (long long)capacity);
+  EG_CHECK_ARG(capacity >= 8 && capacity >= 2 * n && (capacity & (capacity - 1)) == 0 && capacity <= (1LL << 32),
+               "capacity=%lld must be a power of two >= max(8, 2*n)", (long long)capacity);
   EG_CHECK_ARG(table != nullptr && (n == 0 || ids != nullptr), "ids/table is NULL");
+  EG_CHECK_ARG(((uintptr_t)table & 15) == 0, "table must be 16-byte aligned");
   int bits = 0;
   while ((1LL << bits) < capacity) ++bits;
   hipStream_t st = (hipStream_t)stream;
@@ -1219,9 +1237,11 @@ static int check_state(const eg_descent_state* state) {
   EG_CHECK_ARG(state->n == 0 || (state->master && state->m && state->v && state->stamp),
                "state master/m/v/stamp is NULL");
   if (state->index != nullptr)
-    EG_CHECK_ARG(state->index_capacity >= 2 * state->n && state->index_capacity >= 2 &&
-                     (state->index_capacity & (state->index_capacity - 1)) == 0 && state->index_capacity <= (1LL << 32),
-                 "index_capacity=%lld must be a power of two >= 2*n", (long long)state->index_capacity);
+    EG_CHECK_ARG(state->index_capacity >= 2 * state->n && state->index_capacity >= 8 &&
+                     (state->index_capacity & (state->index_capacity - 1)) == 0 &&
+                     state->index_capacity <= (1LL << 32) && ((uintptr_t)state->index & 15) == 0,
+                 "index_capacity=%lld must be a power of two >= max(8, 2*n), the index 16-byte aligned",
+                 (long long)state->index_capacity);
   return EG_OK;
 }
 

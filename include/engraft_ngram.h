@@ -230,8 +230,10 @@ typedef struct eg_descent_state {
 } eg_descent_state;
 
 /* Builds an open-addressing index of sorted unique ids for the backward's
- * lookups: table int64 [capacity] (capacity a power of two >= 2*n), entries
- * (row << 32 | position in ids), -1 when empty.  Built once per state. */
+ * lookups: table int64 [capacity] (capacity a power of two >= max(8, 2*n),
+ * 16-byte aligned; 64-byte aligned, a lookup reads one memory line), entries
+ * (row << 32 | position in ids), -1 when empty, linear probing.  The lookups
+ * read aligned groups of 8 entries.  Built once per state. */
 int eg_build_row_index(const int32_t* ids, int64_t n, int64_t* table, int64_t capacity, void* stream);
 
 /* Workspace bytes eg_scatter_grad(_slots) / eg_descent_step need for
