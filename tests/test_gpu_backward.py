@@ -335,6 +335,47 @@ def test_descent_step_edge_cases(cuda):
     assert torch.equal(st.master, p0)
 
 
+def _index_group(row: int, bits: int) -> int:
+    """The row index's hash group of a row (Fibonacci hashing, groups of 8)."""
+    return (((row * 0x9E3779B1) & 0xFFFFFFFF) >> (32 - bits)) >> 3
+
+
+@pytest.mark.parametrize("cap,n_ids", [(8, 4), (16, 8)])
+def test_row_index_small_and_full_groups(cuda, cap, n_ids):
+    """The row index probes aligned groups of 8 entries.  A table of 8 entries
+    (one group), and a table of 16 whose first group is full (every id hashes
+    into it; lookups of absent rows of that group go on to the second), give
+    the same step, bit for bit, as the state's own index."""
+    from engraft_ngram_amd import _lib
+    from engraft_ngram_amd import descent as D
+    _say(f"row index of {cap} entries, {n_ids} ids")
+    bits = cap.bit_length() - 1
+    grp0 = [r for r in range(1, 200000) if _index_group(r, bits) == 0]
+    ids = np.array(sorted(grp0[:n_ids]), dtype=np.int32)
+    absent = grp0[n_ids:n_ids + 8] + [r for r in range(1, 200000) if _index_group(r, bits) != 0][:8]
+    rng = np.random.default_rng(7)
+    rows = rng.choice(np.concatenate([ids, np.array(absent, dtype=np.int32)]), size=(64, 4)).astype(np.int32)
+    rows.reshape(-1)[:n_ids] = ids  # every id is some slot's row
+    g = torch.Generator(device=cuda).manual_seed(8)
+    master = torch.randn((n_ids, 128), generator=g, device=cuda) * 0.02
+    d = (torch.randn((64, 4 * 128), generator=g, device=cuda) * 1e-3).to(torch.bfloat16)
+    ref = D.DescentState(torch.from_numpy(ids).to(cuda), master.clone())
+    small = D.DescentState(torch.from_numpy(ids).to(cuda), master.clone())
+    small.index = torch.empty(cap, dtype=torch.int64, device=cuda)
+    _lib.call("eg_build_row_index", _lib.ptr(small.ids), n_ids, _lib.ptr(small.index), cap, _lib.stream_ptr(cuda))
+    table = small.index.cpu().numpy()
+    assert (table[:8] != -1).sum() == min(n_ids, 8)  # every id sits in the first group
+    r = torch.from_numpy(rows).to(cuda)
+    for st in (ref, small):
+        st.step(d, r, lr=1e-3)
+        st.step(d, r, lr=1e-3)
+    torch.cuda.synchronize()
+    for a, b in ((ref.master, small.master), (ref.m, small.m), (ref.v, small.v),
+                 (ref.quant.payload, small.quant.payload), (ref.quant.scales, small.quant.scales)):
+        assert torch.equal(a, b)
+    assert not torch.equal(ref.master, master)  # the step moved the rows
+
+
 def test_planned_steps_on_a_second_stream(cuda):
     """A descent loop that groups the next batch's slots on a second stream
     while the current step runs (DescentState.plan + step(plan=...), i.e.
