@@ -31,7 +31,8 @@
 // the last round in K quarters), and the backward's d_emb 400 against 470 us;
 // sixteen wavefronts of 64 x 64 or eight of 64 x 128 ran 1-4 % slower, the
 // same tile without the pipelining 2 % slower, with 2-way LDS bank conflicts
-// on the fragment reads 2-3 % slower.  Measured earlier on the 128 x 128 tile
+// on the fragment reads 2-3 % slower; the reads interleaved one by one with
+// the MFMAs, or the wave priority raised over the MFMA passes, within 1 %.  Measured earlier on the 128 x 128 tile
 // and dropped: three stages, scheduling hints, register-staged loads into a
 // padded LDS tile (20 % slower).  Counters on the key projection: the matrix
 // cores busy 55 % of the cycles (SQ_VALU_MFMA_BUSY_CYCLES) at a shader clock
