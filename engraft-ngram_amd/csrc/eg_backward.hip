@@ -324,6 +324,7 @@ __global__ __launch_bounds__(kGroupThreads) void tile_sort_kernel(
   }
 }
 
+template <int TPT>
 __global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
     const unsigned long long* __restrict__ pairs, const uint32_t* __restrict__ seg, int64_t n_tiles, int nb, int bs,
     int64_t n_var, int64_t long_len, uint32_t* __restrict__ start, uint32_t* __restrict__ end,
@@ -347,7 +348,7 @@ __global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
   if (tid == 0) n_long_b = 0u;
   // this thread's tiles: (count, offset) of the bucket's segment in each; the
   // offsets add up to the bucket's place in the slots array
-  constexpr int kTilesPerThread = 4;  // n_tiles <= kTilesPerThread * kRangeThreads (host checks)
+  constexpr int kTilesPerThread = TPT;  // n_tiles <= TPT * kRangeThreads (the host picks TPT)
   u32x2 sg[kTilesPerThread];
   uint32_t tot = 0, pre = 0;
 #pragma unroll
@@ -1041,8 +1042,15 @@ static int group_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64
     else if (mode == 1) EG_TILE_SORT(1);
     else EG_TILE_SORT(0);
 #undef EG_TILE_SORT
-    hipLaunchKernelGGL(bucket_ranges_kernel, dim3((unsigned)g.nb), dim3(kRangeThreads), 0, st, w.pairs, w.seg,
-                       g.n_tiles, g.nb, g.bs, n_var, n_long_max(n), w.start, w.end, w.slots, w.long_list);
+    // as few tiles a thread as the tile count allows (the loads of a thread's
+    // tiles past the last are wasted issue slots in the kernel's dependent round)
+#define EG_BUCKET_RANGES(TPT)                                                                                     \
+  hipLaunchKernelGGL(bucket_ranges_kernel<TPT>, dim3((unsigned)g.nb), dim3(kRangeThreads), 0, st, w.pairs, w.seg, \
+                     g.n_tiles, g.nb, g.bs, n_var, n_long_max(n), w.start, w.end, w.slots, w.long_list)
+    if (g.n_tiles <= kRangeThreads) EG_BUCKET_RANGES(1);
+    else if (g.n_tiles <= 2 * kRangeThreads) EG_BUCKET_RANGES(2);
+    else EG_BUCKET_RANGES(4);
+#undef EG_BUCKET_RANGES
     return launch_status("slot grouping kernels");
   }
   hipLaunchKernelGGL(clear_kernel, dim3(grid_for(n_var + 2, 256, 1024)), dim3(256), 0, st, w.off, n_var + 2,

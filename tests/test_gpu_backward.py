@@ -78,13 +78,14 @@ def test_scatter_grad_edge_cases(cuda):
         assert np.array_equal(got, exp)
 
 
-@pytest.mark.parametrize("n_slots,n_var", [(1_100_000, 300_000), (1_000_000, 1_500_000)],
-                         ids=["counting-1075-tiles", "buckets-of-2048-variables"])
+@pytest.mark.parametrize("n_slots,n_var", [(1_100_000, 300_000), (1_000_000, 1_500_000), (400_000, 100_000)],
+                         ids=["counting-1075-tiles", "buckets-of-2048-variables", "buckets-391-tiles"])
 def test_scatter_grad_large_groupings(cuda, n_slots, n_var):
     """The two groupings past the common case, bit-exact against the oracle:
     more than 1,024 tiles of 1,024 slots (the counting grouping: per-variable
-    atomics, scan, fill), and more than 1M variables (the tile sort with
-    buckets of 2,048 variables).  Zipf-drawn rows give long segments; a twentieth
+    atomics, scan, fill), more than 1M variables (the tile sort with buckets of
+    2,048 variables), and 391 tiles (the bucket ranges read two tiles a thread;
+    977 tiles, four).  Zipf-drawn rows give long segments; a twentieth
     of the slots hit no variable."""
     from engraft_ngram_amd import descent as D
     _say(f"scatter_grad grouping, {n_slots} slots over {n_var} variables")
