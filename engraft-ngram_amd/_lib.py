@@ -28,6 +28,8 @@ FMT_MXFP8 = 3
 FMT_IQ4_NL = 4
 FMT_F32 = 5
 
+ABI_VERSION = 3  # EG_ABI_VERSION of include/engraft_ngram.h these structures follow
+
 FMT_CODES = {"bf16": FMT_BF16, "q8_0": FMT_Q8_0, "mxfp8": FMT_MXFP8, "iq4_nl": FMT_IQ4_NL, "f32": FMT_F32}
 
 
@@ -74,6 +76,7 @@ class EgAdam(ctypes.Structure):
         ("step", c_int64),
         ("dense", c_int32),
         ("l2_coef", ctypes.c_float),
+        ("anchor", c_void_p),
     ]
 
 
@@ -132,6 +135,7 @@ SIGNATURES = {
     "eg_forward_rows": (c_int32, [c_int32, POINTER(EgTable), POINTER(EgOverlay), c_void_p, c_int64, c_int32,
                                   c_void_p, c_void_p, c_void_p]),
     "eg_stream_copy": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p]),
+    "eg_dequant_blocks": (c_int32, [c_int32, c_void_p, c_int64, c_void_p, c_void_p]),
     "eg_ple_gate": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32,
                               c_int32, ctypes.c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_ple_conv_backward": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_int32, c_int32,
@@ -206,6 +210,9 @@ def load(path: Path | None = None) -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = restype
         fn.argtypes = argtypes
+    if lib.eg_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"HIP library {p} has ABI version {lib.eg_abi_version()}, this package needs "
+                           f"{ABI_VERSION}: rebuild it with `python engraft-ngram_amd/build.py`")
     if path is None:
         _LIB = lib
     return lib

@@ -580,7 +580,8 @@ struct SegArgs {
   float* v;
   int32_t* stamp;
   TableDev quant;         // fmt 0: no requantised copy
-  TableDev base;          // for the pull term
+  TableDev base;          // for the pull term (rows0 at the variables' ids)
+  const float* anchor;    // or rows0 per variable [n_var, dim]
   int64_t step;
   int32_t dense;          // stamp the rows hit (the dense pass skips them)
   float w1, b2, w2, bc2s, eps, neg_step_size, l2c;
@@ -750,7 +751,8 @@ __device__ void adam_apply(const SegArgs& a, int64_t k, int sub, const float g[V
     float gt = g[t];
     if (a.l2c != 0.0f) {
       const int32_t row0 = a.ids[k];
-      const float p0 = ((uint32_t)row0 < (uint64_t)a.base.n_rows)
+      const float p0 = a.anchor != nullptr ? a.anchor[k * a.dim + col_of<VPL, CONSEC>(sub, t)]
+                       : ((uint32_t)row0 < (uint64_t)a.base.n_rows)
                            ? load_value_rt(a.base, row0, col_of<VPL, CONSEC>(sub, t))
                            : __uint_as_float(0x7fc00000u);
       gt = gt + a.l2c * (2.0f * (p[t] - p0));
@@ -1305,11 +1307,12 @@ int eg_descent_apply(const void* d_out, int32_t d_out_f32, int64_t n_pos, int32_
                  "requantised rows must be Q8_0 or MXFP8");
     EG_CHECK_ARG(state->quant.dim == state->dim && state->quant.n_rows >= state->n, "requantised rows shape");
   }
-  if (opt->l2_coef != 0.0f) {
+  if (opt->l2_coef != 0.0f && opt->anchor == nullptr) {
     rc = make_table(base, &a.base, "base table");
     if (rc != EG_OK) return rc;
     EG_CHECK_ARG(base->dim == state->dim, "base table dim %d != state dim %d", base->dim, state->dim);
   }
+  a.anchor = opt->l2_coef != 0.0f ? opt->anchor : nullptr;
   const int64_t n = n_pos * heads;
   if (state->n == 0) return EG_OK;
   hipStream_t st = (hipStream_t)stream;

@@ -813,4 +813,47 @@ int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* r
   return launch_forward<true>(a, (hipStream_t)stream);
 }
 
+// GGML wire blocks (the byte form read_rows_raw returns) to f32, one value a
+// thread: Q8_0 [fp16 d][32 x int8], IQ4_NL [fp16 d][16 nibble bytes], MXFP8
+// [e8m0][32 x e4m3], BF16 and F32 one value a block.  Byte loads: the blocks
+// sit at 34-, 18- and 33-byte strides.
+__global__ __launch_bounds__(256) void dequant_wire_kernel(int fmt, const uint8_t* __restrict__ raw, int64_t n_values,
+                                                           float* __restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n_values; i += (int64_t)gridDim.x * 256) {
+    const int64_t b = i >> 5;
+    const int j = (int)(i & 31);
+    float y;
+    if (fmt == EG_FMT_Q8_0) {
+      const uint8_t* blk = raw + b * 34;
+      y = (float)(int8_t)blk[2 + j] * f16_to_f32((uint16_t)(blk[0] | ((uint32_t)blk[1] << 8)));
+    } else if (fmt == EG_FMT_IQ4_NL) {
+      const uint8_t* blk = raw + b * 18;
+      const uint32_t byte = blk[2 + (j & 15)];
+      y = iq4nl_value(j < 16 ? (byte & 15u) : (byte >> 4)) * f16_to_f32((uint16_t)(blk[0] | ((uint32_t)blk[1] << 8)));
+    } else if (fmt == EG_FMT_MXFP8) {
+      const uint8_t* blk = raw + b * 33;
+      y = e4m3_to_f32(blk[1 + j]) * e8m0_to_f32(blk[0]);
+    } else if (fmt == EG_FMT_BF16) {
+      y = __uint_as_float((uint32_t)(raw[2 * i] | ((uint32_t)raw[2 * i + 1] << 8)) << 16);
+    } else {
+      y = __uint_as_float((uint32_t)raw[4 * i] | ((uint32_t)raw[4 * i + 1] << 8) | ((uint32_t)raw[4 * i + 2] << 16) |
+                          ((uint32_t)raw[4 * i + 3] << 24));
+    }
+    out[i] = y;
+  }
+}
+
+int eg_dequant_blocks(int32_t fmt, const void* raw, int64_t n_blocks, float* out, void* stream) {
+  EG_CHECK_ARG(fmt >= EG_FMT_BF16 && fmt <= EG_FMT_F32, "fmt=%d is not an eg_row_format", fmt);
+  EG_CHECK_ARG(n_blocks >= 0 && n_blocks < (1LL << 40), "n_blocks=%lld outside [0, 2^40)", (long long)n_blocks);
+  EG_CHECK_ARG(n_blocks == 0 || (raw != nullptr && out != nullptr), "raw/out is NULL");
+  const int64_t per_block = (fmt == EG_FMT_BF16 || fmt == EG_FMT_F32) ? 1 : 32;
+  const int64_t n_values = n_blocks * per_block;
+  if (n_values == 0) return EG_OK;
+  const int64_t blocks = (n_values + 255) / 256 < 16384 ? (n_values + 255) / 256 : 16384;
+  hipLaunchKernelGGL(dequant_wire_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (int)fmt,
+                     (const uint8_t*)raw, n_values, out);
+  return launch_status("dequant_wire_kernel");
+}
+
 }  // extern "C"

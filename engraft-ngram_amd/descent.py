@@ -103,7 +103,7 @@ class DescentState:
     ``quant`` the requantised copy the forward reads (``None``: keep fp32 only)."""
 
     def __init__(self, ids: torch.Tensor, master: torch.Tensor, quant_fmt: str | None = "q8_0",
-                 base: DeviceTable | None = None):
+                 base: DeviceTable | None = None, anchor: torch.Tensor | None = None):
         if ids.dtype != torch.int32 or ids.dim() != 1:
             raise ValueError("ids must be a 1-D int32 tensor")
         if master.dtype != torch.float32 or master.dim() != 2 or master.shape[0] != ids.numel():
@@ -132,12 +132,19 @@ class DescentState:
         self.index = torch.empty(cap, dtype=torch.int64, device=dev)
         _lib.call("eg_build_row_index", _lib.ptr(self.ids), ids.numel(), _lib.ptr(self.index), cap,
                   _lib.stream_ptr(dev))
-        # ||rows0||^2 (engraft/descend_corpus.py:936) for the pull term.  rows0 are
-        # the true rows, which the step kernel reads from the base table as the
-        # anchor, so the denominator comes from the same rows (the master may
-        # start elsewhere, e.g. from a resumed overlay); without a base table
-        # the pull term is unavailable and the master stands in.
-        rows0 = base.gather(self.ids.reshape(-1, 1)) if (base is not None and ids.numel()) else self.master
+        # rows0 of the pull term mu*||rows_var - rows0||^2/||rows0||^2: the anchor
+        # rows when given (engraft/descend_corpus.py:780-781, 935-939: rows0 are
+        # the starting rows, a warm start's included), else the true rows, read
+        # by the step kernel from the base table (engraft/replica/descend.py:141,
+        # 252).  The denominator comes from the same rows as the anchor.
+        if anchor is not None:
+            if anchor.dtype != torch.float32 or tuple(anchor.shape) != tuple(self.master.shape):
+                raise ValueError("anchor must be f32 [len(ids), D] like master")
+            self.anchor = anchor.to(self.master.device).contiguous()
+            rows0 = self.anchor
+        else:
+            self.anchor = None
+            rows0 = base.gather(self.ids.reshape(-1, 1)) if (base is not None and ids.numel()) else self.master
         self.rows0_sq = float(rows0.pow(2).sum().clamp_min(1e-12).item()) if ids.numel() else 0.0
 
     @property
@@ -205,6 +212,11 @@ class DescentState:
         ws = plan.workspace if plan is not None and plan.workspace.numel() >= need else \
             torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
         st = self.c_state()
+        # the plan's buffers are used on this stream: the caching allocator must not hand
+        # them out elsewhere before its work is done, even when the plan is dropped unused
+        cur = torch.cuda.current_stream(dev)
+        ws.record_stream(cur)
+        rows.record_stream(cur)
         _lib.call("eg_descent_plan_slots" if direct else "eg_descent_plan", _lib.ptr(rows), n_pos, heads,
                   ctypes.byref(st), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
         return DescentPlan(self, rows, ws)
@@ -214,7 +226,8 @@ class DescentState:
              plan: "DescentPlan | None" = None, slot_var: torch.Tensor | None = None) -> None:
         """One optimizer step from ``d_out`` (bf16/f32 ``[n_pos, heads*D]``) and the
         slots' row ids ``rows`` (int32 ``[n_pos, heads]``).  ``mu``: the pull
-        term ``mu*||rows_var - rows0||^2/||rows0||^2`` (rows0 = the base table).
+        term ``mu*||rows_var - rows0||^2/||rows0||^2`` (rows0 = the state's
+        ``anchor`` rows, or the base table's rows of the ids without one).
 
         ``frozen``: bool ``[R]``, the variables held at their true rows -- the
         masked step of ``engraft/replica/descend.py:262-271`` (``row_mask`` =
@@ -274,10 +287,13 @@ class DescentState:
         opt.dense = 1 if dense else 0
         base = None
         if mu != 0.0:
-            if self.base is None:
-                raise ValueError("the pull term needs the base table (DescentState(base=...))")
+            if self.anchor is not None:
+                opt.anchor = _lib.ptr(self.anchor)
+            elif self.base is None:
+                raise ValueError("the pull term needs its rows0: DescentState(base=...) or (anchor=...)")
+            else:
+                base = self.base.c_table
             opt.l2_coef = float(np.float32(mu) / np.float32(self.rows0_sq))
-            base = self.base.c_table
         st = self.c_state()
         if plan is not None:
             ws = plan.workspace

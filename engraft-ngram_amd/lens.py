@@ -135,8 +135,10 @@ class RowSet:
         more than once must carry equal vectors every time (``ValueError``
         otherwise: NaN never equals itself, -0.0 equals 0.0).
 
-        All parts are concatenated and stably sorted by row; a run of equal
-        rows is compared against its first member and keeps it."""
+        All parts are concatenated and stably sorted by row; every later member
+        of a run of equal rows is compared against the run's first member, which
+        is kept.  A first member is never compared with itself, so a row seen
+        once is accepted whatever it holds (NaN included)."""
         rows_parts, data_parts = [], []
         dim = None
         for rows_global, data in parts:
@@ -158,7 +160,7 @@ class RowSet:
         head = np.ones(n, dtype=bool)
         head[1:] = rows[1:] != rows[:-1]
         first = np.flatnonzero(head)[np.cumsum(head) - 1]  # each entry's run head
-        clash = ~(data == data[first]).all(axis=1)
+        clash = ~head & ~(data == data[first]).all(axis=1)
         if clash.any():
             raise ValueError(f"build_overlay: global row {int(rows[np.flatnonzero(clash)[0]])} "
                              "receives two different vectors")

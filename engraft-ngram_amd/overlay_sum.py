@@ -6,9 +6,13 @@
 
 * gathers the true rows of every file row and of the union (``eg_gather``);
 * forms ``delta = rows_in_file - true_rows`` in fp32;
-* sums the deltas of every union row over the files (``eg_scatter_grad``
-  with one slot per file row, keyed by the union's sorted ids, so each row's
-  deltas are added in file order, deterministically);
+* sums the deltas of every union row over the files in file order, one
+  fp32 addition at a time, as ``np.add.at`` does in the reference
+  (``engraft/replica/overlay_sum.py:74-80``): ``eg_scatter_grad`` with one
+  slot per file row keyed by the union's sorted ids adds a row's slots in slot
+  order when no row has more than 32 of them; past that, each launch takes
+  one layer of rows that are unique within it (a file's first occurrences,
+  then its second ...), in file order, accumulating into the running sum;
 * adds the sum to the union's true rows.
 
 The manifest statistics (norms in float64, histograms) are computed on the
@@ -25,6 +29,28 @@ from .descent import scatter_grad, true_rows_device as _true_rows_dev
 from .lens import read_pleo, write_pleo
 
 QUANT_FLOOR = 0.055  # engraft/replica/overlay_sum.py:19 (recorded only)
+SEQUENTIAL_SLOTS = 32  # eg_scatter_grad adds at most this many slots of one row strictly in order
+
+
+def _unique_layers(file_sizes: list[int], all_rows: np.ndarray) -> list[np.ndarray]:
+    """Positions into the concatenated file rows, cut into layers whose rows
+    are unique within the layer, in the order ``np.add.at`` visits them: per
+    file, the first occurrence of each of its rows, then the second, ..."""
+    layers = []
+    start = 0
+    for size in file_sizes:
+        rows = all_rows[start:start + size]
+        order = np.argsort(rows, kind="stable")
+        srt = rows[order]
+        head = np.ones(size, dtype=bool)
+        head[1:] = srt[1:] != srt[:-1]
+        run_start = np.flatnonzero(head)[np.cumsum(head) - 1] if size else np.empty(0, np.int64)
+        occ = np.empty(size, dtype=np.int64)
+        occ[order] = np.arange(size) - run_start
+        for j in range(int(occ.max()) + 1 if size else 0):
+            layers.append(start + np.flatnonzero(occ == j))
+        start += size
+    return layers
 
 
 def delta_for_pleo(table, pleo_path) -> tuple[np.ndarray, np.ndarray]:
@@ -54,16 +80,24 @@ def sum_overlays(table, pleo_paths: list) -> tuple[np.ndarray, np.ndarray, dict]
 
     # per file row: delta against the true row, on the device
     delta = torch.as_tensor(all_data, device=dev) - _true_rows_dev(table, all_rows)
-    # sum over the files per union row: one slot per file row, in file order
+    # sum over the files per union row, in file order
     ids = torch.as_tensor(rows_union, device=dev)
-    delta_sum = scatter_grad(delta.contiguous(), torch.as_tensor(all_rows.astype(np.int32)).reshape(-1, 1), ids,
-                             row_len)
+    idx = np.searchsorted(rows_union, all_rows)
+    if n == 0 or int(np.bincount(idx, minlength=n).max()) <= SEQUENTIAL_SLOTS:
+        delta_sum = scatter_grad(delta.contiguous(), torch.as_tensor(all_rows.astype(np.int32)).reshape(-1, 1),
+                                 ids, row_len)
+    else:
+        delta_sum = torch.zeros((n, row_len), dtype=torch.float32, device=dev)
+        for layer in _unique_layers([r.shape[0] for r, _ in files], all_rows):
+            sel = torch.as_tensor(layer, device=dev)
+            scatter_grad(delta.index_select(0, sel).contiguous(),
+                         torch.as_tensor(all_rows[layer].astype(np.int32)).reshape(-1, 1), ids, row_len,
+                         grad=delta_sum)
     true_union = _true_rows_dev(table, rows_union)
     data_merged = (true_union + delta_sum).cpu().numpy()
 
     # manifest (host, float64 norms as the reference)
     d_host = delta.cpu().numpy()
-    idx = np.searchsorted(rows_union, all_rows)
     row_norms = np.linalg.norm(d_host.astype(np.float64), axis=1)
     moved = row_norms > 0.0
     moved_count = np.zeros(n, dtype=np.int64)

@@ -18,12 +18,17 @@ hidden, the history and the weights.  The backward runs
 ``eg_ple_conv_backward`` and ``eg_ple_gate_backward`` on the forward's saved
 intermediates, then the projections' backward (one ``gemm_f32`` or
 ``gemm_x3`` call over two K segments); when weights need gradients, also the
-two weight GEMMs (fp32, ``torch.matmul``) and ``eg_ple_weight_grads`` for the
-norm and convolution weights.  Only shapes beyond the HIP kernels' limits (more than 4
+two weight GEMMs (``gemm_f32`` with the positions as K) and
+``eg_ple_weight_grads`` for the norm and convolution weights.  The
+convolution takes 1..8 taps (the reference's blocks have 4; more raise
+``ValueError``).  Only shapes beyond the HIP backward's limits (more than 4
 streams, ``n_embd`` > 4096, a convolution reaching back more than 32 rows)
-fall back to a torch recomputation of the block, differentiated by
-autograd.  Either way the forward values are the HIP kernels'.  ``detach_value`` / ``detach_gate`` change only the backward, as in
-the reference.
+fall back to a recomputation of the block in torch elementwise operations
+around ``gemm_f32`` products, differentiated by autograd.  An input that a
+detached factor cuts off the output gets no gradient (None), as in the
+reference's graph.  Either way the forward values are the HIP kernels'.
+``detach_value`` / ``detach_gate`` change only the backward, as in the
+reference.
 
 ``PleReplica`` (below) is the same block with its weights read from the model
 GGUF, method for method as the reference's numpy replica.
@@ -55,15 +60,34 @@ def _rms(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     return x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + eps) * w
 
 
+class _GemmNT(torch.autograd.Function):
+    """``a @ b.T`` on eg_gemm_f32, differentiable: ``d_a = d b`` and
+    ``d_b = d^T a``, both on eg_gemm_f32 too."""
+
+    @staticmethod
+    def forward(ctx, a, b):
+        ctx.save_for_backward(a, b)
+        return gemm_f32(a.float(), b.float())
+
+    @staticmethod
+    def backward(ctx, d):
+        a, b = ctx.saved_tensors
+        d = d.float().contiguous()
+        d_a = gemm_f32(d, b.float().T).to(a.dtype) if ctx.needs_input_grad[0] else None
+        d_b = _weight_grad(d, a.float(), b).to(b.dtype) if ctx.needs_input_grad[1] else None
+        return d_a, d_b
+
+
 def _block_torch(emb, hidden, w_key, w_value, nk, nq, nc, conv, hist, eps, dil, detach_value, detach_gate):
-    """The block in torch operations (the backward's recomputation): ``(out,
+    """The block as elementwise torch operations around ``gemm_f32`` products
+    (the backward's recomputation beyond the HIP backward's limits): ``(out,
     new_hist)``."""
     t_len, hc, n = hidden.shape
-    key = _rms((emb @ w_key.T).reshape(t_len, hc, n), nk.reshape(hc, n), eps)
+    key = _rms(_GemmNT.apply(emb, w_key).reshape(t_len, hc, n), nk.reshape(hc, n), eps)
     query = _rms(hidden, nq.reshape(hc, n), eps)
     s = (key * query).sum(dim=-1) / (n ** 0.5)
     gate = torch.sigmoid(torch.sign(s) * torch.sqrt(torch.clamp(s.abs(), min=1e-6)))
-    value = emb @ w_value.T
+    value = _GemmNT.apply(emb, w_value)
     g = gate.detach() if detach_gate else gate
     v = value.detach() if detach_value else value
     gated = v.unsqueeze(1) * g.unsqueeze(-1)
@@ -300,9 +324,22 @@ def gemm_f32(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate
     return (out, out2) if n2 else out
 
 
-def _native_backward_ok(hc: int, n: int, taps: int, dil: int) -> bool:
-    """The HIP backward's built limits (eg_ple_gate_backward, eg_ple_conv_backward)."""
-    return hc <= 4 and n <= 4096 and (taps - 1) * dil <= 32
+WGRAD_MAX_TAPS = 8  # eg_ple_weight_grads' built tap counts (1..8)
+
+
+def _weight_grad(d_y: torch.Tensor, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``d_y^T x`` (``[out, T]`` x ``[T, in]``), the gradient of ``w`` in
+    ``y = x w^T``, on eg_gemm_f32 with the positions as K (both operands
+    transposed into K-contiguous copies by the GEMM wrapper)."""
+    if d_y.shape[0] == 0:
+        return torch.zeros_like(w)
+    return gemm_f32(d_y.T, x.T)
+
+
+def _native_backward_ok(hc: int, n: int, taps: int, dil: int, weights: bool = False) -> bool:
+    """The HIP backward's built limits (eg_ple_gate_backward, eg_ple_conv_backward,
+    and with ``weights`` eg_ple_weight_grads)."""
+    return hc <= 4 and n <= 4096 and (taps - 1) * dil <= 32 and (not weights or taps <= WGRAD_MAX_TAPS)
 
 
 class _PleFn(torch.autograd.Function):
@@ -335,7 +372,8 @@ class _PleFn(torch.autograd.Function):
         nk32, nq32, nc32 = (x.to(**f32).contiguous() for x in (nk, nq, nc))
         conv32 = conv.to(**f32).contiguous()
         taps = conv32.shape[1]
-        native = any(ctx.needs_input_grad) and _native_backward_ok(hc, n, taps, int(dil))
+        native = any(ctx.needs_input_grad) and _native_backward_ok(hc, n, taps, int(dil),
+                                                                   weights=any(ctx.needs_input_grad[2:8]))
         rstd = torch.empty((t_len, hc, 3), **f32) if native else None
         _lib.call("eg_ple_gate", _lib.ptr(key), _lib.ptr(value), _lib.ptr(hidden32), _lib.ptr(nk32), _lib.ptr(nq32),
                   _lib.ptr(nc32), t_len, hc, n, float(eps), _lib.ptr(full[h0:]), _lib.ptr(s), _lib.ptr(gate),
@@ -377,10 +415,9 @@ class _PleFn(torch.autograd.Function):
                 outs.append(new_hist)
                 grads_in.append(d_hist)
             grads = iter(torch.autograd.grad(outs, wrt, grads_in, allow_unused=True) if wrt else [])
-        res = []
-        for x, need in zip(leaves, ctx.needs_input_grad[:9]):
-            g = next(grads) if need else None
-            res.append(torch.zeros_like(x) if (need and g is None) else g)
+        # an input the detached graph does not reach keeps autograd's None, as
+        # in the reference's own graph (its .grad stays None)
+        res = [next(grads) if need else None for need in ctx.needs_input_grad[:9]]
         return (*res, None, None, None, None, None)
 
     @staticmethod
@@ -418,12 +455,10 @@ class _PleFn(torch.autograd.Function):
                           st)
             d_emb = None
             if need_emb:
+                # with both factors detached emb has no path to the output: None, as autograd gives
                 parts = [(d, _WT.get(w)) for d, w in ((pk, wk32), (pv, wv32)) if d is not None]
                 if parts:
-                    d_emb = gemm_x3(*[x for part in parts for x in part], cache_b=True)
-                else:
-                    d_emb = torch.zeros((t_len, n), **f32)
-                d_emb = d_emb.to(emb_dt)
+                    d_emb = gemm_x3(*[x for part in parts for x in part], cache_b=True).to(emb_dt)
             d_hist_in = d_full[:h0].reshape(h0, hc, n).to(hist_dt) if need_hist else None
             return (d_emb, d_hidden.to(hidden_dt) if d_hidden is not None else None, None, None, None, None, None,
                     None, d_hist_in, None, None, None, None, None)
@@ -439,14 +474,9 @@ class _PleFn(torch.autograd.Function):
             # the projections' backward, d_emb = d_key w_key + d_value w_value, as
             # products with the weights' transposes (kept between steps)
             parts = [(d, _WT.get(w)) for d, w in ((d_key, wk32), (d_value, wv32)) if d is not None]
-            if not parts:
-                d_emb = torch.zeros((t_len, n), **f32)
-            elif ctx.gemm == "bf16x3":
+            if parts:  # none: both factors detached, emb has no path to the output
                 flat = [x for part in parts for x in part]
-                d_emb = gemm_x3(*flat, cache_b=True)
-            else:
-                d_emb = gemm_f32(*[x for part in parts for x in part])
-            d_emb = d_emb.to(emb_dt)
+                d_emb = (gemm_x3(*flat, cache_b=True) if ctx.gemm == "bf16x3" else gemm_f32(*flat)).to(emb_dt)
         d_hist_in = d_full[:h0].reshape(h0, hc, n).to(hist_dt) if need_hist else None
         return (d_emb, d_hidden.to(hidden_dt) if d_hidden is not None else None, None, None, None, None, None, None,
                 d_hist_in, None, None, None, None, None)
@@ -481,19 +511,16 @@ class _PleFn(torch.autograd.Function):
         d_emb = None
         if need_emb:
             parts = [(d, _WT.get(w)) for d, w in ((d_key, wk32), (d_value, wv32)) if d is not None]
-            if not parts:
-                d_emb = torch.zeros((t_len, n), **f32)
-            elif ctx.gemm == "bf16x3":
-                d_emb = gemm_x3(*[x for part in parts for x in part], cache_b=True)
-            else:
-                d_emb = gemm_f32(*[x for part in parts for x in part])
-            d_emb = d_emb.to(emb_dt)
+            if parts:  # none: both factors detached, emb has no path to the output
+                flat = [x for part in parts for x in part]
+                d_emb = (gemm_x3(*flat, cache_b=True) if ctx.gemm == "bf16x3" else gemm_f32(*flat)).to(emb_dt)
         wdt = ctx.w_dtypes
-        d_wk = d_wv = None
-        if need_wk:
-            d_wk = (d_key.T @ emb32 if d_key is not None else torch.zeros_like(wk32)).to(wdt[0])
-        if need_wv:
-            d_wv = (d_value.T @ emb32 if d_value is not None else torch.zeros_like(wv32)).to(wdt[1])
+        # the projection weights' gradients d_key^T emb and d_value^T emb on eg_gemm_f32
+        # (K = the positions); a weight the detached factor cuts off keeps None
+        d_wk = _weight_grad(d_key, emb32, wk32).to(wdt[0]) if (need_wk and d_key is not None) else None
+        d_wv = _weight_grad(d_value, emb32, wv32).to(wdt[1]) if (need_wv and d_value is not None) else None
+        if detach_gate:  # the gate's whole branch (key, its norm, the query norm) is detached
+            need_nk = need_nq = False
         d_nk = d_nq = d_nc = d_cv = None
         if need_nk or need_nq or need_nc or need_cv:
             taps = conv32.shape[1]
@@ -635,8 +662,7 @@ class PleReplica:
     def _gate_pass(self, emb: torch.Tensor, hidden: torch.Tensor):
         """value [T, n], normed [T, hc*n], s and gate [T, hc] (eg_ple_gate)."""
         t_len = emb.shape[0]
-        key = (emb @ self.w_key.T).contiguous()
-        value = (emb @ self.w_value.T).contiguous()
+        key, value = gemm_f32(emb, self.w_key, b_n2=self.w_value)
         f32 = dict(dtype=torch.float32, device=self.device)
         normed = torch.empty((t_len, self.hc * self.n_embd), **f32)
         s = torch.empty((t_len, self.hc), **f32)
@@ -659,12 +685,12 @@ class PleReplica:
     def key(self, emb) -> torch.Tensor:
         """``[T, n] -> [T, hc, n]``, RMS-normalised per stream (``lens.py:289-294``)."""
         emb = self._in(emb, self.n_embd)
-        raw = (emb @ self.w_key.T).contiguous()
+        raw = gemm_f32(emb, self.w_key)
         return self._rms(raw, self.norm_key).reshape(-1, self.hc, self.n_embd)
 
     def value(self, emb) -> torch.Tensor:
         """``[T, n] -> [T, n]`` (``lens.py:296-299``)."""
-        return self._in(emb, self.n_embd) @ self.w_value.T
+        return gemm_f32(self._in(emb, self.n_embd), self.w_value)
 
     def gate(self, emb, hidden) -> torch.Tensor:
         """``[T, hc]`` (``lens.py:301-312``)."""

@@ -291,6 +291,34 @@ def ple_true_emb_range(table, tokens, start: int, end: int, overlay=None, seg_st
     return table.gather(rows[start:end].contiguous(), overlay=_as_overlay(table, overlay))
 
 
+def exclusive_rows_at_position(table, tokens: list[int], n_positions: int, p: int,
+                               heads: range | None = None) -> set[int]:
+    """Global rows of position ``p`` (among ``heads``, default all) that no
+    other position ``0..n_positions-1`` reads (``engraft/replica/seq.py:
+    924-941``): the rows over which a sequence gradient can be compared with
+    an isolated single-step one.
+
+    One ``eg_hash_rows`` over the whole ``tokens`` stream gives every
+    position's rows (position ``t``'s rows depend only on its own n-gram
+    window, so this is the reference's per-position ``RowSet`` loop), then a
+    set difference on the host.  ``p`` indexes like the reference's list
+    index (a negative ``p`` counts from the end and is never skipped as
+    "itself"); positions past the stream raise ``IndexError`` as there."""
+    heads = heads if heads is not None else range(table.n_heads)
+    n_tok = len(tokens)
+    if n_tok == 0 or n_positions > n_tok:
+        raise IndexError(f"positions [0, {max(n_positions, 1)}) outside a stream of {n_tok} tokens")
+    tok = tokens if isinstance(tokens, torch.Tensor) else torch.as_tensor(np.asarray(tokens, dtype=np.int64))
+    rows = table.rows(tok).cpu().numpy()
+    row_p = rows[p]
+    candidates = {int(row_p[h]) for h in heads}
+    n = max(int(n_positions), 0)
+    others = rows[:n]
+    if 0 <= p < n:
+        others = np.delete(others, p, axis=0)
+    return candidates - set(np.unique(others).tolist())
+
+
 class ReplicaTableMixin:
     """``Replica.ple_true_emb`` as a method (``engraft/replica/model.py:473-495``):
     a model class that keeps its table in ``self.table``, as the reference's

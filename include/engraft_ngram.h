@@ -13,6 +13,8 @@
  *                     vectorized ngram_rows          engraft/damage.py:68-104)
  *   eg_gather        PleTable.read_rows(_raw) + dequant_iq4nl
  *                                                    engraft/table.py:90-109,147-169
+ *   eg_dequant_blocks  dequant_q8_0 / _bf16 / _iq4_nl / _f32 of the wire form
+ *                                                    engraft/replica/dequant.py:71-147
  *                    _read_true_rows                 engraft/replica/distill.py:378-395
  *   eg_forward       RowSet.from_position per position + overlay substitution
  *                    + the residual consumer         engraft/lens.py:126-136,
@@ -47,7 +49,7 @@
 extern "C" {
 #endif
 
-#define EG_ABI_VERSION 2
+#define EG_ABI_VERSION 3
 
 #define EG_MAX_NGRAM 4   /* context slots per hash (2-, 3- and 4-grams) */
 #define EG_MAX_HEADS 32  /* row slots per position and table layer */
@@ -193,6 +195,16 @@ int eg_forward_timed(int32_t n_layers, const eg_hash_spec* specs, const eg_table
 int eg_gather(const eg_table* table, const eg_overlay* overlay, const int32_t* rows,
               int64_t n_pos, int32_t heads, float* out, void* stream);
 
+/* Dequantisation of rows in their GGML wire form (the bytes read_rows_raw
+ * returns), n_blocks blocks of format fmt -> out f32:
+ *   EG_FMT_Q8_0    34-byte blocks [fp16 d][32 x int8]      -> 32 values, y = f32(q) * f32(d)
+ *   EG_FMT_IQ4_NL  18-byte blocks [fp16 d][16 nibble bytes] -> 32 values
+ *   EG_FMT_MXFP8   33-byte blocks [e8m0][32 x e4m3]          -> 32 values
+ *   EG_FMT_BF16    2-byte blocks -> 1 value (bits << 16); EG_FMT_F32 4 bytes -> 1 value.
+ * raw may sit at any byte alignment.  Replaces dequant_q8_0 / dequant_bf16 /
+ * dequant_iq4_nl / dequant_f32 (engraft/replica/dequant.py:71-93,127-147). */
+int eg_dequant_blocks(int32_t fmt, const void* raw, int64_t n_blocks, float* out, void* stream);
+
 /* ---- descent backward ----------------------------------------------------
  * The overlay variables are R rows with sorted unique global ids
  * (engraft/replica/distill.py:401-453 row_map, ascending).  Every slot (p, h)
@@ -210,7 +222,11 @@ typedef struct eg_adam {
   int32_t dense;    /* 1: every variable row steps, as torch.optim.Adam([rows_var]) does;
                        0: only the rows hit by this batch (sparse / lazy Adam) */
   float l2_coef;    /* mu / ||rows0||^2 of engraft/descend_corpus.py:935-939 (0: no pull
-                       term); rows0 = the base table rows of the variables */
+                       term) */
+  const float* anchor; /* DEVICE f32 [R, dim]: rows0 of the pull term, row k for variable k
+                          (descend_corpus's warm-start rows, :780-781); NULL: rows0 = the base
+                          table's rows of the variables' ids (replica/descend.py:141, the true
+                          rows) */
 } eg_adam;
 
 /* Optimizer state of the R overlay variables, all device memory. */
@@ -249,7 +265,8 @@ int eg_scatter_grad(const void* d_out, int32_t d_out_f32, const int32_t* rows, i
 
 /* One descent step: gradient as eg_scatter_grad, then Adam on state->master/m/v
  * (torch's single-tensor op order, fp32), then requantisation into state->quant.
- * base: the table the variables were read from (needed when opt->l2_coef != 0). */
+ * base: the table the variables were read from (needed when opt->l2_coef != 0 and
+ * opt->anchor is NULL). */
 int eg_descent_step(const void* d_out, int32_t d_out_f32, const int32_t* rows, int64_t n_pos,
                     int32_t heads, const eg_descent_state* state, const eg_adam* opt,
                     const eg_table* base, void* workspace, size_t workspace_bytes, void* stream);

@@ -192,6 +192,48 @@ def row_is_zero(raw) -> np.ndarray:
 
 
 # ----------------------------------------------------------------------------
+# GGML wire blocks (read_rows_raw's byte form)
+# ----------------------------------------------------------------------------
+
+WIRE_BLOCK_BYTES = {"f32": 4, "bf16": 2, "q8_0": 34, "iq4_nl": 18, "mxfp8": 33}
+
+
+def wire_rows(fmt: str, payload, scales=None) -> np.ndarray:
+    """Split-layout rows as GGML wire bytes ``uint8 [n, blocks*block_bytes]``:
+    per 32-value block the scale (fp16 ``d`` for Q8_0, the e8m0 byte for
+    MXFP8) then the 32 values; BF16/F32 rows are their own bytes; IQ4_NL rows
+    are wire blocks already."""
+    if fmt in ("bf16", "f32", "iq4_nl"):
+        p = np.ascontiguousarray(payload)
+        return p.view(np.uint8).reshape(p.shape[0], -1)
+    q = np.ascontiguousarray(payload).view(np.uint8)
+    n, dim = q.shape
+    sc = np.ascontiguousarray(scales).view(np.uint8).reshape(n, dim // BLOCK, -1)
+    return np.concatenate([sc, q.reshape(n, dim // BLOCK, BLOCK)], axis=2).reshape(n, -1)
+
+
+def dequant_wire(fmt: str, blocks) -> np.ndarray:
+    """``uint8 [..., block_bytes]`` wire blocks -> ``f32 [..., values]``
+    (``engraft/replica/dequant.py:71-93, 127-147``): split back into payload
+    and scales and decoded by the split-layout functions above."""
+    b = np.ascontiguousarray(np.asarray(blocks, dtype=np.uint8))
+    lead = b.shape[:-1]
+    assert b.shape[-1] == WIRE_BLOCK_BYTES[fmt]
+    b = b.reshape(-1, b.shape[-1])
+    if fmt == "f32":
+        out = b.copy().view(np.float32)
+    elif fmt == "bf16":
+        out = bf16_bits_to_f32(b.copy().view(np.uint16))
+    elif fmt == "iq4_nl":
+        out = dequant_iq4nl(b)
+    elif fmt == "q8_0":
+        out = dequant_q8_0(b[:, 2:].copy().view(np.int8), b[:, :2].copy().view(np.float16))
+    else:
+        out = dequant_mxfp8(b[:, 1:].copy(), b[:, :1].copy())
+    return out.reshape(*lead, out.shape[-1])
+
+
+# ----------------------------------------------------------------------------
 # generic dispatch
 # ----------------------------------------------------------------------------
 

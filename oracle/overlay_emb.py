@@ -46,6 +46,22 @@ def row_set(spec: H.HashSpec, tokens: list[int], t: int, fetch):
     return rows, fetch(rows)
 
 
+def exclusive_rows_at_position(spec: H.HashSpec, tokens: list[int], n_positions: int, p: int, heads=None) -> set:
+    """``engraft/replica/seq.py:924-941``: the rows of position ``p`` (among
+    ``heads``) minus every row read at another position ``0..n_positions-1``,
+    with the per-position ``row_set`` loop of the reference."""
+    heads = heads if heads is not None else range(spec.n_heads)
+    fetch0 = lambda r: None  # noqa: E731  (rows only)
+    rows_p, _ = row_set(spec, tokens, p if p >= 0 else len(tokens) + p, fetch0)
+    candidates = {int(rows_p[h]) for h in heads}
+    for t in range(n_positions):
+        if t == p:
+            continue
+        rows_t, _ = row_set(spec, tokens, t, fetch0)
+        candidates -= {int(g) for g in rows_t}
+    return candidates
+
+
 def build_plan(spec: H.HashSpec, tokens: list[int], row_map: dict, n_positions: int, start: int = 0,
                segment_ids=None, fetch=None):
     """``OverlayEmb.build``'s cached part (``engraft/replica/seq.py:385-426``):

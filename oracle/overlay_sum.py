@@ -3,9 +3,9 @@ oracle/__init__.py).
 
 ``sum_overlays`` restates ``engraft/replica/overlay_sum.py:38-112`` with the
 true rows supplied by ``fetch(ids)``: ``delta_i = rows_i - true`` in fp32, the
-union of the files' rows ascending, ``np.add.at`` of the deltas in file order
-(the device sums each union row's deltas in the same order, with the
-association of ``oracle.backward.segment_sum`` beyond 32 files), and
+union of the files' rows ascending, ``np.add.at`` of each file's deltas into
+one fp32 running sum, file after file (``engraft/replica/overlay_sum.py:74-80``:
+one addition at a time, in file order, for any number of files), and
 ``merged = true_union + delta_sum``.  ``write_merged_rows`` restates the row
 order of ``engraft/descend_corpus.py:627-647``.
 
@@ -18,8 +18,6 @@ from __future__ import annotations
 
 import numpy as np
 
-from oracle import backward as B
-
 
 def sum_overlays(files: list[tuple[np.ndarray, np.ndarray]], fetch) -> tuple[np.ndarray, np.ndarray, dict]:
     rows_union = np.array(sorted({int(r) for rows, _ in files for r in rows.tolist()}), dtype=np.int32)
@@ -29,14 +27,10 @@ def sum_overlays(files: list[tuple[np.ndarray, np.ndarray]], fetch) -> tuple[np.
     per_file = []
     for rows, data in files:
         per_file.append((rows, (np.asarray(data, np.float32) - fetch(rows).astype(np.float32)).astype(np.float32)))
-    # delta sum per union row, file order, with the device's association
-    all_idx = np.concatenate([[row_index[int(g)] for g in rows.tolist()] for rows, _ in per_file]).astype(np.int64)
-    all_delta = np.concatenate([d for _, d in per_file])
+    # delta sum per union row: file after file, np.add.at (sequential fp32)
     delta_sum = np.zeros((n, row_len), dtype=np.float32)
-    for k in range(n):
-        sel = np.flatnonzero(all_idx == k)
-        if sel.size:
-            delta_sum[k] = B.segment_sum(all_delta[sel])
+    for rows, delta in per_file:
+        np.add.at(delta_sum, np.array([row_index[int(g)] for g in rows.tolist()], dtype=np.int64), delta)
     moved_count = np.zeros(n, dtype=np.int64)
     abs_sum = np.zeros(n, dtype=np.float64)
     for rows, delta in per_file:

@@ -197,6 +197,42 @@ def test_dense_with_pull_term_against_torch_adam(cuda):
     _rel_ok(st.master.cpu().numpy(), rv.detach().numpy())
 
 
+@pytest.mark.parametrize("anchor", [True, False])
+def test_warm_start_pull_term_anchor(cuda, anchor):
+    """A warm start (rows_var starting away from the true rows): with
+    ``anchor`` the pull term's rows0 are the warm rows, as in
+    engraft/descend_corpus.py:780-781, 935-939; without it rows0 are the true
+    rows of the base table, as in engraft/replica/descend.py:141, 252.  Three
+    dense steps against torch.optim.Adam on the CPU with that rows0."""
+    from engraft_ngram_amd import descent as D
+    spec = synthetic_spec(n_rows=16 * 2000, seed=181)
+    tab = G.device_table(spec, "q8_0", 16 * 2000, 128, seed=182)
+    tokens = synth.zipf_tokens(183, 1024, 3000)
+    rows = H.ngram_rows_np(spec, tokens)
+    ids = np.unique(rows).astype(np.int32)
+    true = G.synth_fetch("q8_0", 182, 128)(ids)
+    warm = (true + np.random.default_rng(184).standard_normal(true.shape).astype(np.float32) * 0.01).astype(
+        np.float32)
+    ids_d = torch.from_numpy(ids).to(cuda)
+    warm_d = torch.from_numpy(warm).to(cuda)
+    st = D.DescentState(ids_d, warm_d.clone(), base=tab, anchor=warm_d.clone() if anchor else None)
+    rv = torch.from_numpy(warm.copy()).requires_grad_(True)
+    r0 = torch.from_numpy((warm if anchor else true).copy())
+    opt = torch.optim.Adam([rv], lr=1e-3)
+    mu = 0.1
+    for k in range(3):
+        sub = rows[k * 300:(k + 1) * 300]
+        d = (torch.randn((300, 2048), device=cuda) * 1e-3).to(torch.bfloat16)
+        st.step(d, torch.from_numpy(sub.astype(np.int32)), lr=1e-3, dense=True, mu=mu)
+        grad, _ = B.scatter_grad(d.float().cpu().numpy(), sub, ids)
+        opt.zero_grad()
+        rv.grad = torch.from_numpy(grad)
+        reg = mu * ((rv - r0).pow(2).sum() / r0.pow(2).sum().clamp_min(1e-12))
+        reg.backward()
+        opt.step()
+    _rel_ok(st.master.cpu().numpy(), rv.detach().numpy())
+
+
 def test_updated_rows_read_back_through_forward_overlay(cuda):
     """The requantised rows of a step are what the next forward reads
     (overlay-vs-base resolved per id on the device)."""

@@ -645,3 +645,45 @@ def test_forward_slots_two_layers_with_overlays(cuda):
         assert np.array_equal(sv[l], exp[l]), l
     assert (sv >= 0).any() and (sv == -1).any()
     assert torch.equal(call.out.view(torch.int16), plain.view(torch.int16))
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "bf16", "f32", "iq4_nl", "mxfp8"])
+def test_dequant_wire_blocks_against_oracle(cuda, fmt):
+    """eg_dequant_blocks (the dequant_q8_0 / dequant_bf16 / dequant_iq4_nl /
+    dequant_f32 drop-ins, engraft/replica/dequant.py:71-147) on every byte
+    pattern of random blocks, against the oracle's wire decode (bit-exact;
+    NaN where the oracle has NaN); then read_rows_raw's wire form of a device
+    table decoded by the drop-in equals read_rows."""
+    from engraft_ngram_amd import _lib, dequant
+    from oracle import formats as F
+    print(f"[gpu-test] dequant wire blocks {fmt}", flush=True)
+    bb = F.WIRE_BLOCK_BYTES[fmt]
+    raw = np.random.default_rng(3).integers(0, 256, (1000 * 3 + 7, bb)).astype(np.uint8)
+    want = F.dequant_wire(fmt, raw)
+    if fmt == "mxfp8":
+        out = torch.empty((raw.shape[0], 32), dtype=torch.float32, device=cuda)
+        src = torch.as_tensor(raw, device=cuda)
+        _lib.call("eg_dequant_blocks", _lib.FMT_CODES[fmt], _lib.ptr(src), raw.shape[0], _lib.ptr(out),
+                  _lib.stream_ptr(cuda))
+        got = out.cpu().numpy()
+    else:
+        fn = dequant.DEQUANT_FNS[fmt.upper()]
+        got = fn(torch.as_tensor(raw, device=cuda).reshape(1000 * 3 + 7, bb)).cpu().numpy()
+        # a CPU tensor comes back on the CPU; out_dtype as the reference's .to()
+        fin = np.flatnonzero(np.isfinite(want).all(axis=1))[:5]
+        cpu_in = torch.as_tensor(raw[fin].reshape(5, 1, bb))
+        back = fn(cpu_in, out_dtype=torch.bfloat16)
+        assert back.device.type == "cpu" and back.dtype == torch.bfloat16 and back.shape[:2] == (5, 1)
+        assert torch.equal(back.reshape(5, -1), torch.as_tensor(want[fin]).to(torch.bfloat16))
+        with pytest.raises(AssertionError):
+            fn(torch.zeros((2, bb + 1), dtype=torch.uint8, device=cuda))
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    if fmt in ("q8_0", "bf16"):
+        spec = synthetic_spec(n_rows=16 * 300, seed=4)
+        tab = G.device_table(spec, fmt, 16 * 300, 128, seed=5)
+        raw_rows = tab.read_rows_raw(3, 17, 40)
+        fn = dequant.DEQUANT_FNS[fmt.upper()]
+        dec = fn(torch.from_numpy(raw_rows).reshape(40, -1, bb)).reshape(40, -1).numpy()
+        assert np.array_equal(dec, tab.read_rows(3, 17, 40))

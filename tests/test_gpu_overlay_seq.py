@@ -263,8 +263,9 @@ def test_scan_overlay_rank_bitmap(cuda):
 @pytest.mark.parametrize("n_files", [4, 40])
 def test_sum_overlays_against_oracle(cuda, tmp_path, n_files):
     """engraft/replica/overlay_sum.py:38-112 on the device: the union, the
-    merged rows (bit-exact; 40 files put 40 deltas on one row, past the
-    32-slot sequential range) and the manifest; write_merged_pleo's order."""
+    merged rows bit-exact against the reference's order (each row's deltas
+    added one at a time, file after file; 40 files put 40 deltas on a row,
+    one file lists a row twice) and the manifest; write_merged_pleo's order."""
     from engraft_ngram_amd import lens, overlay_sum
     from oracle import overlay_sum as OS
     spec = synthetic_spec(n_rows=16 * 2000, seed=71)
@@ -278,6 +279,9 @@ def test_sum_overlays_against_oracle(cuda, tmp_path, n_files):
                                          always])).astype(np.int32)
         data = (fetch(rows) + rng.standard_normal((rows.size, 128)) * 1e-2).astype(np.float32)
         data[::4] = fetch(rows[::4])
+        if i == 1:  # a row listed twice in one file: both deltas count, in file order
+            rows = np.concatenate([rows, rows[-1:]])
+            data = np.concatenate([data, data[-1:] + np.float32(1e-3)])
         path = tmp_path / f"f{i}.pleo"
         lens.write_pleo(path, rows, data)
         paths.append(path)
@@ -326,3 +330,35 @@ def test_lookup_rows_sorted_search_edges(cuda):
                   _lib.ptr(counts), _lib.stream_ptr(cuda))
         assert np.array_equal(out.cpu().numpy(), exp), n
         assert np.array_equal(counts.cpu().numpy(), np.bincount(exp[exp >= 0], minlength=n)), n
+
+
+def test_exclusive_rows_at_position_against_oracle(cuda):
+    """engraft/replica/seq.py:924-941 from one device hash: against the
+    oracle's per-position RowSet loop on a stream whose n-grams repeat (rows
+    reused at other positions), at the first, a middle and the last position,
+    a position past n_positions, a negative position, and a head subset."""
+    from engraft_ngram_amd import seq
+    _say("exclusive_rows_at_position")
+    spec = fake_table_spec(11, head_vocab_size=200)  # 6 token values: bigrams repeat, trigrams less
+    tab, _ = G.f32_table(spec, 32, seed=12)
+    rng = np.random.default_rng(13)
+    tokens = rng.integers(0, 6, 60).tolist()
+    tokens[20] = spec.eos_token_id
+    n_pos = 48
+    cases = [(0, None), (17, None), (n_pos - 1, None), (len(tokens) - 1, None), (-1, None), (-13, None),
+             (30, range(0, 8)), (5, range(8, 16))]
+    sizes = []
+    for p, heads in cases:
+        got = seq.exclusive_rows_at_position(tab, tokens, n_pos, p, heads)
+        want = OE.exclusive_rows_at_position(spec, tokens, n_pos, p, heads)
+        assert got == want, (p, heads)
+        sizes.append(len(got))
+    # whole sets, sets cut by rows reused elsewhere, and empty ones all occur
+    assert 16 in sizes and 0 in sizes and any(0 < k < 16 for k in sizes[:6])
+    # a row read again at another position is excluded: repeat position 3's window at 40
+    tokens2 = list(tokens)
+    tokens2[38:41] = tokens2[1:4]
+    got = seq.exclusive_rows_at_position(tab, tokens2, 45, 3)
+    assert got == OE.exclusive_rows_at_position(spec, tokens2, 45, 3) == set()
+    with pytest.raises(IndexError):
+        seq.exclusive_rows_at_position(tab, tokens, len(tokens) + 1, 0)

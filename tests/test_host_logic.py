@@ -156,6 +156,54 @@ def test_build_overlay_dedup_and_conflict():
                                    (np.array([5]), np.full((1, 160), 2.0, np.float32))])
 
 
+def _build_overlay_dict_loop(parts):
+    """The reference's dict loop (``engraft/lens.py:177-198``) as a plain
+    specification: a row's first vector is stored without any comparison,
+    every later one must be ``np.array_equal`` to it."""
+    seen = {}
+    for rows_global, data in parts:
+        for r, vec in zip(np.asarray(rows_global).tolist(), np.asarray(data, np.float32)):
+            if r in seen:
+                if not np.array_equal(seen[r], vec):
+                    raise ValueError(r)
+            else:
+                seen[r] = vec
+    keys = sorted(seen)
+    return np.array(keys, np.int32), np.stack([seen[k] for k in keys])
+
+
+def test_build_overlay_nan_row_seen_once_is_accepted():
+    """A NaN-bearing row listed once is stored as given, NaN bits and all;
+    a row with a NaN listed twice is rejected, as np.array_equal rejects it."""
+    lens, _, _, _ = _pkg()
+    d = np.arange(2 * 6, dtype=np.float32).reshape(2, 6)
+    d[1, 3] = np.nan
+    parts = [(np.array([5, 9]), d), (np.array([5]), d[:1].copy())]
+    rows, data = lens.RowSet.build_overlay(parts)
+    want_rows, want_data = _build_overlay_dict_loop(parts)
+    assert rows.tolist() == want_rows.tolist() == [5, 9]
+    assert data.tobytes() == want_data.tobytes()
+    assert np.isnan(data[1, 3]) and np.isfinite(np.delete(data[1], 3)).all()
+    twice = [(np.array([9]), d[1:]), (np.array([9]), d[1:].copy())]
+    with pytest.raises(ValueError):
+        _build_overlay_dict_loop(twice)
+    with pytest.raises(ValueError):
+        lens.RowSet.build_overlay(twice)
+
+
+def test_build_overlay_signed_zero_equal():
+    """-0.0 and 0.0 compare equal under np.array_equal, so a row carrying
+    both is accepted, and the first member's bits are kept."""
+    lens, _, _, _ = _pkg()
+    a = np.zeros((1, 4), np.float32)
+    b = a.copy()
+    b[0, 2] = -0.0
+    rows, data = lens.RowSet.build_overlay([(np.array([3]), b), (np.array([3]), a)])
+    want_rows, want_data = _build_overlay_dict_loop([(np.array([3]), b), (np.array([3]), a)])
+    assert rows.tolist() == want_rows.tolist() == [3]
+    assert data.tobytes() == want_data.tobytes() == b.tobytes()
+
+
 def test_overlay_key_len():
     _, _, seq, _ = _pkg()
     assert seq.overlay_key_len({1: 0, 7: 1}) is None

@@ -161,3 +161,50 @@ def test_zipf_tokens_distribution():
     w = np.arange(1, 151_937, dtype=np.float64) ** -1.1
     p1 = 1.0 / w.sum()
     assert abs(top[0] / 200_000 - p1) < 0.01
+
+
+def test_wire_blocks_known_answers():
+    """Hand-computed wire blocks: Q8_0 with d = 0.5 (fp16 0x3800), BF16 1.0
+    and -2.0, F32 bytes, IQ4_NL with d = 1 and nibble 0 / 15 (-127 / 113)."""
+    q8 = np.zeros(34, np.uint8)
+    q8[0:2] = [0x00, 0x38]
+    q = np.zeros(32, np.int8)
+    q[0], q[1], q[31] = -127, 1, 127
+    q8[2:] = q.view(np.uint8)
+    y = F.dequant_wire("q8_0", q8[None])[0]
+    want = np.zeros(32, np.float32)
+    want[0], want[1], want[31] = -63.5, 0.5, 63.5
+    assert np.array_equal(y, want)
+    bf = np.array([[0x80, 0x3F], [0x00, 0xC0]], np.uint8)
+    assert F.dequant_wire("bf16", bf).tolist() == [[1.0], [-2.0]]
+    assert F.dequant_wire("f32", np.array([[0, 0, 0x80, 0xBF]], np.uint8)).tolist() == [[-1.0]]
+    iq = np.zeros(18, np.uint8)
+    iq[0:2] = [0x00, 0x3C]  # fp16 1.0
+    iq[2] = 0xF0            # value 0: low nibble 0, value 16: high nibble 15
+    y = F.dequant_wire("iq4_nl", iq[None])[0]
+    assert y[0] == -127.0 and y[16] == 113.0 and y[1] == -127.0
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "mxfp8", "bf16", "f32", "iq4_nl"])
+def test_wire_blocks_agree_with_split_layout(fmt):
+    """The wire form of split-layout rows decodes to the split layout's own
+    values (the two layouts hold the same rows)."""
+    rng = np.random.default_rng(5)
+    n, dim = 7, 96
+    if fmt == "q8_0":
+        payload = rng.integers(-127, 128, (n, dim)).astype(np.int8)
+        scales = (rng.standard_normal((n, dim // 32)) * 0.01).astype(np.float16)
+    elif fmt == "mxfp8":
+        payload = rng.integers(0, 256, (n, dim)).astype(np.uint8)
+        scales = rng.integers(100, 150, (n, dim // 32)).astype(np.uint8)
+    elif fmt == "bf16":
+        payload, scales = rng.integers(0, 1 << 16, (n, dim)).astype(np.uint16), None
+    elif fmt == "f32":
+        payload, scales = rng.standard_normal((n, dim)).astype(np.float32), None
+    else:
+        payload, scales = rng.integers(0, 256, (n, dim // 32 * 18)).astype(np.uint8), None
+        payload.reshape(n, -1, 18)[:, :, 1] &= 0x3F  # finite scales
+    wire = F.wire_rows(fmt, payload, scales)
+    got = F.dequant_wire(fmt, wire.reshape(n, -1, F.WIRE_BLOCK_BYTES[fmt])).reshape(n, dim)
+    want = F.dequant(fmt, payload, scales)
+    assert np.array_equal(got, want, equal_nan=True)

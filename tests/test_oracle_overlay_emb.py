@@ -151,22 +151,27 @@ def test_scan_hits_reference_known_answer():
 def _files(rng, fetch, n_files, pool, dim=32, unchanged_every=3):
     files = []
     for i in range(n_files):
-        rows = np.sort(rng.choice(pool, size=int(rng.integers(5, 12)), replace=False)).astype(np.int32)
+        rows = np.sort(rng.choice(pool, size=min(pool, int(rng.integers(5, 12))), replace=False)).astype(np.int32)
         data = fetch(rows) + rng.standard_normal((rows.size, dim)).astype(np.float32) * 1e-2
         data[::unchanged_every] = fetch(rows[::unchanged_every])  # rows the fact left untouched
         files.append((rows, data.astype(np.float32)))
     return files
 
 
-def test_overlay_sum_against_dict_loop():
+@pytest.mark.parametrize("n_files,pool", [(5, 40), (40, 6)])
+def test_overlay_sum_against_dict_loop(n_files, pool):
     """engraft/replica/overlay_sum.py:38-112 by a per-row dictionary loop:
-    union ascending, deltas added in file order, merged = true + sum; an
-    untouched row's delta is exactly zero and is not counted as moved."""
+    union ascending, deltas added one at a time in file order (40 files put
+    far more than 32 deltas on the rows of a 40-row pool; one file lists a
+    row twice), merged = true + sum; an untouched row's delta is exactly zero
+    and is not counted as moved."""
     from oracle import overlay_sum as OS
     data = np.random.default_rng(8).standard_normal((500, 32)).astype(np.float32) * 0.05
     fetch = lambda ids: data[np.asarray(ids, np.int64)]
     rng = np.random.default_rng(9)
-    files = _files(rng, fetch, 5, 40)
+    files = _files(rng, fetch, n_files, pool)
+    r0, d0 = files[1]
+    files[1] = (np.concatenate([r0, r0[:1]]), np.concatenate([d0, d0[:1] + np.float32(3e-3)]))
     rows_u, merged, man = OS.sum_overlays(files, fetch)
     acc: dict[int, np.ndarray] = {}
     moved: dict[int, int] = {}
@@ -177,6 +182,8 @@ def test_overlay_sum_against_dict_loop():
             if np.linalg.norm(delta.astype(np.float64)) > 0:
                 moved[r] = moved.get(r, 0) + 1
     assert rows_u.tolist() == sorted(acc)
+    hits = np.bincount(np.concatenate([r for r, _ in files]))
+    assert (hits.max() > 32) == (n_files == 40)
     for i, r in enumerate(rows_u.tolist()):
         assert np.array_equal(merged[i], (data[r] + acc[r]).astype(np.float32))
     assert man["n_rows_moved_any"] == len(moved)
