@@ -710,6 +710,8 @@ def bench_overlay_emb(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     (torch index_put into the base rows + autograd backward of the same
     gradient) on every host thread."""
 
+    import ctypes
+
     import numpy as np
     import torch
 
@@ -744,8 +746,46 @@ def bench_overlay_emb(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     torch.cuda.synchronize()
     us = a.elapsed_time(b) / steps * 1e3
     hits = int(oe.n_id_hits)
+    # The device's share of the step: the same two launches (eg_gather_slots over
+    # the cached plan, eg_scatter_grad_apply from its cached grouping) issued back
+    # to back without torch autograd around them.  The wall figure above also
+    # holds autograd's own host work (its device thread hand-offs), which varies
+    # from box to box several-fold for the same kernels.
+    from engraft_ngram_amd import _lib
+    from engraft_ngram_amd.seq import _slot_grouping
+
+    plan = oe._plans[(0, t_len)]
+    ws = _slot_grouping(plan, pick.size, dev)
+    emb = torch.empty((t_len, tab.n_heads * DIM), dtype=torch.float32, device=dev)
+    grad = torch.empty((pick.size, DIM), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    st = torch.cuda.current_stream(dev).cuda_stream
+    ct = tab.c_table
+    rvd = rv.detach()
+
+    def device_step():
+        lib.eg_gather_slots(ctypes.byref(ct), plan["rows"].data_ptr(), plan["slot_var"].data_ptr(), t_len,
+                            tab.n_heads, rvd.data_ptr(), pick.size, emb.data_ptr(), st)
+        lib.eg_scatter_grad_apply(g.data_ptr(), 1, t_len, tab.n_heads, DIM, pick.size, grad.data_ptr(), 1,
+                                  ws.data_ptr(), ws.numel(), st)
+
+    device_step()
+    torch.cuda.synchronize()
+    assert torch.equal(emb, oe.build(t_len).detach()) and torch.equal(grad, rv.grad)
+    for _ in range(50):
+        device_step()
+    a.record()
+    for _ in range(steps):
+        device_step()
+    b.record()
+    torch.cuda.synchronize()
+    dev_us = a.elapsed_time(b) / steps * 1e3
     out = {"workload": "OverlayEmb: 2,048-token sequence, config-1 table, 14,032 fp32 variable rows; build + backward",
-           "us_per_step": us, "positions_per_s": t_len / (us * 1e-6), "slots_replaced": hits}
+           "us_per_step": us, "positions_per_s": t_len / (us * 1e-6), "slots_replaced": hits,
+           "device_us_per_step": dev_us,
+           "device_us_per_step_note": "eg_gather_slots + eg_scatter_grad_apply back to back (the step's kernels, "
+                                      "outputs checked equal to the autograd step's); us_per_step adds torch "
+                                      "autograd's host work around them"}
     if cpu_s > 0 and hp is not None:
         # The reference's step on the CPU with the plan cached (seq.py:428-444):
         # base.index_put((idx_t, idx_h), rows_var[idx_r]) and the autograd
@@ -1061,7 +1101,7 @@ def main() -> None:
         result["overlay_emb"] = oe
         log_cpu_leg("overlay_emb", oe)
         log(f"OverlayEmb (a8): {oe['us_per_step']:.0f} us per build + backward of a 2,048-token sequence "
-            f"({oe['slots_replaced']} slots replaced)")
+            f"({oe['slots_replaced']} slots replaced), {oe['device_us_per_step']:.1f} us of it on the device")
         rf = bench_real_format(max(50, args.steps // 4), max(20, args.warmup // 4))
         result["forward_real_format"] = rf
         log(f"forward (real IQ4_NL format): {rf['us_per_launch']:.1f} us/launch, {rf['gb_per_s']:.0f} GB/s "

@@ -173,6 +173,10 @@ SIGNATURES = {
                                   c_void_p, c_void_p]),
     "eg_scatter_grad_slots": (c_int32, [c_void_p, c_int32, c_void_p, c_int64, c_int32, c_int32, c_int64, c_void_p,
                                         c_void_p, ctypes.c_size_t, c_void_p]),
+    "eg_scatter_grad_plan_slots": (c_int32, [c_void_p, c_int64, c_int32, c_int64, c_void_p, ctypes.c_size_t,
+                                             c_void_p]),
+    "eg_scatter_grad_apply": (c_int32, [c_void_p, c_int32, c_int64, c_int32, c_int32, c_int64, c_void_p, c_int32,
+                                        c_void_p, ctypes.c_size_t, c_void_p]),
     "eg_scatter_grad": (c_int32, [c_void_p, c_int32, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64,
                                   c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     "eg_descent_step": (c_int32, [c_void_p, c_int32, c_void_p, c_int64, c_int32, POINTER(EgDescentState),
@@ -207,7 +211,11 @@ def load(path: Path | None = None) -> ctypes.CDLL:
             "(or __graft_entry__.build()); there is no CPU fallback")
     lib = ctypes.CDLL(str(p))
     for name, (restype, argtypes) in SIGNATURES.items():
-        fn = getattr(lib, name)
+        fn = getattr(lib, name, None)
+        if fn is None:
+            if path is None:
+                raise RuntimeError(f"HIP library {p} lacks {name}: rebuild it with `python engraft-ngram_amd/build.py`")
+            continue  # another build of the library, loaded by path: only what it has
         fn.restype = restype
         fn.argtypes = argtypes
     if lib.eg_abi_version() != ABI_VERSION:

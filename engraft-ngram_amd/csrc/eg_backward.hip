@@ -585,6 +585,7 @@ struct SegArgs {
   int64_t step;
   int32_t dense;          // stamp the rows hit (the dense pass skips them)
   float w1, b2, w2, bc2s, eps, neg_step_size, l2c;
+  int32_t overwrite;      // gradient mode: grad_out = the sum (0 for a variable no slot hits), not +=
 };
 
 // A lane owns VPL columns of a row: consecutive (sub*VPL + t) when VPL divides
@@ -778,11 +779,17 @@ __device__ inline void finish(const SegArgs& a, int64_t k, int sub, const float 
     if (a.dense && sub == 0) a.stamp[k] = (int32_t)a.step;
   } else {
     float* dst = a.grad_out + k * a.dim;
-    float cur[VPL];
-    load_f32<VPL, CONSEC>(dst, sub, cur);
+    if (a.overwrite) {
+      // the sum starts from +0, so it is never -0: storing it is bit-identical
+      // to adding it to a zeroed buffer
+      store_f32<VPL, CONSEC>(dst, sub, g);
+    } else {
+      float cur[VPL];
+      load_f32<VPL, CONSEC>(dst, sub, cur);
 #pragma unroll
-    for (int t = 0; t < VPL; ++t) cur[t] = cur[t] + g[t];
-    store_f32<VPL, CONSEC>(dst, sub, cur);
+      for (int t = 0; t < VPL; ++t) cur[t] = cur[t] + g[t];
+      store_f32<VPL, CONSEC>(dst, sub, cur);
+    }
   }
 }
 
@@ -852,7 +859,9 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
       float P[VPL];
 #pragma unroll
       for (int t = 0; t < VPL; ++t) P[t] = 0.0f;
-      sum_piece<VPL, CONSEC, 4, F32>(a, vl, gbase, cnt, sub, P);
+      // eight slots' loads in flight at a time (four with both the optimizer's
+      // state and f32 gradients held: eight would cost occupancy there)
+      sum_piece<VPL, CONSEC, (ADAM && F32) ? 4 : 8, F32>(a, vl, gbase, cnt, sub, P);
 #pragma unroll
       for (int t = 0; t < VPL; ++t) G[t] = G[t] + P[t];
     }
@@ -876,6 +885,13 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
   if (k >= a.n_var) return;  // uniform per group
   const int64_t lo = a.start[k];
   const int64_t len = (int64_t)a.end[k] - lo;
+  if (!ADAM && len == 0 && a.overwrite) {  // a variable no slot hits: its gradient is zero
+    float z[VPL];
+#pragma unroll
+    for (int t = 0; t < VPL; ++t) z[t] = 0.0f;
+    store_f32<VPL, CONSEC>(a.grad_out + k * a.dim, sub, z);
+    return;
+  }
   if (len == 0 || len > kPiece) return;  // not hit, or a long range (its own workgroup)
   float p[VPL], m[VPL], v[VPL];
   if constexpr (ADAM) {  // the state rows do not depend on the gradient: fetch them first
@@ -1239,6 +1255,55 @@ int eg_scatter_grad_slots(const void* d_out, int32_t d_out_f32, const int32_t* s
                           size_t workspace_bytes_, void* stream) {
   return scatter_grad_impl(d_out, d_out_f32, slot_var, n_pos, heads, dim, nullptr, n_var, true, grad_out, workspace,
                            workspace_bytes_, stream);
+}
+
+int eg_scatter_grad_plan_slots(const int32_t* slot_var, int64_t n_pos, int32_t heads, int64_t n_var,
+                               void* workspace, size_t workspace_bytes_, void* stream) {
+  int rc = check_common(nullptr, false, slot_var, true, n_pos, heads, 128, slot_var, n_var, workspace,
+                        workspace_bytes_);
+  if (rc != EG_OK) return rc;
+  const int64_t n = n_pos * heads;
+  if (n == 0 || n_var == 0) return EG_OK;
+  Workspace w;
+  carve(workspace, n, n_var, &w);
+  return group_slots(slot_var, n, nullptr, n_var, nullptr, 0, true, w, (hipStream_t)stream);
+}
+
+int eg_scatter_grad_apply(const void* d_out, int32_t d_out_f32, int64_t n_pos, int32_t heads, int32_t dim,
+                          int64_t n_var, float* grad_out, int32_t overwrite, void* workspace, size_t workspace_bytes_,
+                          void* stream) {
+  EG_CHECK_ARG(n_pos >= 0 && heads >= 1 && heads <= EG_MAX_HEADS, "n_pos=%lld heads=%d", (long long)n_pos, heads);
+  EG_CHECK_ARG(n_var >= 0 && n_var < (1LL << 31), "n_var=%lld", (long long)n_var);
+  EG_CHECK_ARG(dim == 64 || dim == 128 || dim == 160 || dim == 256, "backward dim=%d (built: 64, 128, 160, 256)", dim);
+  EG_CHECK_ARG(n_var == 0 || grad_out != nullptr, "grad_out is NULL");
+  const int64_t n = n_pos * heads;
+  hipStream_t st = (hipStream_t)stream;
+  if (n_var == 0) return EG_OK;
+  if (n == 0) {  // no slot: a zero gradient (a fill kernel, so the call can sit in a captured graph)
+    if (overwrite) {
+      const int64_t words = n_var * dim;
+      hipLaunchKernelGGL(clear_kernel, dim3(grid_for(words, 256, 4096)), dim3(256), 0, st, (uint32_t*)grad_out, words,
+                         (uint32_t*)nullptr, (int64_t)0);
+      return launch_status("clear_kernel");
+    }
+    return EG_OK;
+  }
+  int rc = check_common(d_out, true, nullptr, false, n_pos, heads, dim, (const int32_t*)workspace, n_var, workspace,
+                        workspace_bytes_);
+  if (rc != EG_OK) return rc;
+  Workspace w;
+  carve(workspace, n, n_var, &w);
+  SegArgs a;
+  memset(&a, 0, sizeof(a));
+  fill_seg(&a, w, n, n_var);
+  a.d_out = d_out;
+  a.d_out_f32 = d_out_f32;
+  a.heads = heads;
+  a.dim = dim;
+  a.width = (int64_t)heads * dim;
+  a.grad_out = grad_out;
+  a.overwrite = overwrite != 0;
+  return launch_reduce<false>(a, st);
 }
 
 // The descent state's own checks (every entry point of the step).

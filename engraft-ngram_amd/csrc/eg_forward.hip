@@ -186,6 +186,9 @@ struct FwdArgs {
 };
 
 constexpr int kMaxWidth = 4096;  // W = heads * dim
+#ifndef EG_NCH_F32
+#define EG_NCH_F32 1
+#endif
 constexpr int kWavesPerBlock = 4;
 
 // One wavefront per (position, column part): part q of position p covers the
@@ -449,6 +452,17 @@ static bool launch_special(const FwdArgs& a, bool ovl, hipStream_t st) {
   return true;
 }
 
+// f32 output at dim 128, one layer (eg_gather_slots' OverlayEmb gather,
+// eg_gather's row reads): the generic kernel's divisions by the runtime dim
+// become shifts, and the position's W takes NCH_F32 * 512-column parts.
+constexpr int kNchF32 = EG_NCH_F32;
+template <int FMT, bool ROWS>
+static bool launch_special_f32(const FwdArgs& a, hipStream_t st) {
+  if (a.dim != 128 || a.n_layers != 1) return false;
+  launch_nch<FMT, 128, kNchF32, 1, true, true, 0, ROWS>(a, st);
+  return true;
+}
+
 // The reference's real table shape (16 heads of 160 values, W = 2560, one
 // layer, no overlay): five 512-column chunks per position.
 constexpr int kRealNch = 5;
@@ -478,6 +492,12 @@ static int launch_forward_as(const FwdArgs& a, hipStream_t st) {
     else if (fmt == EG_FMT_BF16) done = launch_special<EG_FMT_BF16, ROWS>(a, ovl, st);
     else if (fmt == EG_FMT_MXFP8) done = launch_special<EG_FMT_MXFP8, ROWS>(a, ovl, st);
     else if (fmt == EG_FMT_IQ4_NL) done = launch_real<EG_FMT_IQ4_NL, ROWS>(a, ovl, st);
+    if (done) return launch_status("forward_kernel");
+  } else if (ROWS) {
+    bool done = false;
+    if (fmt == EG_FMT_Q8_0) done = launch_special_f32<EG_FMT_Q8_0, ROWS>(a, st);
+    else if (fmt == EG_FMT_BF16) done = launch_special_f32<EG_FMT_BF16, ROWS>(a, st);
+    else if (fmt == EG_FMT_MXFP8) done = launch_special_f32<EG_FMT_MXFP8, ROWS>(a, st);
     if (done) return launch_status("forward_kernel");
   }
   switch (fmt) {

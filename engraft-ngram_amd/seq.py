@@ -55,39 +55,66 @@ def overlay_key_len(row_map: dict) -> int | None:
     return next(iter(lengths))
 
 
+def _slot_grouping(plan: dict, n_var: int, dev) -> torch.Tensor:
+    """The slots of ``plan`` grouped by variable (``eg_scatter_grad_plan_slots``),
+    made once per plan and variable count and kept with the plan: every
+    backward of the plan then only sums (``eg_scatter_grad_apply``)."""
+    cache = plan.setdefault("grouping", {})
+    ws = cache.get(n_var)
+    if ws is None:
+        slot_var = plan["slot_var"]
+        n, heads = slot_var.shape
+        need = int(_lib.load().eg_backward_workspace_size(n * heads, n_var))
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+        _lib.call("eg_scatter_grad_plan_slots", _lib.ptr(slot_var), n, heads, n_var, _lib.ptr(ws), ws.numel(),
+                  _lib.stream_ptr(dev))
+        cache[n_var] = ws
+    return ws
+
+
 class _GatherSlots(torch.autograd.Function):
-    """out f32 ``[n, H*D]`` = per slot ``vars[slot_var]`` or the table row;
-    backward: ``eg_scatter_grad_slots``."""
+    """out f32 ``[n, H*D]`` = per slot ``vars[slot_var]`` or the table row
+    (``eg_gather_slots``); backward: the variables' gradients summed over
+    their slots from the plan's cached grouping (``eg_scatter_grad_apply``,
+    written whole: a variable no slot reads gets zeros)."""
 
     @staticmethod
-    def forward(ctx, rows_var, table, rows, slot_var):
+    def forward(ctx, rows_var, table, plan):
+        rows, slot_var = plan["rows"], plan["slot_var"]
         n, heads = rows.shape
         dim = table.row_len
         dev = table.device
-        vars32 = rows_var.detach().to(device=dev, dtype=torch.float32).contiguous()
+        vars32 = rows_var.detach()
+        if vars32.dtype != torch.float32 or vars32.device != dev or not vars32.is_contiguous():
+            vars32 = vars32.to(device=dev, dtype=torch.float32).contiguous()
         out = torch.empty((n, heads * dim), dtype=torch.float32, device=dev)
-        _lib.call("eg_gather_slots", ctypes.byref(table.c_table), _lib.ptr(rows), _lib.ptr(slot_var), n, heads,
-                  _lib.ptr(vars32), vars32.shape[0], _lib.ptr(out), _lib.stream_ptr(dev))
-        ctx.save_for_backward(slot_var)
-        ctx.meta = (heads, dim, vars32.shape[0], rows_var.dtype, rows_var.device)
+        st = torch.cuda.current_stream(dev).cuda_stream
+        rc = _lib.load().eg_gather_slots(ctypes.byref(table.c_table), rows.data_ptr(), slot_var.data_ptr(), n, heads,
+                                         vars32.data_ptr(), vars32.shape[0], out.data_ptr(), st)
+        _lib.check(rc)
+        ctx.plan = plan
+        ctx.meta = (heads, dim, vars32.shape[0], rows_var.dtype, rows_var.device, dev)
         return out
 
     @staticmethod
     def backward(ctx, d_out):
-        (slot_var,) = ctx.saved_tensors
-        heads, dim, n_var, dtype, device = ctx.meta
-        dev = slot_var.device
-        d = d_out.to(device=dev)
+        heads, dim, n_var, dtype, device, dev = ctx.meta
+        d = d_out if d_out.device == dev else d_out.to(device=dev)
         if d.dtype not in (torch.float32, torch.bfloat16):
             d = d.float()
         d = d.contiguous()
-        n = slot_var.shape[0]
-        grad = torch.zeros((n_var, dim), dtype=torch.float32, device=dev)
-        if n > 0 and n_var > 0:
-            ws = _WS.get(n * heads, n_var, dev)
-            _lib.call("eg_scatter_grad_slots", _lib.ptr(d), _dout_args(d), _lib.ptr(slot_var), n, heads, dim,
-                      n_var, _lib.ptr(grad), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
-        return grad.to(device=device, dtype=dtype), None, None, None
+        n = ctx.plan["slot_var"].shape[0]
+        grad = torch.empty((n_var, dim), dtype=torch.float32, device=dev)
+        if n_var > 0:
+            ws = _slot_grouping(ctx.plan, n_var, dev) if n > 0 else None
+            st = torch.cuda.current_stream(dev).cuda_stream
+            rc = _lib.load().eg_scatter_grad_apply(d.data_ptr(), _dout_args(d), n, heads, dim, n_var,
+                                                   grad.data_ptr(), 1, _lib.ptr(ws),
+                                                   ws.numel() if ws is not None else 0, st)
+            _lib.check(rc)
+        if grad.dtype != dtype or grad.device != device:
+            grad = grad.to(device=device, dtype=dtype)
+        return grad, None, None
 
 
 @dataclasses.dataclass
@@ -256,7 +283,7 @@ class OverlayEmb:
                 self._plans[key] = plan
         self.n_key_hits = plan["n_key_hits"]
         self.n_id_hits = plan["n_id_hits"]
-        out = _GatherSlots.apply(self.rows_var, self.table, plan["rows"], plan["slot_var"])
+        out = _GatherSlots.apply(self.rows_var, self.table, plan)
         out = out.to(device=self.rows_var.device, dtype=self.rows_var.dtype)
         return out.reshape(n_positions - start, self.table.n_heads * self.table.row_len)
 

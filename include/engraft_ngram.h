@@ -21,7 +21,7 @@
  *                                                    engraft/replica/model.py:473-495,845-853,
  *                                                    engraft/replica/seq.py:372-444
  *   eg_scatter_grad  autograd of rows_var[idx_r] + index_put (accumulate)
- *   (+ _slots)                                       engraft/replica/seq.py:433-441
+ *   (+ _slots, _plan_slots / _apply)                 engraft/replica/seq.py:433-441
  *   eg_lookup_rows   row_map / sorted-overlay membership + read counts
  *                                                    engraft/replica/seq.py:412-417,
  *                                                    engraft/damage.py:192-197
@@ -369,6 +369,22 @@ int eg_gather_slots(const eg_table* table, const int32_t* rows, const int32_t* s
 int eg_scatter_grad_slots(const void* d_out, int32_t d_out_f32, const int32_t* slot_var,
                           int64_t n_pos, int32_t heads, int32_t dim, int64_t n_var,
                           float* grad_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* eg_scatter_grad_slots in two halves, for a slot-to-variable map used many
+ * times (OverlayEmb's cached plan, engraft/replica/seq.py:382-444, whose
+ * backward runs once per step): _plan groups the slots by variable into the
+ * workspace (eg_backward_workspace_size(n_pos*heads, n_var) bytes); _apply
+ * sums d_out over each variable's slots from that grouping, in the same order
+ * and to the same bits as eg_scatter_grad_slots.  overwrite = 1: grad_out =
+ * the sums, zero for a variable no slot hits (no zeroed buffer needed);
+ * overwrite = 0: grad_out += the sums.  _apply only reads the grouping, except
+ * that a variable of more than 4,096 slots is ordered in place: two _apply
+ * calls on one workspace must not overlap. */
+int eg_scatter_grad_plan_slots(const int32_t* slot_var, int64_t n_pos, int32_t heads, int64_t n_var,
+                               void* workspace, size_t workspace_bytes, void* stream);
+int eg_scatter_grad_apply(const void* d_out, int32_t d_out_f32, int64_t n_pos, int32_t heads,
+                          int32_t dim, int64_t n_var, float* grad_out, int32_t overwrite,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* Seeded synthetic table rows [row0, row0+n_rows) (benchmark/test inputs):
  * value j of row r = qtable[mix64(seed*0xD1B54A32D192ED03 + r*dim + j) >> 50]

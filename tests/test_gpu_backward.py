@@ -78,6 +78,54 @@ def test_scatter_grad_edge_cases(cuda):
         assert np.array_equal(got, exp)
 
 
+@pytest.mark.parametrize("n_slots,n_var,heads,dim,f32", [(30_000, 9_000, 16, 128, True), (20_500, 40, 1, 64, False),
+                                                         (300_000, 3_000_000, 4, 160, True)],
+                         ids=["overlay-emb-shape", "long-ranges", "counting-grouping"])
+def test_scatter_grad_plan_apply_matches_one_call(cuda, n_slots, n_var, heads, dim, f32):
+    """eg_scatter_grad_plan_slots + eg_scatter_grad_apply against
+    eg_scatter_grad_slots, bit for bit: overwrite (every variable written,
+    zeros where no slot reads it) and accumulate, the grouping applied twice
+    (the second apply sees ranges the first ordered in place: a variable of
+    18,000 slots, past the 4,096 ordered in LDS), bf16 and f32 gradients;
+    an empty batch with overwrite writes zeros."""
+    from engraft_ngram_amd import _lib
+    _say(f"scatter plan/apply, {n_slots} slots over {n_var} variables, heads {heads}, dim {dim}")
+    rng = np.random.default_rng(5)
+    n_pos = n_slots // heads
+    sv = ((rng.zipf(1.3, size=n_pos * heads) - 1) % (n_var + n_var // 10)).astype(np.int32)  # some past n_var
+    sv[rng.random(sv.size) < 0.1] = -1
+    if n_var == 40:
+        sv[:18_000] = 3  # one variable of 18,000 slots
+    sv[sv == n_var - 1] = -1  # the last variable: no slot reads it
+    slot_var = torch.from_numpy(sv.reshape(n_pos, heads)).to(cuda)
+    d = torch.randn((n_pos, heads * dim), device=cuda)
+    if not f32:
+        d = d.to(torch.bfloat16)
+    fl = 1 if f32 else 0
+    st = _lib.stream_ptr(cuda)
+    need = int(_lib.load().eg_backward_workspace_size(n_pos * heads, n_var))
+    ws1 = torch.empty(need, dtype=torch.uint8, device=cuda)
+    ref = torch.zeros((n_var, dim), device=cuda)
+    _lib.call("eg_scatter_grad_slots", _lib.ptr(d), fl, _lib.ptr(slot_var), n_pos, heads, dim, n_var, _lib.ptr(ref),
+              _lib.ptr(ws1), need, st)
+    ws = torch.empty(need, dtype=torch.uint8, device=cuda)
+    _lib.call("eg_scatter_grad_plan_slots", _lib.ptr(slot_var), n_pos, heads, n_var, _lib.ptr(ws), need, st)
+    for rep in range(2):
+        got = torch.full((n_var, dim), float("nan"), device=cuda)
+        _lib.call("eg_scatter_grad_apply", _lib.ptr(d), fl, n_pos, heads, dim, n_var, _lib.ptr(got), 1, _lib.ptr(ws),
+                  need, st)
+        assert torch.equal(got.view(torch.int32), ref.view(torch.int32)), rep
+    acc = torch.ones((n_var, dim), device=cuda)
+    _lib.call("eg_scatter_grad_apply", _lib.ptr(d), fl, n_pos, heads, dim, n_var, _lib.ptr(acc), 0, _lib.ptr(ws),
+              need, st)
+    assert torch.equal(acc, 1.0 + ref)
+    hit = np.bincount(sv[(sv >= 0) & (sv < n_var)], minlength=n_var)
+    assert (hit == 0).any() and bool((ref[torch.from_numpy(hit == 0).to(cuda)] == 0).all())
+    empty = torch.full((n_var, dim), float("nan"), device=cuda)
+    _lib.call("eg_scatter_grad_apply", None, fl, 0, heads, dim, n_var, _lib.ptr(empty), 1, None, 0, st)
+    assert bool((empty == 0).all())
+
+
 @pytest.mark.parametrize("n_slots,n_var", [(1_100_000, 300_000), (1_000_000, 1_500_000), (400_000, 100_000)],
                          ids=["counting-1075-tiles", "buckets-of-2048-variables", "buckets-391-tiles"])
 def test_scatter_grad_large_groupings(cuda, n_slots, n_var):
