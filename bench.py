@@ -632,8 +632,7 @@ def bench_damage_scan(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     counts = torch.zeros(ids.size, dtype=torch.int64, device=dev)
     spec = tab.c_spec
     n_bits = tab.n_rows
-    nw = (n_bits + 31) // 32
-    bitmap = torch.empty(2 * nw + (nw + 31) // 32, dtype=torch.int32, device=dev)
+    bitmap = torch.empty(int(_lib.load().eg_id_bitmap_words(n_bits)), dtype=torch.int32, device=dev)
     _lib.call("eg_build_id_bitmap", _lib.ptr(ids_d), ids.size, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(dev))
 
     def timed(bm) -> float:
@@ -676,8 +675,16 @@ def bench_damage_scan(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     res32, wall32 = end_to_end(corpus32)
     assert np.array_equal(res32["pos"], res["pos"]) and np.array_equal(res32["read_count"], res["read_count"])
     lookups = n * tab.n_heads
+    # algorithmic bytes of one block: each token read once (8 B), the three
+    # per-position outputs written (4 B each), every overlay row's read count
+    # read and written (8 + 8 B) and its dnorm read (4 B); the filter, pairs
+    # and hash parameters are the lookup structure's own traffic
+    algo = n * (8 + 12) + ids.size * (8 + 8 + 4)
     out = {"workload": "damage scan: 8,000,000 Zipf tokens x 16 rows against 500,000 sorted overlay rows",
            "us_per_block_kernel": us, "us_per_block_kernel_search_only": us_search,
+           "algorithmic_bytes_per_block": algo, "gb_per_s": algo / (us * 1e-6) / 1e9,
+           "frac_of_hbm_peak": algo / (us * 1e-6) / (HBM_PEAK_GBS * 1e9),
+           "traffic_bytes_per_block": traffic_from_profile("damage_scan_bitmap"),
            "tokens_per_s_kernel": n / (us * 1e-6), "lookups_per_s_kernel": lookups / (us * 1e-6),
            "s_per_block_end_to_end": wall, "s_per_block_end_to_end_int32_tokens": wall32,
            "hit_positions": int(res["pos"].size)}

@@ -194,6 +194,7 @@ SIGNATURES = {
     "eg_scan_overlay": (c_int32, [POINTER(EgHashSpec), c_void_p, c_int32, c_int64, c_int64, c_void_p, c_int64,
                                   c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_build_id_bitmap": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
+    "eg_id_bitmap_words": (c_int64, [c_int64]),
 }
 
 _LIB = None

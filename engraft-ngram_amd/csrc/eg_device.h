@@ -377,20 +377,56 @@ __device__ inline float load_value_rt(const TableDev& t, int64_t row, int col) {
   }
 }
 
-// Index of `key` in the sorted array ids[0..n), or -1.
-// Index of row in the sorted ids behind an eg_build_id_bitmap rank bitmap
-// (fine words [0, nw), ranks [nw, 2 nw), coarse words from 2 nw), or -1: the
-// coarse bit of the row's 32-row word settles most misses, then the fine bit,
-// then rank + popcount of the word's lower bits.
+// A 32-bit mix of a row id (xorshift-multiply rounds).
+__host__ __device__ inline uint32_t mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// The filter block and its five bits of a row in the overlay bitmap's blocked
+// Bloom filter (n_fb 64-bit blocks): the block by a multiply-shift of one mix
+// of the row, the bits from five 6-bit fields of a second mix.
+struct BloomProbe {
+  uint32_t block;
+  uint64_t mask;
+};
+
+__host__ __device__ inline BloomProbe bloom_probe(uint32_t row, uint32_t n_fb) {
+  const uint32_t x = mix32(row);
+  const uint32_t y = mix32(x ^ 0x9e3779b9u);
+  BloomProbe p;
+  p.block = (uint32_t)(((uint64_t)x * n_fb) >> 32);
+  p.mask = (1ull << (y & 63u)) | (1ull << ((y >> 6) & 63u)) | (1ull << ((y >> 12) & 63u)) |
+           (1ull << ((y >> 18) & 63u)) | (1ull << ((y >> 24) & 63u));
+  return p;
+}
+
+// 32-row words and 64-bit filter blocks of an overlay bitmap over n_bits rows.
+__host__ __device__ inline int64_t bitmap_words(int64_t n_bits) { return (n_bits + 31) >> 5; }
+__host__ __device__ inline int64_t bitmap_filter_blocks(int64_t n_bits) { return (bitmap_words(n_bits) + 63) >> 6; }
+
+// Index of row in the sorted ids behind an eg_build_id_bitmap rank bitmap, or
+// -1.  Layout (nw = ceil(n_bits / 32) words of 32 rows): pairs [2 w] = the
+// word's bits, [2 w + 1] = the ids below row 32 w; then ceil(nw / 64) 64-bit
+// filter blocks (a blocked Bloom filter of the ids: five bits in one block an
+// id).  The filter settles almost every miss from an L2-resident block; a row
+// it passes reads its word's pair (bits and rank in one 8-byte load): overlay
+// index = rank + popcount of the bits below the row.
 __device__ inline int64_t bitmap_find(const uint32_t* __restrict__ bm, int64_t n_bits, int32_t row) {
-  const int64_t nw = (n_bits + 31) >> 5;
+  const int64_t nw = bitmap_words(n_bits);
   const bool in = (int64_t)(uint32_t)row < n_bits;
-  const uint32_t w = in ? ((uint32_t)row >> 5) : 0u;
-  const uint32_t coarse = bm[2 * nw + (w >> 5)];
+  const BloomProbe bp = bloom_probe((uint32_t)row, (uint32_t)bitmap_filter_blocks(n_bits));
+  const uint64_t fb = ((const uint64_t*)(bm + 2 * nw))[bp.block];
   int64_t k = -1;
-  if (in && ((coarse >> (w & 31u)) & 1u)) {
-    const uint32_t word = bm[w], below = word & ((1u << ((uint32_t)row & 31u)) - 1u);
-    if ((word >> ((uint32_t)row & 31u)) & 1u) k = (int64_t)bm[nw + w] + __popc(below);
+  if (in && (fb & bp.mask) == bp.mask) {
+    const uint32_t w = (uint32_t)row >> 5;
+    const u32x2 pr = ((const u32x2*)bm)[w];
+    const uint32_t bit = (uint32_t)row & 31u;
+    if ((pr.x >> bit) & 1u) k = (int64_t)pr.y + __popc(pr.x & ((1u << bit) - 1u));
   }
   return k;
 }

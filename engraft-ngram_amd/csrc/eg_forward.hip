@@ -542,6 +542,7 @@ static int fill_overlay(const eg_overlay* o, const TableDev& base, OverlayDev* o
                (long long)o->n, (long long)o->rows.n_rows);
   EG_CHECK_ARG(o->bitmap == nullptr || (o->n_bits >= 1 && o->n_bits <= (1LL << 31)),
                "overlay: bitmap with n_bits=%lld", (long long)o->n_bits);
+  EG_CHECK_ARG(((uintptr_t)o->bitmap & 7) == 0, "overlay: bitmap must be 8-byte aligned");
   out->ids = o->ids;
   out->index = o->index;
   out->n = o->n;
@@ -567,14 +568,16 @@ __global__ __launch_bounds__(256) void bitmap_set_kernel(const int32_t* __restri
   const int64_t r = ids[i];
   if (r >= 0 && r < n_bits) {
     const int64_t nw = (n_bits + 31) >> 5, w = r >> 5;
-    atomicOr(&bitmap[w], 1u << (r & 31));
-    atomicOr(&bitmap[2 * nw + (w >> 5)], 1u << (w & 31));
+    atomicOr(&bitmap[2 * w], 1u << (r & 31));
+    const BloomProbe bp = bloom_probe((uint32_t)r, (uint32_t)bitmap_filter_blocks(n_bits));
+    atomicOr((unsigned long long*)(bitmap + 2 * nw) + bp.block, (unsigned long long)bp.mask);
   }
 }
 
-// rank[w] = number of ids below 32 w (a lower bound in the sorted ids).
+// rank of word w (its pair's second entry) = number of ids below 32 w (a lower
+// bound in the sorted ids).
 __global__ __launch_bounds__(256) void bitmap_rank_kernel(const int32_t* __restrict__ ids, int64_t n_ids,
-                                                          uint32_t* __restrict__ rank, int64_t words) {
+                                                          uint32_t* __restrict__ pairs, int64_t words) {
   for (int64_t w = (int64_t)blockIdx.x * 256 + threadIdx.x; w < words; w += (int64_t)gridDim.x * 256) {
     const int64_t key = w * 32;
     int64_t lo = 0, hi = n_ids;
@@ -582,7 +585,7 @@ __global__ __launch_bounds__(256) void bitmap_rank_kernel(const int32_t* __restr
       const int64_t mid = (lo + hi) >> 1;
       if ((int64_t)ids[mid] < key) lo = mid + 1; else hi = mid;
     }
-    rank[w] = (uint32_t)lo;
+    pairs[2 * w + 1] = (uint32_t)lo;
   }
 }
 
@@ -590,21 +593,25 @@ __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ a,
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < len; i += (int64_t)gridDim.x * 256) a[i] = 0u;
 }
 
+int64_t eg_id_bitmap_words(int64_t n_bits) {
+  return n_bits < 1 ? 0 : 2 * bitmap_words(n_bits) + 2 * bitmap_filter_blocks(n_bits);
+}
+
 int eg_build_id_bitmap(const int32_t* ids, int64_t n_ids, uint32_t* bitmap, int64_t n_bits, void* stream) {
   EG_CHECK_ARG(n_ids >= 0 && n_ids < (1LL << 32) && n_bits >= 1 && n_bits <= (1LL << 31), "n_ids=%lld n_bits=%lld",
                (long long)n_ids, (long long)n_bits);
   EG_CHECK_ARG(bitmap != nullptr && (n_ids == 0 || ids != nullptr), "NULL argument");
-  const int64_t words = (n_bits + 31) / 32;
+  EG_CHECK_ARG(((uintptr_t)bitmap & 7) == 0, "bitmap must be 8-byte aligned");
+  const int64_t words = bitmap_words(n_bits);
+  const int64_t total = eg_id_bitmap_words(n_bits);
   hipStream_t st = (hipStream_t)stream;
-  const int64_t fill_blocks = (words + 255) / 256 < 4096 ? (words + 255) / 256 : 4096;
-  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)fill_blocks), dim3(256), 0, st, bitmap, words);
-  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((words + 31) / 32 + 255) / 256), dim3(256), 0, st,
-                     bitmap + 2 * words, (words + 31) / 32);
+  const int64_t fill_blocks = (total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)fill_blocks), dim3(256), 0, st, bitmap, total);
   if (n_ids > 0)
     hipLaunchKernelGGL(bitmap_set_kernel, dim3((unsigned)((n_ids + 255) / 256)), dim3(256), 0, st, ids, n_ids, bitmap,
                        n_bits);
-  hipLaunchKernelGGL(bitmap_rank_kernel, dim3((unsigned)fill_blocks), dim3(256), 0, st, ids, n_ids, bitmap + words,
-                     words);
+  const int64_t rank_blocks = (words + 255) / 256 < 4096 ? (words + 255) / 256 : 4096;
+  hipLaunchKernelGGL(bitmap_rank_kernel, dim3((unsigned)rank_blocks), dim3(256), 0, st, ids, n_ids, bitmap, words);
   return launch_status("bitmap kernels");
 }
 
@@ -621,7 +628,8 @@ int eg_scan_overlay(const eg_hash_spec* spec, const void* tokens, int32_t token_
   const int64_t m = n_tokens - start;
   if (m == 0) return EG_OK;
   EG_CHECK_ARG(tokens && ids && dnorm && n_hit && dnorm_max && dnorm_sum && read_counts, "NULL argument");
-  EG_CHECK_ARG(bitmap == nullptr || n_bits >= 1, "n_bits=%lld", (long long)n_bits);
+  EG_CHECK_ARG(bitmap == nullptr || (n_bits >= 1 && n_bits <= (1LL << 31)), "n_bits=%lld", (long long)n_bits);
+  EG_CHECK_ARG(((uintptr_t)bitmap & 7) == 0, "bitmap must be 8-byte aligned");
   EG_CHECK_ARG(token_bytes == 4 || token_bytes == 8, "token_bytes=%d (4: int32, 8: int64)", token_bytes);
   const int G = L.n_heads <= 16 ? 16 : 32;
   const int64_t threads = m * G;

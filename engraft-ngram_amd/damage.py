@@ -121,8 +121,7 @@ def scan_hits(tokens: np.ndarray, table, overlay_sorted: np.ndarray, dnorm_sorte
     # membership bitmap over the table's rows: almost every lookup is a miss,
     # settled by one bit instead of the binary search
     n_bits = max(int(table.n_rows), 1)
-    nw = (n_bits + 31) // 32
-    bitmap = torch.empty(2 * nw + (nw + 31) // 32, dtype=torch.int32, device=dev)
+    bitmap = torch.empty(int(_lib.load().eg_id_bitmap_words(n_bits)), dtype=torch.int32, device=dev)
     if n_ov:
         _lib.call("eg_build_id_bitmap", _lib.ptr(ids), n_ov, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(dev))
     # int32 token arrays (a tokenized corpus file) go to the device as they are

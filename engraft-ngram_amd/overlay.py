@@ -63,8 +63,7 @@ class DeviceOverlay:
             # the bitmap holds rows below n_rows only: a larger id would be
             # found by the binary search and missed through the bitmap
             raise ValueError(f"overlay id {int(self.ids[-1])} >= n_rows={n_rows}")
-        nw = (n_rows + 31) // 32
-        bm = torch.empty(2 * nw + (nw + 31) // 32, dtype=torch.int32, device=self.ids.device)
+        bm = torch.empty(int(_lib.load().eg_id_bitmap_words(n_rows)), dtype=torch.int32, device=self.ids.device)
         _lib.call("eg_build_id_bitmap", _lib.ptr(self.ids), self.n, _lib.ptr(bm), n_rows,
                   _lib.stream_ptr(self.ids.device))
         self.bitmap, self.n_bits = bm, n_rows

@@ -348,12 +348,17 @@ int eg_scan_overlay(const eg_hash_spec* spec, const void* tokens, int32_t token_
                     int64_t n_bits, const float* dnorm, int32_t* n_hit, float* dnorm_max,
                     float* dnorm_sum, int64_t* read_counts, void* stream);
 
-/* Rank bitmap of sorted, unique overlay ids for eg_scan_overlay: bitmap is
- * uint32 [2 * nw + ceil(nw/32)], nw = ceil(n_bits/32); word w < nw gets bit b
- * set for every id 32 w + b < n_bits (all other bits cleared), bitmap[nw + w]
- * = the number of ids below 32 w, and coarse word bitmap[2 nw + v] has bit u
- * set when word 32 v + u is not zero.  No counterpart in the reference: it
- * turns the scan's per-lookup binary search into one or two probes. */
+/* Rank bitmap of sorted, unique overlay ids for eg_scan_overlay and the
+ * forward's overlay lookups: bitmap is uint32 [eg_id_bitmap_words(n_bits)],
+ * 8-byte aligned, = 2 * nw + 2 * ceil(nw/64) with nw = ceil(n_bits/32).
+ * Pair w < nw: bitmap[2 w] has bit b set for every id 32 w + b < n_bits (all
+ * other bits cleared), bitmap[2 w + 1] = the number of ids below 32 w.  Then
+ * ceil(nw/64) 64-bit filter blocks: a blocked Bloom filter of the ids below
+ * n_bits (each id sets five bits of one block, picked by a hash of the id; no
+ * false negatives).  A lookup reads its filter block and, only when that
+ * passes, its pair.  No counterpart in the reference: it turns the scan's
+ * per-lookup binary search into one or two probes. */
+int64_t eg_id_bitmap_words(int64_t n_bits);
 int eg_build_id_bitmap(const int32_t* ids, int64_t n_ids, uint32_t* bitmap, int64_t n_bits, void* stream);
 
 /* Gather with per-slot replacement rows (engraft/replica/seq.py:433-441):

@@ -208,12 +208,34 @@ def test_scan_hits_edges_against_oracle(cuda):
         damage.scan_hits(corpus, tab, overlays[1], np.ones(1, np.float32), block=hist - 1)
 
 
+def _mix32(x: int) -> int:
+    m = 0xFFFFFFFF
+    x &= m
+    x ^= x >> 16
+    x = (x * 0x7FEB352D) & m
+    x ^= x >> 15
+    x = (x * 0x846CA68B) & m
+    return x ^ (x >> 16)
+
+
+def _bloom_probe(row: int, n_fb: int) -> tuple[int, int]:
+    """The filter block and bits of a row in eg_build_id_bitmap's blocked
+    Bloom filter (the library's hash, restated to check the built blocks)."""
+    x = _mix32(row)
+    y = _mix32(x ^ 0x9E3779B9)
+    mask = 0
+    for sh in (0, 6, 12, 18, 24):
+        mask |= 1 << ((y >> sh) & 63)
+    return (x * n_fb) >> 32, mask
+
+
 def test_scan_overlay_rank_bitmap(cuda):
     """eg_scan_overlay with and without the eg_build_id_bitmap rank bitmap:
-    the bits hold exactly the ids below n_bits (an id past the table's rows is
-    left out and still never hits), the ranks are the lower bounds of 32 w in
-    the ids, the coarse bits mark the nonempty words, and both launches give
-    the same per-position outputs and read counts (bit-exact)."""
+    the pairs' bits hold exactly the ids below n_bits (an id past the table's
+    rows is left out and still never hits), their ranks are the lower bounds
+    of 32 w in the ids, every id's three filter bits are set in its filter
+    word and the filter holds no other bit, and both launches give the same
+    per-position outputs and read counts (bit-exact)."""
     import ctypes
 
     from engraft_ngram_amd import _lib
@@ -230,18 +252,23 @@ def test_scan_overlay_rank_bitmap(cuda):
     ids = torch.from_numpy(ov).to(cuda)
     dn = torch.from_numpy(rng.random(ov.size).astype(np.float32)).to(cuda)
     nw = (n_bits + 31) // 32
-    bitmap = torch.full((2 * nw + (nw + 31) // 32,), -1, dtype=torch.int32, device=cuda)  # stale bits get cleared
+    n_fb = (nw + 63) // 64
+    assert _lib.load().eg_id_bitmap_words(n_bits) == 2 * nw + 2 * n_fb
+    bitmap = torch.full((2 * nw + 2 * n_fb,), -1, dtype=torch.int32, device=cuda)  # stale bits get cleared
     _lib.call("eg_build_id_bitmap", _lib.ptr(ids), ov.size, _lib.ptr(bitmap), n_bits, _lib.stream_ptr(cuda))
     want = np.zeros(nw * 32, dtype=bool)
     want[ov[ov < n_bits]] = True
     bm = bitmap.cpu().numpy()
-    got_bits = np.unpackbits(bm[:nw].view(np.uint8), bitorder="little").astype(bool)
+    got_bits = np.unpackbits(bm[0:2 * nw:2].copy().view(np.uint8), bitorder="little").astype(bool)
     assert np.array_equal(got_bits, want)
-    assert np.array_equal(bm[nw:2 * nw].astype(np.int64), np.searchsorted(ov, np.arange(nw, dtype=np.int64) * 32))
-    coarse = np.unpackbits(bm[2 * nw:].view(np.uint8), bitorder="little").astype(bool)
-    want_c = np.zeros(coarse.size, dtype=bool)
-    want_c[:nw] = bm[:nw] != 0
-    assert np.array_equal(coarse, want_c)
+    assert np.array_equal(bm[1:2 * nw:2].astype(np.int64), np.searchsorted(ov, np.arange(nw, dtype=np.int64) * 32))
+    filt = bm[2 * nw:].copy().view(np.uint64)
+    want_f = np.zeros(n_fb, dtype=np.uint64)
+    for r in ov[ov < n_bits].tolist():
+        b, mask = _bloom_probe(r, n_fb)
+        want_f[b] |= np.uint64(mask)
+    assert np.array_equal(filt, want_f)
+    assert filt.any()
     tok = torch.from_numpy(np.asarray(tokens, dtype=np.int64)).to(cuda)
     spec_c = tab.c_spec
     outs = []
