@@ -98,57 +98,109 @@ __global__ __launch_bounds__(256) void hash_kernel(const LayerHash L, const int6
 }
 
 // ---------------------------------------------------------------------------
-// Damage scan: one group of G lanes per position (G = 16 or 32 >= n_heads)
+// Damage scan: one group of G lanes per kScanPP positions (G = 16 or 32 >= n_heads)
 // ---------------------------------------------------------------------------
+#ifndef EG_SCAN_PP
+#define EG_SCAN_PP 4
+#endif
+constexpr int kScanPP = EG_SCAN_PP;
 // Position p of the block (p >= start) hashes its n_heads rows (the block as
 // one sequence), looks each up in the sorted overlay ids and reduces over its
 // heads: the number of rows found, the max and the sum of their dnorm (a fixed
 // pairwise tree over the heads); every row found adds one to its read count.
-// Nothing per slot is written to memory.
-// With the rank bitmap of the overlay ids (words [0, nw): bit r set for every
-// id r < n_bits; words [nw, 2 nw): rank[w] = number of ids below 32 w; then
-// ceil(nw / 32) coarse words, bit w set when word w is not zero), a row's
-// overlay index is rank[w] + popcount of its word's lower bits.  The coarse
-// words (1/1024 of the rows: 1.2 MB for 320M rows) stay in each XCD's L2 and
-// settle most misses; only rows in a nonempty 32-row group probe the fine word
-// (the 40 MB level, from the Infinity Cache) -- in place of the ~19 dependent
-// loads of the binary search.
-template <int G, typename TOK>
+// Nothing per slot is written to memory.  A group of G lanes (one head a lane)
+// takes PP positions at once, every load of one stage issued for all of them
+// before any is waited for: the scan is a chain of dependent loads (tokens ->
+// filter -> pair -> dnorm), and PP chains in flight per lane keep more of the
+// memory system busy.
+// With the rank bitmap of the overlay ids (eg_build_id_bitmap: its filter
+// blocks, 1/2048 of the rows' count in bytes, stay in each XCD's L2 and settle
+// almost every miss), a lookup is one filter probe and, rarely, one pair probe:
+// overlay index = the pair's rank + popcount of its bits below the row -- in
+// place of the ~19 dependent loads of the binary search.
+template <int G, typename TOK, int PP>
 __global__ __launch_bounds__(256) void scan_kernel(const LayerHash L, const TOK* __restrict__ tokens, int64_t n,
                                                    int64_t start, const int32_t* __restrict__ ids, int64_t n_ids,
                                                    const uint32_t* __restrict__ bitmap, int64_t n_bits,
                                                    const float* __restrict__ dnorm, int32_t* __restrict__ n_hit,
                                                    float* __restrict__ dmax, float* __restrict__ dsum,
                                                    unsigned long long* __restrict__ counts) {
-  const int64_t t = ((int64_t)blockIdx.x * 256 + threadIdx.x) / G;  // uniform per group
+  // positions start + t0 + j, j < PP, of this group (uniform per group)
+  const int64_t t0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) / G * PP;
   const int h = (int)(threadIdx.x % G);
-  const int64_t p = start + t;
-  if (p >= n) return;
+  if (start + t0 >= n) return;
   const int hh = min(h, L.n_heads - 1);
-  uint64_t ctx[EG_MAX_NGRAM];
-  build_ctx(L, tokens, p, 0, ctx);
-  const int32_t row = head_row(L, hh, ctx, true);
-  const int64_t k = bitmap != nullptr ? bitmap_find(bitmap, n_bits, row) : sorted_find(ids, n_ids, row);
-  const bool hit = h < L.n_heads && k >= 0;
-  if (hit) atomicAdd(&counts[k], 1ull);
-  const float d = hit ? dnorm[k] : 0.0f;
-  // head-order reductions over the group (lane 0 ends with the results)
-  uint32_t cnt = hit ? 1u : 0u;
-  float mx = hit ? d : -INFINITY, sm = d;
+  uint64_t mult[EG_MAX_NGRAM];
+  load_head_mult(L, hh, mult);
+  const HeadConst hc = load_head_const(L, hh);
+  // 1. every position's tokens, then every row id
+  uint64_t raw[PP][EG_MAX_NGRAM];
 #pragma unroll
-  for (int o = 1; o < G; o <<= 1) {
-    const uint32_t c2 = __shfl_down(cnt, o, G);
-    const float m2 = __shfl_down(mx, o, G), s2 = __shfl_down(sm, o, G);
-    if (h + o < G && (h & (2 * o - 1)) == 0) {
-      cnt += c2;
-      mx = fmaxf(mx, m2);
-      sm = sm + s2;
-    }
+  for (int j = 0; j < PP; ++j) load_ctx_tokens(tokens, min(start + t0 + j, n - 1), L.ngram_size, raw[j]);
+  int32_t row[PP];
+#pragma unroll
+  for (int j = 0; j < PP; ++j) {
+    uint64_t ctx[EG_MAX_NGRAM];
+    ctx_from(L, raw[j], min(start + t0 + j, n - 1), 0, ctx);
+    row[j] = row_of(L, hh, ctx, mult, hc, true);
   }
-  if (h == 0) {
-    n_hit[t] = (int32_t)cnt;
-    dmax[t] = cnt ? mx : 0.0f;
-    dsum[t] = sm;
+  // 2. every lookup.  With the bitmap: all filter blocks, then all pairs (a
+  //    row the filter rejects reads pair 0 in place of its own: every lane
+  //    issues every load, and the rejected ones hit one cached line), then
+  //    every hit's dnorm (a miss reads dnorm[0]).
+  int64_t k[PP];
+  if (bitmap != nullptr) {
+    const int64_t nw = bitmap_words(n_bits);
+    const uint32_t n_fb = (uint32_t)bitmap_filter_blocks(n_bits);
+    const uint64_t* filt = (const uint64_t*)(bitmap + 2 * nw);
+    uint64_t fb[PP], mask[PP];
+#pragma unroll
+    for (int j = 0; j < PP; ++j) {
+      const BloomProbe bp = bloom_probe((uint32_t)row[j], n_fb);
+      mask[j] = bp.mask;
+      fb[j] = filt[bp.block];
+    }
+    u32x2 pr[PP];
+    bool pass[PP];
+#pragma unroll
+    for (int j = 0; j < PP; ++j) {
+      pass[j] = (int64_t)(uint32_t)row[j] < n_bits && (fb[j] & mask[j]) == mask[j];
+      pr[j] = ((const u32x2*)bitmap)[pass[j] ? ((uint32_t)row[j] >> 5) : 0u];
+    }
+#pragma unroll
+    for (int j = 0; j < PP; ++j) {
+      const uint32_t bit = (uint32_t)row[j] & 31u;
+      k[j] = (pass[j] && ((pr[j].x >> bit) & 1u)) ? (int64_t)pr[j].y + __popc(pr[j].x & ((1u << bit) - 1u)) : -1;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < PP; ++j) k[j] = sorted_find(ids, n_ids, row[j]);
+  }
+  float d[PP];
+#pragma unroll
+  for (int j = 0; j < PP; ++j) d[j] = dnorm[k[j] >= 0 ? k[j] : 0];
+#pragma unroll
+  for (int j = 0; j < PP; ++j) {
+    const bool hit = start + t0 + j < n && h < L.n_heads && k[j] >= 0;
+    if (hit) atomicAdd(&counts[k[j]], 1ull);
+    // head-order reductions over the group (lane 0 ends with the results)
+    uint32_t cnt = hit ? 1u : 0u;
+    float mx = hit ? d[j] : -INFINITY, sm = hit ? d[j] : 0.0f;
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) {
+      const uint32_t c2 = __shfl_down(cnt, o, G);
+      const float m2 = __shfl_down(mx, o, G), s2 = __shfl_down(sm, o, G);
+      if (h + o < G && (h & (2 * o - 1)) == 0) {
+        cnt += c2;
+        mx = fmaxf(mx, m2);
+        sm = sm + s2;
+      }
+    }
+    if (h == 0 && start + t0 + j < n) {
+      n_hit[t0 + j] = (int32_t)cnt;
+      dmax[t0 + j] = cnt ? mx : 0.0f;
+      dsum[t0 + j] = sm;
+    }
   }
 }
 
@@ -632,14 +684,14 @@ int eg_scan_overlay(const eg_hash_spec* spec, const void* tokens, int32_t token_
   EG_CHECK_ARG(((uintptr_t)bitmap & 7) == 0, "bitmap must be 8-byte aligned");
   EG_CHECK_ARG(token_bytes == 4 || token_bytes == 8, "token_bytes=%d (4: int32, 8: int64)", token_bytes);
   const int G = L.n_heads <= 16 ? 16 : 32;
-  const int64_t threads = m * G;
+  const int64_t threads = (m + kScanPP - 1) / kScanPP * G;
   EG_CHECK_ARG((threads + 255) / 256 < (1LL << 31), "n_tokens=%lld too large for one launch", (long long)n_tokens);
   const dim3 grid((unsigned)((threads + 255) / 256));
   hipStream_t st = (hipStream_t)stream;
   unsigned long long* rc64 = (unsigned long long*)read_counts;
-#define EG_SCAN(GG, T)                                                                                             \
-  hipLaunchKernelGGL((scan_kernel<GG, T>), grid, dim3(256), 0, st, L, (const T*)tokens, n_tokens, start, ids, n_ids, \
-                     bitmap, n_bits, dnorm, n_hit, dnorm_max, dnorm_sum, rc64)
+#define EG_SCAN(GG, T)                                                                                            \
+  hipLaunchKernelGGL((scan_kernel<GG, T, kScanPP>), grid, dim3(256), 0, st, L, (const T*)tokens, n_tokens, start, \
+                     ids, n_ids, bitmap, n_bits, dnorm, n_hit, dnorm_max, dnorm_sum, rc64)
   if (token_bytes == 8) {
     if (G == 16) EG_SCAN(16, int64_t); else EG_SCAN(32, int64_t);
   } else {
