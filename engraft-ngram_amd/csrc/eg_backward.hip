@@ -231,9 +231,8 @@ __global__ __launch_bounds__(kTileThreads) void keys_count_kernel(
 //   them).  Its region of the slots array starts at the slots of every tile
 //   in the earlier buckets, which is the sum over t of its own segments'
 //   offsets: each bucket finds it alone.  Its variables of more than kPiece
-//   slots go to its region of the long list, [start / (kPiece + 1),
-//   end / (kPiece + 1)) (room for every variable of more than kPiece slots in
-//   [start, end)), the rest of the region holds kNoVar.
+//   slots are appended to the long list (one atomic a bucket on its length,
+//   which the tile sort zeroes): the list is dense, in no particular order.
 constexpr int kGroupThreads = 512;
 constexpr int kGroupIPT = 2;
 constexpr int kGroupTile = kGroupThreads * kGroupIPT;  // slots per tile
@@ -281,12 +280,13 @@ template <int MODE>
 __global__ __launch_bounds__(kGroupThreads) void tile_sort_kernel(
     const int32_t* __restrict__ rows, int64_t n, const int32_t* __restrict__ ids, int64_t n_var, int split_shift,
     const unsigned long long* __restrict__ index, int index_bits, int bs, int nb, int64_t n_tiles,
-    unsigned long long* __restrict__ pairs, uint32_t* __restrict__ seg) {
+    unsigned long long* __restrict__ pairs, uint32_t* __restrict__ seg, uint32_t* __restrict__ n_long) {
   __shared__ int32_t spl[MODE == 0 ? kSplitMax : 1];
   __shared__ uint32_t bh[kBucketsMax];
   __shared__ uint32_t wsum[kGroupThreads / 64];
   const int tid = threadIdx.x;
   const int64_t t = blockIdx.x;
+  if (t == 0 && tid == 0) *n_long = 0u;  // the long list's length, counted by the next launch
   for (int i = tid; i < nb; i += kGroupThreads) bh[i] = 0u;
   int ns = 0;
   if constexpr (MODE == 0) ns = load_splitters(ids, n_var, split_shift, spl, tid, kGroupThreads);
@@ -327,8 +327,8 @@ __global__ __launch_bounds__(kGroupThreads) void tile_sort_kernel(
 template <int TPT>
 __global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
     const unsigned long long* __restrict__ pairs, const uint32_t* __restrict__ seg, int64_t n_tiles, int nb, int bs,
-    int64_t n_var, int64_t long_len, uint32_t* __restrict__ start, uint32_t* __restrict__ end,
-    uint32_t* __restrict__ slots, uint32_t* __restrict__ long_list) {
+    int64_t n_var, uint32_t* __restrict__ start, uint32_t* __restrict__ end,
+    uint32_t* __restrict__ slots, uint32_t* __restrict__ long_list, uint32_t* __restrict__ n_long) {
   constexpr int kKeys = 1 << kBucketKeysLog2Max;
   constexpr int kKeep = 4;                         // pairs of one tile a thread holds in registers
   __shared__ uint32_t cnt[kKeys];                  // pairs held in registers, per variable
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
   __shared__ uint32_t lst[kKeys];
   __shared__ uint32_t lng[kKeys];                  // the bucket's variables of more than kPiece slots
   __shared__ uint32_t wsum[2][kRangeThreads / 64];
-  __shared__ uint32_t n_long_b;
+  __shared__ uint32_t n_long_b, long_at;
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
   const int64_t key0 = b << bs;
@@ -411,10 +411,11 @@ __global__ __launch_bounds__(kRangeThreads) void bucket_ranges_kernel(
     over[i] = lst[i] + cnt[i];  // where the variable's overflow pairs go
   }
   __syncthreads();
-  // the bucket's region of the long list: its long variables, then kNoVar
-  const int64_t l0 = base / (kPiece + 1);
-  const int64_t l1 = b == nb - 1 ? long_len : (int64_t)(base + total) / (kPiece + 1);
-  for (int64_t j = tid; j < l1 - l0; j += kRangeThreads) long_list[l0 + j] = j < n_long_b ? lng[j] : kNoVar;
+  // the bucket's long variables, appended to the list (its order is free: each
+  // long variable is reduced by one workgroup, whichever entry holds it)
+  if (tid == 0) long_at = n_long_b ? atomicAdd(n_long, n_long_b) : 0u;
+  __syncthreads();
+  for (uint32_t j = tid; j < n_long_b; j += kRangeThreads) long_list[long_at + j] = lng[j];
   // every slot id at its variable's place (the order inside a range is free)
 #pragma unroll
   for (int j = 0; j < kTilesPerThread; ++j)
@@ -564,7 +565,8 @@ struct SegArgs {
   const uint32_t* start;      // [n_var] start of each variable's range in slots
   const uint32_t* end;        // [n_var] its end
   const uint32_t* slots;      // slot ids grouped by variable (CSR)
-  const uint32_t* long_list;  // variables with more than kPiece slots, unused entries kNoVar
+  const uint32_t* long_list;  // variables with more than kPiece slots, the first *long_count entries
+  const uint32_t* long_count;
   int64_t n;
   int64_t n_var;
   const void* d_out;
@@ -811,25 +813,30 @@ __device__ inline uint32_t sort32(uint32_t v, int sub, int span = 32) {
   return v;
 }
 
-// One launch for every variable hit.  The first n_long_blocks workgroups take
-// the listed variables of more than kPiece slots: the workgroup puts the
-// variable's slot ids in ascending order (in LDS up to kLongLds ids, else in
-// place on global memory), sums pieces of kPiece slots in order, adds piece j
-// to group j mod kLongGroups and the group sums in group order.  They are
-// dispatched first, so their longer chains overlap the rest.  Every other
-// workgroup holds eight 32-lane groups, one per variable: a variable of
-// 1..kPiece slots loads its slot ids, sorts them on the lanes and reduces them
-// in order.
+// One launch for every variable hit.  The workgroups of the long list (the
+// first n_long_head of the grid and every one after the n_short_blocks that
+// follow them) take the listed variables of more than kPiece slots: the
+// workgroup puts the variable's slot ids in ascending order (in LDS up to
+// kLongLds ids, else in place on global memory), sums pieces of kPiece slots
+// in order, adds piece j to group j mod kLongGroups and the group sums in
+// group order.  The head is dispatched first, so the longer chains overlap the
+// rest.  Every short workgroup holds eight 32-lane groups, one per variable: a
+// variable of 1..kPiece slots loads its slot ids, sorts them on the lanes and
+// reduces them in order.
 constexpr int kLongLds = kLongGroups * 512;  // slot ids a long range orders in LDS (the partial-sum buffer)
 
 template <int VPL, bool CONSEC, bool ADAM, bool F32>
-__global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_long_blocks) {
+__global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_long_head, int64_t n_short_blocks) {
   __shared__ uint32_t lds[kLongLds];
   float* part = (float*)lds;  // [kLongGroups][512] once the slot ids are no longer needed
   const int lane = threadIdx.x & 63, sub = lane & 31, gbase = lane & 32;
-  if ((int64_t)blockIdx.x < n_long_blocks) {
-    const uint32_t key = a.long_list[blockIdx.x];
-    if (key == kNoVar) return;  // uniform per workgroup
+  const int64_t bid = blockIdx.x;
+  if (bid < n_long_head || bid >= n_long_head + n_short_blocks) {
+    // long-list entry e: the first entries' workgroups open the grid, the
+    // rest (most of which find no entry) close it
+    const int64_t e = bid < n_long_head ? bid : bid - n_short_blocks;
+    if (e >= (int64_t)*a.long_count) return;  // uniform per workgroup
+    const uint32_t key = a.long_list[e];
     const int grp = threadIdx.x >> 5;
     const int64_t lo = a.start[key];
     const int64_t hi = a.end[key];
@@ -881,7 +888,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
     }
     return;
   }
-  const int64_t k = (((int64_t)blockIdx.x - n_long_blocks) * 256 + threadIdx.x) >> 5;
+  const int64_t k = ((bid - n_long_head) * 256 + threadIdx.x) >> 5;
   if (k >= a.n_var) return;  // uniform per group
   const int64_t lo = a.start[k];
   const int64_t len = (int64_t)a.end[k] - lo;
@@ -986,7 +993,8 @@ struct Workspace {
   uint32_t* slots;      // [n] slot ids grouped by variable
   uint32_t* start;      // [n_var] range start of every variable
   uint32_t* end;        // [n_var] range end (the counting path: start + 1)
-  uint32_t* long_list;  // [n / (kPiece + 1) + 1] variables of more than kPiece slots, the rest kNoVar
+  uint32_t* long_list;  // [n / (kPiece + 1) + 1] variables of more than kPiece slots, first n_long entries
+  uint32_t* n_long;     // the long list's length
   // the counting path
   uint32_t* keys;       // [n] variable of every slot (n_var: none)
   uint32_t* ranks;      // [n] place of every slot in its variable's range
@@ -1016,7 +1024,8 @@ static size_t carve(void* ws, int64_t n, int64_t n_var, Workspace* out) {
     return p;
   };
   w.slots = (uint32_t*)take((size_t)n * 4);
-  w.long_list = (uint32_t*)take((size_t)n_long_max(n) * 4);
+  w.long_list = (uint32_t*)take((size_t)(n_long_max(n) + 1) * 4);
+  w.n_long = w.long_list ? w.long_list + n_long_max(n) : nullptr;
   if (g.bucketed) {
     w.start = (uint32_t*)take((size_t)n_var * 4);
     w.end = (uint32_t*)take((size_t)n_var * 4);
@@ -1055,7 +1064,7 @@ static int group_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64
     const dim3 tgrid((unsigned)g.n_tiles);
 #define EG_TILE_SORT(M)                                                                                            \
   hipLaunchKernelGGL(tile_sort_kernel<M>, tgrid, dim3(kGroupThreads), 0, st, rows, n, ids, n_var, split_shift, idx, \
-                     ib, g.bs, g.nb, g.n_tiles, w.pairs, w.seg)
+                     ib, g.bs, g.nb, g.n_tiles, w.pairs, w.seg, w.n_long)
     if (mode == 2) EG_TILE_SORT(2);
     else if (mode == 1) EG_TILE_SORT(1);
     else EG_TILE_SORT(0);
@@ -1064,7 +1073,7 @@ static int group_slots(const int32_t* rows, int64_t n, const int32_t* ids, int64
     // tiles past the last are wasted issue slots in the kernel's dependent round)
 #define EG_BUCKET_RANGES(TPT)                                                                                     \
   hipLaunchKernelGGL(bucket_ranges_kernel<TPT>, dim3((unsigned)g.nb), dim3(kRangeThreads), 0, st, w.pairs, w.seg, \
-                     g.n_tiles, g.nb, g.bs, n_var, n_long_max(n), w.start, w.end, w.slots, w.long_list)
+                     g.n_tiles, g.nb, g.bs, n_var, w.start, w.end, w.slots, w.long_list, w.n_long)
     if (g.n_tiles <= kRangeThreads) EG_BUCKET_RANGES(1);
     else if (g.n_tiles <= 2 * kRangeThreads) EG_BUCKET_RANGES(2);
     else EG_BUCKET_RANGES(4);
@@ -1099,18 +1108,28 @@ static void fill_seg(SegArgs* a, const Workspace& w, int64_t n, int64_t n_var) {
   a->end = w.end;
   a->slots = w.slots;
   a->long_list = w.long_list;
+  // the counting grouping counts its long variables in off[n_var + 1]
+  a->long_count = plan_for(n, n_var).bucketed ? w.n_long : w.off + n_var + 1;
   a->n = n;
   a->n_var = n_var;
 }
 
+// One workgroup per long-list entry (the list's length is known on the device
+// only): the first kLongHead at the start of the grid, so that the long
+// chains overlap the rest, the others at its end, where the workgroups that
+// find no entry exit within the short ranges' tail.
+constexpr int64_t kLongHead = 256;
+
 template <bool ADAM, int VPL, bool CONSEC>
 static void launch_reduce_t(const SegArgs& a, hipStream_t st) {
-  const int64_t n_long_blocks = n_long_max(a.n);
-  const dim3 grid((unsigned)(n_long_blocks + (a.n_var * 32 + 255) / 256));
+  const int64_t n_long = n_long_max(a.n);
+  const int64_t head = n_long < kLongHead ? n_long : kLongHead;
+  const int64_t n_short = (a.n_var * 32 + 255) / 256;
+  const dim3 grid((unsigned)(n_long + n_short));
   if (a.d_out_f32)
-    hipLaunchKernelGGL((reduce_kernel<VPL, CONSEC, ADAM, true>), grid, dim3(256), 0, st, a, n_long_blocks);
+    hipLaunchKernelGGL((reduce_kernel<VPL, CONSEC, ADAM, true>), grid, dim3(256), 0, st, a, head, n_short);
   else
-    hipLaunchKernelGGL((reduce_kernel<VPL, CONSEC, ADAM, false>), grid, dim3(256), 0, st, a, n_long_blocks);
+    hipLaunchKernelGGL((reduce_kernel<VPL, CONSEC, ADAM, false>), grid, dim3(256), 0, st, a, head, n_short);
 }
 
 template <bool ADAM>
