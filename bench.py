@@ -274,6 +274,42 @@ def cpu_literal_config0(n_pos: int) -> dict:
                       "fp32 add -> bf16; pure Python/numpy"}
 
 
+def forward_table_rows(n_rows: int, dev) -> dict:
+    """The config-1 forward over a table of ``n_rows`` rows (the row ids spread
+    over the whole table as at 320M rows): 16 token batches and four residual
+    sets rotated, 400 launches timed after a warm-up, best of four rounds."""
+    import itertools
+
+    import torch
+
+    from engraft_ngram_amd import synthetic as S
+    from engraft_ngram_amd import table as T
+
+    n_pos = BATCH * SEQ
+    hp = S.hash_params(n_rows, HASH_SEED)
+    tab = T.DeviceTable.synthetic("q8_0", n_rows, DIM, seed=TABLE_SEED, sigma=0.02, device=dev, **hp)
+    toks = [torch.from_numpy(S.zipf_tokens(TOKEN_SEED + 1000 * j, n_pos, VOCAB)).to(dev) for j in range(TOKEN_SETS)]
+    res = [S.residual(n_pos, WIDTH, seed=RES_SEED + i, device=dev) for i in range(RES_SETS)]
+    outs = [torch.empty_like(r) for r in res]
+    n_sets = max(TOKEN_SETS, RES_SETS)
+    calls = [T.PreparedForward([tab], toks[i % TOKEN_SETS], res[i % RES_SETS], out=outs[i % RES_SETS], seq_len=SEQ)
+             for i in range(n_sets)]
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    best = float("inf")
+    for _ in range(4):
+        rot = itertools.count()
+        ramp(lambda: calls[next(rot) % n_sets](), 0.2)
+        torch.cuda.synchronize()
+        a.record()
+        for i in range(400):
+            calls[i % n_sets]()
+        b.record()
+        torch.cuda.synchronize()
+        best = min(best, a.elapsed_time(b) / 400 * 1e3)
+    return {"table_rows": n_rows, "table_bytes": n_rows * Q8_ROW_BYTES, "us_per_launch": best,
+            "frac_of_hbm_peak": forward_bytes(n_pos) / (best * 1e-6) / (HBM_PEAK_GBS * 1e9)}
+
+
 def backward_bytes(positions: int, n_unique: int) -> int:
     """Algorithmic HBM bytes of one descent step (fp32 master
     kept): d_residual read (2 B x W per position), the slots' int32 row ids, and
@@ -412,24 +448,9 @@ def bench_decode(tab, steps: int) -> dict:
     out = torch.empty_like(res)
     ov_bm = DeviceOverlay(ov.ids, store).with_bitmap(tab.n_rows)
 
-    def latencies(overlay, graphs: bool = False) -> list:
+    def latencies(overlay) -> list:
         calls = [T.PreparedForward([tab], tk, res, out=out, overlays=[overlay], decode_ctx=ctx) for tk in toks]
         run = [c for c in calls]
-        if graphs:
-            # one HIP graph per token set (the decode step captured once, replayed per call)
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                for c in calls:
-                    c()
-            torch.cuda.current_stream().wait_stream(side)
-            gs = []
-            for c in calls:
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g):
-                    c()
-                gs.append(g)
-            run = [g.replay for g in gs]
         for i in range(200):
             run[i % 64]()
         rot = itertools.count()
@@ -474,16 +495,14 @@ def bench_decode(tab, steps: int) -> dict:
 
     lat_search = latencies(ov)
     lat = latencies(ov_bm)
-    lat_graph = latencies(ov_bm, graphs=True)
     lat_graph16 = per_step_in_graphs(ov_bm)
     pct = lambda v, q: v[min(len(v) - 1, int(len(v) * q))]
     nbytes = n_seq * (SLOTS * Q8_ROW_BYTES + 2 * 2 * WIDTH + ctx * 8)
     return {"workload": "BASELINE config 3: 256 sequences x (2 context + 1 new token), config-1 table + "
-                        "500,000-row Q8_0 overlay resolved per id through its two-level rank bitmap",
+                        "500,000-row Q8_0 overlay resolved per id through its rank bitmap (Bloom filter + "
+                        "per-word bits and ranks)",
             "calls": steps, "us_p50": pct(lat, 0.5), "us_p99": pct(lat, 0.99), "us_min": lat[0],
             "us_p50_binary_search": pct(lat_search, 0.5), "us_p99_binary_search": pct(lat_search, 0.99),
-            "us_p50_graph_replay": pct(lat_graph, 0.5), "us_p99_graph_replay": pct(lat_graph, 0.99),
-            "us_min_graph_replay": lat_graph[0],
             "us_per_step_p50_graph_of_16_steps": pct(lat_graph16, 0.5),
             "us_per_step_p99_graph_of_16_steps": pct(lat_graph16, 0.99),
             "lookups_per_call": n_seq * SLOTS, "algorithmic_bytes_per_call": nbytes}
@@ -927,6 +946,10 @@ def main() -> None:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (torch copy_) 10 times: the known-size kernel the "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by")
+    ap.add_argument("--forward-table-rows", type=int, default=0,
+                    help="only run the config-1 forward (same tokens, residual and hash seeds) over a table of "
+                         "this many rows, 400 launches, and print its time: the table-size sweep behind the "
+                         "forward's translation-reach measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures the table path on one "
@@ -954,6 +977,10 @@ def main() -> None:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     n_pos = BATCH * SEQ
+
+    if args.forward_table_rows:
+        print(json.dumps({"forward_table_rows": forward_table_rows(args.forward_table_rows, dev)}), flush=True)
+        return
 
     t0 = time.perf_counter()
     hp = S.hash_params(N_ROWS, HASH_SEED)
@@ -1091,8 +1118,7 @@ def main() -> None:
         dc = bench_decode(tab, 200)
         result["decode_config3"] = dc
         log(f"decode (config 3): p50 {dc['us_p50']:.1f} us, p99 {dc['us_p99']:.1f} us per call (binary search in "
-            f"place of the bitmap: p50 {dc['us_p50_binary_search']:.1f} us); as a HIP-graph replay: p50 "
-            f"{dc['us_p50_graph_replay']:.1f} us, p99 {dc['us_p99_graph_replay']:.1f} us; 16 steps captured as one "
+            f"place of the bitmap: p50 {dc['us_p50_binary_search']:.1f} us); 16 steps captured as one "
             f"graph: p50 {dc['us_per_step_p50_graph_of_16_steps']:.1f} us per step")
         c4 = bench_config4(max(50, args.steps // 4), max(20, args.warmup // 4))
         result["forward_config4"] = c4
