@@ -8,12 +8,17 @@ Python on PyTorch-ROCm; every stage runs in hand-written gfx950 HIP kernels
 behind the C ABI of ``include/engraft_ngram.h`` (``libengraft_ngram.so``).
 
 Modules mirror the reference's:
-  table    -- ``engraft.table``       (DeviceTable = PleTable duck type)
-  lens     -- ``engraft.lens``        (.pleo, local_to_global, RowSet)
-  overlay  -- ``engraft.replica.seq`` OverlayEmb / ``model.ple_true_emb``
-  descent  -- ``engraft.replica.distill`` row vars + the optimizer step
-  pack     -- ``engraft.replica.pack`` segments
-  damage   -- ``engraft.damage``      vectorized ngram_rows / scan_hits
+  table       -- ``engraft.table``            (DeviceTable = PleTable duck type)
+  lens        -- ``engraft.lens``             (.pleo, local_to_global, RowSet)
+  seq         -- ``engraft.replica.seq``      OverlayEmb, ple_true_emb, the
+                                               sequence seam, exclusive_rows_at_position
+  overlay     -- the device overlay (sorted ids + rows) the forward resolves per id
+  descent     -- ``engraft.replica.distill``  row vars + the optimizer step
+  dequant     -- ``engraft.replica.dequant``  wire-form row dequantisation
+  pack        -- ``engraft.replica.pack``     segments
+  damage      -- ``engraft.damage``           vectorized ngram_rows / scan_hits
+  overlay_sum -- ``engraft.replica.overlay_sum`` the overlay merge
+  ple         -- ``engraft.replica.layers``   ple_forward / PleWeights, ``engraft.lens`` PleReplica
 """
 from . import _lib  # noqa: F401
 
