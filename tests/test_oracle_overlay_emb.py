@@ -205,3 +205,28 @@ def test_write_merged_rows_order():
     rows, d = OS.write_merged_rows(row_map, rv, [3, 30, 12, 7, 3], fetch)
     assert rows.tolist() == [30, 7, 3, 12]
     assert np.array_equal(d[:2], rv) and np.array_equal(d[2:], data[[3, 12]])
+
+
+def test_exclusive_rows_known_answers():
+    """``engraft/replica/seq.py:924-941`` on streams built so the answer is fixed
+    by the window rule alone (position t's order-n rows depend only on tokens
+    t-n+1..t): a window repeated at another position inside ``n_positions``
+    empties the set, the same repeat past ``n_positions`` leaves all 16 rows,
+    a shared 2-gram with different 3-grams leaves exactly the order-3 heads'
+    rows (heads 8..15), and ``p`` itself is never subtracted.  Large head
+    vocabularies keep hash collisions between the few distinct windows out."""
+    spec = fake_table_spec(2, head_vocab_size=1_000_003)
+    a, b, c, x, y = 11, 12, 13, 14, 15
+    toks = [a, b, c, x, a, b, c]
+    rows = H.ngram_rows_np(spec, toks)
+    assert np.array_equal(rows[2], rows[6])  # the construction: same window
+    assert OE.exclusive_rows_at_position(spec, toks, 7, 2) == set()
+    assert OE.exclusive_rows_at_position(spec, toks, 7, 6) == set()
+    assert OE.exclusive_rows_at_position(spec, toks, 6, 2) == {int(r) for r in rows[2]}
+    assert OE.exclusive_rows_at_position(spec, toks, 7, 3) == {int(r) for r in rows[3]}
+    toks2 = [a, b, c, y, b, c]
+    rows2 = H.ngram_rows_np(spec, toks2)
+    got = OE.exclusive_rows_at_position(spec, toks2, 6, 2)
+    assert got == {int(r) for r in rows2[2, 8:]} and len(got) == 8
+    assert OE.exclusive_rows_at_position(spec, toks2, 6, 2, heads=range(0, 8)) == set()
+    assert OE.exclusive_rows_at_position(spec, toks2, 6, 2, heads=range(8, 10)) == {int(r) for r in rows2[2, 8:10]}
