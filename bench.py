@@ -436,6 +436,7 @@ def bench_decode(tab, steps: int) -> dict:
     from engraft_ngram_amd.overlay import DeviceOverlay
 
     dev = tab.device
+    time.sleep(0.5)  # per-call latency: after the host threads of the CPU leg before it are idle
     n_seq, ctx, n_ov = 256, 3, 500_000
     ids = np.unique(np.random.default_rng(DECODE_SEED).integers(0, N_ROWS, size=n_ov + 4096))[:n_ov]
     store = T.RowStore.empty("q8_0", ids.size, DIM, dev)
@@ -745,6 +746,9 @@ def bench_overlay_emb(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     from engraft_ngram_amd.seq import OverlayEmb
 
     dev = tab.device
+    # a host-bound step: time it after the host threads of earlier CPU legs
+    # (thread pools, BLAS and OpenMP workers that spin after their work) are idle
+    time.sleep(0.5)
     t_len, n_var = 2048, 14_032
     tokens = S.zipf_tokens(SCAN_SEED + 2, t_len, VOCAB)
     rows = tab.rows(torch.from_numpy(tokens).to(dev), seq_len=t_len).cpu().numpy()
@@ -1124,17 +1128,17 @@ def main() -> None:
         result["forward_config4"] = c4
         log(f"forward (config 4): {c4['us_per_launch']:.1f} us/launch, {c4['gb_per_s']:.0f} GB/s algorithmic "
             f"({100 * c4['frac_of_hbm_peak']:.1f}% of peak)")
+        oe = bench_overlay_emb(tab, 100, hp, cpu_leg_s)
+        result["overlay_emb"] = oe
+        log_cpu_leg("overlay_emb", oe)
+        log(f"OverlayEmb (a8): {oe['us_per_step']:.0f} us per build + backward of a 2,048-token sequence "
+            f"({oe['slots_replaced']} slots replaced), {oe['device_us_per_step']:.1f} us of it on the device")
         ds = bench_damage_scan(tab, 20, hp, cpu_leg_s)
         result["damage_scan"] = ds
         log_cpu_leg("damage_scan", ds)
         log(f"damage scan: {ds['us_per_block_kernel']:.0f} us per 8M-token block on the device "
             f"({ds['lookups_per_s_kernel'] / 1e9:.1f} G lookups/s), {ds['s_per_block_end_to_end'] * 1e3:.1f} ms end "
             f"to end ({ds['s_per_block_end_to_end_int32_tokens'] * 1e3:.1f} ms from int32 tokens)")
-        oe = bench_overlay_emb(tab, 100, hp, cpu_leg_s)
-        result["overlay_emb"] = oe
-        log_cpu_leg("overlay_emb", oe)
-        log(f"OverlayEmb (a8): {oe['us_per_step']:.0f} us per build + backward of a 2,048-token sequence "
-            f"({oe['slots_replaced']} slots replaced), {oe['device_us_per_step']:.1f} us of it on the device")
         rf = bench_real_format(max(50, args.steps // 4), max(20, args.warmup // 4))
         result["forward_real_format"] = rf
         log(f"forward (real IQ4_NL format): {rf['us_per_launch']:.1f} us/launch, {rf['gb_per_s']:.0f} GB/s "
