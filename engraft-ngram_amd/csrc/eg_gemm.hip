@@ -379,6 +379,15 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
                                          (__attribute__((address_space(3))) void*)(st + 16 * q * kBK), 16, 0, 0);
       }
     };
+    // load j alone: the half step after the barrier issues them one at a time
+    // between its MFMAs
+    auto issue_one = [&](int64_t kt, int j) {
+      __bf16* st = lds + (kt & 1) * STAGE;
+      const int pl = plane_of(j), q = uwave + NW * j;
+      const __bf16* base = pl == 0 ? sg.a_hi : pl == 1 ? sg.a_lo : pl == 2 ? sg.b_hi[grp] : sg.b_lo[grp];
+      __builtin_amdgcn_global_load_lds((const void*)((const char*)(base + kt * kBK) + off[j]),
+                                       (__attribute__((address_space(3))) void*)(st + 16 * q * kBK), 16, 0, 0);
+    };
     // fragments of half step ks (16 k) of stage kt into set f
     bf16x8 ah[2][TI], al[2][TI], bh[2][TJ], bl[2][TJ];
     auto read = [&](int f, int64_t kt, int ks) {
@@ -416,7 +425,8 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
     // step's reads, long issued, are outstanding; and the next reads reuse the
     // registers of the lo*hi pass's lo planes.  The loads of step kt + 2 are
     // issued once every wavefront has read step kt (the barrier in the middle
-    // of step kt), a step ahead of their use.
+    // of step kt), a step ahead of their use, spread over the half step after
+    // that barrier.
     issue(lo - seg0);
     if (lo + 1 < hi) {
       issue(lo + 1 - seg0);
@@ -441,13 +451,31 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
       wait_vm<0>();
       wait_lgkm0();
       __builtin_amdgcn_s_barrier();
-      if (kv + 2 < hi) issue(kt + 2);
-      mfma(1, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      read(0, kt + 1, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma(1, 1);
-      mfma(1, 2);
+      {
+        // the second half step's MFMAs (its three passes) with the next half
+        // step's fragment reads after the first pass and the loads of step
+        // kt + 2 one after every second MFMA: a wavefront's direct-to-LDS loads
+        // go out one at a time, and in a burst they held the younger wavefront
+        // of each SIMD for ~2,700 cycles without an MFMA (the burst form took
+        // 2 % longer a step)
+        const bool ld = kv + 2 < hi;
+#pragma unroll
+        for (int t = 0; t < 3 * TI * TJ; ++t) {
+          const int pass = t / (TI * TJ), i = (t % (TI * TJ)) / TJ, j = t % TJ;
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pass == 0 ? al[1][i] : ah[1][i],
+                                                               pass == 1 ? bl[1][j] : bh[1][j], acc[i][j], 0, 0, 0);
+          if (t == TI * TJ - 1) {
+            __builtin_amdgcn_sched_barrier(0);
+            read(0, kt + 1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          if ((t + 1) % 2 == 0 && (t + 1) / 2 - 1 < LPW) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (ld) issue_one(kt + 2, (t + 1) / 2 - 1);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
     }
     mfma(0, 0);
     read(1, hi - 1 - seg0, 1);
