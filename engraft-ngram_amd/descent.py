@@ -53,7 +53,7 @@ class _Workspace:
     def get(self, n_slots: int, n_var: int, device) -> torch.Tensor:
         need = int(_lib.load().eg_backward_workspace_size(int(n_slots), int(n_var)))
         dev = torch.device(device)
-        key = (dev, int(torch.cuda.current_stream(dev).cuda_stream))
+        key = (dev, _lib.stream_ptr(dev))
         buf = self._buf.get(key)
         if buf is None or buf.numel() < need:
             buf = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)

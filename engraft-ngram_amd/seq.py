@@ -88,7 +88,7 @@ class _GatherSlots(torch.autograd.Function):
         if vars32.dtype != torch.float32 or vars32.device != dev or not vars32.is_contiguous():
             vars32 = vars32.to(device=dev, dtype=torch.float32).contiguous()
         out = torch.empty((n, heads * dim), dtype=torch.float32, device=dev)
-        st = torch.cuda.current_stream(dev).cuda_stream
+        st = _lib.stream_ptr(dev)
         rc = _lib.load().eg_gather_slots(ctypes.byref(table.c_table), rows.data_ptr(), slot_var.data_ptr(), n, heads,
                                          vars32.data_ptr(), vars32.shape[0], out.data_ptr(), st)
         _lib.check(rc)
@@ -107,7 +107,7 @@ class _GatherSlots(torch.autograd.Function):
         grad = torch.empty((n_var, dim), dtype=torch.float32, device=dev)
         if n_var > 0:
             ws = _slot_grouping(ctx.plan, n_var, dev) if n > 0 else None
-            st = torch.cuda.current_stream(dev).cuda_stream
+            st = _lib.stream_ptr(dev)
             rc = _lib.load().eg_scatter_grad_apply(d.data_ptr(), _dout_args(d), n, heads, dim, n_var,
                                                    grad.data_ptr(), 1, _lib.ptr(ws),
                                                    ws.numel() if ws is not None else 0, st)
@@ -284,8 +284,10 @@ class OverlayEmb:
         self.n_key_hits = plan["n_key_hits"]
         self.n_id_hits = plan["n_id_hits"]
         out = _GatherSlots.apply(self.rows_var, self.table, plan)
-        out = out.to(device=self.rows_var.device, dtype=self.rows_var.dtype)
-        return out.reshape(n_positions - start, self.table.n_heads * self.table.row_len)
+        if out.dtype != self.rows_var.dtype or out.device != self.rows_var.device:
+            out = out.to(device=self.rows_var.device, dtype=self.rows_var.dtype)
+        # [n_positions - start, n_heads * row_len] as the plan's rows are
+        return out if out.shape[0] == n_positions - start else out.reshape(n_positions - start, -1)
 
 
 def _as_overlay(table, overlay) -> DeviceOverlay | None:

@@ -489,7 +489,7 @@ class PreparedForward:
         self.n_positions = n
 
     def __call__(self, stream: int | None = None) -> None:
-        st = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
+        st = stream if stream is not None else _lib.stream_ptr(self.device)
         rc = self._fn(*self._args, st)
         if rc != _lib.EG_OK:
             _lib.check(rc)
@@ -499,7 +499,7 @@ class PreparedForward:
         handles receive the kernel dispatch's own start / end timestamps."""
         if self._decode or self.slot_vars is not None:
             raise ValueError("timed launches are for eg_forward")
-        st = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
+        st = stream if stream is not None else _lib.stream_ptr(self.device)
         rc = _lib.load().eg_forward_timed(*self._args, start_event, stop_event, st)
         if rc != _lib.EG_OK:
             _lib.check(rc)
@@ -557,7 +557,7 @@ class PreparedForwardRows:
         self.device = dev
 
     def __call__(self, stream: int | None = None) -> None:
-        st = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
+        st = stream if stream is not None else _lib.stream_ptr(self.device)
         rc = self._fn(*self._args, st)
         if rc != _lib.EG_OK:
             _lib.check(rc)

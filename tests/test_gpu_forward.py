@@ -687,3 +687,21 @@ def test_dequant_wire_blocks_against_oracle(cuda, fmt):
         fn = dequant.DEQUANT_FNS[fmt.upper()]
         dec = fn(torch.from_numpy(raw_rows).reshape(40, -1, bb)).reshape(40, -1).numpy()
         assert np.array_equal(dec, tab.read_rows(3, 17, 40))
+
+
+def test_stream_ptr_is_the_current_stream(cuda):
+    """``_lib.stream_ptr`` (torch's raw-stream query) names the stream torch
+    calls current, for every way of giving the device and inside a stream
+    context: the launches go where torch's own work goes."""
+    from engraft_ngram_amd import _lib
+
+    _say("stream_ptr")
+    dev = torch.device("cuda", torch.cuda.current_device())
+    forms = (None, dev, dev.index, f"cuda:{dev.index}", torch.device("cuda"))
+    want = int(torch.cuda.current_stream(dev).cuda_stream)
+    assert all(_lib.stream_ptr(d) == want for d in forms)
+    s = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s):
+        assert int(s.cuda_stream) != want
+        assert all(_lib.stream_ptr(d) == int(s.cuda_stream) for d in forms)
+    assert _lib.stream_ptr(dev) == want
