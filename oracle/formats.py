@@ -142,7 +142,8 @@ def dequant_mxfp8(payload, scales) -> np.ndarray:
     e = np.asarray(scales, dtype=np.uint8).astype(np.int32)
     n, dim = v.shape
     scale = np.where(e == 255, np.nan, np.ldexp(np.float32(1.0), e - 127)).astype(np.float32)
-    return (v.reshape(n, dim // BLOCK, BLOCK) * scale[:, :, None]).reshape(n, dim).astype(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):  # large scales give inf, NaN scales NaN: the format's values
+        return (v.reshape(n, dim // BLOCK, BLOCK) * scale[:, :, None]).reshape(n, dim).astype(np.float32)
 
 
 def quant_mxfp8(x) -> tuple[np.ndarray, np.ndarray]:
