@@ -14,7 +14,7 @@ reference (``engraft/replica/distill.py:378-453`` row variables,
   requantised copy in HBM; ``step`` runs scatter + Adam (torch's single-tensor
   order, fp32) + requantisation in one call (``eg_descent_step``), in the
   reference's dense mode (every variable steps, ``torch.optim.Adam([rows_var])``)
-  or the sparse mode of BASELINE config 2 (only the rows this batch hit).
+  or the sparse mode of the benchmark's config 2 (only the rows this batch hit).
 """
 from __future__ import annotations
 

@@ -12,7 +12,7 @@
   variant generators and ``build_overlay`` keep the reference's semantics.
 
 The ``.pleo`` dimension is the table's row length (160 for the reference's real
-tables; the synthetic tables of BASELINE use 128).
+tables; the benchmark's synthetic tables use 128).
 """
 from __future__ import annotations
 

@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs of BASELINE's configurations (benchmark inputs).
+"""Seeded synthetic inputs of the benchmark's configurations.
 
 * ``hash_params``  -- BASELINE's synthetic table addressing: the table is split
   evenly between the ``(ngram_size-1)*heads_per_ngram`` heads, and every head
