@@ -1,10 +1,10 @@
 """Seeded synthetic inputs of the benchmark's configurations.
 
-* ``hash_params``  -- BASELINE's synthetic table addressing: the table is split
-  evenly between the ``(ngram_size-1)*heads_per_ngram`` heads, and every head
-  has its own seeded odd 64-bit multiplier per context slot (BASELINE: "16 fixed
-  seeded 64-bit odd multipliers, mod rows").  EOS, which BASELINE leaves open, is
-  151,643 (Qwen ``<|endoftext|>``).
+* ``hash_params``  -- the benchmark's synthetic table addressing: the table is
+  split evenly between the ``(ngram_size-1)*heads_per_ngram`` heads, and every
+  head has its own seeded odd 64-bit multiplier per context slot (the
+  benchmark's "16 fixed seeded 64-bit odd multipliers, mod rows").  EOS, which
+  the benchmark's definition leaves open, is 151,643 (Qwen ``<|endoftext|>``).
 * ``table``        -- a seeded table generated in place on the device
   (``eg_synth_table``): value j of row r is a normal quantile picked by
   SplitMix64 of ``(seed, r, j)``, quantised with the format's rule.
