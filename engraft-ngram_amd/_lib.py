@@ -11,6 +11,9 @@ from ctypes import POINTER, c_char_p, c_int32, c_int64, c_uint64, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libengraft_ngram.so"
+# the C++ autograd functions over the library's entry points (csrc/eg_autograd.cpp)
+EXT_NAME = "_eg_autograd"
+EXT_PATH = Path(__file__).resolve().parent / "_eg_autograd.so"
 
 EG_MAX_NGRAM = 4
 EG_MAX_HEADS = 32
@@ -225,6 +228,35 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     if path is None:
         _LIB = lib
     return lib
+
+
+_EXT = None
+
+
+def autograd_ext():
+    """The C++ autograd module (``_eg_autograd.so``, built beside the library
+    by the same build), bound once to the loaded library's entry points;
+    raises RuntimeError if it is absent (no Python stand-in)."""
+    global _EXT
+    if _EXT is not None:
+        return _EXT
+    if not EXT_PATH.exists():
+        raise RuntimeError(f"{EXT_PATH} not found: build it with `python engraft-ngram_amd/build.py` "
+                           "(or __graft_entry__.build())")
+    import importlib.machinery
+    import importlib.util
+
+    import torch  # noqa: F401  (the module links torch's libraries)
+
+    loader = importlib.machinery.ExtensionFileLoader(EXT_NAME, str(EXT_PATH))
+    spec = importlib.util.spec_from_file_location(EXT_NAME, str(EXT_PATH), loader=loader)
+    mod = importlib.util.module_from_spec(spec)
+    loader.exec_module(mod)
+    lib = load()
+    mod.init(*(ctypes.cast(getattr(lib, f), c_void_p).value
+               for f in ("eg_gather_slots", "eg_scatter_grad_apply", "eg_last_error")))
+    _EXT = mod
+    return mod
 
 
 class EgError(RuntimeError):

@@ -16,15 +16,18 @@ per-position Python loop:
    keys, which win over the global row -- host dict lookups, one per
    position, only when ``row_map`` has tuple keys;
 3. gather: every slot reads ``rows_var[slot_var]`` or, without a variable, its
-   dequantised table row (``eg_gather_slots``).
+   dequantised table row (``eg_gather_slots``), through a C++ autograd
+   function (``csrc/eg_autograd.cpp``) whose backward takes no GIL.
 
 The slot plan (rows + slot variables, the part that does not depend on
 ``rows_var``) is cached per ``(tokens, start, n_positions, segment starts)``
 on the instance, and per fragment in the caller's ``overlay_cache`` (FIFO,
 4096 entries), like the reference's base cache.  The backward of the gather
-is ``eg_scatter_grad_slots``: every variable's slot gradients summed in
-ascending slot order, deterministically (the same association as the descent
-step's scatter).
+sums every variable's slot gradients in ascending slot order,
+deterministically (the same association as the descent step's scatter), from
+the slots' grouping by variable that the first build wanting a gradient makes
+and keeps with the plan (``eg_scatter_grad_plan_slots``, then
+``eg_scatter_grad_apply`` every backward).
 """
 from __future__ import annotations
 
@@ -37,7 +40,6 @@ import numpy as np
 import torch
 
 from . import _lib
-from .descent import _WS, _dout_args
 from .overlay import DeviceOverlay
 from .pack import seg_starts_from_segment_ids
 
@@ -72,49 +74,15 @@ def _slot_grouping(plan: dict, n_var: int, dev) -> torch.Tensor:
     return ws
 
 
-class _GatherSlots(torch.autograd.Function):
-    """out f32 ``[n, H*D]`` = per slot ``vars[slot_var]`` or the table row
-    (``eg_gather_slots``); backward: the variables' gradients summed over
-    their slots from the plan's cached grouping (``eg_scatter_grad_apply``,
-    written whole: a variable no slot reads gets zeros)."""
+_NO_WS: dict = {}
 
-    @staticmethod
-    def forward(ctx, rows_var, table, plan):
-        rows, slot_var = plan["rows"], plan["slot_var"]
-        n, heads = rows.shape
-        dim = table.row_len
-        dev = table.device
-        vars32 = rows_var.detach()
-        if vars32.dtype != torch.float32 or vars32.device != dev or not vars32.is_contiguous():
-            vars32 = vars32.to(device=dev, dtype=torch.float32).contiguous()
-        out = torch.empty((n, heads * dim), dtype=torch.float32, device=dev)
-        st = _lib.stream_ptr(dev)
-        rc = _lib.load().eg_gather_slots(ctypes.byref(table.c_table), rows.data_ptr(), slot_var.data_ptr(), n, heads,
-                                         vars32.data_ptr(), vars32.shape[0], out.data_ptr(), st)
-        _lib.check(rc)
-        ctx.plan = plan
-        ctx.meta = (heads, dim, vars32.shape[0], rows_var.dtype, rows_var.device, dev)
-        return out
 
-    @staticmethod
-    def backward(ctx, d_out):
-        heads, dim, n_var, dtype, device, dev = ctx.meta
-        d = d_out if d_out.device == dev else d_out.to(device=dev)
-        if d.dtype not in (torch.float32, torch.bfloat16):
-            d = d.float()
-        d = d.contiguous()
-        n = ctx.plan["slot_var"].shape[0]
-        grad = torch.empty((n_var, dim), dtype=torch.float32, device=dev)
-        if n_var > 0:
-            ws = _slot_grouping(ctx.plan, n_var, dev) if n > 0 else None
-            st = _lib.stream_ptr(dev)
-            rc = _lib.load().eg_scatter_grad_apply(d.data_ptr(), _dout_args(d), n, heads, dim, n_var,
-                                                   grad.data_ptr(), 1, _lib.ptr(ws),
-                                                   ws.numel() if ws is not None else 0, st)
-            _lib.check(rc)
-        if grad.dtype != dtype or grad.device != device:
-            grad = grad.to(device=device, dtype=dtype)
-        return grad, None, None
+def _no_grouping(dev) -> torch.Tensor:
+    """The empty workspace that stands for "no grouping" on ``dev``."""
+    ws = _NO_WS.get(dev)
+    if ws is None:
+        ws = _NO_WS[dev] = torch.empty(0, dtype=torch.uint8, device=dev)
+    return ws
 
 
 @dataclasses.dataclass
@@ -283,9 +251,21 @@ class OverlayEmb:
                 self._plans[key] = plan
         self.n_key_hits = plan["n_key_hits"]
         self.n_id_hits = plan["n_id_hits"]
-        out = _GatherSlots.apply(self.rows_var, self.table, plan)
-        if out.dtype != self.rows_var.dtype or out.device != self.rows_var.device:
-            out = out.to(device=self.rows_var.device, dtype=self.rows_var.dtype)
+        # out f32 [n, heads * dim] = per slot rows_var[slot_var] or the table row
+        # (eg_gather_slots), differentiable in rows_var: its backward sums the
+        # output gradient into the variables from the plan's slot grouping
+        # (eg_scatter_grad_apply; written whole, a variable no slot reads gets
+        # zeros).  A C++ autograd function (csrc/eg_autograd.cpp).
+        rv = self.rows_var
+        dev = self.table.device
+        n, n_var = plan["rows"].shape[0], rv.shape[0]
+        wants_grad = rv.requires_grad and torch.is_grad_enabled()
+        ws = _slot_grouping(plan, n_var, dev) if wants_grad and n > 0 and n_var > 0 else _no_grouping(dev)
+        ct = self.table.c_table
+        out = _lib.autograd_ext().gather_slots(rv, plan["rows"], plan["slot_var"], ws, ctypes.addressof(ct),
+                                               self.table.row_len, _lib.stream_ptr(dev))
+        if out.dtype != rv.dtype or out.device != rv.device:
+            out = out.to(device=rv.device, dtype=rv.dtype)
         # [n_positions - start, n_heads * row_len] as the plan's rows are
         return out if out.shape[0] == n_positions - start else out.reshape(n_positions - start, -1)
 

@@ -36,6 +36,28 @@ def test_library_exports_every_declared_symbol():
     assert set(declared_symbols()) <= set(_lib.SIGNATURES)
 
 
+def test_autograd_module_loads_and_checks_its_arguments():
+    """The C++ autograd module (OverlayEmb's gather) is built beside the
+    library, binds to the library's entry points, and refuses a malformed plan
+    on the host before calling them."""
+    import torch
+
+    from engraft_ngram_amd import _lib
+
+    if not _lib.EXT_PATH.exists():
+        pytest.fail(f"{_lib.EXT_PATH} not built: run __graft_entry__.build()")
+    ext = _lib.autograd_ext()
+    assert callable(ext.init) and callable(ext.gather_slots)
+    rows = torch.zeros((3, 16), dtype=torch.int32)
+    ws = torch.empty(0, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="slot_var"):
+        ext.gather_slots(torch.zeros((2, 128)), rows, rows[:2].clone(), ws, 0, 128, 0)
+    with pytest.raises(RuntimeError, match="rows_var"):
+        ext.gather_slots(torch.zeros((2, 64)), rows, rows.clone(), ws, 0, 128, 0)
+    with pytest.raises(RuntimeError, match="ws"):
+        ext.gather_slots(torch.zeros((2, 128)), rows, rows.clone(), torch.empty(0), 0, 128, 0)
+
+
 def test_abi_version_and_error_string():
     from engraft_ngram_amd import _lib
 

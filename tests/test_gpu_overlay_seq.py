@@ -64,6 +64,43 @@ def test_overlay_emb_int_keys_forward_and_grad(cuda):
     assert np.array_equal(e2, exp2)
 
 
+def test_overlay_emb_backward_is_the_native_function(cuda):
+    """build() returns the C++ autograd function's output (its backward takes
+    no GIL); an upstream gradient in bf16 (which autograd casts to the output's
+    f32) gives the gradient of its f32 copy; bf16 variables give a bf16
+    embedding and the f32 gradient rounded once; a forward without a gradient
+    makes no slot grouping."""
+    from engraft_ngram_amd.seq import OverlayEmb
+    _say("OverlayEmb native autograd node, bf16 gradient")
+    spec = synthetic_spec(n_rows=16 * 700, seed=41)
+    tab = G.device_table(spec, "q8_0", 16 * 700, 128, seed=42)
+    tokens = [int(x) for x in np.random.default_rng(43).zipf(1.3, 300) % 900]
+    rows = H.ngram_rows_np(spec, tokens)
+    row_map = _row_map(rows, 4)
+    R = len(row_map)
+    rv = (torch.randn((R, 128), generator=torch.Generator().manual_seed(44)) * 0.05).to(cuda)
+    oe = OverlayEmb(tab, tokens, rv, row_map)
+    with torch.no_grad():
+        oe.build(300)
+    assert "grouping" not in oe._plans[(0, 300)]
+    rv.requires_grad_(True)
+    emb = oe.build(300)
+    assert "GatherSlots" in emb.grad_fn.name()
+    d = torch.randn(emb.shape, generator=torch.Generator().manual_seed(45)).to(cuda).bfloat16()
+    emb.backward(d)
+    g32 = rv.grad.clone()
+    rv.grad = None
+    oe.build(300).backward(d.float())
+    assert torch.equal(g32, rv.grad)
+    rvb = rv.detach().bfloat16().requires_grad_(True)
+    oe.rows_var = rvb
+    eb = oe.build(300)
+    assert eb.dtype == torch.bfloat16
+    assert torch.equal(eb.float(), oe.build(300).detach().float())
+    eb.backward(d)
+    assert rvb.grad.dtype == torch.bfloat16 and torch.equal(rvb.grad, g32.bfloat16())
+
+
 def test_overlay_emb_long_keys_segments_and_start(cuda):
     from engraft_ngram_amd.pack import pack_fragments
     from engraft_ngram_amd.seq import OverlayEmb
