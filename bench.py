@@ -775,6 +775,19 @@ def bench_overlay_emb(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     b.record()
     torch.cuda.synchronize()
     us = a.elapsed_time(b) / steps * 1e3
+    # The same steps with autograd's backward run on the calling thread (torch's
+    # thread-local switch; by default the engine hands a CUDA backward to its
+    # device thread and waits for it).
+    with torch.autograd.set_multithreading_enabled(False):
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(steps):
+            step()
+        b.record()
+        torch.cuda.synchronize()
+    us_calling_thread = a.elapsed_time(b) / steps * 1e3
     hits = int(oe.n_id_hits)
     # The device's share of the step: the same two launches (eg_gather_slots over
     # the cached plan, eg_scatter_grad_apply from its cached grouping) issued back
@@ -812,10 +825,14 @@ def bench_overlay_emb(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     dev_us = a.elapsed_time(b) / steps * 1e3
     out = {"workload": "OverlayEmb: 2,048-token sequence, config-1 table, 14,032 fp32 variable rows; build + backward",
            "us_per_step": us, "positions_per_s": t_len / (us * 1e-6), "slots_replaced": hits,
+           "us_per_step_backward_on_calling_thread": us_calling_thread,
            "device_us_per_step": dev_us,
            "device_us_per_step_note": "eg_gather_slots + eg_scatter_grad_apply back to back (the step's kernels, "
                                       "outputs checked equal to the autograd step's); us_per_step adds torch "
-                                      "autograd's host work around them"}
+                                      "autograd's host work around them (build() and the backward are C++ autograd "
+                                      "code; torch's engine runs a CUDA backward on its device thread, and "
+                                      "us_per_step_backward_on_calling_thread is the same step under "
+                                      "torch.autograd.set_multithreading_enabled(False))"}
     if cpu_s > 0 and hp is not None:
         # The reference's step on the CPU with the plan cached (seq.py:428-444):
         # base.index_put((idx_t, idx_h), rows_var[idx_r]) and the autograd

@@ -83,7 +83,8 @@ def dequant_q8_0(payload, scales) -> np.ndarray:
     d = np.asarray(scales, dtype=np.float16).astype(np.float32)
     n, dim = q.shape
     qb = q.reshape(n, dim // BLOCK, BLOCK).astype(np.float32)
-    return (qb * d[:, :, None]).reshape(n, dim)
+    with np.errstate(invalid="ignore"):  # inf scales times zero codes give NaN, as the format's arithmetic does
+        return (qb * d[:, :, None]).reshape(n, dim)
 
 
 def quant_q8_0(x) -> tuple[np.ndarray, np.ndarray]:
@@ -141,8 +142,8 @@ def dequant_mxfp8(payload, scales) -> np.ndarray:
     v = e4m3_to_f32(payload)
     e = np.asarray(scales, dtype=np.uint8).astype(np.int32)
     n, dim = v.shape
-    scale = np.where(e == 255, np.nan, np.ldexp(np.float32(1.0), e - 127)).astype(np.float32)
     with np.errstate(over="ignore", invalid="ignore"):  # large scales give inf, NaN scales NaN: the format's values
+        scale = np.where(e == 255, np.nan, np.ldexp(np.float32(1.0), e - 127)).astype(np.float32)
         return (v.reshape(n, dim // BLOCK, BLOCK) * scale[:, :, None]).reshape(n, dim).astype(np.float32)
 
 
@@ -180,7 +181,8 @@ def dequant_iq4nl(raw) -> np.ndarray:
     d = blocks[:, :, 0:2].copy().view(np.float16).astype(np.float32).reshape(n, nb)
     qs = blocks[:, :, 2:]
     y = np.concatenate([KVALUES_IQ4NL[qs & 0x0F], KVALUES_IQ4NL[qs >> 4]], axis=2)
-    return (y * d[:, :, None]).reshape(n, nb * BLOCK).astype(np.float32)
+    with np.errstate(invalid="ignore"):  # inf scales times zero codes give NaN, as the format's arithmetic does
+        return (y * d[:, :, None]).reshape(n, nb * BLOCK).astype(np.float32)
 
 
 def row_is_zero(raw) -> np.ndarray:
