@@ -5,7 +5,9 @@ gather + dequantisation of block-quantised table rows, their add into the
 residual stream, and the descent backward (deterministic sparse gradient
 scatter + Adam + requantisation on the touched overlay rows).  Host code is
 Python on PyTorch-ROCm; every stage runs in hand-written gfx950 HIP kernels
-behind the C ABI of ``include/engraft_ngram.h`` (``libengraft_ngram.so``).
+behind the C ABI of ``include/engraft_ngram.h`` (``libengraft_ngram.so``);
+``OverlayEmb``'s differentiable gather is a C++ autograd function over two of
+those entry points (``_eg_autograd.so``, host code built beside the library).
 
 Modules mirror the reference's:
   table       -- ``engraft.table``            (DeviceTable = PleTable duck type)
