@@ -765,8 +765,10 @@ def bench_overlay_emb(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
         oe.build(t_len).backward(g)
 
     step()  # plans the sequence once, as the reference's overlay_cache does
-    for _ in range(20):
-        step()
+    # a host-bound step: timed in steady state, after a fifth of a second of
+    # steps (the host cores at speed) and over at least 1,000 steps
+    steps = max(steps, 1000)
+    repeat_for(step, 0.2)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
@@ -779,8 +781,7 @@ def bench_overlay_emb(tab, steps: int, hp: dict | None = None, cpu_s: float = 0.
     # thread-local switch; by default the engine hands a CUDA backward to its
     # device thread and waits for it).
     with torch.autograd.set_multithreading_enabled(False):
-        for _ in range(20):
-            step()
+        repeat_for(step, 0.2)
         torch.cuda.synchronize()
         a.record()
         for _ in range(steps):

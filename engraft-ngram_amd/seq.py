@@ -120,6 +120,8 @@ class OverlayEmb:
             edges = [0] + bounds.tolist() + [len(starts)]
             self._seg_ranges = [(edges[i], edges[i + 1]) for i in range(len(edges) - 1) if edges[i + 1] > edges[i]]
         dev = self.table.device
+        self._dev = dev
+        self._row_len = self.table.row_len
         int_keys = [k for k in self.row_map if not isinstance(k, tuple)]
         ids = np.array(int_keys, dtype=np.int64)
         var = np.array([self.row_map[k] for k in int_keys], dtype=np.int64)
@@ -236,10 +238,14 @@ class OverlayEmb:
     def build(self, n_positions: int, start: int = 0) -> torch.Tensor:
         if not 0 <= start <= n_positions <= len(self._tok):
             raise IndexError(f"positions [{start}, {n_positions}) outside the {len(self._tok)} tokens")
-        if self.rows_var.dim() != 2 or self.rows_var.shape[1] != self.table.row_len:
-            raise ValueError(f"rows_var must be [R, {self.table.row_len}], got {tuple(self.rows_var.shape)}")
-        if self._max_var >= self.rows_var.shape[0]:
-            raise IndexError(f"row_map names row {self._max_var} of a {self.rows_var.shape[0]}-row rows_var")
+        rv = self.rows_var
+        shape = rv.shape
+        row_len, dev = self._row_len, self._dev
+        if len(shape) != 2 or shape[1] != row_len:
+            raise ValueError(f"rows_var must be [R, {row_len}], got {tuple(shape)}")
+        n_var = shape[0]
+        if self._max_var >= n_var:
+            raise IndexError(f"row_map names row {self._max_var} of a {n_var}-row rows_var")
         if self.overlay_cache is not None and self._seg_ranges is not None and start == 0:
             plan = self._plan_fragments(n_positions)
         else:
@@ -256,15 +262,14 @@ class OverlayEmb:
         # output gradient into the variables from the plan's slot grouping
         # (eg_scatter_grad_apply; written whole, a variable no slot reads gets
         # zeros).  A C++ autograd function (csrc/eg_autograd.cpp).
-        rv = self.rows_var
-        dev = self.table.device
-        n, n_var = plan["rows"].shape[0], rv.shape[0]
-        wants_grad = rv.requires_grad and torch.is_grad_enabled()
-        ws = _slot_grouping(plan, n_var, dev) if wants_grad and n > 0 and n_var > 0 else _no_grouping(dev)
+        rows = plan["rows"]
+        n = rows.shape[0]
+        ws = (_slot_grouping(plan, n_var, dev) if n > 0 and n_var > 0 and rv.requires_grad and torch.is_grad_enabled()
+              else _no_grouping(dev))
         ct = self.table.c_table
-        out = _lib.autograd_ext().gather_slots(rv, plan["rows"], plan["slot_var"], ws, ctypes.addressof(ct),
-                                               self.table.row_len, _lib.stream_ptr(dev))
-        if out.dtype != rv.dtype or out.device != rv.device:
+        out = _lib.autograd_ext().gather_slots(rv, rows, plan["slot_var"], ws, ctypes.addressof(ct), row_len,
+                                               _lib.stream_ptr(dev))
+        if rv.dtype is not torch.float32 or rv.device != dev:
             out = out.to(device=rv.device, dtype=rv.dtype)
         # [n_positions - start, n_heads * row_len] as the plan's rows are
         return out if out.shape[0] == n_positions - start else out.reshape(n_positions - start, -1)
