@@ -195,13 +195,17 @@ def test_gemm_f32_argument_errors(cuda):
 # inside one tile); 280 tiles, 24 in ranges of 9-10 of their 100 K steps (most
 # ranges meet two tiles); 264 tiles of 16 K steps, too short for ranges, the 8
 # past the first round in halves after 256 whole tiles.  bf16x3, the same
-# tiles and plans: ranges inside one tile and ranges across two.
+# tiles and plans: ranges inside one tile and ranges across two.  The ragged
+# shapes' last row and column tiles lie partly outside C (the parts' sum is
+# stored only inside it).
 _LAST_ROUND = [
     ("f32", 1024, 18432, 2048, "ranges", 2 * 256 * 256 * 256 * 4),
     ("f32", 1024, 17920, 3200, "ranges", 2 * 256 * 256 * 256 * 4),
+    ("f32", 1000, 18400, 3200, "ranges", 2 * 256 * 256 * 256 * 4),
     ("f32", 2048, 8448, 512, "halves", 8 * 2 * 256 * 256 * 4),
     ("bf16x3", 1024, 18432, 2048, "ranges", 2 * 256 * 256 * 256 * 4),
     ("bf16x3", 1024, 17920, 3200, "ranges", 2 * 256 * 256 * 256 * 4),
+    ("bf16x3", 1000, 18400, 3200, "ranges", 2 * 256 * 256 * 256 * 4),
 ]
 
 
