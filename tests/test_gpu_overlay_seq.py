@@ -68,8 +68,9 @@ def test_overlay_emb_backward_is_the_native_function(cuda):
     """build() returns the C++ autograd function's output (its backward takes
     no GIL); an upstream gradient in bf16 (which autograd casts to the output's
     f32) gives the gradient of its f32 copy; bf16 variables give a bf16
-    embedding and the f32 gradient rounded once; a forward without a gradient
-    makes no slot grouping."""
+    embedding and the f32 gradient rounded once; host variables give a host
+    embedding and gradient; a forward without a gradient makes no slot
+    grouping."""
     from engraft_ngram_amd.seq import OverlayEmb
     _say("OverlayEmb native autograd node, bf16 gradient")
     spec = synthetic_spec(n_rows=16 * 700, seed=41)
@@ -99,6 +100,13 @@ def test_overlay_emb_backward_is_the_native_function(cuda):
     assert torch.equal(eb.float(), oe.build(300).detach().float())
     eb.backward(d)
     assert rvb.grad.dtype == torch.bfloat16 and torch.equal(rvb.grad, g32.bfloat16())
+    # variables on the host: the embedding comes back there, the gradient too
+    rvc = rv.detach().cpu().requires_grad_(True)
+    oe.rows_var = rvc
+    ec = oe.build(300)
+    assert ec.device.type == "cpu" and torch.equal(ec.detach(), emb.detach().cpu())
+    ec.backward(d.float().cpu())
+    assert rvc.grad.device.type == "cpu" and torch.equal(rvc.grad, g32.cpu())
 
 
 def test_overlay_emb_long_keys_segments_and_start(cuda):
