@@ -64,17 +64,16 @@ struct GatherSlots : public torch::autograd::Function<GatherSlots> {
                    (int32_t)heads, vars.data_ptr<float>(), n_var, out.data_ptr<float>(),
                    reinterpret_cast<void*>(stream)));
     ctx->saved_data["ws"] = ws;
-    ctx->saved_data["shape"] = std::vector<int64_t>{n, heads, dim, n_var, stream};
-    ctx->saved_data["var_dtype"] = rows_var.scalar_type();
-    ctx->saved_data["var_device"] = rows_var.device();
+    ctx->saved_data["meta"] = std::vector<int64_t>{n, heads, dim, n_var, stream, (int64_t)rows_var.scalar_type(),
+                                                   (int64_t)rows_var.device().type(), rows_var.device().index()};
     return out;
   }
 
   static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
                                                  torch::autograd::variable_list grads) {
-    const auto shape = ctx->saved_data["shape"].toIntVector();
-    const int64_t n = shape[0], heads = shape[1], dim = shape[2], n_var = shape[3], stream = shape[4];
-    const torch::Tensor ws = ctx->saved_data["ws"].toTensor();
+    const c10::List<int64_t> meta = ctx->saved_data["meta"].toIntList();
+    const int64_t n = meta[0], heads = meta[1], dim = meta[2], n_var = meta[3], stream = meta[4];
+    const torch::Tensor& ws = ctx->saved_data["ws"].toTensor();
     torch::Tensor d = grads[0];
     if (d.device() != ws.device()) d = d.to(ws.device());
     if (d.scalar_type() != torch::kFloat32 && d.scalar_type() != torch::kBFloat16) d = d.to(torch::kFloat32);
@@ -86,8 +85,8 @@ struct GatherSlots : public torch::autograd::Function<GatherSlots> {
                       grad.data_ptr<float>(), 1, ws.numel() > 0 ? ws.data_ptr() : nullptr, (size_t)ws.numel(),
                       reinterpret_cast<void*>(stream)));
     }
-    const auto dtype = ctx->saved_data["var_dtype"].toScalarType();
-    const auto device = ctx->saved_data["var_device"].toDevice();
+    const auto dtype = (c10::ScalarType)meta[5];
+    const c10::Device device((c10::DeviceType)meta[6], (c10::DeviceIndex)meta[7]);
     if (grad.scalar_type() != dtype || grad.device() != device) grad = grad.to(device, dtype);
     return {grad, torch::Tensor(), torch::Tensor(), torch::Tensor(), torch::Tensor(), torch::Tensor(),
             torch::Tensor()};
