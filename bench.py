@@ -905,7 +905,7 @@ def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
     d_out = rnd(t_len, hc, n, sc=1e-3)
     emb_v = emb.clone().requires_grad_(True)
     res = {}
-    for mode in ("fp32", "bf16x3"):
+    for mode in ("fp32", "bf16x3", "bf16x6"):
         with torch.no_grad():
             for _ in range(warmup):
                 ple.ple_forward(emb, hidden, w, hist, HP, gemm=mode)
@@ -921,9 +921,12 @@ def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
                 ramp(lib, 0.3)  # its first calls under a new setting pick and load kernels
                 lib_ms = timed(lib, steps)
                 torch.backends.cuda.matmul.allow_tf32 = allow
-            else:
+            elif mode == "bf16x3":
                 pk, pv = ple.SplitPlanes(w.w_key), ple.SplitPlanes(w.w_value)
                 gemm_ms = timed(lambda: ple.gemm_x3(emb, pk, b_n2=pv), steps)
+            else:
+                pk, pv = ple.SplitPlanes(w.w_key, three=True), ple.SplitPlanes(w.w_value, three=True)
+                gemm_ms = timed(lambda: ple.gemm_x6(emb, pk, b_n2=pv), steps)
         # forward + backward to emb (the descent's use: the weights stay fixed)
         fb = lambda: torch.autograd.grad(ple.ple_forward(emb_v, hidden, w, hist, HP, gemm=mode)[0], emb_v, d_out)
         fb()
@@ -935,11 +938,34 @@ def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
         if mode == "fp32":
             res[mode]["hipblaslt_gemm_us"] = lib_ms * 1e3
             res[mode]["hipblaslt_gemm_tflops"] = flops / (lib_ms * 1e-3) / 1e12
+    # each GEMM's largest error against the float64 products, relative to
+    # |emb| |W|^T (the scale of an fp32 sum's rounding), key and value together
+    with torch.no_grad():
+        e64 = emb.double()
+        refs = [(e64 @ x.double().T, e64.abs() @ x.double().abs().T) for x in (w.w_key, w.w_value)]
+
+        def err(outs) -> float:
+            return max(float(((o.double() - r).abs() / (bd + 1e-30)).max()) for o, (r, bd) in zip(outs, refs))
+
+        allow = torch.backends.cuda.matmul.allow_tf32
+        torch.backends.cuda.matmul.allow_tf32 = False
+        errs = {"fp32": err(ple.gemm_f32(emb, w.w_key, b_n2=w.w_value)),
+                "hipblaslt": err((emb @ w.w_key.T, emb @ w.w_value.T)),
+                "bf16x3": err(ple.gemm_x3(emb, w.w_key, b_n2=w.w_value)),
+                "bf16x6": err(ple.gemm_x6(emb, w.w_key, b_n2=w.w_value))}
+        torch.backends.cuda.matmul.allow_tf32 = allow
+        del refs, e64
+    res["fp32"]["gemm_err_vs_fp64"] = errs["fp32"]
+    res["fp32"]["hipblaslt_gemm_err_vs_fp64"] = errs["hipblaslt"]
+    res["bf16x3"]["gemm_err_vs_fp64"] = errs["bf16x3"]
+    res["bf16x6"]["gemm_err_vs_fp64"] = errs["bf16x6"]
     out = {"workload": "ple_forward: T 2048, hc 4, n_embd 2560, 4 taps, dilation 3, fp32 activations; key/value "
                        "GEMMs (one launch) either fp32 (eg_gemm_f32 on the fp32 matrix cores; the reference's "
-                       "arithmetic; hipBLASLt's time for the same products beside it) or bf16x3 (eg_gemm_bf16x3 "
-                       "on the bf16 matrix cores, 16 mantissa bits per operand); gate/norm and conv in HIP",
-           **res["fp32"], "bf16x3": res["bf16x3"], "fp32_mfma_peak_tflops": 157.3,
+                       "arithmetic; hipBLASLt's time for the same products beside it), bf16x3 (eg_gemm_bf16x3 "
+                       "on the bf16 matrix cores, 16 mantissa bits per operand) or bf16x6 (eg_gemm_bf16x6: three "
+                       "bf16 planes an operand, six products, fp32 accuracy); gate/norm and conv in HIP; "
+                       "gemm_err_vs_fp64: the largest |C - C64| / (|emb| |W|^T)",
+           **res["fp32"], "bf16x3": res["bf16x3"], "bf16x6": res["bf16x6"], "fp32_mfma_peak_tflops": 157.3,
            "bf16_mfma_peak_tflops": 2500.0}
     if cpu_s > 0:
         from oracle import ple as OP
@@ -1171,6 +1197,11 @@ def main() -> None:
         log(f"ple_forward with bf16x3 GEMMs: {x3['us_per_step']:.0f} us/step; GEMMs {x3['gemm_us']:.0f} us "
             f"({x3['gemm_tflops']:.1f} TFLOP/s fp32-equivalent); forward + backward to emb "
             f"{x3['us_forward_backward_to_emb']:.0f} us")
+        x6 = pl["bf16x6"]
+        log(f"ple_forward with bf16x6 GEMMs: {x6['us_per_step']:.0f} us/step; GEMMs {x6['gemm_us']:.0f} us; "
+            f"forward + backward to emb {x6['us_forward_backward_to_emb']:.0f} us; GEMM error / (|A||B|): fp32 "
+            f"{pl['gemm_err_vs_fp64']:.2e}, hipBLASLt {pl['hipblaslt_gemm_err_vs_fp64']:.2e}, bf16x3 "
+            f"{x3['gemm_err_vs_fp64']:.2e}, bf16x6 {x6['gemm_err_vs_fp64']:.2e}")
 
     if not args.no_cpu:
         calls[0]()  # outs[0] = the step on token batch 0 and residual set 0, which the CPU repeats

@@ -161,6 +161,10 @@ SIGNATURES = {
                                  c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_void_p]),
     "eg_gemm_f32": (c_int32, [POINTER(EgGemmF32Operands), c_int32, c_int64, c_int64, c_int64, c_void_p, c_int64,
                               c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_void_p]),
+    "eg_split_bf16x6": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "eg_gemm_bf16x6": (c_int32, [POINTER(EgGemmOperands), POINTER(EgGemmOperands), c_int32, c_int64, c_int64,
+                                 c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64,
+                                 c_void_p]),
     "eg_forward_decode": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,
                                     c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eg_forward_timed": (c_int32, [c_int32, POINTER(EgHashSpec), POINTER(EgTable), POINTER(EgOverlay), c_void_p,

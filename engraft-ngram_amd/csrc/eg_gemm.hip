@@ -137,10 +137,12 @@ __device__ inline void split4(const float4 v, bf16x4& hi, bf16x4& lo) {
 
 // x [rows, cols] (row stride ld) -> hi, lo [rows, kp] with kp = cols rounded up
 // to 32 and the padding zero; blockIdx.y walks rows, each thread 4 values.
-template <bool VEC>
+// With a third plane lo2 (bf16x6's split): hi, mid = lo as above, and
+// lo2 = rne(x - hi - lo) (both differences exact in fp32).
+template <bool VEC, bool THREE>
 __global__ __launch_bounds__(256) void split_kernel(const float* __restrict__ x, int64_t rows, int64_t cols,
                                                     int64_t ld, int64_t kp, __bf16* __restrict__ hi,
-                                                    __bf16* __restrict__ lo) {
+                                                    __bf16* __restrict__ lo, __bf16* __restrict__ lo2) {
   const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (c >= kp) return;
   for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
@@ -158,6 +160,14 @@ __global__ __launch_bounds__(256) void split_kernel(const float* __restrict__ x,
     split4(v, h, l);
     *(bf16x4*)(hi + r * kp + c) = h;
     *(bf16x4*)(lo + r * kp + c) = l;
+    if constexpr (THREE) {
+      bf16x4 l2;
+      l2[0] = (__bf16)((v.x - (float)h[0]) - (float)l[0]);
+      l2[1] = (__bf16)((v.y - (float)h[1]) - (float)l[1]);
+      l2[2] = (__bf16)((v.z - (float)h[2]) - (float)l[2]);
+      l2[3] = (__bf16)((v.w - (float)h[3]) - (float)l[3]);
+      *(bf16x4*)(lo2 + r * kp + c) = l2;
+    }
   }
 }
 
@@ -305,6 +315,20 @@ __device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) 
     __VA_ARGS__;                                                                                        \
   }
 
+// The products a bf16 GEMM launch adds, over the hi and lo planes it loads
+// (a pass: A's lo or hi plane times B's lo or hi plane), the small ones first:
+//   PR 3 (bf16x3): lo*hi, hi*lo, hi*hi;
+//   PR 4: lo*lo, lo*hi, hi*lo, hi*hi (bf16x6's first launch, on hi and mid planes);
+//   PR 2: lo*hi, hi*lo (bf16x6's second launch, on hi and lo planes).
+template <int PR>
+__device__ constexpr bool pass_alo(int pass) {
+  return PR == 4 ? pass < 2 : pass == 0;
+}
+template <int PR>
+__device__ constexpr bool pass_blo(int pass) {
+  return PR == 4 ? (pass == 0 || pass == 2) : pass == 1;
+}
+
 // gemm_x3: one tile's (or piece's) K steps [w.kv0, w.kv1) and its store.
 // BM x BN tile of WMW x WNW wavefronts, each 32 TI x 32 TJ outputs (TI x TJ
 // MFMA tiles).  A stage holds the four bf16 planes ah, al (BM rows) and bh, bl
@@ -316,8 +340,9 @@ __device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) 
 // conflicts).  A direct-to-LDS load fills 16
 // rows of a plane (1 KB), so load q of a stage lands at 16 q rows from the
 // stage's start.
-template <int BM, int BN, int WMW, int WNW>
+template <int BM, int BN, int WMW, int WNW, int PR>
 __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds) {
+  constexpr int NP = PR;  // passes (products) a half step
   constexpr int NW = WMW * WNW, TI = BM / WMW / 32, TJ = BN / WNW / 32;
   constexpr int LA = BM / 16, LB = BN / 16;         // loads per A / B plane
   constexpr int LPW = 2 * (LA + LB) / NW;           // loads per wavefront per stage
@@ -408,15 +433,16 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
         bl[f][j] = *(const bf16x8*)(st + (2 * BM + BN) * kBK + bo);
       }
     };
-    // the products of set f: lo*hi, hi*lo, hi*hi (the small ones first), as
-    // three passes over the TI x TJ tiles
+    // the products of set f, the small ones first, a pass over the TI x TJ
+    // tiles each (pass_alo / pass_blo: which planes a pass multiplies)
     auto mfma = [&](int f, int pass) {
 #pragma unroll
       for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pass == 0 ? al[f][i] : ah[f][i],
-                                                               pass == 1 ? bl[f][j] : bh[f][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pass_alo<PR>(pass) ? al[f][i] : ah[f][i],
+                                                               pass_blo<PR>(pass) ? bl[f][j] : bh[f][j], acc[i][j],
+                                                               0, 0, 0);
     };
     // Software pipeline, one barrier a step.  The fragments of one half step
     // are read during the other half step's MFMAs, after its first pass: the
@@ -443,8 +469,8 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
       __builtin_amdgcn_sched_barrier(0);  // the reads stay between the passes
       read(1, kt, 1);
       __builtin_amdgcn_sched_barrier(0);
-      mfma(0, 1);
-      mfma(0, 2);
+#pragma unroll
+      for (int pass = 1; pass < NP; ++pass) mfma(0, pass);
       __builtin_amdgcn_sched_barrier(0);
       // this wavefront's part of step kt + 1 is in LDS and its reads of step kt
       // are in registers; after the barrier, every wavefront's are
@@ -460,10 +486,11 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
         // 2 % longer a step)
         const bool ld = kv + 2 < hi;
 #pragma unroll
-        for (int t = 0; t < 3 * TI * TJ; ++t) {
+        for (int t = 0; t < NP * TI * TJ; ++t) {
           const int pass = t / (TI * TJ), i = (t % (TI * TJ)) / TJ, j = t % TJ;
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pass == 0 ? al[1][i] : ah[1][i],
-                                                               pass == 1 ? bl[1][j] : bh[1][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pass_alo<PR>(pass) ? al[1][i] : ah[1][i],
+                                                               pass_blo<PR>(pass) ? bl[1][j] : bh[1][j], acc[i][j],
+                                                               0, 0, 0);
           if (t == TI * TJ - 1) {
             __builtin_amdgcn_sched_barrier(0);
             read(0, kt + 1, 0);
@@ -479,20 +506,19 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
     }
     mfma(0, 0);
     read(1, hi - 1 - seg0, 1);
-    mfma(0, 1);
-    mfma(0, 2);
-    mfma(1, 0);
-    mfma(1, 1);
-    mfma(1, 2);
+#pragma unroll
+    for (int pass = 1; pass < NP; ++pass) mfma(0, pass);
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass) mfma(1, pass);
     __builtin_amdgcn_s_barrier();  // the ring is refilled by the next segment or tile
   }
   store_acc<BM, BN, TI, TJ>(p, w, acc, wave / WNW, wave % WNW, lane);
 }
 
-template <int BM, int BN, int WMW, int WNW>
+template <int BM, int BN, int WMW, int WNW, int PR>
 __global__ __launch_bounds__(WMW * WNW * 64) void gemm_x3_kernel(const GemmArgs args) {
   extern __shared__ __attribute__((aligned(16))) __bf16 lds[];
-  EG_GEMM_WALK(x3_tile<BM, BN, WMW, WNW>(args, w, lds))
+  EG_GEMM_WALK(x3_tile<BM, BN, WMW, WNW, PR>(args, w, lds))
 }
 
 // One MFMA takes one A and one B value per lane (lane l: row / column l % 32,
@@ -899,23 +925,46 @@ int launch_gemm(const Shape& sh, void (*kernel)(const Args), const char* name, A
 
 extern "C" {
 
-int eg_split_bf16(const float* x, int64_t rows, int64_t cols, int64_t ld, void* hi, void* lo, void* stream) {
-  using namespace eg;
+}  // extern "C"
+
+namespace eg {
+namespace {
+// eg_split_bf16 (lo2 == nullptr) and eg_split_bf16x6.
+int split_planes(const float* x, int64_t rows, int64_t cols, int64_t ld, void* hi, void* lo, void* lo2,
+                 void* stream) {
   EG_CHECK_ARG(rows >= 0 && cols >= 0 && ld >= cols, "rows=%lld cols=%lld ld=%lld", (long long)rows, (long long)cols,
                (long long)ld);
   const int64_t kp = (cols + 31) / 32 * 32;
   if (rows == 0 || kp == 0) return 0;
   EG_CHECK_ARG(x != nullptr && hi != nullptr && lo != nullptr, "NULL argument");
-  EG_CHECK_ARG(((uintptr_t)hi & 15) == 0 && ((uintptr_t)lo & 15) == 0, "hi / lo must be 16-byte aligned");
+  EG_CHECK_ARG(((uintptr_t)hi & 15) == 0 && ((uintptr_t)lo & 15) == 0 && ((uintptr_t)lo2 & 15) == 0,
+               "the planes must be 16-byte aligned");
   const dim3 grid((unsigned)((kp / 4 + 255) / 256), (unsigned)(rows < 65535 ? rows : 65535));
   const bool vec = ld % 4 == 0 && ((uintptr_t)x & 15) == 0;
-  if (vec)
-    hipLaunchKernelGGL(split_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, x, rows, cols, ld, kp,
-                       (__bf16*)hi, (__bf16*)lo);
-  else
-    hipLaunchKernelGGL(split_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, x, rows, cols, ld, kp,
-                       (__bf16*)hi, (__bf16*)lo);
+  hipStream_t st = (hipStream_t)stream;
+  __bf16 *h = (__bf16*)hi, *l = (__bf16*)lo, *l2 = (__bf16*)lo2;
+  if (lo2 != nullptr) {
+    if (vec) hipLaunchKernelGGL((split_kernel<true, true>), grid, dim3(256), 0, st, x, rows, cols, ld, kp, h, l, l2);
+    else hipLaunchKernelGGL((split_kernel<false, true>), grid, dim3(256), 0, st, x, rows, cols, ld, kp, h, l, l2);
+  } else {
+    if (vec) hipLaunchKernelGGL((split_kernel<true, false>), grid, dim3(256), 0, st, x, rows, cols, ld, kp, h, l, l2);
+    else hipLaunchKernelGGL((split_kernel<false, false>), grid, dim3(256), 0, st, x, rows, cols, ld, kp, h, l, l2);
+  }
   return launch_status("split_kernel");
+}
+}  // namespace
+}  // namespace eg
+
+extern "C" {
+
+int eg_split_bf16(const float* x, int64_t rows, int64_t cols, int64_t ld, void* hi, void* lo, void* stream) {
+  return eg::split_planes(x, rows, cols, ld, hi, lo, nullptr, stream);
+}
+
+int eg_split_bf16x6(const float* x, int64_t rows, int64_t cols, int64_t ld, void* hi, void* mid, void* lo,
+                    void* stream) {
+  EG_CHECK_ARG(lo != nullptr, "NULL argument");
+  return eg::split_planes(x, rows, cols, ld, hi, mid, lo, stream);
 }
 
 int64_t eg_gemm_workspace_size(int64_t m, int64_t n, int64_t n2, int64_t k, int32_t k_slices) {
@@ -926,12 +975,13 @@ int64_t eg_gemm_f32_workspace_size(int64_t m, int64_t n, int64_t n2, int64_t k, 
   return eg::workspace_size(eg::kF32Shape, m, n, n2, k, k_slices);
 }
 
-int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,
-                   int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate, int32_t k_slices, void* workspace,
-                   int64_t workspace_bytes, void* stream) {
-  using namespace eg;
+}  // extern "C"
+
+namespace eg {
+namespace {
+// The kernel arguments of eg_gemm_bf16x3 / eg_gemm_bf16x6 operands (the planes checked).
+int bf16_operands(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, GemmArgs& g) {
   EG_CHECK_ARG(ops != nullptr && n_seg >= 0 && n_seg <= 2, "n_seg=%d", n_seg);
-  GemmArgs g{};
   for (int s = 0; s < n_seg; ++s) {
     const eg_gemm_operands& o = ops[s];
     EG_CHECK_ARG(o.k >= 0 && o.k % 32 == 0, "segment %d: k must be a multiple of 32 (k=%lld)", s, (long long)o.k);
@@ -962,9 +1012,45 @@ int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_
     sg.ktiles = o.k / 32;
     ++g.n_seg;
   }
-  return launch_gemm<kX3BM, kX3BN>(kX3Shape, gemm_x3_kernel<kX3BM, kX3BN, kX3WM, kX3WN>, "gemm_x3_kernel", g, m, n,
+  return EG_OK;
+}
+}  // namespace
+}  // namespace eg
+
+extern "C" {
+
+int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,
+                   int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate, int32_t k_slices, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
+  using namespace eg;
+  GemmArgs g{};
+  const int rc = bf16_operands(ops, n_seg, m, n, n2, g);
+  if (rc != EG_OK) return rc;
+  return launch_gemm<kX3BM, kX3BN>(kX3Shape, gemm_x3_kernel<kX3BM, kX3BN, kX3WM, kX3WN, 3>, "gemm_x3_kernel", g, m, n,
                                    n2, c, ldc, c2, ldc2, accumulate, k_slices, workspace, workspace_bytes,
                                    stream);
+}
+
+int eg_gemm_bf16x6(const eg_gemm_operands* hi_mid, const eg_gemm_operands* hi_lo, int32_t n_seg, int64_t m,
+                   int64_t n, int64_t n2, float* c, int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate,
+                   int32_t k_slices, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace eg;
+  GemmArgs g1{}, g2{};
+  int rc = bf16_operands(hi_mid, n_seg, m, n, n2, g1);
+  if (rc != EG_OK) return rc;
+  rc = bf16_operands(hi_lo, n_seg, m, n, n2, g2);
+  if (rc != EG_OK) return rc;
+  bool same = g1.n_seg == g2.n_seg;
+  for (int s = 0; same && s < g1.n_seg; ++s) same = g1.seg[s].ktiles == g2.seg[s].ktiles;
+  EG_CHECK_ARG(same, "hi_mid and hi_lo must describe the same K segments");
+  // lo*lo + lo*hi + hi*lo + hi*hi over the hi and mid planes, then lo*hi + hi*lo
+  // over the hi and lo planes, added to it
+  rc = launch_gemm<kX3BM, kX3BN>(kX3Shape, gemm_x3_kernel<kX3BM, kX3BN, kX3WM, kX3WN, 4>, "gemm_x3_kernel<4>", g1,
+                                 m, n, n2, c, ldc, c2, ldc2, accumulate, k_slices, workspace, workspace_bytes,
+                                 stream);
+  if (rc != EG_OK) return rc;
+  return launch_gemm<kX3BM, kX3BN>(kX3Shape, gemm_x3_kernel<kX3BM, kX3BN, kX3WM, kX3WN, 2>, "gemm_x3_kernel<2>", g2,
+                                   m, n, n2, c, ldc, c2, ldc2, 1, k_slices, workspace, workspace_bytes, stream);
 }
 
 int eg_gemm_f32(const eg_gemm_f32_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,

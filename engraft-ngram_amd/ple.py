@@ -7,7 +7,9 @@ Forward:
   ``gemm_f32`` kernel on the fp32 matrix cores (fp32 arithmetic, as the
   reference's torch matmuls), or with ``gemm="bf16x3"`` of the ``gemm_x3``
   kernel on the bf16 matrix cores (operands split into bf16 hi + lo, three
-  products accumulated in fp32: 16 mantissa bits per operand);
+  products accumulated in fp32: 16 mantissa bits per operand), or with
+  ``gemm="bf16x6"`` two launches of it over three planes an operand
+  (``gemm_x6``: six products, fp32 accuracy);
 * ``eg_ple_gate``: per position and stream, the RMS norms of key and hidden,
   the score ``s``, the gate, ``gated = value * gate`` and its RMS norm;
 * ``eg_ple_conv``: the dilated causal depthwise convolution over
@@ -16,8 +18,8 @@ Forward:
 The result -- the output and the new history -- is differentiable in emb,
 hidden, the history and the weights.  The backward runs
 ``eg_ple_conv_backward`` and ``eg_ple_gate_backward`` on the forward's saved
-intermediates, then the projections' backward (one ``gemm_f32`` or
-``gemm_x3`` call over two K segments); when weights need gradients, also the
+intermediates, then the projections' backward (one ``gemm_f32``, ``gemm_x3``
+or ``gemm_x6`` call over two K segments); when weights need gradients, also the
 two weight GEMMs (``gemm_f32`` with the positions as K) and
 ``eg_ple_weight_grads`` for the norm and convolution weights.  The
 convolution takes 1..8 taps (the reference's blocks have 4; more raise
@@ -134,9 +136,11 @@ _WT = _TransposedCache()
 
 class SplitPlanes:
     """The bf16 hi / lo planes of an fp32 matrix ``[rows, cols]`` (``eg_split_bf16``),
-    each ``[rows, kp]`` with ``kp`` = cols rounded up to 32, zero-padded."""
+    each ``[rows, kp]`` with ``kp`` = cols rounded up to 32, zero-padded.  With
+    ``three=True`` (``eg_split_bf16x6``, the planes of :func:`gemm_x6`) ``lo``
+    is the second plane rne(x - hi) and ``lo2`` the third, rne(x - hi - lo)."""
 
-    def __init__(self, x: torch.Tensor):
+    def __init__(self, x: torch.Tensor, three: bool = False):
         if x.dim() != 2:
             raise ValueError("SplitPlanes: a 2-D matrix expected")
         x = x if x.dtype == torch.float32 else x.float()
@@ -146,8 +150,13 @@ class SplitPlanes:
         self.rows, self.cols, self.kp = rows, cols, (cols + 31) // 32 * 32
         self.hi = torch.empty((rows, self.kp), dtype=torch.bfloat16, device=x.device)
         self.lo = torch.empty_like(self.hi)
-        _lib.call("eg_split_bf16", _lib.ptr(x), rows, cols, max(x.stride(0), cols), _lib.ptr(self.hi),
-                  _lib.ptr(self.lo), _lib.stream_ptr(x.device))
+        self.lo2 = torch.empty_like(self.hi) if three else None
+        if three:
+            _lib.call("eg_split_bf16x6", _lib.ptr(x), rows, cols, max(x.stride(0), cols), _lib.ptr(self.hi),
+                      _lib.ptr(self.lo), _lib.ptr(self.lo2), _lib.stream_ptr(x.device))
+        else:
+            _lib.call("eg_split_bf16", _lib.ptr(x), rows, cols, max(x.stride(0), cols), _lib.ptr(self.hi),
+                      _lib.ptr(self.lo), _lib.stream_ptr(x.device))
 
 
 def _empty_planes(rows: int, cols: int, device) -> "SplitPlanes":
@@ -168,12 +177,12 @@ class _PlaneCache:
         self._entries: list = []
         self._size = size
 
-    def get(self, w: torch.Tensor) -> SplitPlanes:
+    def get(self, w: torch.Tensor, three: bool = False) -> SplitPlanes:
         import weakref
         for ref, version, planes in self._entries:
-            if ref() is w and version == w._version:
+            if ref() is w and version == w._version and (planes.lo2 is not None) == three:
                 return planes
-        planes = SplitPlanes(w)
+        planes = SplitPlanes(w, three=three)
         self._entries = [e for e in self._entries if e[0]() is not None][-(self._size - 1):]
         self._entries.append((weakref.ref(w), w._version, planes))
         return planes
@@ -182,10 +191,12 @@ class _PlaneCache:
 _PLANES = _PlaneCache()
 
 
-def _planes(x, cached: bool) -> SplitPlanes:
+def _planes(x, cached: bool, three: bool = False) -> SplitPlanes:
     if isinstance(x, SplitPlanes):
+        if three and x.lo2 is None:
+            raise ValueError("gemm_x6 needs three-plane SplitPlanes (SplitPlanes(x, three=True))")
         return x
-    return _PLANES.get(x) if cached else SplitPlanes(x)
+    return _PLANES.get(x, three) if cached else SplitPlanes(x, three=three)
 
 
 def _gemm_workspace(m: int, n: int, n2: int, k: int, k_slices: int | None, dev, size_fn: str):
@@ -253,6 +264,56 @@ def gemm_x3(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate:
     out2 = _out(out2, m, n2, "out2") if n2 else None
     slices, ws, ws_bytes = _gemm_workspace(m, n, n2, 32 * k_tiles, k_slices, dev, "eg_gemm_workspace_size")
     _lib.call("eg_gemm_bf16x3", ops, len(segs), m, n, n2, _lib.ptr(out), max(out.stride(0), n),
+              _lib.ptr(out2), max(out2.stride(0), n2) if n2 else 0, int(accumulate), slices, _lib.ptr(ws),
+              ws_bytes, _lib.stream_ptr(dev))
+    return (out, out2) if n2 else out
+
+
+def gemm_x6(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate: bool = False,
+            cache_b: bool = False, b_n2=None, b2_n2=None, out2: torch.Tensor | None = None,
+            k_slices: int | None = None):
+    """:func:`gemm_x3`'s GEMM with fp32 accuracy on the bf16 matrix cores
+    (``eg_gemm_bf16x6``): every operand split into three bf16 planes, hi + mid
+    + lo keeping its 24 mantissa bits, and the six plane products above
+    2^-23 of |a||b| accumulated in fp32.  Arguments, operands (fp32 tensors or
+    three-plane ``SplitPlanes``) and result as :func:`gemm_x3`."""
+    segs = [(_planes(a, False, True), _planes(b, cache_b, True),
+             None if b_n2 is None else _planes(b_n2, cache_b, True))]
+    if a2 is not None:
+        segs.append((_planes(a2, False, True), _planes(b2, cache_b, True),
+                     None if b2_n2 is None else _planes(b2_n2, cache_b, True)))
+    m, n = segs[0][0].rows, segs[0][1].rows
+    n2 = 0 if segs[0][2] is None else segs[0][2].rows
+    hm, hl = (_lib.EgGemmOperands * 2)(), (_lib.EgGemmOperands * 2)()
+    k_tiles = 0
+    for i, (pa, pb, pb2) in enumerate(segs):
+        if pa.rows != m or pb.rows != n or pb.cols != pa.cols:
+            raise ValueError(f"gemm_x6: segment {i}: a [m, k] and b [n, k] expected, got [{pa.rows}, {pa.cols}] "
+                             f"and [{pb.rows}, {pb.cols}]")
+        if (pb2 is None) != (n2 == 0) or (pb2 is not None and (pb2.rows != n2 or pb2.cols != pa.cols)):
+            raise ValueError(f"gemm_x6: segment {i}: the second column group needs b [n2, k] in every segment")
+        for o, second in ((hm[i], "lo"), (hl[i], "lo2")):
+            o.a_hi, o.a_lo, o.lda = _lib.ptr(pa.hi), _lib.ptr(getattr(pa, second)), pa.kp
+            o.b_hi, o.b_lo, o.ldb = _lib.ptr(pb.hi), _lib.ptr(getattr(pb, second)), pb.kp
+            if pb2 is not None:
+                o.b2_hi, o.b2_lo, o.ldb2 = _lib.ptr(pb2.hi), _lib.ptr(getattr(pb2, second)), pb2.kp
+            o.k = pa.kp
+        k_tiles += pa.kp // 32
+    dev = segs[0][0].hi.device
+
+    def _out(t, rows, cols, name):
+        if t is None:
+            if accumulate:
+                raise ValueError(f"gemm_x6: accumulate needs {name}")
+            return torch.empty((rows, cols), dtype=torch.float32, device=dev)
+        if t.dtype != torch.float32 or t.shape != (rows, cols) or t.stride(1) != 1:
+            raise ValueError(f"gemm_x6: {name} must be fp32 [{rows}, {cols}] with unit column stride")
+        return t
+
+    out = _out(out, m, n, "out")
+    out2 = _out(out2, m, n2, "out2") if n2 else None
+    slices, ws, ws_bytes = _gemm_workspace(m, n, n2, 32 * k_tiles, k_slices, dev, "eg_gemm_workspace_size")
+    _lib.call("eg_gemm_bf16x6", hm, hl, len(segs), m, n, n2, _lib.ptr(out), max(out.stride(0), n),
               _lib.ptr(out2), max(out2.stride(0), n2) if n2 else 0, int(accumulate), slices, _lib.ptr(ws),
               ws_bytes, _lib.stream_ptr(dev))
     return (out, out2) if n2 else out
@@ -336,6 +397,16 @@ def _weight_grad(d_y: torch.Tensor, x: torch.Tensor, w: torch.Tensor) -> torch.T
     return gemm_f32(d_y.T, x.T)
 
 
+def _projection_backward(gemm: str, flat: list) -> torch.Tensor:
+    """``d_emb = sum d_i w_i`` over the (d_i, w_i^T) pairs in ``flat``, on the
+    forward's GEMM."""
+    if gemm == "bf16x3":
+        return gemm_x3(*flat, cache_b=True)
+    if gemm == "bf16x6":
+        return gemm_x6(*flat, cache_b=True)
+    return gemm_f32(*flat)
+
+
 def _native_backward_ok(hc: int, n: int, taps: int, dil: int, weights: bool = False) -> bool:
     """The HIP backward's built limits (eg_ple_gate_backward, eg_ple_conv_backward,
     and with ``weights`` eg_ple_weight_grads)."""
@@ -359,6 +430,8 @@ class _PleFn(torch.autograd.Function):
         wv32 = w_value.to(**f32)
         if gemm == "bf16x3":
             key, value = gemm_x3(SplitPlanes(emb32), wk32, cache_b=True, b_n2=wv32)
+        elif gemm == "bf16x6":
+            key, value = gemm_x6(SplitPlanes(emb32, three=True), wk32, cache_b=True, b_n2=wv32)
         else:
             key, value = gemm_f32(emb32, wk32, b_n2=wv32)
         hidden32 = hidden.to(**f32).contiguous()
@@ -476,7 +549,7 @@ class _PleFn(torch.autograd.Function):
             parts = [(d, _WT.get(w)) for d, w in ((d_key, wk32), (d_value, wv32)) if d is not None]
             if parts:  # none: both factors detached, emb has no path to the output
                 flat = [x for part in parts for x in part]
-                d_emb = (gemm_x3(*flat, cache_b=True) if ctx.gemm == "bf16x3" else gemm_f32(*flat)).to(emb_dt)
+                d_emb = _projection_backward(ctx.gemm, flat).to(emb_dt)
         d_hist_in = d_full[:h0].reshape(h0, hc, n).to(hist_dt) if need_hist else None
         return (d_emb, d_hidden.to(hidden_dt) if d_hidden is not None else None, None, None, None, None, None, None,
                 d_hist_in, None, None, None, None, None)
@@ -513,7 +586,7 @@ class _PleFn(torch.autograd.Function):
             parts = [(d, _WT.get(w)) for d, w in ((d_key, wk32), (d_value, wv32)) if d is not None]
             if parts:  # none: both factors detached, emb has no path to the output
                 flat = [x for part in parts for x in part]
-                d_emb = (gemm_x3(*flat, cache_b=True) if ctx.gemm == "bf16x3" else gemm_f32(*flat)).to(emb_dt)
+                d_emb = _projection_backward(ctx.gemm, flat).to(emb_dt)
         wdt = ctx.w_dtypes
         # the projection weights' gradients d_key^T emb and d_value^T emb on eg_gemm_f32
         # (K = the positions); a weight the detached factor cuts off keeps None
@@ -549,10 +622,11 @@ def ple_forward(emb: torch.Tensor, hidden: torch.Tensor, w: PleWeights, hist: to
     ``[rows, hc, n_embd]`` (at most ``(K-1)*ple_ngram_size`` rows, empty at a
     sequence start); all on the device.  ``gemm`` picks the projections' GEMM:
     ``"fp32"`` (the reference's arithmetic: ``gemm_f32`` on the fp32 matrix
-    cores) or ``"bf16x3"`` (``gemm_x3`` on the bf16 matrix cores: 16 mantissa
-    bits per operand, about 1e-5 relative per projection, 2.5x faster)."""
-    if gemm not in ("fp32", "bf16x3"):
-        raise ValueError(f"gemm must be 'fp32' or 'bf16x3', got {gemm!r}")
+    cores), ``"bf16x3"`` (``gemm_x3`` on the bf16 matrix cores: 16 mantissa
+    bits per operand, about 1e-5 relative per projection, 2.5x faster) or
+    ``"bf16x6"`` (``gemm_x6``: the bf16 matrix cores with fp32 accuracy)."""
+    if gemm not in ("fp32", "bf16x3", "bf16x6"):
+        raise ValueError(f"gemm must be 'fp32', 'bf16x3' or 'bf16x6', got {gemm!r}")
     hc = hparams.hc_mult
     n = hparams.n_embd
     eps = float(hparams.f_norm_rms_eps)

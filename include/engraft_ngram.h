@@ -35,7 +35,8 @@
  *   eg_ple_gate, eg_ple_conv  ple_forward after its two projections
  *   (+ _backward)    and the autograd of it          engraft/replica/layers.py:565-626
  *   eg_ple_rms, eg_ple_conv's other modes  PleReplica engraft/lens.py:221-385
- *   eg_split_bf16, eg_gemm_bf16x3, eg_gemm_f32 (+ _workspace_size)
+ *   eg_split_bf16, eg_gemm_bf16x3, eg_gemm_f32 (+ _workspace_size),
+ *   eg_split_bf16x6, eg_gemm_bf16x6
  *                    ple_forward's projections and their backward
  *                                                    engraft/replica/layers.py:594-606
  */
@@ -541,6 +542,28 @@ int64_t eg_gemm_workspace_size(int64_t m, int64_t n, int64_t n2, int64_t k, int3
 int eg_gemm_bf16x3(const eg_gemm_operands* ops, int32_t n_seg, int64_t m, int64_t n, int64_t n2, float* c,
                    int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate, int32_t k_slices,
                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The three bf16 planes of an fp32 matrix for eg_gemm_bf16x6: hi = rne(x),
+ * mid = rne(x - hi), lo = rne(x - hi - mid) (both differences exact in fp32),
+ * each bf16 [rows, kp] as eg_split_bf16's.  hi + mid + lo keeps x's 24
+ * mantissa bits.  No counterpart in the reference (part of its fp32 matmuls). */
+int eg_split_bf16x6(const float* x, int64_t rows, int64_t cols, int64_t ld, void* hi, void* mid, void* lo,
+                    void* stream);
+
+/* eg_gemm_bf16x3's GEMM (segments, column groups, K slices, the workspace of
+ * eg_gemm_workspace_size) with every operand split into three planes
+ * (eg_split_bf16x6) and six of the nine plane products accumulated in fp32:
+ * mid*mid + mid*hi + hi*mid + hi*hi over hi_mid (each segment's planes given
+ * as hi in the *_hi and mid in the *_lo fields), then lo*hi + hi*lo over
+ * hi_lo (hi in *_hi, lo in *_lo) added to it; the same K segments in both.
+ * The dropped products (mid*lo, lo*mid, lo*lo) are below 2^-23 of |a||b|, so
+ * the result carries an fp32 matmul's error (the tests hold it to the fp32
+ * GEMM's bound against float64).  Two launches on the stream, the second
+ * adding to C / C2.  The same reference products as eg_gemm_bf16x3
+ * (engraft/replica/layers.py:594-606, torch fp32 matmuls). */
+int eg_gemm_bf16x6(const eg_gemm_operands* hi_mid, const eg_gemm_operands* hi_lo, int32_t n_seg, int64_t m,
+                   int64_t n, int64_t n2, float* c, int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate,
+                   int32_t k_slices, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* One K segment of eg_gemm_f32: A [m, k] and B [n, k] (and B2 [n2, k] for
  * the second column group, only read when n2 > 0), fp32, row-major. */
