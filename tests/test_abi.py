@@ -108,6 +108,19 @@ def test_host_side_argument_checks():
         ("taps", _lib.EG_ERR_ARG, lib.eg_ple_conv_backward, None, 0, 1, 4, 64, None, 9, 1, None, None, None, 0,
          None, None),
     ]
+    # bf16x6: the third plane, and the two plane sets' K segments checked against each other
+    hm, hl = (_lib.EgGemmOperands * 2)(), (_lib.EgGemmOperands * 2)()
+    for o, k in ((hm[0], 32), (hl[0], 64)):
+        o.a_hi = o.a_lo = o.b_hi = o.b_lo = 256
+        o.lda = o.ldb = 64
+        o.k = k
+    cases += [
+        ("NULL", _lib.EG_ERR_ARG, lib.eg_split_bf16x6, ctypes.c_void_p(256), 4, 32, 32, ctypes.c_void_p(256),
+         ctypes.c_void_p(256), None, None),
+        ("n_seg", _lib.EG_ERR_ARG, lib.eg_gemm_bf16x6, hm, hl, 3, 8, 8, 0, None, 8, None, 0, 0, 0, None, 0, None),
+        ("same K segments", _lib.EG_ERR_ARG, lib.eg_gemm_bf16x6, hm, hl, 1, 8, 8, 0, ctypes.c_void_p(256), 8, None,
+         0, 0, 0, None, 0, None),
+    ]
     for needle, code, fn, *args in cases:
         rc, msg = _rejects(fn, *args)
         assert rc == code, (fn.__name__, rc, msg)
