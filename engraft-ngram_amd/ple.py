@@ -388,12 +388,16 @@ def gemm_f32(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate
 WGRAD_MAX_TAPS = 8  # eg_ple_weight_grads' built tap counts (1..8)
 
 
-def _weight_grad(d_y: torch.Tensor, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+def _weight_grad(d_y: torch.Tensor, x: torch.Tensor, w: torch.Tensor, gemm: str = "fp32") -> torch.Tensor:
     """``d_y^T x`` (``[out, T]`` x ``[T, in]``), the gradient of ``w`` in
-    ``y = x w^T``, on eg_gemm_f32 with the positions as K (both operands
-    transposed into K-contiguous copies by the GEMM wrapper)."""
+    ``y = x w^T``, with the positions as K (both operands transposed into
+    K-contiguous copies): on eg_gemm_f32, or with ``gemm="bf16x6"`` on
+    eg_gemm_bf16x6 (the same fp32 accuracy; bf16x3's 16-bit operands are kept
+    to the projections)."""
     if d_y.shape[0] == 0:
         return torch.zeros_like(w)
+    if gemm == "bf16x6":
+        return gemm_x6(d_y.T, x.T)
     return gemm_f32(d_y.T, x.T)
 
 
@@ -590,8 +594,8 @@ class _PleFn(torch.autograd.Function):
         wdt = ctx.w_dtypes
         # the projection weights' gradients d_key^T emb and d_value^T emb on eg_gemm_f32
         # (K = the positions); a weight the detached factor cuts off keeps None
-        d_wk = _weight_grad(d_key, emb32, wk32).to(wdt[0]) if (need_wk and d_key is not None) else None
-        d_wv = _weight_grad(d_value, emb32, wv32).to(wdt[1]) if (need_wv and d_value is not None) else None
+        d_wk = _weight_grad(d_key, emb32, wk32, ctx.gemm).to(wdt[0]) if (need_wk and d_key is not None) else None
+        d_wv = _weight_grad(d_value, emb32, wv32, ctx.gemm).to(wdt[1]) if (need_wv and d_value is not None) else None
         if detach_gate:  # the gate's whole branch (key, its norm, the query norm) is detached
             need_nk = need_nq = False
         d_nk = d_nq = d_nc = d_cv = None

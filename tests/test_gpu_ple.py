@@ -197,7 +197,7 @@ def _grad_close(got, exp, tol, name):
 
 
 @pytest.mark.parametrize("gemm,dv,dg", [("fp32", False, False), ("bf16x3", False, False), ("fp32", True, False),
-                                        ("fp32", False, True), ("fp32", True, True)])
+                                        ("fp32", False, True), ("fp32", True, True), ("bf16x6", False, False)])
 def test_ple_weight_gradients_native(cuda, gemm, dv, dg):
     """Every weight's gradient (w_key, w_value, the three norms, the conv taps)
     together with emb's, hidden's and the history's, from the HIP backward
@@ -251,14 +251,15 @@ def test_ple_weight_gradients_native(cuda, gemm, dv, dg):
     # small |s| (150 positions reach |s| ~ 1.6e-3) amplifies the projections'
     # rounding: fp32 oracles land 2e-5 .. 2e-4 off float64 in the hidden,
     # w_key and key / query norm gradients, depending on the summation order
-    # alone.  bf16x3 (16-bit mantissas in the projections): 2e-3.
+    # alone.  bf16x3 (16-bit mantissas in the projections): 2e-3.  bf16x6
+    # (the projections and the weight GEMMs at fp32 accuracy): the fp32 bar.
     for name, exp in ref64.items():
         if exp is None:
             _grad_close(got[name], None, 0.0, name)
             continue
         scale = exp.abs().max().clamp_min(1e-300)
         spread = max(float((ref[name].double() - exp).abs().max() / scale) for ref in refs32)
-        tol = max(3 * spread, 1e-4) if gemm == "fp32" else 2e-3
+        tol = max(3 * spread, 1e-4) if gemm in ("fp32", "bf16x6") else 2e-3
         _grad_close(got[name], exp, tol, name)
 
 
