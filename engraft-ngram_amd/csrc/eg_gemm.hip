@@ -29,7 +29,9 @@
 // On the key projection (M 2048, N 10240, K 2560) 290 us against 319 us for
 // the 128 x 128 tiles of four wavefronts it replaces (two workgroups a CU,
 // the last round in K quarters), and the backward's d_emb 400 against 470 us;
-// sixteen wavefronts of 64 x 64 or eight of 64 x 128 ran 1-4 % slower, the
+// sixteen wavefronts of 64 x 64 or eight of 64 x 128 ran 1-4 % slower, four
+// of 128 x 128 (one a SIMD, the accumulators in the accumulation registers,
+// a third less LDS read a step) 8-13 % slower on the bf16x3 and bf16x6 shapes, the
 // same tile without the pipelining 2 % slower, with 2-way LDS bank conflicts
 // on the fragment reads 2-3 % slower; the reads interleaved one by one with
 // the MFMAs, or the wave priority raised over the MFMA passes, within 1 %.  Measured earlier on the 128 x 128 tile
