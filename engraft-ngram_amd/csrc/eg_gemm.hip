@@ -320,8 +320,9 @@ __device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xf | (7 << 4) 
 // The products a bf16 GEMM launch adds, over the hi and lo planes it loads
 // (a pass: A's lo or hi plane times B's lo or hi plane), the small ones first:
 //   PR 3 (bf16x3): lo*hi, hi*lo, hi*hi;
-//   PR 4: lo*lo, lo*hi, hi*lo, hi*hi (bf16x6's first launch, on hi and mid planes);
-//   PR 2: lo*hi, hi*lo (bf16x6's second launch, on hi and lo planes).
+//   PR 4: lo*lo, lo*hi, hi*lo, hi*hi (bf16x6 on the hi and mid planes);
+//   PR 2: lo*hi, hi*lo (bf16x6 on the hi and lo planes), passes 1 and 2 of PR 4,
+//   which is how gemm_x6_kernel runs them (pass set 4 with a run-time mask).
 template <int PR>
 __device__ constexpr bool pass_alo(int pass) {
   return PR == 4 ? pass < 2 : pass == 0;
@@ -342,9 +343,16 @@ __device__ constexpr bool pass_blo(int pass) {
 // conflicts).  A direct-to-LDS load fills 16
 // rows of a plane (1 KB), so load q of a stage lands at 16 q rows from the
 // stage's start.
-template <int BM, int BN, int WMW, int WNW, int PR>
+// A segment's pass set: PR passes of pass_alo / pass_blo; with RT, only the
+// passes whose bit is set in a uniform run-time mask run.
+template <int PR, bool RT>
+struct PassSet {
+  static constexpr int value = PR;
+  static constexpr bool masked = RT;
+};
+
+template <int BM, int BN, int WMW, int WNW, int PR0, int PR1>
 __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds) {
-  constexpr int NP = PR;  // passes (products) a half step
   constexpr int NW = WMW * WNW, TI = BM / WMW / 32, TJ = BN / WNW / 32;
   constexpr int LA = BM / 16, LB = BN / 16;         // loads per A / B plane
   constexpr int LPW = 2 * (LA + LB) / NW;           // loads per wavefront per stage
@@ -371,30 +379,28 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
   auto plane_of = [](int j) { return NW * j < LA ? 0 : NW * j < 2 * LA ? 1 : NW * j < 2 * LA + LB ? 2 : 3; };
   auto first_of = [](int pl) { return pl == 0 ? 0 : pl == 1 ? LA : pl == 2 ? 2 * LA : 2 * LA + LB; };
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
-  int64_t row_of[LPW];
-  int col_of[LPW];
-#pragma unroll
-  for (int j = 0; j < LPW; ++j) {
-    const int pl = plane_of(j), q = uwave + NW * j, row = 16 * (q - first_of(pl)) + (lane >> 2);
-    const bool is_a = pl < 2;
-    const int64_t gr = (is_a ? w.m0 : w.n0) + row, lim = is_a ? p.m : n_grp;
-    row_of[j] = gr < lim ? gr : lim - 1;
-    col_of[j] = swz(row, lane & 3) * 8;
-  }
 
-  // the block's K steps, segment by segment (the ring drains at a segment change)
-  for (int s = 0; s < args.n_seg; ++s) {
+  // the block's K steps of segment s, whose products are pass set PR
+  auto seg_steps = [&](const int s, auto pass_set, const uint32_t live) {
+    constexpr int PR = decltype(pass_set)::value, NP = PR;  // passes (products) a half step
+    auto on = [&](int pass) { return !decltype(pass_set)::masked || ((live >> pass) & 1u); };
     const int64_t seg0 = s ? p.kt0 : 0, seg1 = s ? p.kt_total : p.kt0;
     const int64_t lo = w.kv0 > seg0 ? w.kv0 : seg0, hi = w.kv1 < seg1 ? w.kv1 : seg1;
-    if (lo >= hi) continue;
+    if (lo >= hi) return;
     const GemmSeg& sg = args.seg[s];
     // a load's address: the plane's base (uniform) + a 32-bit byte offset
     // (the host keeps every plane under 4 GiB), one VGPR a load
+    // (from an opaque copy of the lane: computed here, not ahead of an earlier segment's loop and held)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
     uint32_t off[LPW];
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const int pl = plane_of(j);
-      off[j] = (uint32_t)((row_of[j] * (pl < 2 ? sg.lda : sg.ldb[grp]) + col_of[j]) * 2);
+      const int pl = plane_of(j), q = uwave + NW * j, row = 16 * (q - first_of(pl)) + (ln >> 2);
+      const bool is_a = pl < 2;
+      const int64_t gr = (is_a ? w.m0 : w.n0) + row, lim = is_a ? p.m : n_grp;
+      const int64_t rr = gr < lim ? gr : lim - 1;
+      off[j] = (uint32_t)((rr * (pl < 2 ? sg.lda : sg.ldb[grp]) + swz(row, ln & 3) * 8) * 2);
     }
     auto issue = [&](int64_t kt) {  // K step kt of the segment
       __bf16* st = lds + (kt & 1) * STAGE;
@@ -438,6 +444,7 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
     // the products of set f, the small ones first, a pass over the TI x TJ
     // tiles each (pass_alo / pass_blo: which planes a pass multiplies)
     auto mfma = [&](int f, int pass) {
+      if (!on(pass)) return;
 #pragma unroll
       for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -490,7 +497,8 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
 #pragma unroll
         for (int t = 0; t < NP * TI * TJ; ++t) {
           const int pass = t / (TI * TJ), i = (t % (TI * TJ)) / TJ, j = t % TJ;
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pass_alo<PR>(pass) ? al[1][i] : ah[1][i],
+          if (on(pass))
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pass_alo<PR>(pass) ? al[1][i] : ah[1][i],
                                                                pass_blo<PR>(pass) ? bl[1][j] : bh[1][j], acc[i][j],
                                                                0, 0, 0);
           if (t == TI * TJ - 1) {
@@ -513,6 +521,13 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
 #pragma unroll
     for (int pass = 0; pass < NP; ++pass) mfma(1, pass);
     __builtin_amdgcn_s_barrier();  // the ring is refilled by the next segment or tile
+  };
+  // segment by segment (the ring drains at a segment change)
+  for (int s = 0; s < args.n_seg; ++s) {
+    if constexpr (PR0 == PR1)
+      seg_steps(s, PassSet<PR0, false>{}, 0u);
+    else  // PR0 4, PR1 2: segment 1 runs passes 1 and 2 of the four (lo*hi, hi*lo)
+      seg_steps(s, PassSet<4, true>{}, s ? 0x6u : 0xfu);
   }
   store_acc<BM, BN, TI, TJ>(p, w, acc, wave / WNW, wave % WNW, lane);
 }
@@ -520,7 +535,16 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
 template <int BM, int BN, int WMW, int WNW, int PR>
 __global__ __launch_bounds__(WMW * WNW * 64) void gemm_x3_kernel(const GemmArgs args) {
   extern __shared__ __attribute__((aligned(16))) __bf16 lds[];
-  EG_GEMM_WALK(x3_tile<BM, BN, WMW, WNW, PR>(args, w, lds))
+  EG_GEMM_WALK(x3_tile<BM, BN, WMW, WNW, PR, PR>(args, w, lds))
+}
+
+// bf16x6 of one K segment in one launch: segment 0 is its hi and mid planes
+// (the four products of pass set 4), segment 1 the same K over its hi and lo
+// planes (lo*hi and hi*lo), both into the same accumulators.
+template <int BM, int BN, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * 64) void gemm_x6_kernel(const GemmArgs args) {
+  extern __shared__ __attribute__((aligned(16))) __bf16 lds[];
+  EG_GEMM_WALK((x3_tile<BM, BN, WMW, WNW, 4, 2>(args, w, lds)))
 }
 
 // One MFMA takes one A and one B value per lane (lane l: row / column l % 32,
@@ -1045,6 +1069,22 @@ int eg_gemm_bf16x6(const eg_gemm_operands* hi_mid, const eg_gemm_operands* hi_lo
   bool same = g1.n_seg == g2.n_seg;
   for (int s = 0; same && s < g1.n_seg; ++s) same = g1.seg[s].ktiles == g2.seg[s].ktiles;
   EG_CHECK_ARG(same, "hi_mid and hi_lo must describe the same K segments");
+  // One K segment: the six products in one launch, the hi / lo planes as a
+  // second segment over the same K (one last round and one sum of its parts;
+  // 12 % faster on the PLE key + value), when the workspace covers that
+  // launch's plan.  Two K segments keep two launches: one launch's last round
+  // of ranges, all of the backward's tiles, mixes steps of four and of two
+  // products unevenly (4 % slower).
+  if (g1.n_seg == 1) {
+    GemmArgs g = g1;
+    g.seg[1] = g2.seg[0];
+    g.n_seg = 2;
+    const int64_t need = workspace_size(kX3Shape, m, n, n2, 2 * 32 * g1.seg[0].ktiles, k_slices);
+    if (need >= 0 && workspace_bytes >= need)
+      return launch_gemm<kX3BM, kX3BN>(kX3Shape, gemm_x6_kernel<kX3BM, kX3BN, kX3WM, kX3WN>, "gemm_x6_kernel", g, m,
+                                       n, n2, c, ldc, c2, ldc2, accumulate, k_slices, workspace, workspace_bytes,
+                                       stream);
+  }
   // lo*lo + lo*hi + hi*lo + hi*hi over the hi and mid planes, then lo*hi + hi*lo
   // over the hi and lo planes, added to it
   rc = launch_gemm<kX3BM, kX3BN>(kX3Shape, gemm_x3_kernel<kX3BM, kX3BN, kX3WM, kX3WN, 4>, "gemm_x3_kernel<4>", g1,

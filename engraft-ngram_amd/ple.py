@@ -8,8 +8,8 @@ Forward:
   reference's torch matmuls), or with ``gemm="bf16x3"`` of the ``gemm_x3``
   kernel on the bf16 matrix cores (operands split into bf16 hi + lo, three
   products accumulated in fp32: 16 mantissa bits per operand), or with
-  ``gemm="bf16x6"`` two launches of it over three planes an operand
-  (``gemm_x6``: six products, fp32 accuracy);
+  ``gemm="bf16x6"`` of its six-product form over three planes an operand
+  (``gemm_x6``: fp32 accuracy);
 * ``eg_ple_gate``: per position and stream, the RMS norms of key and hidden,
   the score ``s``, the gate, ``gated = value * gate`` and its RMS norm;
 * ``eg_ple_conv``: the dilated causal depthwise convolution over
@@ -275,8 +275,9 @@ def gemm_x6(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate:
     """:func:`gemm_x3`'s GEMM with fp32 accuracy on the bf16 matrix cores
     (``eg_gemm_bf16x6``): every operand split into three bf16 planes, hi + mid
     + lo keeping its 24 mantissa bits, and the six plane products above
-    2^-23 of |a||b| accumulated in fp32.  Arguments, operands (fp32 tensors or
-    three-plane ``SplitPlanes``) and result as :func:`gemm_x3`."""
+    2^-23 of |a||b| accumulated in fp32 (one launch for one K segment, two
+    for two).  Arguments, operands (fp32 tensors or three-plane
+    ``SplitPlanes``) and result as :func:`gemm_x3`."""
     segs = [(_planes(a, False, True), _planes(b, cache_b, True),
              None if b_n2 is None else _planes(b_n2, cache_b, True))]
     if a2 is not None:
@@ -312,7 +313,9 @@ def gemm_x6(a, b, a2=None, b2=None, out: torch.Tensor | None = None, accumulate:
 
     out = _out(out, m, n, "out")
     out2 = _out(out2, m, n2, "out2") if n2 else None
-    slices, ws, ws_bytes = _gemm_workspace(m, n, n2, 32 * k_tiles, k_slices, dev, "eg_gemm_workspace_size")
+    # one K segment runs as one launch over both plane sets: its plan covers 2 k steps
+    k_plan = 32 * k_tiles * (2 if len(segs) == 1 else 1)
+    slices, ws, ws_bytes = _gemm_workspace(m, n, n2, k_plan, k_slices, dev, "eg_gemm_workspace_size")
     _lib.call("eg_gemm_bf16x6", hm, hl, len(segs), m, n, n2, _lib.ptr(out), max(out.stride(0), n),
               _lib.ptr(out2), max(out2.stride(0), n2) if n2 else 0, int(accumulate), slices, _lib.ptr(ws),
               ws_bytes, _lib.stream_ptr(dev))

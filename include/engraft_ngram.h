@@ -558,8 +558,12 @@ int eg_split_bf16x6(const float* x, int64_t rows, int64_t cols, int64_t ld, void
  * hi_lo (hi in *_hi, lo in *_lo) added to it; the same K segments in both.
  * The dropped products (mid*lo, lo*mid, lo*lo) are below 2^-23 of |a||b|, so
  * the result carries an fp32 matmul's error (the tests hold it to the fp32
- * GEMM's bound against float64).  Two launches on the stream, the second
- * adding to C / C2.  The same reference products as eg_gemm_bf16x3
+ * GEMM's bound against float64).  One K segment: one launch, the hi / lo
+ * products continuing the hi / mid products' accumulators, when the
+ * workspace also covers eg_gemm_workspace_size(m, n, n2, 2 k, k_slices) (that
+ * launch's plan runs 2 k steps); else, and for two K segments, two launches
+ * on the stream, the second adding to C / C2.  The same reference products as
+ * eg_gemm_bf16x3
  * (engraft/replica/layers.py:594-606, torch fp32 matmuls). */
 int eg_gemm_bf16x6(const eg_gemm_operands* hi_mid, const eg_gemm_operands* hi_lo, int32_t n_seg, int64_t m,
                    int64_t n, int64_t n2, float* c, int64_t ldc, float* c2, int64_t ldc2, int32_t accumulate,

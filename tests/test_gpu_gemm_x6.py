@@ -14,8 +14,9 @@ any 24-bit mantissa.  The GEMM, three bars:
   smallest, ~2^-18 |a b|), so a missing or doubled pass fails it, as does a
   plane read in the wrong place; gemm_x3 on the same data (16 mantissa bits)
   is off by ~2^-17;
-* the shapes of the other GEMM tests: partial tiles, two K segments, two
-  column groups, accumulation, the last round's K ranges on a ragged shape."""
+* the shapes of the other GEMM tests: partial tiles, two K segments (two
+  launches), two column groups, accumulation, the last round's K ranges and
+  equal K pieces on a ragged shape (one launch over both plane sets)."""
 from __future__ import annotations
 
 import sys
@@ -141,19 +142,22 @@ def test_gemm_x6_segments_groups_accumulate(cuda):
     assert torch.equal(again, gemm_x6(a1, b1, a2, b2))
 
 
-def test_gemm_x6_last_round_ranges(cuda):
+@pytest.mark.parametrize("k_slices", [None, 5])
+def test_gemm_x6_last_round_ranges(cuda, k_slices):
     """A ragged shape whose last round of tiles the library cuts into K ranges
-    (both launches use the plan and the workspace)."""
+    (or, with k_slices, every tile into equal K pieces).  One K segment: the
+    hi / mid and hi / lo plane sets run as the two segments of one launch, so
+    ranges and pieces cross from one plane set to the other."""
     from engraft_ngram_amd.ple import gemm_x6
-    _say("gemm_x6 last round in K ranges, ragged")
+    _say(f"gemm_x6 last round in K ranges, ragged, k_slices={k_slices}")
     g = torch.Generator(device=cuda).manual_seed(81)
     m, n, k = 1000, 18400, 3200
     a = torch.randn(m, k, generator=g, device=cuda)
     b = torch.randn(n, k, generator=g, device=cuda) * 0.05
-    got = gemm_x6(a, b)
+    got = gemm_x6(a, b, k_slices=k_slices)
     _check_f32_bound(got, k, a, b)
     torch.cuda.synchronize()
-    assert torch.equal(got, gemm_x6(a, b))
+    assert torch.equal(got, gemm_x6(a, b, k_slices=k_slices))
 
 
 def test_gemm_x6_needs_three_planes(cuda):
