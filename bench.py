@@ -963,9 +963,11 @@ def bench_ple(steps: int, warmup: int, cpu_s: float = 0.0) -> dict:
                        "GEMMs (one launch) either fp32 (eg_gemm_f32 on the fp32 matrix cores; the reference's "
                        "arithmetic; hipBLASLt's time for the same products beside it), bf16x3 (eg_gemm_bf16x3 "
                        "on the bf16 matrix cores, 16 mantissa bits per operand) or bf16x6 (eg_gemm_bf16x6: three "
-                       "bf16 planes an operand, six products, fp32 accuracy); gate/norm and conv in HIP; "
-                       "gemm_err_vs_fp64: the largest |C - C64| / (|emb| |W|^T)",
-           **res["fp32"], "bf16x3": res["bf16x3"], "bf16x6": res["bf16x6"], "fp32_mfma_peak_tflops": 157.3,
+                       "bf16 planes an operand, six products, fp32 accuracy; ple_forward's default); gate/norm "
+                       "and conv in HIP; gemm_err_vs_fp64: the largest |C - C64| / (|emb| |W|^T); the top-level "
+                       "figures are the fp32 mode's",
+           **res["fp32"], "default_gemm": "bf16x6", "bf16x3": res["bf16x3"], "bf16x6": res["bf16x6"],
+           "fp32_mfma_peak_tflops": 157.3,
            "bf16_mfma_peak_tflops": 2500.0}
     if cpu_s > 0:
         from oracle import ple as OP

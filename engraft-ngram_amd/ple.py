@@ -3,13 +3,13 @@ for ``PleWeights`` / ``ple_forward`` (``engraft/replica/layers.py:555-626``).
 
 Forward:
 
-* ``key = emb @ w_key^T`` and ``value = emb @ w_value^T``, one launch of the
-  ``gemm_f32`` kernel on the fp32 matrix cores (fp32 arithmetic, as the
-  reference's torch matmuls), or with ``gemm="bf16x3"`` of the ``gemm_x3``
-  kernel on the bf16 matrix cores (operands split into bf16 hi + lo, three
-  products accumulated in fp32: 16 mantissa bits per operand), or with
-  ``gemm="bf16x6"`` of its six-product form over three planes an operand
-  (``gemm_x6``: fp32 accuracy);
+* ``key = emb @ w_key^T`` and ``value = emb @ w_value^T`` in one launch: by
+  default (``gemm="bf16x6"``) on the bf16 matrix cores with fp32 accuracy
+  (``gemm_x6``: operands split into three bf16 planes, six products
+  accumulated in fp32), with ``gemm="fp32"`` of the ``gemm_f32`` kernel on
+  the fp32 matrix cores (fp32 products, as the reference's torch matmuls), or
+  with ``gemm="bf16x3"`` of the ``gemm_x3`` kernel (hi + lo planes, three
+  products: 16 mantissa bits per operand);
 * ``eg_ple_gate``: per position and stream, the RMS norms of key and hidden,
   the score ``s``, the gate, ``gated = value * gate`` and its RMS norm;
 * ``eg_ple_conv``: the dilated causal depthwise convolution over
@@ -623,15 +623,17 @@ class _PleFn(torch.autograd.Function):
 
 def ple_forward(emb: torch.Tensor, hidden: torch.Tensor, w: PleWeights, hist: torch.Tensor, hparams,
                 diag: dict | None = None, detach_value: bool = False, detach_gate: bool = False,
-                gemm: str = "fp32") -> tuple[torch.Tensor, torch.Tensor]:
+                gemm: str = "bf16x6") -> tuple[torch.Tensor, torch.Tensor]:
     """``(hidden + gated + conv_out, new history)`` (``engraft/replica/layers.py:
     565-626``).  ``emb [T, n_embd]``, ``hidden [T, hc, n_embd]``, ``hist``
     ``[rows, hc, n_embd]`` (at most ``(K-1)*ple_ngram_size`` rows, empty at a
     sequence start); all on the device.  ``gemm`` picks the projections' GEMM:
-    ``"fp32"`` (the reference's arithmetic: ``gemm_f32`` on the fp32 matrix
-    cores), ``"bf16x3"`` (``gemm_x3`` on the bf16 matrix cores: 16 mantissa
-    bits per operand, about 1e-5 relative per projection, 2.5x faster) or
-    ``"bf16x6"`` (``gemm_x6``: the bf16 matrix cores with fp32 accuracy)."""
+    ``"bf16x6"``, the default (``gemm_x6``: the bf16 matrix cores with fp32
+    accuracy, its error against float64 below both fp32 paths' and the
+    fastest of the three at that accuracy), ``"fp32"`` (``gemm_f32``: fp32
+    products on the fp32 matrix cores, the reference's torch matmul
+    arithmetic) or ``"bf16x3"`` (``gemm_x3``: 16 mantissa bits per operand,
+    about 1e-5 relative per projection, 1.7x faster than bf16x6)."""
     if gemm not in ("fp32", "bf16x3", "bf16x6"):
         raise ValueError(f"gemm must be 'fp32', 'bf16x3' or 'bf16x6', got {gemm!r}")
     hc = hparams.hc_mult
