@@ -390,7 +390,8 @@ __device__ inline void x3_tile(const GemmArgs& args, const Work& w, __bf16* lds)
     const GemmSeg& sg = args.seg[s];
     // a load's address: the plane's base (uniform) + a 32-bit byte offset
     // (the host keeps every plane under 4 GiB), one VGPR a load
-    // (from an opaque copy of the lane: computed here, not ahead of an earlier segment's loop and held)
+    // (from an opaque copy of the lane: computed here for the segment, not once
+    // for the tile and held across the K loops, which spilled)
     int ln = lane;
     asm volatile("" : "+v"(ln));
     uint32_t off[LPW];
@@ -583,25 +584,25 @@ __device__ inline void f32_tile(const F32Args& args, const Work& w, float* ldsf)
   // 8 q' + 7 of A (j < LA, q' = q) or B (q' = q - BM / 8); lane i fills row
   // 8 q' + i / 8, slot i % 8.  Rows past m or n read row m-1 or n-1 (not stored).
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
-  int64_t row_of[LPW];
-  int col_of[LPW];
-#pragma unroll
-  for (int j = 0; j < LPW; ++j) {
-    const int q = uwave + NW * j, row = 8 * (j < LA ? q : q - BM / 8) + (lane >> 3);
-    const int64_t gr = (j < LA ? w.m0 : w.n0) + row, lim = j < LA ? p.m : n_grp;
-    row_of[j] = gr < lim ? gr : lim - 1;
-    col_of[j] = swz8(row, lane & 7) * 4;
-  }
 
   for (int s = 0; s < args.n_seg; ++s) {
     const int64_t seg0 = s ? p.kt0 : 0, seg1 = s ? p.kt_total : p.kt0;
     const int64_t lo = w.kv0 > seg0 ? w.kv0 : seg0, hi = w.kv1 < seg1 ? w.kv1 : seg1;
     if (lo >= hi) continue;
     const F32Seg& sg = args.seg[s];
+    // the load addresses, from an opaque copy of the lane: computed here for the
+    // segment rather than once for the tile and held across the K loops (the
+    // held form spilled 160 B a lane outside the loop and ran 2-4 % slower)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
     const float* src[LPW];
 #pragma unroll
-    for (int j = 0; j < LPW; ++j)
-      src[j] = (j < LA ? sg.a : sg.b[grp]) + row_of[j] * (j < LA ? sg.lda : sg.ldb[grp]) + col_of[j];
+    for (int j = 0; j < LPW; ++j) {
+      const int q = uwave + NW * j, row = 8 * (j < LA ? q : q - BM / 8) + (ln >> 3);
+      const int64_t gr = (j < LA ? w.m0 : w.n0) + row, lim = j < LA ? p.m : n_grp;
+      src[j] = (j < LA ? sg.a : sg.b[grp]) + (gr < lim ? gr : lim - 1) * (j < LA ? sg.lda : sg.ldb[grp]) +
+               swz8(row, ln & 7) * 4;
+    }
     auto issue = [&](int64_t kt) {
       float* st = ldsf + (kt & 1) * STAGE;
 #pragma unroll
