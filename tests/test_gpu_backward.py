@@ -132,8 +132,8 @@ def test_scatter_grad_large_groupings(cuda, n_slots, n_var):
     """The two groupings past the common case, bit-exact against the oracle:
     more than 1,024 tiles of 1,024 slots (the counting grouping: per-variable
     atomics, scan, fill), more than 1M variables (the tile sort with buckets of
-    2,048 variables), and 391 tiles (the bucket ranges read two tiles a thread;
-    977 tiles, four).  Zipf-drawn rows give long segments; a twentieth
+    2,048 variables, 977 tiles: the bucket ranges read two tiles a thread), and
+    391 tiles (one a thread).  Zipf-drawn rows give long segments; a twentieth
     of the slots hit no variable."""
     from engraft_ngram_amd import descent as D
     _say(f"scatter_grad grouping, {n_slots} slots over {n_var} variables")
