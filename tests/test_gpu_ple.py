@@ -130,15 +130,17 @@ def test_ple_history_gradient_across_chunks(cuda):
 
 
 @pytest.mark.parametrize("dv,dg,gemm", [(False, False, "fp32"), (True, False, "fp32"), (False, True, "fp32"),
-                                        (False, False, "bf16x3"), (True, False, "bf16x3"), (False, False, "bf16x6")])
+                                        (False, False, "bf16x3"), (True, False, "bf16x3"), (False, False, "bf16x6"),
+                                        (False, False, None)])
 def test_ple_native_backward_against_oracle(cuda, dv, dg, gemm):
     """The HIP backward (no weight gradients): d_emb, d_hidden and the incoming
     history's gradient, with a gradient on the returned history too, against
     autograd of the oracle on the CPU (T 40 after a 9-row history), for the
     plain block and with either factor of gated detached; the projections run
-    on the library's GEMM of the chosen arithmetic (eg_gemm_f32 or
-    eg_gemm_bf16x3), key and value as one launch and the backward's d_emb as
-    one call over two K segments."""
+    on the library's GEMM of the chosen arithmetic (eg_gemm_f32,
+    eg_gemm_bf16x3 or eg_gemm_bf16x6; None: ple_forward's default, bf16x6),
+    key and value as one call and the backward's d_emb as one call over two K
+    segments."""
     from engraft_ngram_amd import _lib, ple
     print(f"[gpu-test] ple native backward detach_value={dv} detach_gate={dg} gemm={gemm}", file=sys.stderr,
           flush=True)
@@ -164,16 +166,18 @@ def test_ple_native_backward_against_oracle(cuda, dv, dg, gemm):
 
     _lib.call = spy
     try:
+        kw = {} if gemm is None else {"gemm": gemm}
         out_d, nh_d = ple.ple_forward(leaves_d[0], leaves_d[1], wd, leaves_d[2], _HP, detach_value=dv,
-                                      detach_gate=dg, gemm=gemm)
+                                      detach_gate=dg, **kw)
         ((out_d * r.to(cuda)).sum() + (nh_d * rh.to(cuda)).sum()).backward()
     finally:
         _lib.call = real_call
     gate_bwd = "eg_ple_gate_backward_planes" if gemm == "bf16x3" else "eg_ple_gate_backward"
     assert "eg_ple_conv_backward" in called and gate_bwd in called  # bf16x3: d_key, d_value written as planes
+    mode = gemm or "bf16x6"
     entry = {"fp32": "eg_gemm_f32", "bf16x3": "eg_gemm_bf16x3", "bf16x6": "eg_gemm_bf16x6"}
-    assert called.count(entry[gemm]) == 2  # key + value in one call, then d_emb
-    assert not any(entry[o] in called for o in entry if o != gemm)
+    assert called.count(entry[mode]) == 2  # key + value in one call, then d_emb
+    assert not any(entry[o] in called for o in entry if o != mode)
     for name, got, exp in zip(("emb", "hidden", "hist"), (x.grad for x in leaves_d), (x.grad for x in leaves_c)):
         scale = exp.abs().max().item()
         err = (got.cpu() - exp).abs().max().item()
