@@ -31,7 +31,7 @@ FMT_MXFP8 = 3
 FMT_IQ4_NL = 4
 FMT_F32 = 5
 
-ABI_VERSION = 3  # EG_ABI_VERSION of include/engraft_ngram.h these structures follow
+ABI_VERSION = 4  # EG_ABI_VERSION of include/engraft_ngram.h these structures follow
 
 FMT_CODES = {"bf16": FMT_BF16, "q8_0": FMT_Q8_0, "mxfp8": FMT_MXFP8, "iq4_nl": FMT_IQ4_NL, "f32": FMT_F32}
 
@@ -95,6 +95,7 @@ class EgDescentState(ctypes.Structure):
         ("quant", EgTable),
         ("index", c_void_p),
         ("index_capacity", c_int64),
+        ("row_stride", c_int64),
     ]
 
 

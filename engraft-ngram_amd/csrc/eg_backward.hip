@@ -585,6 +585,7 @@ struct SegArgs {
   float* master;
   float* m;
   float* v;
+  int64_t stride;         // floats from one variable's master / m / v row to the next
   int32_t* stamp;
   TableDev quant;         // fmt 0: no requantised copy
   TableDev base;          // for the pull term (rows0 at the variables' ids)
@@ -770,7 +771,7 @@ __device__ void adam_apply(const SegArgs& a, int64_t k, int sub, const float g[V
     const float denom = sqrtf(v[t]) / a.bc2s + a.eps;
     p[t] = p[t] + a.neg_step_size * (m[t] / denom);
   }
-  const int64_t off = k * a.dim;
+  const int64_t off = k * a.stride;
   store_f32<VPL, CONSEC>(a.master + off, sub, p);
   store_f32<VPL, CONSEC>(a.m + off, sub, m);
   store_f32<VPL, CONSEC>(a.v + off, sub, v);
@@ -848,7 +849,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
     const int64_t len = hi - lo;
     float p[VPL], m[VPL], v[VPL];
     if (ADAM && grp == 0) {  // independent of the gradient: fetched first
-      const int64_t off = (int64_t)key * a.dim;
+      const int64_t off = (int64_t)key * a.stride;
       load_f32<VPL, CONSEC>(a.master + off, sub, p);
       load_f32<VPL, CONSEC>(a.m + off, sub, m);
       load_f32<VPL, CONSEC>(a.v + off, sub, v);
@@ -907,7 +908,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const SegArgs a, int64_t n_
   if (len == 0 || len > kPiece) return;  // not hit, or a long range (its own workgroup)
   float p[VPL], m[VPL], v[VPL];
   if constexpr (ADAM) {  // the state rows do not depend on the gradient: fetch them first
-    const int64_t off = k * a.dim;
+    const int64_t off = k * a.stride;
     load_f32<VPL, CONSEC>(a.master + off, sub, p);
     load_f32<VPL, CONSEC>(a.m + off, sub, m);
     load_f32<VPL, CONSEC>(a.v + off, sub, v);
@@ -944,7 +945,7 @@ __global__ __launch_bounds__(256) void dense_kernel(const SegArgs a) {
   float g[VPL], p[VPL], m[VPL], v[VPL];
 #pragma unroll
   for (int t = 0; t < VPL; ++t) g[t] = 0.0f;
-  const int64_t off = k * a.dim;
+  const int64_t off = k * a.stride;
   load_f32<VPL, CONSEC>(a.master + off, sub, p);
   load_f32<VPL, CONSEC>(a.m + off, sub, m);
   load_f32<VPL, CONSEC>(a.v + off, sub, v);
@@ -1340,6 +1341,8 @@ static int check_state(const eg_descent_state* state) {
   EG_CHECK_ARG(state != nullptr, "state is NULL");
   EG_CHECK_ARG(state->n == 0 || (state->master && state->m && state->v && state->stamp),
                "state master/m/v/stamp is NULL");
+  EG_CHECK_ARG(state->row_stride == 0 || state->row_stride >= state->dim, "row_stride=%lld below dim=%d",
+               (long long)state->row_stride, state->dim);
   if (state->index != nullptr)
     EG_CHECK_ARG(state->index_capacity >= 2 * state->n && state->index_capacity >= 8 &&
                      (state->index_capacity & (state->index_capacity - 1)) == 0 &&
@@ -1422,6 +1425,7 @@ int eg_descent_apply(const void* d_out, int32_t d_out_f32, int64_t n_pos, int32_
   a.master = state->master;
   a.m = state->m;
   a.v = state->v;
+  a.stride = state->row_stride > 0 ? state->row_stride : state->dim;
   a.stamp = state->stamp;
   a.step = opt->step;
   a.dense = opt->dense != 0;

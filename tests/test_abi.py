@@ -62,7 +62,7 @@ def test_abi_version_and_error_string():
     from engraft_ngram_amd import _lib
 
     lib = _lib.load()
-    assert lib.eg_abi_version() == 3
+    assert lib.eg_abi_version() == 4
     # an argument error is reported without touching the device
     spec = _lib.EgHashSpec()
     spec.ngram_size = 9
