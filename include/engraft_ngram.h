@@ -235,9 +235,9 @@ typedef struct eg_descent_state {
   int64_t n;          /* R */
   int32_t dim;
   const int32_t* ids; /* [R] sorted unique global rows */
-  float* master;      /* [R, dim] fp32 rows (rows_var) */
-  float* m;           /* [R, dim] Adam first moment */
-  float* v;           /* [R, dim] Adam second moment */
+  float* master;      /* R fp32 rows of dim (rows_var), row_stride floats apart */
+  float* m;           /* R rows: Adam first moment, the same layout */
+  float* v;           /* R rows: Adam second moment, the same layout */
   int32_t* stamp;     /* [R] last dense step that hit the row (0 before the first) */
   eg_table quant;     /* requantised copy [R] written after the update (Q8_0 or MXFP8;
                          payload NULL: none) -- the rows a forward overlay reads */
